@@ -1,0 +1,142 @@
+/*
+ * nmsparse_hip.h — C ABI of the MI355X (gfx950) shared-mask N:M sparse GEMV.
+ *
+ * The library (libnmsparse_hip.so) computes, for batch-1 decode,
+ *
+ *     out[r] = RNE_T( sum_{c < w} f32(mat_data[c, r]) * f32(vec[(c / nnz) * m + mat_index[c]]) )
+ *
+ * for r < h, with fp32 fused multiply-add accumulation, where
+ *   - mat_data  is [w, h] row-major (h contiguous), element type T,
+ *   - mat_index is [w / nnz, nnz] uint8, the kept positions inside each
+ *     m-wide input group; one pattern is shared by all h output rows,
+ *   - vec       is [1, K] with K = (w / nnz) * m, element stride vec_stride,
+ *   - out       is [1, h], element type T (fp32 -> T rounds to nearest even).
+ *
+ * Reference interface replaced: the Triton launch wrapper
+ * `nmsparse_spmv_forward_triton_ptx(vec, mat_data, mat_index, w, h,
+ * BLOCK_WIDTH, NUM_THREADS, VEC_WIDTH, minibatch, vecNum, ...)`
+ * (triton_spmv.py:229-318) together with the kernels it launches
+ * (triton_spmv.py:56-115 generic, triton_spmv.py:149-214 A100). The
+ * reference's zero-fill (triton_spmv.py:285), relaxed fp32 atomics
+ * (triton_spmv.py:110-115, 209-214) and fp32 -> T cast (triton_spmv.py:318)
+ * are folded into one launch: split-K partial sums go to a caller-provided
+ * workspace and the last-arriving workgroup of each output tile reduces them
+ * in a fixed order, so results are deterministic.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers (HBM). `stream` is a hipStream_t passed as
+ *     void* (NULL = the default stream). Launches are asynchronous: nothing
+ *     here synchronises, allocates device memory or reads device memory on
+ *     the host, so the calls may be captured in a hipGraph.
+ *   - Return value: 0 on success; a negative NM_ERR_* code for an argument
+ *     the library rejects before launching; a positive hipError_t if the
+ *     launch itself failed. nm_strerror() names every code.
+ *   - Preconditions checked here (a subset of the reference wrapper's, which
+ *     the Python layer re-checks with the reference's exception types):
+ *     h > 0, h % 128 == 0 (triton_spmv.py:263-264); 0 < nnz <= m <= 256
+ *     (uint8 positions); w > 0, w % nnz == 0 (triton_spmv.py:265-266);
+ *     vec_stride >= 1; non-NULL pointers; 16-byte aligned mat_data and out
+ *     base addresses; workspace_bytes >= nm_gemv_workspace_bytes(...).
+ *   - A position with (c / nnz) * m + mat_index[c] >= K contributes 0 (the
+ *     reference kernel would read outside vec there).
+ *
+ * Workspace layout: the first NM_TICKET_BYTES bytes hold uint32 arrival
+ * counters that must be zero before the first call that uses the workspace
+ * (allocate it zero-filled once); every launch leaves them zero again. The
+ * rest holds fp32 split-K partial sums. Calls that share one workspace must be
+ * ordered (same stream, or synchronised); overlapping calls on one workspace
+ * race.
+ */
+#ifndef NMSPARSE_HIP_H
+#define NMSPARSE_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NM_TICKET_BYTES 65536
+
+/* Negative status codes (positive codes are hipError_t values). */
+#define NM_OK 0
+#define NM_ERR_NULL_POINTER (-1)
+#define NM_ERR_BAD_SHAPE (-2)        /* h, w, nnz, m or vec_stride out of range */
+#define NM_ERR_H_NOT_MULTIPLE_128 (-3)
+#define NM_ERR_W_NOT_MULTIPLE_NNZ (-4)
+#define NM_ERR_MISALIGNED (-5)       /* mat_data or out not 16-byte aligned */
+#define NM_ERR_WORKSPACE (-6)        /* workspace missing or too small */
+#define NM_ERR_BAD_CONFIG (-7)       /* explicit config id / split count rejected */
+
+/* Element type codes for the *_ex entry point and nm_gemv_workspace_bytes. */
+#define NM_DTYPE_F16 0
+#define NM_DTYPE_BF16 1
+#define NM_DTYPE_F32 2
+
+/*
+ * Bytes of workspace a call with these sizes needs (NM_TICKET_BYTES plus the
+ * split-K partials of the configuration the library picks for the shape).
+ * Replaces the reference's per-call `torch.zeros((1, h), float32)` scratch
+ * (triton_spmv.py:285). Returns 0 for arguments nm_gemv_* would reject.
+ */
+size_t nm_gemv_workspace_bytes(int h, int w, int nnz, int m);
+
+/*
+ * Typed GEMV entry points. vec, mat_data and out share the element type.
+ * Replace `nmsparse_spmv_forward_triton_ptx` (triton_spmv.py:229-318) for
+ * vec.dtype == float16 / bfloat16 / float32 (triton_spmv.py:248-251); the
+ * op layer `torch.ops.nmsparse.gemv` (src/spmv/nmsparse_op.py:77-96) calls
+ * the fp16 one.
+ */
+int nm_gemv_f16(const void* vec, int vec_stride, const void* mat_data,
+                const uint8_t* mat_index, void* out, void* workspace,
+                size_t workspace_bytes, int h, int w, int nnz, int m,
+                void* stream);
+int nm_gemv_bf16(const void* vec, int vec_stride, const void* mat_data,
+                 const uint8_t* mat_index, void* out, void* workspace,
+                 size_t workspace_bytes, int h, int w, int nnz, int m,
+                 void* stream);
+int nm_gemv_f32(const void* vec, int vec_stride, const void* mat_data,
+                const uint8_t* mat_index, void* out, void* workspace,
+                size_t workspace_bytes, int h, int w, int nnz, int m,
+                void* stream);
+
+/*
+ * Same computation with an explicit kernel configuration, for tuning sweeps
+ * and tests of every configuration. config_id < 0 selects the library's own
+ * choice; otherwise 0 <= config_id < nm_num_configs(). splits <= 0 lets the
+ * library choose the split-K count for that configuration. Replaces the
+ * reference's autotune search space (triton_spmv.py:40-55, 122-148), which
+ * the harness reads back via `best_config` (microbench_triton_torchmv.py:271-297).
+ * The workspace must then hold nm_gemv_workspace_bytes_ex(...) bytes.
+ */
+int nm_gemv_ex(int dtype, const void* vec, int vec_stride, const void* mat_data,
+               const uint8_t* mat_index, void* out, void* workspace,
+               size_t workspace_bytes, int h, int w, int nnz, int m,
+               int config_id, int splits, void* stream);
+size_t nm_gemv_workspace_bytes_ex(int h, int w, int nnz, int m, int config_id,
+                                  int splits);
+
+/*
+ * Configuration introspection. nm_config_describe writes a short text such as
+ * "th32_u8" into buf; nm_gemv_plan reports the configuration and split count
+ * the library would use for a shape (config_id < 0: its own choice).
+ */
+int nm_num_configs(void);
+int nm_config_describe(int config_id, char* buf, int buf_len);
+int nm_gemv_plan(int h, int w, int nnz, int m, int config_id, int splits,
+                 int* out_config_id, int* out_splits, int* out_blocks,
+                 int* out_rows_per_block);
+
+/* Human-readable text for a status code returned above. */
+const char* nm_strerror(int code);
+
+/* ABI version of this header (bumped on any signature change). */
+int nm_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NMSPARSE_HIP_H */

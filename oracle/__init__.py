@@ -1,0 +1,32 @@
+"""CPU oracle for the shared-mask N:M sparse GEMV — TEST INFRASTRUCTURE ONLY.
+
+Only `tests/`, `__graft_entry__.smoke()` and the `cpu_baseline` leg of
+`bench.py` may import this package, and only as the checker (or the timed CPU
+baseline). Nothing in `spmv_decode_amd/` imports it; the product path fails
+loudly when its HIP library is missing instead of falling back to this code.
+
+Contents and what pins each function (tests/test_oracle.py):
+
+* `nm_oracle.gather_activations`, `gemv_f64`, `gemv_fp32_dense`: the GEMV
+  value (triton_spmv.py:56-115, 149-214; microbench_triton_torchmv.py:383-386).
+  Pinned by closed forms: one-hot activations reproduce a packed row exactly,
+  a one-hot at a pruned position gives zero, linearity under powers of two,
+  group-permutation invariance, and brute force over every 2:4 pattern.
+* `nm_oracle.scatter` / `pack`: compressed <-> dense masked weight
+  (microbench_triton_torchmv.py:145-164). Pinned by the round trips
+  pack(scatter(x)) == x and scatter(pack(W*mask)) == W*mask, bit-exact.
+* `nm_oracle.make_sparse`: synthetic packing / index generation
+  (src/spmv/nmsparse_linear.py:14-33). Pinned bit-exactly by the golden
+  fixtures in tests/golden/, written by importing the reference.
+* `nm_oracle.error_metrics`: max_abs, mean_abs, rmse, rel_l2
+  (microbench_triton_torchmv.py:408-423). Pinned against hand-computed values.
+* `nm_oracle.expected_exception`: the reference wrapper's and op's argument
+  checks (triton_spmv.py:245-283, src/spmv/nmsparse_op.py:83-86).
+  **Parity unpinned**: the reference wrapper rejects non-CUDA tensors first
+  (triton_spmv.py:245-246) and cannot run without an NVIDIA GPU, so this
+  restatement is checked only by reading.
+* `c_oracle` (ctypes binding of oracle/nm_gemv_ref.c): the same GEMV in plain
+  C with fp32 FMA in the reference's in-program order and software
+  fp16/bf16 conversions. Pinned by exhaustive conversion checks against
+  numpy and by agreement with the fp64 oracle.
+"""

@@ -1,0 +1,57 @@
+"""Build the HIP library `libnmsparse_hip.so` for gfx950, in-tree.
+
+    python -m spmv_decode_amd.build          # or __graft_entry__.build()
+
+The library is a plain C-ABI shared object (include/nmsparse_hip.h) compiled
+by hipcc from spmv_decode_amd/csrc/nm_gemv.hip; nothing links against torch.
+"""
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+ROOT = PKG.parent
+SOURCES = [PKG / "csrc" / "nm_gemv.hip"]
+LIB_PATH = PKG / "libnmsparse_hip.so"
+ARCH = "gfx950"
+
+# Packed-fp32 VALU ops are disabled for every HIP build of this project; the
+# compiler's host pass warns that it does not know the feature (harmless).
+HIPCC_FLAGS = [
+    "-O3",
+    "-std=c++17",
+    f"--offload-arch={ARCH}",
+    "-fPIC",
+    "-shared",
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-Wno-unused-command-line-argument",
+]
+
+
+def hipcc() -> str:
+    for cand in (os.environ.get("HIPCC"), shutil.which("hipcc"), "/opt/rocm/bin/hipcc"):
+        if cand and Path(cand).exists():
+            return cand
+    raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile the HIP sources to LIB_PATH (always recompiles)."""
+    tmp = LIB_PATH.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *map(str, SOURCES)]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        sys.stderr.write(res.stdout + res.stderr)
+        raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
+    os.replace(tmp, LIB_PATH)
+    return LIB_PATH
+
+
+if __name__ == "__main__":
+    print(build_library(verbose=True))

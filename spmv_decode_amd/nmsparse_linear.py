@@ -1,0 +1,218 @@
+"""Sparse Linear module and model surgery for the N:M shared-mask GEMV.
+
+Mirrors the reference module API (src/spmv/nmsparse_linear.py):
+
+* `_make_sparse(K, N, M, seed, device)` — synthetic 50% N:M weights, bit-exact
+  with the reference (src/spmv/nmsparse_linear.py:14-33, shared-mask branch).
+* `NmSparseLinear(N, K, M, seed, device, dense_weight=None)` — buffers
+  `mat_data` [w, N] fp16 and `mat_index` [K/M, M/2] uint8, attributes
+  `h, w, block_width, vec_width`; decode rows (x.shape[-2] == 1) go through
+  `torch.ops.nmsparse.gemv`, longer inputs through dense `F.linear`
+  (src/spmv/nmsparse_linear.py:36-68).
+* `swap_to_nmsparse(model, M, device, seed=0, block_devices=None)` — replaces
+  every attention / MLP Linear of a gpt-fast or Hugging Face decoder stack,
+  Linear j getting seed `seed + j` (src/spmv/nmsparse_linear.py:83-144).
+
+Environment, read at import like the reference (src/spmv/nmsparse_linear.py:7-8):
+NM_DECODE_ONLY=1 drops dense weights (prefill then raises), NM_WEIGHT_CPU=1
+keeps them on the host. NM_SYNTH_INIT=device (this build only) draws the
+synthetic weights with a seeded on-device generator instead of the CPU
+stream — same distribution and shapes, much faster for 8B+ models, NOT
+bit-exact with the reference; the default is the bit-exact CPU stream.
+
+Beyond the reference: `NmSparseLinear.from_dense` / `pack_dense` build the
+packed buffers from a real dense weight and a shared N:M mask (a pure gather).
+"""
+from __future__ import annotations
+
+import os
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+from . import nmsparse_op  # noqa: F401  (registers torch.ops.nmsparse.gemv)
+
+DECODE_ONLY = os.environ.get("NM_DECODE_ONLY", "0") == "1"
+WEIGHT_CPU = os.environ.get("NM_WEIGHT_CPU", "0") == "1" or DECODE_ONLY
+SYNTH_INIT = os.environ.get("NM_SYNTH_INIT", "reference")
+if SYNTH_INIT not in ("reference", "device"):
+    raise ValueError(f"Unknown NM_SYNTH_INIT={SYNTH_INIT!r}; use 'reference' or 'device'")
+
+
+def _bank_patterns(gen: torch.Generator, banks: int, M: int, nnz: int) -> torch.Tensor:
+    """One sorted draw of nnz distinct positions out of M per bank, in bank order."""
+    rows = [torch.randperm(M, generator=gen)[:nnz].sort().values for _ in range(banks)]
+    if not rows:
+        return torch.empty(0, nnz, dtype=torch.uint8)
+    return torch.stack(rows).to(torch.uint8)
+
+
+def _make_sparse(K, N, M, seed, device, init=None):
+    """Synthetic packed weights for an N-output, K-input Linear at 50% N:M.
+
+    Returns (mat_data [w, N] fp16, mat_index [K/M, M/2] uint8, w, nnz) on
+    `device`. With the default init the values are bit-exact with the
+    reference: the same CPU generator consumed by the same calls in the same
+    order (fp32 normal draws scaled by 1/sqrt(K) then rounded to fp16, then one
+    sorted randperm prefix per bank).
+    """
+    init = SYNTH_INIT if init is None else init
+    nnz = M // 2
+    banks = K // M
+    w = banks * nnz
+    if init == "device" and device != "cpu":
+        gen = torch.Generator(device=device).manual_seed(seed)
+        mat_data = (torch.randn(w, N, generator=gen, dtype=torch.float32, device=device) / (K ** 0.5)).to(
+            torch.float16)
+        keys = torch.rand(banks, M, generator=gen, device=device)
+        mat_index = keys.argsort(dim=1)[:, :nnz].sort(dim=1).values.to(torch.uint8).contiguous()
+        return mat_data, mat_index, w, nnz
+    gen = torch.Generator().manual_seed(seed)
+    scaled = torch.randn(w, N, generator=gen, dtype=torch.float32) / (K ** 0.5)
+    mat_data = scaled.to(torch.float16)
+    mat_index = _bank_patterns(gen, banks, M, nnz)
+    if device != "cpu":
+        mat_data = mat_data.to(device)
+        mat_index = mat_index.to(device)
+    return mat_data, mat_index, w, nnz
+
+
+def pack_dense(weight: torch.Tensor, mat_index: torch.Tensor, M: int) -> torch.Tensor:
+    """Packed [w, N] buffer of a dense [N, K] weight under a shared N:M pattern.
+
+    mat_index is [K/M, nnz] (sorted in-group positions); mat_data[c, :] =
+    weight[:, (c // nnz) * M + mat_index.flat[c]]. A pure gather (bit-exact);
+    entries of `weight` outside the pattern are ignored.
+    """
+    N, K = weight.shape
+    banks, nnz = mat_index.shape
+    if banks * M != K:
+        raise ValueError(f"mat_index has {banks} banks of M={M}, weight has K={K}")
+    pos = (torch.arange(banks * nnz, device=mat_index.device) // nnz) * M + mat_index.reshape(-1).long()
+    return weight[:, pos.to(weight.device)].t().contiguous()
+
+
+class NmSparseLinear(nn.Module):
+    """Linear layer whose decode path is the N:M sparse GEMV.
+
+    N is the number of outputs (h), K the number of inputs, M the group size
+    (50% sparsity: M/2 kept per group). Asserts K % M == 0 and N % 128 == 0 as
+    the reference does (src/spmv/nmsparse_linear.py:39).
+    """
+
+    def __init__(self, N, K, M, seed, device, dense_weight=None):
+        super().__init__()
+        assert K % M == 0 and N % 128 == 0, (K, N, M)
+        self._weight_cpu = None
+        self.weight = None
+        if dense_weight is not None:
+            if WEIGHT_CPU:
+                self._weight_cpu = dense_weight.detach().cpu()
+                del dense_weight
+                if device != "cpu":
+                    torch.cuda.empty_cache()
+            else:
+                self.weight = dense_weight
+        md, mi, w, nnz = _make_sparse(K, N, M, seed, device)
+        self.register_buffer("mat_data", md)
+        self.register_buffer("mat_index", mi)
+        self.h, self.w, self.block_width, self.vec_width = N, w, nnz, M
+
+    @classmethod
+    def from_dense(cls, weight: torch.Tensor, mat_index: torch.Tensor, M: int, keep_dense: bool = False):
+        """Build from a real dense [N, K] weight and its shared N:M pattern
+        (mat_index [K/M, M/2] uint8). `keep_dense` keeps `weight` for prefill."""
+        N, K = weight.shape
+        if K % M or N % 128 or mat_index.shape != (K // M, M // 2):
+            raise ValueError(f"need K % M == 0, N % 128 == 0 and mat_index [K/M, M/2]; got N={N}, K={K}, M={M}, "
+                             f"mat_index {tuple(mat_index.shape)}")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self._weight_cpu = None
+        self.weight = weight if keep_dense else None
+        mi = mat_index.to(device=weight.device, dtype=torch.uint8).contiguous()
+        self.register_buffer("mat_data", pack_dense(weight, mi, M).to(torch.float16))
+        self.register_buffer("mat_index", mi)
+        self.h, self.w, self.block_width, self.vec_width = N, (K // M) * (M // 2), M // 2, M
+        return self
+
+    def _prefill_weight(self, device):
+        if self.weight is not None:
+            return self.weight
+        if self._weight_cpu is None:
+            raise RuntimeError("prefill requires dense weight")
+        return self._weight_cpu.to(device)
+
+    def forward(self, x):
+        if x.shape[-2] == 1:
+            return torch.ops.nmsparse.gemv(x, self.mat_data, self.mat_index,
+                                           self.w, self.h, self.block_width, self.vec_width)
+        return F.linear(x, self._prefill_weight(x.device))
+
+    def extra_repr(self) -> str:
+        return f"h={self.h}, w={self.w}, N:M={self.block_width}:{self.vec_width}"
+
+
+# Decoder-block layouts: (sub-module attribute, Linear names in swap order).
+# gpt-fast fuses attention into wqkv/wo and names the MLP w1/w3/w2; Hugging
+# Face decoder layers use self_attn.{q,k,v,o}_proj and mlp.{gate,up,down}_proj
+# (src/spmv/nmsparse_linear.py:83-91).
+_ATTENTION_LAYOUTS = (
+    ("attention", ("wqkv", "wo")),
+    ("self_attn", ("q_proj", "k_proj", "v_proj", "o_proj")),
+)
+_MLP_LAYOUTS = (
+    ("feed_forward", ("w1", "w3", "w2")),
+    ("mlp", ("gate_proj", "up_proj", "down_proj")),
+)
+
+
+def _resolve_layout(blk, layouts, kind):
+    """The (sub-module, Linear names) of the first known layout `blk` has."""
+    for attr, names in layouts:
+        sub = getattr(blk, attr, None)
+        if sub is not None:
+            return sub, names
+    known = ", ".join(f".{attr}" for attr, _ in layouts)
+    raise AttributeError(
+        f"decoder block {type(blk).__name__} has none of the known {kind} sub-modules ({known}); "
+        "swap_to_nmsparse does not recognize this block's layout."
+    )
+
+
+def _swap_linears(submodule, names, M, device, seed, cnt):
+    """Replace submodule.<name> for each name, numbering seeds from seed + cnt."""
+    for name in names:
+        old = getattr(submodule, name)
+        N, K = old.weight.shape
+        dense = None if DECODE_ONLY else old.weight
+        del old
+        torch.cuda.empty_cache()
+        setattr(submodule, name, NmSparseLinear(N, K, M, seed + cnt, device, dense_weight=dense))
+        cnt += 1
+    return cnt
+
+
+def swap_to_nmsparse(model, M, device, seed=0, block_devices=None):
+    """Swap every attention and MLP Linear of `model.layers` to NmSparseLinear.
+
+    Blocks are visited in order, attention before MLP, Linears in layout
+    order; the j-th swapped Linear uses seed `seed + j`. `block_devices`
+    optionally gives one device (index or "cuda:N") per block. Returns the
+    number of swapped Linears.
+    """
+    cnt = 0
+    for i, blk in enumerate(model.layers):
+        blk_device = device
+        if block_devices is not None:
+            d = block_devices[i]
+            blk_device = d if isinstance(d, str) else f"cuda:{d}"
+        attn, attn_names = _resolve_layout(blk, _ATTENTION_LAYOUTS, "attention")
+        cnt = _swap_linears(attn, attn_names, M, blk_device, seed, cnt)
+        mlp, mlp_names = _resolve_layout(blk, _MLP_LAYOUTS, "feed-forward")
+        cnt = _swap_linears(mlp, mlp_names, M, blk_device, seed, cnt)
+    return cnt
+
+
+__all__ = ["NmSparseLinear", "swap_to_nmsparse", "pack_dense", "_make_sparse"]

@@ -1,0 +1,122 @@
+"""C-ABI checks that need no GPU: the library loads, exports exactly what
+include/nmsparse_hip.h declares, and rejects bad arguments before launching.
+
+Every call below that passes placeholder device pointers carries an argument
+the library rejects before any HIP call, so no kernel is ever launched.
+"""
+import ctypes
+import re
+import subprocess
+
+import pytest
+
+from conftest import ROOT
+from spmv_decode_amd import _lib
+
+HEADER = ROOT / "include" / "nmsparse_hip.h"
+FAKE = 0x10000  # 256-byte aligned placeholder address, never dereferenced
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return set(re.findall(r"\b(nm_[a-z0-9_]+)\s*\(", text))
+
+
+def test_header_declarations_match_binding_table():
+    assert _declared_functions() == set(_lib.ABI)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True, text=True,
+                         check=True).stdout
+    exported = {line.split()[-1] for line in out.splitlines() if " T " in line}
+    for name in _declared_functions():
+        assert name in exported, name
+        assert getattr(lib, name) is not None
+    assert lib.nm_abi_version() == _lib.ABI_VERSION
+
+
+def test_constants_match_header():
+    text = HEADER.read_text()
+    assert f"#define NM_TICKET_BYTES {_lib.NM_TICKET_BYTES}" in text
+    for code, name in _lib.NM_ERR.items():
+        assert re.search(rf"#define {name} \({code}\)", text), name
+    assert "#define NM_DTYPE_F16 0" in text and "#define NM_DTYPE_BF16 1" in text and "#define NM_DTYPE_F32 2" in text
+
+
+def _gemv(fn="nm_gemv_f16", vec=FAKE, stride=1, md=FAKE, mi=FAKE, out=FAKE, ws=FAKE, ws_bytes=1 << 30,
+          h=4096, w=2048, nnz=32, m=64):
+    return getattr(_lib.load(), fn)(vec, stride, md, mi, out, ws, ws_bytes, h, w, nnz, m, None)
+
+
+@pytest.mark.parametrize("fn", ["nm_gemv_f16", "nm_gemv_bf16", "nm_gemv_f32"])
+def test_rejections_before_launch(fn):
+    assert _gemv(fn, vec=None) == -1
+    assert _gemv(fn, md=None) == -1
+    assert _gemv(fn, mi=None) == -1
+    assert _gemv(fn, out=None) == -1
+    assert _gemv(fn, ws=None) == -1
+    assert _gemv(fn, h=100) == -3
+    assert _gemv(fn, h=0) == -2
+    assert _gemv(fn, w=2047) == -4
+    assert _gemv(fn, nnz=0) == -2
+    assert _gemv(fn, nnz=65, m=64) == -2
+    assert _gemv(fn, m=257, nnz=2) == -2
+    assert _gemv(fn, stride=0) == -2
+    assert _gemv(fn, md=FAKE + 2) == -5
+    assert _gemv(fn, out=FAKE + 8) == -5
+    assert _gemv(fn, ws=FAKE + 16) == -5
+    assert _gemv(fn, ws_bytes=1024) == -6
+
+
+def test_ex_rejects_bad_dtype_and_config():
+    lib = _lib.load()
+    args = (FAKE, 1, FAKE, FAKE, FAKE, FAKE, 1 << 30, 4096, 2048, 32, 64)
+    assert lib.nm_gemv_ex(3, *args, -1, 0, None) == -7
+    assert lib.nm_gemv_ex(0, *args, lib.nm_num_configs(), 0, None) == -7
+    assert lib.nm_gemv_workspace_bytes_ex(4096, 2048, 32, 64, 999, 0) == 0
+
+
+def test_workspace_and_plan_invariants():
+    lib = _lib.load()
+    n = _lib.num_configs()
+    assert n >= 1
+    shapes = [(3072, 512, 2, 4), (4096, 2048, 32, 64), (1024, 2048, 32, 64), (14336, 2048, 32, 64),
+              (4096, 7168, 32, 64), (128, 2, 2, 4), (384, 96, 3, 4), (128256, 2048, 32, 64), (5120, 12800, 8, 16)]
+    for h, w, nnz, m in shapes:
+        for cfg in [-1, *range(n)]:
+            for splits in (0, 1, 3, 1000):
+                p = _lib.plan(h, w, nnz, m, cfg, splits)
+                th = int(re.match(r"th(\d+)_u(\d+)", p["config"]).group(1))
+                u = int(re.match(r"th(\d+)_u(\d+)", p["config"]).group(2))
+                chunk = (256 // th) * u
+                tiles = -(-h // (8 * th))
+                assert p["blocks"] == tiles * p["splits"]
+                assert p["rows_per_split"] % chunk == 0 and 0 < p["rows_per_split"] <= 1024
+                assert (p["splits"] - 1) * p["rows_per_split"] < w <= p["splits"] * p["rows_per_split"]
+                need = lib.nm_gemv_workspace_bytes_ex(h, w, nnz, m, cfg, splits)
+                expect = _lib.NM_TICKET_BYTES + (p["splits"] * h * 4 if p["splits"] > 1 else 0)
+                assert need == expect
+        assert lib.nm_gemv_workspace_bytes(h, w, nnz, m) == lib.nm_gemv_workspace_bytes_ex(h, w, nnz, m, -1, 0)
+    assert lib.nm_gemv_workspace_bytes(100, 2048, 32, 64) == 0
+
+
+def test_strerror_names_every_code():
+    for code in [0, *_lib.NM_ERR]:
+        assert _lib.strerror(code)
+    assert "unknown" in _lib.strerror(-99)
+
+
+def test_describe_configs():
+    names = [_lib.describe(i) for i in range(_lib.num_configs())]
+    assert len(set(names)) == len(names)
+    buf = ctypes.create_string_buffer(8)
+    assert _lib.load().nm_config_describe(-1, buf, 8) == -7
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "absent.so")
+    monkeypatch.setattr(_lib, "_lib", None)
+    with pytest.raises(_lib.NmSparseLibraryError, match="not built"):
+        _lib.load()
