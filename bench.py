@@ -79,8 +79,7 @@ def main():
     nnz, m = (int(v) for v in args.ratio.split(":"))
 
     import torch
-    import torch.nn.functional as F
-
+    
     from spmv_decode_amd import _lib, hip_spmv
 
     dev = torch.device("cuda:0")
@@ -126,20 +125,6 @@ def main():
             fn()
         torch.cuda.synchronize()
         return g
-
-    def time_graph(g, reps, warm):
-        for _ in range(warm):
-            g.replay()
-        torch.cuda.synchronize()
-        s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        samples = []
-        for _ in range(reps):
-            s.record()
-            g.replay()
-            e.record()
-            e.synchronize()
-            samples.append(s.elapsed_time(e))
-        return samples
 
     def step():
         for li in range(L):
@@ -192,26 +177,28 @@ def main():
         print(json.dumps(result), flush=True)
         return
 
-    # ---- per-shape launch times (sparse) --------------------------------------
+    # ---- per-shape launch times, weights rotated over >= 1 GiB --------------
+    from spmv_decode_amd import microbench as MB
+
     per_shape = {}
     classes = {"q_o": ("q_proj", "o_proj"), "k_v": ("k_proj", "v_proj"), "gate_up": ("gate_proj", "up_proj"),
                "down": ("down_proj",)}
     reps = max(10, args.steps // 2)
     for cls, names in classes.items():
-        name = names[0]
-        K, h = SHAPES[name]
-        g = capture(lambda: [gemv(name, li) for li in range(L)])
-        samples = time_graph(g, reps, 3)
-        us = statistics.median(samples) * 1e3 / L
+        K, h = SHAPES[names[0]]
+        case = MB.RotatingCase(h, K, nnz, m, torch.float16, rotate_bytes=1 << 30, seed=7)
+        us = MB.time_sparse(case, reps=reps)
         b = sparse_bytes(K, h, nnz, m)
         plan = _lib.plan(h, (K // m) * nnz, nnz, m)
         per_shape[cls] = {"K": K, "h": h, "launches_per_step": L * len(names), "us_per_launch": round(us, 3),
                           "bytes_per_launch": b, "GBps": round(b / (us * 1e-6) / 1e9, 1),
                           "pct_peak": round(100 * b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
-                          "kernel_config": plan["config"], "splits": plan["splits"], "blocks": plan["blocks"]}
+                          "kernel_config": plan["config"], "splits": plan["splits"], "blocks": plan["blocks"],
+                          "rotated_copies": case.copies}
         log(f"sparse {cls:8s} K={K:5d} h={h:5d}: {us:7.2f} us/launch {per_shape[cls]['GBps']:7.1f} GB/s "
-            f"({per_shape[cls]['pct_peak']}%) {plan}")
-        del g
+            f"({per_shape[cls]['pct_peak']}%) {plan} x{case.copies} copies")
+        del case
+        torch.cuda.empty_cache()
     # dominant kernel: largest share of the step
     dom = max(per_shape, key=lambda c: per_shape[c]["us_per_launch"] * per_shape[c]["launches_per_step"])
     d = per_shape[dom]
@@ -240,22 +227,11 @@ def main():
         except Exception as exc:  # pragma: no cover - informational
             log(f"could not select hipBLASLt: {exc}")
         blas = str(torch.backends.cuda.preferred_blas_library())
-        dense = {}
         per_dense = {}
         dense_step_us = 0.0
         for cls, names in classes.items():
             K, h = SHAPES[names[0]]
-            Ws = [(torch.randn(h, K, generator=gen, device=dev) * 0.02).to(torch.float16) for _ in range(L)]
-            dense[cls] = Ws
-            xo = torch.empty(1, h, dtype=torch.float16, device=dev)
-
-            def dense_run(Ws=Ws, K=K, xo=xo):
-                for W in Ws:
-                    torch.matmul(xs[K], W.t(), out=xo)
-
-            g = capture(dense_run)
-            samples = time_graph(g, reps, 3)
-            us = statistics.median(samples) * 1e3 / L
+            us = MB.time_dense(h, K, torch.float16, rotate_bytes=1 << 30, reps=reps)
             b = dense_bytes(K, h)
             per_dense[cls] = {"us_per_launch": round(us, 3), "GBps": round(b / (us * 1e-6) / 1e9, 1),
                               "pct_peak": round(100 * b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
@@ -263,8 +239,6 @@ def main():
             dense_step_us += us * L * len(names)
             log(f"dense  {cls:8s}: {us:7.2f} us/launch {per_dense[cls]['GBps']:7.1f} GB/s "
                 f"-> sparse speedup {per_dense[cls]['speedup_sparse_vs_dense']}x")
-            del g, Ws
-            dense.pop(cls)
             torch.cuda.empty_cache()
         sparse_step_us = sum(per_shape[c]["us_per_launch"] * per_shape[c]["launches_per_step"] for c in per_shape)
         result["dense_fp16_baseline"] = {

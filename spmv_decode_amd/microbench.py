@@ -1,0 +1,224 @@
+"""Kernel timing harness for the N:M sparse GEMV (role of the reference's
+microbench_triton_torchmv.py, re-designed for MI355X).
+
+    python -m spmv_decode_amd.microbench [--dims 4096x4096,...] [--ratios 2:4,...]
+        [--dtype fp16|bf16] [--sweep] [--rotate-mib 1024] [--csv out.csv]
+
+Differences from the reference harness (microbench_triton_torchmv.py:218-364):
+* Weights are rotated over enough distinct copies (default >= 1 GiB) that
+  every timed launch streams from HBM, not from the 256 MB Infinity Cache.
+* Launches are captured in a hipGraph and replayed; time per launch is the
+  replay time divided by the number of launches (HIP events on the stream).
+* `--sweep` times every kernel configuration and split count of the static
+  table (the replacement for Triton autotuning, triton_spmv.py:40-55,
+  122-148) and reports the fastest; the library's own choice is `cfg=-1`.
+* Correctness uses the harness's own fp32 dense reference on the scattered
+  masked weight, like the reference (microbench_triton_torchmv.py:371-430),
+  and reports max_abs / mean_abs / rmse / rel_l2.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+import math
+import statistics
+import sys
+from pathlib import Path
+
+import torch
+
+from . import _lib
+from .hip_spmv import nmsparse_spmv_forward_hip
+
+HBM_PEAK_GBS = 8000.0
+DEFAULT_DIMS = [(4096, 4096), (1024, 4096), (14336, 4096), (4096, 14336)]  # (n_out, n_in) Llama-3.1-8B
+DEFAULT_RATIOS = [(2, 4), (4, 8), (8, 16), (16, 32), (32, 64), (64, 128), (128, 256)]
+DTYPES = {"fp16": torch.float16, "bf16": torch.bfloat16, "fp32": torch.float32}
+
+
+def sparse_bytes(n_in: int, n_out: int, nnz: int, m: int, elem: int = 2) -> int:
+    """Algorithmic bytes of one GEMV: packed weights + index bytes + activations + outputs."""
+    w = (n_in // m) * nnz
+    return elem * w * n_out + w + elem * n_in + elem * n_out
+
+
+def dense_bytes(n_in: int, n_out: int, elem: int = 2) -> int:
+    return elem * n_in * n_out + elem * n_in + elem * n_out
+
+
+def make_patterns(banks: int, m: int, nnz: int, gen: torch.Generator, device) -> torch.Tensor:
+    """Seeded random sorted in-group positions [banks, nnz] uint8 on `device`."""
+    keys = torch.rand(banks, m, generator=gen, device=device)
+    return keys.argsort(dim=1)[:, :nnz].sort(dim=1).values.to(torch.uint8).contiguous()
+
+
+class RotatingCase:
+    """`copies` independent packed weights of one shape, plus one activation vector."""
+
+    def __init__(self, n_out, n_in, nnz, m, dtype=torch.float16, rotate_bytes=1 << 30, min_copies=1,
+                 seed=0, device="cuda", wstd=0.02):
+        self.n_out, self.n_in, self.nnz, self.m, self.dtype = n_out, n_in, nnz, m, dtype
+        self.w = (n_in // m) * nnz
+        self.bytes = sparse_bytes(n_in, n_out, nnz, m, torch.finfo(dtype).bits // 8)
+        self.copies = max(min_copies, math.ceil(rotate_bytes / self.bytes))
+        g = torch.Generator(device=device).manual_seed(seed)
+        banks = n_in // m
+        self.mats = []
+        for _ in range(self.copies):
+            mi = make_patterns(banks, m, nnz, g, device)
+            md = (torch.randn(self.w, n_out, generator=g, device=device) * wstd).to(dtype)
+            self.mats.append((md, mi))
+        self.x = torch.randn(1, n_in, generator=g, device=device).to(dtype)
+        self.out = torch.empty(1, n_out, dtype=dtype, device=device)
+
+    def launch(self, i, config_id=-1, splits=0):
+        md, mi = self.mats[i % self.copies]
+        return nmsparse_spmv_forward_hip(self.x, md, mi, self.w, self.n_out, self.nnz, 128, self.m, 1, self.n_in,
+                                         out=self.out, config_id=config_id, splits=splits)
+
+
+def graph_us_per_launch(launches, reps=20, warmup=3, stream=None) -> float:
+    """Capture `launches` (callables) in one hipGraph; median replay time / len in us."""
+    stream = stream or torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for fn in launches:
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=stream):
+        for fn in launches:
+            fn()
+    for _ in range(warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    s, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    samples = []
+    for _ in range(reps):
+        s.record()
+        g.replay()
+        e.record()
+        e.synchronize()
+        samples.append(s.elapsed_time(e) * 1e3 / len(launches))
+    del g
+    return statistics.median(samples)
+
+
+def dense_reference_check(case: RotatingCase, out: torch.Tensor) -> dict:
+    """fp32 dense matvec on the scattered masked weight vs `out` (copy 0)."""
+    md, mi = case.mats[0]
+    pos = (torch.arange(case.w, device=md.device) // case.nnz) * case.m + mi.reshape(-1).long()
+    dense = torch.zeros(case.n_out, case.n_in, dtype=torch.float32, device=md.device)
+    dense[:, pos] = md.float().t()
+    ref = torch.mv(dense, case.x.float().reshape(-1))
+    d = (ref - out.float().reshape(-1)).abs()
+    return {"max_abs": d.max().item(), "mean_abs": d.mean().item(), "rmse": d.pow(2).mean().sqrt().item(),
+            "rel_l2": (d.norm() / ref.norm().clamp_min(1e-12)).item()}
+
+
+def time_sparse(case: RotatingCase, config_id=-1, splits=0, reps=20) -> float:
+    return graph_us_per_launch([lambda i=i: case.launch(i, config_id, splits) for i in range(case.copies)], reps)
+
+
+def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda") -> float:
+    b = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
+    copies = max(1, math.ceil(rotate_bytes / b))
+    g = torch.Generator(device=device).manual_seed(seed)
+    Ws = [(torch.randn(n_out, n_in, generator=g, device=device) * 0.02).to(dtype) for _ in range(copies)]
+    x = torch.randn(1, n_in, generator=g, device=device).to(dtype)
+    o = torch.empty(1, n_out, dtype=dtype, device=device)
+    us = graph_us_per_launch([lambda W=W: torch.matmul(x, W.t(), out=o) for W in Ws], reps)
+    del Ws
+    return us
+
+
+def candidate_splits(case: RotatingCase):
+    return [0, 1, 2, 4, 8, 16, 24, 32, 48, 64, 96, 128, 192, 256]
+
+
+def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, csv_path=None, dense=True,
+        log=print):
+    dtype = DTYPES[dtype_name]
+    rows = []
+    try:
+        torch.backends.cuda.preferred_blas_library("cublaslt")
+    except Exception:
+        pass
+    for n_out, n_in in dims:
+        dense_us = time_dense(n_out, n_in, dtype, rotate_mib << 20, reps) if dense else float("nan")
+        db = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
+        log(f"--- ({n_out},{n_in}) dense {dense_us:.2f} us {db / dense_us / 1e3:.1f} GB/s")
+        for nnz, m in ratios:
+            case = RotatingCase(n_out, n_in, nnz, m, dtype, rotate_mib << 20)
+            plan = _lib.plan(n_out, case.w, nnz, m)
+            out = case.launch(0).clone()
+            err = dense_reference_check(case, out)
+            configs = [(-1, 0)]
+            if sweep:
+                configs += [(c, s) for c in range(_lib.num_configs()) for s in candidate_splits(case)]
+            best = None
+            seen = set()
+            for cfg, sp in configs:
+                p = _lib.plan(n_out, case.w, nnz, m, cfg, sp)
+                key = (p["config_id"], p["splits"])
+                if key in seen and cfg != -1:
+                    continue
+                seen.add(key)
+                us = time_sparse(case, cfg, sp, reps)
+                gbs = case.bytes / us / 1e3
+                row = {"n_out": n_out, "n_in": n_in, "ratio": f"{nnz}:{m}", "dtype": dtype_name,
+                       "config": p["config"] if cfg >= 0 else f"auto:{plan['config']}", "splits": p["splits"],
+                       "blocks": p["blocks"], "rows_per_split": p["rows_per_split"], "us": round(us, 3),
+                       "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                       "dense_us": round(dense_us, 3), "speedup_vs_dense": round(dense_us / us, 3),
+                       "copies": case.copies, **{k: float(f"{v:.3e}") for k, v in err.items()}}
+                rows.append(row)
+                if best is None or us < best["us"]:
+                    best = row
+            log(f"  {nnz}:{m} auto {rows[-len(seen)]['us']:.2f} us {rows[-len(seen)]['GBps']:.0f} GB/s | best "
+                f"{best['config']} s={best['splits']} {best['us']:.2f} us {best['GBps']:.0f} GB/s "
+                f"({best['pct_peak']}%) x{best['speedup_vs_dense']} vs dense | max_abs {err['max_abs']:.2e} "
+                f"rel_l2 {err['rel_l2']:.2e}")
+            del case
+            torch.cuda.empty_cache()
+    if csv_path:
+        Path(csv_path).parent.mkdir(parents=True, exist_ok=True)
+        with open(csv_path, "w", newline="") as f:
+            wr = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+            wr.writeheader()
+            wr.writerows(rows)
+    return rows
+
+
+def _parse_pairs(text, sep):
+    return [tuple(int(v) for v in item.split(sep)) for item in text.split(",") if item]
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--dims", default=",".join(f"{a}x{b}" for a, b in DEFAULT_DIMS), help="n_out x n_in list")
+    p.add_argument("--ratios", default=",".join(f"{a}:{b}" for a, b in DEFAULT_RATIOS))
+    p.add_argument("--dtype", default="fp16", choices=sorted(DTYPES))
+    p.add_argument("--sweep", action="store_true", help="time every config / split count")
+    p.add_argument("--rotate-mib", type=int, default=1024)
+    p.add_argument("--reps", type=int, default=20)
+    p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--csv", default=None)
+    p.add_argument("--json", default=None, help="write the best row per (shape, ratio) as JSON")
+    a = p.parse_args(argv)
+    rows = run(_parse_pairs(a.dims, "x"), _parse_pairs(a.ratios, ":"), a.dtype, a.sweep, a.rotate_mib, a.reps,
+               a.csv, not a.no_dense, log=lambda s: print(s, flush=True))
+    if a.json:
+        best = {}
+        for r in rows:
+            k = f"{r['n_out']}x{r['n_in']}_{r['ratio']}"
+            if k not in best or r["us"] < best[k]["us"]:
+                best[k] = r
+        Path(a.json).write_text(json.dumps(best, indent=1))
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

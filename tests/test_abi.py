@@ -93,7 +93,7 @@ def test_workspace_and_plan_invariants():
                 chunk = (256 // th) * u
                 tiles = -(-h // (8 * th))
                 assert p["blocks"] == tiles * p["splits"]
-                assert p["rows_per_split"] % chunk == 0 and 0 < p["rows_per_split"] <= 1024
+                assert p["rows_per_split"] % chunk == 0 and 0 < p["rows_per_split"] <= 2048
                 assert (p["splits"] - 1) * p["rows_per_split"] < w <= p["splits"] * p["rows_per_split"]
                 need = lib.nm_gemv_workspace_bytes_ex(h, w, nnz, m, cfg, splits)
                 expect = _lib.NM_TICKET_BYTES + (p["splits"] * h * 4 if p["splits"] > 1 else 0)

@@ -46,19 +46,25 @@ def check_parity(out, x, md, mi, nnz, m, tag=""):
     ref = O.gemv_f64(x.cpu(), md.cpu(), mi.cpu(), nnz, m)
     got = out.detach().float().cpu().numpy().reshape(-1)
     assert np.isfinite(got).all(), tag
+    # fp32 accumulation error bound of a sum of w products (each within one
+    # fp32 rounding): 4*sqrt(w)*eps32*sum|terms|, a probabilistic bound that
+    # a wrong term or index exceeds by orders of magnitude.
+    w = md.shape[0]
+    abs_terms = O.to_f64(md.cpu()).__abs__().T @ np.abs(O.gather_activations(x.cpu(), mi.cpu(), nnz, m))
+    acc_tol = 4.0 * np.sqrt(w) * 2.0 ** -24 * abs_terms
     dtype = out.dtype
     if dtype == torch.float32:
-        scale = max(float(np.abs(ref).max()), 1.0)
-        assert np.abs(got - ref).max() <= 1e-5 * scale, tag
+        bad = np.abs(got - ref) > acc_tol + 1e-30
+        assert not bad.any(), (tag, int(bad.sum()))
         return
     e = O.error_metrics(ref, got)
     if dtype == torch.float16:
         assert e["max_abs"] <= 1e-2 and e["rel_l2"] <= 1e-3, (tag, e)
-    # one ulp of the output type around the float64 value
+    # one ulp of the output type around the float64 value, plus accumulation
     exp = np.floor(np.log2(np.maximum(np.abs(ref), 1e-30)))
     exp = np.maximum(exp, MIN_NORMAL_EXP[dtype])
     ulp = np.exp2(exp - ULP_BITS[dtype])
-    bad = np.abs(got - ref) > ulp
+    bad = np.abs(got - ref) > ulp + acc_tol
     assert not bad.any(), (tag, int(bad.sum()), float(np.abs(got - ref)[bad].max()))
 
 
@@ -134,11 +140,14 @@ def test_power_of_two_scaling_and_determinism_full_size(gpu):
         y = run(x, md, mi, 32, 64)
         for _ in range(4):
             assert torch.equal(run(x, md, mi, 32, 64), y)
-        y2 = run(x * 2, md, mi, 32, 64)
-        assert torch.equal(y2, y * 2)
-        yq = run(x * 0.25, md, mi, 32, 64)
-        assert torch.equal(yq.float(), (y.float() * 0.25).half().float()) or \
-            (yq.float() - y.float() * 0.25).abs().max() <= 2 ** -24
+        # Doubling x doubles every fp32 term and sum exactly; rounding to fp16
+        # commutes with doubling except in the subnormal range (|y| < 2^-14),
+        # where the two can differ by one subnormal step (2^-24).
+        y2 = run(x * 2, md, mi, 32, 64).float()
+        ref2 = y.float() * 2
+        normal = y.float().abs() >= 2.0 ** -14
+        assert torch.equal(y2[normal], ref2[normal])
+        assert (y2[~normal] - ref2[~normal]).abs().max().item() <= 2.0 ** -24 if (~normal).any() else True
 
 
 def test_tickets_rearm_and_workspace_reuse(gpu):
