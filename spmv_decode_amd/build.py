@@ -17,6 +17,9 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 SOURCES = [PKG / "csrc" / "nm_gemv.hip"]
 LIB_PATH = PKG / "libnmsparse_hip.so"
+# Measurement-only streaming-read kernel used by the microbenchmark.
+PROBE_SOURCES = [PKG / "csrc" / "roofline_probe.hip"]
+PROBE_LIB_PATH = PKG / "libnm_roofline_probe.so"
 ARCH = "gfx950"
 
 # Packed-fp32 VALU ops are disabled for every HIP build of this project; the
@@ -39,18 +42,23 @@ def hipcc() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm)")
 
 
-def build_library(verbose: bool = False) -> Path:
-    """Compile the HIP sources to LIB_PATH (always recompiles)."""
-    tmp = LIB_PATH.with_suffix(".so.tmp")
-    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *map(str, SOURCES)]
+def _compile(sources, out: Path, verbose: bool) -> Path:
+    tmp = out.with_suffix(".so.tmp")
+    cmd = [hipcc(), *HIPCC_FLAGS, f"-I{ROOT / 'include'}", "-o", str(tmp), *map(str, sources)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         sys.stderr.write(res.stdout + res.stderr)
         raise RuntimeError(f"hipcc failed with exit code {res.returncode}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
+
+
+def build_library(verbose: bool = False) -> Path:
+    """Compile the GEMV library and the measurement probe (always recompiles)."""
+    _compile(PROBE_SOURCES, PROBE_LIB_PATH, verbose)
+    return _compile(SOURCES, LIB_PATH, verbose)
 
 
 if __name__ == "__main__":

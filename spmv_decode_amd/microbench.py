@@ -192,6 +192,58 @@ def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, 
     return rows
 
 
+def read_ceiling(sizes=(4_206_592, 16_795_648, 58_759_168, 268_435_456, 1 << 30), pool_bytes=2 << 30,
+                 blocks_list=(64, 128, 256, 512, 1024, 2048, 4096), us_list=(4, 8, 16), reps=10, log=print):
+    """Best time of one plain streaming-read launch per byte count: the
+    practical HBM ceiling for a bandwidth-bound kernel of that size. Reads
+    rotate through a `pool_bytes` buffer so no launch hits the Infinity Cache."""
+    import ctypes
+
+    from .build import PROBE_LIB_PATH
+
+    lib = ctypes.CDLL(str(PROBE_LIB_PATH))
+    lib.nm_probe_stream_read.restype = ctypes.c_int
+    lib.nm_probe_stream_read.argtypes = [ctypes.c_void_p, ctypes.c_longlong, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    buf = torch.randint(0, 255, (pool_bytes,), dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(max(blocks_list), dtype=torch.int32, device="cuda")
+    out = {}
+    for nb in sizes:
+        copies = min(256, max(1, pool_bytes // nb))
+        best = None
+        for blocks in blocks_list:
+            for u in us_list:
+                def launch(i, blocks=blocks, u=u, nb=nb):
+                    rc = lib.nm_probe_stream_read(buf.data_ptr() + i * nb, nb, blocks, u, sink.data_ptr(),
+                                                  torch.cuda.current_stream().cuda_stream)
+                    if rc != 0:
+                        raise RuntimeError(f"nm_probe_stream_read failed: {rc}")
+                us = graph_us_per_launch([lambda i=i: launch(i) for i in range(copies)], reps)
+                if best is None or us < best[0]:
+                    best = (us, blocks, u)
+        out[nb] = {"us": round(best[0], 3), "GBps": round(nb / best[0] / 1e3, 1), "blocks": best[1], "u": best[2]}
+        log(f"read ceiling {nb / 1e6:9.1f} MB: {best[0]:8.2f} us {nb / best[0] / 1e3:7.0f} GB/s "
+            f"(blocks {best[1]}, {best[2]} loads/lane)")
+    return out
+
+
+def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
+    """Workload for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
+    three copies of a 256 MiB buffer (the known-size calibration kernel), then
+    three GEMV launches per shape, each on distinct weights."""
+    x = torch.empty(128 << 20, dtype=torch.float16, device="cuda").normal_()
+    y = torch.empty_like(x)
+    for _ in range(3):
+        y.copy_(x)
+    torch.cuda.synchronize()
+    for n_out, n_in in shapes:
+        case = RotatingCase(n_out, n_in, nnz, m, rotate_bytes=0, min_copies=3, seed=3)
+        for i in range(3):
+            case.launch(i)
+        torch.cuda.synchronize()
+        log(f"traffic probe: {n_out}x{n_in} {nnz}:{m} plan {_lib.plan(n_out, case.w, nnz, m)}")
+
+
 def _parse_pairs(text, sep):
     return [tuple(int(v) for v in item.split(sep)) for item in text.split(",") if item]
 
@@ -207,7 +259,17 @@ def main(argv=None):
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--csv", default=None)
     p.add_argument("--json", default=None, help="write the best row per (shape, ratio) as JSON")
+    p.add_argument("--read-ceiling", action="store_true", help="measure plain streaming-read launches only")
+    p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
     a = p.parse_args(argv)
+    if a.read_ceiling:
+        res = read_ceiling(log=lambda s: print(s, flush=True))
+        if a.json:
+            Path(a.json).write_text(json.dumps({str(k): v for k, v in res.items()}, indent=1))
+        return 0
+    if a.traffic_probe:
+        traffic_probe(_parse_pairs(a.dims, "x"), log=lambda s: print(s, flush=True))
+        return 0
     rows = run(_parse_pairs(a.dims, "x"), _parse_pairs(a.ratios, ":"), a.dtype, a.sweep, a.rotate_mib, a.reps,
                a.csv, not a.no_dense, log=lambda s: print(s, flush=True))
     if a.json:
