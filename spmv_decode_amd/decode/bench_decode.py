@@ -1,0 +1,124 @@
+"""End-to-end decode benchmark: random-init decoder, dense fp16 vs N:M sparse.
+
+    python -m spmv_decode_amd.decode.bench_decode --model llama-3.1-8b --m 64 \\
+        [--prompt 128] [--gen 256] [--no-dense] [--json out.json]
+
+Protocol: random-init weights of the named architecture
+in fp16 on one GPU; the prompt (seeded random token ids) is fed one token per
+graph replay (untimed), then `--gen` greedy decode steps are replayed from one
+captured hipGraph and timed with HIP events. Dense first (nn.Linear ->
+hipBLASLt), then every q/k/v/o/gate/up/down Linear is swapped to
+NmSparseLinear at N:M = (M/2):M with on-device synthetic patterns, and the
+same protocol runs again. Embeddings, norms and lm_head stay dense in both.
+Prints a `RESULT` line per model variant (like the reference benchmarks,
+benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:186-189) and one JSON line.
+"""
+from __future__ import annotations
+
+import argparse
+import gc
+import json
+import sys
+import time
+
+import torch
+
+from ..nmsparse_linear import swap_to_nmsparse
+from .model import CONFIGS, Decoder, init_weights_
+from .runner import GraphDecoder
+
+
+def linear_bytes(cfg, m: int) -> int:
+    """Algorithmic bytes of one token's Linear weights (dense when m == 0)."""
+    qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+    shapes = [(cfg.dim, qd), (cfg.dim, kvd), (cfg.dim, kvd), (qd, cfg.dim), (cfg.dim, cfg.inter),
+              (cfg.dim, cfg.inter), (cfg.inter, cfg.dim)]
+    total = 0
+    for K, h in shapes:
+        if m:
+            w = K // 2
+            total += 2 * w * h + w + 2 * K + 2 * h
+        else:
+            total += 2 * K * h + 2 * K + 2 * h
+    return total * cfg.n_layers
+
+
+def run_variant(model, cfg, prompt, gen, label, log):
+    dec = GraphDecoder(model, prompt.numel() + gen + 8)
+    t0 = time.time()
+    dec.capture()
+    log(f"{label}: captured decode step in {time.time() - t0:.1f} s")
+    dec.run_prompt(prompt)
+    ids, ms_mean, ms_median = dec.generate(gen)
+    ok = bool(torch.isfinite(dec.logits).all().item())
+    del dec
+    return {"ms_per_token": round(ms_mean, 4), "ms_per_token_median_of_16": round(ms_median, 4),
+            "tokens_per_s": round(1e3 / ms_mean, 2), "finite_logits": ok,
+            "first_tokens": ids[:8].tolist()}
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    p.add_argument("--model", default="llama-3.1-8b", choices=sorted(CONFIGS))
+    p.add_argument("--m", type=int, default=64, help="group size M (N = M/2 kept); 0 = dense only")
+    p.add_argument("--prompt", type=int, default=128)
+    p.add_argument("--gen", type=int, default=256)
+    p.add_argument("--seed", type=int, default=0)
+    p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--json", default=None)
+    a = p.parse_args(argv)
+
+    def log(msg):
+        print(f"[decode] {msg}", file=sys.stderr, flush=True)
+
+    cfg = CONFIGS[a.model]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    try:
+        torch.backends.cuda.preferred_blas_library("cublaslt")  # hipBLASLt on ROCm
+    except Exception:
+        pass
+    torch.manual_seed(a.seed)
+    t0 = time.time()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device(dev):
+            model = Decoder(cfg)
+    finally:
+        torch.set_default_dtype(prev)
+    init_weights_(model, seed=a.seed)
+    model.eval()
+    log(f"{cfg.name}: {sum(p.numel() for p in model.parameters()) / 1e9:.2f} B params built in {time.time() - t0:.1f} s")
+    prompt = torch.randint(0, cfg.vocab, (a.prompt,), generator=torch.Generator().manual_seed(a.seed + 1))
+    res = {"model": cfg.name, "prompt": a.prompt, "gen": a.gen, "dtype": "fp16", "batch": 1,
+           "gpu": torch.cuda.get_device_name(dev)}
+    if not a.no_dense:
+        d = run_variant(model, cfg, prompt, a.gen, "dense", log)
+        d["linear_bytes_per_token"] = linear_bytes(cfg, 0)
+        res["dense"] = d
+        print(f"RESULT model={cfg.name} dense_float16 prompt={a.prompt} gen={a.gen} "
+              f"decode_ms_per_token={d['ms_per_token']:.6f} median={d['ms_per_token_median_of_16']:.6f}", flush=True)
+    if a.m:
+        t0 = time.time()
+        n = swap_to_nmsparse(model, a.m, "cuda", seed=a.seed, init="device", keep_dense=False)
+        gc.collect()
+        torch.cuda.empty_cache()
+        log(f"swapped {n} Linears to {a.m // 2}:{a.m} in {time.time() - t0:.1f} s")
+        s = run_variant(model, cfg, prompt, a.gen, "sparse", log)
+        s["linear_bytes_per_token"] = linear_bytes(cfg, a.m)
+        s["ratio"] = f"{a.m // 2}:{a.m}"
+        res["sparse"] = s
+        print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) prompt={a.prompt} gen={a.gen} "
+              f"decode_ms_per_token={s['ms_per_token']:.6f} median={s['ms_per_token_median_of_16']:.6f}", flush=True)
+        if "dense" in res:
+            res["speedup_sparse_vs_dense"] = round(res["dense"]["ms_per_token"] / s["ms_per_token"], 4)
+    print(json.dumps(res), flush=True)
+    if a.json:
+        with open(a.json, "w") as f:
+            json.dump(res, f, indent=1)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,204 @@
+"""A compact Llama-3.1 / Qwen3 decoder for batch-1 decode on MI355X.
+
+This is the caller of the sparse GEMV on the decode path (the role of the
+reference's gpt-fast `model.py` / Hugging Face Qwen3): every
+attention and MLP projection is a `nn.Linear` under the Hugging Face names
+(`self_attn.{q,k,v,o}_proj`, `mlp.{gate,up,down}_proj`) on `model.layers`, so
+`swap_to_nmsparse(model, M, device)` turns each into an `NmSparseLinear`
+unchanged. Only decode (one token per step) is implemented: the KV cache is
+static, the position is a device tensor, and a step contains no host
+synchronisation, so it can be captured once in a hipGraph and replayed.
+
+Numerics follow the published architectures: RMSNorm in fp32, rotary
+embeddings in the split-half ("rotate half") convention with Llama-3.1's
+frequency scaling, grouped-query attention with fp32 softmax, SiLU-gated MLP,
+Qwen3's per-head RMSNorm on queries and keys before the rotary embedding.
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass, field
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+
+@dataclass(frozen=True)
+class DecoderConfig:
+    name: str
+    n_layers: int
+    dim: int
+    n_heads: int
+    n_kv_heads: int
+    head_dim: int
+    inter: int
+    vocab: int
+    rope_theta: float
+    norm_eps: float
+    qk_norm: bool = False
+    rope_scaling: dict | None = field(default=None, hash=False, compare=False)
+
+
+LLAMA31_8B = DecoderConfig("llama-3.1-8b", 32, 4096, 32, 8, 128, 14336, 128256, 500000.0, 1e-5, False,
+                           dict(factor=8.0, low_freq_factor=1.0, high_freq_factor=4.0,
+                                original_max_position_embeddings=8192))
+QWEN3_14B = DecoderConfig("qwen3-14b", 40, 5120, 40, 8, 128, 17408, 151936, 1000000.0, 1e-6, True)
+QWEN3_32B = DecoderConfig("qwen3-32b", 64, 5120, 64, 8, 128, 25600, 151936, 1000000.0, 1e-6, True)
+QWEN3_06B = DecoderConfig("qwen3-0.6b", 28, 1024, 16, 8, 128, 3072, 151936, 1000000.0, 1e-6, True)
+CONFIGS = {c.name: c for c in (LLAMA31_8B, QWEN3_14B, QWEN3_32B, QWEN3_06B)}
+
+
+def tiny_config(qk_norm: bool = False, n_layers: int = 2) -> DecoderConfig:
+    """A small config with the same structure, for tests."""
+    return DecoderConfig("tiny", n_layers, 256, 4, 2, 64, 384, 512, 10000.0, 1e-5, qk_norm)
+
+
+def rope_inv_freq(cfg: DecoderConfig) -> torch.Tensor:
+    """Inverse rotary frequencies (float64), with Llama-3.1 scaling when configured:
+    wavelengths shorter than original/high_freq_factor keep their frequency,
+    longer than original/low_freq_factor are divided by `factor`, and the band
+    between is interpolated linearly in original_len/wavelength."""
+    half = cfg.head_dim // 2
+    inv = 1.0 / (cfg.rope_theta ** (torch.arange(half, dtype=torch.float64) * 2.0 / cfg.head_dim))
+    sc = cfg.rope_scaling
+    if sc:
+        orig = sc["original_max_position_embeddings"]
+        lo, hi, factor = sc["low_freq_factor"], sc["high_freq_factor"], sc["factor"]
+        wavelen = 2 * math.pi / inv
+        smooth = ((orig / wavelen) - lo) / (hi - lo)
+        scaled = torch.where(wavelen > orig / lo, inv / factor, inv)
+        mid = (wavelen <= orig / lo) & (wavelen >= orig / hi)
+        scaled = torch.where(mid, (1 - smooth) * inv / factor + smooth * inv, scaled)
+        inv = scaled
+    return inv
+
+
+class RMSNorm(nn.Module):
+    def __init__(self, dim: int, eps: float):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return xf.to(x.dtype) * self.weight
+
+
+def rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
+    """Rotary embedding, split-half convention, computed in fp32. x: [..., head_dim]."""
+    xf = x.float()
+    h = xf.shape[-1] // 2
+    x1, x2 = xf[..., :h], xf[..., h:]
+    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+
+
+class Attention(nn.Module):
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.cfg = cfg
+        qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        self.q_proj = nn.Linear(cfg.dim, qd, bias=False)
+        self.k_proj = nn.Linear(cfg.dim, kvd, bias=False)
+        self.v_proj = nn.Linear(cfg.dim, kvd, bias=False)
+        self.o_proj = nn.Linear(qd, cfg.dim, bias=False)
+        if cfg.qk_norm:
+            self.q_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
+            self.k_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
+
+    def forward(self, x, cos, sin, k_cache_t, v_cache, pos, mask):
+        """x [1, 1, dim]; k_cache_t [kvh, head_dim, S] (pre-transposed keys);
+        v_cache [kvh, S, head_dim]; pos [1] int64; mask [S] additive fp32."""
+        c = self.cfg
+        g = c.n_heads // c.n_kv_heads
+        q = self.q_proj(x).view(c.n_heads, c.head_dim)
+        k = self.k_proj(x).view(c.n_kv_heads, c.head_dim)
+        v = self.v_proj(x).view(c.n_kv_heads, c.head_dim)
+        if c.qk_norm:
+            q = self.q_norm(q)
+            k = self.k_norm(k)
+        q = rotate(q, cos, sin)
+        k = rotate(k, cos, sin)
+        k_cache_t.index_copy_(2, pos, k.unsqueeze(-1))
+        v_cache.index_copy_(1, pos, v.unsqueeze(1))
+        qg = q.view(c.n_kv_heads, g, c.head_dim)
+        scores = torch.bmm(qg, k_cache_t).float() * (1.0 / math.sqrt(c.head_dim)) + mask
+        probs = torch.softmax(scores, dim=-1).to(x.dtype)
+        y = torch.bmm(probs, v_cache)  # [kvh, g, head_dim]
+        return self.o_proj(y.reshape(1, 1, c.n_heads * c.head_dim))
+
+
+class MLP(nn.Module):
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.gate_proj = nn.Linear(cfg.dim, cfg.inter, bias=False)
+        self.up_proj = nn.Linear(cfg.dim, cfg.inter, bias=False)
+        self.down_proj = nn.Linear(cfg.inter, cfg.dim, bias=False)
+
+    def forward(self, x):
+        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+
+
+class Block(nn.Module):
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.input_layernorm = RMSNorm(cfg.dim, cfg.norm_eps)
+        self.self_attn = Attention(cfg)
+        self.post_attention_layernorm = RMSNorm(cfg.dim, cfg.norm_eps)
+        self.mlp = MLP(cfg)
+
+    def forward(self, x, cos, sin, k_cache_t, v_cache, pos, mask):
+        h = x + self.self_attn(self.input_layernorm(x), cos, sin, k_cache_t, v_cache, pos, mask)
+        return h + self.mlp(self.post_attention_layernorm(h))
+
+
+class Decoder(nn.Module):
+    """Decoder stack with a static KV cache; `model.layers` is what
+    `swap_to_nmsparse` walks."""
+
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.cfg = cfg
+        self.embed_tokens = nn.Embedding(cfg.vocab, cfg.dim)
+        self.layers = nn.ModuleList(Block(cfg) for _ in range(cfg.n_layers))
+        self.norm = RMSNorm(cfg.dim, cfg.norm_eps)
+        self.lm_head = nn.Linear(cfg.dim, cfg.vocab, bias=False)
+        self.max_seq = 0
+
+    def setup_cache(self, max_seq: int, device, dtype=torch.float16):
+        c = self.cfg
+        self.max_seq = max_seq
+        self.k_cache_t = [torch.zeros(c.n_kv_heads, c.head_dim, max_seq, device=device, dtype=dtype)
+                          for _ in range(c.n_layers)]
+        self.v_cache = [torch.zeros(c.n_kv_heads, max_seq, c.head_dim, device=device, dtype=dtype)
+                        for _ in range(c.n_layers)]
+        t = torch.arange(max_seq, dtype=torch.float64)
+        ang = torch.outer(t, rope_inv_freq(c))
+        self.rope_cos = ang.cos().float().to(device)
+        self.rope_sin = ang.sin().float().to(device)
+        self.positions = torch.arange(max_seq, device=device)
+
+    def forward_step(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
+        """One decode step: token [1, 1] int64 and pos [1] int64 on the device
+        -> logits [1, vocab]. No host synchronisation."""
+        x = self.embed_tokens(token)  # [1, 1, dim]
+        cos = self.rope_cos.index_select(0, pos)
+        sin = self.rope_sin.index_select(0, pos)
+        mask = torch.where(self.positions <= pos, 0.0, float("-inf")).float()
+        for i, layer in enumerate(self.layers):
+            x = layer(x, cos, sin, self.k_cache_t[i], self.v_cache[i], pos, mask)
+        return self.lm_head(self.norm(x)).view(1, -1)
+
+
+def init_weights_(model: Decoder, seed: int = 0, std: float = 0.02) -> Decoder:
+    """Random-init every weight in place on its device (N(0, std) for
+    matrices and embeddings, ones for norms)."""
+    gen = torch.Generator(device=next(model.parameters()).device).manual_seed(seed)
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if name.endswith("norm.weight"):
+                p.fill_(1.0)
+            else:
+                p.normal_(0.0, std, generator=gen)
+    return model

@@ -1,0 +1,119 @@
+"""hipGraph-captured greedy decode for `Decoder` (dense or N:M-sparse Linears).
+
+One replay of the captured graph runs one decode step entirely on the device:
+embed the current token, run every layer (KV cache written at the device-side
+position), final norm and lm_head, greedy argmax, store the token, advance the
+position. The host only replays the graph, so per-token time is GPU time
+(the reference captures a fixed-position step in a CUDA graph,
+benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:155-180; here the position moves).
+"""
+from __future__ import annotations
+
+import statistics
+
+import torch
+
+from .model import Decoder
+
+
+class GraphDecoder:
+    def __init__(self, model: Decoder, max_seq: int, device="cuda"):
+        self.model = model
+        self.device = torch.device(device)
+        model.setup_cache(max_seq, self.device, dtype=model.embed_tokens.weight.dtype)
+        self.max_seq = max_seq
+        self.host_pos = 0  # host mirror of `pos`: no step may index past the static cache
+        self.token = torch.zeros(1, 1, dtype=torch.long, device=self.device)
+        self.pos = torch.zeros(1, dtype=torch.long, device=self.device)
+        self.tokens = torch.zeros(max_seq + 1, dtype=torch.long, device=self.device)
+        self.logits = None
+        self.graph = None
+        self.stream = torch.cuda.Stream(device=self.device)
+
+    @torch.no_grad()
+    def _step(self):
+        logits = self.model.forward_step(self.token, self.pos)
+        nxt = torch.argmax(logits, dim=-1)  # [1]
+        self.tokens.index_copy_(0, self.pos + 1, nxt)
+        self.token.copy_(nxt.view(1, 1))
+        self.pos.add_(1)
+        return logits
+
+    def _advance(self, n: int = 1):
+        if self.host_pos + n > self.max_seq:
+            raise RuntimeError(f"decode past the static cache: position {self.host_pos} + {n} > {self.max_seq}")
+        self.host_pos += n
+
+    @torch.no_grad()
+    def eager_step(self):
+        self._advance()
+        self.logits = self._step()
+        return self.logits
+
+    @torch.no_grad()
+    def capture(self, warmup: int = 2):
+        """Warm up on the capture stream (creates every workspace the sparse
+        kernels need), then capture one step. Cache contents and counters are
+        reset afterwards."""
+        self.reset()
+        self.stream.wait_stream(torch.cuda.current_stream(self.device))
+        with torch.cuda.stream(self.stream):
+            for _ in range(min(warmup, self.max_seq)):
+                self._step()
+        torch.cuda.current_stream(self.device).wait_stream(self.stream)
+        torch.cuda.synchronize(self.device)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph, stream=self.stream):
+            self.logits = self._step()
+        torch.cuda.synchronize(self.device)
+        self.reset()
+
+    @torch.no_grad()
+    def reset(self, first_token: int = 0):
+        for k in self.model.k_cache_t:
+            k.zero_()
+        for v in self.model.v_cache:
+            v.zero_()
+        self.pos.zero_()
+        self.host_pos = 0
+        self.token.fill_(first_token)
+        self.tokens.zero_()
+
+    def replay(self):
+        self._advance()
+        self.graph.replay()
+
+    @torch.no_grad()
+    def run_prompt(self, prompt_ids: torch.Tensor):
+        """Feed prompt tokens one step at a time (untimed). After the last one
+        `token` holds the first generated token."""
+        ids = prompt_ids.to(self.device).view(-1)
+        self.reset(int(0))
+        self.tokens[0] = ids[0]
+        for i in range(ids.numel()):
+            self.token.copy_(ids[i].view(1, 1))
+            self.replay() if self.graph is not None else self.eager_step()
+
+    @torch.no_grad()
+    def generate(self, n: int, chunk: int = 16):
+        """n greedy steps by graph replay; returns (generated ids [n], ms/token,
+        median ms/token over chunks of `chunk` steps)."""
+        if self.host_pos + n > self.max_seq:
+            raise RuntimeError(f"decode past the static cache: position {self.host_pos} + {n} > {self.max_seq}")
+        first = self.host_pos + 1
+        ev = [torch.cuda.Event(enable_timing=True) for _ in range(n // chunk + 2)]
+        begin, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        begin.record()
+        k = 0
+        ev[0].record()
+        for i in range(n):
+            self.replay()
+            if (i + 1) % chunk == 0:
+                k += 1
+                ev[k].record()
+        end.record()
+        end.synchronize()
+        total = begin.elapsed_time(end)
+        chunks = [ev[j].elapsed_time(ev[j + 1]) / chunk for j in range(k)]
+        gen = self.tokens[first:first + n].clone()
+        return gen, total / n, (statistics.median(chunks) if chunks else total / n)

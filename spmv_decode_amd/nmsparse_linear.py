@@ -101,7 +101,7 @@ class NmSparseLinear(nn.Module):
     the reference does (src/spmv/nmsparse_linear.py:39).
     """
 
-    def __init__(self, N, K, M, seed, device, dense_weight=None):
+    def __init__(self, N, K, M, seed, device, dense_weight=None, *, init=None):
         super().__init__()
         assert K % M == 0 and N % 128 == 0, (K, N, M)
         self._weight_cpu = None
@@ -114,7 +114,7 @@ class NmSparseLinear(nn.Module):
                     torch.cuda.empty_cache()
             else:
                 self.weight = dense_weight
-        md, mi, w, nnz = _make_sparse(K, N, M, seed, device)
+        md, mi, w, nnz = _make_sparse(K, N, M, seed, device, init=init)
         self.register_buffer("mat_data", md)
         self.register_buffer("mat_index", mi)
         self.h, self.w, self.block_width, self.vec_width = N, w, nnz, M
@@ -181,26 +181,30 @@ def _resolve_layout(blk, layouts, kind):
     )
 
 
-def _swap_linears(submodule, names, M, device, seed, cnt):
+def _swap_linears(submodule, names, M, device, seed, cnt, init=None, keep_dense=None):
     """Replace submodule.<name> for each name, numbering seeds from seed + cnt."""
+    keep = (not DECODE_ONLY) if keep_dense is None else keep_dense
     for name in names:
         old = getattr(submodule, name)
         N, K = old.weight.shape
-        dense = None if DECODE_ONLY else old.weight
+        dense = old.weight if keep else None
         del old
+        setattr(submodule, name, None)
         torch.cuda.empty_cache()
-        setattr(submodule, name, NmSparseLinear(N, K, M, seed + cnt, device, dense_weight=dense))
+        setattr(submodule, name, NmSparseLinear(N, K, M, seed + cnt, device, dense_weight=dense, init=init))
         cnt += 1
     return cnt
 
 
-def swap_to_nmsparse(model, M, device, seed=0, block_devices=None):
+def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None, keep_dense=None):
     """Swap every attention and MLP Linear of `model.layers` to NmSparseLinear.
 
     Blocks are visited in order, attention before MLP, Linears in layout
     order; the j-th swapped Linear uses seed `seed + j`. `block_devices`
     optionally gives one device (index or "cuda:N") per block. Returns the
-    number of swapped Linears.
+    number of swapped Linears. Keyword-only extras of this build: `init`
+    ("reference" | "device", default from NM_SYNTH_INIT) and `keep_dense`
+    (default: not NM_DECODE_ONLY).
     """
     cnt = 0
     for i, blk in enumerate(model.layers):
@@ -209,9 +213,9 @@ def swap_to_nmsparse(model, M, device, seed=0, block_devices=None):
             d = block_devices[i]
             blk_device = d if isinstance(d, str) else f"cuda:{d}"
         attn, attn_names = _resolve_layout(blk, _ATTENTION_LAYOUTS, "attention")
-        cnt = _swap_linears(attn, attn_names, M, blk_device, seed, cnt)
+        cnt = _swap_linears(attn, attn_names, M, blk_device, seed, cnt, init, keep_dense)
         mlp, mlp_names = _resolve_layout(blk, _MLP_LAYOUTS, "feed-forward")
-        cnt = _swap_linears(mlp, mlp_names, M, blk_device, seed, cnt)
+        cnt = _swap_linears(mlp, mlp_names, M, blk_device, seed, cnt, init, keep_dense)
     return cnt
 
 

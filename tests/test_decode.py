@@ -1,0 +1,164 @@
+"""The decode-step caller (f1): KV-cached single-token decode vs an independent
+full-sequence reference, RoPE scaling, sparse swap, and hipGraph replay."""
+import math
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from spmv_decode_amd import NmSparseLinear, swap_to_nmsparse
+from spmv_decode_amd.decode.model import LLAMA31_8B, Decoder, init_weights_, rope_inv_freq, tiny_config
+
+
+def _llama31_freqs_loop(cfg):
+    """Per-frequency rule as published for Llama 3.1 rope scaling, in plain floats."""
+    sc = cfg.rope_scaling
+    out = []
+    for i in range(cfg.head_dim // 2):
+        f = 1.0 / (cfg.rope_theta ** (2 * i / cfg.head_dim))
+        wl = 2 * math.pi / f
+        lo_wl = sc["original_max_position_embeddings"] / sc["low_freq_factor"]
+        hi_wl = sc["original_max_position_embeddings"] / sc["high_freq_factor"]
+        if wl < hi_wl:
+            out.append(f)
+        elif wl > lo_wl:
+            out.append(f / sc["factor"])
+        else:
+            s = (sc["original_max_position_embeddings"] / wl - sc["low_freq_factor"]) / (
+                sc["high_freq_factor"] - sc["low_freq_factor"])
+            out.append((1 - s) * f / sc["factor"] + s * f)
+    return torch.tensor(out, dtype=torch.float64)
+
+
+def test_rope_scaling_matches_published_rule():
+    torch.testing.assert_close(rope_inv_freq(LLAMA31_8B), _llama31_freqs_loop(LLAMA31_8B), rtol=1e-12, atol=0)
+
+
+def _reference_logits(model, tokens):
+    """Full-sequence forward without a cache: causal attention recomputed over
+    all tokens, GQA by repeating KV heads. Independent of forward_step."""
+    c = model.cfg
+    T = tokens.numel()
+    x = model.embed_tokens(tokens.view(1, T))[0]  # [T, dim]
+    inv = rope_inv_freq(c)
+    ang = torch.outer(torch.arange(T, dtype=torch.float64), inv)
+    cos, sin = ang.cos().float(), ang.sin().float()
+
+    def rope(t):  # t [T, heads, hd]
+        h = t.shape[-1] // 2
+        a, b = t[..., :h], t[..., h:]
+        return torch.cat((a * cos[:, None] - b * sin[:, None], b * cos[:, None] + a * sin[:, None]), -1)
+
+    def rms(t, mod):
+        return (t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + mod.eps)) * mod.weight
+
+    for blk in model.layers:
+        at = blk.self_attn
+        hn = rms(x, blk.input_layernorm)
+        q = F.linear(hn, at.q_proj.weight).view(T, c.n_heads, c.head_dim)
+        k = F.linear(hn, at.k_proj.weight).view(T, c.n_kv_heads, c.head_dim)
+        v = F.linear(hn, at.v_proj.weight).view(T, c.n_kv_heads, c.head_dim)
+        if c.qk_norm:
+            q, k = rms(q, at.q_norm), rms(k, at.k_norm)
+        q, k = rope(q), rope(k)
+        rep = c.n_heads // c.n_kv_heads
+        k = k.repeat_interleave(rep, dim=1)
+        v = v.repeat_interleave(rep, dim=1)
+        s = torch.einsum("thd,shd->hts", q, k) / math.sqrt(c.head_dim)
+        s = s.masked_fill(torch.triu(torch.ones(T, T, dtype=torch.bool), 1), float("-inf"))
+        y = torch.einsum("hts,shd->thd", torch.softmax(s, -1), v).reshape(T, -1)
+        x = x + F.linear(y, at.o_proj.weight)
+        hn = rms(x, blk.post_attention_layernorm)
+        mlp = blk.mlp
+        x = x + F.linear(F.silu(F.linear(hn, mlp.gate_proj.weight)) * F.linear(hn, mlp.up_proj.weight),
+                         mlp.down_proj.weight)
+    return F.linear(rms(x, model.norm), model.lm_head.weight)
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_cached_decode_matches_full_sequence_reference(qk_norm):
+    torch.manual_seed(0)
+    model = Decoder(tiny_config(qk_norm=qk_norm)).float()
+    init_weights_(model, seed=1, std=0.05)
+    T = 9
+    tokens = torch.randint(0, model.cfg.vocab, (T,), generator=torch.Generator().manual_seed(2))
+    model.setup_cache(16, "cpu", dtype=torch.float32)
+    got = []
+    with torch.no_grad():
+        for t in range(T):
+            got.append(model.forward_step(tokens[t].view(1, 1), torch.tensor([t]))[0])
+        ref = _reference_logits(model, tokens)
+    torch.testing.assert_close(torch.stack(got), ref, rtol=1e-4, atol=1e-4)
+
+
+def test_swap_applies_to_decoder_layout():
+    model = Decoder(tiny_config())
+    n = swap_to_nmsparse(model, 8, "cpu", seed=3, keep_dense=False)
+    assert n == 7 * model.cfg.n_layers
+    blk = model.layers[0]
+    for mod in (blk.self_attn.q_proj, blk.self_attn.k_proj, blk.mlp.down_proj):
+        assert isinstance(mod, NmSparseLinear) and mod.weight is None
+    assert blk.self_attn.k_proj.h == model.cfg.n_kv_heads * model.cfg.head_dim
+
+
+# ---------------------------------------------------------------------------
+# GPU: graph replay and sparse vs masked-dense
+# ---------------------------------------------------------------------------
+def _masked_pair(cfg, M, seed=0):
+    """A dense fp16 model whose Linear weights are N:M-masked, and the sparse
+    model packed from exactly those weights (NmSparseLinear.from_dense)."""
+    torch.manual_seed(seed)
+    dense = Decoder(cfg).to("cuda", torch.float16)
+    init_weights_(dense, seed=seed, std=0.05)
+    sparse = Decoder(cfg).to("cuda", torch.float16)
+    sparse.load_state_dict(dense.state_dict())
+    g = torch.Generator(device="cuda").manual_seed(seed + 7)
+    for bd, bs in zip(dense.layers, sparse.layers):
+        for sub_d, sub_s, names in ((bd.self_attn, bs.self_attn, ("q_proj", "k_proj", "v_proj", "o_proj")),
+                                    (bd.mlp, bs.mlp, ("gate_proj", "up_proj", "down_proj"))):
+            for name in names:
+                lin = getattr(sub_d, name)
+                N, K = lin.weight.shape
+                keys = torch.rand(K // M, M, generator=g, device="cuda")
+                mi = keys.argsort(1)[:, : M // 2].sort(1).values.to(torch.uint8)
+                mask = torch.zeros(K // M, M, dtype=torch.bool, device="cuda")
+                mask.scatter_(1, mi.long(), True)
+                with torch.no_grad():
+                    lin.weight.mul_(mask.view(1, K))
+                setattr(sub_s, name, NmSparseLinear.from_dense(lin.weight.detach(), mi, M))
+    return dense, sparse
+
+
+@pytest.mark.gpu
+def test_graph_replay_matches_eager_and_masked_dense(gpu):
+    from spmv_decode_amd.decode.runner import GraphDecoder
+
+    cfg = tiny_config(qk_norm=True)
+    dense, sparse = _masked_pair(cfg, 8)
+    prompt = torch.randint(0, cfg.vocab, (5,), generator=torch.Generator().manual_seed(3))
+    # eager reference tokens and logits
+    eager = GraphDecoder(sparse, 32)
+    eager.run_prompt(prompt)
+    eager_logits = [eager.eager_step().clone() for _ in range(6)]
+    eager_tokens = eager.tokens[: eager.host_pos + 1].clone()
+    # the dense masked model, eager, same tokens
+    dref = GraphDecoder(dense, 32)
+    dref.run_prompt(prompt)
+    dense_logits = [dref.eager_step().clone() for _ in range(6)]
+    for a, b in zip(eager_logits, dense_logits):
+        torch.testing.assert_close(a.float(), b.float(), rtol=2e-2, atol=2e-2)
+    # graph replays of the sparse model, three times over, bit-identical to eager
+    gd = GraphDecoder(sparse, 32)
+    gd.capture()
+    for rep in range(3):
+        gd.run_prompt(prompt)
+        logits = []
+        for _ in range(6):
+            gd.replay()
+            logits.append(gd.logits.clone())
+        torch.cuda.synchronize()
+        assert torch.equal(gd.tokens[: gd.host_pos + 1], eager_tokens), rep
+        for a, b in zip(logits, eager_logits):
+            assert torch.equal(a, b), rep
+    with pytest.raises(RuntimeError, match="static cache"):
+        gd.generate(64)
