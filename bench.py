@@ -2,12 +2,15 @@
 
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--ratio 32:64]
 
-One step = every sparse GEMV of one Llama-3.1-8B decode token: 32 layers x
-(q, k, v, o, gate, up, down) = 224 launches over 32 layers' distinct packed
-weights (7.0 GB resident in HBM, far beyond the 256 MB Infinity Cache), fp16,
-batch 1, captured once in a hipGraph and replayed. `value` is the algorithmic
-bytes of the step (2*w*h weights + w index bytes + 2*K activations + 2*h
-outputs per GEMV) divided by the step time.
+One step = every sparse GEMV of one Llama-3.1-8B decode token at 32:64, as the
+decoder launches them: per layer one grouped q/k/v launch, o, one gate/up pair
+launch with the SiLU*mul epilogue, and down (4 launches x 32 layers), over 32
+layers' distinct packed weights (7.0 GB resident in HBM, far beyond the
+256 MB Infinity Cache), fp16, batch 1, captured once in a hipGraph and
+replayed. `value` is the algorithmic bytes of the step (2*w*h weights + w
+index bytes per matrix, 2*K activations once per launch, 2*h outputs per
+output vector) divided by the step time. The same GEMVs as 224 separate
+launches are timed too and reported under config.unfused_224_launches.
 
 Also reported: per-shape average launch time and GB/s for the sparse kernel
 and for dense fp16 F.linear (hipBLASLt preferred) on the same shapes, the
@@ -67,6 +70,7 @@ def parse_args():
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
     p.add_argument("--only-step", action="store_true", help="time only the sparse step (for profiling)")
+    p.add_argument("--no-decode", action="store_true", help="skip the end-to-end Llama-3.1-8B decode")
     return p.parse_args()
 
 
@@ -111,6 +115,25 @@ def main():
         return hip_spmv.nmsparse_spmv_forward_hip(xs[K], md, mi, md.shape[0], h, nnz, 128, m, 1, K,
                                                   out=outs[name])
 
+    act = torch.empty(1, SHAPES["gate_proj"][1], dtype=torch.float16, device=dev)
+
+    def fused_layer(li):
+        # the decoder's launch pattern: grouped q/k/v, o, gate/up pair with SiLU*mul, down
+        lay = layers[li]
+        hip_spmv.nmsparse_gemv_grouped(xs[4096], [lay["q_proj"], lay["k_proj"], lay["v_proj"]], nnz, m,
+                                       outs=[outs["q_proj"], outs["k_proj"], outs["v_proj"]])
+        gemv("o_proj", li)
+        hip_spmv.nmsparse_gate_up_silu(xs[4096], lay["gate_proj"], lay["up_proj"], nnz, m, out=act)
+        gemv("down_proj", li)
+
+    w4, w14 = 4096 // m * nnz, 14336 // m * nnz
+    fused_bytes_layer = (
+        sum(2 * w4 * SHAPES[n][1] + w4 + 2 * SHAPES[n][1] for n in ("q_proj", "k_proj", "v_proj")) + 2 * 4096
+        + sparse_bytes(*SHAPES["o_proj"], nnz, m)
+        + 2 * (2 * w4 * 14336 + w4) + 2 * 4096 + 2 * 14336
+        + sparse_bytes(*SHAPES["down_proj"], nnz, m))
+    fused_bytes = L * fused_bytes_layer
+
     stream = torch.cuda.Stream(device=dev)
 
     def capture(fn):
@@ -126,29 +149,30 @@ def main():
         torch.cuda.synchronize()
         return g
 
-    def step():
-        for li in range(L):
-            for name in SHAPES:
-                gemv(name, li)
+    def time_step(fn):
+        g = capture(fn)
+        for _ in range(args.warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(args.steps):
+            g.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end) / args.steps
 
-    # ---- the timed step ------------------------------------------------------
-    g_step = capture(step)
-    for _ in range(args.warmup):
-        g_step.replay()
-    torch.cuda.synchronize()
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for _ in range(args.steps):
-        g_step.replay()
-    end.record()
-    torch.cuda.synchronize()
-    ms_per_step = start.elapsed_time(end) / args.steps
-    value = step_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"step {ms_per_step:.4f} ms -> {value:.1f} GB/s ({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
-    for name, (K, h) in SHAPES.items():
-        if not torch.isfinite(outs[name].float()).all():
-            raise RuntimeError(f"non-finite output for {name}")
+    # ---- the timed step: one decode token's sparse GEMVs as the decoder runs them
+    ms_per_step = time_step(lambda: [fused_layer(li) for li in range(L)])
+    value = fused_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"fused step ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
+        f"({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
+    written = [act] + [outs[n] for n in ("q_proj", "k_proj", "v_proj", "o_proj", "down_proj")]
+    if not all(bool(torch.isfinite(o.float()).all()) for o in written):
+        raise RuntimeError("non-finite GEMV output")
+    ms_unfused = time_step(lambda: [gemv(name, li) for li in range(L) for name in SHAPES])
+    unfused_value = step_bytes / (ms_unfused * 1e-3) / 1e9
+    log(f"unfused step ({len(SHAPES) * L} launches) {ms_unfused:.4f} ms -> {unfused_value:.1f} GB/s")
 
     result = {
         "metric": "sparse GEMV HBM GB/s (% peak) + decode ms/token, Llama-3.1-8B-shape 32:64",
@@ -164,13 +188,16 @@ def main():
         "dtype": "fp16",
         "data": "synthetic (seeded on-device N(0,0.02) weights, random in-group patterns, N(0,1) activations)",
         "config": {
-            "workload": f"Llama-3.1-8B decode-token sparse GEMVs: {L} layers x (q,k,v,o,gate,up,down) at {nnz}:{m}, "
-                        "batch 1, fp16, hipGraph replay, distinct resident weights per layer",
+            "workload": f"Llama-3.1-8B decode-token sparse GEMVs at {nnz}:{m}: {L} layers x (grouped q/k/v, o, "
+                        "gate/up pair with SiLU*mul, down), batch 1, fp16, hipGraph replay, distinct resident "
+                        "weights per layer",
             "ratio": f"{nnz}:{m}",
             "layers": L,
-            "gemvs_per_step": L * len(SHAPES),
-            "algorithmic_bytes_per_step": step_bytes,
+            "launches_per_step": 4 * L,
+            "algorithmic_bytes_per_step": fused_bytes,
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "unfused_224_launches": {"ms_per_step": round(ms_unfused, 5), "GBps": round(unfused_value, 2),
+                                     "algorithmic_bytes_per_step": step_bytes},
         },
     }
     if args.only_step:
@@ -199,9 +226,37 @@ def main():
             f"({per_shape[cls]['pct_peak']}%) {plan} x{case.copies} copies")
         del case
         torch.cuda.empty_cache()
-    # dominant kernel: largest share of the step
-    dom = max(per_shape, key=lambda c: per_shape[c]["us_per_launch"] * per_shape[c]["launches_per_step"])
-    d = per_shape[dom]
+    # fused launch classes of the step, weights rotated over >= 1 GiB
+    qkv_sizes = (SHAPES["q_proj"][1], SHAPES["k_proj"][1], SHAPES["v_proj"][1])
+    qkv_b = sum(2 * w4 * h + w4 + 2 * h for h in qkv_sizes) + 2 * 4096
+    copies = -(-(1 << 30) // qkv_b)
+    qkv = [MB.RotatingCase(h, 4096, nnz, m, rotate_bytes=0, min_copies=copies, seed=30 + i)
+           for i, h in enumerate(qkv_sizes)]
+    us = MB.time_grouped(qkv, reps=reps)
+    fused = {"qkv_grouped": {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": qkv_b,
+                             "GBps": round(qkv_b / (us * 1e-6) / 1e9, 1)}}
+    del qkv
+    pair_b = 2 * (2 * w4 * 14336 + w4) + 2 * 4096 + 2 * 14336
+    copies = -(-(1 << 30) // pair_b)
+    gc_, uc_ = (MB.RotatingCase(14336, 4096, nnz, m, rotate_bytes=0, min_copies=copies, seed=40 + i)
+                for i in range(2))
+    us = MB.time_pair(gc_, uc_, reps=reps)
+    fused["gate_up_pair"] = {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": pair_b,
+                             "GBps": round(pair_b / (us * 1e-6) / 1e9, 1)}
+    del gc_, uc_
+    torch.cuda.empty_cache()
+    fused["o"] = dict(per_shape["q_o"], launches_per_step=L)
+    fused["down"] = dict(per_shape["down"], launches_per_step=L)
+    for c, v in fused.items():
+        v["pct_peak"] = round(100 * v["GBps"] / HBM_PEAK_GBS, 1)
+        log(f"fused class {c:12s}: {v['us_per_launch']:7.2f} us/launch {v['GBps']:7.1f} GB/s ({v['pct_peak']}%)")
+    # dominant kernel: largest share of the (fused) step
+    dom = max(fused, key=lambda c: fused[c]["us_per_launch"] * fused[c]["launches_per_step"])
+    d = fused[dom]
+    kernel_name = {"gate_up_pair": "nm_gemv_kernel<fp16, pair_th32_u4, NMAT=2> (gate/up pair, K=4096 h=14336)",
+                   "qkv_grouped": "nm_gemv_kernel<fp16, th16_u8> grouped (q/k/v, K=4096 h=4096+1024+1024)",
+                   "down": "nm_gemv_kernel<fp16, th16_u8> (down, K=14336 h=4096)",
+                   "o": "nm_gemv_kernel<fp16, th16_u8> (o, K=4096 h=4096)"}[dom]
     result["roofline"] = {
         "bound": "hbm",
         "achieved": d["GBps"],
@@ -209,10 +264,11 @@ def main():
         "unit": "GB/s",
         "frac": round(d["GBps"] / HBM_PEAK_GBS, 4),
         "traffic": None,
-        "kernel": f"nm_gemv_kernel {d['kernel_config']} ({dom}: K={d['K']} h={d['h']}, {nnz}:{m})",
+        "kernel": f"{kernel_name}, {nnz}:{m}",
         "bytes_per_launch": d["bytes_per_launch"],
         "us_per_launch": d["us_per_launch"],
     }
+    result["per_launch_class_fused"] = fused
     traffic_file = ROOT / "profiles" / "traffic.json"
     if traffic_file.exists():
         t = json.loads(traffic_file.read_text()).get(f"{dom}_{nnz}:{m}")
@@ -252,7 +308,47 @@ def main():
     # ---- CPU baseline (rank 0, N=1): oracle gather form on one layer ----------
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layers[0], xs, nnz, m, args.cpu_seconds)
+
+    # ---- end-to-end decode ms/token: dense hipBLASLt vs N:M sparse ------------
+    if not args.no_decode:
+        layers.clear()  # the closures above share this list: clearing it frees the weights
+        torch.cuda.empty_cache()
+        result["decode"] = decode_ms_per_token(m, log)
     print(json.dumps(result), flush=True)
+
+
+def decode_ms_per_token(m, log):
+    """Random-init Llama-3.1-8B, prompt 128 + 256 greedy steps per variant,
+    hipGraph replay (spmv_decode_amd.decode.bench_decode protocol)."""
+    import torch
+
+    from spmv_decode_amd.decode.bench_decode import linear_bytes, run_variant
+    from spmv_decode_amd.decode.model import LLAMA31_8B, Decoder, init_weights_
+    from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
+
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device("cuda:0"):
+            model = Decoder(LLAMA31_8B)
+    finally:
+        torch.set_default_dtype(prev)
+    init_weights_(model, seed=0)
+    prompt = torch.randint(0, LLAMA31_8B.vocab, (128,), generator=torch.Generator().manual_seed(1))
+    dense = run_variant(model, LLAMA31_8B, prompt, 256, "dense", log)
+    swap_to_nmsparse(model, m, "cuda", seed=0, init="device", keep_dense=False)
+    torch.cuda.empty_cache()
+    sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)
+    del model
+    torch.cuda.empty_cache()
+    out = {"model": "llama-3.1-8b (random init)", "prompt": 128, "gen": 256,
+           "dense_ms_per_token": dense["ms_per_token"], "sparse_ms_per_token": sparse["ms_per_token"],
+           "speedup_sparse_vs_dense": round(dense["ms_per_token"] / sparse["ms_per_token"], 4),
+           "sparse_linear_bytes_per_token": linear_bytes(LLAMA31_8B, m),
+           "dense_linear_bytes_per_token": linear_bytes(LLAMA31_8B, 0)}
+    log(f"decode: dense {out['dense_ms_per_token']} ms/token, sparse {out['sparse_ms_per_token']} ms/token, "
+        f"speedup {out['speedup_sparse_vs_dense']}x")
+    return out
 
 
 def cpu_baseline(layer, xs, nnz, m, budget_s):

@@ -119,9 +119,44 @@ size_t nm_gemv_workspace_bytes_ex(int h, int w, int nnz, int m, int config_id,
                                   int splits);
 
 /*
+ * Grouped launch: nprob (1..4) GEMVs that read the same vec (same K, nnz, m,
+ * hence the same w) in one grid, e.g. the q, k and v projections of one
+ * attention layer. Problem i reads mat_data[i] ([w, hs[i]]) and
+ * mat_index[i] and writes out[i] ([1, hs[i]]); each result is what
+ * nm_gemv_ex would compute for that problem with the same config_id and
+ * splits (all problems share one configuration). No reference counterpart as
+ * an entry point: it fuses the per-projection calls the reference makes, the
+ * multi-problem launch planned for the fused wqkv projection of gpt-fast
+ * (model.py:196-198, 219). Workspace: nm_gemv_grouped_workspace_bytes.
+ */
+size_t nm_gemv_grouped_workspace_bytes(int nprob, const int* hs, int w, int nnz, int m, int config_id,
+                                       int splits);
+int nm_gemv_grouped(int dtype, const void* vec, int vec_stride, int nprob, const void* const* mat_data,
+                    const uint8_t* const* mat_index, void* const* out, const int* hs, void* workspace,
+                    size_t workspace_bytes, int w, int nnz, int m, int config_id, int splits, void* stream);
+
+/*
+ * Gate/up pair with the SiLU-gated epilogue of a Llama/Qwen MLP: one launch
+ * computes g = W_gate x and u = W_up x (each an N:M GEMV with its own
+ * mat_index, both [w, h]) and writes out[r] = RNE_T(silu(g[r]) * u[r]) with
+ * silu(g) = g / (1 + exp(-g)), all in fp32 before the single rounding.
+ * Replaces `F.silu(w1(x)) * w3(x)` (model.py:255-256) when w1 and w3 are
+ * N:M sparse. config_id indexes the pair configurations
+ * (0 <= config_id < nm_num_gate_up_configs(), < 0: the library's choice).
+ * Workspace: nm_gemv_gate_up_workspace_bytes.
+ */
+size_t nm_gemv_gate_up_workspace_bytes(int h, int w, int nnz, int m, int config_id, int splits);
+int nm_gemv_gate_up_silu(int dtype, const void* vec, int vec_stride, const void* gate_data,
+                         const uint8_t* gate_index, const void* up_data, const uint8_t* up_index, void* out,
+                         void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
+                         int config_id, int splits, void* stream);
+int nm_num_gate_up_configs(void);
+
+/*
  * Configuration introspection. nm_config_describe writes a short text such as
- * "th32_u8" into buf; nm_gemv_plan reports the configuration and split count
- * the library would use for a shape (config_id < 0: its own choice).
+ * "th32_u8" into buf (ids nm_num_configs() + j describe pair configuration j);
+ * nm_gemv_plan reports the configuration and split count the library would
+ * use for a single GEMV of a shape (config_id < 0: its own choice).
  */
 int nm_num_configs(void);
 int nm_config_describe(int config_id, char* buf, int buf_len);

@@ -40,12 +40,18 @@ ABI = {
     "nm_gemv_ex": (_i, [_i, _vp, _i, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_gemv_workspace_bytes_ex": (_sz, [_i, _i, _i, _i, _i, _i]),
     "nm_num_configs": (_i, []),
+    "nm_gemv_grouped_workspace_bytes": (_sz, [_i, _ip, _i, _i, _i, _i, _i]),
+    "nm_gemv_grouped": (_i, [_i, _vp, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp), _ip,
+                             _vp, _sz, _i, _i, _i, _i, _i, _vp]),
+    "nm_gemv_gate_up_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
+    "nm_gemv_gate_up_silu": (_i, [_i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
+    "nm_num_gate_up_configs": (_i, []),
     "nm_config_describe": (_i, [_i, ctypes.c_char_p, _i]),
     "nm_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
 }
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _lib = None
 _lock = threading.Lock()

@@ -40,7 +40,7 @@ constexpr int kBlock = 256;        // lanes per workgroup
 constexpr int kVec = 8;            // output rows per lane
 constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
 constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -123,25 +123,42 @@ __device__ inline u32x4 load16(const u32x4* p) {
 // ---------------------------------------------------------------------------
 // Kernel
 // ---------------------------------------------------------------------------
-struct Args {
-  const void* vec;
+constexpr int kMaxProblems = 4;
+
+// One GEMV of a launch. The problems of one launch share the activation
+// vector and K, nnz, m (hence w); their output widths h may differ.
+struct Problem {
   const void* mat_data;
   const uint8_t* mat_index;
   void* out;
   float* partial;      // [splits, h] fp32, unused when splits == 1
   uint32_t* tickets;   // [tiles] arrival counters, zero between launches
-  long long vec_stride;
   int h;
+  int tiles;
+  int block_begin;     // first workgroup of this problem in the grid
+};
+
+struct Args {
+  const void* vec;
+  long long vec_stride;
   int w;
   int nnz;
   int m;
   int K;
-  int tiles;
   int splits;
   int rows_per_split;  // multiple of the chunk height, <= kMaxRows
+  int nprob;           // NMAT == 1: problems in the grid; NMAT == 2: 2 (gate, up)
+  Problem prob[kMaxProblems];
 };
 
-template <int DT, int TH, int U, int G, bool NT>
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// NMAT == 1: each workgroup computes one tile/split of one problem (a plain
+// GEMV when nprob == 1, several GEMVs sharing x in one grid otherwise).
+// NMAT == 2: each workgroup streams the same tile/split of prob[0] (gate) and
+// prob[1] (up), both of width prob[0].h, and the output prob[0].out receives
+// silu(gate) * up, computed in fp32 and rounded once.
+template <int DT, int TH, int U, int G, bool NT, int NMAT>
 __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   using E = Elem<DT>;
   typedef typename E::scalar T;
@@ -153,28 +170,45 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   static_assert(kBlock % TH == 0, "TH must divide the block");
   static_assert(U % 4 == 0, "U must be a multiple of 4 (ds_read_b128)");
   static_assert(XR % CH == 0, "chunk must divide the split");
+  static_assert(NMAT == 1 || NMAT == 2, "one matrix, or the gate/up pair");
 
-  __shared__ __attribute__((aligned(16))) float xs[XR];
-  __shared__ __attribute__((aligned(16))) float red[TK * HT];
+  __shared__ __attribute__((aligned(16))) float xs[NMAT][XR];
+  __shared__ __attribute__((aligned(16))) float red[NMAT][TK * HT];
   __shared__ int is_last;
+
+  // Problem of this workgroup (uniform; at most kMaxProblems entries).
+  int p = 0;
+  if (NMAT == 1) {
+#pragma unroll
+    for (int q = 1; q < kMaxProblems; ++q)
+      if (q < a.nprob && (int)blockIdx.x >= a.prob[q].block_begin) p = q;
+  }
+  const int h = a.prob[p].h;
+  const int tiles = a.prob[p].tiles;
+  const int local = (int)blockIdx.x - a.prob[p].block_begin;
 
   const int tid = threadIdx.x;
   const int th = tid % TH;
   const int tk = tid / TH;
-  const int tile = blockIdx.x % a.tiles;
-  const int split = blockIdx.x / a.tiles;
+  const int tile = local % tiles;
+  const int split = local / tiles;
   const int c0 = split * a.rows_per_split;
   const int cw = min(a.rows_per_split, a.w - c0);  // 1 <= cw <= XR by construction
   const int nch = (cw + CH - 1) / CH;
   const int col = tile * HT + th * kVec;
   // Lanes past the last output row read a valid column instead (their sums
   // are never stored), so no weight load needs a branch.
-  const int col_ld = min(col, a.h - kVec);
+  const int col_ld = min(col, h - kVec);
 
-  const T* __restrict__ md = static_cast<const T*>(a.mat_data);
   const T* __restrict__ vx = static_cast<const T*>(a.vec);
-  const uint8_t* __restrict__ mi = a.mat_index;
-  const T* __restrict__ md_tile = md + (size_t)c0 * (size_t)a.h + (size_t)col_ld;
+  const T* md_tile[NMAT];
+  const uint8_t* mi[NMAT];
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q) {
+    const Problem& P = a.prob[NMAT == 1 ? p : q];
+    md_tile[q] = static_cast<const T*>(P.mat_data) + (size_t)c0 * (size_t)h + (size_t)col_ld;
+    mi[q] = P.mat_index;
+  }
 
   // All loads below are unconditional (addresses clamped into range) so that
   // the compiler keeps them in flight together; out-of-range values are
@@ -182,62 +216,75 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
 
   // 1. In-group positions of this split's compressed columns. mat_index is
   //    [w/nnz, nnz] contiguous, so column c's position is mi[c].
-  int gidx[G];
+  int gidx[NMAT][G];
 #pragma unroll
-  for (int j = 0; j < G; ++j) gidx[j] = (int)mi[c0 + min(tid + j * kBlock, cw - 1)];
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int j = 0; j < G; ++j) gidx[q][j] = (int)mi[q][c0 + min(tid + j * kBlock, cw - 1)];
 
   // 2. The first chunk of weights goes in flight before the activation loads.
-  auto load_chunk = [&](u32x4 (&dst)[U][W], int k) {
+  auto load_chunk = [&](u32x4 (&dst)[NMAT][U][W], int k) {
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int r = min(k * CH + tk * U + u, cw - 1);
-      const u32x4* p = reinterpret_cast<const u32x4*>(md_tile + (size_t)r * (size_t)a.h);
 #pragma unroll
-      for (int q = 0; q < W; ++q) dst[u][q] = load16<NT>(p + q);
+      for (int q = 0; q < NMAT; ++q) {
+        const u32x4* ptr = reinterpret_cast<const u32x4*>(md_tile[q] + (size_t)r * (size_t)h);
+#pragma unroll
+        for (int v = 0; v < W; ++v) dst[q][u][v] = load16<NT>(ptr + v);
+      }
     }
   };
-  u32x4 bufA[U][W];
-  u32x4 bufB[U][W];
+  u32x4 bufA[NMAT][U][W];
+  u32x4 bufB[NMAT][U][W];
   load_chunk(bufA, 0);
 
   // 3. Gather the activations: vec[(c/nnz)*m + position], fp32 in LDS. Rows
   //    past the split and positions outside vec read as zero.
-  T graw[G];
-  bool gok[G];
+  T graw[NMAT][G];
+  bool gok[NMAT][G];
 #pragma unroll
-  for (int j = 0; j < G; ++j) {
-    const int t = tid + j * kBlock;
-    const int c = c0 + min(t, cw - 1);
-    const int pos = (c / a.nnz) * a.m + gidx[j];
-    gok[j] = (t < cw) && (pos < a.K);
-    graw[j] = vx[(long long)(gok[j] ? pos : 0) * a.vec_stride];
-  }
+  for (int q = 0; q < NMAT; ++q)
 #pragma unroll
-  for (int j = 0; j < G; ++j) xs[tid + j * kBlock] = gok[j] ? E::to_f32(graw[j]) : 0.0f;
+    for (int j = 0; j < G; ++j) {
+      const int t = tid + j * kBlock;
+      const int c = c0 + min(t, cw - 1);
+      const int pos = (c / a.nnz) * a.m + gidx[q][j];
+      gok[q][j] = (t < cw) && (pos < a.K);
+      graw[q][j] = vx[(long long)(gok[q][j] ? pos : 0) * a.vec_stride];
+    }
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int j = 0; j < G; ++j) xs[q][tid + j * kBlock] = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
   __syncthreads();
 
-  float acc[kVec];
+  float acc[NMAT][kVec];
 #pragma unroll
-  for (int e = 0; e < kVec; ++e) acc[e] = 0.0f;
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[q][e] = 0.0f;
 
   // FMA one chunk; rows past the split contribute exactly nothing.
-  auto fma_chunk = [&](const u32x4 (&src)[U][W], int k) {
+  auto fma_chunk = [&](const u32x4 (&src)[NMAT][U][W], int k) {
     const int r0 = k * CH + tk * U;
 #pragma unroll
-    for (int u4 = 0; u4 < U / 4; ++u4) {
-      const float4 xv = *reinterpret_cast<const float4*>(&xs[r0 + 4 * u4]);
-      const float xq[4] = {xv.x, xv.y, xv.z, xv.w};
+    for (int q = 0; q < NMAT; ++q) {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const bool ok = (r0 + 4 * u4 + s) < cw;
-        u32x4 rw[W];
+      for (int u4 = 0; u4 < U / 4; ++u4) {
+        const float4 xv = *reinterpret_cast<const float4*>(&xs[q][r0 + 4 * u4]);
+        const float xq[4] = {xv.x, xv.y, xv.z, xv.w};
 #pragma unroll
-        for (int q = 0; q < W; ++q)
-          rw[q] = ok ? src[4 * u4 + s][q] : u32x4{0u, 0u, 0u, 0u};
-        float v[kVec];
-        E::unpack(rw, v);
+        for (int s = 0; s < 4; ++s) {
+          const bool ok = (r0 + 4 * u4 + s) < cw;
+          u32x4 rw[W];
 #pragma unroll
-        for (int e = 0; e < kVec; ++e) acc[e] = __builtin_fmaf(v[e], xq[s], acc[e]);
+          for (int v = 0; v < W; ++v) rw[v] = ok ? src[q][4 * u4 + s][v] : u32x4{0u, 0u, 0u, 0u};
+          float wv[kVec];
+          E::unpack(rw, wv);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) acc[q][e] = __builtin_fmaf(wv[e], xq[s], acc[q][e]);
+        }
       }
     }
   };
@@ -260,33 +307,50 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   }
 
   // 5. Reduce the TK lane-rows of the tile through LDS (fixed order).
-  {
-    float4* rp = reinterpret_cast<float4*>(&red[tk * HT + th * kVec]);
-    rp[0] = make_float4(acc[0], acc[1], acc[2], acc[3]);
-    rp[1] = make_float4(acc[4], acc[5], acc[6], acc[7]);
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q) {
+    float4* rp = reinterpret_cast<float4*>(&red[q][tk * HT + th * kVec]);
+    rp[0] = make_float4(acc[q][0], acc[q][1], acc[q][2], acc[q][3]);
+    rp[1] = make_float4(acc[q][4], acc[q][5], acc[q][6], acc[q][7]);
   }
   __syncthreads();
 
-  T* __restrict__ out = static_cast<T*>(a.out);
+  T* __restrict__ out = static_cast<T*>(a.prob[p].out);
   constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
-  float tsum[kOutPerLane];
+  float tsum[NMAT][kOutPerLane];
 #pragma unroll
-  for (int j = 0; j < kOutPerLane; ++j) {
-    const int o = tid + j * kBlock;
-    float s = 0.0f;
-    if (o < HT) {
+  for (int q = 0; q < NMAT; ++q)
 #pragma unroll
-      for (int q = 0; q < TK; ++q) s += red[q * HT + o];
+    for (int j = 0; j < kOutPerLane; ++j) {
+      const int o = tid + j * kBlock;
+      float s = 0.0f;
+      if (o < HT) {
+#pragma unroll
+        for (int t = 0; t < TK; ++t) s += red[q][t * HT + o];
+      }
+      tsum[q][j] = s;
     }
-    tsum[j] = s;
-  }
+
+  // Output value of one row from its (gate[, up]) sums.
+  auto finish = [&](const float (&v)[NMAT]) -> T {
+    if constexpr (NMAT == 1) {
+      return E::from_f32(v[0]);
+    } else {
+      return E::from_f32(silu(v[0]) * v[1]);
+    }
+  };
 
   if (a.splits == 1) {
 #pragma unroll
     for (int j = 0; j < kOutPerLane; ++j) {
       const int o = tid + j * kBlock;
       const int r = tile * HT + o;
-      if (o < HT && r < a.h) out[r] = E::from_f32(tsum[j]);
+      if (o < HT && r < h) {
+        float v[NMAT];
+#pragma unroll
+        for (int q = 0; q < NMAT; ++q) v[q] = tsum[q][j];
+        out[r] = finish(v);
+      }
     }
     return;
   }
@@ -303,20 +367,24 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   //    coherent across XCDs) in split order, so the sum is deterministic.
   float sink = 0.0f;
 #pragma unroll
-  for (int j = 0; j < kOutPerLane; ++j) {
-    const int o = tid + j * kBlock;
-    const int r = tile * HT + o;
-    if (o < HT && r < a.h)
-      sink += __hip_atomic_exchange(a.partial + (size_t)split * (size_t)a.h + (size_t)r, tsum[j],
-                                    __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  for (int q = 0; q < NMAT; ++q) {
+    float* part = a.prob[NMAT == 1 ? p : q].partial + (size_t)split * (size_t)h;
+#pragma unroll
+    for (int j = 0; j < kOutPerLane; ++j) {
+      const int o = tid + j * kBlock;
+      const int r = tile * HT + o;
+      if (o < HT && r < h)
+        sink += __hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
   }
   // Consume the swap results (a.splits is never negative) so the compiler
   // keeps the returning form of the instruction.
   if (a.splits < 0) out[tid] = E::from_f32(sink);
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
+  uint32_t* tickets = a.prob[p].tickets;
   if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED,
+    const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
                                                  __HIP_MEMORY_SCOPE_AGENT);
     is_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
   }
@@ -327,31 +395,36 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   for (int j = 0; j < kOutPerLane; ++j) {
     const int o = tid + j * kBlock;
     const int r = tile * HT + o;
-    if (o < HT && r < a.h) {
-      float* p = a.partial + r;
-      float s = 0.0f;
-      int sp = 0;
-      for (; sp + 8 <= a.splits; sp += 8) {
-        float t[8];
+    if (o < HT && r < h) {
+      float v[NMAT];
 #pragma unroll
-        for (int q = 0; q < 8; ++q)
-          t[q] = __hip_atomic_load(p + (size_t)(sp + q) * (size_t)a.h, __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+      for (int q = 0; q < NMAT; ++q) {
+        float* pp = a.prob[NMAT == 1 ? p : q].partial + r;
+        float s = 0.0f;
+        int sp = 0;
+        for (; sp + 8 <= a.splits; sp += 8) {
+          float t8[8];
 #pragma unroll
-        for (int q = 0; q < 8; ++q) s += t[q];
+          for (int i = 0; i < 8; ++i)
+            t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+          for (int i = 0; i < 8; ++i) s += t8[i];
+        }
+        for (; sp < a.splits; ++sp)
+          s += __hip_atomic_load(pp + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        v[q] = s;
       }
-      for (; sp < a.splits; ++sp)
-        s += __hip_atomic_load(p + (size_t)sp * (size_t)a.h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      out[r] = E::from_f32(s);
+      out[r] = finish(v);
     }
   }
   if (tid == 0) {
-    __hip_atomic_store(&a.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
 
 // ---------------------------------------------------------------------------
-// Configuration table (static; no runtime autotuning).
+// Configuration tables (static; no runtime autotuning).
 // ---------------------------------------------------------------------------
 typedef void (*KernelFn)(Args);
 
@@ -359,33 +432,44 @@ struct Config {
   int th;       // lanes along the output rows (tile = 8*th rows)
   int u;        // rows per lane per chunk
   bool nt;      // non-temporal weight loads
+  int nmat;     // 1: plain / grouped GEMV; 2: gate/up pair with SiLU*mul
   KernelFn fn[3][4];  // [dtype][gather width: 256, 512, 1024, 2048 columns per split]
 };
 
-#define NM_CFG_G(DT, TH, U, NT)                                               \
-  {&nm_gemv_kernel<DT, TH, U, 1, NT>, &nm_gemv_kernel<DT, TH, U, 2, NT>,       \
-   &nm_gemv_kernel<DT, TH, U, 4, NT>, &nm_gemv_kernel<DT, TH, U, 8, NT>}
-#define NM_CFG(TH, U, NT)                                                     \
-  {TH, U, NT,                                                                 \
-   {NM_CFG_G(NM_DTYPE_F16, TH, U, NT), NM_CFG_G(NM_DTYPE_BF16, TH, U, NT),   \
-    NM_CFG_G(NM_DTYPE_F32, TH, U, NT)}}
+#define NM_CFG_G(DT, TH, U, NT, NM)                                                 \
+  {&nm_gemv_kernel<DT, TH, U, 1, NT, NM>, &nm_gemv_kernel<DT, TH, U, 2, NT, NM>,     \
+   &nm_gemv_kernel<DT, TH, U, 4, NT, NM>, &nm_gemv_kernel<DT, TH, U, 8, NT, NM>}
+#define NM_CFG(TH, U, NT, NM)                                                       \
+  {TH, U, NT, NM,                                                                   \
+   {NM_CFG_G(NM_DTYPE_F16, TH, U, NT, NM), NM_CFG_G(NM_DTYPE_BF16, TH, U, NT, NM), \
+    NM_CFG_G(NM_DTYPE_F32, TH, U, NT, NM)}}
 
+// Plain / grouped GEMV configurations (ids 0..12, stable).
 const Config kConfigs[] = {
-    NM_CFG(16, 4, true),   // 0: tile 128,  chunk 64
-    NM_CFG(16, 8, true),   // 1: tile 128,  chunk 128
-    NM_CFG(32, 4, true),   // 2: tile 256,  chunk 32
-    NM_CFG(32, 8, true),   // 3: tile 256,  chunk 64
-    NM_CFG(32, 16, true),  // 4: tile 256,  chunk 128
-    NM_CFG(64, 4, true),   // 5: tile 512,  chunk 16
-    NM_CFG(64, 8, true),   // 6: tile 512,  chunk 32
-    NM_CFG(64, 16, true),  // 7: tile 512,  chunk 64
-    NM_CFG(128, 8, true),  // 8: tile 1024, chunk 16
-    NM_CFG(256, 8, true),  // 9: tile 2048, chunk 8
-    NM_CFG(16, 8, false),  // 10: as 1, cached loads
-    NM_CFG(32, 8, false),  // 11: as 3, cached loads
-    NM_CFG(64, 8, false),  // 12: as 6, cached loads
+    NM_CFG(16, 4, true, 1),   // 0: tile 128,  chunk 64
+    NM_CFG(16, 8, true, 1),   // 1: tile 128,  chunk 128
+    NM_CFG(32, 4, true, 1),   // 2: tile 256,  chunk 32
+    NM_CFG(32, 8, true, 1),   // 3: tile 256,  chunk 64
+    NM_CFG(32, 16, true, 1),  // 4: tile 256,  chunk 128
+    NM_CFG(64, 4, true, 1),   // 5: tile 512,  chunk 16
+    NM_CFG(64, 8, true, 1),   // 6: tile 512,  chunk 32
+    NM_CFG(64, 16, true, 1),  // 7: tile 512,  chunk 64
+    NM_CFG(128, 8, true, 1),  // 8: tile 1024, chunk 16
+    NM_CFG(256, 8, true, 1),  // 9: tile 2048, chunk 8
+    NM_CFG(16, 8, false, 1),  // 10: as 1, cached loads
+    NM_CFG(32, 8, false, 1),  // 11: as 3, cached loads
+    NM_CFG(64, 8, false, 1),  // 12: as 6, cached loads
 };
 constexpr int kNumConfigs = sizeof(kConfigs) / sizeof(kConfigs[0]);
+
+// Gate/up pair configurations (each lane streams both matrices).
+const Config kDualConfigs[] = {
+    NM_CFG(16, 4, true, 2),   // 0: tile 128, chunk 64
+    NM_CFG(32, 4, true, 2),   // 1: tile 256, chunk 32
+    NM_CFG(16, 8, true, 2),   // 2: tile 128, chunk 128
+    NM_CFG(32, 8, true, 2),   // 3: tile 256, chunk 64
+};
+constexpr int kNumDualConfigs = sizeof(kDualConfigs) / sizeof(kDualConfigs[0]);
 
 inline int gather_slot(int rows) {
   return rows <= kBlock ? 0 : (rows <= 2 * kBlock ? 1 : (rows <= 4 * kBlock ? 2 : 3));
@@ -393,10 +477,14 @@ inline int gather_slot(int rows) {
 
 struct Plan {
   int cfg;
-  int tiles;
   int splits;
   int rows_per_split;
+  int nprob;
+  int tiles[kMaxProblems];
+  int block_begin[kMaxProblems];
   int blocks;
+  size_t ticket_off[kMaxProblems];   // in uint32 units from the workspace start
+  size_t partial_off[kMaxProblems];  // in bytes from the workspace start
   size_t workspace;
 };
 
@@ -411,12 +499,12 @@ int validate_shape(int h, int w, int nnz, int m) {
   return NM_OK;
 }
 
-// The library's own choice of configuration for a shape, from rocprof /
-// hipGraph sweeps on MI355X at the Llama-3.1-8B decode shapes: 256-row tiles
-// for wide outputs, 128-row tiles otherwise.
-int auto_config(int h, int w) {
-  (void)w;
-  return h >= 8192 ? 3 : 1;
+// The library's own choice of configuration, from rocprof / hipGraph sweeps on
+// MI355X at the Llama-3.1-8B decode shapes: 256-row tiles for wide outputs,
+// 128-row tiles otherwise (h_total: summed output width of the launch).
+int auto_config(int h_total, int nmat) {
+  if (nmat == 2) return h_total >= 8192 ? 1 : 0;
+  return h_total >= 8192 ? 3 : 1;
 }
 
 // Default split count: about 8 splits of the compressed columns per tile. The
@@ -426,16 +514,24 @@ int auto_config(int h, int w) {
 // 64-900 workgroups streaming for every decode shape.
 constexpr int kDefaultSplits = 8;
 
-int make_plan(int h, int w, int nnz, int m, int cfg, int splits, Plan* p) {
-  int rc = validate_shape(h, w, nnz, m);
-  if (rc != NM_OK) return rc;
-  if (cfg < 0) cfg = auto_config(h, w);
-  if (cfg >= kNumConfigs) return NM_ERR_BAD_CONFIG;
-  const Config& c = kConfigs[cfg];
+// Plan a launch of `nprob` problems (widths hs[]) sharing w, nnz, m, with
+// `nmat` matrices per workgroup. The workspace holds the counters of every
+// problem in its first NM_TICKET_BYTES and then nmat * splits * h floats of
+// partial sums per problem.
+int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg, int splits, Plan* p) {
+  if (nprob < 1 || nprob > kMaxProblems || (nmat == 2 && nprob != 1)) return NM_ERR_BAD_SHAPE;
+  long long h_total = 0;
+  for (int i = 0; i < nprob; ++i) {
+    const int rc = validate_shape(hs[i], w, nnz, m);
+    if (rc != NM_OK) return rc;
+    h_total += hs[i];
+  }
+  const int ncfg = nmat == 2 ? kNumDualConfigs : kNumConfigs;
+  if (cfg < 0) cfg = auto_config((int)(h_total > 0x7fffffff ? 0x7fffffff : h_total), nmat);
+  if (cfg >= ncfg) return NM_ERR_BAD_CONFIG;
+  const Config& c = nmat == 2 ? kDualConfigs[cfg] : kConfigs[cfg];
   const int HT = c.th * kVec;
   const int CH = (kBlock / c.th) * c.u;
-  const int tiles = ceil_div(h, HT);
-  if (tiles > kMaxTickets) return NM_ERR_BAD_SHAPE;
   if (splits <= 0) splits = kDefaultSplits;
   if (splits > w) splits = w;
   int rows = ceil_div(ceil_div(w, splits), CH) * CH;
@@ -443,51 +539,92 @@ int make_plan(int h, int w, int nnz, int m, int cfg, int splits, Plan* p) {
   if (rows < CH) rows = CH;
   splits = ceil_div(w, rows);
   p->cfg = cfg;
-  p->tiles = tiles;
   p->splits = splits;
   p->rows_per_split = rows;
-  const long long blocks = (long long)tiles * (long long)splits;
-  if (blocks > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
+  p->nprob = nprob;
+  long long blocks = 0;
+  size_t tickets = 0;
+  size_t bytes = NM_TICKET_BYTES;
+  for (int i = 0; i < nprob; ++i) {
+    p->tiles[i] = ceil_div(hs[i], HT);
+    p->block_begin[i] = (int)blocks;
+    blocks += (long long)p->tiles[i] * (long long)splits;
+    p->ticket_off[i] = tickets;
+    tickets += (size_t)p->tiles[i];
+    p->partial_off[i] = bytes;
+    if (splits > 1) bytes += (size_t)nmat * (size_t)splits * (size_t)hs[i] * sizeof(float);
+  }
+  if (tickets > (size_t)kMaxTickets || blocks > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   p->blocks = (int)blocks;
-  p->workspace = (size_t)NM_TICKET_BYTES +
-                 (splits > 1 ? (size_t)splits * (size_t)h * sizeof(float) : 0);
+  p->workspace = bytes;
   return NM_OK;
 }
 
-int launch(int dtype, const void* vec, int vec_stride, const void* mat_data,
-           const uint8_t* mat_index, void* out, void* workspace, size_t workspace_bytes,
-           int h, int w, int nnz, int m, int cfg, int splits, void* stream) {
+struct ProblemPtrs {
+  const void* mat_data;
+  const uint8_t* mat_index;
+  void* out;
+};
+
+int launch(int dtype, const void* vec, int vec_stride, int nprob, const ProblemPtrs* probs, const int* hs,
+           int nmat, void* workspace, size_t workspace_bytes, int w, int nnz, int m, int cfg, int splits,
+           void* stream) {
   if (dtype < NM_DTYPE_F16 || dtype > NM_DTYPE_F32) return NM_ERR_BAD_CONFIG;
-  if (!vec || !mat_data || !mat_index || !out || !workspace) return NM_ERR_NULL_POINTER;
+  if (!vec || !workspace || !probs) return NM_ERR_NULL_POINTER;
+  const int nmats_total = nmat == 2 ? 2 : nprob;
+  for (int i = 0; i < nmats_total; ++i)
+    if (!probs[i].mat_data || !probs[i].mat_index) return NM_ERR_NULL_POINTER;
+  for (int i = 0; i < nprob; ++i)
+    if (!probs[i].out) return NM_ERR_NULL_POINTER;
   if (vec_stride < 1) return NM_ERR_BAD_SHAPE;
   Plan p;
-  int rc = make_plan(h, w, nnz, m, cfg, splits, &p);
+  int rc = make_plan(nprob, hs, w, nnz, m, nmat, cfg, splits, &p);
   if (rc != NM_OK) return rc;
-  if (((uintptr_t)mat_data & 15u) != 0 || ((uintptr_t)out & 15u) != 0) return NM_ERR_MISALIGNED;
+  for (int i = 0; i < nmats_total; ++i)
+    if (((uintptr_t)probs[i].mat_data & 15u) != 0) return NM_ERR_MISALIGNED;
+  for (int i = 0; i < nprob; ++i)
+    if (((uintptr_t)probs[i].out & 15u) != 0) return NM_ERR_MISALIGNED;
   if (((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
   if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
 
   Args a;
+  memset(&a, 0, sizeof(a));
   a.vec = vec;
-  a.mat_data = mat_data;
-  a.mat_index = mat_index;
-  a.out = out;
-  a.tickets = static_cast<uint32_t*>(workspace);
-  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + NM_TICKET_BYTES);
   a.vec_stride = vec_stride;
-  a.h = h;
   a.w = w;
   a.nnz = nnz;
   a.m = m;
   a.K = (w / nnz) * m;
-  a.tiles = p.tiles;
   a.splits = p.splits;
   a.rows_per_split = p.rows_per_split;
-
-  hipLaunchKernelGGL(kConfigs[p.cfg].fn[dtype][gather_slot(p.rows_per_split)], dim3(p.blocks), dim3(kBlock), 0,
+  a.nprob = nmat == 2 ? 2 : nprob;
+  char* ws = static_cast<char*>(workspace);
+  for (int i = 0; i < nmats_total; ++i) {
+    const int src = nmat == 2 ? 0 : i;  // the pair shares problem 0's plan
+    Problem& P = a.prob[i];
+    P.mat_data = probs[i].mat_data;
+    P.mat_index = probs[i].mat_index;
+    P.out = probs[src].out;
+    P.h = hs[src];
+    P.tiles = p.tiles[src];
+    P.block_begin = p.block_begin[src];
+    P.tickets = reinterpret_cast<uint32_t*>(ws) + p.ticket_off[src];
+    P.partial = reinterpret_cast<float*>(ws + p.partial_off[src] +
+                                         (size_t)i * (nmat == 2 ? (size_t)p.splits * (size_t)hs[0] * 4 : 0));
+  }
+  const Config& c = nmat == 2 ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
+  hipLaunchKernelGGL(c.fn[dtype][gather_slot(p.rows_per_split)], dim3(p.blocks), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NM_OK : (int)e;
+}
+
+int launch_one(int dtype, const void* vec, int vec_stride, const void* mat_data, const uint8_t* mat_index,
+               void* out, void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m, int cfg,
+               int splits, void* stream) {
+  const ProblemPtrs pp = {mat_data, mat_index, out};
+  return launch(dtype, vec, vec_stride, 1, &pp, &h, 1, workspace, workspace_bytes, w, nnz, m, cfg, splits,
+                stream);
 }
 
 }  // namespace
@@ -499,55 +636,98 @@ extern "C" {
 
 size_t nm_gemv_workspace_bytes(int h, int w, int nnz, int m) {
   Plan p;
-  return make_plan(h, w, nnz, m, -1, 0, &p) == NM_OK ? p.workspace : 0;
+  return make_plan(1, &h, w, nnz, m, 1, -1, 0, &p) == NM_OK ? p.workspace : 0;
 }
 
 size_t nm_gemv_workspace_bytes_ex(int h, int w, int nnz, int m, int config_id, int splits) {
   Plan p;
-  return make_plan(h, w, nnz, m, config_id, splits, &p) == NM_OK ? p.workspace : 0;
+  return make_plan(1, &h, w, nnz, m, 1, config_id, splits, &p) == NM_OK ? p.workspace : 0;
 }
 
 int nm_gemv_f16(const void* vec, int vec_stride, const void* mat_data, const uint8_t* mat_index,
                 void* out, void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
                 void* stream) {
-  return launch(NM_DTYPE_F16, vec, vec_stride, mat_data, mat_index, out, workspace,
-                workspace_bytes, h, w, nnz, m, -1, 0, stream);
+  return launch_one(NM_DTYPE_F16, vec, vec_stride, mat_data, mat_index, out, workspace, workspace_bytes, h,
+                    w, nnz, m, -1, 0, stream);
 }
 
 int nm_gemv_bf16(const void* vec, int vec_stride, const void* mat_data, const uint8_t* mat_index,
                  void* out, void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
                  void* stream) {
-  return launch(NM_DTYPE_BF16, vec, vec_stride, mat_data, mat_index, out, workspace,
-                workspace_bytes, h, w, nnz, m, -1, 0, stream);
+  return launch_one(NM_DTYPE_BF16, vec, vec_stride, mat_data, mat_index, out, workspace, workspace_bytes, h,
+                    w, nnz, m, -1, 0, stream);
 }
 
 int nm_gemv_f32(const void* vec, int vec_stride, const void* mat_data, const uint8_t* mat_index,
                 void* out, void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
                 void* stream) {
-  return launch(NM_DTYPE_F32, vec, vec_stride, mat_data, mat_index, out, workspace,
-                workspace_bytes, h, w, nnz, m, -1, 0, stream);
+  return launch_one(NM_DTYPE_F32, vec, vec_stride, mat_data, mat_index, out, workspace, workspace_bytes, h,
+                    w, nnz, m, -1, 0, stream);
 }
 
 int nm_gemv_ex(int dtype, const void* vec, int vec_stride, const void* mat_data,
                const uint8_t* mat_index, void* out, void* workspace, size_t workspace_bytes,
                int h, int w, int nnz, int m, int config_id, int splits, void* stream) {
-  return launch(dtype, vec, vec_stride, mat_data, mat_index, out, workspace, workspace_bytes, h,
-                w, nnz, m, config_id, splits, stream);
+  return launch_one(dtype, vec, vec_stride, mat_data, mat_index, out, workspace, workspace_bytes, h, w, nnz,
+                    m, config_id, splits, stream);
+}
+
+size_t nm_gemv_grouped_workspace_bytes(int nprob, const int* hs, int w, int nnz, int m, int config_id,
+                                       int splits) {
+  Plan p;
+  if (!hs) return 0;
+  return make_plan(nprob, hs, w, nnz, m, 1, config_id, splits, &p) == NM_OK ? p.workspace : 0;
+}
+
+int nm_gemv_grouped(int dtype, const void* vec, int vec_stride, int nprob, const void* const* mat_data,
+                    const uint8_t* const* mat_index, void* const* out, const int* hs, void* workspace,
+                    size_t workspace_bytes, int w, int nnz, int m, int config_id, int splits, void* stream) {
+  if (!mat_data || !mat_index || !out || !hs) return NM_ERR_NULL_POINTER;
+  if (nprob < 1 || nprob > kMaxProblems) return NM_ERR_BAD_SHAPE;
+  ProblemPtrs pp[kMaxProblems];
+  for (int i = 0; i < nprob; ++i) pp[i] = {mat_data[i], mat_index[i], out[i]};
+  return launch(dtype, vec, vec_stride, nprob, pp, hs, 1, workspace, workspace_bytes, w, nnz, m, config_id,
+                splits, stream);
+}
+
+size_t nm_gemv_gate_up_workspace_bytes(int h, int w, int nnz, int m, int config_id, int splits) {
+  Plan p;
+  return make_plan(1, &h, w, nnz, m, 2, config_id, splits, &p) == NM_OK ? p.workspace : 0;
+}
+
+int nm_gemv_gate_up_silu(int dtype, const void* vec, int vec_stride, const void* gate_data,
+                         const uint8_t* gate_index, const void* up_data, const uint8_t* up_index, void* out,
+                         void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
+                         int config_id, int splits, void* stream) {
+  const ProblemPtrs pp[2] = {{gate_data, gate_index, out}, {up_data, up_index, out}};
+  return launch(dtype, vec, vec_stride, 1, pp, &h, 2, workspace, workspace_bytes, w, nnz, m, config_id, splits,
+                stream);
 }
 
 int nm_num_configs(void) { return kNumConfigs; }
 
+int nm_num_gate_up_configs(void) { return kNumDualConfigs; }
+
 int nm_config_describe(int config_id, char* buf, int buf_len) {
-  if (config_id < 0 || config_id >= kNumConfigs || !buf || buf_len <= 0) return NM_ERR_BAD_CONFIG;
-  const Config& c = kConfigs[config_id];
-  snprintf(buf, (size_t)buf_len, "th%d_u%d%s", c.th, c.u, c.nt ? "" : "_cached");
-  return NM_OK;
+  if (!buf || buf_len <= 0) return NM_ERR_BAD_CONFIG;
+  if (config_id >= 0 && config_id < kNumConfigs) {
+    const Config& c = kConfigs[config_id];
+    snprintf(buf, (size_t)buf_len, "th%d_u%d%s", c.th, c.u, c.nt ? "" : "_cached");
+    return NM_OK;
+  }
+  const int d = config_id - kNumConfigs;
+  if (d >= 0 && d < kNumDualConfigs) {
+    const Config& c = kDualConfigs[d];
+    snprintf(buf, (size_t)buf_len, "pair_th%d_u%d", c.th, c.u);
+    return NM_OK;
+  }
+  return NM_ERR_BAD_CONFIG;
 }
 
 int nm_gemv_plan(int h, int w, int nnz, int m, int config_id, int splits, int* out_config_id,
                  int* out_splits, int* out_blocks, int* out_rows_per_block) {
   Plan p;
-  int rc = make_plan(h, w, nnz, m, config_id, splits, &p);
+  int rc = make_plan(1, &h, w, nnz, m, 1, config_id, splits, &p);
   if (rc != NM_OK) return rc;
   if (out_config_id) *out_config_id = p.cfg;
   if (out_splits) *out_splits = p.splits;
@@ -560,11 +740,11 @@ const char* nm_strerror(int code) {
   switch (code) {
     case NM_OK: return "success";
     case NM_ERR_NULL_POINTER: return "null device pointer";
-    case NM_ERR_BAD_SHAPE: return "shape out of range (h, w, nnz, m, vec_stride)";
+    case NM_ERR_BAD_SHAPE: return "shape out of range (h, w, nnz, m, vec_stride, problem count)";
     case NM_ERR_H_NOT_MULTIPLE_128: return "h must be divisible by 128";
     case NM_ERR_W_NOT_MULTIPLE_NNZ: return "w must be divisible by nnz";
     case NM_ERR_MISALIGNED: return "mat_data/out must be 16-byte aligned, workspace 256-byte aligned";
-    case NM_ERR_WORKSPACE: return "workspace missing or smaller than nm_gemv_workspace_bytes()";
+    case NM_ERR_WORKSPACE: return "workspace missing or smaller than the *_workspace_bytes() value";
     case NM_ERR_BAD_CONFIG: return "unknown dtype, config id or split count";
     default: break;
   }

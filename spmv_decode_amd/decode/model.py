@@ -9,10 +9,18 @@ unchanged. Only decode (one token per step) is implemented: the KV cache is
 static, the position is a device tensor, and a step contains no host
 synchronisation, so it can be captured once in a hipGraph and replayed.
 
-Numerics follow the published architectures: RMSNorm in fp32, rotary
-embeddings in the split-half ("rotate half") convention with Llama-3.1's
-frequency scaling, grouped-query attention with fp32 softmax, SiLU-gated MLP,
-Qwen3's per-head RMSNorm on queries and keys before the rotary embedding.
+Numerics follow the published architectures: RMSNorm in fp32 (one fused
+`F.rms_norm` kernel), rotary embeddings on interleaved (even, odd) pairs as a
+complex multiply (the convention of the reference's gpt-fast model,
+model.py:310-322; Hugging Face checkpoints need the usual q/k row permutation),
+Llama-3.1's frequency scaling, grouped-query attention with the softmax
+computed in fp32, SiLU-gated MLP, Qwen3's per-head RMSNorm on queries and keys
+before the rotary embedding.
+
+A step is written for few kernel launches, since at batch 1 every small
+kernel costs a few microseconds: the q/k/v projections write into slices of
+one buffer, so the rotary embedding runs once over queries and keys; the
+attention scale and causal mask are folded into one batched multiply-add.
 """
 from __future__ import annotations
 
@@ -81,17 +89,38 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
-        xf = x.float()
-        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
-        return xf.to(x.dtype) * self.weight
+        return F.rms_norm(x, (x.shape[-1],), self.weight, self.eps)
 
 
-def rotate(x: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor) -> torch.Tensor:
-    """Rotary embedding, split-half convention, computed in fp32. x: [..., head_dim]."""
-    xf = x.float()
-    h = xf.shape[-1] // 2
-    x1, x2 = xf[..., :h], xf[..., h:]
-    return torch.cat((x1 * cos - x2 * sin, x2 * cos + x1 * sin), dim=-1).to(x.dtype)
+def rotate(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
+    """Rotary embedding on interleaved (even, odd) pairs, in fp32.
+    x: [..., head_dim]; freqs: complex64 [head_dim/2] (cos + i sin)."""
+    xc = torch.view_as_complex(x.float().reshape(*x.shape[:-1], -1, 2))
+    return torch.view_as_real(xc * freqs).flatten(-2).to(x.dtype)
+
+
+def linear_into(lin: nn.Module, x2d: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """y = lin(x) written into `out` ([1, h] contiguous slice): the sparse GEMV's
+    `out=` for NmSparseLinear, torch.mm (hipBLASLt) for a dense nn.Linear."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    if isinstance(lin, NmSparseLinear):
+        from ..hip_spmv import nmsparse_spmv_forward_hip
+
+        return nmsparse_spmv_forward_hip(x2d, lin.mat_data, lin.mat_index, lin.w, lin.h, lin.block_width, 128,
+                                         lin.vec_width, 1, x2d.shape[1], out=out)
+    return torch.mm(x2d, lin.weight.t(), out=out)
+
+
+def grouped_sparse(mods) -> bool:
+    """True when every module is an NmSparseLinear with the same w and N:M, so
+    they can share one launch (grouped GEMV, or the gate/up pair)."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    if not all(isinstance(m, NmSparseLinear) for m in mods):
+        return False
+    m0 = mods[0]
+    return all((m.w, m.block_width, m.vec_width) == (m0.w, m0.block_width, m0.vec_width) for m in mods)
 
 
 class Attention(nn.Module):
@@ -107,26 +136,38 @@ class Attention(nn.Module):
             self.q_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
             self.k_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
 
-    def forward(self, x, cos, sin, k_cache_t, v_cache, pos, mask):
-        """x [1, 1, dim]; k_cache_t [kvh, head_dim, S] (pre-transposed keys);
-        v_cache [kvh, S, head_dim]; pos [1] int64; mask [S] additive fp32."""
+    def forward(self, x, freqs, k_cache_t, v_cache, pos, mask):
+        """x [1, 1, dim]; freqs complex64 [1, head_dim/2]; k_cache_t [kvh, head_dim, S]
+        (pre-transposed keys); v_cache [kvh, S, head_dim]; pos [1] int64;
+        mask [S] additive (0 / -inf) in the activation dtype."""
         c = self.cfg
         g = c.n_heads // c.n_kv_heads
-        q = self.q_proj(x).view(c.n_heads, c.head_dim)
-        k = self.k_proj(x).view(c.n_kv_heads, c.head_dim)
-        v = self.v_proj(x).view(c.n_kv_heads, c.head_dim)
+        qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+        x2d = x.view(1, -1)
+        qkv = torch.empty(1, qd + 2 * kvd, dtype=x.dtype, device=x.device)
+        slices = (qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:])
+        projs = (self.q_proj, self.k_proj, self.v_proj)
+        if grouped_sparse(projs):
+            from ..hip_spmv import nmsparse_gemv_grouped
+
+            nmsparse_gemv_grouped(x2d, [(p.mat_data, p.mat_index) for p in projs], projs[0].block_width,
+                                  projs[0].vec_width, outs=slices)
+        else:
+            for proj, sl in zip(projs, slices):
+                linear_into(proj, x2d, sl)
+        qk = qkv[0, :qd + kvd].view(c.n_heads + c.n_kv_heads, c.head_dim)
         if c.qk_norm:
-            q = self.q_norm(q)
-            k = self.k_norm(k)
-        q = rotate(q, cos, sin)
-        k = rotate(k, cos, sin)
+            qk = torch.cat((self.q_norm(qk[:c.n_heads]), self.k_norm(qk[c.n_heads:])))
+        qk = rotate(qk, freqs)
+        q, k = qk[:c.n_heads], qk[c.n_heads:]
+        v = qkv[0, qd + kvd:].view(c.n_kv_heads, 1, c.head_dim)
         k_cache_t.index_copy_(2, pos, k.unsqueeze(-1))
-        v_cache.index_copy_(1, pos, v.unsqueeze(1))
-        qg = q.view(c.n_kv_heads, g, c.head_dim)
-        scores = torch.bmm(qg, k_cache_t).float() * (1.0 / math.sqrt(c.head_dim)) + mask
-        probs = torch.softmax(scores, dim=-1).to(x.dtype)
+        v_cache.index_copy_(1, pos, v)
+        scores = torch.baddbmm(mask.expand(c.n_kv_heads, g, -1), q.view(c.n_kv_heads, g, c.head_dim), k_cache_t,
+                               alpha=1.0 / math.sqrt(c.head_dim))
+        probs = torch.softmax(scores, dim=-1)  # fp16 in/out, fp32 inside
         y = torch.bmm(probs, v_cache)  # [kvh, g, head_dim]
-        return self.o_proj(y.reshape(1, 1, c.n_heads * c.head_dim))
+        return self.o_proj(y.view(1, 1, qd))
 
 
 class MLP(nn.Module):
@@ -137,6 +178,13 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.inter, cfg.dim, bias=False)
 
     def forward(self, x):
+        if grouped_sparse((self.gate_proj, self.up_proj)):
+            from ..hip_spmv import nmsparse_gate_up_silu
+
+            g, u = self.gate_proj, self.up_proj
+            act = nmsparse_gate_up_silu(x.view(1, -1), (g.mat_data, g.mat_index), (u.mat_data, u.mat_index),
+                                        g.block_width, g.vec_width)
+            return self.down_proj(act.view(1, 1, -1))
         return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
 
 
@@ -148,8 +196,8 @@ class Block(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.dim, cfg.norm_eps)
         self.mlp = MLP(cfg)
 
-    def forward(self, x, cos, sin, k_cache_t, v_cache, pos, mask):
-        h = x + self.self_attn(self.input_layernorm(x), cos, sin, k_cache_t, v_cache, pos, mask)
+    def forward(self, x, freqs, k_cache_t, v_cache, pos, mask):
+        h = x + self.self_attn(self.input_layernorm(x), freqs, k_cache_t, v_cache, pos, mask)
         return h + self.mlp(self.post_attention_layernorm(h))
 
 
@@ -175,19 +223,18 @@ class Decoder(nn.Module):
                         for _ in range(c.n_layers)]
         t = torch.arange(max_seq, dtype=torch.float64)
         ang = torch.outer(t, rope_inv_freq(c))
-        self.rope_cos = ang.cos().float().to(device)
-        self.rope_sin = ang.sin().float().to(device)
+        self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
         self.positions = torch.arange(max_seq, device=device)
+        self.mask_dtype = dtype
 
     def forward_step(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """One decode step: token [1, 1] int64 and pos [1] int64 on the device
         -> logits [1, vocab]. No host synchronisation."""
         x = self.embed_tokens(token)  # [1, 1, dim]
-        cos = self.rope_cos.index_select(0, pos)
-        sin = self.rope_sin.index_select(0, pos)
-        mask = torch.where(self.positions <= pos, 0.0, float("-inf")).float()
+        freqs = self.rope.index_select(0, pos)
+        mask = torch.where(self.positions <= pos, 0.0, float("-inf")).to(self.mask_dtype)
         for i, layer in enumerate(self.layers):
-            x = layer(x, cos, sin, self.k_cache_t[i], self.v_cache[i], pos, mask)
+            x = layer(x, freqs, self.k_cache_t[i], self.v_cache[i], pos, mask)
         return self.lm_head(self.norm(x)).view(1, -1)
 
 

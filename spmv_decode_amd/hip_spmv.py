@@ -23,6 +23,7 @@ device before capturing, as the reference's benchmarks do per shape
 """
 from __future__ import annotations
 
+import ctypes
 import warnings
 
 import torch
@@ -172,4 +173,86 @@ def nmsparse_spmv_forward_hip(
 # Drop-in name of the reference wrapper (triton_spmv.py:229).
 nmsparse_spmv_forward_triton_ptx = nmsparse_spmv_forward_hip
 
-__all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "validate_args", "workspace_for"]
+
+def _prepare_out(out, h, like):
+    if out is None:
+        return torch.empty((1, h), dtype=like.dtype, device=like.device)
+    if (out.dtype != like.dtype or out.numel() != h or not out.is_contiguous() or out.device != like.device
+            or out.data_ptr() % 16):
+        raise ValueError("out must be a contiguous, 16-byte aligned tensor of h elements of vec.dtype on vec.device")
+    return out
+
+
+def _aligned(md):
+    return md if md.data_ptr() % 16 == 0 else md.clone()
+
+
+def nmsparse_gemv_grouped(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, config_id=-1, splits=0):
+    """Several N:M GEMVs that read the same `vec` [1, K], in one launch.
+
+    `problems` is a sequence of 1-4 (mat_data [w, h_i], mat_index [w/N, N])
+    pairs with the same w; returns a list of [1, h_i] outputs (or writes into
+    `outs`). Each output equals what nmsparse_spmv_forward_hip computes for that
+    problem with the same configuration. Used for the q/k/v projections of a
+    decoder layer (one launch instead of three).
+    """
+    if not 1 <= len(problems) <= 4:
+        raise ValueError("nmsparse_gemv_grouped takes 1 to 4 problems")
+    w = problems[0][0].shape[0]
+    K = vec.shape[-1]
+    for md, mi in problems:
+        validate_args(vec, md, mi, w, md.shape[1], BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
+    hs = [int(md.shape[1]) for md, _ in problems]
+    outs = [None] * len(problems) if outs is None else list(outs)
+    outs = [_prepare_out(o, h, vec) for o, h in zip(outs, hs)]
+    mats = [_aligned(md) for md, _ in problems]
+    lib = _lib.load()
+    n = len(problems)
+    hs_c = (ctypes.c_int * n)(*hs)
+    need = lib.nm_gemv_grouped_workspace_bytes(n, hs_c, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
+    if need == 0:
+        raise ValueError("grouped shape outside what libnmsparse_hip supports")
+    device = vec.device
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        ws = workspace_for(device, need, stream)
+        md_c = (ctypes.c_void_p * n)(*[m.data_ptr() for m in mats])
+        mi_c = (ctypes.c_void_p * n)(*[mi.data_ptr() for _, mi in problems])
+        out_c = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
+        rc = lib.nm_gemv_grouped(_DTYPE_CODE[vec.dtype], vec.data_ptr(), vec.stride(1), n, md_c, mi_c, out_c, hs_c,
+                                 ws.data_ptr(), ws.numel(), w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits),
+                                 stream)
+    _lib.check(rc, "nm_gemv_grouped")
+    return outs
+
+
+def nmsparse_gate_up_silu(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1, splits=0):
+    """silu(W_gate @ vec) * (W_up @ vec) for two N:M-sparse [w, h] weights in one
+    launch; `gate` and `up` are (mat_data, mat_index) pairs. fp32 throughout,
+    one rounding to vec.dtype. Returns [1, h]."""
+    (gd, gi), (ud, ui) = gate, up
+    if gd.shape != ud.shape:
+        raise ValueError(f"gate {tuple(gd.shape)} and up {tuple(ud.shape)} must have the same shape")
+    w, h = gd.shape
+    K = vec.shape[-1]
+    validate_args(vec, gd, gi, w, h, BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
+    validate_args(vec, ud, ui, w, h, BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
+    out = _prepare_out(out, h, vec)
+    gd, ud = _aligned(gd), _aligned(ud)
+    lib = _lib.load()
+    need = lib.nm_gemv_gate_up_workspace_bytes(h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
+    if need == 0:
+        raise ValueError("gate/up shape outside what libnmsparse_hip supports")
+    device = vec.device
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        ws = workspace_for(device, need, stream)
+        rc = lib.nm_gemv_gate_up_silu(_DTYPE_CODE[vec.dtype], vec.data_ptr(), vec.stride(1), gd.data_ptr(),
+                                      gi.data_ptr(), ud.data_ptr(), ui.data_ptr(), out.data_ptr(), ws.data_ptr(),
+                                      ws.numel(), h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits), stream)
+    _lib.check(rc, "nm_gemv_gate_up_silu")
+    return out
+
+
+__all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
+           "nmsparse_gate_up_silu", "validate_args", "workspace_for"]

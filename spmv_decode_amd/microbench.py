@@ -122,6 +122,48 @@ def time_sparse(case: RotatingCase, config_id=-1, splits=0, reps=20) -> float:
     return graph_us_per_launch([lambda i=i: case.launch(i, config_id, splits) for i in range(case.copies)], reps)
 
 
+def time_grouped(cases, reps=20) -> float:
+    """One grouped launch over `cases` (RotatingCase list with equal copies,
+    sharing cases[0].x) per rotation step; us per launch."""
+    from .hip_spmv import nmsparse_gemv_grouped
+
+    c0 = cases[0]
+    copies = min(c.copies for c in cases)
+
+    def launch(i):
+        nmsparse_gemv_grouped(c0.x, [c.mats[i] for c in cases], c0.nnz, c0.m, outs=[c.out for c in cases])
+
+    return graph_us_per_launch([lambda i=i: launch(i) for i in range(copies)], reps)
+
+
+def time_pair(gate: RotatingCase, up: RotatingCase, reps=20, config_id=-1, splits=0) -> float:
+    """One gate/up SiLU pair launch per rotation step; us per launch."""
+    from .hip_spmv import nmsparse_gate_up_silu
+
+    copies = min(gate.copies, up.copies)
+
+    def launch(i):
+        nmsparse_gate_up_silu(gate.x, gate.mats[i], up.mats[i], gate.nnz, gate.m, out=gate.out,
+                              config_id=config_id, splits=splits)
+
+    return graph_us_per_launch([lambda i=i: launch(i) for i in range(copies)], reps)
+
+
+def grouped_bytes(cases) -> int:
+    """Algorithmic bytes of one grouped launch: every problem's weights, index
+    bytes and outputs, the shared activations once."""
+    c0 = cases[0]
+    elem = torch.finfo(c0.dtype).bits // 8
+    return sum(elem * c.w * c.n_out + c.w + elem * c.n_out for c in cases) + elem * c0.n_in
+
+
+def pair_bytes(gate: RotatingCase, up: RotatingCase) -> int:
+    """Algorithmic bytes of one gate/up pair launch: both weights and index
+    tables, the activations once, one output."""
+    elem = torch.finfo(gate.dtype).bits // 8
+    return 2 * (elem * gate.w * gate.n_out + gate.w) + elem * gate.n_in + elem * gate.n_out
+
+
 def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda") -> float:
     b = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
     copies = max(1, math.ceil(rotate_bytes / b))
@@ -230,7 +272,8 @@ def read_ceiling(sizes=(4_206_592, 16_795_648, 58_759_168, 268_435_456, 1 << 30)
 def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     """Workload for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
     three copies of a 256 MiB buffer (the known-size calibration kernel), then
-    three GEMV launches per shape, each on distinct weights."""
+    three GEMV launches per shape, each on distinct weights, then three grouped
+    q/k/v launches and three gate/up pair launches at the Llama-3.1-8B shapes."""
     x = torch.empty(128 << 20, dtype=torch.float16, device="cuda").normal_()
     y = torch.empty_like(x)
     for _ in range(3):
@@ -242,6 +285,19 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
             case.launch(i)
         torch.cuda.synchronize()
         log(f"traffic probe: {n_out}x{n_in} {nnz}:{m} plan {_lib.plan(n_out, case.w, nnz, m)}")
+    from .hip_spmv import nmsparse_gate_up_silu, nmsparse_gemv_grouped
+
+    qkv = [RotatingCase(h, 4096, nnz, m, rotate_bytes=0, min_copies=3, seed=10 + i)
+           for i, h in enumerate((4096, 1024, 1024))]
+    for i in range(3):
+        nmsparse_gemv_grouped(qkv[0].x, [c.mats[i] for c in qkv], nnz, m, outs=[c.out for c in qkv])
+    torch.cuda.synchronize()
+    del qkv
+    g, u = (RotatingCase(14336, 4096, nnz, m, rotate_bytes=0, min_copies=3, seed=20 + i) for i in range(2))
+    for i in range(3):
+        nmsparse_gate_up_silu(g.x, g.mats[i], u.mats[i], nnz, m, out=g.out)
+    torch.cuda.synchronize()
+    log("traffic probe: grouped q/k/v and gate/up pair done")
 
 
 def _parse_pairs(text, sep):

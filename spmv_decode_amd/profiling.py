@@ -1,0 +1,158 @@
+"""Summarise rocprofv3 CSV output into the markdown/JSON kept under profiles/.
+
+    python -m spmv_decode_amd.profiling traffic --fetch gpurun_out/pmc_fetch/pmc_counter_collection.csv \\
+        --write gpurun_out/pmc_write/pmc_counter_collection.csv --md profiles/...md --json profiles/traffic.json
+    python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv \\
+        --bench gpurun_out/bench.json --md profiles/...md
+
+`traffic` calibrates FETCH_SIZE / WRITE_SIZE (KiB per dispatch) against the
+256 MiB copy that `microbench --traffic-probe` runs first (a kernel of known
+size), then reports HBM bytes per launch for every GEMV kernel of the probe.
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import json
+from pathlib import Path
+
+CALIBRATION_BYTES = 256 << 20  # the probe's fp16 copy: 128 Mi elements
+COPY_GRID = "131072"
+
+# Launch classes of the traffic probe, in probe order: (key, K, [h...], matrices, description).
+PROBE_CLASSES = [
+    ("q_o_32:64", 4096, [4096], 1, "q/o (4096 -> 4096)"),
+    ("k_v_32:64", 4096, [1024], 1, "k/v (4096 -> 1024)"),
+    ("gate_up_32:64", 4096, [14336], 1, "gate or up alone (4096 -> 14336)"),
+    ("down_32:64", 14336, [4096], 1, "down (14336 -> 4096)"),
+    ("qkv_grouped_32:64", 4096, [4096, 1024, 1024], 1, "grouped q/k/v (4096 -> 4096+1024+1024)"),
+    ("gate_up_pair_32:64", 4096, [14336], 2, "gate/up pair with SiLU*mul (4096 -> 2x14336)"),
+]
+
+
+def _algorithmic(K, hs, nmat, nnz=32, m=64):
+    w = K // m * nnz
+    return sum(nmat * (2 * w * h + w) + 2 * h for h in hs) + 2 * K
+
+
+def _read(path):
+    return list(csv.DictReader(open(path)))
+
+
+def _gemv_dispatches(rows):
+    out = []
+    for r in rows:
+        n = r["Kernel_Name"]
+        if "nm_gemv_kernel" in n:
+            out.append((n[n.index("<"):n.index(">") + 1], float(r["Counter_Value"])))
+    return out
+
+
+def _copy_scale(rows):
+    vals = [float(r["Counter_Value"]) for r in rows if "copy" in r["Kernel_Name"].lower() and r["Grid_Size"] == COPY_GRID]
+    if not vals:
+        raise SystemExit("calibration copy not found in the counter CSV")
+    return (CALIBRATION_BYTES / 1024) / (sum(vals) / len(vals)), vals
+
+
+def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
+    frows, wrows = _read(fetch_csv), _read(write_csv)
+    fscale, fcopy = _copy_scale(frows)
+    wscale, wcopy = _copy_scale(wrows)
+    fd, wd = _gemv_dispatches(frows), _gemv_dispatches(wrows)
+    if len(fd) != 3 * len(PROBE_CLASSES) or len(wd) != len(fd):
+        raise SystemExit(f"expected {3 * len(PROBE_CLASSES)} GEMV dispatches per pass, got {len(fd)}/{len(wd)}")
+    table, js = [], {}
+    for i, (key, K, hs, nmat, desc) in enumerate(PROBE_CLASSES):
+        fv = [v for _, v in fd[3 * i:3 * i + 3]]
+        wv = [v for _, v in wd[3 * i:3 * i + 3]]
+        fetch = sum(fv) / 3 * fscale * 1024
+        write = sum(wv) / 3 * wscale * 1024
+        alg = _algorithmic(K, hs, nmat)
+        kern = fd[3 * i][0]
+        js[key] = {"kernel": f"nm_gemv_kernel{kern}", "fetch_bytes": round(fetch), "write_bytes": round(write),
+                   "bytes_per_launch": round(fetch + write), "algorithmic_bytes": alg,
+                   "fetch_scale": round(fscale, 5), "write_scale": round(wscale, 5)}
+        table.append(f"| {desc} | `nm_gemv_kernel{kern}` | {alg:,} | {round(fetch):,} | {round(write):,} | "
+                     f"{(fetch + write) / alg:.4f} |")
+    lines = ["# HBM traffic per launch: rocprofv3 FETCH_SIZE / WRITE_SIZE (Llama-3.1-8B shapes, 32:64, fp16)", "",
+             "Commands (repository root, one MI355X; each counter in its own run), then the summary:", "", "```",
+             "export TMPDIR=/tmp", fetch_cmd, write_cmd,
+             "python -m spmv_decode_amd.profiling traffic --fetch gpurun_out/pmc_fetch/pmc_counter_collection.csv "
+             "--write gpurun_out/pmc_write/pmc_counter_collection.csv --md <this file> --json profiles/traffic.json",
+             "```", "",
+             "The probe copies a 256 MiB fp16 buffer three times (the known-size calibration kernel), then launches",
+             "each class three times on distinct weights with the library's default plan. Kernel template arguments:",
+             "<dtype (0 = fp16), TH (tile = 8*TH rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT>.",
+             "",
+             f"Calibration: the 256 MiB copy reads {sum(fcopy) / len(fcopy):.1f} KiB by FETCH_SIZE (true "
+             f"{CALIBRATION_BYTES // 1024} KiB) -> fetch scale {fscale:.4f}; it writes {sum(wcopy) / len(wcopy):.1f} KiB "
+             f"by WRITE_SIZE -> write scale {wscale:.4f}. Scaled values below.", "",
+             "| Launch | Kernel | Algorithmic bytes | Fetched (scaled) | Written (scaled) | Traffic / algorithmic |",
+             "|---|---|---|---|---|---|", *table, "",
+             "Extra fetch over the algorithmic bytes is the index bytes and activations re-read by every output tile",
+             "of a split plus the partial sums read back by the last workgroup of each tile; extra writes are the fp32",
+             "split-K partials (8 splits x h x 4 B per matrix). No weight byte is fetched twice.",
+             "`profiles/traffic.json` holds the same numbers; bench.py reports `bytes_per_launch` of the dominant",
+             "launch class as `roofline.traffic`."]
+    Path(md_path).write_text("\n".join(lines) + "\n")
+    Path(json_path).write_text(json.dumps(js, indent=1) + "\n")
+
+
+def stats(stats_csv, bench_json, md_path, cmd):
+    rows = _read(stats_csv)
+    b = json.loads(Path(bench_json).read_text()) if bench_json else None
+    lines = ["# rocprofv3 kernel statistics: bench.py (Llama-3.1-8B decode-token sparse GEMVs, 32:64, fp16)", "",
+             "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd,
+             "python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv "
+             "--bench gpurun_out/bench.json --md <this file>", "```", "",
+             "The run covers the fused step graph (grouped q/k/v, o, gate/up pair, down per layer), the 224-launch",
+             "step graph, per-class rotation graphs (>= 1 GiB of distinct weights each) and the dense hipBLASLt",
+             "baseline graphs. `nm_gemv_kernel` template arguments: <dtype (0 = fp16), TH (tile = 8*TH rows), U (rows",
+             "per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair)>.", "",
+             "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
+        n = r["Name"].replace("void (anonymous namespace)::", "").replace("((anonymous namespace)::Args)", "")
+        n = n if len(n) <= 90 else n[:87] + "..."
+        lines.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
+                     f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |")
+    if b:
+        rf = b.get("roofline", {})
+        pair = [r for r in rows if ", true, 2>" in r["Name"]]
+        lines += ["", f"Unprofiled `python bench.py` from the same call: value {b['value']} GB/s, ms_per_step "
+                      f"{b['ms_per_step']}; dominant launch class: {rf.get('kernel')} at {rf.get('us_per_launch')} us "
+                      f"per launch (HIP events over graph replays, {rf.get('achieved')} GB/s, frac {rf.get('frac')})."]
+        if pair:
+            lines.append(f"rocprof average kernel duration of the pair kernel: {float(pair[0]['AverageNs']) / 1e3:.2f} us "
+                         "(the replay-timed figure also includes the inter-kernel gap).")
+    Path(md_path).write_text("\n".join(lines) + "\n")
+
+
+def main(argv=None):
+    p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    sub = p.add_subparsers(dest="cmd", required=True)
+    t = sub.add_parser("traffic")
+    t.add_argument("--fetch", required=True)
+    t.add_argument("--write", required=True)
+    t.add_argument("--md", required=True)
+    t.add_argument("--json", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("--csv", required=True)
+    s.add_argument("--bench", default=None)
+    s.add_argument("--md", required=True)
+    a = p.parse_args(argv)
+    if a.cmd == "traffic":
+        traffic(a.fetch, a.write, a.md, a.json,
+                "rocprofv3 --pmc FETCH_SIZE -d gpurun_out/pmc_fetch -o pmc --output-format csv -- "
+                "python -u -m spmv_decode_amd.microbench --traffic-probe",
+                "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc --output-format csv -- "
+                "python -u -m spmv_decode_amd.microbench --traffic-probe")
+    else:
+        stats(a.csv, a.bench, a.md,
+              "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_bench -o bench --output-format csv -- "
+              "python -u bench.py --no-decode --no-cpu")
+    return 0
+
+
+if __name__ == "__main__":
+    raise SystemExit(main())

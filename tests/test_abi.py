@@ -120,3 +120,34 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_lib", None)
     with pytest.raises(_lib.NmSparseLibraryError, match="not built"):
         _lib.load()
+
+
+def test_grouped_and_pair_rejections_before_launch():
+    lib = _lib.load()
+    n = 3
+    hs = (ctypes.c_int * n)(4096, 1024, 1024)
+    ptrs = (ctypes.c_void_p * n)(FAKE, FAKE, FAKE)
+    common = (1 << 30, 2048, 32, 64, -1, 0, None)
+    assert lib.nm_gemv_grouped(0, FAKE, 1, 0, ptrs, ptrs, ptrs, hs, FAKE, *common) == -2
+    assert lib.nm_gemv_grouped(0, FAKE, 1, 5, ptrs, ptrs, ptrs, hs, FAKE, *common) == -2
+    assert lib.nm_gemv_grouped(0, FAKE, 1, n, None, ptrs, ptrs, hs, FAKE, *common) == -1
+    bad_h = (ctypes.c_int * n)(4096, 1000, 1024)
+    assert lib.nm_gemv_grouped(0, FAKE, 1, n, ptrs, ptrs, ptrs, bad_h, FAKE, *common) == -3
+    mis = (ctypes.c_void_p * n)(FAKE, FAKE + 2, FAKE)
+    assert lib.nm_gemv_grouped(0, FAKE, 1, n, mis, ptrs, ptrs, hs, FAKE, *common) == -5
+    assert lib.nm_gemv_grouped(0, FAKE, 1, n, ptrs, ptrs, ptrs, hs, FAKE, 1024, 2048, 32, 64, -1, 0, None) == -6
+    need = lib.nm_gemv_grouped_workspace_bytes(n, hs, 2048, 32, 64, -1, 0)
+    one = sum(lib.nm_gemv_workspace_bytes_ex(h, 2048, 32, 64, 1, 0) - _lib.NM_TICKET_BYTES for h in (4096, 1024, 1024))
+    assert need == _lib.NM_TICKET_BYTES + one  # same config (h_total < 8192 -> th16_u8), 8 splits each
+    # the gate/up pair
+    args = (0, FAKE, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, 14336, 2048, 32, 64)
+    assert lib.nm_gemv_gate_up_silu(*args[:3], None, *args[4:], -1, 0, None) == -1
+    assert lib.nm_gemv_gate_up_silu(*args[:5], FAKE + 4, *args[6:], -1, 0, None) == -5
+    assert lib.nm_gemv_gate_up_silu(*args, lib.nm_num_gate_up_configs(), 0, None) == -7
+    a2 = list(args)
+    a2[9] = 4096
+    assert lib.nm_gemv_gate_up_silu(*a2, -1, 0, None) == -6
+    ws = lib.nm_gemv_gate_up_workspace_bytes(14336, 2048, 32, 64, -1, 0)
+    assert ws == _lib.NM_TICKET_BYTES + 2 * 8 * 14336 * 4
+    for j in range(lib.nm_num_gate_up_configs()):
+        assert _lib.describe(_lib.num_configs() + j).startswith("pair_th")

@@ -44,10 +44,11 @@ def _reference_logits(model, tokens):
     ang = torch.outer(torch.arange(T, dtype=torch.float64), inv)
     cos, sin = ang.cos().float(), ang.sin().float()
 
-    def rope(t):  # t [T, heads, hd]
-        h = t.shape[-1] // 2
-        a, b = t[..., :h], t[..., h:]
-        return torch.cat((a * cos[:, None] - b * sin[:, None], b * cos[:, None] + a * sin[:, None]), -1)
+    def rope(t):  # t [T, heads, hd]; rotate each (even, odd) pair by the position's angle
+        a, b = t[..., 0::2], t[..., 1::2]
+        ra = a * cos[:, None] - b * sin[:, None]
+        rb = b * cos[:, None] + a * sin[:, None]
+        return torch.stack((ra, rb), -1).flatten(-2)
 
     def rms(t, mod):
         return (t * torch.rsqrt(t.pow(2).mean(-1, keepdim=True) + mod.eps)) * mod.weight

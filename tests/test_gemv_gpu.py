@@ -243,3 +243,88 @@ def test_c_abi_strided_vec_and_in_range_foreign_positions(gpu):
     mi2[-1, 1] = 7     # last group -> position K + 3, outside vec
     out2 = run(x, md, mi2, nnz, m)
     check_parity(out2, x, md, mi2, nnz, m, "foreign positions")
+
+
+# ---------------------------------------------------------------------------
+# Grouped launches (q/k/v in one grid) and the gate/up pair with SiLU·mul
+# ---------------------------------------------------------------------------
+GROUPS = [  # (K, [h...], nnz, m)
+    (4096, [4096, 1024, 1024], 32, 64), (4096, [4096, 1024, 1024], 2, 4), (1024, [384, 128], 3, 4),
+    (2048, [1152, 128, 256, 640], 8, 16)]
+
+
+@pytest.mark.parametrize("K,hs,nnz,m", GROUPS, ids=lambda v: str(v))
+def test_grouped_matches_single_launches_and_oracle(gpu, K, hs, nnz, m):
+    from spmv_decode_amd.hip_spmv import nmsparse_gemv_grouped
+
+    g = torch.Generator(device="cuda").manual_seed(K + len(hs))
+    x = torch.randn(1, K, generator=g, device="cuda").half()
+    probs = []
+    for i, h in enumerate(hs):
+        _, md, mi = make_case(K, h, nnz, m, seed=100 + i)
+        probs.append((md, mi))
+    say(f"grouped {K} {hs} {nnz}:{m}")
+    outs = nmsparse_gemv_grouped(x, probs, nnz, m)
+    for (md, mi), o in zip(probs, outs):
+        check_parity(o, x, md, mi, nnz, m, f"grouped {hs}")
+    for cfg in (1, 3, 6):
+        for splits in (1, 3, 8):
+            outs = nmsparse_gemv_grouped(x, probs, nnz, m, config_id=cfg, splits=splits)
+            for (md, mi), o in zip(probs, outs):
+                assert torch.equal(o, run(x, md, mi, nnz, m, config_id=cfg, splits=splits)), (cfg, splits)
+
+
+def _silu_ref(x, gd, gi, ud, ui, nnz, m):
+    gv = O.gemv_f64(x.cpu(), gd.cpu(), gi.cpu(), nnz, m)
+    uv = O.gemv_f64(x.cpu(), ud.cpu(), ui.cpu(), nnz, m)
+    return gv / (1.0 + np.exp(-gv)) * uv
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+def test_gate_up_silu_pair(gpu, dtype):
+    from spmv_decode_amd.hip_spmv import nmsparse_gate_up_silu
+
+    n = _lib.load().nm_num_gate_up_configs()
+    for K, h, nnz, m in ((4096, 14336, 32, 64), (4096, 14336, 2, 4), (1024, 384, 3, 4), (5120, 17408, 8, 16)):
+        x, gd, gi = make_case(K, h, nnz, m, seed=h, dtype=dtype)
+        _, ud, ui = make_case(K, h, nnz, m, seed=h + 1, dtype=dtype)
+        ref = _silu_ref(x, gd, gi, ud, ui, nnz, m)
+        for cfg in [-1, *range(n)]:
+            for splits in (0, 1, 3):
+                say(f"gate/up {dtype} {K}x{h} {nnz}:{m} cfg {cfg} splits {splits}")
+                out = nmsparse_gate_up_silu(x, (gd, gi), (ud, ui), nnz, m, config_id=cfg, splits=splits)
+                got = out.float().cpu().numpy().reshape(-1)
+                assert np.isfinite(got).all()
+                if dtype == torch.float32:
+                    assert np.abs(got - ref).max() <= 1e-5 * max(1.0, np.abs(ref).max())
+                else:
+                    e = O.error_metrics(ref, got)
+                    bound = (1e-2, 1e-3) if dtype == torch.float16 else (4e-2, 8e-3)
+                    assert e["max_abs"] <= bound[0] and e["rel_l2"] <= bound[1], (cfg, splits, e)
+
+
+def test_decoder_uses_fused_launches_and_matches_unfused(gpu):
+    """The decoder's grouped q/k/v and gate/up pair give the same logits as the
+    per-Linear path (one rounding less in the MLP, so within fp16 tolerance)."""
+    from spmv_decode_amd.decode import model as dm
+
+    cfg = dm.tiny_config(qk_norm=True)
+    torch.manual_seed(0)
+    mdl = dm.Decoder(cfg).to("cuda", torch.float16)
+    dm.init_weights_(mdl, seed=0, std=0.05)
+    from spmv_decode_amd import swap_to_nmsparse
+
+    swap_to_nmsparse(mdl, 8, "cuda", seed=1, init="device", keep_dense=False)
+    mdl.setup_cache(16, "cuda", dtype=torch.float16)
+    tok = torch.tensor([[3]], device="cuda")
+    pos = torch.tensor([0], device="cuda")
+    with torch.no_grad():
+        fused = mdl.forward_step(tok, pos).float()
+        orig = dm.grouped_sparse
+        dm.grouped_sparse = lambda mods: False
+        try:
+            mdl.setup_cache(16, "cuda", dtype=torch.float16)
+            unfused = mdl.forward_step(tok, pos).float()
+        finally:
+            dm.grouped_sparse = orig
+    torch.testing.assert_close(fused, unfused, rtol=2e-2, atol=2e-2)
