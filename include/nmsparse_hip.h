@@ -68,6 +68,7 @@ extern "C" {
 #define NM_ERR_MISALIGNED (-5)       /* mat_data or out not 16-byte aligned */
 #define NM_ERR_WORKSPACE (-6)        /* workspace missing or too small */
 #define NM_ERR_BAD_CONFIG (-7)       /* explicit config id / split count rejected */
+#define NM_ERR_BAD_EPILOGUE (-8)     /* input-norm / residual / head-layout arguments rejected */
 
 /* Element type codes for the *_ex entry point and nm_gemv_workspace_bytes. */
 #define NM_DTYPE_F16 0
@@ -151,6 +152,78 @@ int nm_gemv_gate_up_silu(int dtype, const void* vec, int vec_stride, const void*
                          void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
                          int config_id, int splits, void* stream);
 int nm_num_gate_up_configs(void);
+
+/*
+ * General launch descriptor: the grouped launch or the gate/up pair, plus the
+ * fusions at the GEMV's edges that a decoder layer needs. No reference
+ * counterpart as an entry point; each fusion replaces PyTorch operations of
+ * the reference's decode step around the sparse Linear:
+ *
+ *  - norm_weight != NULL: the input is RMSNorm(vec) = vec * s * norm_weight
+ *    with s = 1 / sqrt(mean(vec^2) + norm_eps), computed in fp32. The gather
+ *    reads vec * norm_weight and s scales the finished sums, so the
+ *    normalised activation is never stored or rounded. Replaces the
+ *    RMSNorm before the q/k/v and gate/up projections (attention_norm /
+ *    ffn_norm, model.py:182-187; RMSNorm, model.py:258-270). Requires vec_stride == 1, a 16-byte aligned
+ *    vec and K * sizeof(element) a multiple of 16.
+ *  - prob[i].residual != NULL: out = residual + result, added in fp32 before
+ *    the single rounding (the residual adds, model.py:186-187). residual
+ *    may be the same buffer as out (each element is read before it is
+ *    written, by the same lane); it must not overlap vec.
+ *  - heads (grouped kind only; head_dim a multiple of 64 dividing h and the
+ *    configuration's tile of 8*th rows): rows are head_dim-wide heads.
+ *    head_norm != NULL applies a per-head RMSNorm (weight [head_dim],
+ *    head_norm_eps; Qwen3's q_norm / k_norm); rope != 0 then rotates each
+ *    (even, odd) row pair of a head by the angle of position *pos
+ *    (rope_table [pos_limit, head_dim / 2] pairs (cos, sin), fp32), the
+ *    complex-multiply convention of model.py:310-322. A non-zero
+ *    head_stride / elem_stride / pos_stride writes row r to
+ *    out[(r / head_dim) * head_stride + (r % head_dim) * elem_stride
+ *        + (*pos) * pos_stride] (elements), e.g. straight into a KV cache
+ *    slot, replacing the cache update (KVCache.update, model.py:114-123); nothing is stored
+ *    when *pos is outside [0, pos_limit). The residual is added last.
+ *
+ * For NM_KIND_GATE_UP, nprob is 2 (prob[0] gate, prob[1] up, same h); the
+ * output, residual and h are prob[0]'s, and no heads fusion is allowed.
+ * Workspace: nm_gemv_launch_workspace_bytes(desc) (0 if the shape is
+ * rejected). Every other convention is that of the entry points above.
+ */
+#define NM_KIND_GROUPED 0
+#define NM_KIND_GATE_UP 1
+
+typedef struct nm_gemv_problem {
+  const void* mat_data;        /* [w, h] */
+  const uint8_t* mat_index;    /* [w / nnz, nnz] */
+  void* out;                   /* [h] (or the heads layout base) */
+  const void* residual;        /* NULL or [h] */
+  const void* head_norm;       /* NULL or [head_dim] */
+  long long head_stride;       /* heads layout, in elements (all 0: out[r]) */
+  long long elem_stride;
+  long long pos_stride;
+  int h;
+  int rope;                    /* 0 or 1 */
+} nm_gemv_problem;
+
+typedef struct nm_gemv_launch_desc {
+  int dtype;                   /* NM_DTYPE_* */
+  int kind;                    /* NM_KIND_* */
+  int nprob;                   /* grouped: 1..4; gate/up: 2 */
+  int vec_stride;
+  const void* vec;             /* [1, K], K = (w / nnz) * m */
+  const void* norm_weight;     /* NULL or [K] */
+  float norm_eps;
+  float head_norm_eps;
+  int head_dim;
+  int pos_limit;
+  const long long* pos;        /* device int64 [1] */
+  const float* rope_table;     /* device fp32 [pos_limit, head_dim / 2, 2] */
+  int w, nnz, m;
+  int config_id, splits;       /* as nm_gemv_ex (pair configs for the gate/up kind) */
+  nm_gemv_problem prob[4];
+} nm_gemv_launch_desc;
+
+size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);
+int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
  * Configuration introspection. nm_config_describe writes a short text such as

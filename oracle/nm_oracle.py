@@ -95,6 +95,56 @@ def gemv_gather_torch(x, mat_data, mat_index, nnz: int, m: int) -> torch.Tensor:
 
 
 # ---------------------------------------------------------------------------
+# Decode-layer operations around the GEMV (the fused prologue / epilogues)
+# ---------------------------------------------------------------------------
+def rms_norm_f64(x, weight, eps: float) -> np.ndarray:
+    """RMSNorm in float64 over the last axis: x / sqrt(mean(x^2) + eps) * weight
+    (model.py:258-270, RMSNorm._norm and forward; the reference rounds the
+    normalised value to the input dtype before the weight, this value does not)."""
+    xv = to_f64(x)
+    s = 1.0 / np.sqrt(np.mean(xv * xv, axis=-1, keepdims=True) + eps)
+    return xv * s * to_f64(weight)
+
+
+def rope_f64(v, angle_row) -> np.ndarray:
+    """Rotary embedding of interleaved (even, odd) pairs of the last axis by
+    the angles angle_row [head_dim/2] (radians), float64: (a, b) ->
+    (a cos - b sin, b cos + a sin) (model.py:310-322, apply_rotary_emb)."""
+    vv = to_f64(v)
+    a, b = vv[..., 0::2], vv[..., 1::2]
+    c, s = np.cos(angle_row), np.sin(angle_row)
+    out = np.empty_like(vv)
+    out[..., 0::2] = a * c - b * s
+    out[..., 1::2] = b * c + a * s
+    return out
+
+
+def silu_f64(g) -> np.ndarray:
+    """silu(g) = g / (1 + exp(-g)) (model.py:255-256, F.silu)."""
+    gv = np.asarray(g, dtype=np.float64)
+    return gv / (1.0 + np.exp(-gv))
+
+
+def qkv_decode_f64(x, q, k, v, nnz: int, m: int, *, angle_row, head_dim: int, norm=None, q_norm=None,
+                   k_norm=None, eps: float = 1e-6):
+    """Queries, keys and values of one decode step in float64 (model.py:186,
+    attention_norm(x); model.py:219-231, the projections, apply_rotary_emb and
+    the cache update; Qwen3 adds a per-head RMSNorm of q and k before the
+    rotation). q/k/v are (mat_data, mat_index); norm = (weight, eps).
+    Returns (q [n_heads, hd], k [kv_heads, hd], v [kv_heads, hd])."""
+    xin = x
+    if norm is not None:
+        xin = rms_norm_f64(x, norm[0], norm[1]).reshape(-1)
+    outs = []
+    for (md, mi), hn in ((q, q_norm), (k, k_norm), (v, None)):
+        y = gemv_f64(xin, md, mi, nnz, m).reshape(-1, head_dim)
+        if hn is not None:
+            y = rms_norm_f64(y, hn, eps)
+        outs.append(y)
+    return rope_f64(outs[0], angle_row), rope_f64(outs[1], angle_row), outs[2]
+
+
+# ---------------------------------------------------------------------------
 # Packing
 # ---------------------------------------------------------------------------
 def scatter(mat_data, mat_index, nnz: int, m: int, K: int):

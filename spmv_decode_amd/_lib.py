@@ -23,13 +23,35 @@ NM_ERR = {
     -5: "NM_ERR_MISALIGNED",
     -6: "NM_ERR_WORKSPACE",
     -7: "NM_ERR_BAD_CONFIG",
+    -8: "NM_ERR_BAD_EPILOGUE",
 }
+NM_KIND_GROUPED, NM_KIND_GATE_UP = 0, 1
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
 _sz = ctypes.c_size_t
 _ip = ctypes.POINTER(ctypes.c_int)
 _GEMV_ARGS = [_vp, _i, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]
+_ll = ctypes.c_longlong
+
+
+class NmGemvProblem(ctypes.Structure):
+    """struct nm_gemv_problem (include/nmsparse_hip.h)."""
+
+    _fields_ = [("mat_data", _vp), ("mat_index", _vp), ("out", _vp), ("residual", _vp), ("head_norm", _vp),
+                ("head_stride", _ll), ("elem_stride", _ll), ("pos_stride", _ll), ("h", _i), ("rope", _i)]
+
+
+class NmGemvLaunchDesc(ctypes.Structure):
+    """struct nm_gemv_launch_desc (include/nmsparse_hip.h)."""
+
+    _fields_ = [("dtype", _i), ("kind", _i), ("nprob", _i), ("vec_stride", _i), ("vec", _vp),
+                ("norm_weight", _vp), ("norm_eps", ctypes.c_float), ("head_norm_eps", ctypes.c_float),
+                ("head_dim", _i), ("pos_limit", _i), ("pos", _vp), ("rope_table", _vp), ("w", _i), ("nnz", _i),
+                ("m", _i), ("config_id", _i), ("splits", _i), ("prob", NmGemvProblem * 4)]
+
+
+_descp = ctypes.POINTER(NmGemvLaunchDesc)
 
 # Every function declared in include/nmsparse_hip.h: name -> (restype, argtypes).
 ABI = {
@@ -46,12 +68,14 @@ ABI = {
     "nm_gemv_gate_up_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i]),
     "nm_gemv_gate_up_silu": (_i, [_i, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_num_gate_up_configs": (_i, []),
+    "nm_gemv_launch_workspace_bytes": (_sz, [_descp]),
+    "nm_gemv_launch": (_i, [_descp, _vp, _sz, _vp]),
     "nm_config_describe": (_i, [_i, ctypes.c_char_p, _i]),
     "nm_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
 }
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _lib = None
 _lock = threading.Lock()

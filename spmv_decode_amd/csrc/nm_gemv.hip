@@ -40,7 +40,7 @@ constexpr int kBlock = 256;        // lanes per workgroup
 constexpr int kVec = 8;            // output rows per lane
 constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
 constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
-constexpr int kAbiVersion = 2;
+constexpr int kAbiVersion = 3;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -133,14 +133,30 @@ struct Problem {
   void* out;
   float* partial;      // [splits, h] fp32, unused when splits == 1
   uint32_t* tickets;   // [tiles] arrival counters, zero between launches
+  const void* resid;   // optional [h] residual added before the rounding
+  const void* head_w;  // optional [head_dim] per-head RMSNorm weight
+  // Output element of row r: out + (r / head_dim) * head_stride
+  //   + (r % head_dim) * elem_stride + pos * pos_stride (heads layout), or
+  // out + r when all three are zero.
+  long long head_stride;
+  long long elem_stride;
+  long long pos_stride;
   int h;
   int tiles;
   int block_begin;     // first workgroup of this problem in the grid
+  int rope;            // rotate (even, odd) row pairs of each head by pos
 };
 
 struct Args {
   const void* vec;
   long long vec_stride;
+  const void* norm_w;  // optional [K] RMSNorm weight of the input (folded into the gather)
+  const float2* rope;  // [pos_limit, head_dim / 2] (cos, sin) when a problem rotates
+  const long long* pos;  // device position for the heads layout / rotation
+  float norm_eps;
+  float head_eps;
+  int head_dim;
+  int pos_limit;       // positions >= pos_limit (or < 0) store nothing
   int w;
   int nnz;
   int m;
@@ -172,8 +188,11 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   static_assert(XR % CH == 0, "chunk must divide the split");
   static_assert(NMAT == 1 || NMAT == 2, "one matrix, or the gate/up pair");
 
+  constexpr int kWaves = kBlock / 64;
+  constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
   __shared__ __attribute__((aligned(16))) float xs[NMAT][XR];
   __shared__ __attribute__((aligned(16))) float red[NMAT][TK * HT];
+  __shared__ float wsum[kOutPerLane * kWaves];  // per-wave sums (input norm, head norms)
   __shared__ int is_last;
 
   // Problem of this workgroup (uniform; at most kMaxProblems entries).
@@ -241,7 +260,13 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
 
   // 3. Gather the activations: vec[(c/nnz)*m + position], fp32 in LDS. Rows
   //    past the split and positions outside vec read as zero.
+  //    With an input RMSNorm, rmsnorm(x) = s * (x * g) with the scalar
+  //    s = 1 / sqrt(mean(x^2) + eps): the gather reads x * g and s scales the
+  //    finished sums.
+  const bool has_norm = a.norm_w != nullptr;
+  const T* __restrict__ gx = static_cast<const T*>(has_norm ? a.norm_w : a.vec);
   T graw[NMAT][G];
+  T wraw[NMAT][G];
   bool gok[NMAT][G];
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
@@ -252,12 +277,63 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
       const int pos = (c / a.nnz) * a.m + gidx[q][j];
       gok[q][j] = (t < cw) && (pos < a.K);
       graw[q][j] = vx[(long long)(gok[q][j] ? pos : 0) * a.vec_stride];
+      if (has_norm) wraw[q][j] = gx[gok[q][j] ? pos : 0];
     }
+  // Sum of squares of the whole input for s (vec is contiguous and 16-byte
+  // aligned with K * sizeof(T) a multiple of 16 when has_norm; the host
+  // checks). Every workgroup computes it, in a fixed order.
+  float ssq = 0.0f;
+  if (has_norm) {
+    const u32x4* xw = static_cast<const u32x4*>(a.vec);
+    const int nw = (int)(((long long)a.K * (long long)sizeof(T)) / 16);  // 16-byte words of vec
+    for (int base = 0; base < nw; base += 4 * kBlock) {
+      u32x4 raw[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) raw[i] = xw[min(base + i * kBlock + tid, nw - 1)];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool ok = base + i * kBlock + tid < nw;
+        float f[8];
+        if constexpr (W == 1) {
+          const u32x4 one[1] = {raw[i]};
+          E::unpack(one, f);
+        } else {
+          const u32x4 r4 = raw[i];
+          const uint32_t d[4] = {r4.x, r4.y, r4.z, r4.w};
+#pragma unroll
+          for (int e = 0; e < 4; ++e) f[e] = __uint_as_float(d[e]);
+#pragma unroll
+          for (int e = 4; e < 8; ++e) f[e] = 0.0f;
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float fe = ok ? f[e] : 0.0f;
+          ssq = __builtin_fmaf(fe, fe, ssq);
+        }
+      }
+    }
+  }
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
 #pragma unroll
-    for (int j = 0; j < G; ++j) xs[q][tid + j * kBlock] = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
+    for (int j = 0; j < G; ++j) {
+      float xv = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
+      if (has_norm) xv *= E::to_f32(wraw[q][j]);
+      xs[q][tid + j * kBlock] = xv;
+    }
+  if (has_norm) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) ssq += __shfl_xor(ssq, off, 64);
+    if ((tid & 63) == 0) wsum[tid >> 6] = ssq;
+  }
   __syncthreads();
+  float s_in = 1.0f;
+  if (has_norm) {
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) t += wsum[i];
+    s_in = rsqrtf(t / (float)a.K + a.norm_eps);
+  }
 
   float acc[NMAT][kVec];
 #pragma unroll
@@ -315,8 +391,7 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   }
   __syncthreads();
 
-  T* __restrict__ out = static_cast<T*>(a.prob[p].out);
-  constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
+  const Problem& P = a.prob[p];
   float tsum[NMAT][kOutPerLane];
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
@@ -331,97 +406,163 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
       tsum[q][j] = s;
     }
 
-  // Output value of one row from its (gate[, up]) sums.
-  auto finish = [&](const float (&v)[NMAT]) -> T {
-    if constexpr (NMAT == 1) {
-      return E::from_f32(v[0]);
-    } else {
-      return E::from_f32(silu(v[0]) * v[1]);
+  uint32_t* tickets = P.tickets;
+  if (a.splits > 1) {
+    // 6. Split-K: publish the partial tile, count arrivals, last one reduces.
+    //    The handoff uses agent-scope atomics only, never an agent-scope
+    //    fence: on gfx950 such a fence writes back and invalidates the whole
+    //    L2 of the workgroup's XCD (buffer_wbl2 / buffer_inv), which costs
+    //    more than the GEMV itself. Each partial is published with a
+    //    returning atomic swap: its result comes back only after the swap has
+    //    been performed at the device coherence point, and each lane waits
+    //    for all of its results (vmcnt(0)) before the barrier. Lane 0 then
+    //    counts the arrival; the last arrival reads every partial with
+    //    agent-scope atomic loads (sc1, coherent across XCDs) in split order,
+    //    so the sum is deterministic.
+    float sink = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q) {
+      float* part = a.prob[NMAT == 1 ? p : q].partial + (size_t)split * (size_t)h;
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int r = tile * HT + o;
+        if (o < HT && r < h)
+          sink += __hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
     }
-  };
+    // Consume the swap results (a.splits is never negative) so the compiler
+    // keeps the returning form of the instruction.
+    if (a.splits < 0) static_cast<T*>(P.out)[tid] = E::from_f32(sink);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      is_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!is_last) return;
+  }
 
-  if (a.splits == 1) {
+  // 7. Epilogue of the workgroup that owns the finished tile. Its operands
+  //    (residual, head-norm weights, position, rotation) are loaded first so
+  //    that they are in flight together with the partial sums.
+  const int hd = a.head_dim;
+  const bool heads = NMAT == 1 && (P.head_w != nullptr || P.rope != 0);
+  const bool head_layout = (P.head_stride | P.elem_stride | P.pos_stride) != 0;
+  const bool need_pos = P.rope != 0 || P.pos_stride != 0;
+  long long pos = 0;
+  if (need_pos) pos = *a.pos;
+  const bool pos_ok = !need_pos || (pos >= 0 && pos < (long long)a.pos_limit);
+  const long long pos_c = pos_ok ? pos : 0;
+  const T* __restrict__ resid = static_cast<const T*>(P.resid);
+  const T* __restrict__ head_w = static_cast<const T*>(P.head_w);
+  float rv[kOutPerLane], hw[kOutPerLane];
+  float2 cs[kOutPerLane];
+#pragma unroll
+  for (int j = 0; j < kOutPerLane; ++j) {
+    const int o = tid + j * kBlock;
+    const int r = min(tile * HT + min(o, HT - 1), h - 1);  // clamped: loads stay in range
+    rv[j] = resid ? E::to_f32(resid[r]) : 0.0f;
+    hw[j] = 1.0f;
+    cs[j] = make_float2(1.0f, 0.0f);
+    if (heads) {
+      if (head_w) hw[j] = E::to_f32(head_w[r % hd]);
+      if (P.rope) cs[j] = a.rope[pos_c * (long long)(hd / 2) + (r % hd) / 2];
+    }
+  }
+  if (a.splits > 1) {
 #pragma unroll
     for (int j = 0; j < kOutPerLane; ++j) {
       const int o = tid + j * kBlock;
       const int r = tile * HT + o;
       if (o < HT && r < h) {
-        float v[NMAT];
 #pragma unroll
-        for (int q = 0; q < NMAT; ++q) v[q] = tsum[q][j];
-        out[r] = finish(v);
+        for (int q = 0; q < NMAT; ++q) {
+          float* pp = a.prob[NMAT == 1 ? p : q].partial + r;
+          float s = 0.0f;
+          int sp = 0;
+          for (; sp + 8 <= a.splits; sp += 8) {
+            float t8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += t8[i];
+          }
+          for (; sp < a.splits; ++sp)
+            s += __hip_atomic_load(pp + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          tsum[q][j] = s;
+        }
       }
     }
-    return;
   }
 
-  // 6. Split-K: publish the partial tile, count arrivals, last one reduces.
-  //    The handoff uses agent-scope atomics only, never an agent-scope fence:
-  //    on gfx950 such a fence writes back and invalidates the whole L2 of the
-  //    workgroup's XCD (buffer_wbl2 / buffer_inv), which costs more than the
-  //    GEMV itself. Each partial is published with a returning atomic swap:
-  //    its result comes back only after the swap has been performed at the
-  //    device coherence point, and each lane waits for all of its results
-  //    (vmcnt(0)) before the barrier. Lane 0 then counts the arrival; the
-  //    last arrival reads every partial with agent-scope atomic loads (sc1,
-  //    coherent across XCDs) in split order, so the sum is deterministic.
-  float sink = 0.0f;
+  float val[kOutPerLane];
 #pragma unroll
-  for (int q = 0; q < NMAT; ++q) {
-    float* part = a.prob[NMAT == 1 ? p : q].partial + (size_t)split * (size_t)h;
+  for (int j = 0; j < kOutPerLane; ++j) {
+    const int o = tid + j * kBlock;
+    const bool valid = o < HT && tile * HT + o < h;
+    float v;
+    if constexpr (NMAT == 1) {
+      v = tsum[0][j] * s_in;
+    } else {
+      v = silu(tsum[0][j] * s_in) * (tsum[1][j] * s_in);
+    }
+    val[j] = valid ? v : 0.0f;
+  }
+
+  if (heads) {
+    // Per-head RMSNorm over head_dim consecutive rows (head_dim is a multiple
+    // of 64 dividing the tile, so a head is whole waves of this workgroup),
+    // then the rotation of each (even, odd) row pair by the angle at pos.
+    if (head_w) {
 #pragma unroll
-    for (int j = 0; j < kOutPerLane; ++j) {
-      const int o = tid + j * kBlock;
-      const int r = tile * HT + o;
-      if (o < HT && r < h)
-        sink += __hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      for (int j = 0; j < kOutPerLane; ++j) {
+        float sq = val[j] * val[j];
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) sq += __shfl_xor(sq, off, 64);
+        if ((tid & 63) == 0) wsum[(j * kBlock + tid) >> 6] = sq;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int f0 = ((o / hd) * hd) >> 6;
+        float t = 0.0f;
+        if (o < HT)
+          for (int f = f0; f < f0 + (hd >> 6); ++f) t += wsum[f];
+        val[j] *= rsqrtf(t / (float)hd + a.head_eps) * hw[j];
+      }
+    }
+    if (P.rope) {
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const float partner = __shfl_xor(val[j], 1, 64);
+        val[j] = (tid & 1) == 0 ? val[j] * cs[j].x - partner * cs[j].y : val[j] * cs[j].x + partner * cs[j].y;
+      }
     }
   }
-  // Consume the swap results (a.splits is never negative) so the compiler
-  // keeps the returning form of the instruction.
-  if (a.splits < 0) out[tid] = E::from_f32(sink);
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  uint32_t* tickets = a.prob[p].tickets;
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
-                                                 __HIP_MEMORY_SCOPE_AGENT);
-    is_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
-  }
-  __syncthreads();
-  if (!is_last) return;
 
+  T* __restrict__ out = static_cast<T*>(P.out);
 #pragma unroll
   for (int j = 0; j < kOutPerLane; ++j) {
     const int o = tid + j * kBlock;
     const int r = tile * HT + o;
-    if (o < HT && r < h) {
-      float v[NMAT];
-#pragma unroll
-      for (int q = 0; q < NMAT; ++q) {
-        float* pp = a.prob[NMAT == 1 ? p : q].partial + r;
-        float s = 0.0f;
-        int sp = 0;
-        for (; sp + 8 <= a.splits; sp += 8) {
-          float t8[8];
-#pragma unroll
-          for (int i = 0; i < 8; ++i)
-            t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
-                                      __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-          for (int i = 0; i < 8; ++i) s += t8[i];
-        }
-        for (; sp < a.splits; ++sp)
-          s += __hip_atomic_load(pp + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        v[q] = s;
-      }
-      out[r] = finish(v);
+    if (o < HT && r < h && pos_ok) {
+      long long off = r;
+      if (head_layout)
+        off = (long long)(r / hd) * P.head_stride + (long long)(r % hd) * P.elem_stride + pos * P.pos_stride;
+      out[off] = E::from_f32(val[j] + rv[j]);
     }
   }
-  if (tid == 0) {
+  if (a.splits > 1 && tid == 0) {
     __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 }
+
 
 // ---------------------------------------------------------------------------
 // Configuration tables (static; no runtime autotuning).
@@ -560,71 +701,136 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
   return NM_OK;
 }
 
-struct ProblemPtrs {
-  const void* mat_data;
-  const uint8_t* mat_index;
-  void* out;
-};
-
-int launch(int dtype, const void* vec, int vec_stride, int nprob, const ProblemPtrs* probs, const int* hs,
-           int nmat, void* workspace, size_t workspace_bytes, int w, int nnz, int m, int cfg, int splits,
-           void* stream) {
-  if (dtype < NM_DTYPE_F16 || dtype > NM_DTYPE_F32) return NM_ERR_BAD_CONFIG;
-  if (!vec || !workspace || !probs) return NM_ERR_NULL_POINTER;
-  const int nmats_total = nmat == 2 ? 2 : nprob;
-  for (int i = 0; i < nmats_total; ++i)
-    if (!probs[i].mat_data || !probs[i].mat_index) return NM_ERR_NULL_POINTER;
-  for (int i = 0; i < nprob; ++i)
-    if (!probs[i].out) return NM_ERR_NULL_POINTER;
-  if (vec_stride < 1) return NM_ERR_BAD_SHAPE;
+// Validate a launch descriptor, plan it and launch. Every entry point of the
+// C ABI goes through here.
+int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes, void* stream,
+           size_t* workspace_needed) {
+  if (d.dtype < NM_DTYPE_F16 || d.dtype > NM_DTYPE_F32) return NM_ERR_BAD_CONFIG;
+  if (d.kind != NM_KIND_GROUPED && d.kind != NM_KIND_GATE_UP) return NM_ERR_BAD_CONFIG;
+  const bool pair = d.kind == NM_KIND_GATE_UP;
+  const int nmat = pair ? 2 : 1;
+  const int nprob = pair ? 1 : d.nprob;  // output problems
+  if (pair ? d.nprob != 2 : (d.nprob < 1 || d.nprob > kMaxProblems)) return NM_ERR_BAD_SHAPE;
+  int hs[kMaxProblems];
+  for (int i = 0; i < nprob; ++i) hs[i] = d.prob[i].h;
+  if (pair && d.prob[1].h != d.prob[0].h) return NM_ERR_BAD_SHAPE;
   Plan p;
-  int rc = make_plan(nprob, hs, w, nnz, m, nmat, cfg, splits, &p);
+  int rc = make_plan(nprob, hs, d.w, d.nnz, d.m, nmat, d.config_id, d.splits, &p);
   if (rc != NM_OK) return rc;
-  for (int i = 0; i < nmats_total; ++i)
-    if (((uintptr_t)probs[i].mat_data & 15u) != 0) return NM_ERR_MISALIGNED;
+  if (workspace_needed) {
+    *workspace_needed = p.workspace;
+    return NM_OK;
+  }
+  if (!d.vec || !workspace) return NM_ERR_NULL_POINTER;
+  for (int i = 0; i < d.nprob; ++i)
+    if (!d.prob[i].mat_data || !d.prob[i].mat_index) return NM_ERR_NULL_POINTER;
   for (int i = 0; i < nprob; ++i)
-    if (((uintptr_t)probs[i].out & 15u) != 0) return NM_ERR_MISALIGNED;
+    if (!d.prob[i].out) return NM_ERR_NULL_POINTER;
+  if (d.vec_stride < 1) return NM_ERR_BAD_SHAPE;
+  for (int i = 0; i < d.nprob; ++i)
+    if (((uintptr_t)d.prob[i].mat_data & 15u) != 0) return NM_ERR_MISALIGNED;
+  for (int i = 0; i < nprob; ++i)
+    if (((uintptr_t)d.prob[i].out & 15u) != 0) return NM_ERR_MISALIGNED;
   if (((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
   if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
 
+  // Epilogue / prologue arguments.
+  const int K = (d.w / d.nnz) * d.m;
+  const size_t esize = d.dtype == NM_DTYPE_F32 ? 4 : 2;
+  if (d.norm_weight) {
+    if (!(d.norm_eps >= 0.0f) || d.vec_stride != 1 || ((uintptr_t)d.vec & 15u) != 0 ||
+        ((size_t)K * esize) % 16 != 0)
+      return NM_ERR_BAD_EPILOGUE;
+  }
+  const Config& c = pair ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
+  const int HT = c.th * kVec;
+  bool any_pos = false, any_rope = false;
+  for (int i = 0; i < nprob; ++i) {
+    const nm_gemv_problem& q = d.prob[i];
+    const bool layout = q.head_stride != 0 || q.elem_stride != 0 || q.pos_stride != 0;
+    const bool heads = q.head_norm != nullptr || q.rope != 0 || layout;
+    if (!heads) continue;
+    if (pair) return NM_ERR_BAD_EPILOGUE;  // the pair writes a plain [h] output
+    if (d.head_dim <= 0 || d.head_dim % 64 != 0 || q.h % d.head_dim != 0 || HT % d.head_dim != 0)
+      return NM_ERR_BAD_EPILOGUE;
+    if (q.head_norm && !(d.head_norm_eps >= 0.0f)) return NM_ERR_BAD_EPILOGUE;
+    any_pos = any_pos || q.rope != 0 || q.pos_stride != 0;
+    any_rope = any_rope || q.rope != 0;
+  }
+  if (any_pos && (!d.pos || d.pos_limit <= 0)) return NM_ERR_BAD_EPILOGUE;
+  if (any_rope && !d.rope_table) return NM_ERR_BAD_EPILOGUE;
+
   Args a;
   memset(&a, 0, sizeof(a));
-  a.vec = vec;
-  a.vec_stride = vec_stride;
-  a.w = w;
-  a.nnz = nnz;
-  a.m = m;
-  a.K = (w / nnz) * m;
+  a.vec = d.vec;
+  a.vec_stride = d.vec_stride;
+  a.norm_w = d.norm_weight;
+  a.norm_eps = d.norm_eps;
+  a.head_eps = d.head_norm_eps;
+  a.head_dim = d.head_dim;
+  a.pos = d.pos;
+  a.pos_limit = d.pos_limit;
+  a.rope = reinterpret_cast<const float2*>(d.rope_table);
+  a.w = d.w;
+  a.nnz = d.nnz;
+  a.m = d.m;
+  a.K = K;
   a.splits = p.splits;
   a.rows_per_split = p.rows_per_split;
-  a.nprob = nmat == 2 ? 2 : nprob;
+  a.nprob = d.nprob;
   char* ws = static_cast<char*>(workspace);
-  for (int i = 0; i < nmats_total; ++i) {
-    const int src = nmat == 2 ? 0 : i;  // the pair shares problem 0's plan
+  for (int i = 0; i < d.nprob; ++i) {
+    const int src = pair ? 0 : i;  // the pair shares problem 0's plan and output
+    const nm_gemv_problem& q = d.prob[src];
     Problem& P = a.prob[i];
-    P.mat_data = probs[i].mat_data;
-    P.mat_index = probs[i].mat_index;
-    P.out = probs[src].out;
+    P.mat_data = d.prob[i].mat_data;
+    P.mat_index = d.prob[i].mat_index;
+    P.out = q.out;
+    P.resid = q.residual;
+    P.head_w = q.head_norm;
+    P.head_stride = q.head_stride;
+    P.elem_stride = q.elem_stride;
+    P.pos_stride = q.pos_stride;
+    P.rope = q.rope;
     P.h = hs[src];
     P.tiles = p.tiles[src];
     P.block_begin = p.block_begin[src];
     P.tickets = reinterpret_cast<uint32_t*>(ws) + p.ticket_off[src];
     P.partial = reinterpret_cast<float*>(ws + p.partial_off[src] +
-                                         (size_t)i * (nmat == 2 ? (size_t)p.splits * (size_t)hs[0] * 4 : 0));
+                                         (size_t)i * (pair ? (size_t)p.splits * (size_t)hs[0] * 4 : 0));
   }
-  const Config& c = nmat == 2 ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
-  hipLaunchKernelGGL(c.fn[dtype][gather_slot(p.rows_per_split)], dim3(p.blocks), dim3(kBlock), 0,
+  hipLaunchKernelGGL(c.fn[d.dtype][gather_slot(p.rows_per_split)], dim3(p.blocks), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NM_OK : (int)e;
 }
 
+nm_gemv_launch_desc plain_desc(int dtype, int kind, const void* vec, int vec_stride, int w, int nnz, int m,
+                               int cfg, int splits) {
+  nm_gemv_launch_desc d;
+  memset(&d, 0, sizeof(d));
+  d.dtype = dtype;
+  d.kind = kind;
+  d.vec = vec;
+  d.vec_stride = vec_stride;
+  d.w = w;
+  d.nnz = nnz;
+  d.m = m;
+  d.config_id = cfg;
+  d.splits = splits;
+  return d;
+}
+
 int launch_one(int dtype, const void* vec, int vec_stride, const void* mat_data, const uint8_t* mat_index,
                void* out, void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m, int cfg,
                int splits, void* stream) {
-  const ProblemPtrs pp = {mat_data, mat_index, out};
-  return launch(dtype, vec, vec_stride, 1, &pp, &h, 1, workspace, workspace_bytes, w, nnz, m, cfg, splits,
-                stream);
+  nm_gemv_launch_desc d = plain_desc(dtype, NM_KIND_GROUPED, vec, vec_stride, w, nnz, m, cfg, splits);
+  d.nprob = 1;
+  d.prob[0].mat_data = mat_data;
+  d.prob[0].mat_index = mat_index;
+  d.prob[0].out = out;
+  d.prob[0].h = h;
+  return launch(d, workspace, workspace_bytes, stream, nullptr);
 }
 
 }  // namespace
@@ -684,10 +890,15 @@ int nm_gemv_grouped(int dtype, const void* vec, int vec_stride, int nprob, const
                     size_t workspace_bytes, int w, int nnz, int m, int config_id, int splits, void* stream) {
   if (!mat_data || !mat_index || !out || !hs) return NM_ERR_NULL_POINTER;
   if (nprob < 1 || nprob > kMaxProblems) return NM_ERR_BAD_SHAPE;
-  ProblemPtrs pp[kMaxProblems];
-  for (int i = 0; i < nprob; ++i) pp[i] = {mat_data[i], mat_index[i], out[i]};
-  return launch(dtype, vec, vec_stride, nprob, pp, hs, 1, workspace, workspace_bytes, w, nnz, m, config_id,
-                splits, stream);
+  nm_gemv_launch_desc d = plain_desc(dtype, NM_KIND_GROUPED, vec, vec_stride, w, nnz, m, config_id, splits);
+  d.nprob = nprob;
+  for (int i = 0; i < nprob; ++i) {
+    d.prob[i].mat_data = mat_data[i];
+    d.prob[i].mat_index = mat_index[i];
+    d.prob[i].out = out[i];
+    d.prob[i].h = hs[i];
+  }
+  return launch(d, workspace, workspace_bytes, stream, nullptr);
 }
 
 size_t nm_gemv_gate_up_workspace_bytes(int h, int w, int nnz, int m, int config_id, int splits) {
@@ -699,9 +910,27 @@ int nm_gemv_gate_up_silu(int dtype, const void* vec, int vec_stride, const void*
                          const uint8_t* gate_index, const void* up_data, const uint8_t* up_index, void* out,
                          void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m,
                          int config_id, int splits, void* stream) {
-  const ProblemPtrs pp[2] = {{gate_data, gate_index, out}, {up_data, up_index, out}};
-  return launch(dtype, vec, vec_stride, 1, pp, &h, 2, workspace, workspace_bytes, w, nnz, m, config_id, splits,
-                stream);
+  nm_gemv_launch_desc d = plain_desc(dtype, NM_KIND_GATE_UP, vec, vec_stride, w, nnz, m, config_id, splits);
+  d.nprob = 2;
+  d.prob[0].mat_data = gate_data;
+  d.prob[0].mat_index = gate_index;
+  d.prob[0].out = out;
+  d.prob[0].h = h;
+  d.prob[1].mat_data = up_data;
+  d.prob[1].mat_index = up_index;
+  d.prob[1].h = h;
+  return launch(d, workspace, workspace_bytes, stream, nullptr);
+}
+
+size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc) {
+  if (!desc) return 0;
+  size_t need = 0;
+  return launch(*desc, nullptr, 0, nullptr, &need) == NM_OK ? need : 0;
+}
+
+int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream) {
+  if (!desc) return NM_ERR_NULL_POINTER;
+  return launch(*desc, workspace, workspace_bytes, stream, nullptr);
 }
 
 int nm_num_configs(void) { return kNumConfigs; }
@@ -745,7 +974,10 @@ const char* nm_strerror(int code) {
     case NM_ERR_W_NOT_MULTIPLE_NNZ: return "w must be divisible by nnz";
     case NM_ERR_MISALIGNED: return "mat_data/out must be 16-byte aligned, workspace 256-byte aligned";
     case NM_ERR_WORKSPACE: return "workspace missing or smaller than the *_workspace_bytes() value";
-    case NM_ERR_BAD_CONFIG: return "unknown dtype, config id or split count";
+    case NM_ERR_BAD_CONFIG: return "unknown dtype, launch kind, config id or split count";
+    case NM_ERR_BAD_EPILOGUE:
+      return "input-norm / residual / head-layout arguments rejected (contiguous 16-byte aligned vec for the "
+             "norm; head_dim a multiple of 64 dividing h and the tile; pos and rope table when used)";
     default: break;
   }
   if (code > 0) return hipGetErrorString(static_cast<hipError_t>(code));

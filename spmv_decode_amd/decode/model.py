@@ -21,6 +21,15 @@ A step is written for few kernel launches, since at batch 1 every small
 kernel costs a few microseconds: the q/k/v projections write into slices of
 one buffer, so the rotary embedding runs once over queries and keys; the
 attention scale and causal mask are folded into one batched multiply-add.
+
+When every projection of every layer is an `NmSparseLinear` (after
+`swap_to_nmsparse`), `forward_step` runs the fused layer instead
+(`fuse_epilogues`, on by default): the input RMSNorm, Qwen3's q/k norms, the
+rotary embedding and the KV-cache write happen inside the grouped q/k/v
+launch, the residual adds inside the o and down launches (in place on the
+residual stream), and the post-attention RMSNorm inside the gate/up launch.
+A layer is then 7 kernels: q/k/v, three attention kernels, o, gate/up, down.
+The per-Linear path above stays for dense models and for comparison.
 """
 from __future__ import annotations
 
@@ -201,6 +210,48 @@ class Block(nn.Module):
         return h + self.mlp(self.post_attention_layernorm(h))
 
 
+def fusable(block: Block) -> bool:
+    """True when the block's projections can run as the fused sparse layer:
+    q/k/v and gate/up each share one launch, o and down are sparse too."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    at, mlp = block.self_attn, block.mlp
+    return (grouped_sparse((at.q_proj, at.k_proj, at.v_proj)) and grouped_sparse((mlp.gate_proj, mlp.up_proj))
+            and isinstance(at.o_proj, NmSparseLinear) and isinstance(mlp.down_proj, NmSparseLinear))
+
+
+def fused_block_step(blk: Block, x2d, k_cache_t, v_cache, pos, mask, rope):
+    """One fused sparse layer on the residual stream x2d [1, dim], updated in
+    place. rope: complex64 [S, head_dim/2] table of the cache's positions."""
+    from ..hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
+
+    at, mlp = blk.self_attn, blk.mlp
+    c = at.cfg
+    g = c.n_heads // c.n_kv_heads
+    qd = c.n_heads * c.head_dim
+    q = torch.empty(1, qd, dtype=x2d.dtype, device=x2d.device)
+    ln1, ln2 = blk.input_layernorm, blk.post_attention_layernorm
+    qp, kp, vp = at.q_proj, at.k_proj, at.v_proj
+    nmsparse_qkv_decode(x2d, (qp.mat_data, qp.mat_index), (kp.mat_data, kp.mat_index), (vp.mat_data, vp.mat_index),
+                        qp.block_width, qp.vec_width, q_out=q, k_cache_t=k_cache_t, v_cache=v_cache, pos=pos,
+                        rope_table=rope, head_dim=c.head_dim, norm=(ln1.weight, ln1.eps),
+                        q_norm=at.q_norm.weight if c.qk_norm else None,
+                        k_norm=at.k_norm.weight if c.qk_norm else None, head_eps=c.norm_eps)
+    scores = torch.baddbmm(mask.expand(c.n_kv_heads, g, -1), q.view(c.n_kv_heads, g, c.head_dim), k_cache_t,
+                           alpha=1.0 / math.sqrt(c.head_dim))
+    probs = torch.softmax(scores, dim=-1)
+    y = torch.bmm(probs, v_cache).view(1, qd)
+    o = at.o_proj
+    nmsparse_gemv_launch(y, [GemvProblem(o.mat_data, o.mat_index, x2d, residual=x2d)], o.block_width, o.vec_width)
+    gp, up = mlp.gate_proj, mlp.up_proj
+    act = nmsparse_gate_up_silu(x2d, (gp.mat_data, gp.mat_index), (up.mat_data, up.mat_index), gp.block_width,
+                                gp.vec_width, norm=(ln2.weight, ln2.eps))
+    d = mlp.down_proj
+    nmsparse_gemv_launch(act, [GemvProblem(d.mat_data, d.mat_index, x2d, residual=x2d)], d.block_width,
+                         d.vec_width)
+    return x2d
+
+
 class Decoder(nn.Module):
     """Decoder stack with a static KV cache; `model.layers` is what
     `swap_to_nmsparse` walks."""
@@ -208,6 +259,7 @@ class Decoder(nn.Module):
     def __init__(self, cfg: DecoderConfig):
         super().__init__()
         self.cfg = cfg
+        self.fuse_epilogues = True
         self.embed_tokens = nn.Embedding(cfg.vocab, cfg.dim)
         self.layers = nn.ModuleList(Block(cfg) for _ in range(cfg.n_layers))
         self.norm = RMSNorm(cfg.dim, cfg.norm_eps)
@@ -231,8 +283,13 @@ class Decoder(nn.Module):
         """One decode step: token [1, 1] int64 and pos [1] int64 on the device
         -> logits [1, vocab]. No host synchronisation."""
         x = self.embed_tokens(token)  # [1, 1, dim]
-        freqs = self.rope.index_select(0, pos)
         mask = torch.where(self.positions <= pos, 0.0, float("-inf")).to(self.mask_dtype)
+        if self.fuse_epilogues and all(fusable(b) for b in self.layers):
+            x2d = x.view(1, -1)
+            for i, blk in enumerate(self.layers):
+                fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache[i], pos, mask, self.rope)
+            return self.lm_head(self.norm(x)).view(1, -1)
+        freqs = self.rope.index_select(0, pos)
         for i, layer in enumerate(self.layers):
             x = layer(x, freqs, self.k_cache_t[i], self.v_cache[i], pos, mask)
         return self.lm_head(self.norm(x)).view(1, -1)

@@ -187,72 +187,206 @@ def _aligned(md):
     return md if md.data_ptr() % 16 == 0 else md.clone()
 
 
-def nmsparse_gemv_grouped(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, config_id=-1, splits=0):
+def _check_vector(t, n, like, what):
+    """t must be a contiguous [n] or [1, n] tensor of like.dtype on like.device."""
+    if t.device != like.device or t.dtype != like.dtype or t.numel() != n or not t.is_contiguous():
+        raise ValueError(f"{what} must be a contiguous tensor of {n} elements of {like.dtype} on {like.device}")
+
+
+class GemvProblem:
+    """One GEMV of a fused launch (struct nm_gemv_problem).
+
+    mat_data [w, h] / mat_index [w/N, N] as for nmsparse_spmv_forward_hip;
+    `out` receives the result ([1, h], or a heads-layout base with `layout`);
+    `residual` ([h]) is added before the rounding and may be `out` itself;
+    `head_norm` ([head_dim]) applies a per-head RMSNorm; `rope` rotates each
+    (even, odd) row pair of a head by the angle at the launch's position;
+    `layout` = (head_stride, elem_stride, pos_stride) in elements writes row r
+    to out[(r // head_dim) * head_stride + (r % head_dim) * elem_stride +
+    pos * pos_stride].
+    """
+
+    __slots__ = ("mat_data", "mat_index", "out", "residual", "head_norm", "rope", "layout")
+
+    def __init__(self, mat_data, mat_index, out=None, *, residual=None, head_norm=None, rope=False, layout=None):
+        self.mat_data, self.mat_index, self.out = mat_data, mat_index, out
+        self.residual, self.head_norm, self.rope, self.layout = residual, head_norm, bool(rope), layout
+
+
+def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, norm=None, head_dim=0,
+                         head_eps=1e-6, pos=None, pos_limit=None, rope_table=None, config_id=-1, splits=0):
+    """One launch of 1-4 GEMVs that share `vec` [1, K] (or the gate/up pair),
+    with the fusions of include/nmsparse_hip.h's nm_gemv_launch.
+
+    `norm` = (weight [K], eps) folds an RMSNorm of vec into the gather.
+    `gate_up=True` takes exactly two problems (gate, up) and writes
+    silu(gate) * up into problems[0].out. Heads fusions need `head_dim`, and
+    `pos` (device int64 [1]) plus `rope_table` (fp32 [S, head_dim/2, 2] or
+    complex64 [S, head_dim/2]) when used; positions outside [0, pos_limit)
+    store nothing (pos_limit defaults to the rope table's length). Returns the
+    list of outputs (the pair: one). Outputs left as None are allocated ([1, h]).
+    """
+    n = len(problems)
+    if gate_up and n != 2:
+        raise ValueError("the gate/up pair takes exactly two problems")
+    if not 1 <= n <= 4:
+        raise ValueError("a fused launch takes 1 to 4 problems")
+    w = problems[0].mat_data.shape[0]
+    K = vec.shape[-1]
+    for pr in problems:
+        validate_args(vec, pr.mat_data, pr.mat_index, w, pr.mat_data.shape[1], BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
+    if gate_up and problems[0].mat_data.shape != problems[1].mat_data.shape:
+        raise ValueError(f"gate {tuple(problems[0].mat_data.shape)} and up {tuple(problems[1].mat_data.shape)} "
+                         "must have the same shape")
+    n_out = 1 if gate_up else n
+    desc = _lib.NmGemvLaunchDesc()
+    desc.dtype = _DTYPE_CODE[vec.dtype]
+    desc.kind = _lib.NM_KIND_GATE_UP if gate_up else _lib.NM_KIND_GROUPED
+    desc.nprob = n
+    desc.vec_stride = vec.stride(1)
+    desc.vec = vec.data_ptr()
+    desc.w, desc.nnz, desc.m = w, BLOCK_WIDTH, VEC_WIDTH
+    desc.config_id, desc.splits = int(config_id), int(splits)
+    keep = []  # tensors whose pointers the descriptor holds
+    if norm is not None:
+        weight, eps = norm
+        _check_vector(weight, K, vec, "norm weight")
+        if vec.data_ptr() % 16 or (K * vec.element_size()) % 16:
+            raise ValueError("an input RMSNorm needs a 16-byte aligned vec with K * element size a multiple of 16")
+        desc.norm_weight, desc.norm_eps = weight.data_ptr(), float(eps)
+    heads = any(pr.head_norm is not None or pr.rope or pr.layout is not None for pr in problems[:n_out])
+    needs_pos = any(pr.rope or (pr.layout is not None and pr.layout[2] != 0) for pr in problems[:n_out])
+    if heads:
+        if gate_up:
+            raise ValueError("the gate/up pair writes a plain [h] output (no heads fusions)")
+        if head_dim <= 0 or head_dim % 64:
+            raise ValueError(f"head_dim must be a positive multiple of 64, got {head_dim}")
+        desc.head_dim, desc.head_norm_eps = int(head_dim), float(head_eps)
+    pos_limit = 0 if pos_limit is None else int(pos_limit)
+    if needs_pos:
+        if pos is None or pos.dtype != torch.int64 or pos.numel() != 1 or pos.device != vec.device:
+            raise ValueError("pos must be a device int64 tensor of one element")
+        desc.pos = pos.data_ptr()
+    if any(pr.rope for pr in problems[:n_out]):
+        if rope_table is None:
+            raise ValueError("rope needs rope_table")
+        rt = torch.view_as_real(rope_table) if rope_table.is_complex() else rope_table
+        if (rt.dtype != torch.float32 or rt.ndim != 3 or rt.shape[1:] != (head_dim // 2, 2) or not rt.is_contiguous()
+                or rt.device != vec.device):
+            raise ValueError(f"rope_table must be contiguous fp32 [S, {head_dim // 2}, 2] (or complex64) on the device")
+        desc.rope_table = rt.data_ptr()
+        if not pos_limit:
+            pos_limit = rt.shape[0]
+        elif pos_limit > rt.shape[0]:
+            raise ValueError(f"pos_limit {pos_limit} exceeds the rope table's {rt.shape[0]} positions")
+        keep.append(rt)
+    if needs_pos and pos_limit <= 0:
+        raise ValueError("a position-dependent launch needs pos_limit (or a rope_table)")
+    outs = []
+    for i, pr in enumerate(problems):
+        h = int(pr.mat_data.shape[1])
+        P = desc.prob[i]
+        md = _aligned(pr.mat_data)
+        keep.append(md)
+        P.mat_data, P.mat_index, P.h = md.data_ptr(), pr.mat_index.data_ptr(), h
+        if i >= n_out:
+            continue
+        if pr.layout is None:
+            out = _prepare_out(pr.out, h, vec)
+        else:
+            out = pr.out
+            hs_, es_, ps_ = (int(v) for v in pr.layout)
+            if out is None or out.dtype != vec.dtype or out.device != vec.device or out.data_ptr() % 16:
+                raise ValueError("a heads-layout output must be a 16-byte aligned tensor of vec.dtype on vec.device")
+            if min(hs_, es_, ps_) < 0:
+                raise ValueError("layout strides must be non-negative")
+            top = (h // head_dim - 1) * hs_ + (head_dim - 1) * es_ + max(pos_limit - 1, 0) * ps_
+            if not out.is_contiguous() or top >= out.numel():
+                raise ValueError(f"heads layout {pr.layout} reaches element {top} of a {out.numel()}-element output")
+            P.head_stride, P.elem_stride, P.pos_stride = hs_, es_, ps_
+        outs.append(out)
+        P.out = out.data_ptr()
+        if pr.residual is not None:
+            _check_vector(pr.residual, h, vec, "residual")
+            P.residual = pr.residual.data_ptr()
+        if pr.head_norm is not None:
+            _check_vector(pr.head_norm, head_dim, vec, "head_norm")
+            P.head_norm = pr.head_norm.data_ptr()
+        P.rope = int(pr.rope)
+    desc.pos_limit = pos_limit
+    lib = _lib.load()
+    need = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(desc))
+    if need == 0:
+        raise ValueError("launch shape outside what libnmsparse_hip supports")
+    device = vec.device
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        ws = workspace_for(device, need, stream)
+        rc = lib.nm_gemv_launch(ctypes.byref(desc), ws.data_ptr(), ws.numel(), stream)
+    _lib.check(rc, "nm_gemv_launch")
+    return outs
+
+
+def nmsparse_gemv_grouped(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, norm=None, residuals=None,
+                          config_id=-1, splits=0):
     """Several N:M GEMVs that read the same `vec` [1, K], in one launch.
 
     `problems` is a sequence of 1-4 (mat_data [w, h_i], mat_index [w/N, N])
     pairs with the same w; returns a list of [1, h_i] outputs (or writes into
     `outs`). Each output equals what nmsparse_spmv_forward_hip computes for that
     problem with the same configuration. Used for the q/k/v projections of a
-    decoder layer (one launch instead of three).
+    decoder layer (one launch instead of three). `norm` = (weight [K], eps)
+    applies an RMSNorm to vec first; `residuals[i]` is added to output i.
     """
     if not 1 <= len(problems) <= 4:
         raise ValueError("nmsparse_gemv_grouped takes 1 to 4 problems")
-    w = problems[0][0].shape[0]
-    K = vec.shape[-1]
-    for md, mi in problems:
-        validate_args(vec, md, mi, w, md.shape[1], BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
-    hs = [int(md.shape[1]) for md, _ in problems]
     outs = [None] * len(problems) if outs is None else list(outs)
-    outs = [_prepare_out(o, h, vec) for o, h in zip(outs, hs)]
-    mats = [_aligned(md) for md, _ in problems]
-    lib = _lib.load()
-    n = len(problems)
-    hs_c = (ctypes.c_int * n)(*hs)
-    need = lib.nm_gemv_grouped_workspace_bytes(n, hs_c, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
-    if need == 0:
-        raise ValueError("grouped shape outside what libnmsparse_hip supports")
-    device = vec.device
-    with torch.cuda.device(device):
-        stream = torch.cuda.current_stream(device).cuda_stream
-        ws = workspace_for(device, need, stream)
-        md_c = (ctypes.c_void_p * n)(*[m.data_ptr() for m in mats])
-        mi_c = (ctypes.c_void_p * n)(*[mi.data_ptr() for _, mi in problems])
-        out_c = (ctypes.c_void_p * n)(*[o.data_ptr() for o in outs])
-        rc = lib.nm_gemv_grouped(_DTYPE_CODE[vec.dtype], vec.data_ptr(), vec.stride(1), n, md_c, mi_c, out_c, hs_c,
-                                 ws.data_ptr(), ws.numel(), w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits),
-                                 stream)
-    _lib.check(rc, "nm_gemv_grouped")
-    return outs
+    residuals = [None] * len(problems) if residuals is None else list(residuals)
+    probs = [GemvProblem(md, mi, o, residual=r) for (md, mi), o, r in zip(problems, outs, residuals)]
+    return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, norm=norm, config_id=config_id, splits=splits)
 
 
-def nmsparse_gate_up_silu(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1, splits=0):
+def nmsparse_gate_up_silu(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, *, out=None, norm=None, residual=None,
+                          config_id=-1, splits=0):
     """silu(W_gate @ vec) * (W_up @ vec) for two N:M-sparse [w, h] weights in one
     launch; `gate` and `up` are (mat_data, mat_index) pairs. fp32 throughout,
-    one rounding to vec.dtype. Returns [1, h]."""
+    one rounding to vec.dtype. Returns [1, h]. `norm` = (weight [K], eps)
+    applies an RMSNorm to vec first; `residual` ([h]) is added last."""
     (gd, gi), (ud, ui) = gate, up
-    if gd.shape != ud.shape:
-        raise ValueError(f"gate {tuple(gd.shape)} and up {tuple(ud.shape)} must have the same shape")
-    w, h = gd.shape
-    K = vec.shape[-1]
-    validate_args(vec, gd, gi, w, h, BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
-    validate_args(vec, ud, ui, w, h, BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
-    out = _prepare_out(out, h, vec)
-    gd, ud = _aligned(gd), _aligned(ud)
-    lib = _lib.load()
-    need = lib.nm_gemv_gate_up_workspace_bytes(h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
-    if need == 0:
-        raise ValueError("gate/up shape outside what libnmsparse_hip supports")
-    device = vec.device
-    with torch.cuda.device(device):
-        stream = torch.cuda.current_stream(device).cuda_stream
-        ws = workspace_for(device, need, stream)
-        rc = lib.nm_gemv_gate_up_silu(_DTYPE_CODE[vec.dtype], vec.data_ptr(), vec.stride(1), gd.data_ptr(),
-                                      gi.data_ptr(), ud.data_ptr(), ui.data_ptr(), out.data_ptr(), ws.data_ptr(),
-                                      ws.numel(), h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits), stream)
-    _lib.check(rc, "nm_gemv_gate_up_silu")
-    return out
+    probs = [GemvProblem(gd, gi, out, residual=residual), GemvProblem(ud, ui)]
+    return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, gate_up=True, norm=norm, config_id=config_id,
+                                splits=splits)[0]
+
+
+def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_t, v_cache, pos, rope_table,
+                        head_dim, norm=None, q_norm=None, k_norm=None, head_eps=1e-6, config_id=-1, splits=0):
+    """The q/k/v projections of one decode step in one launch.
+
+    q, k, v are (mat_data, mat_index) pairs sharing `vec` [1, K]. Writes the
+    rotated queries to `q_out` [1, n_heads * head_dim], the rotated keys into
+    `k_cache_t` [kv_heads, head_dim, S] at column pos and the values into
+    `v_cache` [kv_heads, S, head_dim] at row pos (the decoder's pre-transposed
+    static cache). `norm` = (weight [K], eps) is the layer's input RMSNorm;
+    `q_norm` / `k_norm` ([head_dim]) are Qwen3's per-head norms.
+    """
+    kvh, hd, S = k_cache_t.shape
+    if hd != head_dim or tuple(v_cache.shape) != (kvh, S, hd):
+        raise ValueError(f"k_cache_t {tuple(k_cache_t.shape)} / v_cache {tuple(v_cache.shape)} do not match "
+                         f"head_dim {head_dim}")
+    for name, (md, _), rows in (("k", k, kvh * hd), ("v", v, kvh * hd)):
+        if md.shape[1] != rows:
+            raise ValueError(f"{name} projection has {md.shape[1]} outputs, the cache holds {rows}")
+    rt = torch.view_as_real(rope_table) if rope_table.is_complex() else rope_table
+    if rt.shape[0] < S:
+        raise ValueError(f"rope_table has {rt.shape[0]} positions, the cache {S}")
+    probs = [GemvProblem(q[0], q[1], q_out, head_norm=q_norm, rope=True),
+             GemvProblem(k[0], k[1], k_cache_t, head_norm=k_norm, rope=True, layout=(hd * S, S, 1)),
+             GemvProblem(v[0], v[1], v_cache, layout=(S * hd, 1, hd))]
+    return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, norm=norm, head_dim=head_dim,
+                                head_eps=head_eps, pos=pos, rope_table=rt[:S], config_id=config_id,
+                                splits=splits)
 
 
 __all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
-           "nmsparse_gate_up_silu", "validate_args", "workspace_for"]
+           "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "GemvProblem", "validate_args",
+           "workspace_for"]

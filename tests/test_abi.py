@@ -151,3 +151,78 @@ def test_grouped_and_pair_rejections_before_launch():
     assert ws == _lib.NM_TICKET_BYTES + 2 * 8 * 14336 * 4
     for j in range(lib.nm_num_gate_up_configs()):
         assert _lib.describe(_lib.num_configs() + j).startswith("pair_th")
+
+
+def test_launch_descriptor_layout_matches_header(tmp_path):
+    """ctypes' nm_gemv_problem / nm_gemv_launch_desc agree with the C compiler's
+    layout of the header's structs (offset of every field, and sizes)."""
+    gcc = subprocess.run(["which", "gcc"], capture_output=True, text=True).stdout.strip()
+    if not gcc:
+        pytest.skip("gcc not available")
+    fields = []
+    for sname, cls in (("nm_gemv_problem", _lib.NmGemvProblem), ("nm_gemv_launch_desc", _lib.NmGemvLaunchDesc)):
+        fields += [(sname, f[0], getattr(cls, f[0]).offset) for f in cls._fields_]
+    src = tmp_path / "layout.c"
+    lines = ["#include <stdio.h>", "#include <stddef.h>", '#include "nmsparse_hip.h"', "int main(void) {"]
+    for sname, fname, _ in fields:
+        lines.append(f'  printf("%zu\\n", offsetof({sname}, {fname}));')
+    lines += ['  printf("%zu\\n%zu\\n", sizeof(nm_gemv_problem), sizeof(nm_gemv_launch_desc));', "  return 0;", "}"]
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, f"-I{ROOT / 'include'}", str(src), "-o", str(exe)], check=True)
+    got = [int(v) for v in subprocess.run([str(exe)], capture_output=True, text=True, check=True).stdout.split()]
+    assert got[:-2] == [off for _, _, off in fields]
+    assert got[-2:] == [ctypes.sizeof(_lib.NmGemvProblem), ctypes.sizeof(_lib.NmGemvLaunchDesc)]
+
+
+def _desc(kind=0, nprob=3, hs=(4096, 1024, 1024), **kw):
+    d = _lib.NmGemvLaunchDesc()
+    d.dtype, d.kind, d.nprob, d.vec_stride, d.vec = 0, kind, nprob, 1, FAKE
+    d.w, d.nnz, d.m, d.config_id, d.splits = 2048, 32, 64, -1, 0
+    for i in range(nprob):
+        d.prob[i].mat_data, d.prob[i].mat_index, d.prob[i].out, d.prob[i].h = FAKE, FAKE, FAKE, hs[i]
+    for k, v in kw.items():
+        setattr(d, k, v)
+    return d
+
+
+def _launch(d, ws_bytes=1 << 30):
+    return _lib.load().nm_gemv_launch(ctypes.byref(d), FAKE, ws_bytes, None)
+
+
+def test_launch_descriptor_rejections_before_launch():
+    lib = _lib.load()
+    assert lib.nm_gemv_launch(None, FAKE, 1 << 30, None) == -1
+    assert lib.nm_gemv_launch_workspace_bytes(None) == 0
+    assert _launch(_desc(dtype=3)) == -7
+    assert _launch(_desc(kind=2)) == -7
+    assert _launch(_desc(nprob=0)) == -2
+    assert _launch(_desc(kind=1, nprob=3)) == -2          # the pair takes exactly two matrices
+    assert _launch(_desc(kind=1, nprob=2, hs=(4096, 1024))) == -2
+    assert _launch(_desc(vec=None)) == -1
+    assert _launch(_desc(), ws_bytes=1024) == -6
+    # input RMSNorm: contiguous, aligned vec; non-negative eps
+    assert _launch(_desc(norm_weight=FAKE, vec_stride=2)) == -8
+    assert _launch(_desc(norm_weight=FAKE, vec=FAKE + 2)) == -8
+    assert _launch(_desc(norm_weight=FAKE, norm_eps=-1.0)) == -8
+    # heads fusions: head_dim a multiple of 64 dividing h and the tile; pos and table when used
+    d = _desc()
+    d.prob[0].rope = 1
+    assert _launch(d) == -8                               # no head_dim
+    d.head_dim = 96
+    assert _launch(d) == -8
+    d.head_dim = 128
+    assert _launch(d) == -8                               # no pos / pos_limit
+    d.pos, d.pos_limit = FAKE, 16
+    assert _launch(d) == -8                               # no rope table
+    d.config_id = 9                                       # tile 2048 rows, fine for head_dim 128
+    e = _desc(config_id=-1, head_dim=256)
+    e.prob[1].head_norm = FAKE                            # h = 1024, th16 tile of 128 rows < head_dim
+    assert _launch(e) == -8
+    p = _desc(kind=1, nprob=2, hs=(14336, 14336))
+    p.prob[0].pos_stride, p.head_dim = 1, 128
+    assert _launch(p) == -8                               # the pair has no heads layout
+    assert lib.nm_gemv_launch_workspace_bytes(ctypes.byref(_desc())) == lib.nm_gemv_grouped_workspace_bytes(
+        3, (ctypes.c_int * 3)(4096, 1024, 1024), 2048, 32, 64, -1, 0)
+    assert lib.nm_gemv_launch_workspace_bytes(ctypes.byref(p)) == lib.nm_gemv_gate_up_workspace_bytes(
+        14336, 2048, 32, 64, -1, 0)

@@ -303,28 +303,233 @@ def test_gate_up_silu_pair(gpu, dtype):
                     assert e["max_abs"] <= bound[0] and e["rel_l2"] <= bound[1], (cfg, splits, e)
 
 
-def test_decoder_uses_fused_launches_and_matches_unfused(gpu):
-    """The decoder's grouped q/k/v and gate/up pair give the same logits as the
-    per-Linear path (one rounding less in the MLP, so within fp16 tolerance)."""
+# ---------------------------------------------------------------------------
+# Fusions at the GEMV's edges: input RMSNorm, residual, per-head norm, RoPE,
+# KV-cache layout
+# ---------------------------------------------------------------------------
+def _fp_bound(ref, got, dtype, abs_terms, w):
+    """|got - ref| <= one ulp of the output type + the fp32 accumulation bound
+    + 1e-6 relative (the fp32 normalisation scale)."""
+    if dtype == torch.float32:
+        return np.abs(got - ref) <= 4.0 * np.sqrt(w) * 2.0 ** -24 * abs_terms + 1e-6 * np.abs(ref) + 1e-30
+    exp = np.maximum(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))), MIN_NORMAL_EXP[dtype])
+    ulp = np.exp2(exp - ULP_BITS[dtype])
+    return np.abs(got - ref) <= ulp + 4.0 * np.sqrt(w) * 2.0 ** -24 * abs_terms + 1e-6 * np.abs(ref)
+
+
+def _normed_ref(x, lnw, eps, md, mi, nnz, m):
+    xn = O.rms_norm_f64(x.cpu().reshape(-1), lnw.cpu(), eps)
+    ref = O.gemv_f64(xn, md.cpu(), mi.cpu(), nnz, m)
+    terms = np.abs(O.to_f64(md.cpu())).T @ np.abs(O.gather_activations(xn, mi.cpu(), nnz, m))
+    return ref, terms
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
+@pytest.mark.parametrize("K,hs,nnz,m", [(4096, [4096, 1024, 1024], 32, 64), (1024, [384, 128], 3, 4),
+                                        (5120, [1280], 8, 16)], ids=str)
+def test_input_rmsnorm_and_residual_grouped(gpu, K, hs, nnz, m, dtype):
+    from spmv_decode_amd.hip_spmv import GemvProblem, nmsparse_gemv_launch
+
+    g = torch.Generator(device="cuda").manual_seed(K + sum(hs))
+    x = (torch.randn(1, K, generator=g, device="cuda") * 3).to(dtype)
+    lnw = (torch.rand(K, generator=g, device="cuda") + 0.5).to(dtype)
+    probs = [make_case(K, h, nnz, m, seed=200 + i, dtype=dtype)[1:] for i, h in enumerate(hs)]
+    res = [torch.randn(1, h, generator=g, device="cuda").to(dtype) for h in hs]
+    for cfg, splits in ((-1, 0), (1, 1), (3, 3), (6, 8)):
+        say(f"norm+residual {dtype} K{K} {hs} {nnz}:{m} cfg {cfg} splits {splits}")
+        keep = [r.clone() for r in res]
+        inplace = [r.clone() for r in res]
+        pr = [GemvProblem(md, mi, o, residual=o) for (md, mi), o in zip(probs, inplace)]
+        outs = nmsparse_gemv_launch(x, pr, nnz, m, norm=(lnw, 1e-5), config_id=cfg, splits=splits)
+        assert all(o.data_ptr() == r.data_ptr() for o, r in zip(outs, inplace))
+        for (md, mi), o, r in zip(probs, outs, keep):
+            ref, terms = _normed_ref(x, lnw, 1e-5, md, mi, nnz, m)
+            ref = ref + O.to_f64(r.cpu()).reshape(-1)
+            got = o.float().cpu().numpy().reshape(-1)
+            ok = _fp_bound(ref, got, dtype, terms, md.shape[0])
+            assert ok.all(), (cfg, splits, int((~ok).sum()), float(np.abs(got - ref).max()))
+        # without the residual: the normalised GEMV alone
+        outs = nmsparse_gemv_launch(x, [GemvProblem(md, mi) for md, mi in probs], nnz, m, norm=(lnw, 1e-5),
+                                    config_id=cfg, splits=splits)
+        for (md, mi), o in zip(probs, outs):
+            ref, terms = _normed_ref(x, lnw, 1e-5, md, mi, nnz, m)
+            got = o.float().cpu().numpy().reshape(-1)
+            assert _fp_bound(ref, got, dtype, terms, md.shape[0]).all(), (cfg, splits)
+
+
+def test_input_rmsnorm_rejections(gpu):
+    from spmv_decode_amd.hip_spmv import GemvProblem, nmsparse_gemv_launch
+
+    x, md, mi = make_case(1024, 256, 2, 4, seed=1)
+    lnw = torch.ones(1024, device="cuda", dtype=torch.float16)
+    with pytest.raises(ValueError, match="norm weight"):
+        nmsparse_gemv_launch(x, [GemvProblem(md, mi)], 2, 4, norm=(lnw[:512], 1e-5))
+    with pytest.raises(ValueError, match="norm weight"):
+        nmsparse_gemv_launch(x, [GemvProblem(md, mi)], 2, 4, norm=(lnw.float(), 1e-5))
+    with pytest.raises(ValueError, match="residual"):
+        nmsparse_gemv_launch(x, [GemvProblem(md, mi, residual=torch.zeros(128, device="cuda").half())], 2, 4)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+def test_gate_up_pair_with_input_rmsnorm_and_residual(gpu, dtype):
+    from spmv_decode_amd.hip_spmv import nmsparse_gate_up_silu
+
+    for K, h, nnz, m in ((4096, 14336, 32, 64), (1024, 384, 3, 4)):
+        x, gd, gi = make_case(K, h, nnz, m, seed=h + 5, dtype=dtype)
+        _, ud, ui = make_case(K, h, nnz, m, seed=h + 6, dtype=dtype)
+        lnw = (torch.rand(K, device="cuda") + 0.5).to(dtype)
+        res = torch.randn(1, h, device="cuda").to(dtype)
+        xn = O.rms_norm_f64(x.cpu().reshape(-1), lnw.cpu(), 1e-6)
+        gv = O.gemv_f64(xn, gd.cpu(), gi.cpu(), nnz, m)
+        uv = O.gemv_f64(xn, ud.cpu(), ui.cpu(), nnz, m)
+        for cfg in (-1, 0, 3):
+            for splits in (0, 1, 3):
+                say(f"gate/up norm {dtype} {K}x{h} {nnz}:{m} cfg {cfg} splits {splits}")
+                out = nmsparse_gate_up_silu(x, (gd, gi), (ud, ui), nnz, m, norm=(lnw, 1e-6), residual=res,
+                                            config_id=cfg, splits=splits)
+                ref = O.silu_f64(gv) * uv + O.to_f64(res.cpu()).reshape(-1)
+                got = out.float().cpu().numpy().reshape(-1)
+                e = O.error_metrics(ref, got)
+                bound = (1e-2, 1e-3) if dtype == torch.float16 else (4e-2, 8e-3)
+                assert e["max_abs"] <= bound[0] and e["rel_l2"] <= bound[1], (cfg, splits, e)
+
+
+def _qkv_case(K, nh, kvh, hd, S, nnz, m, dtype, seed):
+    g = torch.Generator(device="cuda").manual_seed(seed)
+    x = (torch.randn(1, K, generator=g, device="cuda") * 2).to(dtype)
+    q = make_case(K, nh * hd, nnz, m, seed=seed + 1, dtype=dtype)[1:]
+    k = make_case(K, kvh * hd, nnz, m, seed=seed + 2, dtype=dtype)[1:]
+    v = make_case(K, kvh * hd, nnz, m, seed=seed + 3, dtype=dtype)[1:]
+    lnw = (torch.rand(K, generator=g, device="cuda") + 0.5).to(dtype)
+    qn = (torch.rand(hd, generator=g, device="cuda") + 0.5).to(dtype)
+    kn = (torch.rand(hd, generator=g, device="cuda") + 0.5).to(dtype)
+    ang = torch.outer(torch.arange(S, dtype=torch.float64), 1.0 / (10000.0 ** (torch.arange(hd // 2) * 2.0 / hd)))
+    rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).cuda()
+    kc = torch.randn(kvh, hd, S, generator=g, device="cuda").to(dtype)
+    vc = torch.randn(kvh, S, hd, generator=g, device="cuda").to(dtype)
+    return x, q, k, v, lnw, qn, kn, ang, rope, kc, vc
+
+
+def _check_heads(got, ref, dtype, what):
+    got = got.float().cpu().numpy().reshape(ref.shape)
+    scale = np.abs(ref).max()
+    exp = np.maximum(np.floor(np.log2(np.maximum(np.abs(ref), 1e-30))), MIN_NORMAL_EXP[dtype])
+    tol = np.exp2(exp - ULP_BITS[dtype]) + 1e-5 * scale
+    bad = np.abs(got - ref) > tol
+    assert not bad.any(), (what, int(bad.sum()), float(np.abs(got - ref).max()))
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+@pytest.mark.parametrize("K,nh,kvh,hd,nnz,m", [(4096, 32, 8, 128, 32, 64), (512, 4, 2, 64, 2, 4),
+                                               (5120, 40, 8, 128, 8, 16)], ids=str)
+def test_qkv_decode_rope_and_cache_write(gpu, K, nh, kvh, hd, nnz, m, dtype, qk_norm):
+    from spmv_decode_amd.hip_spmv import nmsparse_qkv_decode
+
+    S = 48
+    x, q, k, v, lnw, qn, kn, ang, rope, kc, vc = _qkv_case(K, nh, kvh, hd, S, nnz, m, dtype, seed=K + nh)
+    for pos_v, cfg, splits in ((0, -1, 0), (37, -1, 0), (S - 1, 3, 3), (5, 1, 1)):
+        say(f"qkv decode {dtype} K{K} {nh}/{kvh}x{hd} {nnz}:{m} qk_norm {qk_norm} pos {pos_v} cfg {cfg}")
+        kc1, vc1 = kc.clone(), vc.clone()
+        qo = torch.empty(1, nh * hd, device="cuda", dtype=dtype)
+        pos = torch.tensor([pos_v], device="cuda")
+        nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qo, k_cache_t=kc1, v_cache=vc1, pos=pos, rope_table=rope,
+                            head_dim=hd, norm=(lnw, 1e-5), q_norm=qn if qk_norm else None,
+                            k_norm=kn if qk_norm else None, head_eps=1e-6, config_id=cfg, splits=splits)
+        rq, rk, rv = O.qkv_decode_f64(x.cpu().reshape(-1), (q[0].cpu(), q[1].cpu()), (k[0].cpu(), k[1].cpu()),
+                                      (v[0].cpu(), v[1].cpu()), nnz, m, angle_row=ang[pos_v].numpy(), head_dim=hd,
+                                      norm=(lnw.cpu(), 1e-5), q_norm=qn.cpu() if qk_norm else None,
+                                      k_norm=kn.cpu() if qk_norm else None, eps=1e-6)
+        _check_heads(qo, rq, dtype, "q")
+        _check_heads(kc1[:, :, pos_v], rk, dtype, "k")
+        _check_heads(vc1[:, pos_v, :], rv, dtype, "v")
+        # every other cache slot is untouched, bit for bit
+        km = torch.ones(S, dtype=torch.bool)
+        km[pos_v] = False
+        assert torch.equal(kc1[:, :, km.cuda()], kc[:, :, km.cuda()])
+        assert torch.equal(vc1[:, km.cuda(), :], vc[:, km.cuda(), :])
+    # a position outside the cache stores nothing at all
+    kc1, vc1 = kc.clone(), vc.clone()
+    qo = torch.full((1, nh * hd), 7.0, device="cuda", dtype=dtype)
+    nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qo, k_cache_t=kc1, v_cache=vc1, pos=torch.tensor([S], device="cuda"),
+                        rope_table=rope, head_dim=hd, norm=(lnw, 1e-5))
+    torch.cuda.synchronize()
+    assert torch.equal(kc1, kc) and torch.equal(vc1, vc) and bool((qo == 7.0).all())
+
+
+def test_qkv_decode_graph_replays_follow_the_device_position(gpu):
+    """Captured once, replayed at successive positions (the position is a
+    device tensor): every replay writes its own cache slot, as eager calls do."""
+    from spmv_decode_amd.hip_spmv import nmsparse_qkv_decode
+
+    K, nh, kvh, hd, S, nnz, m = 1024, 8, 2, 128, 16, 8, 16
+    x, q, k, v, lnw, qn, kn, ang, rope, kc, vc = _qkv_case(K, nh, kvh, hd, S, nnz, m, torch.float16, seed=9)
+    pos = torch.tensor([0], device="cuda")
+    qo = torch.empty(1, nh * hd, device="cuda", dtype=torch.float16)
+    ke, ve = kc.clone(), vc.clone()
+    kw = dict(rope_table=rope, head_dim=hd, norm=(lnw, 1e-5), q_norm=qn, k_norm=kn)
+    eager_q = []
+    for t in range(6):
+        nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qo, k_cache_t=ke, v_cache=ve,
+                            pos=torch.tensor([t], device="cuda"), **kw)
+        eager_q.append(qo.clone())
+    kg, vg = kc.clone(), vc.clone()
+    nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qo, k_cache_t=kg, v_cache=vg, pos=pos, **kw)  # warm
+    torch.cuda.synchronize()
+    kg.copy_(kc)
+    vg.copy_(vc)
+    graph = torch.cuda.CUDAGraph()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        with torch.cuda.graph(graph, stream=s):
+            nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qo, k_cache_t=kg, v_cache=vg, pos=pos, **kw)
+    torch.cuda.current_stream().wait_stream(s)
+    for t in range(6):
+        pos.fill_(t)
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(qo, eager_q[t]), t
+    assert torch.equal(kg, ke) and torch.equal(vg, ve)
+
+
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_decoder_fused_layer_matches_grouped_and_per_linear_paths(gpu, qk_norm):
+    """Three ways through the same sparse model give the same logits over
+    several steps: the fused layer (norms, RoPE, cache write and residuals
+    inside the GEMV launches), the grouped q/k/v + gate/up launches with
+    PyTorch norms/RoPE, and one launch per Linear (within fp16 tolerance:
+    the fused forms round less often)."""
+    from spmv_decode_amd import swap_to_nmsparse
     from spmv_decode_amd.decode import model as dm
 
-    cfg = dm.tiny_config(qk_norm=True)
+    cfg = dm.tiny_config(qk_norm=qk_norm)
     torch.manual_seed(0)
     mdl = dm.Decoder(cfg).to("cuda", torch.float16)
     dm.init_weights_(mdl, seed=0, std=0.05)
-    from spmv_decode_amd import swap_to_nmsparse
-
-    swap_to_nmsparse(mdl, 8, "cuda", seed=1, init="device", keep_dense=False)
-    mdl.setup_cache(16, "cuda", dtype=torch.float16)
-    tok = torch.tensor([[3]], device="cuda")
-    pos = torch.tensor([0], device="cuda")
     with torch.no_grad():
-        fused = mdl.forward_step(tok, pos).float()
+        for name, prm in mdl.named_parameters():
+            if name.endswith("norm.weight"):
+                prm.uniform_(0.5, 1.5)  # non-trivial norm weights
+    swap_to_nmsparse(mdl, 8, "cuda", seed=1, init="device", keep_dense=False)
+    assert all(dm.fusable(b) for b in mdl.layers)
+    toks = [3, 5, 7, 9, 11]
+
+    def run(fuse, grouped=True):
+        mdl.fuse_epilogues = fuse
         orig = dm.grouped_sparse
-        dm.grouped_sparse = lambda mods: False
+        if not grouped:
+            dm.grouped_sparse = lambda mods: False
         try:
             mdl.setup_cache(16, "cuda", dtype=torch.float16)
-            unfused = mdl.forward_step(tok, pos).float()
+            with torch.no_grad():
+                return [mdl.forward_step(torch.tensor([[t]], device="cuda"), torch.tensor([i], device="cuda")).float()
+                        for i, t in enumerate(toks)]
         finally:
             dm.grouped_sparse = orig
-    torch.testing.assert_close(fused, unfused, rtol=2e-2, atol=2e-2)
+            mdl.fuse_epilogues = True
+
+    fused, grouped, per_linear = run(True), run(False), run(False, grouped=False)
+    for a, b, c in zip(fused, grouped, per_linear):
+        torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
+        torch.testing.assert_close(b, c, rtol=2e-2, atol=2e-2)

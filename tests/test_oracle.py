@@ -247,3 +247,71 @@ def test_error_metrics_hand_values():
     assert abs(e["rmse"] - np.sqrt(0.5)) < 1e-15
     assert abs(e["rel_l2"] - np.sqrt(2.0) / 5.0) < 1e-15
     assert O.error_metrics(np.zeros(3), np.ones(3))["rel_l2"] == pytest.approx(np.sqrt(3) / 1e-12)
+
+
+# ---------------------------------------------------------------------------
+# Decode-layer operations around the GEMV (fused prologue / epilogues)
+# ---------------------------------------------------------------------------
+def test_rms_norm_matches_library_and_closed_form():
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(3, 320, generator=g, dtype=torch.float64)
+    wt = torch.randn(320, generator=g, dtype=torch.float64)
+    ref = torch.nn.functional.rms_norm(x, (320,), wt, 1e-5).numpy()
+    np.testing.assert_allclose(O.rms_norm_f64(x, wt, 1e-5), ref, rtol=1e-13, atol=0)
+    # constant input c: every element becomes c / sqrt(c^2 + eps) * weight
+    c, eps = 3.0, 0.25
+    out = O.rms_norm_f64(np.full(64, c), np.arange(64.0), eps)
+    np.testing.assert_allclose(out, c / np.sqrt(c * c + eps) * np.arange(64.0), rtol=1e-15)
+
+
+def test_rope_matches_complex_multiply_and_invariants():
+    rng = np.random.default_rng(3)
+    v = rng.standard_normal((5, 128))
+    ang = rng.uniform(-7, 7, 64)
+    got = O.rope_f64(v, ang)
+    z = (v[:, 0::2] + 1j * v[:, 1::2]) * np.exp(1j * ang)
+    np.testing.assert_allclose(got[:, 0::2], z.real, rtol=1e-13, atol=1e-13)
+    np.testing.assert_allclose(got[:, 1::2], z.imag, rtol=1e-13, atol=1e-13)
+    np.testing.assert_array_equal(O.rope_f64(v, np.zeros(64)), v)            # position 0: identity
+    pair_norm = np.hypot(v[:, 0::2], v[:, 1::2])
+    np.testing.assert_allclose(np.hypot(got[:, 0::2], got[:, 1::2]), pair_norm, rtol=1e-13)
+    # a quarter turn maps (a, b) to (-b, a); pairs, not halves, are rotated
+    q = O.rope_f64(np.array([1.0, 2.0, 3.0, 4.0]), np.full(2, np.pi / 2))
+    np.testing.assert_allclose(q, [-2.0, 1.0, -4.0, 3.0], atol=1e-15)
+
+
+def test_silu_matches_library():
+    g = torch.linspace(-30, 30, 1001, dtype=torch.float64)
+    np.testing.assert_allclose(O.silu_f64(g.numpy()), torch.nn.functional.silu(g).numpy(), rtol=1e-14, atol=1e-300)
+
+
+def test_qkv_decode_composes_norms_gemv_and_rope():
+    """qkv_decode_f64 against the same steps written out with torch float64
+    library calls (dense masked weights, F.rms_norm, complex rotation)."""
+    K, hd, nnz, m = 256, 64, 2, 4
+    x, qd, qi = _case(K, 2 * hd, nnz, m, seed=11)
+    _, kd, ki = _case(K, hd, nnz, m, seed=12)
+    _, vd, vi = _case(K, hd, nnz, m, seed=13)
+    g = torch.Generator().manual_seed(14)
+    lnw = torch.rand(K, generator=g, dtype=torch.float64) + 0.5
+    qn = torch.rand(hd, generator=g, dtype=torch.float64) + 0.5
+    kn = torch.rand(hd, generator=g, dtype=torch.float64) + 0.5
+    ang = np.linspace(0.1, 3.0, hd // 2)
+    q, k, v = O.qkv_decode_f64(x, (qd, qi), (kd, ki), (vd, vi), nnz, m, angle_row=ang, head_dim=hd,
+                               norm=(lnw, 1e-5), q_norm=qn, k_norm=kn, eps=1e-6)
+    xn = torch.nn.functional.rms_norm(torch.from_numpy(O.to_f64(x)).reshape(1, K), (K,), lnw, 1e-5).reshape(-1)
+
+    def lin(md, mi):
+        dense = O.scatter(torch.from_numpy(O.to_f64(md)), mi, nnz, m, K)
+        return dense @ xn
+
+    def rot(t):
+        z = torch.view_as_complex(t.reshape(*t.shape[:-1], -1, 2).contiguous()) * torch.polar(
+            torch.ones(hd // 2, dtype=torch.float64), torch.from_numpy(ang))
+        return torch.view_as_real(z).flatten(-2)
+
+    rq = rot(torch.nn.functional.rms_norm(lin(qd, qi).reshape(2, hd), (hd,), qn, 1e-6))
+    rk = rot(torch.nn.functional.rms_norm(lin(kd, ki).reshape(1, hd), (hd,), kn, 1e-6))
+    np.testing.assert_allclose(q, rq.numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(k, rk.numpy(), rtol=1e-11, atol=1e-12)
+    np.testing.assert_allclose(v, lin(vd, vi).reshape(1, hd).numpy(), rtol=1e-11, atol=1e-12)
