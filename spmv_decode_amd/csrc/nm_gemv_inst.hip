@@ -1,0 +1,34 @@
+// nm_gemv_inst.hip — instantiates every kernel configuration of one element
+// type (NM_INST_DTYPE = NM_DTYPE_F16 / _BF16 / _F32, set by the build), so the
+// three element types compile in parallel.
+
+#include "nm_gemv_kernel.h"
+
+#ifndef NM_INST_DTYPE
+#error "compile with -DNM_INST_DTYPE=<0|1|2>"
+#endif
+
+namespace nm_hip {
+
+#define NM_ROW_N(TH, U, G, NT, NM) \
+  {&nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, false>, &nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, true>}
+#define NM_ROW(NM, TH, U, NT) \
+  {{NM_ROW_N(TH, U, 1, NT, NM), NM_ROW_N(TH, U, 2, NT, NM), NM_ROW_N(TH, U, 4, NT, NM), NM_ROW_N(TH, U, 8, NT, NM)}},
+#define NM_PLAIN_ROW(TH, U, NT) NM_ROW(1, TH, U, NT)
+#define NM_PAIR_ROW(TH, U, NT) NM_ROW(2, TH, U, NT)
+
+#if NM_INST_DTYPE == NM_DTYPE_F16
+#define NM_PLAIN_TABLE kPlainKernelsF16
+#define NM_PAIR_TABLE kPairKernelsF16
+#elif NM_INST_DTYPE == NM_DTYPE_BF16
+#define NM_PLAIN_TABLE kPlainKernelsBF16
+#define NM_PAIR_TABLE kPairKernelsBF16
+#else
+#define NM_PLAIN_TABLE kPlainKernelsF32
+#define NM_PAIR_TABLE kPairKernelsF32
+#endif
+
+const KernelRow NM_PLAIN_TABLE[kNumConfigs] = {NM_PLAIN_CONFIGS(NM_PLAIN_ROW)};
+const KernelRow NM_PAIR_TABLE[kNumDualConfigs] = {NM_PAIR_CONFIGS(NM_PAIR_ROW)};
+
+}  // namespace nm_hip

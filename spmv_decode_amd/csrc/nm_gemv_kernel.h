@@ -1,0 +1,661 @@
+// nm_gemv_kernel.h — device side of the shared-mask N:M sparse GEMV for
+// MI355X (gfx950, CDNA4): element types, launch arguments and the kernel
+// template. Instantiated per element type by nm_gemv_inst.hip (compiled once
+// per dtype, in parallel); the host side and C ABI are in nm_gemv.hip.
+//
+//
+// out[r] = RNE_T( sum_{c<w} f32(mat_data[c, r]) * f32(vec[(c/nnz)*m + mat_index[c]]) )
+//
+// Semantics follow the reference kernels (triton_spmv.py:56-115 and
+// triton_spmv.py:149-214): the same packed layout, fp32 fused multiply-add
+// accumulation (triton_spmv.py:24-35 is an fma.rn.f32), and an fp32 -> T
+// round-to-nearest-even cast of the result (triton_spmv.py:318). The work
+// decomposition is this file's own:
+//
+//  * A workgroup (256 lanes = 4 wave64) owns an output tile of HT = 8*TH
+//    consecutive rows r and a contiguous range of compressed columns c
+//    (a "split" of w). Lane (tk, th) streams 16 B of every mat_data row it
+//    owns (8 fp16/bf16 outputs; 2 x 16 B for fp32), so one wave reads whole
+//    128 B lines of each row with dwordx4 non-temporal loads.
+//  * The activations a split needs, vec[(c/nnz)*m + mat_index[c]], are
+//    gathered once per workgroup into LDS as fp32. Because the mask is shared
+//    by all rows, every lane reading row c reads the same LDS word (a
+//    broadcast), four rows per ds_read_b128.
+//  * Partial sums of the TK lane-rows are reduced through LDS in a fixed
+//    order. With more than one split, each workgroup writes its fp32 partial
+//    tile to the workspace; the last workgroup to arrive at a tile (an
+//    agent-scope arrival counter) adds the partials in split order, rounds to
+//    T and writes the output, then re-arms the counter. One launch replaces
+//    the reference's zero-fill + atomics + cast kernels and is deterministic.
+//
+// The C ABI at the bottom is declared in include/nmsparse_hip.h.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+#include "../../include/nmsparse_hip.h"
+
+namespace nm_hip {
+
+constexpr int kBlock = 256;        // lanes per workgroup
+constexpr int kVec = 8;            // output rows per lane
+constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
+constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
+constexpr int kAbiVersion = 3;
+
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// ---------------------------------------------------------------------------
+// Element types. Raw rows are kept as 16 B words until the FMA so that the
+// loads of a whole chunk can be in flight at once.
+// ---------------------------------------------------------------------------
+template <int DT>
+struct Elem;
+
+template <>
+struct Elem<NM_DTYPE_F16> {
+  static constexpr int kWords = 1;  // 16 B words per 8 elements
+  typedef uint16_t scalar;
+  __device__ static inline float to_f32(scalar v) {
+    return (float)__builtin_bit_cast(_Float16, v);
+  }
+  __device__ static inline scalar from_f32(float f) {
+    return __builtin_bit_cast(uint16_t, (_Float16)f);
+  }
+  // Whole-vector bitcast: a bitcast of a single vector element read through
+  // an array reference loses the element index in this compiler.
+  __device__ static inline void unpack(const u32x4 (&raw)[1], float (&v)[8]) {
+    const f16x8 p = __builtin_bit_cast(f16x8, raw[0]);
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = (float)p[i];
+  }
+};
+
+template <>
+struct Elem<NM_DTYPE_BF16> {
+  static constexpr int kWords = 1;
+  typedef uint16_t scalar;
+  __device__ static inline float to_f32(scalar v) {
+    return __uint_as_float(((uint32_t)v) << 16);
+  }
+  // Round to nearest, ties to even, on the bit pattern; NaN -> quiet NaN.
+  __device__ static inline scalar from_f32(float f) {
+    uint32_t u = __float_as_uint(f);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (scalar)0x7fc0u;
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (scalar)(u >> 16);
+  }
+  __device__ static inline void unpack(const u32x4 (&raw)[1], float (&v)[8]) {
+    const u32x4 r = raw[0];
+    const uint32_t d[4] = {r.x, r.y, r.z, r.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      v[2 * i] = __uint_as_float(d[i] << 16);
+      v[2 * i + 1] = __uint_as_float(d[i] & 0xffff0000u);
+    }
+  }
+};
+
+template <>
+struct Elem<NM_DTYPE_F32> {
+  static constexpr int kWords = 2;
+  typedef float scalar;
+  __device__ static inline float to_f32(scalar v) { return v; }
+  __device__ static inline scalar from_f32(float f) { return f; }
+  __device__ static inline void unpack(const u32x4 (&raw)[2], float (&v)[8]) {
+    const u32x4 lo = raw[0];
+    const u32x4 hi = raw[1];
+    const uint32_t d[8] = {lo.x, lo.y, lo.z, lo.w, hi.x, hi.y, hi.z, hi.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) v[i] = __uint_as_float(d[i]);
+  }
+};
+
+template <bool NT>
+__device__ inline u32x4 load16(const u32x4* p) {
+  if constexpr (NT) {
+    return __builtin_nontemporal_load(p);
+  } else {
+    return *p;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Kernel
+// ---------------------------------------------------------------------------
+constexpr int kMaxProblems = 4;
+
+// One GEMV of a launch. The problems of one launch share the activation
+// vector and K, nnz, m (hence w); their output widths h may differ.
+struct Problem {
+  const void* mat_data;
+  const uint8_t* mat_index;
+  void* out;
+  float* partial;      // [splits, h] fp32, unused when splits == 1
+  uint32_t* tickets;   // [tiles] arrival counters, zero between launches
+  const void* resid;   // optional [h] residual added before the rounding
+  const void* head_w;  // optional [head_dim] per-head RMSNorm weight
+  // Output element of row r: out + (r / head_dim) * head_stride
+  //   + (r % head_dim) * elem_stride + pos * pos_stride (heads layout), or
+  // out + r when all three are zero.
+  long long head_stride;
+  long long elem_stride;
+  long long pos_stride;
+  int h;
+  int tiles;
+  int block_begin;     // first workgroup of this problem in the grid
+  int rope;            // rotate (even, odd) row pairs of each head by pos
+};
+
+struct Args {
+  const void* vec;
+  long long vec_stride;
+  const void* norm_w;  // optional [K] RMSNorm weight of the input (folded into the gather)
+  const float2* rope;  // [pos_limit, head_dim / 2] (cos, sin) when a problem rotates
+  const long long* pos;  // device position for the heads layout / rotation
+  float norm_eps;
+  float head_eps;
+  int head_dim;
+  int pos_limit;       // positions >= pos_limit (or < 0) store nothing
+  int w;
+  int nnz;
+  int m;
+  int K;
+  int splits;
+  int rows_per_split;  // multiple of the chunk height, <= kMaxRows
+  int nprob;           // NMAT == 1: problems in the grid; NMAT == 2: 2 (gate, up)
+  Problem prob[kMaxProblems];
+};
+
+__device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
+
+// Lane exchange inside each group of 4 lanes (DPP quad_perm): lane i reads
+// lane i ^ 1 (0xB1) or i ^ 2 (0x4E). No LDS round trip.
+template <int CTRL>
+__device__ inline float dpp(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_mov_dpp(__builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+
+// Sum over the 64 lanes of a wavefront (all lanes active), the same value
+// returned to every lane, in a fixed order: quads, then half rows and rows
+// (DPP row_half_mirror 0x141, row_mirror 0x140), then the four rows.
+__device__ inline float wave_sum(float v) {
+  v += dpp<0xB1>(v);
+  v += dpp<0x4E>(v);
+  v += dpp<0x141>(v);
+  v += dpp<0x140>(v);
+  const int b = __builtin_bit_cast(int, v);
+  return (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 0)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 16))) +
+         (__builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 32)) +
+          __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, 48)));
+}
+
+// Sum of squares of the elements in a 16-byte word (invalid words count 0).
+template <int DT>
+__device__ inline float word_ssq(const u32x4 raw, bool ok, float acc) {
+  float f[8];
+  if constexpr (Elem<DT>::kWords == 1) {
+    const u32x4 one[1] = {raw};
+    Elem<DT>::unpack(one, f);
+  } else {
+    const uint32_t d[4] = {raw.x, raw.y, raw.z, raw.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) f[e] = __uint_as_float(d[e]);
+#pragma unroll
+    for (int e = 4; e < 8; ++e) f[e] = 0.0f;
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float fe = ok ? f[e] : 0.0f;
+    acc = __builtin_fmaf(fe, fe, acc);
+  }
+  return acc;
+}
+
+// NMAT == 1: each workgroup computes one tile/split of one problem (a plain
+// GEMV when nprob == 1, several GEMVs sharing x in one grid otherwise).
+// NMAT == 2: each workgroup streams the same tile/split of prob[0] (gate) and
+// prob[1] (up), both of width prob[0].h, and the output prob[0].out receives
+// silu(gate) * up, computed in fp32 and rounded once.
+template <int DT, int TH, int U, int G, bool NT, int NMAT, bool NORM>
+__global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
+  using E = Elem<DT>;
+  typedef typename E::scalar T;
+  constexpr int W = E::kWords;
+  constexpr int TK = kBlock / TH;   // lane-rows per workgroup
+  constexpr int HT = TH * kVec;     // output rows per tile
+  constexpr int CH = TK * U;        // compressed columns per chunk
+  constexpr int XR = G * kBlock;    // compressed columns per split (max)
+  static_assert(kBlock % TH == 0, "TH must divide the block");
+  static_assert(U % 4 == 0, "U must be a multiple of 4 (ds_read_b128)");
+  static_assert(XR % CH == 0, "chunk must divide the split");
+  static_assert(NMAT == 1 || NMAT == 2, "one matrix, or the gate/up pair");
+
+  constexpr int kWaves = kBlock / 64;
+  constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
+  __shared__ __attribute__((aligned(16))) float xs[NMAT][XR];
+  __shared__ __attribute__((aligned(16))) float red[NMAT][TK * HT];
+  __shared__ float wsum[kOutPerLane * kWaves];  // per-wave sums of the head norms
+  __shared__ float nsum[kWaves];                // per-wave sums of the input norm
+  __shared__ int is_last;
+
+  // Problem of this workgroup (uniform; at most kMaxProblems entries).
+  int p = 0;
+  if (NMAT == 1) {
+#pragma unroll
+    for (int q = 1; q < kMaxProblems; ++q)
+      if (q < a.nprob && (int)blockIdx.x >= a.prob[q].block_begin) p = q;
+  }
+  const Problem& P = a.prob[p];
+  const int h = P.h;
+  const int tiles = P.tiles;
+  const int local = (int)blockIdx.x - P.block_begin;
+  // The decode position is read at the start although only the epilogue uses
+  // it, so that its latency is hidden behind the weight stream.
+  const bool need_pos = P.rope != 0 || P.pos_stride != 0;
+  long long pos = 0;
+  if (need_pos) pos = *a.pos;
+
+  const int tid = threadIdx.x;
+  const int th = tid % TH;
+  const int tk = tid / TH;
+  const int tile = local % tiles;
+  const int split = local / tiles;
+  const int c0 = split * a.rows_per_split;
+  const int cw = min(a.rows_per_split, a.w - c0);  // 1 <= cw <= XR by construction
+  const int nch = (cw + CH - 1) / CH;
+  const int col = tile * HT + th * kVec;
+  // Lanes past the last output row read a valid column instead (their sums
+  // are never stored), so no weight load needs a branch.
+  const int col_ld = min(col, h - kVec);
+
+  const T* __restrict__ vx = static_cast<const T*>(a.vec);
+  const T* md_tile[NMAT];
+  const uint8_t* mi[NMAT];
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q) {
+    const Problem& P = a.prob[NMAT == 1 ? p : q];
+    md_tile[q] = static_cast<const T*>(P.mat_data) + (size_t)c0 * (size_t)h + (size_t)col_ld;
+    mi[q] = P.mat_index;
+  }
+
+  // All loads below are unconditional (addresses clamped into range) so that
+  // the compiler keeps them in flight together; out-of-range values are
+  // zeroed with selects after they arrive.
+
+  // 1. In-group positions of this split's compressed columns. mat_index is
+  //    [w/nnz, nnz] contiguous, so column c's position is mi[c].
+  int gidx[NMAT][G];
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int j = 0; j < G; ++j) gidx[q][j] = (int)mi[q][c0 + min(tid + j * kBlock, cw - 1)];
+
+  // 2. The first chunk of weights goes in flight before the activation loads.
+  auto load_chunk = [&](u32x4 (&dst)[NMAT][U][W], int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = min(k * CH + tk * U + u, cw - 1);
+#pragma unroll
+      for (int q = 0; q < NMAT; ++q) {
+        const u32x4* ptr = reinterpret_cast<const u32x4*>(md_tile[q] + (size_t)r * (size_t)h);
+#pragma unroll
+        for (int v = 0; v < W; ++v) dst[q][u][v] = load16<NT>(ptr + v);
+      }
+    }
+  };
+  u32x4 bufA[NMAT][U][W];
+  u32x4 bufB[NMAT][U][W];
+  load_chunk(bufA, 0);
+  // Keep the scheduler from moving the activation gather (which must wait
+  // for the position loads) ahead of the first chunk's weight requests, and
+  // wait for all position loads at once (vmcnt counts in issue order: only
+  // the chunk's NMAT * U * W weight loads may stay outstanding).
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int kChunkLoads = NMAT * U * W;
+  static_assert(kChunkLoads < 64, "vmcnt is a 6-bit counter");
+  __builtin_amdgcn_s_waitcnt((kChunkLoads & 15) | (((kChunkLoads >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+
+  // 3. Gather the activations: vec[(c/nnz)*m + position], fp32 in LDS. Rows
+  //    past the split and positions outside vec read as zero.
+  //    With an input RMSNorm, rmsnorm(x) = s * (x * g) with the scalar
+  //    s = 1 / sqrt(mean(x^2) + eps): the gather reads x * g and s scales the
+  //    finished sums. Every load here is unconditional (vec stands in for the
+  //    norm weights, and mat_data for vec's words, when there is no norm; the
+  //    values are then ignored): a load inside a branch makes the compiler
+  //    wait at the branch's end for every load in flight, weights included.
+  const T* __restrict__ gx = static_cast<const T*>(a.norm_w);
+  T graw[NMAT][G];
+  T wraw[NMAT][G];
+  bool gok[NMAT][G];
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const int t = tid + j * kBlock;
+      const int c = c0 + min(t, cw - 1);
+      const int pos = (c / a.nnz) * a.m + gidx[q][j];
+      gok[q][j] = (t < cw) && (pos < a.K);
+      graw[q][j] = vx[(long long)(gok[q][j] ? pos : 0) * a.vec_stride];
+      if constexpr (NORM) wraw[q][j] = gx[gok[q][j] ? pos : 0];
+    }
+  // The words of vec for mean(x^2) (contiguous, 16-byte aligned, K * size a
+  // multiple of 16 with a norm; the host checks) are requested now and
+  // summed after the main loop, so they never delay the weight stream.
+  constexpr int kSsqWords = NORM ? 3 : 1;  // per lane: K * sizeof(T) <= 12 KiB in flight
+  const u32x4* __restrict__ xw = static_cast<const u32x4*>(a.vec);
+  const int nw = (int)(((long long)a.K * (long long)sizeof(T)) / 16);
+  u32x4 sraw[kSsqWords];
+  if constexpr (NORM) {
+#pragma unroll
+    for (int i = 0; i < kSsqWords; ++i) sraw[i] = xw[min(i * kBlock + tid, nw - 1)];
+  }
+  __builtin_amdgcn_sched_barrier(0);  // every gather request before the first use of one
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int j = 0; j < G; ++j) {
+      const float xv = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
+      if constexpr (NORM) {
+        xs[q][tid + j * kBlock] = xv * E::to_f32(wraw[q][j]);
+      } else {
+        xs[q][tid + j * kBlock] = xv;
+      }
+    }
+  __syncthreads();
+
+  float acc[NMAT][kVec];
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[q][e] = 0.0f;
+
+  // FMA one chunk; rows past the split contribute exactly nothing.
+  auto fma_chunk = [&](const u32x4 (&src)[NMAT][U][W], int k) {
+    const int r0 = k * CH + tk * U;
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q) {
+#pragma unroll
+      for (int u4 = 0; u4 < U / 4; ++u4) {
+        const float4 xv = *reinterpret_cast<const float4*>(&xs[q][r0 + 4 * u4]);
+        const float xq[4] = {xv.x, xv.y, xv.z, xv.w};
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const bool ok = (r0 + 4 * u4 + s) < cw;
+          u32x4 rw[W];
+#pragma unroll
+          for (int v = 0; v < W; ++v) rw[v] = ok ? src[q][4 * u4 + s][v] : u32x4{0u, 0u, 0u, 0u};
+          float wv[kVec];
+          E::unpack(rw, wv);
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) acc[q][e] = __builtin_fmaf(wv[e], xq[s], acc[q][e]);
+        }
+      }
+    }
+  };
+
+  // 4. Stream the split two chunks at a time: chunk k+1 is in flight while
+  //    chunk k is consumed. Loads inside the loop are unconditional.
+  int k = 0;
+  for (; k + 2 < nch; k += 2) {
+    load_chunk(bufB, k + 1);
+    fma_chunk(bufA, k);
+    load_chunk(bufA, k + 2);
+    fma_chunk(bufB, k + 1);
+  }
+  if (k + 1 < nch) {
+    load_chunk(bufB, k + 1);
+    fma_chunk(bufA, k);
+    fma_chunk(bufB, k + 1);
+  } else {
+    fma_chunk(bufA, k);
+  }
+
+  // 5. Reduce the TK lane-rows of the tile through LDS (fixed order), and
+  //    the input norm's sum of squares (fixed order too).
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q) {
+    float4* rp = reinterpret_cast<float4*>(&red[q][tk * HT + th * kVec]);
+    rp[0] = make_float4(acc[q][0], acc[q][1], acc[q][2], acc[q][3]);
+    rp[1] = make_float4(acc[q][4], acc[q][5], acc[q][6], acc[q][7]);
+  }
+  if constexpr (NORM) {
+    float ssq = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kSsqWords; ++i) ssq = word_ssq<DT>(sraw[i], i * kBlock + tid < nw, ssq);
+    for (int base = kSsqWords * kBlock; base < nw; base += kBlock)  // K * sizeof(T) > 12 KiB only
+      ssq = word_ssq<DT>(xw[min(base + tid, nw - 1)], base + tid < nw, ssq);
+    ssq = wave_sum(ssq);
+    if ((tid & 63) == 0) nsum[tid >> 6] = ssq;
+  }
+  __syncthreads();
+  float s_in = 1.0f;
+  if constexpr (NORM) {
+    float t = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kWaves; ++i) t += nsum[i];
+    s_in = rsqrtf(t / (float)a.K + a.norm_eps);
+  }
+
+  float tsum[NMAT][kOutPerLane];
+#pragma unroll
+  for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+    for (int j = 0; j < kOutPerLane; ++j) {
+      const int o = tid + j * kBlock;
+      float s = 0.0f;
+      if (o < HT) {
+#pragma unroll
+        for (int t = 0; t < TK; ++t) s += red[q][t * HT + o];
+      }
+      tsum[q][j] = s;
+    }
+
+  uint32_t* tickets = P.tickets;
+  if (a.splits > 1) {
+    // 6. Split-K: publish the partial tile, count arrivals, last one reduces.
+    //    The handoff uses agent-scope atomics only, never an agent-scope
+    //    fence: on gfx950 such a fence writes back and invalidates the whole
+    //    L2 of the workgroup's XCD (buffer_wbl2 / buffer_inv), which costs
+    //    more than the GEMV itself. Each partial is published with a
+    //    returning atomic swap: its result comes back only after the swap has
+    //    been performed at the device coherence point, and each lane waits
+    //    for all of its results (vmcnt(0)) before the barrier. Lane 0 then
+    //    counts the arrival; the last arrival reads every partial with
+    //    agent-scope atomic loads (sc1, coherent across XCDs) in split order,
+    //    so the sum is deterministic.
+    float sink = 0.0f;
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q) {
+      float* part = a.prob[NMAT == 1 ? p : q].partial + (size_t)split * (size_t)h;
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int r = tile * HT + o;
+        if (o < HT && r < h)
+          sink += __hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    // Consume the swap results (a.splits is never negative) so the compiler
+    // keeps the returning form of the instruction.
+    if (a.splits < 0) static_cast<T*>(P.out)[tid] = E::from_f32(sink);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&tickets[tile], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      is_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!is_last) return;
+  }
+
+  // 7. Epilogue of the workgroup that owns the finished tile. Its operands
+  //    (residual, head-norm weights, position, rotation) are loaded first so
+  //    that they are in flight together with the partial sums.
+  const int hd = a.head_dim;
+  const bool heads = NMAT == 1 && (P.head_w != nullptr || P.rope != 0);
+  const bool head_layout = (P.head_stride | P.elem_stride | P.pos_stride) != 0;
+  const bool pos_ok = !need_pos || (pos >= 0 && pos < (long long)a.pos_limit);
+  const long long pos_c = pos_ok ? pos : 0;
+  const T* __restrict__ resid = static_cast<const T*>(P.resid);
+  const T* __restrict__ head_w = static_cast<const T*>(P.head_w);
+  float rv[kOutPerLane], hw[kOutPerLane];
+  float2 cs[kOutPerLane];
+#pragma unroll
+  for (int j = 0; j < kOutPerLane; ++j) {
+    const int o = tid + j * kBlock;
+    const int r = min(tile * HT + min(o, HT - 1), h - 1);  // clamped: loads stay in range
+    rv[j] = resid ? E::to_f32(resid[r]) : 0.0f;
+    hw[j] = 1.0f;
+    cs[j] = make_float2(1.0f, 0.0f);
+    if (heads) {
+      if (head_w) hw[j] = E::to_f32(head_w[r % hd]);
+      if (P.rope) cs[j] = a.rope[pos_c * (long long)(hd / 2) + (r % hd) / 2];
+    }
+  }
+  if (a.splits > 1) {
+#pragma unroll
+    for (int j = 0; j < kOutPerLane; ++j) {
+      const int o = tid + j * kBlock;
+      const int r = tile * HT + o;
+      if (o < HT && r < h) {
+#pragma unroll
+        for (int q = 0; q < NMAT; ++q) {
+          float* pp = a.prob[NMAT == 1 ? p : q].partial + r;
+          float s = 0.0f;
+          int sp = 0;
+          for (; sp + 8 <= a.splits; sp += 8) {
+            float t8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
+                                        __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += t8[i];
+          }
+          for (; sp < a.splits; ++sp)
+            s += __hip_atomic_load(pp + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          tsum[q][j] = s;
+        }
+      }
+    }
+  }
+
+  float val[kOutPerLane];
+#pragma unroll
+  for (int j = 0; j < kOutPerLane; ++j) {
+    const int o = tid + j * kBlock;
+    const bool valid = o < HT && tile * HT + o < h;
+    float v;
+    if constexpr (NMAT == 1) {
+      v = tsum[0][j] * s_in;
+    } else {
+      v = silu(tsum[0][j] * s_in) * (tsum[1][j] * s_in);
+    }
+    val[j] = valid ? v : 0.0f;
+  }
+
+  if (heads) {
+    // Per-head RMSNorm over head_dim consecutive rows (head_dim is a multiple
+    // of 64 dividing the tile, so a head is whole waves of this workgroup),
+    // then the rotation of each (even, odd) row pair by the angle at pos.
+    if (head_w) {
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const float sq = wave_sum(val[j] * val[j]);
+        if ((tid & 63) == 0) wsum[(j * kBlock + tid) >> 6] = sq;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int f0 = ((o / hd) * hd) >> 6;
+        float t = 0.0f;
+        if (o < HT)
+          for (int f = f0; f < f0 + (hd >> 6); ++f) t += wsum[f];
+        val[j] *= rsqrtf(t / (float)hd + a.head_eps) * hw[j];
+      }
+    }
+    if (P.rope) {
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const float partner = dpp<0xB1>(val[j]);  // row r ^ 1 is lane tid ^ 1
+        val[j] = (tid & 1) == 0 ? val[j] * cs[j].x - partner * cs[j].y : val[j] * cs[j].x + partner * cs[j].y;
+      }
+    }
+  }
+
+  T* __restrict__ out = static_cast<T*>(P.out);
+#pragma unroll
+  for (int j = 0; j < kOutPerLane; ++j) {
+    const int o = tid + j * kBlock;
+    const int r = tile * HT + o;
+    if (o < HT && r < h && pos_ok) {
+      long long off = r;
+      if (head_layout)
+        off = (long long)(r / hd) * P.head_stride + (long long)(r % hd) * P.elem_stride + pos * P.pos_stride;
+      out[off] = E::from_f32(val[j] + rv[j]);
+    }
+  }
+  if (a.splits > 1 && tid == 0) {
+    __hip_atomic_store(&tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+
+
+// ---------------------------------------------------------------------------
+// Kernel configurations (ids are stable; the host side keeps the metadata).
+// X(TH, U, NT): lanes along the output rows (tile = 8 * TH rows), rows per lane
+// per chunk, non-temporal weight loads.
+// ---------------------------------------------------------------------------
+#define NM_PLAIN_CONFIGS(X)                                                       \
+  X(16, 4, true)   /* 0: tile 128,  chunk 64 */                                   \
+  X(16, 8, true)   /* 1: tile 128,  chunk 128 */                                  \
+  X(32, 4, true)   /* 2: tile 256,  chunk 32 */                                   \
+  X(32, 8, true)   /* 3: tile 256,  chunk 64 */                                   \
+  X(32, 16, true)  /* 4: tile 256,  chunk 128 */                                  \
+  X(64, 4, true)   /* 5: tile 512,  chunk 16 */                                   \
+  X(64, 8, true)   /* 6: tile 512,  chunk 32 */                                   \
+  X(64, 16, true)  /* 7: tile 512,  chunk 64 */                                   \
+  X(128, 8, true)  /* 8: tile 1024, chunk 16 */                                   \
+  X(256, 8, true)  /* 9: tile 2048, chunk 8 */                                    \
+  X(16, 8, false)  /* 10: as 1, cached loads */                                   \
+  X(32, 8, false)  /* 11: as 3, cached loads */                                   \
+  X(64, 8, false)  /* 12: as 6, cached loads */
+
+// Gate/up pair configurations (each lane streams both matrices).
+#define NM_PAIR_CONFIGS(X)                                                        \
+  X(16, 4, true)   /* 0: tile 128, chunk 64 */                                    \
+  X(32, 4, true)   /* 1: tile 256, chunk 32 */                                    \
+  X(16, 8, true)   /* 2: tile 128, chunk 128 */                                   \
+  X(32, 8, true)   /* 3: tile 256, chunk 64 */
+
+#define NM_COUNT_CONFIG(TH, U, NT) +1
+constexpr int kNumConfigs = 0 NM_PLAIN_CONFIGS(NM_COUNT_CONFIG);
+constexpr int kNumDualConfigs = 0 NM_PAIR_CONFIGS(NM_COUNT_CONFIG);
+#undef NM_COUNT_CONFIG
+
+typedef void (*KernelFn)(Args);
+
+// The kernels of one configuration and element type:
+// fn[gather slot: 256, 512, 1024, 2048 columns per split][input norm].
+struct KernelRow {
+  KernelFn fn[4][2];
+};
+
+// Defined in nm_gemv_inst.hip, one object per element type.
+extern const KernelRow kPlainKernelsF16[kNumConfigs];
+extern const KernelRow kPlainKernelsBF16[kNumConfigs];
+extern const KernelRow kPlainKernelsF32[kNumConfigs];
+extern const KernelRow kPairKernelsF16[kNumDualConfigs];
+extern const KernelRow kPairKernelsBF16[kNumDualConfigs];
+extern const KernelRow kPairKernelsF32[kNumDualConfigs];
+
+}  // namespace nm_hip

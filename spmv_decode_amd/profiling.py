@@ -112,7 +112,7 @@ def stats(stats_csv, bench_json, md_path, cmd):
              "per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair)>.", "",
              "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
-        n = r["Name"].replace("void (anonymous namespace)::", "").replace("((anonymous namespace)::Args)", "")
+        n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
         n = n if len(n) <= 90 else n[:87] + "..."
         lines.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {float(r['MinNs']) / 1e3:.2f} | "
                      f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |")
