@@ -21,7 +21,13 @@ stream — same distribution and shapes, much faster for 8B+ models, NOT
 bit-exact with the reference; the default is the bit-exact CPU stream.
 
 Beyond the reference: `NmSparseLinear.from_dense` / `pack_dense` build the
-packed buffers from a real dense weight and a shared N:M mask (a pure gather).
+packed buffers from a real dense weight and a shared N:M mask (a pure gather);
+`index_from_pruned` / `NmSparseLinear.from_pruned` recover the shared mask of
+an already N:M-pruned dense weight, and `swap_to_nmsparse(...,
+from_weights=True)` swaps a pruned checkpoint's own weights instead of
+synthetic ones. `NmSparseLinear.empty` builds a module with uninitialised
+buffers for `load_state_dict` (the packed buffers are ordinary state_dict
+entries, `mat_data` and `mat_index`).
 """
 from __future__ import annotations
 
@@ -93,6 +99,32 @@ def pack_dense(weight: torch.Tensor, mat_index: torch.Tensor, M: int) -> torch.T
     return weight[:, pos.to(weight.device)].t().contiguous()
 
 
+def index_from_pruned(weight: torch.Tensor, M: int, nnz: int | None = None) -> torch.Tensor:
+    """Shared N:M pattern [K/M, nnz] (sorted uint8 positions) of a dense [N, K]
+    weight pruned with one mask for all N output rows.
+
+    A position is kept when any row is non-zero there. A group with fewer than
+    nnz such positions (kept weights that happen to be zero in every row) is
+    completed with its lowest all-zero positions, which pack to zeros, so the
+    packed weight still reproduces `weight` exactly. A group with more than
+    nnz non-zero positions is not N:M with a shared mask: ValueError.
+    """
+    N, K = weight.shape
+    nnz = M // 2 if nnz is None else nnz
+    if K % M or not 0 < nnz <= M:
+        raise ValueError(f"need K % M == 0 and 0 < nnz <= M; got K={K}, M={M}, nnz={nnz}")
+    used = (weight != 0).any(dim=0).view(K // M, M)
+    count = used.sum(dim=1)
+    if bool((count > nnz).any()):
+        g = int(torch.nonzero(count > nnz)[0, 0])
+        raise ValueError(f"group {g} has {int(count[g])} non-zero positions, more than nnz={nnz}: the weight is "
+                         f"not {nnz}:{M} sparse with a shared mask")
+    # kept positions first (in ascending order), then the lowest unused ones
+    key = (~used).to(torch.int64) * M + torch.arange(M, device=weight.device)
+    pos = key.argsort(dim=1)[:, :nnz].sort(dim=1).values
+    return pos.to(torch.uint8).contiguous()
+
+
 class NmSparseLinear(nn.Module):
     """Linear layer whose decode path is the N:M sparse GEMV.
 
@@ -135,6 +167,28 @@ class NmSparseLinear(nn.Module):
         self.register_buffer("mat_data", pack_dense(weight, mi, M).to(torch.float16))
         self.register_buffer("mat_index", mi)
         self.h, self.w, self.block_width, self.vec_width = N, (K // M) * (M // 2), M // 2, M
+        return self
+
+    @classmethod
+    def from_pruned(cls, weight: torch.Tensor, M: int, keep_dense: bool = False):
+        """Build from a dense [N, K] weight already pruned to 50% N:M with one
+        mask shared by all rows (the mask is recovered by index_from_pruned)."""
+        return cls.from_dense(weight, index_from_pruned(weight, M), M, keep_dense=keep_dense)
+
+    @classmethod
+    def empty(cls, N: int, K: int, M: int, device, dtype=torch.float16):
+        """Module with uninitialised packed buffers of the right shapes, to be
+        filled by load_state_dict (e.g. from a saved compressed checkpoint)."""
+        if K % M or N % 128:
+            raise ValueError(f"need K % M == 0 and N % 128 == 0; got N={N}, K={K}, M={M}")
+        self = cls.__new__(cls)
+        nn.Module.__init__(self)
+        self._weight_cpu = None
+        self.weight = None
+        nnz, banks = M // 2, K // M
+        self.register_buffer("mat_data", torch.empty(banks * nnz, N, dtype=dtype, device=device))
+        self.register_buffer("mat_index", torch.zeros(banks, nnz, dtype=torch.uint8, device=device))
+        self.h, self.w, self.block_width, self.vec_width = N, banks * nnz, nnz, M
         return self
 
     def _prefill_weight(self, device):
@@ -181,30 +235,38 @@ def _resolve_layout(blk, layouts, kind):
     )
 
 
-def _swap_linears(submodule, names, M, device, seed, cnt, init=None, keep_dense=None):
+def _swap_linears(submodule, names, M, device, seed, cnt, init=None, keep_dense=None, from_weights=False):
     """Replace submodule.<name> for each name, numbering seeds from seed + cnt."""
     keep = (not DECODE_ONLY) if keep_dense is None else keep_dense
     for name in names:
         old = getattr(submodule, name)
         N, K = old.weight.shape
-        dense = old.weight if keep else None
-        del old
-        setattr(submodule, name, None)
-        torch.cuda.empty_cache()
-        setattr(submodule, name, NmSparseLinear(N, K, M, seed + cnt, device, dense_weight=dense, init=init))
+        if from_weights:
+            w = old.weight.detach().to(device)
+            new = NmSparseLinear.from_pruned(w, M, keep_dense=keep)
+        else:
+            dense = old.weight if keep else None
+            del old
+            setattr(submodule, name, None)
+            torch.cuda.empty_cache()
+            new = NmSparseLinear(N, K, M, seed + cnt, device, dense_weight=dense, init=init)
+        setattr(submodule, name, new)
         cnt += 1
     return cnt
 
 
-def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None, keep_dense=None):
+def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None, keep_dense=None,
+                     from_weights=False):
     """Swap every attention and MLP Linear of `model.layers` to NmSparseLinear.
 
     Blocks are visited in order, attention before MLP, Linears in layout
     order; the j-th swapped Linear uses seed `seed + j`. `block_devices`
     optionally gives one device (index or "cuda:N") per block. Returns the
     number of swapped Linears. Keyword-only extras of this build: `init`
-    ("reference" | "device", default from NM_SYNTH_INIT) and `keep_dense`
-    (default: not NM_DECODE_ONLY).
+    ("reference" | "device", default from NM_SYNTH_INIT), `keep_dense`
+    (default: not NM_DECODE_ONLY) and `from_weights` (pack each Linear's own
+    weight, which must already be 50% M-group pruned with a shared mask,
+    instead of drawing synthetic weights; seeds are then unused).
     """
     cnt = 0
     for i, blk in enumerate(model.layers):
@@ -213,10 +275,10 @@ def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None,
             d = block_devices[i]
             blk_device = d if isinstance(d, str) else f"cuda:{d}"
         attn, attn_names = _resolve_layout(blk, _ATTENTION_LAYOUTS, "attention")
-        cnt = _swap_linears(attn, attn_names, M, blk_device, seed, cnt, init, keep_dense)
+        cnt = _swap_linears(attn, attn_names, M, blk_device, seed, cnt, init, keep_dense, from_weights)
         mlp, mlp_names = _resolve_layout(blk, _MLP_LAYOUTS, "feed-forward")
-        cnt = _swap_linears(mlp, mlp_names, M, blk_device, seed, cnt, init, keep_dense)
+        cnt = _swap_linears(mlp, mlp_names, M, blk_device, seed, cnt, init, keep_dense, from_weights)
     return cnt
 
 
-__all__ = ["NmSparseLinear", "swap_to_nmsparse", "pack_dense", "_make_sparse"]
+__all__ = ["NmSparseLinear", "swap_to_nmsparse", "pack_dense", "index_from_pruned", "_make_sparse"]

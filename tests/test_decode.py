@@ -163,3 +163,30 @@ def test_graph_replay_matches_eager_and_masked_dense(gpu):
             assert torch.equal(a, b), rep
     with pytest.raises(RuntimeError, match="static cache"):
         gd.generate(64)
+
+
+@pytest.mark.gpu
+def test_restored_compressed_checkpoint_decodes_identically(gpu):
+    """A swapped model saved with torch.save and restored into a fresh
+    skeleton (weights_only load) produces bit-identical logits."""
+    import io
+
+    cfg = tiny_config(qk_norm=True)
+    torch.manual_seed(0)
+    a = Decoder(cfg).to("cuda", torch.float16)
+    init_weights_(a, seed=4, std=0.05)
+    swap_to_nmsparse(a, 16, "cuda", seed=5, init="device", keep_dense=False)
+    buf = io.BytesIO()
+    torch.save(a.state_dict(), buf)
+    buf.seek(0)
+    b = Decoder(cfg).to("cuda", torch.float16)
+    swap_to_nmsparse(b, 16, "cuda", seed=77, init="device", keep_dense=False)
+    b.load_state_dict(torch.load(buf, weights_only=True))
+    outs = []
+    for mdl in (a, b):
+        mdl.setup_cache(8, "cuda", dtype=torch.float16)
+        with torch.no_grad():
+            outs.append([mdl.forward_step(torch.tensor([[t]], device="cuda"), torch.tensor([i], device="cuda"))
+                         for i, t in enumerate((1, 2, 3))])
+    for x, y in zip(*outs):
+        assert torch.equal(x, y)
