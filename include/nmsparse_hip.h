@@ -226,6 +226,27 @@ size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);
 int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream);
 
 /*
+ * Small-batch SpMM: out[b, :] = W x[b, :] for 1 <= batch <= NM_MAX_BATCH
+ * activation rows that share one pass over the packed weights (multi-token
+ * decode, batched serving, short prefills). x rows are x_row_stride elements
+ * apart with unit column stride; out rows out_row_stride elements apart.
+ * config_id: 0..3 (th16_u4, th16_u8, th32_u4, th32_u8) or < 0 for the
+ * library's choice. With the same config_id and splits as nm_gemv_ex, and at
+ * most 1024 compressed columns per split (nm_spmm_plan reports the plan),
+ * every output row is bit-identical to nm_gemv_ex of that row. No reference
+ * counterpart: the reference op rejects rows != 1 (src/spmv/nmsparse_op.py:83-86,
+ * triton_spmv.py:257-258) and its module runs such inputs through a dense
+ * F.linear (src/spmv/nmsparse_linear.py:62-68).
+ */
+#define NM_MAX_BATCH 8
+size_t nm_spmm_workspace_bytes(int batch, int h, int w, int nnz, int m, int config_id, int splits);
+int nm_spmm(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
+            const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace,
+            size_t workspace_bytes, int h, int w, int nnz, int m, int config_id, int splits, void* stream);
+int nm_spmm_plan(int batch, int h, int w, int nnz, int m, int config_id, int splits, int* out_config_id,
+                 int* out_splits, int* out_blocks, int* out_rows_per_block);
+
+/*
  * Configuration introspection. nm_config_describe writes a short text such as
  * "th32_u8" into buf (ids nm_num_configs() + j describe pair configuration j);
  * nm_gemv_plan reports the configuration and split count the library would

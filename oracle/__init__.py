@@ -12,6 +12,14 @@ Contents and what pins each function (tests/test_oracle.py):
   Pinned by closed forms: one-hot activations reproduce a packed row exactly,
   a one-hot at a pruned position gives zero, linearity under powers of two,
   group-permutation invariance, and brute force over every 2:4 pattern.
+* `nm_oracle.spmm_f64`: the batch > 1 extension, row by row. Pinned against
+  a float64 dense matmul on the scattered weight and against gemv_f64 row by
+  row.
+* `nm_oracle.rms_norm_f64`, `rope_f64`, `silu_f64`, `qkv_decode_f64`: the
+  decode-layer operations fused around the GEMV (model.py:258-270, 310-322,
+  255-256, 182-187). Pinned against torch's float64 library routines
+  (F.rms_norm, complex multiplication, F.silu) and closed forms (constant
+  input, identity at angle 0, pair norms preserved, quarter turn).
 * `nm_oracle.scatter` / `pack`: compressed <-> dense masked weight
   (microbench_triton_torchmv.py:145-164). Pinned by the round trips
   pack(scatter(x)) == x and scatter(pack(W*mask)) == W*mask, bit-exact.

@@ -72,6 +72,19 @@ def gemv_f64(x, mat_data, mat_index, nnz: int, m: int) -> np.ndarray:
     return md.T @ gather_activations(x, mat_index, nnz, m)
 
 
+def spmm_f64(x, mat_data, mat_index, nnz: int, m: int) -> np.ndarray:
+    """Rows of x [B, K] each through gemv_f64: [B, h] in float64 (the batch > 1
+    extension; the reference op itself rejects rows != 1,
+    src/spmv/nmsparse_op.py:83-86)."""
+    xv = to_f64(x).reshape(-1, to_f64(x).shape[-1])
+    md = to_f64(mat_data)
+    pos = gather_positions(mat_index, nnz, m)
+    g = np.zeros((xv.shape[0], pos.size), dtype=np.float64)
+    ok = pos < xv.shape[1]
+    g[:, ok] = xv[:, pos[ok]]
+    return g @ md
+
+
 def gemv_fp32_dense(x, mat_data, mat_index, nnz: int, m: int) -> torch.Tensor:
     """The reference microbenchmark's own oracle: fp32 dense matvec on the
     scattered masked weight, `torch.mv(weight_sparse.float(), vec.float())`

@@ -26,6 +26,7 @@ NM_ERR = {
     -8: "NM_ERR_BAD_EPILOGUE",
 }
 NM_KIND_GROUPED, NM_KIND_GATE_UP = 0, 1
+NM_MAX_BATCH = 8
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -70,12 +71,15 @@ ABI = {
     "nm_num_gate_up_configs": (_i, []),
     "nm_gemv_launch_workspace_bytes": (_sz, [_descp]),
     "nm_gemv_launch": (_i, [_descp, _vp, _sz, _vp]),
+    "nm_spmm_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
+    "nm_spmm": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
+    "nm_spmm_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_config_describe": (_i, [_i, ctypes.c_char_p, _i]),
     "nm_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
 }
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _lib = None
 _lock = threading.Lock()
@@ -128,6 +132,16 @@ def plan(h: int, w: int, nnz: int, m: int, config_id: int = -1, splits: int = 0)
     rc = load().nm_gemv_plan(h, w, nnz, m, config_id, splits, ctypes.byref(cfg), ctypes.byref(sp),
                              ctypes.byref(blocks), ctypes.byref(rows))
     check(rc, "nm_gemv_plan")
+    return {"config_id": cfg.value, "splits": sp.value, "blocks": blocks.value, "rows_per_split": rows.value,
+            "config": describe(cfg.value)}
+
+
+def spmm_plan(batch: int, h: int, w: int, nnz: int, m: int, config_id: int = -1, splits: int = 0) -> dict:
+    """Configuration, split count, grid size and rows per split of an SpMM launch."""
+    cfg, sp, blocks, rows = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = load().nm_spmm_plan(batch, h, w, nnz, m, config_id, splits, ctypes.byref(cfg), ctypes.byref(sp),
+                             ctypes.byref(blocks), ctypes.byref(rows))
+    check(rc, "nm_spmm_plan")
     return {"config_id": cfg.value, "splits": sp.value, "blocks": blocks.value, "rows_per_split": rows.value,
             "config": describe(cfg.value)}
 

@@ -77,7 +77,8 @@ constexpr int kDefaultSplits = 8;
 // `nmat` matrices per workgroup. The workspace holds the counters of every
 // problem in its first NM_TICKET_BYTES and then nmat * splits * h floats of
 // partial sums per problem.
-int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg, int splits, Plan* p) {
+int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg, int splits, Plan* p,
+              int max_rows = kMaxRows, int batch = 1) {
   if (nprob < 1 || nprob > kMaxProblems || (nmat == 2 && nprob != 1)) return NM_ERR_BAD_SHAPE;
   long long h_total = 0;
   for (int i = 0; i < nprob; ++i) {
@@ -94,7 +95,7 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
   if (splits <= 0) splits = kDefaultSplits;
   if (splits > w) splits = w;
   int rows = ceil_div(ceil_div(w, splits), CH) * CH;
-  if (rows > kMaxRows) rows = kMaxRows;
+  if (rows > max_rows) rows = max_rows;
   if (rows < CH) rows = CH;
   splits = ceil_div(w, rows);
   p->cfg = cfg;
@@ -111,7 +112,7 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
     p->ticket_off[i] = tickets;
     tickets += (size_t)p->tiles[i];
     p->partial_off[i] = bytes;
-    if (splits > 1) bytes += (size_t)nmat * (size_t)splits * (size_t)hs[i] * sizeof(float);
+    if (splits > 1) bytes += (size_t)nmat * (size_t)batch * (size_t)splits * (size_t)hs[i] * sizeof(float);
   }
   if (tickets > (size_t)kMaxTickets || blocks > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   p->blocks = (int)blocks;
@@ -251,6 +252,71 @@ int launch_one(int dtype, const void* vec, int vec_stride, const void* mat_data,
   return launch(d, workspace, workspace_bytes, stream, nullptr);
 }
 
+// Batch rows per SpMM launch (2, 4 or 8 instantiated; a slot of the table).
+inline int spmm_nb_slot(int batch) { return batch <= 2 ? 0 : (batch <= 4 ? 1 : 2); }
+
+const SpmmRow* spmm_table(int dtype) {
+  switch (dtype) {
+    case NM_DTYPE_F16: return kSpmmKernelsF16;
+    case NM_DTYPE_BF16: return kSpmmKernelsBF16;
+    default: return kSpmmKernelsF32;
+  }
+}
+
+// SpMM plan: the GEMV plan of the same configuration (so rows are bitwise the
+// GEMV's), with at most kMaxRowsSpmm columns per split and batch-wide partials.
+int make_spmm_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, Plan* p) {
+  if (batch < 1 || batch > kMaxBatch) return NM_ERR_BAD_SHAPE;
+  if (cfg < 0) {
+    const int rc = validate_shape(h, w, nnz, m);
+    if (rc != NM_OK) return rc;
+    const bool wide = h >= 8192;
+    const bool u8 = batch <= 2;
+    cfg = (wide ? 2 : 0) + (u8 ? 1 : 0);  // th16_u4, th16_u8, th32_u4, th32_u8
+  }
+  if (cfg >= kNumSpmmConfigs) return NM_ERR_BAD_CONFIG;
+  return make_plan(1, &h, w, nnz, m, 1, cfg, splits, p, kMaxRowsSpmm, batch);
+}
+
+int launch_spmm(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
+                const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace,
+                size_t workspace_bytes, int h, int w, int nnz, int m, int cfg, int splits, void* stream) {
+  if (dtype < NM_DTYPE_F16 || dtype > NM_DTYPE_F32) return NM_ERR_BAD_CONFIG;
+  Plan p;
+  const int rc = make_spmm_plan(batch, h, w, nnz, m, cfg, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (!x || !mat_data || !mat_index || !out || !workspace) return NM_ERR_NULL_POINTER;
+  const long long K = (long long)(w / nnz) * (long long)m;
+  if (batch > 1 && (x_row_stride < K || out_row_stride < h)) return NM_ERR_BAD_SHAPE;
+  if (((uintptr_t)mat_data & 15u) != 0 || ((uintptr_t)out & 15u) != 0) return NM_ERR_MISALIGNED;
+  if (((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
+  if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
+  SpmmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = x;
+  a.x_row_stride = x_row_stride;
+  a.mat_data = mat_data;
+  a.mat_index = mat_index;
+  a.out = out;
+  a.out_row_stride = out_row_stride;
+  a.tickets = reinterpret_cast<uint32_t*>(workspace) + p.ticket_off[0];
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + p.partial_off[0]);
+  a.batch = batch;
+  a.h = h;
+  a.tiles = p.tiles[0];
+  a.w = w;
+  a.nnz = nnz;
+  a.m = m;
+  a.K = (int)K;
+  a.splits = p.splits;
+  a.rows_per_split = p.rows_per_split;
+  const int gslot = gather_slot(p.rows_per_split);  // <= 2: rows_per_split <= kMaxRowsSpmm
+  const SpmmFn fn = spmm_table(dtype)[p.cfg].fn[spmm_nb_slot(batch)][gslot];
+  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, static_cast<hipStream_t>(stream), a);
+  hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NM_OK : (int)e;
+}
+
 }  // namespace
 }  // namespace nm_hip
 
@@ -352,6 +418,30 @@ size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc) {
 int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream) {
   if (!desc) return NM_ERR_NULL_POINTER;
   return launch(*desc, workspace, workspace_bytes, stream, nullptr);
+}
+
+size_t nm_spmm_workspace_bytes(int batch, int h, int w, int nnz, int m, int config_id, int splits) {
+  Plan p;
+  return make_spmm_plan(batch, h, w, nnz, m, config_id, splits, &p) == NM_OK ? p.workspace : 0;
+}
+
+int nm_spmm(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
+            const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace, size_t workspace_bytes,
+            int h, int w, int nnz, int m, int config_id, int splits, void* stream) {
+  return launch_spmm(dtype, x, x_row_stride, batch, mat_data, mat_index, out, out_row_stride, workspace,
+                     workspace_bytes, h, w, nnz, m, config_id, splits, stream);
+}
+
+int nm_spmm_plan(int batch, int h, int w, int nnz, int m, int config_id, int splits, int* out_config_id,
+                 int* out_splits, int* out_blocks, int* out_rows_per_block) {
+  Plan p;
+  const int rc = make_spmm_plan(batch, h, w, nnz, m, config_id, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (out_config_id) *out_config_id = p.cfg;
+  if (out_splits) *out_splits = p.splits;
+  if (out_blocks) *out_blocks = p.blocks;
+  if (out_rows_per_block) *out_rows_per_block = p.rows_per_split;
+  return NM_OK;
 }
 
 int nm_num_configs(void) { return kNumConfigs; }

@@ -17,18 +17,27 @@ namespace nm_hip {
 #define NM_PLAIN_ROW(TH, U, NT) NM_ROW(1, TH, U, NT)
 #define NM_PAIR_ROW(TH, U, NT) NM_ROW(2, TH, U, NT)
 
+#define NM_SPMM_G(TH, U, NT, NB) \
+  {&nm_spmm_kernel<NM_INST_DTYPE, TH, U, 1, NT, NB>, &nm_spmm_kernel<NM_INST_DTYPE, TH, U, 2, NT, NB>, \
+   &nm_spmm_kernel<NM_INST_DTYPE, TH, U, 4, NT, NB>}
+#define NM_SPMM_ROW(TH, U, NT) {{NM_SPMM_G(TH, U, NT, 2), NM_SPMM_G(TH, U, NT, 4), NM_SPMM_G(TH, U, NT, 8)}},
+
 #if NM_INST_DTYPE == NM_DTYPE_F16
 #define NM_PLAIN_TABLE kPlainKernelsF16
 #define NM_PAIR_TABLE kPairKernelsF16
+#define NM_SPMM_TABLE kSpmmKernelsF16
 #elif NM_INST_DTYPE == NM_DTYPE_BF16
 #define NM_PLAIN_TABLE kPlainKernelsBF16
 #define NM_PAIR_TABLE kPairKernelsBF16
+#define NM_SPMM_TABLE kSpmmKernelsBF16
 #else
 #define NM_PLAIN_TABLE kPlainKernelsF32
 #define NM_PAIR_TABLE kPairKernelsF32
+#define NM_SPMM_TABLE kSpmmKernelsF32
 #endif
 
 const KernelRow NM_PLAIN_TABLE[kNumConfigs] = {NM_PLAIN_CONFIGS(NM_PLAIN_ROW)};
 const KernelRow NM_PAIR_TABLE[kNumDualConfigs] = {NM_PAIR_CONFIGS(NM_PAIR_ROW)};
+const SpmmRow NM_SPMM_TABLE[kNumSpmmConfigs] = {NM_SPMM_CONFIGS(NM_SPMM_ROW)};
 
 }  // namespace nm_hip

@@ -44,7 +44,7 @@ constexpr int kBlock = 256;        // lanes per workgroup
 constexpr int kVec = 8;            // output rows per lane
 constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
 constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
-constexpr int kAbiVersion = 3;
+constexpr int kAbiVersion = 4;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -611,6 +611,253 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
 
 
 // ---------------------------------------------------------------------------
+// Small-batch SpMM: out[b, r] for b < batch <= NB rows of activations that
+// share the weight stream (multi-token decode, batched serving, short
+// prefills). The work decomposition, FMA order, lane-row reduction and
+// split-K handoff are those of nm_gemv_kernel, so with the same tile, chunk
+// and split plan each output row is bit-identical to the GEMV of that row.
+// ---------------------------------------------------------------------------
+constexpr int kMaxBatch = 8;
+constexpr int kMaxRowsSpmm = 1024;  // compressed columns per split (LDS: NB * (rows + 2048) floats)
+
+struct SpmmArgs {
+  const void* x;            // [batch, K], rows x_row_stride elements apart, unit column stride
+  long long x_row_stride;
+  const void* mat_data;     // [w, h]
+  const uint8_t* mat_index; // [w / nnz, nnz]
+  void* out;                // [batch, h], rows out_row_stride elements apart
+  long long out_row_stride;
+  float* partial;           // [splits, batch, h] fp32, unused when splits == 1
+  uint32_t* tickets;        // [tiles] arrival counters, zero between launches
+  int batch;
+  int h;
+  int tiles;
+  int w;
+  int nnz;
+  int m;
+  int K;
+  int splits;
+  int rows_per_split;
+};
+
+template <int DT, int TH, int U, int G, bool NT, int NB>
+__global__ __launch_bounds__(kBlock) void nm_spmm_kernel(SpmmArgs a) {
+  using E = Elem<DT>;
+  typedef typename E::scalar T;
+  constexpr int W = E::kWords;
+  constexpr int TK = kBlock / TH;
+  constexpr int HT = TH * kVec;
+  constexpr int CH = TK * U;
+  constexpr int XR = G * kBlock;
+  constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
+  static_assert(U % 4 == 0 && XR % CH == 0, "chunk shape");
+  static_assert(NB >= 1 && NB <= kMaxBatch, "batch rows per launch");
+
+  __shared__ __attribute__((aligned(16))) float xs[NB][XR];
+  __shared__ __attribute__((aligned(16))) float red[NB][TK * HT];
+  __shared__ int is_last;
+
+  const int h = a.h;
+  const int tid = threadIdx.x;
+  const int th = tid % TH;
+  const int tk = tid / TH;
+  const int tile = (int)blockIdx.x % a.tiles;
+  const int split = (int)blockIdx.x / a.tiles;
+  const int c0 = split * a.rows_per_split;
+  const int cw = min(a.rows_per_split, a.w - c0);
+  const int nch = (cw + CH - 1) / CH;
+  const int col = tile * HT + th * kVec;
+  const int col_ld = min(col, h - kVec);
+  const T* __restrict__ md_tile = static_cast<const T*>(a.mat_data) + (size_t)c0 * (size_t)h + (size_t)col_ld;
+
+  // 1. In-group positions, 2. the first chunk of weights, then all position
+  //    loads waited for at once (see nm_gemv_kernel).
+  int gidx[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) gidx[j] = (int)a.mat_index[c0 + min(tid + j * kBlock, cw - 1)];
+  auto load_chunk = [&](u32x4 (&dst)[U][W], int k) {
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int r = min(k * CH + tk * U + u, cw - 1);
+      const u32x4* ptr = reinterpret_cast<const u32x4*>(md_tile + (size_t)r * (size_t)h);
+#pragma unroll
+      for (int v = 0; v < W; ++v) dst[u][v] = load16<NT>(ptr + v);
+    }
+  };
+  u32x4 bufA[U][W];
+  u32x4 bufB[U][W];
+  load_chunk(bufA, 0);
+  __builtin_amdgcn_sched_barrier(0);
+  constexpr int kAfterIdx = U * W;
+  __builtin_amdgcn_s_waitcnt((kAfterIdx & 15) | (((kAfterIdx >> 4) & 3) << 14) | (7 << 4) | (15 << 8));
+
+  // 3. Gather every batch row's activations (rows past `batch` read row
+  //    batch - 1 and are zeroed) into LDS as fp32.
+  int gpos[G];
+  bool gok[G];
+#pragma unroll
+  for (int j = 0; j < G; ++j) {
+    const int t = tid + j * kBlock;
+    const int c = c0 + min(t, cw - 1);
+    const int pos = (c / a.nnz) * a.m + gidx[j];
+    gok[j] = (t < cw) && (pos < a.K);
+    gpos[j] = gok[j] ? pos : 0;
+  }
+  T graw[NB][G];
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    const T* __restrict__ xb = static_cast<const T*>(a.x) + (long long)min(b, a.batch - 1) * a.x_row_stride;
+#pragma unroll
+    for (int j = 0; j < G; ++j) graw[b][j] = xb[gpos[j]];
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < G; ++j)
+      xs[b][tid + j * kBlock] = (gok[j] && b < a.batch) ? E::to_f32(graw[b][j]) : 0.0f;
+  __syncthreads();
+
+  float acc[NB][kVec];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int e = 0; e < kVec; ++e) acc[b][e] = 0.0f;
+
+  auto fma_chunk = [&](const u32x4 (&src)[U][W], int k) {
+    const int r0 = k * CH + tk * U;
+#pragma unroll
+    for (int u4 = 0; u4 < U / 4; ++u4) {
+      float4 xv[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) xv[b] = *reinterpret_cast<const float4*>(&xs[b][r0 + 4 * u4]);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const bool ok = (r0 + 4 * u4 + s) < cw;
+        u32x4 rw[W];
+#pragma unroll
+        for (int v = 0; v < W; ++v) rw[v] = ok ? src[4 * u4 + s][v] : u32x4{0u, 0u, 0u, 0u};
+        float wv[kVec];
+        E::unpack(rw, wv);
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const float xq = s == 0 ? xv[b].x : (s == 1 ? xv[b].y : (s == 2 ? xv[b].z : xv[b].w));
+#pragma unroll
+          for (int e = 0; e < kVec; ++e) acc[b][e] = __builtin_fmaf(wv[e], xq, acc[b][e]);
+        }
+      }
+    }
+  };
+
+  // 4. Stream the split (as nm_gemv_kernel).
+  int k = 0;
+  for (; k + 2 < nch; k += 2) {
+    load_chunk(bufB, k + 1);
+    fma_chunk(bufA, k);
+    load_chunk(bufA, k + 2);
+    fma_chunk(bufB, k + 1);
+  }
+  if (k + 1 < nch) {
+    load_chunk(bufB, k + 1);
+    fma_chunk(bufA, k);
+    fma_chunk(bufB, k + 1);
+  } else {
+    fma_chunk(bufA, k);
+  }
+
+  // 5. Lane-row reduction per batch row (fixed order).
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    float4* rp = reinterpret_cast<float4*>(&red[b][tk * HT + th * kVec]);
+    rp[0] = make_float4(acc[b][0], acc[b][1], acc[b][2], acc[b][3]);
+    rp[1] = make_float4(acc[b][4], acc[b][5], acc[b][6], acc[b][7]);
+  }
+  __syncthreads();
+  float tsum[NB][kOutPerLane];
+#pragma unroll
+  for (int b = 0; b < NB; ++b)
+#pragma unroll
+    for (int j = 0; j < kOutPerLane; ++j) {
+      const int o = tid + j * kBlock;
+      float s = 0.0f;
+      if (o < HT) {
+#pragma unroll
+        for (int t = 0; t < TK; ++t) s += red[b][t * HT + o];
+      }
+      tsum[b][j] = s;
+    }
+
+  // 6. Split-K handoff (as nm_gemv_kernel; partials [split, batch, h]).
+  if (a.splits > 1) {
+    float sink = 0.0f;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b >= a.batch) break;
+      float* part = a.partial + ((size_t)split * (size_t)a.batch + (size_t)b) * (size_t)h;
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int r = tile * HT + o;
+        if (o < HT && r < h)
+          sink += __hip_atomic_exchange(part + r, tsum[b][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      }
+    }
+    if (a.splits < 0) static_cast<T*>(a.out)[tid] = E::from_f32(sink);
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      is_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!is_last) return;
+#pragma unroll
+    for (int b = 0; b < NB; ++b) {
+      if (b >= a.batch) break;
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int r = tile * HT + o;
+        if (o < HT && r < h) {
+          const float* pp = a.partial + (size_t)b * (size_t)h + r;
+          const size_t step = (size_t)a.batch * (size_t)h;
+          float s = 0.0f;
+          int sp = 0;
+          for (; sp + 8 <= a.splits; sp += 8) {
+            float t8[8];
+#pragma unroll
+            for (int i = 0; i < 8; ++i)
+              t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+            for (int i = 0; i < 8; ++i) s += t8[i];
+          }
+          for (; sp < a.splits; ++sp)
+            s += __hip_atomic_load(pp + (size_t)sp * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          tsum[b][j] = s;
+        }
+      }
+    }
+  }
+
+  // 7. Outputs of the finished tile.
+  T* __restrict__ out = static_cast<T*>(a.out);
+#pragma unroll
+  for (int b = 0; b < NB; ++b) {
+    if (b >= a.batch) break;
+#pragma unroll
+    for (int j = 0; j < kOutPerLane; ++j) {
+      const int o = tid + j * kBlock;
+      const int r = tile * HT + o;
+      if (o < HT && r < h) out[(long long)b * a.out_row_stride + r] = E::from_f32(tsum[b][j]);
+    }
+  }
+  if (a.splits > 1 && tid == 0) {
+    __hip_atomic_store(&a.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// ---------------------------------------------------------------------------
 // Kernel configurations (ids are stable; the host side keeps the metadata).
 // X(TH, U, NT): lanes along the output rows (tile = 8 * TH rows), rows per lane
 // per chunk, non-temporal weight loads.
@@ -650,6 +897,17 @@ struct KernelRow {
   KernelFn fn[4][2];
 };
 
+// SpMM configurations: the plain ids 0-3 (th16/th32 x u4/u8, non-temporal).
+#define NM_SPMM_CONFIGS(X) X(16, 4, true) X(16, 8, true) X(32, 4, true) X(32, 8, true)
+constexpr int kNumSpmmConfigs = 4;
+
+typedef void (*SpmmFn)(SpmmArgs);
+
+// fn[batch rows per launch: 2, 4, 8][gather slot: 256, 512, 1024 columns per split].
+struct SpmmRow {
+  SpmmFn fn[3][3];
+};
+
 // Defined in nm_gemv_inst.hip, one object per element type.
 extern const KernelRow kPlainKernelsF16[kNumConfigs];
 extern const KernelRow kPlainKernelsBF16[kNumConfigs];
@@ -657,5 +915,8 @@ extern const KernelRow kPlainKernelsF32[kNumConfigs];
 extern const KernelRow kPairKernelsF16[kNumDualConfigs];
 extern const KernelRow kPairKernelsBF16[kNumDualConfigs];
 extern const KernelRow kPairKernelsF32[kNumDualConfigs];
+extern const SpmmRow kSpmmKernelsF16[kNumSpmmConfigs];
+extern const SpmmRow kSpmmKernelsBF16[kNumSpmmConfigs];
+extern const SpmmRow kSpmmKernelsF32[kNumSpmmConfigs];
 
 }  // namespace nm_hip

@@ -187,6 +187,69 @@ def _aligned(md):
     return md if md.data_ptr() % 16 == 0 else md.clone()
 
 
+def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1,
+                              splits=0):
+    """out[..., r, :] = W_sparse @ x[..., r, :] for every row of x ([..., rows, K]),
+    NM_MAX_BATCH rows per launch, each launch streaming the packed weights once.
+
+    Same layout and limits as nmsparse_spmv_forward_hip; rows may be any
+    number >= 1. Returns [..., rows, h] in x.dtype (or writes `out`, a
+    contiguous tensor of that shape). With the same config_id and splits,
+    each row equals the batch-1 GEMV of that row bit for bit when at most 1024
+    compressed columns fall in a split (see _lib.spmm_plan).
+    """
+    if not (x.is_cuda and mat_data.is_cuda and mat_index.is_cuda):
+        raise ValueError("x, mat_data, and mat_index must be GPU (HIP) tensors")
+    if x.dtype not in _DTYPE_CODE:
+        raise TypeError(f"unsupported x dtype: {x.dtype}")
+    if mat_data.dtype != x.dtype:
+        raise TypeError("x and mat_data must have same dtype")
+    if mat_index.dtype != torch.uint8:
+        raise TypeError("mat_index must be uint8")
+    if h % 128 != 0:
+        raise ValueError("h must be divisible by 128")
+    if w % BLOCK_WIDTH != 0:
+        raise ValueError(f"w={w} must be divisible by N={BLOCK_WIDTH}")
+    if VEC_WIDTH < BLOCK_WIDTH or VEC_WIDTH > 256:
+        raise ValueError(f"need N <= M <= 256 (uint8 positions), got N={BLOCK_WIDTH}, M={VEC_WIDTH}")
+    K = (w // BLOCK_WIDTH) * VEC_WIDTH
+    if x.ndim < 2 or x.shape[-1] != K:
+        raise ValueError(f"x must be [..., rows, {K}], got {tuple(x.shape)}")
+    if tuple(mat_data.shape) != (w, h) or not mat_data.is_contiguous():
+        raise ValueError(f"mat_data must be a contiguous {(w, h)} tensor, got {tuple(mat_data.shape)}")
+    if tuple(mat_index.shape) != (w // BLOCK_WIDTH, BLOCK_WIDTH) or not mat_index.is_contiguous():
+        raise ValueError(f"mat_index must be a contiguous {(w // BLOCK_WIDTH, BLOCK_WIDTH)} tensor")
+    lead = x.shape[:-1]
+    x2d = x.reshape(-1, K).contiguous()
+    rows = x2d.shape[0]
+    if out is None:
+        out = torch.empty(*lead, h, dtype=x.dtype, device=x.device)
+    elif (out.dtype != x.dtype or tuple(out.shape) != (*lead, h) or not out.is_contiguous()
+          or out.device != x.device or out.data_ptr() % 16):
+        raise ValueError(f"out must be a contiguous, 16-byte aligned {(*lead, h)} tensor of x.dtype")
+    if rows == 0:
+        return out
+    md = _aligned(mat_data)
+    lib = _lib.load()
+    nb = min(rows, _lib.NM_MAX_BATCH)
+    need = lib.nm_spmm_workspace_bytes(nb, h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
+    if need == 0:
+        raise ValueError("spmm shape outside what libnmsparse_hip supports")
+    o2d = out.view(rows, h)
+    esize = x.element_size()
+    device = x.device
+    with torch.cuda.device(device):
+        stream = torch.cuda.current_stream(device).cuda_stream
+        ws = workspace_for(device, need, stream)
+        for r0 in range(0, rows, _lib.NM_MAX_BATCH):
+            b = min(_lib.NM_MAX_BATCH, rows - r0)
+            rc = lib.nm_spmm(_DTYPE_CODE[x.dtype], x2d.data_ptr() + r0 * K * esize, K, b, md.data_ptr(),
+                             mat_index.data_ptr(), o2d.data_ptr() + r0 * h * esize, h, ws.data_ptr(), ws.numel(),
+                             h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits), stream)
+            _lib.check(rc, "nm_spmm")
+    return out
+
+
 def _check_vector(t, n, like, what):
     """t must be a contiguous [n] or [1, n] tensor of like.dtype on like.device."""
     if t.device != like.device or t.dtype != like.dtype or t.numel() != n or not t.is_contiguous():
@@ -388,5 +451,5 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
 
 
 __all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
-           "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "GemvProblem", "validate_args",
-           "workspace_for"]
+           "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "nmsparse_spmm_forward_hip",
+           "GemvProblem", "validate_args", "workspace_for"]

@@ -14,8 +14,14 @@ Mirrors the reference module API (src/spmv/nmsparse_linear.py):
   Linear j getting seed `seed + j` (src/spmv/nmsparse_linear.py:83-144).
 
 Environment, read at import like the reference (src/spmv/nmsparse_linear.py:7-8):
-NM_DECODE_ONLY=1 drops dense weights (prefill then raises), NM_WEIGHT_CPU=1
-keeps them on the host. NM_SYNTH_INIT=device (this build only) draws the
+NM_DECODE_ONLY=1 drops dense weights, NM_WEIGHT_CPU=1 keeps them on the host.
+Inputs of more than one row (batch > 1): with a dense weight they go through
+dense F.linear as in the reference; without one the reference raises
+"prefill requires dense weight", and so does a [B, 1, K] input (the op
+rejects rows != 1), where this build computes them with the small-batch SpMM
+(`torch.ops.nmsparse.spmm`). NM_SPARSE_BATCH=0 restores the reference's
+errors; NM_SPARSE_BATCH=1 also sends inputs of up to 64 rows to the SpMM when
+a dense weight is present. NM_SYNTH_INIT=device (this build only) draws the
 synthetic weights with a seeded on-device generator instead of the CPU
 stream — same distribution and shapes, much faster for 8B+ models, NOT
 bit-exact with the reference; the default is the bit-exact CPU stream.
@@ -41,6 +47,10 @@ from . import nmsparse_op  # noqa: F401  (registers torch.ops.nmsparse.gemv)
 
 DECODE_ONLY = os.environ.get("NM_DECODE_ONLY", "0") == "1"
 WEIGHT_CPU = os.environ.get("NM_WEIGHT_CPU", "0") == "1" or DECODE_ONLY
+SPARSE_BATCH = os.environ.get("NM_SPARSE_BATCH", "auto")
+if SPARSE_BATCH not in ("auto", "0", "1"):
+    raise ValueError(f"Unknown NM_SPARSE_BATCH={SPARSE_BATCH!r}; use auto, 0 or 1")
+SPARSE_BATCH_MAX_ROWS = 64
 SYNTH_INIT = os.environ.get("NM_SYNTH_INIT", "reference")
 if SYNTH_INIT not in ("reference", "device"):
     raise ValueError(f"Unknown NM_SYNTH_INIT={SYNTH_INIT!r}; use 'reference' or 'device'")
@@ -198,10 +208,17 @@ class NmSparseLinear(nn.Module):
             raise RuntimeError("prefill requires dense weight")
         return self._weight_cpu.to(device)
 
+    def _has_dense(self) -> bool:
+        return self.weight is not None or self._weight_cpu is not None
+
     def forward(self, x):
+        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        args = (self.mat_data, self.mat_index, self.w, self.h, self.block_width, self.vec_width)
+        if SPARSE_BATCH != "0" and rows > 1:
+            if not self._has_dense() or (SPARSE_BATCH == "1" and rows <= SPARSE_BATCH_MAX_ROWS):
+                return torch.ops.nmsparse.spmm(x, *args)
         if x.shape[-2] == 1:
-            return torch.ops.nmsparse.gemv(x, self.mat_data, self.mat_index,
-                                           self.w, self.h, self.block_width, self.vec_width)
+            return torch.ops.nmsparse.gemv(x, *args)
         return F.linear(x, self._prefill_weight(x.device))
 
     def extra_repr(self) -> str:

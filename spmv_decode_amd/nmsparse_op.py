@@ -6,6 +6,10 @@ Same schema, argument handling and errors as the reference op
 fp16 if needed, the result is cast back to x.dtype and reshaped to
 [*x.shape[:-1], h]. A fake (meta) implementation lets torch.compile trace it.
 
+`nmsparse::spmm` (no reference counterpart) is the batch > 1 form: any number
+of rows, NM_MAX_BATCH per launch of the small-batch SpMM kernel, same casts
+and output shape rule as `gemv`.
+
 Backend selection keeps the reference's `NM_KERNEL` contract of refusing
 unknown values (src/spmv/nmsparse_op.py:20-22). Unset, "hip" and
 "triton_ptx" all select the one shared-mask HIP kernel. "guarded", "fp16" and
@@ -18,7 +22,7 @@ import os
 
 import torch
 
-from .hip_spmv import nmsparse_spmv_forward_hip
+from .hip_spmv import nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip
 
 _kernel = os.environ.get("NM_KERNEL", "")
 if _kernel not in ("", "hip", "triton_ptx", "guarded", "fp16", "fp16_split"):
@@ -52,4 +56,19 @@ def _(x, mat_data, mat_index, w, h, block_width, vec_width):
     return x.new_empty((*x.shape[:-1], int(h)))
 
 
-__all__ = ["gemv"]
+@torch.library.custom_op("nmsparse::spmm", mutates_args=())
+def spmm(x: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor,
+         w: int, h: int, block_width: int, vec_width: int) -> torch.Tensor:
+    """y[..., r, :] = W_sparse @ x[..., r, :] for every row (batch >= 1)."""
+    xh = x if x.dtype == torch.float16 else x.to(torch.float16)
+    md = mat_data if mat_data.dtype == torch.float16 else mat_data.to(torch.float16)
+    out = nmsparse_spmm_forward_hip(xh, md, mat_index, int(w), int(h), int(block_width), int(vec_width))
+    return out.to(dtype=x.dtype)
+
+
+@spmm.register_fake
+def _(x, mat_data, mat_index, w, h, block_width, vec_width):
+    return x.new_empty((*x.shape[:-1], int(h)))
+
+
+__all__ = ["gemv", "spmm"]

@@ -226,3 +226,32 @@ def test_launch_descriptor_rejections_before_launch():
         3, (ctypes.c_int * 3)(4096, 1024, 1024), 2048, 32, 64, -1, 0)
     assert lib.nm_gemv_launch_workspace_bytes(ctypes.byref(p)) == lib.nm_gemv_gate_up_workspace_bytes(
         14336, 2048, 32, 64, -1, 0)
+
+
+def test_spmm_rejections_and_plans():
+    lib = _lib.load()
+
+    def call(dtype=0, x=FAKE, xs=4096, batch=4, md=FAKE, mi=FAKE, out=FAKE, os_=4096, ws=FAKE, wsb=1 << 30,
+             h=4096, w=2048, nnz=32, m=64, cfg=-1, splits=0):
+        return lib.nm_spmm(dtype, x, xs, batch, md, mi, out, os_, ws, wsb, h, w, nnz, m, cfg, splits, None)
+
+    assert call(batch=0) == -2 and call(batch=_lib.NM_MAX_BATCH + 1) == -2
+    assert call(cfg=4) == -7 and call(dtype=3) == -7
+    assert call(x=None) == -1 and call(out=None) == -1
+    assert call(xs=4095) == -2 and call(os_=4000) == -2
+    assert call(md=FAKE + 2) == -5 and call(out=FAKE + 4) == -5
+    assert call(wsb=1024) == -6
+    assert call(h=100) == -3 and call(w=2047) == -4
+    for batch in range(1, _lib.NM_MAX_BATCH + 1):
+        for h, w in ((4096, 2048), (4096, 7168), (14336, 2048), (384, 768)):
+            for cfg in (-1, 0, 1, 2, 3):
+                for splits in (0, 1, 3):
+                    sp = _lib.spmm_plan(batch, h, w, 32 if w % 32 == 0 else 3, 64 if w % 32 == 0 else 4, cfg, splits)
+                    assert 0 < sp["rows_per_split"] <= 1024
+                    need = lib.nm_spmm_workspace_bytes(batch, h, w, 32 if w % 32 == 0 else 3,
+                                                       64 if w % 32 == 0 else 4, cfg, splits)
+                    assert need == _lib.NM_TICKET_BYTES + (sp["splits"] * batch * h * 4 if sp["splits"] > 1 else 0)
+    # same configuration and splits -> the GEMV's plan where it has <= 1024 rows per split
+    for cfg in range(4):
+        g, s = _lib.plan(4096, 7168, 32, 64, cfg, 0), _lib.spmm_plan(8, 4096, 7168, 32, 64, cfg, 0)
+        assert (g["rows_per_split"], g["splits"]) == (s["rows_per_split"], s["splits"])

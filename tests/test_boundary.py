@@ -202,8 +202,17 @@ def test_linear_prefill_uses_dense_weight():
     x = torch.randn(1, 3, 64)
     torch.testing.assert_close(lin(x), torch.nn.functional.linear(x, dense))
     bare = nmsparse_linear.NmSparseLinear(256, 64, 8, 0, "cpu")
-    with pytest.raises(RuntimeError, match="prefill requires dense weight"):
+    # without a dense weight this build computes batch > 1 with the sparse
+    # SpMM (a device kernel: CPU tensors are rejected like the GEMV's) ...
+    with pytest.raises(ValueError, match="must be GPU"):
         bare(x)
+    # ... and NM_SPARSE_BATCH=0 restores the reference's error
+    code = ("import torch; from spmv_decode_amd import nmsparse_linear as s; "
+            "m = s.NmSparseLinear(256, 64, 8, 0, 'cpu'); m(torch.randn(1, 3, 64))")
+    r = _run_py(code, NM_SPARSE_BATCH="0")
+    assert r.returncode != 0 and "prefill requires dense weight" in r.stderr
+    r = _run_py("import spmv_decode_amd", NM_SPARSE_BATCH="2")
+    assert r.returncode != 0 and "Unknown NM_SPARSE_BATCH" in r.stderr
 
 
 def test_decode_only_env_drops_dense_weight():

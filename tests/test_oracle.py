@@ -315,3 +315,14 @@ def test_qkv_decode_composes_norms_gemv_and_rope():
     np.testing.assert_allclose(q, rq.numpy(), rtol=1e-11, atol=1e-12)
     np.testing.assert_allclose(k, rk.numpy(), rtol=1e-11, atol=1e-12)
     np.testing.assert_allclose(v, lin(vd, vi).reshape(1, hd).numpy(), rtol=1e-11, atol=1e-12)
+
+
+def test_spmm_rows_match_gemv_and_dense_matmul():
+    x0, md, mi = _case(256, 384, 3, 4, seed=21)
+    g = torch.Generator().manual_seed(22)
+    X = torch.randn(5, 256, generator=g).to(torch.float16)
+    got = O.spmm_f64(X, md, mi, 3, 4)
+    dense = O.scatter(torch.from_numpy(O.to_f64(md)), mi, 3, 4, 256)  # [h, K] float64
+    np.testing.assert_allclose(got, (torch.from_numpy(O.to_f64(X)) @ dense.T).numpy(), rtol=1e-12, atol=1e-12)
+    for b in range(5):
+        np.testing.assert_array_equal(got[b], O.gemv_f64(X[b], md, mi, 3, 4))
