@@ -3,14 +3,17 @@
     python bench.py [--gpus 1] [--steps 50] [--warmup 10] [--ratio 32:64]
 
 One step = every sparse GEMV of one Llama-3.1-8B decode token at 32:64, as the
-decoder launches them: per layer one grouped q/k/v launch, o, one gate/up pair
-launch with the SiLU*mul epilogue, and down (4 launches x 32 layers), over 32
-layers' distinct packed weights (7.0 GB resident in HBM, far beyond the
-256 MB Infinity Cache), fp16, batch 1, captured once in a hipGraph and
-replayed. `value` is the algorithmic bytes of the step (2*w*h weights + w
-index bytes per matrix, 2*K activations once per launch, 2*h outputs per
-output vector) divided by the step time. The same GEMVs as 224 separate
-launches are timed too and reported under config.unfused_224_launches.
+decoder launches them: per layer one q/k/v launch with the input RMSNorm,
+RoPE and KV-cache write fused in, o with the residual add, one gate/up pair
+launch with the post-attention RMSNorm and the SiLU*mul epilogue, and down
+with the residual add (4 launches x 32 layers), over 32 layers' distinct
+packed weights (7.0 GB resident in HBM, far beyond the 256 MB Infinity Cache),
+fp16, batch 1, captured once in a hipGraph and replayed. `value` is the
+algorithmic bytes of the step (2*w*h weights + w index bytes per matrix,
+2*K activations once per launch, norm weights, residual reads, 2*h outputs
+per output vector, the RoPE table row) divided by the step time. The same
+launches without the fusions (config.plain_fused_step) and the GEMVs as 224
+separate launches (config.unfused_224_launches) are timed too.
 
 Also reported: per-shape average launch time and GB/s for the sparse kernel
 and for dense fp16 F.linear (hipBLASLt preferred) on the same shapes, the
@@ -126,6 +129,35 @@ def main():
         hip_spmv.nmsparse_gate_up_silu(xs[4096], lay["gate_proj"], lay["up_proj"], nnz, m, out=act)
         gemv("down_proj", li)
 
+    from spmv_decode_amd.hip_spmv import GemvProblem
+    from spmv_decode_amd.microbench import DECODE_CLASSES, decode_form_bytes
+
+    # decode-form buffers: residual stream, attention output, norms, KV cache, RoPE table, position
+    S = 512
+    x_res = torch.randn(1, 4096, generator=gen, device=dev).to(torch.float16)
+    attn = torch.randn(1, 4096, generator=gen, device=dev).to(torch.float16)
+    h1, h2, qo = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(3))
+    ln1, ln2 = ((torch.rand(4096, generator=gen, device=dev) + 0.5).to(torch.float16) for _ in range(2))
+    kcs = [torch.zeros(8, 128, S, dtype=torch.float16, device=dev) for _ in range(L)]
+    vcs = [torch.zeros(8, S, 128, dtype=torch.float16, device=dev) for _ in range(L)]
+    ang = torch.outer(torch.arange(S, dtype=torch.float64),
+                      1.0 / (500000.0 ** (torch.arange(64, dtype=torch.float64) * 2.0 / 128)))
+    rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(dev)
+    pos = torch.tensor([S // 2], device=dev)
+
+    def decode_layer(li):
+        # the decoder's fused layer: q/k/v (+norm, RoPE, cache write), o (+residual),
+        # gate/up (+norm, SiLU*mul), down (+residual)
+        lay = layers[li]
+        hip_spmv.nmsparse_qkv_decode(x_res, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, q_out=qo,
+                                     k_cache_t=kcs[li], v_cache=vcs[li], pos=pos, rope_table=rope, head_dim=128,
+                                     norm=(ln1, 1e-5))
+        hip_spmv.nmsparse_gemv_launch(attn, [GemvProblem(*lay["o_proj"], h1, residual=x_res)], nnz, m)
+        hip_spmv.nmsparse_gate_up_silu(h1, lay["gate_proj"], lay["up_proj"], nnz, m, out=act, norm=(ln2, 1e-5))
+        hip_spmv.nmsparse_gemv_launch(act, [GemvProblem(*lay["down_proj"], h2, residual=h1)], nnz, m)
+
+    decode_bytes = L * sum(decode_form_bytes(c, nnz, m) for c in DECODE_CLASSES)
+
     w4, w14 = 4096 // m * nnz, 14336 // m * nnz
     fused_bytes_layer = (
         sum(2 * w4 * SHAPES[n][1] + w4 + 2 * SHAPES[n][1] for n in ("q_proj", "k_proj", "v_proj")) + 2 * 4096
@@ -163,13 +195,17 @@ def main():
         return start.elapsed_time(end) / args.steps
 
     # ---- the timed step: one decode token's sparse GEMVs as the decoder runs them
-    ms_per_step = time_step(lambda: [fused_layer(li) for li in range(L)])
-    value = fused_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"fused step ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
+    ms_per_step = time_step(lambda: [decode_layer(li) for li in range(L)])
+    value = decode_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"decode-form step ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
-    written = [act] + [outs[n] for n in ("q_proj", "k_proj", "v_proj", "o_proj", "down_proj")]
+    written = [act, qo, h1, h2, kcs[0][:, :, S // 2], vcs[0][:, S // 2]]
     if not all(bool(torch.isfinite(o.float()).all()) for o in written):
         raise RuntimeError("non-finite GEMV output")
+    ms_plain = time_step(lambda: [fused_layer(li) for li in range(L)])
+    plain_value = fused_bytes / (ms_plain * 1e-3) / 1e9
+    log(f"plain fused step ({4 * L} launches, no norm/RoPE/residual fusions) {ms_plain:.4f} ms -> "
+        f"{plain_value:.1f} GB/s")
     ms_unfused = time_step(lambda: [gemv(name, li) for li in range(L) for name in SHAPES])
     unfused_value = step_bytes / (ms_unfused * 1e-3) / 1e9
     log(f"unfused step ({len(SHAPES) * L} launches) {ms_unfused:.4f} ms -> {unfused_value:.1f} GB/s")
@@ -188,14 +224,18 @@ def main():
         "dtype": "fp16",
         "data": "synthetic (seeded on-device N(0,0.02) weights, random in-group patterns, N(0,1) activations)",
         "config": {
-            "workload": f"Llama-3.1-8B decode-token sparse GEMVs at {nnz}:{m}: {L} layers x (grouped q/k/v, o, "
-                        "gate/up pair with SiLU*mul, down), batch 1, fp16, hipGraph replay, distinct resident "
-                        "weights per layer",
+            "workload": f"Llama-3.1-8B decode-token sparse GEMVs at {nnz}:{m}: {L} layers x (q/k/v + input "
+                        "RMSNorm + RoPE + KV-cache write, o + residual, gate/up pair + RMSNorm + SiLU*mul, down + "
+                        "residual), batch 1, fp16, hipGraph replay, distinct resident weights per layer",
             "ratio": f"{nnz}:{m}",
             "layers": L,
             "launches_per_step": 4 * L,
-            "algorithmic_bytes_per_step": fused_bytes,
+            "algorithmic_bytes_per_step": decode_bytes,
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "plain_fused_step": {"ms_per_step": round(ms_plain, 5), "GBps": round(plain_value, 2),
+                                 "algorithmic_bytes_per_step": fused_bytes,
+                                 "launches": "grouped q/k/v, o, gate/up pair with SiLU*mul, down (no norm, RoPE, "
+                                             "cache or residual fusions)"},
             "unfused_224_launches": {"ms_per_step": round(ms_unfused, 5), "GBps": round(unfused_value, 2),
                                      "algorithmic_bytes_per_step": step_bytes},
         },
@@ -226,37 +266,28 @@ def main():
             f"({per_shape[cls]['pct_peak']}%) {plan} x{case.copies} copies")
         del case
         torch.cuda.empty_cache()
-    # fused launch classes of the step, weights rotated over >= 1 GiB
-    qkv_sizes = (SHAPES["q_proj"][1], SHAPES["k_proj"][1], SHAPES["v_proj"][1])
-    qkv_b = sum(2 * w4 * h + w4 + 2 * h for h in qkv_sizes) + 2 * 4096
-    copies = -(-(1 << 30) // qkv_b)
-    qkv = [MB.RotatingCase(h, 4096, nnz, m, rotate_bytes=0, min_copies=copies, seed=30 + i)
-           for i, h in enumerate(qkv_sizes)]
-    us = MB.time_grouped(qkv, reps=reps)
-    fused = {"qkv_grouped": {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": qkv_b,
-                             "GBps": round(qkv_b / (us * 1e-6) / 1e9, 1)}}
-    del qkv
-    pair_b = 2 * (2 * w4 * 14336 + w4) + 2 * 4096 + 2 * 14336
-    copies = -(-(1 << 30) // pair_b)
-    gc_, uc_ = (MB.RotatingCase(14336, 4096, nnz, m, rotate_bytes=0, min_copies=copies, seed=40 + i)
-                for i in range(2))
-    us = MB.time_pair(gc_, uc_, reps=reps)
-    fused["gate_up_pair"] = {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": pair_b,
-                             "GBps": round(pair_b / (us * 1e-6) / 1e9, 1)}
-    del gc_, uc_
+    # the step's launch classes (decode forms), weights rotated over >= 1 GiB
+    forms = MB.DecodeForms(nnz, m, rotate_bytes=1 << 30)
+    fused = {}
+    for c in DECODE_CLASSES:
+        us = forms.time(c, reps=reps)
+        b = forms.bytes(c)
+        fused[c] = {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": b,
+                    "GBps": round(b / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+                    "rotated_copies": forms.copies[c]}
+        log(f"decode class {c:18s}: {us:7.2f} us/launch {fused[c]['GBps']:7.1f} GB/s ({fused[c]['pct_peak']}%)")
+    del forms
     torch.cuda.empty_cache()
-    fused["o"] = dict(per_shape["q_o"], launches_per_step=L)
-    fused["down"] = dict(per_shape["down"], launches_per_step=L)
-    for c, v in fused.items():
-        v["pct_peak"] = round(100 * v["GBps"] / HBM_PEAK_GBS, 1)
-        log(f"fused class {c:12s}: {v['us_per_launch']:7.2f} us/launch {v['GBps']:7.1f} GB/s ({v['pct_peak']}%)")
-    # dominant kernel: largest share of the (fused) step
+    # dominant kernel: largest share of the step
     dom = max(fused, key=lambda c: fused[c]["us_per_launch"] * fused[c]["launches_per_step"])
     d = fused[dom]
-    kernel_name = {"gate_up_pair": "nm_gemv_kernel<fp16, pair_th32_u4, NMAT=2> (gate/up pair, K=4096 h=14336)",
-                   "qkv_grouped": "nm_gemv_kernel<fp16, th16_u8> grouped (q/k/v, K=4096 h=4096+1024+1024)",
-                   "down": "nm_gemv_kernel<fp16, th16_u8> (down, K=14336 h=4096)",
-                   "o": "nm_gemv_kernel<fp16, th16_u8> (o, K=4096 h=4096)"}[dom]
+    kernel_name = {
+        "gate_up_pair_norm": "nm_gemv_kernel<fp16, pair_th32_u4, NMAT=2, NORM> (gate/up pair + RMSNorm + SiLU*mul, "
+                             "K=4096 h=14336)",
+        "qkv_decode": "nm_gemv_kernel<fp16, th16_u8, NORM> (q/k/v + RMSNorm + RoPE + cache write, K=4096 "
+                      "h=4096+1024+1024)",
+        "down_resid": "nm_gemv_kernel<fp16, th16_u8> (down + residual, K=14336 h=4096)",
+        "o_resid": "nm_gemv_kernel<fp16, th16_u8> (o + residual, K=4096 h=4096)"}[dom]
     result["roofline"] = {
         "bound": "hbm",
         "achieved": d["GBps"],
@@ -268,13 +299,30 @@ def main():
         "bytes_per_launch": d["bytes_per_launch"],
         "us_per_launch": d["us_per_launch"],
     }
-    result["per_launch_class_fused"] = fused
+    result["per_launch_class"] = fused
     traffic_file = ROOT / "profiles" / "traffic.json"
     if traffic_file.exists():
         t = json.loads(traffic_file.read_text()).get(f"{dom}_{nnz}:{m}")
         if t:
             result["roofline"]["traffic"] = t.get("bytes_per_launch")
     result["per_shape_sparse"] = per_shape
+
+    # ---- batch > 1: the small-batch SpMM, per row vs the batch-1 GEMV ---------
+    spmm = {}
+    for cls in ("q_o", "gate_up", "down"):
+        K, h = SHAPES[classes[cls][0]]
+        b1 = per_shape[cls]["us_per_launch"]
+        rows = {}
+        for batch in (2, 4, 8):
+            us = MB.time_spmm(h, K, nnz, m, batch, reps=reps)
+            rows[str(batch)] = {"us_per_launch": round(us, 3), "us_per_row": round(us / batch, 3),
+                                "speedup_per_row_vs_batch1": round(b1 * batch / us, 3),
+                                "weight_GBps": round(sparse_bytes(K, h, nnz, m) / (us * 1e-6) / 1e9, 1)}
+            log(f"spmm {cls:8s} batch {batch}: {us:7.2f} us/launch, {us / batch:6.2f} us/row "
+                f"({rows[str(batch)]['speedup_per_row_vs_batch1']}x per row vs batch 1)")
+        spmm[cls] = rows
+        torch.cuda.empty_cache()
+    result["spmm_batch"] = spmm
 
     # ---- dense fp16 baseline on the same shapes ------------------------------
     if not args.no_dense:

@@ -164,6 +164,118 @@ def pair_bytes(gate: RotatingCase, up: RotatingCase) -> int:
     return 2 * (elem * gate.w * gate.n_out + gate.w) + elem * gate.n_in + elem * gate.n_out
 
 
+def decode_form_bytes(cls, nnz=32, m=64, dim=4096, inter=14336, qd=4096, kvd=1024, hd=128) -> int:
+    """Algorithmic bytes of one decode-form launch (fp16): packed weights and
+    index bytes, activations once, norm weights, residual reads, outputs (the
+    k/v outputs are the cache slots written) and the RoPE table row."""
+    wd, wi, wq = dim // m * nnz, inter // m * nnz, qd // m * nnz
+    if cls == "qkv_decode":
+        return sum(2 * wd * h + wd for h in (qd, kvd, kvd)) + 2 * dim + 2 * dim + 2 * (qd + 2 * kvd) + 8 * (hd // 2)
+    if cls == "o_resid":
+        return 2 * wq * dim + wq + 2 * qd + 2 * dim + 2 * dim
+    if cls == "gate_up_pair_norm":
+        return 2 * (2 * wd * inter + wd) + 2 * dim + 2 * dim + 2 * inter
+    if cls == "down_resid":
+        return 2 * wi * dim + wi + 2 * inter + 2 * dim + 2 * dim
+    raise ValueError(cls)
+
+
+class DecodeForms:
+    """The four launches of one fused decoder layer as the decoder issues them
+    (Llama-3.1-8B shapes): q/k/v with the input RMSNorm, RoPE and the KV-cache
+    write; o with the residual add; gate/up with the post-attention RMSNorm
+    and SiLU*mul; down with the residual add. Each class rotates over its own
+    packed weights (>= rotate_bytes); activations, norms, cache and position
+    are shared and fixed (no residual accumulates across replays)."""
+
+    KV_SLOTS = 512
+
+    def __init__(self, nnz=32, m=64, rotate_bytes=1 << 30, dim=4096, inter=14336, n_heads=32, n_kv_heads=8,
+                 head_dim=128, device="cuda", seed=50, min_copies=1):
+        self.nnz, self.m, self.hd = nnz, m, head_dim
+        self.dim, self.inter = dim, inter
+        qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
+        self.hs = {"q": qd, "kv": kvd}
+        w_dim = dim // m * nnz
+        qkv_b = sum(2 * w_dim * h + w_dim for h in (qd, kvd, kvd))
+        cq = max(min_copies, math.ceil(rotate_bytes / qkv_b))
+        self.q = RotatingCase(qd, dim, nnz, m, rotate_bytes=0, min_copies=cq, seed=seed, device=device)
+        self.k = RotatingCase(kvd, dim, nnz, m, rotate_bytes=0, min_copies=cq, seed=seed + 1, device=device)
+        self.v = RotatingCase(kvd, dim, nnz, m, rotate_bytes=0, min_copies=cq, seed=seed + 2, device=device)
+        self.o = RotatingCase(dim, qd, nnz, m, rotate_bytes=rotate_bytes, min_copies=min_copies, seed=seed + 3,
+                              device=device)
+        pair_b = 2 * (2 * w_dim * inter + w_dim)
+        cp = max(min_copies, math.ceil(rotate_bytes / pair_b))
+        self.gate = RotatingCase(inter, dim, nnz, m, rotate_bytes=0, min_copies=cp, seed=seed + 4, device=device)
+        self.up = RotatingCase(inter, dim, nnz, m, rotate_bytes=0, min_copies=cp, seed=seed + 5, device=device)
+        self.down = RotatingCase(dim, inter, nnz, m, rotate_bytes=rotate_bytes, min_copies=min_copies,
+                                 seed=seed + 6, device=device)
+        g = torch.Generator(device=device).manual_seed(seed + 7)
+        f16 = torch.float16
+        self.x = torch.randn(1, dim, generator=g, device=device).to(f16)
+        self.attn = torch.randn(1, qd, generator=g, device=device).to(f16)
+        self.act = torch.randn(1, inter, generator=g, device=device).to(f16) * 0.1
+        self.h1 = torch.empty(1, dim, dtype=f16, device=device)
+        self.h2 = torch.empty(1, dim, dtype=f16, device=device)
+        self.ln1 = (torch.rand(dim, generator=g, device=device) + 0.5).to(f16)
+        self.ln2 = (torch.rand(dim, generator=g, device=device) + 0.5).to(f16)
+        self.qo = torch.empty(1, qd, dtype=f16, device=device)
+        self.pair_out = torch.empty(1, inter, dtype=f16, device=device)
+        S = self.KV_SLOTS
+        self.k_cache = torch.zeros(n_kv_heads, head_dim, S, dtype=f16, device=device)
+        self.v_cache = torch.zeros(n_kv_heads, S, head_dim, dtype=f16, device=device)
+        ang = torch.outer(torch.arange(S, dtype=torch.float64),
+                          1.0 / (500000.0 ** (torch.arange(head_dim // 2, dtype=torch.float64) * 2.0 / head_dim)))
+        self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
+        self.pos = torch.tensor([S // 2], device=device)
+        self.copies = {"qkv_decode": cq, "o_resid": self.o.copies, "gate_up_pair_norm": cp,
+                       "down_resid": self.down.copies}
+
+    def launch(self, cls, i):
+        from .hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
+
+        nnz, m = self.nnz, self.m
+        if cls == "qkv_decode":
+            nmsparse_qkv_decode(self.x, self.q.mats[i], self.k.mats[i], self.v.mats[i], nnz, m, q_out=self.qo,
+                                k_cache_t=self.k_cache, v_cache=self.v_cache, pos=self.pos, rope_table=self.rope,
+                                head_dim=self.hd, norm=(self.ln1, 1e-5))
+        elif cls == "o_resid":
+            nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i], self.h1, residual=self.x)], nnz, m)
+        elif cls == "gate_up_pair_norm":
+            nmsparse_gate_up_silu(self.h1, self.gate.mats[i], self.up.mats[i], nnz, m, out=self.pair_out,
+                                  norm=(self.ln2, 1e-5))
+        elif cls == "down_resid":
+            nmsparse_gemv_launch(self.act, [GemvProblem(*self.down.mats[i], self.h2, residual=self.h1)], nnz, m)
+        else:
+            raise ValueError(cls)
+
+    def bytes(self, cls) -> int:
+        return decode_form_bytes(cls, self.nnz, self.m, self.dim, self.inter, self.hs["q"], self.hs["kv"], self.hd)
+
+    def time(self, cls, reps=20) -> float:
+        return graph_us_per_launch([lambda i=i: self.launch(cls, i) for i in range(self.copies[cls])], reps)
+
+
+DECODE_CLASSES = ("qkv_decode", "o_resid", "gate_up_pair_norm", "down_resid")
+
+
+def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60) -> float:
+    """us per small-batch SpMM launch of `batch` rows, weights rotated."""
+    from .hip_spmv import nmsparse_spmm_forward_hip
+
+    case = RotatingCase(n_out, n_in, nnz, m, rotate_bytes=rotate_bytes, seed=seed)
+    X = torch.randn(batch, n_in, device="cuda").to(case.dtype)
+    out = torch.empty(batch, n_out, dtype=case.dtype, device="cuda")
+
+    def launch(i):
+        md, mi = case.mats[i]
+        nmsparse_spmm_forward_hip(X, md, mi, case.w, n_out, nnz, m, out=out)
+
+    us = graph_us_per_launch([lambda i=i: launch(i) for i in range(case.copies)], reps)
+    del case
+    return us
+
+
 def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda") -> float:
     b = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
     copies = max(1, math.ceil(rotate_bytes / b))
@@ -297,7 +409,14 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     for i in range(3):
         nmsparse_gate_up_silu(g.x, g.mats[i], u.mats[i], nnz, m, out=g.out)
     torch.cuda.synchronize()
+    del g, u
     log("traffic probe: grouped q/k/v and gate/up pair done")
+    forms = DecodeForms(nnz, m, rotate_bytes=0, min_copies=3)
+    for cls in DECODE_CLASSES:
+        for i in range(3):
+            forms.launch(cls, i)
+        torch.cuda.synchronize()
+    log("traffic probe: decode-form launches done")
 
 
 def _parse_pairs(text, sep):

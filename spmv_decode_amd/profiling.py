@@ -27,10 +27,18 @@ PROBE_CLASSES = [
     ("down_32:64", 14336, [4096], 1, "down (14336 -> 4096)"),
     ("qkv_grouped_32:64", 4096, [4096, 1024, 1024], 1, "grouped q/k/v (4096 -> 4096+1024+1024)"),
     ("gate_up_pair_32:64", 4096, [14336], 2, "gate/up pair with SiLU*mul (4096 -> 2x14336)"),
+    ("qkv_decode_32:64", None, None, None, "q/k/v + input RMSNorm + RoPE + KV-cache write (decode form)"),
+    ("o_resid_32:64", None, None, None, "o + residual add (decode form)"),
+    ("gate_up_pair_norm_32:64", None, None, None, "gate/up pair + input RMSNorm (decode form)"),
+    ("down_resid_32:64", None, None, None, "down + residual add (decode form)"),
 ]
 
 
-def _algorithmic(K, hs, nmat, nnz=32, m=64):
+def _algorithmic(K, hs, nmat, nnz=32, m=64, key=None):
+    if K is None:  # a decode-form class
+        from .microbench import decode_form_bytes
+
+        return decode_form_bytes(key.rsplit("_", 1)[0], nnz, m)
     w = K // m * nnz
     return sum(nmat * (2 * w * h + w) + 2 * h for h in hs) + 2 * K
 
@@ -68,7 +76,7 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
         wv = [v for _, v in wd[3 * i:3 * i + 3]]
         fetch = sum(fv) / 3 * fscale * 1024
         write = sum(wv) / 3 * wscale * 1024
-        alg = _algorithmic(K, hs, nmat)
+        alg = _algorithmic(K, hs, nmat, key=key)
         kern = fd[3 * i][0]
         js[key] = {"kernel": f"nm_gemv_kernel{kern}", "fetch_bytes": round(fetch), "write_bytes": round(write),
                    "bytes_per_launch": round(fetch + write), "algorithmic_bytes": alg,
@@ -83,7 +91,9 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
              "```", "",
              "The probe copies a 256 MiB fp16 buffer three times (the known-size calibration kernel), then launches",
              "each class three times on distinct weights with the library's default plan. Kernel template arguments:",
-             "<dtype (0 = fp16), TH (tile = 8*TH rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT>.",
+             "<dtype (0 = fp16), TH (tile = 8*TH rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT",
+             "(2 = gate/up pair), NORM (input RMSNorm folded into the gather)>. The decode-form classes are the",
+             "launches bench.py times as its step (microbench.DecodeForms).",
              "",
              f"Calibration: the 256 MiB copy reads {sum(fcopy) / len(fcopy):.1f} KiB by FETCH_SIZE (true "
              f"{CALIBRATION_BYTES // 1024} KiB) -> fetch scale {fscale:.4f}; it writes {sum(wcopy) / len(wcopy):.1f} KiB "
@@ -106,10 +116,12 @@ def stats(stats_csv, bench_json, md_path, cmd):
              "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd,
              "python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv "
              "--bench gpurun_out/bench.json --md <this file>", "```", "",
-             "The run covers the fused step graph (grouped q/k/v, o, gate/up pair, down per layer), the 224-launch",
-             "step graph, per-class rotation graphs (>= 1 GiB of distinct weights each) and the dense hipBLASLt",
-             "baseline graphs. `nm_gemv_kernel` template arguments: <dtype (0 = fp16), TH (tile = 8*TH rows), U (rows",
-             "per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair)>.", "",
+             "The run covers the decode-form step graph (q/k/v + RMSNorm + RoPE + cache write, o + residual, gate/up",
+             "pair + RMSNorm + SiLU*mul, down + residual per layer), the plain fused step, the 224-launch step graph,",
+             "per-class rotation graphs (>= 1 GiB of distinct weights each), the small-batch SpMM graphs and the dense",
+             "hipBLASLt baseline graphs. `nm_gemv_kernel` template arguments: <dtype (0 = fp16), TH (tile = 8*TH",
+             "rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair), NORM (input",
+             "RMSNorm)>; `nm_spmm_kernel`: <dtype, TH, U, G, NT, batch rows per launch>.", "",
              "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
         n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
@@ -118,13 +130,15 @@ def stats(stats_csv, bench_json, md_path, cmd):
                      f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |")
     if b:
         rf = b.get("roofline", {})
-        pair = [r for r in rows if ", true, 2>" in r["Name"]]
+        pair = [r for r in rows if ", true, 2, " in r["Name"]]
         lines += ["", f"Unprofiled `python bench.py` from the same call: value {b['value']} GB/s, ms_per_step "
                       f"{b['ms_per_step']}; dominant launch class: {rf.get('kernel')} at {rf.get('us_per_launch')} us "
                       f"per launch (HIP events over graph replays, {rf.get('achieved')} GB/s, frac {rf.get('frac')})."]
-        if pair:
-            lines.append(f"rocprof average kernel duration of the pair kernel: {float(pair[0]['AverageNs']) / 1e3:.2f} us "
-                         "(the replay-timed figure also includes the inter-kernel gap).")
+        pair_norm = [r for r in pair if r["Name"].rstrip().endswith("true>(nm_hip::Args)")]
+        if pair_norm:
+            lines.append(f"rocprof average kernel duration of the gate/up pair + RMSNorm kernel: "
+                         f"{float(pair_norm[0]['AverageNs']) / 1e3:.2f} us (the replay-timed figure also includes the "
+                         "inter-kernel gap of the graph).")
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 
