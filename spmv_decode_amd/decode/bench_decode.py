@@ -10,6 +10,9 @@ captured hipGraph and timed with HIP events. Dense first (nn.Linear ->
 hipBLASLt), then every q/k/v/o/gate/up/down Linear is swapped to
 NmSparseLinear at N:M = (M/2):M with on-device synthetic patterns, and the
 same protocol runs again. Embeddings, norms and lm_head stay dense in both.
+The sparse model runs the fused layer (norms, RoPE, cache write and residuals
+inside the GEMV launches); `--per-linear` also times it with one launch per
+Linear and PyTorch norms/RoPE, the dense model's step structure.
 Prints a `RESULT` line per model variant (like the reference benchmarks,
 benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:186-189) and one JSON line.
 """
@@ -65,6 +68,9 @@ def main(argv=None):
     p.add_argument("--gen", type=int, default=256)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--per-linear", action="store_true",
+                   help="also time the sparse model with one launch per Linear and PyTorch norms/RoPE (the "
+                        "dense model's step structure, so the ratio isolates the GEMVs)")
     p.add_argument("--json", default=None)
     a = p.parse_args(argv)
 
@@ -113,6 +119,16 @@ def main(argv=None):
               f"decode_ms_per_token={s['ms_per_token']:.6f} median={s['ms_per_token_median_of_16']:.6f}", flush=True)
         if "dense" in res:
             res["speedup_sparse_vs_dense"] = round(res["dense"]["ms_per_token"] / s["ms_per_token"], 4)
+        if a.per_linear:
+            model.set_launch_mode("per_linear")
+            u = run_variant(model, cfg, prompt, a.gen, "sparse per-Linear", log)
+            model.set_launch_mode("fused")
+            res["sparse_per_linear"] = u
+            print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) per_linear prompt={a.prompt} gen={a.gen} "
+                  f"decode_ms_per_token={u['ms_per_token']:.6f} median={u['ms_per_token_median_of_16']:.6f}",
+                  flush=True)
+            if "dense" in res:
+                res["speedup_sparse_per_linear_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
     print(json.dumps(res), flush=True)
     if a.json:
         with open(a.json, "w") as f:

@@ -133,6 +133,8 @@ def grouped_sparse(mods) -> bool:
 
 
 class Attention(nn.Module):
+    group_launches = True  # one q/k/v launch when all three are sparse (Decoder.set_launch_mode)
+
     def __init__(self, cfg: DecoderConfig):
         super().__init__()
         self.cfg = cfg
@@ -156,7 +158,7 @@ class Attention(nn.Module):
         qkv = torch.empty(1, qd + 2 * kvd, dtype=x.dtype, device=x.device)
         slices = (qkv[:, :qd], qkv[:, qd:qd + kvd], qkv[:, qd + kvd:])
         projs = (self.q_proj, self.k_proj, self.v_proj)
-        if grouped_sparse(projs):
+        if self.group_launches and grouped_sparse(projs):
             from ..hip_spmv import nmsparse_gemv_grouped
 
             nmsparse_gemv_grouped(x2d, [(p.mat_data, p.mat_index) for p in projs], projs[0].block_width,
@@ -180,6 +182,8 @@ class Attention(nn.Module):
 
 
 class MLP(nn.Module):
+    group_launches = True  # one gate/up launch when both are sparse (Decoder.set_launch_mode)
+
     def __init__(self, cfg: DecoderConfig):
         super().__init__()
         self.gate_proj = nn.Linear(cfg.dim, cfg.inter, bias=False)
@@ -187,7 +191,7 @@ class MLP(nn.Module):
         self.down_proj = nn.Linear(cfg.inter, cfg.dim, bias=False)
 
     def forward(self, x):
-        if grouped_sparse((self.gate_proj, self.up_proj)):
+        if self.group_launches and grouped_sparse((self.gate_proj, self.up_proj)):
             from ..hip_spmv import nmsparse_gate_up_silu
 
             g, u = self.gate_proj, self.up_proj
@@ -266,6 +270,19 @@ class Decoder(nn.Module):
         self.lm_head = nn.Linear(cfg.dim, cfg.vocab, bias=False)
         self.max_seq = 0
 
+    LAUNCH_MODES = ("fused", "grouped", "per_linear")
+
+    def set_launch_mode(self, mode: str) -> None:
+        """How sparse projections are launched: "fused" (the fused layer, the
+        default), "grouped" (one q/k/v and one gate/up launch, norms and RoPE
+        in PyTorch) or "per_linear" (one launch per Linear, like the
+        reference's decode step and the dense model)."""
+        if mode not in self.LAUNCH_MODES:
+            raise ValueError(f"launch mode must be one of {self.LAUNCH_MODES}, got {mode!r}")
+        self.fuse_epilogues = mode == "fused"
+        for blk in self.layers:
+            blk.self_attn.group_launches = blk.mlp.group_launches = mode != "per_linear"
+
     def setup_cache(self, max_seq: int, device, dtype=torch.float16):
         c = self.cfg
         self.max_seq = max_seq
@@ -284,7 +301,7 @@ class Decoder(nn.Module):
         -> logits [1, vocab]. No host synchronisation."""
         x = self.embed_tokens(token)  # [1, 1, dim]
         mask = torch.where(self.positions <= pos, 0.0, float("-inf")).to(self.mask_dtype)
-        if self.fuse_epilogues and all(fusable(b) for b in self.layers):
+        if self.fuse_epilogues and all(fusable(b) and b.self_attn.group_launches for b in self.layers):
             x2d = x.view(1, -1)
             for i, blk in enumerate(self.layers):
                 fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache[i], pos, mask, self.rope)

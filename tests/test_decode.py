@@ -190,3 +190,15 @@ def test_restored_compressed_checkpoint_decodes_identically(gpu):
                          for i, t in enumerate((1, 2, 3))])
     for x, y in zip(*outs):
         assert torch.equal(x, y)
+
+
+def test_launch_modes_are_validated_and_applied():
+    model = Decoder(tiny_config())
+    with pytest.raises(ValueError, match="launch mode"):
+        model.set_launch_mode("fast")
+    model.set_launch_mode("per_linear")
+    assert not model.fuse_epilogues and not model.layers[0].self_attn.group_launches
+    model.set_launch_mode("grouped")
+    assert not model.fuse_epilogues and model.layers[1].mlp.group_launches
+    model.set_launch_mode("fused")
+    assert model.fuse_epilogues

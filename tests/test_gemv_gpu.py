@@ -515,21 +515,17 @@ def test_decoder_fused_layer_matches_grouped_and_per_linear_paths(gpu, qk_norm):
     assert all(dm.fusable(b) for b in mdl.layers)
     toks = [3, 5, 7, 9, 11]
 
-    def run(fuse, grouped=True):
-        mdl.fuse_epilogues = fuse
-        orig = dm.grouped_sparse
-        if not grouped:
-            dm.grouped_sparse = lambda mods: False
+    def run(mode):
+        mdl.set_launch_mode(mode)
         try:
             mdl.setup_cache(16, "cuda", dtype=torch.float16)
             with torch.no_grad():
                 return [mdl.forward_step(torch.tensor([[t]], device="cuda"), torch.tensor([i], device="cuda")).float()
                         for i, t in enumerate(toks)]
         finally:
-            dm.grouped_sparse = orig
-            mdl.fuse_epilogues = True
+            mdl.set_launch_mode("fused")
 
-    fused, grouped, per_linear = run(True), run(False), run(False, grouped=False)
+    fused, grouped, per_linear = run("fused"), run("grouped"), run("per_linear")
     for a, b, c in zip(fused, grouped, per_linear):
         torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
         torch.testing.assert_close(b, c, rtol=2e-2, atol=2e-2)
