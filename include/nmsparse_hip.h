@@ -223,6 +223,11 @@ typedef struct nm_gemv_launch_desc {
 } nm_gemv_launch_desc;
 
 size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);
+/* The plan of such a launch (only the kind, counts, sizes, config_id and
+ * splits of desc are read): configuration, splits, workgroups, compressed
+ * rows per split and rows per chunk. */
+int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int* out_splits, int* out_blocks,
+                        int* out_rows_per_split, int* out_chunk_rows);
 int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream);
 
 /*

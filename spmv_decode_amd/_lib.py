@@ -71,6 +71,7 @@ ABI = {
     "nm_num_gate_up_configs": (_i, []),
     "nm_gemv_launch_workspace_bytes": (_sz, [_descp]),
     "nm_gemv_launch": (_i, [_descp, _vp, _sz, _vp]),
+    "nm_gemv_launch_plan": (_i, [_descp, _ip, _ip, _ip, _ip, _ip]),
     "nm_spmm_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "nm_spmm": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_spmm_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
@@ -79,7 +80,7 @@ ABI = {
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
 }
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _lib = None
 _lock = threading.Lock()

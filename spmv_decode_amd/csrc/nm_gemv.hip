@@ -415,6 +415,27 @@ size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc) {
   return launch(*desc, nullptr, 0, nullptr, &need) == NM_OK ? need : 0;
 }
 
+int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int* out_splits, int* out_blocks,
+                        int* out_rows_per_split, int* out_chunk_rows) {
+  if (!desc) return NM_ERR_NULL_POINTER;
+  const bool pair = desc->kind == NM_KIND_GATE_UP;
+  if (desc->kind != NM_KIND_GROUPED && !pair) return NM_ERR_BAD_CONFIG;
+  const int nprob = pair ? 1 : desc->nprob;
+  if (pair ? desc->nprob != 2 : (nprob < 1 || nprob > kMaxProblems)) return NM_ERR_BAD_SHAPE;
+  int hs[kMaxProblems];
+  for (int i = 0; i < nprob; ++i) hs[i] = desc->prob[i].h;
+  Plan p;
+  const int rc = make_plan(nprob, hs, desc->w, desc->nnz, desc->m, pair ? 2 : 1, desc->config_id, desc->splits, &p);
+  if (rc != NM_OK) return rc;
+  const Config& c = pair ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
+  if (out_config_id) *out_config_id = p.cfg;
+  if (out_splits) *out_splits = p.splits;
+  if (out_blocks) *out_blocks = p.blocks;
+  if (out_rows_per_split) *out_rows_per_split = p.rows_per_split;
+  if (out_chunk_rows) *out_chunk_rows = (kBlock / c.th) * c.u;
+  return NM_OK;
+}
+
 int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream) {
   if (!desc) return NM_ERR_NULL_POINTER;
   return launch(*desc, workspace, workspace_bytes, stream, nullptr);

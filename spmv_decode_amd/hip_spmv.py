@@ -276,6 +276,24 @@ class GemvProblem:
         self.residual, self.head_norm, self.rope, self.layout = residual, head_norm, bool(rope), layout
 
 
+def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1, splits=0) -> dict:
+    """The library's plan for a launch over `problems` ((mat_data, mat_index)
+    pairs): configuration, splits, grid, compressed rows per split and rows
+    per chunk (the rows a workgroup streams first)."""
+    desc = _lib.NmGemvLaunchDesc()
+    desc.dtype, desc.kind = _lib.NM_DTYPE_F16, _lib.NM_KIND_GATE_UP if gate_up else _lib.NM_KIND_GROUPED
+    desc.nprob = len(problems)
+    w = problems[0][0].shape[0]
+    desc.w, desc.nnz, desc.m, desc.config_id, desc.splits = w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits)
+    for i, (md, _) in enumerate(problems):
+        desc.prob[i].h = int(md.shape[1])
+    out = [ctypes.c_int() for _ in range(5)]
+    rc = _lib.load().nm_gemv_launch_plan(ctypes.byref(desc), *[ctypes.byref(v) for v in out])
+    _lib.check(rc, "nm_gemv_launch_plan")
+    keys = ("config_id", "splits", "blocks", "rows_per_split", "chunk_rows")
+    return {k: v.value for k, v in zip(keys, out)}
+
+
 def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, norm=None, head_dim=0,
                          head_eps=1e-6, pos=None, pos_limit=None, rope_table=None, config_id=-1, splits=0):
     """One launch of 1-4 GEMVs that share `vec` [1, K] (or the gate/up pair),
@@ -452,4 +470,4 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
 
 __all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
            "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "nmsparse_spmm_forward_hip",
-           "GemvProblem", "validate_args", "workspace_for"]
+           "GemvProblem", "launch_plan", "validate_args", "workspace_for"]

@@ -255,3 +255,23 @@ def test_spmm_rejections_and_plans():
     for cfg in range(4):
         g, s = _lib.plan(4096, 7168, 32, 64, cfg, 0), _lib.spmm_plan(8, 4096, 7168, 32, 64, cfg, 0)
         assert (g["rows_per_split"], g["splits"]) == (s["rows_per_split"], s["splits"])
+
+
+def test_launch_plan_query():
+    """Host-only plan query of a fused launch (shapes only: no kernel runs)."""
+    import torch
+
+    from spmv_decode_amd.hip_spmv import launch_plan
+
+    def mats(K, h):
+        return torch.empty(K // 64 * 32, h, dtype=torch.float16), torch.empty(K // 64, 32, dtype=torch.uint8)
+
+    qkv = [mats(4096, 4096), mats(4096, 1024), mats(4096, 1024)]
+    p = launch_plan(qkv, 32, 64)
+    assert p == {"config_id": 1, "splits": 8, "blocks": (32 + 8 + 8) * 8, "rows_per_split": 256, "chunk_rows": 128}
+    pair = launch_plan([mats(4096, 14336), mats(4096, 14336)], 32, 64, gate_up=True)
+    assert pair["config_id"] == 1 and pair["chunk_rows"] == 32 and pair["blocks"] == 56 * 8
+    down = launch_plan([mats(14336, 4096)], 32, 64)
+    assert down["rows_per_split"] == 896 and down["chunk_rows"] == 128
+    with pytest.raises(_lib.NmSparseLibraryError):
+        launch_plan([mats(4096, 1000)], 32, 64)
