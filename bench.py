@@ -81,7 +81,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU only; --gpus {args.gpus} is not supported "
-              "(the path would shard by output rows / input groups across GPUs, see DESIGN.md)", file=sys.stderr)
+              "(the GEMV would shard by output rows for q/k/v/gate/up and by input groups for o/down, with one "
+              "all-reduce of the fp32 partials per row-parallel Linear)", file=sys.stderr)
         sys.exit(2)
     nnz, m = (int(v) for v in args.ratio.split(":"))
 
@@ -387,11 +388,15 @@ def decode_ms_per_token(m, log):
     swap_to_nmsparse(model, m, "cuda", seed=0, init="device", keep_dense=False)
     torch.cuda.empty_cache()
     sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)
+    model.set_launch_mode("per_linear")  # the dense model's step structure: isolates the GEMVs
+    per_linear = run_variant(model, LLAMA31_8B, prompt, 256, "sparse per-Linear", log)
     del model
     torch.cuda.empty_cache()
     out = {"model": "llama-3.1-8b (random init)", "prompt": 128, "gen": 256,
            "dense_ms_per_token": dense["ms_per_token"], "sparse_ms_per_token": sparse["ms_per_token"],
            "speedup_sparse_vs_dense": round(dense["ms_per_token"] / sparse["ms_per_token"], 4),
+           "sparse_per_linear_ms_per_token": per_linear["ms_per_token"],
+           "speedup_sparse_per_linear_vs_dense": round(dense["ms_per_token"] / per_linear["ms_per_token"], 4),
            "sparse_linear_bytes_per_token": linear_bytes(LLAMA31_8B, m),
            "dense_linear_bytes_per_token": linear_bytes(LLAMA31_8B, 0)}
     log(f"decode: dense {out['dense_ms_per_token']} ms/token, sparse {out['sparse_ms_per_token']} ms/token, "

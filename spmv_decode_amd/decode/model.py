@@ -1,7 +1,7 @@
 """A compact Llama-3.1 / Qwen3 decoder for batch-1 decode on MI355X.
 
 This is the caller of the sparse GEMV on the decode path (the role of the
-reference's gpt-fast `model.py` / Hugging Face Qwen3): every
+reference's gpt-fast `model.py` / Hugging Face Qwen3 decoders): every
 attention and MLP projection is a `nn.Linear` under the Hugging Face names
 (`self_attn.{q,k,v,o}_proj`, `mlp.{gate,up,down}_proj`) on `model.layers`, so
 `swap_to_nmsparse(model, M, device)` turns each into an `NmSparseLinear`

@@ -1,9 +1,11 @@
 """Summarise rocprofv3 CSV output into the markdown/JSON kept under profiles/.
 
-    python -m spmv_decode_amd.profiling traffic --fetch gpurun_out/pmc_fetch/pmc_counter_collection.csv \\
-        --write gpurun_out/pmc_write/pmc_counter_collection.csv --md profiles/...md --json profiles/traffic.json
-    python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv \\
-        --bench gpurun_out/bench.json --md profiles/...md
+    python -m spmv_decode_amd.profiling traffic --fetch <out>/pmc_fetch/pmc_counter_collection.csv \\
+        --write <out>/pmc_write/pmc_counter_collection.csv --md <summary> --json profiles/traffic.json
+    python -m spmv_decode_amd.profiling stats --csv <out>/prof_bench/bench_kernel_stats.csv \\
+        --bench <out>/bench.json --md <summary>
+
+(<out>: the rocprofv3 output directory of the profiled run.)
 
 `traffic` calibrates FETCH_SIZE / WRITE_SIZE (KiB per dispatch) against the
 256 MiB copy that `microbench --traffic-probe` runs first (a kernel of known
