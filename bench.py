@@ -432,6 +432,15 @@ def cpu_baseline(layer, xs, nnz, m, budget_s):
         times.append(time.perf_counter() - t0)
     med = statistics.median(times)
     gbs = layer_bytes / med / 1e9
+    # the reference benchmarks' own CPU thread default is 1 (BENCH_CPU_THREADS)
+    torch.set_num_threads(1)
+    one = []
+    for _ in range(3):
+        t0 = time.perf_counter()
+        one_layer()
+        one.append(time.perf_counter() - t0)
+    torch.set_num_threads(threads)
+    med1 = statistics.median(one)
     cpu_model = "unknown"
     try:
         for line in open("/proc/cpuinfo"):
@@ -450,6 +459,11 @@ def cpu_baseline(layer, xs, nnz, m, budget_s):
                   f"Llama-3.1-8B layer's 7 GEMVs at {nnz}:{m} ({layer_bytes / 1e6:.1f} MB), median of "
                   f"{len(times)} passes in ~{budget_s:.0f} s; CPU: {cpu_model}",
         "ms_per_layer": round(med * 1e3, 2),
+        "one_thread": {"value": round(layer_bytes / med1 / 1e9, 3), "unit": "GB/s", "ms_per_layer": round(med1 * 1e3, 2),
+                       "sample": "median of 3 passes over the same layer"},
+        "decode_token_gemv_ms": round(LLAMA["n_layers"] * med * 1e3, 1),
+        "decode_token_gemv_note": "32 layers x the measured per-layer time: the sparse GEMVs of one Llama-3.1-8B "
+                                  "decode token on the host cores (attention, norms and lm_head not included)",
     }
 
 
