@@ -355,6 +355,13 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
 #pragma unroll
     for (int i = 0; i < kSsqWords; ++i) sraw[i] = xw[min(i * kBlock + tid, nw - 1)];
   }
+  // Single-matrix launches request chunk 1 here, behind the gather: the
+  // barrier below then waits for chunk 0 and the gather only, and chunk 1
+  // arrives during chunk 0's FMAs (a one-chunk split re-reads its last row).
+  // The gate/up pair keeps chunk 1 after the barrier, which measured faster
+  // for its two weight streams.
+  constexpr bool kEarlyChunk1 = NMAT == 1;
+  if constexpr (kEarlyChunk1) load_chunk(bufB, 1);
   __builtin_amdgcn_sched_barrier(0);  // every gather request before the first use of one
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
@@ -402,18 +409,32 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   // 4. Stream the split two chunks at a time: chunk k+1 is in flight while
   //    chunk k is consumed. Loads inside the loop are unconditional.
   int k = 0;
-  for (; k + 2 < nch; k += 2) {
-    load_chunk(bufB, k + 1);
+  if constexpr (kEarlyChunk1) {
+    // Chunks k and k+1 are in flight on entry; each buffer is refilled as
+    // soon as it has been consumed (past the split's end the clamped rows
+    // are re-read and never used).
+    for (; k + 2 < nch; k += 2) {
+      fma_chunk(bufA, k);
+      load_chunk(bufA, k + 2);
+      fma_chunk(bufB, k + 1);
+      load_chunk(bufB, k + 3);
+    }
     fma_chunk(bufA, k);
-    load_chunk(bufA, k + 2);
-    fma_chunk(bufB, k + 1);
-  }
-  if (k + 1 < nch) {
-    load_chunk(bufB, k + 1);
-    fma_chunk(bufA, k);
-    fma_chunk(bufB, k + 1);
+    if (k + 1 < nch) fma_chunk(bufB, k + 1);
   } else {
-    fma_chunk(bufA, k);
+    for (; k + 2 < nch; k += 2) {
+      load_chunk(bufB, k + 1);
+      fma_chunk(bufA, k);
+      load_chunk(bufA, k + 2);
+      fma_chunk(bufB, k + 1);
+    }
+    if (k + 1 < nch) {
+      load_chunk(bufB, k + 1);
+      fma_chunk(bufA, k);
+      fma_chunk(bufB, k + 1);
+    } else {
+      fma_chunk(bufA, k);
+    }
   }
 
   // 5. Reduce the TK lane-rows of the tile through LDS (fixed order), and
