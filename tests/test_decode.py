@@ -202,3 +202,49 @@ def test_launch_modes_are_validated_and_applied():
     assert not model.fuse_epilogues and model.layers[1].mlp.group_launches
     model.set_launch_mode("fused")
     assert model.fuse_epilogues
+
+
+@pytest.mark.parametrize("V", [128256, 151936, 512, 1000, 97])
+def test_greedy_token_matches_argmax_with_ties(V):
+    """The two-stage greedy argmax returns torch.argmax's index (the first
+    occurrence of the maximum), also when the maximum repeats across chunks."""
+    from spmv_decode_amd.decode.runner import greedy_token
+
+    g = torch.Generator().manual_seed(V)
+    for trial in range(6):
+        logits = torch.randn(1, V, generator=g).half()
+        if trial >= 2:  # plant the maximum at several positions (first one wins)
+            k = 2 + trial
+            pos = torch.randperm(V, generator=g)[:k]
+            logits[0, pos] = 30.0
+        if trial == 5:
+            logits.fill_(1.0)  # all equal: index 0
+        assert int(greedy_token(logits)) == int(torch.argmax(logits, dim=-1)), (V, trial)
+
+
+@pytest.mark.gpu
+def test_greedy_token_in_a_captured_graph(gpu):
+    """The two-stage greedy argmax at Llama-3.1's vocabulary, captured in a
+    hipGraph and replayed over new logits, equals torch.argmax each time."""
+    from spmv_decode_amd.decode.runner import greedy_token
+
+    V = 128256
+    logits = torch.randn(1, V, device="cuda").half()
+    out = torch.zeros(1, dtype=torch.long, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        out.copy_(greedy_token(logits))
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        out.copy_(greedy_token(logits))
+    gen = torch.Generator(device="cuda").manual_seed(0)
+    for rep in range(4):
+        logits.copy_(torch.randn(1, V, generator=gen, device="cuda").half())
+        if rep == 3:
+            logits[0, 5000] = logits[0, 90000] = 40.0  # a repeated maximum: the first one wins
+        g.replay()
+        torch.cuda.synchronize()
+        assert int(out) == int(torch.argmax(logits, dim=-1)), rep
