@@ -72,6 +72,11 @@ def parse_args():
     p.add_argument("--no-dense", action="store_true", help="skip the dense hipBLASLt comparison")
     p.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     p.add_argument("--cpu-seconds", type=float, default=12.0, help="CPU baseline time budget")
+    p.add_argument("--cpu-detail", action="store_true",
+                   help="also time CPU-A (dense scatter + fp32 mv) and CPU-B (gather form) per shape, config 1 "
+                        "and every Llama-3.1-8B shape, all host threads and one (minutes)")
+    p.add_argument("--cpu-decode", action="store_true",
+                   help="also time a CPU Llama-3.1-8B decode step (the decoder code, every Linear via CPU-B)")
     p.add_argument("--only-step", action="store_true", help="time only the sparse step (for profiling)")
     p.add_argument("--no-decode", action="store_true", help="skip the end-to-end Llama-3.1-8B decode")
     return p.parse_args()
@@ -357,6 +362,10 @@ def main():
     # ---- CPU baseline (rank 0, N=1): oracle gather form on one layer ----------
     if not args.no_cpu:
         result["cpu_baseline"] = cpu_baseline(layers[0], xs, nnz, m, args.cpu_seconds)
+        if args.cpu_detail:
+            result["cpu_baseline"]["detail"] = cpu_detail(nnz, m)
+        if args.cpu_decode:
+            result["cpu_baseline"]["decode"] = cpu_decode(nnz, m)
 
     # ---- end-to-end decode ms/token: dense hipBLASLt vs N:M sparse ------------
     if not args.no_decode:
@@ -465,6 +474,116 @@ def cpu_baseline(layer, xs, nnz, m, budget_s):
         "decode_token_gemv_note": "32 layers x the measured per-layer time: the sparse GEMVs of one Llama-3.1-8B "
                                   "decode token on the host cores (attention, norms and lm_head not included)",
     }
+
+
+def _median_stdev(fn, reps, warmup=3):
+    for _ in range(warmup):
+        fn()
+    t = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        t.append(time.perf_counter() - t0)
+    return statistics.median(t), (statistics.stdev(t) if len(t) > 1 else 0.0)
+
+
+def cpu_detail(nnz, m, reps=20):
+    """CPU-A (the oracle: scatter to dense, fp32 torch.mv) and CPU-B (gather
+    form) per shape: config 1 (Qwen3-0.6B up-proj, 2:4, the reference's own
+    generator) and the Llama-3.1-8B shapes at nnz:m, all host threads and one
+    thread; median and stdev of `reps` calls after 3 warm-ups."""
+    import torch
+
+    from oracle import nm_oracle as O
+
+    threads = os.cpu_count() or 1
+    cases = []
+    md1, mi1 = O.make_sparse(1024, 3072, 4, 0)[:2]
+    cases.append(("config1_up_proj 1024->3072 2:4", 1024, 3072, 2, 4, md1, mi1))
+    g = torch.Generator().manual_seed(7)
+    for name, (K, h) in SHAPES.items():
+        w = K // m * nnz
+        md = (torch.randn(w, h, generator=g) * 0.02).half()
+        mi = torch.stack([torch.randperm(m, generator=g)[:nnz].sort().values for _ in range(K // m)]).to(torch.uint8)
+        cases.append((f"{name} {K}->{h} {nnz}:{m}", K, h, nnz, m, md, mi))
+    rows = []
+    for label, K, h, n_, m_, md, mi in cases:
+        x = torch.randn(1, K, generator=g).half()
+        b = sparse_bytes(K, h, n_, m_)
+        row = {"shape": label, "bytes": b}
+        for th in (threads, 1):
+            torch.set_num_threads(th)
+            for form, fn in (("cpu_a", lambda: O.gemv_fp32_dense(x, md, mi, n_, m_)),
+                             ("cpu_b", lambda: O.gemv_gather_torch(x, md, mi, n_, m_))):
+                med, sd = _median_stdev(fn, reps if th > 1 or b < 60e6 else max(5, reps // 4))
+                row[f"{form}_{th}t_ms"] = round(med * 1e3, 3)
+                row[f"{form}_{th}t_sd_ms"] = round(sd * 1e3, 3)
+                row[f"{form}_{th}t_GBps"] = round(b / med / 1e9, 3)
+        torch.set_num_threads(threads)
+        log(f"cpu detail {label}: CPU-A {row[f'cpu_a_{threads}t_ms']:.2f} ms / CPU-B {row[f'cpu_b_{threads}t_ms']:.2f} "
+            f"ms ({threads} threads); CPU-A {row['cpu_a_1t_ms']:.2f} / CPU-B {row['cpu_b_1t_ms']:.2f} ms (1 thread)")
+        rows.append(row)
+    return {"threads": threads, "reps": reps, "rows": rows}
+
+
+def cpu_decode(nnz, m, tokens=4):
+    """ms/token of a CPU decode step of the Llama-3.1-8B architecture with the
+    decoder's own code (fp32 activations, static cache, per-Linear path) and
+    every q/k/v/o/gate/up/down Linear computed in the CPU-B gather form from
+    packed fp16 weights (random values; the timing does not depend on them)."""
+    import torch
+    import torch.nn as nn
+
+    from oracle import nm_oracle as O
+    from spmv_decode_amd.decode.model import LLAMA31_8B, Decoder, RMSNorm
+
+    class CpuGatherLinear(nn.Module):
+        def __init__(self, md, mi):
+            super().__init__()
+            self.md, self.mi = md, mi
+
+        def forward(self, x):
+            y = O.gemv_gather_torch(x, self.md, self.mi, nnz, m)
+            return y.view(*x.shape[:-1], -1).to(x.dtype)
+
+    cfg = LLAMA31_8B
+    t0 = time.perf_counter()
+    with torch.device("meta"):
+        model = Decoder(cfg)
+    g = torch.Generator().manual_seed(11)
+    for blk in model.layers:
+        for sub, names in ((blk.self_attn, ("q_proj", "k_proj", "v_proj", "o_proj")),
+                           (blk.mlp, ("gate_proj", "up_proj", "down_proj"))):
+            for name in names:
+                h, K = getattr(sub, name).weight.shape
+                w = K // m * nnz
+                md = (torch.randn(w, h, generator=g) * 0.02).half()  # fp32 draws: CPU fp16 randn is 5x slower
+                mi = torch.rand(K // m, m, generator=g).argsort(dim=1)[:, :nnz].sort(dim=1).values.to(torch.uint8)
+                setattr(sub, name, CpuGatherLinear(md, mi))
+    for mod in model.modules():
+        for pname, par in list(mod._parameters.items()):
+            if par is not None and par.is_meta:
+                val = torch.ones(par.shape) if isinstance(mod, RMSNorm) else torch.randn(par.shape, generator=g) * 0.02
+                mod._parameters[pname] = nn.Parameter(val, requires_grad=False)
+    model.eval()
+    model.setup_cache(tokens + 2, "cpu", dtype=torch.float32)
+    build_s = time.perf_counter() - t0
+    token = torch.zeros(1, 1, dtype=torch.long)
+    times = []
+    with torch.no_grad():
+        for i in range(tokens + 1):  # the first step is a warm-up
+            t1 = time.perf_counter()
+            logits = model.forward_step(token, torch.tensor([i]))
+            token = torch.argmax(logits, dim=-1).view(1, 1)
+            times.append(time.perf_counter() - t1)
+    times = times[1:]
+    ms = statistics.median(times) * 1e3
+    log(f"cpu decode: {ms:.1f} ms/token over {tokens} tokens ({os.cpu_count()} threads; model built in {build_s:.0f} s)")
+    return {"ms_per_token": round(ms, 1), "tokens": tokens, "threads": os.cpu_count(),
+            "per_token_ms": [round(t * 1e3, 1) for t in times],
+            "sample": "Llama-3.1-8B architecture, fp32 activations, every projection in the CPU-B gather form from "
+                      f"packed fp16 {nnz}:{m} weights, dense fp32 embedding / lm_head, {tokens} greedy steps after "
+                      "one warm-up step"}
 
 
 if __name__ == "__main__":

@@ -110,7 +110,8 @@ def rotate(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
 
 def linear_into(lin: nn.Module, x2d: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     """y = lin(x) written into `out` ([1, h] contiguous slice): the sparse GEMV's
-    `out=` for NmSparseLinear, torch.mm (hipBLASLt) for a dense nn.Linear."""
+    `out=` for NmSparseLinear, torch.mm (hipBLASLt) for a dense nn.Linear, the
+    module's own forward for any other Linear-like module."""
     from ..nmsparse_linear import NmSparseLinear
 
     if isinstance(lin, NmSparseLinear):
@@ -118,7 +119,9 @@ def linear_into(lin: nn.Module, x2d: torch.Tensor, out: torch.Tensor) -> torch.T
 
         return nmsparse_spmv_forward_hip(x2d, lin.mat_data, lin.mat_index, lin.w, lin.h, lin.block_width, 128,
                                          lin.vec_width, 1, x2d.shape[1], out=out)
-    return torch.mm(x2d, lin.weight.t(), out=out)
+    if isinstance(lin, nn.Linear):
+        return torch.mm(x2d, lin.weight.t(), out=out)
+    return out.copy_(lin(x2d).view_as(out))
 
 
 def grouped_sparse(mods) -> bool:

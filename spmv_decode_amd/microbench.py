@@ -78,8 +78,9 @@ class RotatingCase:
                                          out=self.out, config_id=config_id, splits=splits)
 
 
-def graph_us_per_launch(launches, reps=20, warmup=3, stream=None) -> float:
-    """Capture `launches` (callables) in one hipGraph; median replay time / len in us."""
+def graph_us_per_launch(launches, reps=20, warmup=3, stream=None, stats=False):
+    """Capture `launches` (callables) in one hipGraph; median replay time / len in
+    us (with stats=True: (median, sample stdev) over the `reps` replays)."""
     stream = stream or torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -103,7 +104,10 @@ def graph_us_per_launch(launches, reps=20, warmup=3, stream=None) -> float:
         e.synchronize()
         samples.append(s.elapsed_time(e) * 1e3 / len(launches))
     del g
-    return statistics.median(samples)
+    med = statistics.median(samples)
+    if stats:
+        return med, (statistics.stdev(samples) if len(samples) > 1 else 0.0)
+    return med
 
 
 def dense_reference_check(case: RotatingCase, out: torch.Tensor) -> dict:
@@ -118,8 +122,9 @@ def dense_reference_check(case: RotatingCase, out: torch.Tensor) -> dict:
             "rel_l2": (d.norm() / ref.norm().clamp_min(1e-12)).item()}
 
 
-def time_sparse(case: RotatingCase, config_id=-1, splits=0, reps=20) -> float:
-    return graph_us_per_launch([lambda i=i: case.launch(i, config_id, splits) for i in range(case.copies)], reps)
+def time_sparse(case: RotatingCase, config_id=-1, splits=0, reps=20, warmup=3, stats=False):
+    return graph_us_per_launch([lambda i=i: case.launch(i, config_id, splits) for i in range(case.copies)], reps,
+                               warmup, stats=stats)
 
 
 def time_grouped(cases, reps=20) -> float:
@@ -276,14 +281,15 @@ def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60
     return us
 
 
-def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda") -> float:
+def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda", warmup=3,
+               stats=False):
     b = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
     copies = max(1, math.ceil(rotate_bytes / b))
     g = torch.Generator(device=device).manual_seed(seed)
     Ws = [(torch.randn(n_out, n_in, generator=g, device=device) * 0.02).to(dtype) for _ in range(copies)]
     x = torch.randn(1, n_in, generator=g, device=device).to(dtype)
     o = torch.empty(1, n_out, dtype=dtype, device=device)
-    us = graph_us_per_launch([lambda W=W: torch.matmul(x, W.t(), out=o) for W in Ws], reps)
+    us = graph_us_per_launch([lambda W=W: torch.matmul(x, W.t(), out=o) for W in Ws], reps, warmup, stats=stats)
     del Ws
     return us
 
@@ -293,7 +299,7 @@ def candidate_splits(case: RotatingCase):
 
 
 def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, csv_path=None, dense=True,
-        log=print):
+        log=print, warmup=3):
     dtype = DTYPES[dtype_name]
     rows = []
     try:
@@ -301,7 +307,8 @@ def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, 
     except Exception:
         pass
     for n_out, n_in in dims:
-        dense_us = time_dense(n_out, n_in, dtype, rotate_mib << 20, reps) if dense else float("nan")
+        dense_us, dense_sd = (time_dense(n_out, n_in, dtype, rotate_mib << 20, reps, warmup=warmup, stats=True)
+                              if dense else (float("nan"), float("nan")))
         db = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
         log(f"--- ({n_out},{n_in}) dense {dense_us:.2f} us {db / dense_us / 1e3:.1f} GB/s")
         for nnz, m in ratios:
@@ -320,13 +327,15 @@ def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, 
                 if key in seen and cfg != -1:
                     continue
                 seen.add(key)
-                us = time_sparse(case, cfg, sp, reps)
+                us, sd = time_sparse(case, cfg, sp, reps, warmup, stats=True)
                 gbs = case.bytes / us / 1e3
                 row = {"n_out": n_out, "n_in": n_in, "ratio": f"{nnz}:{m}", "dtype": dtype_name,
                        "config": p["config"] if cfg >= 0 else f"auto:{plan['config']}", "splits": p["splits"],
                        "blocks": p["blocks"], "rows_per_split": p["rows_per_split"], "us": round(us, 3),
-                       "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                       "dense_us": round(dense_us, 3), "speedup_vs_dense": round(dense_us / us, 3),
+                       "us_sd": round(sd, 3), "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
+                       "dense_us": round(dense_us, 3), "dense_us_sd": round(dense_sd, 3),
+                       "dense_GBps": round(dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8) / dense_us / 1e3, 1),
+                       "speedup_vs_dense": round(dense_us / us, 3),
                        "copies": case.copies, **{k: float(f"{v:.3e}") for k, v in err.items()}}
                 rows.append(row)
                 if best is None or us < best["us"]:
@@ -419,6 +428,27 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     log("traffic probe: decode-form launches done")
 
 
+def write_sweep_md(rows, path, cmd):
+    """Markdown table of the library's own plan (`auto:` rows) per (shape, ratio)."""
+    lines = ["# N:M sparse GEMV vs dense hipBLASLt per shape and ratio (MI355X, fp16, batch 1)", "",
+             "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
+             "Each (shape, ratio) rotates over >= 1 GiB of distinct packed weights in one hipGraph (so neither L2 nor",
+             "the 256 MB Infinity Cache serves them); median and stdev over the timed replays, per launch, including",
+             "the graph's inter-kernel gap. GB/s counts the algorithmic bytes 2*w*h + w + 2*K + 2*h (dense:",
+             "2*K*h + 2*K + 2*h); % of the 8 TB/s HBM peak. Errors are against the fp32 dense matvec on the",
+             "scattered masked weight (the reference microbenchmark's oracle).", "",
+             "| Shape (K -> h) | N:M | Plan | us (median +- sd) | GB/s | % peak | Dense us | Dense GB/s | Speedup | "
+             "max_abs | rel_l2 |", "|---|---|---|---|---|---|---|---|---|---|---|"]
+    for r in rows:
+        if not str(r["config"]).startswith("auto:"):
+            continue
+        lines.append(f"| {r['n_in']} -> {r['n_out']} | {r['ratio']} | {r['config'][5:]} s{r['splits']} | "
+                     f"{r['us']:.2f} +- {r['us_sd']:.2f} | {r['GBps']:.0f} | {r['pct_peak']:.1f}% | "
+                     f"{r['dense_us']:.2f} +- {r['dense_us_sd']:.2f} | {r['dense_GBps']:.0f} | "
+                     f"{r['speedup_vs_dense']:.2f}x | {r['max_abs']:.1e} | {r['rel_l2']:.1e} |")
+    Path(path).write_text("\n".join(lines) + "\n")
+
+
 def _parse_pairs(text, sep):
     return [tuple(int(v) for v in item.split(sep)) for item in text.split(",") if item]
 
@@ -431,6 +461,8 @@ def main(argv=None):
     p.add_argument("--sweep", action="store_true", help="time every config / split count")
     p.add_argument("--rotate-mib", type=int, default=1024)
     p.add_argument("--reps", type=int, default=20)
+    p.add_argument("--warmup", type=int, default=3, help="untimed graph replays before the timed ones")
+    p.add_argument("--md", default=None, help="write a markdown summary of the library's choice per (shape, ratio)")
     p.add_argument("--no-dense", action="store_true")
     p.add_argument("--csv", default=None)
     p.add_argument("--json", default=None, help="write the best row per (shape, ratio) as JSON")
@@ -446,7 +478,9 @@ def main(argv=None):
         traffic_probe(_parse_pairs(a.dims, "x"), log=lambda s: print(s, flush=True))
         return 0
     rows = run(_parse_pairs(a.dims, "x"), _parse_pairs(a.ratios, ":"), a.dtype, a.sweep, a.rotate_mib, a.reps,
-               a.csv, not a.no_dense, log=lambda s: print(s, flush=True))
+               a.csv, not a.no_dense, log=lambda s: print(s, flush=True), warmup=a.warmup)
+    if a.md:
+        write_sweep_md(rows, a.md, " ".join(["python -u -m spmv_decode_amd.microbench", *(argv or sys.argv[1:])]))
     if a.json:
         best = {}
         for r in rows:

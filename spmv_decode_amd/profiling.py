@@ -4,6 +4,7 @@
         --write <out>/pmc_write/pmc_counter_collection.csv --md <summary> --json profiles/traffic.json
     python -m spmv_decode_amd.profiling stats --csv <out>/prof_bench/bench_kernel_stats.csv \\
         --bench <out>/bench.json --md <summary>
+    python -m spmv_decode_amd.profiling cpu --bench <out>/bench_cpu.json --md <summary>
 
 (<out>: the rocprofv3 output directory of the profiled run.)
 
@@ -144,6 +145,36 @@ def stats(stats_csv, bench_json, md_path, cmd):
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 
+def cpu(bench_json, md_path, cmd):
+    """CPU baseline summary from a `bench.py --cpu-detail --cpu-decode` JSON line."""
+    b = json.loads(Path(bench_json).read_text())
+    c = b["cpu_baseline"]
+    d = c["detail"]
+    t = d["threads"]
+    lines = ["# CPU baseline on the GPU box's host cores (the reference's PyTorch formulation of the op)", "",
+             "Command (repository root, one MI355X box):", "", "```", cmd, "```", "",
+             "The reference has no CPU kernel for this op (every call rejects CPU tensors), so its CPU path is its",
+             "own PyTorch formulation: CPU-A = the microbenchmark's oracle, scatter to a dense weight then fp32",
+             "`torch.mv`; CPU-B = the gather form `mat_data.float().T @ x.float()[sel]` (same math, no dense",
+             "weight). Both from `oracle/nm_oracle.py`, timed with `time.perf_counter`: 3 warm-ups, then the median",
+             f"(and stdev) of {d['reps']} calls ({max(5, d['reps'] // 4)} at one thread for the 58 MB shapes). GB/s counts",
+             "the same algorithmic bytes as the GPU figures.", "",
+             f"| Shape | Bytes | CPU-A {t} thr (ms) | CPU-B {t} thr (ms) | CPU-B {t} thr GB/s | CPU-A 1 thr (ms) | "
+             "CPU-B 1 thr (ms) | CPU-B 1 thr GB/s |", "|---|---|---|---|---|---|---|---|"]
+    for r in d["rows"]:
+        lines.append(f"| {r['shape']} | {r['bytes']:,} | {r[f'cpu_a_{t}t_ms']:.2f} +- {r[f'cpu_a_{t}t_sd_ms']:.2f} | "
+                     f"{r[f'cpu_b_{t}t_ms']:.2f} +- {r[f'cpu_b_{t}t_sd_ms']:.2f} | {r[f'cpu_b_{t}t_GBps']:.2f} | "
+                     f"{r['cpu_a_1t_ms']:.2f} | {r['cpu_b_1t_ms']:.2f} | {r['cpu_b_1t_GBps']:.2f} |")
+    dec = c.get("decode")
+    lines += ["", f"Headline `cpu_baseline` of the same run: {c['value']} GB/s ({c['ms_per_layer']} ms per Llama-3.1-8B "
+                  f"layer of 7 CPU-B GEMVs, {c['cores']} threads; one thread {c['one_thread']['value']} GB/s)."]
+    if dec:
+        lines.append(f"CPU decode step: {dec['ms_per_token']} ms/token ({dec['sample']}; per token "
+                     f"{', '.join(str(v) for v in dec['per_token_ms'])} ms; {dec['threads']} threads), against "
+                     f"{b['decode']['sparse_ms_per_token']} ms/token for the hipGraph decode on the GPU in the same run.")
+    Path(md_path).write_text("\n".join(lines) + "\n")
+
+
 def main(argv=None):
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     sub = p.add_subparsers(dest="cmd", required=True)
@@ -152,6 +183,9 @@ def main(argv=None):
     t.add_argument("--write", required=True)
     t.add_argument("--md", required=True)
     t.add_argument("--json", required=True)
+    c = sub.add_parser("cpu")
+    c.add_argument("--bench", required=True)
+    c.add_argument("--md", required=True)
     s = sub.add_parser("stats")
     s.add_argument("--csv", required=True)
     s.add_argument("--bench", default=None)
@@ -163,6 +197,8 @@ def main(argv=None):
                 "python -u -m spmv_decode_amd.microbench --traffic-probe",
                 "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc --output-format csv -- "
                 "python -u -m spmv_decode_amd.microbench --traffic-probe")
+    elif a.cmd == "cpu":
+        cpu(a.bench, a.md, "python -u bench.py --cpu-detail --cpu-decode > gpurun_out/bench_cpu.json")
     else:
         stats(a.csv, a.bench, a.md,
               "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_bench -o bench --output-format csv -- "
