@@ -92,6 +92,38 @@ def test_cached_decode_matches_full_sequence_reference(qk_norm):
     torch.testing.assert_close(torch.stack(got), ref, rtol=1e-4, atol=1e-4)
 
 
+def test_linear_like_projection_modules_run_the_decoder():
+    """Projections that are neither nn.Linear nor NmSparseLinear (e.g. a
+    CPU gather-form module) go through their own forward: same logits as the
+    dense model."""
+    import torch.nn as nn
+
+    class Wrapped(nn.Module):
+        def __init__(self, lin):
+            super().__init__()
+            self.lin = lin
+
+        def forward(self, x):
+            return F.linear(x, self.lin.weight)
+
+    torch.manual_seed(0)
+    model = Decoder(tiny_config()).float()
+    init_weights_(model, seed=3, std=0.05)
+    model.setup_cache(8, "cpu", dtype=torch.float32)
+    tokens = torch.tensor([5, 17, 300, 2])
+    with torch.no_grad():
+        ref = [model.forward_step(t.view(1, 1), torch.tensor([i])) for i, t in enumerate(tokens)]
+        for blk in model.layers:
+            for sub, names in ((blk.self_attn, ("q_proj", "k_proj", "v_proj", "o_proj")),
+                               (blk.mlp, ("gate_proj", "up_proj", "down_proj"))):
+                for n in names:
+                    setattr(sub, n, Wrapped(getattr(sub, n)))
+        model.setup_cache(8, "cpu", dtype=torch.float32)
+        got = [model.forward_step(t.view(1, 1), torch.tensor([i])) for i, t in enumerate(tokens)]
+    for a, b in zip(got, ref):
+        torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
+
+
 def test_swap_applies_to_decoder_layout():
     model = Decoder(tiny_config())
     n = swap_to_nmsparse(model, 8, "cpu", seed=3, keep_dense=False)
