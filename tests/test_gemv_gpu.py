@@ -529,3 +529,32 @@ def test_decoder_fused_layer_matches_grouped_and_per_linear_paths(gpu, qk_norm):
     for a, b, c in zip(fused, grouped, per_linear):
         torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
         torch.testing.assert_close(b, c, rtol=2e-2, atol=2e-2)
+
+
+def test_module_under_torch_compile_matches_eager(gpu):
+    """The reference benchmarks compile the model around the op
+    (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:155): a full-graph
+    torch.compile (aot_eager: no code generation) of a block that uses
+    NmSparseLinear traces through the op's fake implementation and calls the
+    HIP kernel, bit for bit as eager."""
+    import torch.nn as nn
+
+    class Block(nn.Module):
+        def __init__(self):
+            super().__init__()
+            self.a = nmsparse_linear.NmSparseLinear(1024, 2048, 16, 1, "cuda", init="device")
+            self.b = nmsparse_linear.NmSparseLinear(2048, 1024, 16, 2, "cuda", init="device")
+
+        def forward(self, x):
+            return self.b(torch.nn.functional.silu(self.a(x))) + x
+
+    torch._dynamo.reset()
+    blk = Block()
+    x = torch.randn(1, 1, 2048, device="cuda").half()
+    eager = blk(x)
+    compiled = torch.compile(blk, backend="aot_eager", fullgraph=True)
+    say("torch.compile aot_eager over NmSparseLinear")
+    for _ in range(2):
+        got = compiled(x)
+        torch.cuda.synchronize()
+        assert torch.equal(got, eager)
