@@ -559,31 +559,54 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
     }
   }
   if (a.splits > 1) {
+    // The partials of a group of 8 splits are read for every matrix and
+    // output of the lane at once (one round trip per group, not one per
+    // matrix); each output sums them in split order. Lanes past the tile
+    // read the tile's last column (clamped) and keep their sums unused.
+    float sacc[NMAT][kOutPerLane];
+    const float* pp[NMAT][kOutPerLane];
 #pragma unroll
-    for (int j = 0; j < kOutPerLane; ++j) {
-      const int o = tid + j * kBlock;
-      const int r = tile * HT + o;
-      if (o < HT && r < h) {
+    for (int q = 0; q < NMAT; ++q)
 #pragma unroll
-        for (int q = 0; q < NMAT; ++q) {
-          float* pp = a.prob[NMAT == 1 ? p : q].partial + r;
-          float s = 0.0f;
-          int sp = 0;
-          for (; sp + 8 <= a.splits; sp += 8) {
-            float t8[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
-                                        __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) s += t8[i];
-          }
-          for (; sp < a.splits; ++sp)
-            s += __hip_atomic_load(pp + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          tsum[q][j] = s;
-        }
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int r = min(tile * HT + min(tid + j * kBlock, HT - 1), h - 1);
+        pp[q][j] = a.prob[NMAT == 1 ? p : q].partial + r;
+        sacc[q][j] = 0.0f;
       }
+    int sp = 0;
+    for (; sp + 8 <= a.splits; sp += 8) {
+      float t8[NMAT][kOutPerLane][8];
+#pragma unroll
+      for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            t8[q][j][i] = __hip_atomic_load(pp[q][j] + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
+                                            __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i) sacc[q][j] += t8[q][j][i];
     }
+    for (; sp < a.splits; ++sp) {
+      float t1[NMAT][kOutPerLane];
+#pragma unroll
+      for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j)
+          t1[q][j] = __hip_atomic_load(pp[q][j] + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j) sacc[q][j] += t1[q][j];
+    }
+#pragma unroll
+    for (int q = 0; q < NMAT; ++q)
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) tsum[q][j] = sacc[q][j];
   }
 
   float val[kOutPerLane];
@@ -855,32 +878,56 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_kernel(SpmmArgs a) {
     }
     __syncthreads();
     if (!is_last) return;
+    // Partials of a group of splits read for every batch row and output at
+    // once (as nm_gemv_kernel); rows >= batch read row batch - 1, unused.
+    const size_t step = (size_t)a.batch * (size_t)h;
+    constexpr int G8 = NB * kOutPerLane * 8 <= 32 ? 8 : 4;  // splits per group: <= 32 loads in flight per lane
+    float sacc[NB][kOutPerLane];
+    const float* pp[NB][kOutPerLane];
 #pragma unroll
-    for (int b = 0; b < NB; ++b) {
-      if (b >= a.batch) break;
+    for (int b = 0; b < NB; ++b)
 #pragma unroll
       for (int j = 0; j < kOutPerLane; ++j) {
-        const int o = tid + j * kBlock;
-        const int r = tile * HT + o;
-        if (o < HT && r < h) {
-          const float* pp = a.partial + (size_t)b * (size_t)h + r;
-          const size_t step = (size_t)a.batch * (size_t)h;
-          float s = 0.0f;
-          int sp = 0;
-          for (; sp + 8 <= a.splits; sp += 8) {
-            float t8[8];
-#pragma unroll
-            for (int i = 0; i < 8; ++i)
-              t8[i] = __hip_atomic_load(pp + (size_t)(sp + i) * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-#pragma unroll
-            for (int i = 0; i < 8; ++i) s += t8[i];
-          }
-          for (; sp < a.splits; ++sp)
-            s += __hip_atomic_load(pp + (size_t)sp * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-          tsum[b][j] = s;
-        }
+        const int r = min(tile * HT + min(tid + j * kBlock, HT - 1), h - 1);
+        pp[b][j] = a.partial + (size_t)min(b, a.batch - 1) * (size_t)h + r;
+        sacc[b][j] = 0.0f;
       }
+    int sp = 0;
+    for (; sp + G8 <= a.splits; sp += G8) {
+      float t8[NB][kOutPerLane][8];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < G8)
+              t8[b][j][i] = __hip_atomic_load(pp[b][j] + (size_t)(sp + i) * step, __ATOMIC_RELAXED,
+                                              __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j)
+#pragma unroll
+          for (int i = 0; i < 8; ++i)
+            if (i < G8) sacc[b][j] += t8[b][j][i];
     }
+    for (; sp < a.splits; ++sp) {
+      float t1[NB][kOutPerLane];
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j)
+          t1[b][j] = __hip_atomic_load(pp[b][j] + (size_t)sp * step, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int b = 0; b < NB; ++b)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j) sacc[b][j] += t1[b][j];
+    }
+#pragma unroll
+    for (int b = 0; b < NB; ++b)
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) tsum[b][j] = sacc[b][j];
   }
 
   // 7. Outputs of the finished tile.
