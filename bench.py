@@ -145,7 +145,7 @@ def main():
     h1, h2, qo = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(3))
     ln1, ln2 = ((torch.rand(4096, generator=gen, device=dev) + 0.5).to(torch.float16) for _ in range(2))
     kcs = [torch.zeros(8, 128, S, dtype=torch.float16, device=dev) for _ in range(L)]
-    vcs = [torch.zeros(8, S, 128, dtype=torch.float16, device=dev) for _ in range(L)]
+    vcs = [torch.zeros(8, 128, S, dtype=torch.float16, device=dev) for _ in range(L)]
     ang = torch.outer(torch.arange(S, dtype=torch.float64),
                       1.0 / (500000.0 ** (torch.arange(64, dtype=torch.float64) * 2.0 / 128)))
     rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(dev)
@@ -156,7 +156,7 @@ def main():
         # gate/up (+norm, SiLU*mul), down (+residual)
         lay = layers[li]
         hip_spmv.nmsparse_qkv_decode(x_res, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, q_out=qo,
-                                     k_cache_t=kcs[li], v_cache=vcs[li], pos=pos, rope_table=rope, head_dim=128,
+                                     k_cache_t=kcs[li], v_cache_t=vcs[li], pos=pos, rope_table=rope, head_dim=128,
                                      norm=(ln1, 1e-5))
         hip_spmv.nmsparse_gemv_launch(attn, [GemvProblem(*lay["o_proj"], h1, residual=x_res)], nnz, m)
         hip_spmv.nmsparse_gate_up_silu(h1, lay["gate_proj"], lay["up_proj"], nnz, m, out=act, norm=(ln2, 1e-5))

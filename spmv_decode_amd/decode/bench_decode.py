@@ -47,7 +47,7 @@ def linear_bytes(cfg, m: int) -> int:
 
 
 def run_variant(model, cfg, prompt, gen, label, log):
-    dec = GraphDecoder(model, prompt.numel() + gen + 8)
+    dec = GraphDecoder(model, prompt.numel() + gen)
     t0 = time.time()
     dec.capture()
     log(f"{label}: captured decode step in {time.time() - t0:.1f} s")

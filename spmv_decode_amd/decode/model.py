@@ -9,6 +9,12 @@ unchanged. Only decode (one token per step) is implemented: the KV cache is
 static, the position is a device tensor, and a step contains no host
 synchronisation, so it can be captured once in a hipGraph and replayed.
 
+Keys and values are cached transposed, [kv_heads, head_dim, S]: the score
+product then reads contiguous rows of keys, and the probability-times-values
+product takes the values as a transposed operand, which the BLAS library runs
+faster at these shapes (MI355X, S = 384: 6.6 µs against 8.2 µs for a
+[kv_heads, S, head_dim] cache; S = 1024: 4.3 µs against 12-16 µs).
+
 Numerics follow the published architectures: RMSNorm in fp32 (one fused
 `F.rms_norm` kernel), rotary embeddings on interleaved (even, odd) pairs as a
 complex multiply (the convention of the reference's gpt-fast model,
@@ -150,10 +156,10 @@ class Attention(nn.Module):
             self.q_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
             self.k_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
 
-    def forward(self, x, freqs, k_cache_t, v_cache, pos, mask):
-        """x [1, 1, dim]; freqs complex64 [1, head_dim/2]; k_cache_t [kvh, head_dim, S]
-        (pre-transposed keys); v_cache [kvh, S, head_dim]; pos [1] int64;
-        mask [S] additive (0 / -inf) in the activation dtype."""
+    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, mask):
+        """x [1, 1, dim]; freqs complex64 [1, head_dim/2]; k_cache_t and v_cache_t
+        [kvh, head_dim, S] (keys and values both stored transposed); pos [1]
+        int64; mask [S] additive (0 / -inf) in the activation dtype."""
         c = self.cfg
         g = c.n_heads // c.n_kv_heads
         qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
@@ -174,13 +180,13 @@ class Attention(nn.Module):
             qk = torch.cat((self.q_norm(qk[:c.n_heads]), self.k_norm(qk[c.n_heads:])))
         qk = rotate(qk, freqs)
         q, k = qk[:c.n_heads], qk[c.n_heads:]
-        v = qkv[0, qd + kvd:].view(c.n_kv_heads, 1, c.head_dim)
+        v = qkv[0, qd + kvd:].view(c.n_kv_heads, c.head_dim, 1)
         k_cache_t.index_copy_(2, pos, k.unsqueeze(-1))
-        v_cache.index_copy_(1, pos, v)
+        v_cache_t.index_copy_(2, pos, v)
         scores = torch.baddbmm(mask.expand(c.n_kv_heads, g, -1), q.view(c.n_kv_heads, g, c.head_dim), k_cache_t,
                                alpha=1.0 / math.sqrt(c.head_dim))
         probs = torch.softmax(scores, dim=-1)  # fp16 in/out, fp32 inside
-        y = torch.bmm(probs, v_cache)  # [kvh, g, head_dim]
+        y = torch.bmm(probs, v_cache_t.transpose(1, 2))  # [kvh, g, head_dim]
         return self.o_proj(y.view(1, 1, qd))
 
 
@@ -212,8 +218,8 @@ class Block(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.dim, cfg.norm_eps)
         self.mlp = MLP(cfg)
 
-    def forward(self, x, freqs, k_cache_t, v_cache, pos, mask):
-        h = x + self.self_attn(self.input_layernorm(x), freqs, k_cache_t, v_cache, pos, mask)
+    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, mask):
+        h = x + self.self_attn(self.input_layernorm(x), freqs, k_cache_t, v_cache_t, pos, mask)
         return h + self.mlp(self.post_attention_layernorm(h))
 
 
@@ -227,7 +233,7 @@ def fusable(block: Block) -> bool:
             and isinstance(at.o_proj, NmSparseLinear) and isinstance(mlp.down_proj, NmSparseLinear))
 
 
-def fused_block_step(blk: Block, x2d, k_cache_t, v_cache, pos, mask, rope):
+def fused_block_step(blk: Block, x2d, k_cache_t, v_cache_t, pos, mask, rope):
     """One fused sparse layer on the residual stream x2d [1, dim], updated in
     place. rope: complex64 [S, head_dim/2] table of the cache's positions."""
     from ..hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
@@ -240,14 +246,14 @@ def fused_block_step(blk: Block, x2d, k_cache_t, v_cache, pos, mask, rope):
     ln1, ln2 = blk.input_layernorm, blk.post_attention_layernorm
     qp, kp, vp = at.q_proj, at.k_proj, at.v_proj
     nmsparse_qkv_decode(x2d, (qp.mat_data, qp.mat_index), (kp.mat_data, kp.mat_index), (vp.mat_data, vp.mat_index),
-                        qp.block_width, qp.vec_width, q_out=q, k_cache_t=k_cache_t, v_cache=v_cache, pos=pos,
+                        qp.block_width, qp.vec_width, q_out=q, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
                         rope_table=rope, head_dim=c.head_dim, norm=(ln1.weight, ln1.eps),
                         q_norm=at.q_norm.weight if c.qk_norm else None,
                         k_norm=at.k_norm.weight if c.qk_norm else None, head_eps=c.norm_eps)
     scores = torch.baddbmm(mask.expand(c.n_kv_heads, g, -1), q.view(c.n_kv_heads, g, c.head_dim), k_cache_t,
                            alpha=1.0 / math.sqrt(c.head_dim))
     probs = torch.softmax(scores, dim=-1)
-    y = torch.bmm(probs, v_cache).view(1, qd)
+    y = torch.bmm(probs, v_cache_t.transpose(1, 2)).view(1, qd)
     o = at.o_proj
     nmsparse_gemv_launch(y, [GemvProblem(o.mat_data, o.mat_index, x2d, residual=x2d)], o.block_width, o.vec_width)
     gp, up = mlp.gate_proj, mlp.up_proj
@@ -291,8 +297,8 @@ class Decoder(nn.Module):
         self.max_seq = max_seq
         self.k_cache_t = [torch.zeros(c.n_kv_heads, c.head_dim, max_seq, device=device, dtype=dtype)
                           for _ in range(c.n_layers)]
-        self.v_cache = [torch.zeros(c.n_kv_heads, max_seq, c.head_dim, device=device, dtype=dtype)
-                        for _ in range(c.n_layers)]
+        self.v_cache_t = [torch.zeros(c.n_kv_heads, c.head_dim, max_seq, device=device, dtype=dtype)
+                          for _ in range(c.n_layers)]
         t = torch.arange(max_seq, dtype=torch.float64)
         ang = torch.outer(t, rope_inv_freq(c))
         self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
@@ -307,11 +313,11 @@ class Decoder(nn.Module):
         if self.fuse_epilogues and all(fusable(b) and b.self_attn.group_launches for b in self.layers):
             x2d = x.view(1, -1)
             for i, blk in enumerate(self.layers):
-                fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache[i], pos, mask, self.rope)
+                fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, mask, self.rope)
             return self.lm_head(self.norm(x)).view(1, -1)
         freqs = self.rope.index_select(0, pos)
         for i, layer in enumerate(self.layers):
-            x = layer(x, freqs, self.k_cache_t[i], self.v_cache[i], pos, mask)
+            x = layer(x, freqs, self.k_cache_t[i], self.v_cache_t[i], pos, mask)
         return self.lm_head(self.norm(x)).view(1, -1)
 
 

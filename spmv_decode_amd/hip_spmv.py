@@ -439,20 +439,29 @@ def nmsparse_gate_up_silu(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, *, out=None, no
                                 splits=splits)[0]
 
 
-def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_t, v_cache, pos, rope_table,
-                        head_dim, norm=None, q_norm=None, k_norm=None, head_eps=1e-6, config_id=-1, splits=0):
+def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_t, v_cache=None, v_cache_t=None,
+                        pos, rope_table, head_dim, norm=None, q_norm=None, k_norm=None, head_eps=1e-6, config_id=-1,
+                        splits=0):
     """The q/k/v projections of one decode step in one launch.
 
     q, k, v are (mat_data, mat_index) pairs sharing `vec` [1, K]. Writes the
     rotated queries to `q_out` [1, n_heads * head_dim], the rotated keys into
-    `k_cache_t` [kv_heads, head_dim, S] at column pos and the values into
-    `v_cache` [kv_heads, S, head_dim] at row pos (the decoder's pre-transposed
-    static cache). `norm` = (weight [K], eps) is the layer's input RMSNorm;
-    `q_norm` / `k_norm` ([head_dim]) are Qwen3's per-head norms.
+    `k_cache_t` [kv_heads, head_dim, S] at column pos and the values either
+    into `v_cache` [kv_heads, S, head_dim] at row pos or into `v_cache_t`
+    [kv_heads, head_dim, S] at column pos (exactly one of the two; the
+    decoder keeps both caches transposed). `norm` = (weight [K], eps) is the
+    layer's input RMSNorm; `q_norm` / `k_norm` ([head_dim]) are Qwen3's
+    per-head norms.
     """
     kvh, hd, S = k_cache_t.shape
-    if hd != head_dim or tuple(v_cache.shape) != (kvh, S, hd):
-        raise ValueError(f"k_cache_t {tuple(k_cache_t.shape)} / v_cache {tuple(v_cache.shape)} do not match "
+    if (v_cache is None) == (v_cache_t is None):
+        raise ValueError("pass exactly one of v_cache [kv_heads, S, head_dim] and v_cache_t [kv_heads, head_dim, S]")
+    if v_cache is not None:
+        vc, want, v_layout = v_cache, (kvh, S, hd), (S * hd, 1, hd)
+    else:
+        vc, want, v_layout = v_cache_t, (kvh, hd, S), (hd * S, S, 1)
+    if hd != head_dim or tuple(vc.shape) != want:
+        raise ValueError(f"k_cache_t {tuple(k_cache_t.shape)} / value cache {tuple(vc.shape)} do not match "
                          f"head_dim {head_dim}")
     for name, (md, _), rows in (("k", k, kvh * hd), ("v", v, kvh * hd)):
         if md.shape[1] != rows:
@@ -462,7 +471,7 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
         raise ValueError(f"rope_table has {rt.shape[0]} positions, the cache {S}")
     probs = [GemvProblem(q[0], q[1], q_out, head_norm=q_norm, rope=True),
              GemvProblem(k[0], k[1], k_cache_t, head_norm=k_norm, rope=True, layout=(hd * S, S, 1)),
-             GemvProblem(v[0], v[1], v_cache, layout=(S * hd, 1, hd))]
+             GemvProblem(v[0], v[1], vc, layout=v_layout)]
     return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, norm=norm, head_dim=head_dim,
                                 head_eps=head_eps, pos=pos, rope_table=rt[:S], config_id=config_id,
                                 splits=splits)

@@ -228,7 +228,7 @@ class DecodeForms:
         self.pair_out = torch.empty(1, inter, dtype=f16, device=device)
         S = self.KV_SLOTS
         self.k_cache = torch.zeros(n_kv_heads, head_dim, S, dtype=f16, device=device)
-        self.v_cache = torch.zeros(n_kv_heads, S, head_dim, dtype=f16, device=device)
+        self.v_cache = torch.zeros(n_kv_heads, head_dim, S, dtype=f16, device=device)  # transposed, as the decoder
         ang = torch.outer(torch.arange(S, dtype=torch.float64),
                           1.0 / (500000.0 ** (torch.arange(head_dim // 2, dtype=torch.float64) * 2.0 / head_dim)))
         self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
@@ -242,7 +242,7 @@ class DecodeForms:
         nnz, m = self.nnz, self.m
         if cls == "qkv_decode":
             nmsparse_qkv_decode(self.x, self.q.mats[i], self.k.mats[i], self.v.mats[i], nnz, m, q_out=self.qo,
-                                k_cache_t=self.k_cache, v_cache=self.v_cache, pos=self.pos, rope_table=self.rope,
+                                k_cache_t=self.k_cache, v_cache_t=self.v_cache, pos=self.pos, rope_table=self.rope,
                                 head_dim=self.hd, norm=(self.ln1, 1e-5))
         elif cls == "o_resid":
             nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i], self.h1, residual=self.x)], nnz, m)

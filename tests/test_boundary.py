@@ -105,6 +105,22 @@ def test_implementation_limits_raise_value_error():
         hip_spmv.validate_args(vec, md, mi, 128, 256, 2, 128, 4, 1, 300, require_device=False)
 
 
+def test_qkv_decode_value_cache_arguments():
+    """Exactly one value cache, of the layout its name states; checked before
+    any launch."""
+    kvh, hd, S, K = 2, 64, 16, 256
+    x = torch.zeros(1, K, dtype=torch.float16)
+    mat = (torch.zeros(128, kvh * hd, dtype=torch.float16), torch.zeros(64, 2, dtype=torch.uint8))
+    kc = torch.zeros(kvh, hd, S, dtype=torch.float16)
+    rope = torch.zeros(S, hd // 2, dtype=torch.complex64)
+    kw = dict(q_out=torch.zeros(1, 2 * kvh * hd, dtype=torch.float16), k_cache_t=kc, pos=torch.zeros(1, dtype=torch.long),
+              rope_table=rope, head_dim=hd)
+    rows, cols = torch.zeros(kvh, S, hd, dtype=torch.float16), torch.zeros(kvh, hd, S, dtype=torch.float16)
+    for bad in (dict(), dict(v_cache=rows, v_cache_t=cols), dict(v_cache=cols), dict(v_cache_t=rows)):
+        with pytest.raises(ValueError):
+            hip_spmv.nmsparse_qkv_decode(x, mat, mat, mat, 2, 4, **kw, **bad)
+
+
 # ---------------------------------------------------------------------------
 # the custom op
 # ---------------------------------------------------------------------------

@@ -254,6 +254,14 @@ def test_greedy_token_matches_argmax_with_ties(V):
         assert int(greedy_token(logits)) == int(torch.argmax(logits, dim=-1)), (V, trial)
 
 
+def test_cache_length_rounds_up_to_the_alignment():
+    from spmv_decode_amd.decode.runner import CACHE_ALIGN, cache_length
+
+    assert CACHE_ALIGN == 128
+    assert [cache_length(n) for n in (1, 127, 128, 129, 384, 392, 1024, 1032)] == \
+        [128, 128, 128, 256, 384, 512, 1024, 1152]
+
+
 @pytest.mark.gpu
 def test_greedy_token_in_a_captured_graph(gpu):
     """The two-stage greedy argmax at Llama-3.1's vocabulary, captured in a
