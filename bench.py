@@ -135,6 +135,7 @@ def main():
         hip_spmv.nmsparse_gate_up_silu(xs[4096], lay["gate_proj"], lay["up_proj"], nnz, m, out=act)
         gemv("down_proj", li)
 
+    from spmv_decode_amd.decode.model import KEY_PAD
     from spmv_decode_amd.hip_spmv import GemvProblem
     from spmv_decode_amd.microbench import DECODE_CLASSES, decode_form_bytes
 
@@ -142,9 +143,10 @@ def main():
     S = 512
     x_res = torch.randn(1, 4096, generator=gen, device=dev).to(torch.float16)
     attn = torch.randn(1, 4096, generator=gen, device=dev).to(torch.float16)
-    h1, h2, qo = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(3))
+    h1, h2 = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(2))
+    qo = torch.zeros(32, 128 + KEY_PAD, dtype=torch.float16, device=dev)  # the decoder's query rows
     ln1, ln2 = ((torch.rand(4096, generator=gen, device=dev) + 0.5).to(torch.float16) for _ in range(2))
-    kcs = [torch.zeros(8, 128, S, dtype=torch.float16, device=dev) for _ in range(L)]
+    kcs = [torch.zeros(8, 128 + KEY_PAD, S, dtype=torch.float16, device=dev) for _ in range(L)]
     vcs = [torch.zeros(8, 128, S, dtype=torch.float16, device=dev) for _ in range(L)]
     ang = torch.outer(torch.arange(S, dtype=torch.float64),
                       1.0 / (500000.0 ** (torch.arange(64, dtype=torch.float64) * 2.0 / 128)))
@@ -205,7 +207,7 @@ def main():
     value = decode_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode-form step ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
-    written = [act, qo, h1, h2, kcs[0][:, :, S // 2], vcs[0][:, S // 2]]
+    written = [act, qo, h1, h2, kcs[0][:, :, S // 2], vcs[0][:, :, S // 2]]
     if not all(bool(torch.isfinite(o.float()).all()) for o in written):
         raise RuntimeError("non-finite GEMV output")
     ms_plain = time_step(lambda: [fused_layer(li) for li in range(L)])

@@ -13,7 +13,12 @@ Keys and values are cached transposed, [kv_heads, head_dim, S]: the score
 product then reads contiguous rows of keys, and the probability-times-values
 product takes the values as a transposed operand, which the BLAS library runs
 faster at these shapes (MI355X, S = 384: 6.6 µs against 8.2 µs for a
-[kv_heads, S, head_dim] cache; S = 1024: 4.3 µs against 12-16 µs).
+[kv_heads, S, head_dim] cache; S = 1024: 4.3 µs against 12-16 µs). The causal
+mask lives in the key cache: each head has KEY_PAD extra rows, the first of
+them holding the additive mask (0 at positions <= pos, -inf after), and the
+query buffer holds a 1 in that column, so one plain batched product yields the
+masked scores (an additive mask operand makes PyTorch copy it into the output
+before the product: one more kernel per layer and a slower GEMM).
 
 Numerics follow the published architectures: RMSNorm in fp32 (one fused
 `F.rms_norm` kernel), rotary embeddings on interleaved (even, odd) pairs as a
@@ -26,7 +31,7 @@ before the rotary embedding.
 A step is written for few kernel launches, since at batch 1 every small
 kernel costs a few microseconds: the q/k/v projections write into slices of
 one buffer, so the rotary embedding runs once over queries and keys; the
-attention scale and causal mask are folded into one batched multiply-add.
+attention scale and causal mask are folded into one batched product.
 
 When every projection of every layer is an `NmSparseLinear` (after
 `swap_to_nmsparse`), `forward_step` runs the fused layer instead
@@ -114,6 +119,24 @@ def rotate(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
     return torch.view_as_real(xc * freqs).flatten(-2).to(x.dtype)
 
 
+KEY_PAD = 8  # rows per head after head_dim in the key cache (and columns in the query buffer)
+
+
+def attend(q_pad: torch.Tensor, k_cache_t: torch.Tensor, v_cache_t: torch.Tensor, cfg: "DecoderConfig",
+           zero: torch.Tensor) -> torch.Tensor:
+    """softmax(q k / sqrt(head_dim) + mask) v for one decode token, grouped
+    query heads. q_pad [n_heads, head_dim + KEY_PAD]: the query, then 1, then
+    zeros; k_cache_t [kv_heads, head_dim + KEY_PAD, S]: the keys, then the
+    additive mask row, then zero rows; v_cache_t [kv_heads, head_dim, S]; zero:
+    a 0-dim tensor (the product's ignored addend). Returns [kv_heads, g,
+    head_dim] with g = n_heads / kv_heads, contiguous."""
+    kvh = cfg.n_kv_heads
+    scores = torch.baddbmm(zero, q_pad.view(kvh, cfg.n_heads // kvh, q_pad.shape[1]), k_cache_t, beta=0.0,
+                           alpha=1.0 / math.sqrt(cfg.head_dim))
+    probs = torch.softmax(scores, dim=-1)  # fp16 in/out, fp32 inside
+    return torch.bmm(probs, v_cache_t.transpose(1, 2))
+
+
 def linear_into(lin: nn.Module, x2d: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
     """y = lin(x) written into `out` ([1, h] contiguous slice): the sparse GEMV's
     `out=` for NmSparseLinear, torch.mm (hipBLASLt) for a dense nn.Linear, the
@@ -156,10 +179,11 @@ class Attention(nn.Module):
             self.q_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
             self.k_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
 
-    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, mask):
-        """x [1, 1, dim]; freqs complex64 [1, head_dim/2]; k_cache_t and v_cache_t
-        [kvh, head_dim, S] (keys and values both stored transposed); pos [1]
-        int64; mask [S] additive (0 / -inf) in the activation dtype."""
+    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
+        """x [1, 1, dim]; freqs complex64 [1, head_dim/2]; k_cache_t [kvh,
+        head_dim + KEY_PAD, S] and v_cache_t [kvh, head_dim, S] (see attend);
+        pos [1] int64; q_pad [n_heads, head_dim + KEY_PAD] query buffer; zero a
+        0-dim tensor."""
         c = self.cfg
         g = c.n_heads // c.n_kv_heads
         qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
@@ -181,12 +205,10 @@ class Attention(nn.Module):
         qk = rotate(qk, freqs)
         q, k = qk[:c.n_heads], qk[c.n_heads:]
         v = qkv[0, qd + kvd:].view(c.n_kv_heads, c.head_dim, 1)
-        k_cache_t.index_copy_(2, pos, k.unsqueeze(-1))
+        q_pad[:, :c.head_dim].copy_(q)
+        k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
         v_cache_t.index_copy_(2, pos, v)
-        scores = torch.baddbmm(mask.expand(c.n_kv_heads, g, -1), q.view(c.n_kv_heads, g, c.head_dim), k_cache_t,
-                               alpha=1.0 / math.sqrt(c.head_dim))
-        probs = torch.softmax(scores, dim=-1)  # fp16 in/out, fp32 inside
-        y = torch.bmm(probs, v_cache_t.transpose(1, 2))  # [kvh, g, head_dim]
+        y = attend(q_pad, k_cache_t, v_cache_t, c, zero)  # [kvh, g, head_dim]
         return self.o_proj(y.view(1, 1, qd))
 
 
@@ -218,8 +240,8 @@ class Block(nn.Module):
         self.post_attention_layernorm = RMSNorm(cfg.dim, cfg.norm_eps)
         self.mlp = MLP(cfg)
 
-    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, mask):
-        h = x + self.self_attn(self.input_layernorm(x), freqs, k_cache_t, v_cache_t, pos, mask)
+    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
+        h = x + self.self_attn(self.input_layernorm(x), freqs, k_cache_t, v_cache_t, pos, q_pad, zero)
         return h + self.mlp(self.post_attention_layernorm(h))
 
 
@@ -233,27 +255,23 @@ def fusable(block: Block) -> bool:
             and isinstance(at.o_proj, NmSparseLinear) and isinstance(mlp.down_proj, NmSparseLinear))
 
 
-def fused_block_step(blk: Block, x2d, k_cache_t, v_cache_t, pos, mask, rope):
+def fused_block_step(blk: Block, x2d, k_cache_t, v_cache_t, pos, q_pad, zero, rope):
     """One fused sparse layer on the residual stream x2d [1, dim], updated in
-    place. rope: complex64 [S, head_dim/2] table of the cache's positions."""
+    place. rope: complex64 [S, head_dim/2] table of the cache's positions;
+    caches, q_pad and zero as in attend."""
     from ..hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
 
     at, mlp = blk.self_attn, blk.mlp
     c = at.cfg
-    g = c.n_heads // c.n_kv_heads
     qd = c.n_heads * c.head_dim
-    q = torch.empty(1, qd, dtype=x2d.dtype, device=x2d.device)
     ln1, ln2 = blk.input_layernorm, blk.post_attention_layernorm
     qp, kp, vp = at.q_proj, at.k_proj, at.v_proj
     nmsparse_qkv_decode(x2d, (qp.mat_data, qp.mat_index), (kp.mat_data, kp.mat_index), (vp.mat_data, vp.mat_index),
-                        qp.block_width, qp.vec_width, q_out=q, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
+                        qp.block_width, qp.vec_width, q_out=q_pad, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
                         rope_table=rope, head_dim=c.head_dim, norm=(ln1.weight, ln1.eps),
                         q_norm=at.q_norm.weight if c.qk_norm else None,
                         k_norm=at.k_norm.weight if c.qk_norm else None, head_eps=c.norm_eps)
-    scores = torch.baddbmm(mask.expand(c.n_kv_heads, g, -1), q.view(c.n_kv_heads, g, c.head_dim), k_cache_t,
-                           alpha=1.0 / math.sqrt(c.head_dim))
-    probs = torch.softmax(scores, dim=-1)
-    y = torch.bmm(probs, v_cache_t.transpose(1, 2)).view(1, qd)
+    y = attend(q_pad, k_cache_t, v_cache_t, c, zero).view(1, qd)
     o = at.o_proj
     nmsparse_gemv_launch(y, [GemvProblem(o.mat_data, o.mat_index, x2d, residual=x2d)], o.block_width, o.vec_width)
     gp, up = mlp.gate_proj, mlp.up_proj
@@ -293,31 +311,47 @@ class Decoder(nn.Module):
             blk.self_attn.group_launches = blk.mlp.group_launches = mode != "per_linear"
 
     def setup_cache(self, max_seq: int, device, dtype=torch.float16):
+        """Static caches for max_seq positions (see attend for the layouts); the
+        key caches of all layers are views of one tensor so that one kernel per
+        step rewrites every layer's mask row."""
         c = self.cfg
         self.max_seq = max_seq
-        self.k_cache_t = [torch.zeros(c.n_kv_heads, c.head_dim, max_seq, device=device, dtype=dtype)
+        hd, D = c.head_dim, c.head_dim + KEY_PAD
+        self.k_store = torch.zeros(c.n_layers, c.n_kv_heads, D, max_seq, device=device, dtype=dtype)
+        self.k_cache_t = list(self.k_store.unbind(0))
+        self.k_mask = self.k_store[:, :, hd, :]  # [layers, kv_heads, S] view: the mask rows
+        self.v_cache_t = [torch.zeros(c.n_kv_heads, hd, max_seq, device=device, dtype=dtype)
                           for _ in range(c.n_layers)]
-        self.v_cache_t = [torch.zeros(c.n_kv_heads, c.head_dim, max_seq, device=device, dtype=dtype)
-                          for _ in range(c.n_layers)]
+        self.q_pad = torch.zeros(c.n_heads, D, device=device, dtype=dtype)
+        self.q_pad[:, hd] = 1.0
+        self.zero = torch.zeros((), device=device, dtype=dtype)
+        self.neg_inf = torch.full((), float("-inf"), device=device, dtype=dtype)
         t = torch.arange(max_seq, dtype=torch.float64)
         ang = torch.outer(t, rope_inv_freq(c))
         self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
         self.positions = torch.arange(max_seq, device=device)
-        self.mask_dtype = dtype
+
+    def reset_cache(self):
+        """Zero every cached key and value (the mask rows are rewritten by each step)."""
+        self.k_store[:, :, :self.cfg.head_dim].zero_()
+        for v in self.v_cache_t:
+            v.zero_()
 
     def forward_step(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """One decode step: token [1, 1] int64 and pos [1] int64 on the device
         -> logits [1, vocab]. No host synchronisation."""
         x = self.embed_tokens(token)  # [1, 1, dim]
-        mask = torch.where(self.positions <= pos, 0.0, float("-inf")).to(self.mask_dtype)
+        # causal mask of this step in every layer's key cache: 0 up to pos, -inf after
+        torch.where((self.positions <= pos).expand_as(self.k_mask), self.zero, self.neg_inf, out=self.k_mask)
         if self.fuse_epilogues and all(fusable(b) and b.self_attn.group_launches for b in self.layers):
             x2d = x.view(1, -1)
             for i, blk in enumerate(self.layers):
-                fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, mask, self.rope)
+                fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero,
+                                 self.rope)
             return self.lm_head(self.norm(x)).view(1, -1)
         freqs = self.rope.index_select(0, pos)
         for i, layer in enumerate(self.layers):
-            x = layer(x, freqs, self.k_cache_t[i], self.v_cache_t[i], pos, mask)
+            x = layer(x, freqs, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero)
         return self.lm_head(self.norm(x)).view(1, -1)
 
 

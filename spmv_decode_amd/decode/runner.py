@@ -107,10 +107,7 @@ class GraphDecoder:
 
     @torch.no_grad()
     def reset(self, first_token: int = 0):
-        for k in self.model.k_cache_t:
-            k.zero_()
-        for v in self.model.v_cache_t:
-            v.zero_()
+        self.model.reset_cache()
         self.pos.zero_()
         self.host_pos = 0
         self.token.fill_(first_token)

@@ -445,32 +445,42 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
     """The q/k/v projections of one decode step in one launch.
 
     q, k, v are (mat_data, mat_index) pairs sharing `vec` [1, K]. Writes the
-    rotated queries to `q_out` [1, n_heads * head_dim], the rotated keys into
-    `k_cache_t` [kv_heads, head_dim, S] at column pos and the values either
-    into `v_cache` [kv_heads, S, head_dim] at row pos or into `v_cache_t`
-    [kv_heads, head_dim, S] at column pos (exactly one of the two; the
-    decoder keeps both caches transposed). `norm` = (weight [K], eps) is the
-    layer's input RMSNorm; `q_norm` / `k_norm` ([head_dim]) are Qwen3's
+    rotated queries to `q_out`, either [1, n_heads * head_dim] or a buffer of
+    rows [n_heads, D] with D >= head_dim (head h in row h, columns past
+    head_dim untouched); the rotated keys into `k_cache_t` [kv_heads, D, S]
+    (D >= head_dim; rows past head_dim untouched) at column pos; the values
+    either into `v_cache` [kv_heads, S, head_dim] at row pos or into
+    `v_cache_t` [kv_heads, head_dim, S] at column pos (exactly one of the two;
+    the decoder keeps both caches transposed). `norm` = (weight [K], eps) is
+    the layer's input RMSNorm; `q_norm` / `k_norm` ([head_dim]) are Qwen3's
     per-head norms.
     """
-    kvh, hd, S = k_cache_t.shape
+    kvh, kd, S = k_cache_t.shape
+    hd = head_dim
+    nh = q[0].shape[1] // hd if q[0].dim() == 2 else 0
     if (v_cache is None) == (v_cache_t is None):
         raise ValueError("pass exactly one of v_cache [kv_heads, S, head_dim] and v_cache_t [kv_heads, head_dim, S]")
     if v_cache is not None:
         vc, want, v_layout = v_cache, (kvh, S, hd), (S * hd, 1, hd)
     else:
         vc, want, v_layout = v_cache_t, (kvh, hd, S), (hd * S, S, 1)
-    if hd != head_dim or tuple(vc.shape) != want:
+    if kd < hd or tuple(vc.shape) != want:
         raise ValueError(f"k_cache_t {tuple(k_cache_t.shape)} / value cache {tuple(vc.shape)} do not match "
                          f"head_dim {head_dim}")
+    if tuple(q_out.shape) == (1, nh * hd):
+        q_layout = None
+    elif q_out.dim() == 2 and q_out.shape[0] == nh and q_out.shape[1] >= hd and q_out.stride(1) == 1:
+        q_layout = (q_out.stride(0), 1, 0)
+    else:
+        raise ValueError(f"q_out {tuple(q_out.shape)} is neither [1, {nh * hd}] nor [{nh}, >= {hd}]")
     for name, (md, _), rows in (("k", k, kvh * hd), ("v", v, kvh * hd)):
         if md.shape[1] != rows:
             raise ValueError(f"{name} projection has {md.shape[1]} outputs, the cache holds {rows}")
     rt = torch.view_as_real(rope_table) if rope_table.is_complex() else rope_table
     if rt.shape[0] < S:
         raise ValueError(f"rope_table has {rt.shape[0]} positions, the cache {S}")
-    probs = [GemvProblem(q[0], q[1], q_out, head_norm=q_norm, rope=True),
-             GemvProblem(k[0], k[1], k_cache_t, head_norm=k_norm, rope=True, layout=(hd * S, S, 1)),
+    probs = [GemvProblem(q[0], q[1], q_out, head_norm=q_norm, rope=True, layout=q_layout),
+             GemvProblem(k[0], k[1], k_cache_t, head_norm=k_norm, rope=True, layout=(kd * S, S, 1)),
              GemvProblem(v[0], v[1], vc, layout=v_layout)]
     return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, norm=norm, head_dim=head_dim,
                                 head_eps=head_eps, pos=pos, rope_table=rt[:S], config_id=config_id,

@@ -29,6 +29,7 @@ from pathlib import Path
 import torch
 
 from . import _lib
+from .decode.model import KEY_PAD
 from .hip_spmv import nmsparse_spmv_forward_hip
 
 HBM_PEAK_GBS = 8000.0
@@ -224,10 +225,10 @@ class DecodeForms:
         self.h2 = torch.empty(1, dim, dtype=f16, device=device)
         self.ln1 = (torch.rand(dim, generator=g, device=device) + 0.5).to(f16)
         self.ln2 = (torch.rand(dim, generator=g, device=device) + 0.5).to(f16)
-        self.qo = torch.empty(1, qd, dtype=f16, device=device)
+        self.qo = torch.zeros(n_heads, head_dim + KEY_PAD, dtype=f16, device=device)  # the decoder's query rows
         self.pair_out = torch.empty(1, inter, dtype=f16, device=device)
         S = self.KV_SLOTS
-        self.k_cache = torch.zeros(n_kv_heads, head_dim, S, dtype=f16, device=device)
+        self.k_cache = torch.zeros(n_kv_heads, head_dim + KEY_PAD, S, dtype=f16, device=device)
         self.v_cache = torch.zeros(n_kv_heads, head_dim, S, dtype=f16, device=device)  # transposed, as the decoder
         ang = torch.outer(torch.arange(S, dtype=torch.float64),
                           1.0 / (500000.0 ** (torch.arange(head_dim // 2, dtype=torch.float64) * 2.0 / head_dim)))

@@ -105,20 +105,28 @@ def test_implementation_limits_raise_value_error():
         hip_spmv.validate_args(vec, md, mi, 128, 256, 2, 128, 4, 1, 300, require_device=False)
 
 
-def test_qkv_decode_value_cache_arguments():
-    """Exactly one value cache, of the layout its name states; checked before
-    any launch."""
+def test_qkv_decode_buffer_arguments():
+    """Exactly one value cache, of the layout its name states; queries as one
+    row or as padded head rows; keys with at least head_dim rows. Checked
+    before any launch (these CPU tensors never reach one)."""
     kvh, hd, S, K = 2, 64, 16, 256
     x = torch.zeros(1, K, dtype=torch.float16)
     mat = (torch.zeros(128, kvh * hd, dtype=torch.float16), torch.zeros(64, 2, dtype=torch.uint8))
-    kc = torch.zeros(kvh, hd, S, dtype=torch.float16)
-    rope = torch.zeros(S, hd // 2, dtype=torch.complex64)
-    kw = dict(q_out=torch.zeros(1, 2 * kvh * hd, dtype=torch.float16), k_cache_t=kc, pos=torch.zeros(1, dtype=torch.long),
-              rope_table=rope, head_dim=hd)
     rows, cols = torch.zeros(kvh, S, hd, dtype=torch.float16), torch.zeros(kvh, hd, S, dtype=torch.float16)
-    for bad in (dict(), dict(v_cache=rows, v_cache_t=cols), dict(v_cache=cols), dict(v_cache_t=rows)):
+    good = dict(q_out=torch.zeros(1, kvh * hd, dtype=torch.float16), k_cache_t=torch.zeros(kvh, hd + 8, S,
+                dtype=torch.float16), v_cache_t=cols, pos=torch.zeros(1, dtype=torch.long),
+                rope_table=torch.zeros(S, hd // 2, dtype=torch.complex64), head_dim=hd)
+    bad = [dict(v_cache_t=None), dict(v_cache=rows), dict(v_cache_t=None, v_cache=cols), dict(v_cache_t=rows),
+           dict(q_out=torch.zeros(1, kvh * hd + 8, dtype=torch.float16)),
+           dict(q_out=torch.zeros(kvh, hd - 8, dtype=torch.float16)),
+           dict(k_cache_t=torch.zeros(kvh, hd - 8, S, dtype=torch.float16))]
+    for change in bad:
         with pytest.raises(ValueError):
-            hip_spmv.nmsparse_qkv_decode(x, mat, mat, mat, 2, 4, **kw, **bad)
+            hip_spmv.nmsparse_qkv_decode(x, mat, mat, mat, 2, 4, **{**good, **change})
+    # the same arguments get past these checks to the device check of the launch
+    for q_out in (good["q_out"], torch.zeros(kvh, hd + 8, dtype=torch.float16)):
+        with pytest.raises(ValueError, match="GPU"):
+            hip_spmv.nmsparse_qkv_decode(x, mat, mat, mat, 2, 4, **{**good, "q_out": q_out})
 
 
 # ---------------------------------------------------------------------------

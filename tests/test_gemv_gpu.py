@@ -419,32 +419,37 @@ def _check_heads(got, ref, dtype, what):
     assert not bad.any(), (what, int(bad.sum()), float(np.abs(got - ref).max()))
 
 
-@pytest.mark.parametrize("v_transposed", [False, True], ids=["v_rows", "v_cols"])
+@pytest.mark.parametrize("layout", ["plain", "decoder"])
 @pytest.mark.parametrize("qk_norm", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("K,nh,kvh,hd,nnz,m", [(4096, 32, 8, 128, 32, 64), (512, 4, 2, 64, 2, 4),
                                                (5120, 40, 8, 128, 8, 16)], ids=str)
-def test_qkv_decode_rope_and_cache_write(gpu, K, nh, kvh, hd, nnz, m, dtype, qk_norm, v_transposed):
-    """Values go to a [kvh, S, hd] cache (row pos) or, as the decoder keeps
-    them, to a [kvh, hd, S] cache (column pos); the test reads both through the
-    [kvh, S, hd] view."""
+def test_qkv_decode_rope_and_cache_write(gpu, K, nh, kvh, hd, nnz, m, dtype, qk_norm, layout):
+    """plain: q_out [1, nh*hd], keys [kvh, hd, S], values [kvh, S, hd] (row pos).
+    decoder: the decoder's buffers, q_out rows [nh, hd + 8] and keys
+    [kvh, hd + 8, S] whose extra columns / rows must stay untouched, values
+    [kvh, hd, S] (column pos). Values are read through a [kvh, S, hd] view."""
     from spmv_decode_amd.hip_spmv import nmsparse_qkv_decode
 
-    S = 48
+    S, pad = 48, 8
     x, q, k, v, lnw, qn, kn, ang, rope, kc, vc = _qkv_case(K, nh, kvh, hd, S, nnz, m, dtype, seed=K + nh)
+    if layout == "decoder":
+        g = torch.Generator(device="cuda").manual_seed(K)
+        kc = torch.cat([kc, torch.randn(kvh, pad, S, generator=g, device="cuda").to(dtype)], dim=1)
     for pos_v, cfg, splits in ((0, -1, 0), (37, -1, 0), (S - 1, 3, 3), (5, 1, 1)):
-        say(f"qkv decode {dtype} K{K} {nh}/{kvh}x{hd} {nnz}:{m} qk_norm {qk_norm} v_t {v_transposed} pos {pos_v} "
-            f"cfg {cfg}")
+        say(f"qkv decode {dtype} K{K} {nh}/{kvh}x{hd} {nnz}:{m} qk_norm {qk_norm} {layout} pos {pos_v} cfg {cfg}")
         kc1 = kc.clone()
-        if v_transposed:
+        if layout == "decoder":
             vct = vc.transpose(1, 2).contiguous()
             vkw, vc1 = dict(v_cache_t=vct), vct.transpose(1, 2)
+            qbuf = torch.full((nh, hd + pad), 3.0, device="cuda", dtype=dtype)
+            qo = qbuf[:, :hd]
         else:
             vc1 = vc.clone()
             vkw = dict(v_cache=vc1)
-        qo = torch.empty(1, nh * hd, device="cuda", dtype=dtype)
+            qbuf = qo = torch.empty(1, nh * hd, device="cuda", dtype=dtype)
         pos = torch.tensor([pos_v], device="cuda")
-        nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qo, k_cache_t=kc1, **vkw, pos=pos, rope_table=rope,
+        nmsparse_qkv_decode(x, q, k, v, nnz, m, q_out=qbuf, k_cache_t=kc1, **vkw, pos=pos, rope_table=rope,
                             head_dim=hd, norm=(lnw, 1e-5), q_norm=qn if qk_norm else None,
                             k_norm=kn if qk_norm else None, head_eps=1e-6, config_id=cfg, splits=splits)
         rq, rk, rv = O.qkv_decode_f64(x.cpu().reshape(-1), (q[0].cpu(), q[1].cpu()), (k[0].cpu(), k[1].cpu()),
@@ -452,13 +457,16 @@ def test_qkv_decode_rope_and_cache_write(gpu, K, nh, kvh, hd, nnz, m, dtype, qk_
                                       norm=(lnw.cpu(), 1e-5), q_norm=qn.cpu() if qk_norm else None,
                                       k_norm=kn.cpu() if qk_norm else None, eps=1e-6)
         _check_heads(qo, rq, dtype, "q")
-        _check_heads(kc1[:, :, pos_v], rk, dtype, "k")
+        _check_heads(kc1[:, :hd, pos_v], rk, dtype, "k")
         _check_heads(vc1[:, pos_v, :], rv, dtype, "v")
-        # every other cache slot is untouched, bit for bit
+        # every other cache slot, and the padding, is untouched, bit for bit
         km = torch.ones(S, dtype=torch.bool)
         km[pos_v] = False
         assert torch.equal(kc1[:, :, km.cuda()], kc[:, :, km.cuda()])
+        assert torch.equal(kc1[:, hd:], kc[:, hd:])
         assert torch.equal(vc1[:, km.cuda(), :], vc[:, km.cuda(), :])
+        if layout == "decoder":
+            assert bool((qbuf[:, hd:] == 3.0).all())
     # a position outside the cache stores nothing at all
     kc1, vc1 = kc.clone(), vc.clone()
     qo = torch.full((1, nh * hd), 7.0, device="cuda", dtype=dtype)
