@@ -58,20 +58,51 @@ int validate_shape(int h, int w, int nnz, int m) {
   return NM_OK;
 }
 
-// The library's own choice of configuration, from rocprof / hipGraph sweeps on
-// MI355X at the Llama-3.1-8B decode shapes: 256-row tiles for wide outputs,
-// 128-row tiles otherwise (h_total: summed output width of the launch).
-int auto_config(int h_total, int nmat) {
-  if (nmat == 2) return h_total >= 8192 ? 1 : 0;
-  return h_total >= 8192 ? 3 : 1;
+// The library's own choice of configuration and split count, from hipGraph
+// sweeps of the decoder's launches on MI355X at the Llama-3.1-8B, Qwen3-14B and
+// Qwen3-32B shapes (h_total: summed output width of the launch). Single
+// matrix: 128-row tiles up to 4096 outputs, 256-row tiles beyond. Gate/up
+// pair: 256-row tiles with 32-row chunks up to 14336 outputs, 64-row chunks
+// beyond.
+int auto_config(long long h_total, int nmat) {
+  if (nmat == 2) return h_total > 14336 ? 3 : 1;
+  return h_total > 4096 ? 3 : 1;
 }
 
-// Default split count: about 8 splits of the compressed columns per tile. The
-// sweeps show the cost of a split-K handoff (one partial publish, one arrival
-// atomic on a per-tile counter, one reduction) grows faster with the split
-// count than the extra parallelism pays back; 8 splits of 256+ columns keep
-// 64-900 workgroups streaming for every decode shape.
-constexpr int kDefaultSplits = 8;
+// Workgroups that run at once, one per CU: an MI355X has 256 CUs. The split
+// count below is chosen for this many; it changes speed only, never results.
+constexpr int kPlanCUs = 256;
+
+// Default split count. About 8 splits of the compressed columns per tile: the
+// cost of a split-K handoff (one partial publish, one arrival atomic on a
+// per-tile counter, one reduction) grows with the split count faster than
+// the extra parallelism pays back. Two corrections from the sweeps:
+//  * a single matrix with long columns (w >= 6144) and few tiles takes up to
+//    12 splits while the grid still fits one workgroup per CU;
+//  * a grid of more workgroups than CUs whose last round is mostly empty
+//    (e.g. 320 = 1.25 rounds) waits for the few CUs that run two: then the
+//    split count nearest 8 whose rounds are fullest is taken.
+// `eff(s)` is the number of splits a request for s splits gets once the rows
+// per split are rounded to whole chunks.
+template <class EffSplits>
+int auto_splits(int tiles, int w, int nmat, EffSplits eff) {
+  auto balance = [&](int s) {
+    const double rounds = (double)tiles * eff(s) / kPlanCUs;
+    return rounds <= 1.0 ? 1.0 : rounds / ceil(rounds);
+  };
+  if (nmat == 1 && w >= 6144 && tiles * 8 <= kPlanCUs) return max(8, min(12, kPlanCUs / tiles));
+  int best = 8;
+  double best_balance = balance(8);
+  if (best_balance >= 0.8) return best;
+  for (int s : {7, 9, 6, 10, 5, 11, 4, 12}) {  // nearest to 8 first; ties keep the nearer
+    const double b = balance(s);
+    if (b > best_balance + 1e-9) {
+      best = s;
+      best_balance = b;
+    }
+  }
+  return best;
+}
 
 // Plan a launch of `nprob` problems (widths hs[]) sharing w, nnz, m, with
 // `nmat` matrices per workgroup. The workspace holds the counters of every
@@ -87,16 +118,23 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
     h_total += hs[i];
   }
   const int ncfg = nmat == 2 ? kNumDualConfigs : kNumConfigs;
-  if (cfg < 0) cfg = auto_config((int)(h_total > 0x7fffffff ? 0x7fffffff : h_total), nmat);
+  if (cfg < 0) cfg = auto_config(h_total, nmat);
   if (cfg >= ncfg) return NM_ERR_BAD_CONFIG;
   const Config& c = nmat == 2 ? kDualConfigs[cfg] : kConfigs[cfg];
   const int HT = c.th * kVec;
   const int CH = (kBlock / c.th) * c.u;
-  if (splits <= 0) splits = kDefaultSplits;
-  if (splits > w) splits = w;
-  int rows = ceil_div(ceil_div(w, splits), CH) * CH;
-  if (rows > max_rows) rows = max_rows;
-  if (rows < CH) rows = CH;
+  auto rows_for = [&](int s) {
+    if (s > w) s = w;
+    int r = ceil_div(ceil_div(w, s), CH) * CH;
+    if (r > max_rows) r = max_rows;
+    return r < CH ? CH : r;
+  };
+  if (splits <= 0) {
+    int tiles = 0;
+    for (int i = 0; i < nprob; ++i) tiles += ceil_div(hs[i], HT);
+    splits = auto_splits(tiles, w, nmat, [&](int s) { return ceil_div(w, rows_for(s)); });
+  }
+  const int rows = rows_for(splits);
   splits = ceil_div(w, rows);
   p->cfg = cfg;
   p->splits = splits;

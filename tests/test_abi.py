@@ -138,7 +138,7 @@ def test_grouped_and_pair_rejections_before_launch():
     assert lib.nm_gemv_grouped(0, FAKE, 1, n, ptrs, ptrs, ptrs, hs, FAKE, 1024, 2048, 32, 64, -1, 0, None) == -6
     need = lib.nm_gemv_grouped_workspace_bytes(n, hs, 2048, 32, 64, -1, 0)
     one = sum(lib.nm_gemv_workspace_bytes_ex(h, 2048, 32, 64, 1, 0) - _lib.NM_TICKET_BYTES for h in (4096, 1024, 1024))
-    assert need == _lib.NM_TICKET_BYTES + one  # same config (h_total < 8192 -> th16_u8), 8 splits each
+    assert need == _lib.NM_TICKET_BYTES + one  # 8 splits each, as alone
     # the gate/up pair
     args = (0, FAKE, 1, FAKE, FAKE, FAKE, FAKE, FAKE, FAKE, 1 << 30, 14336, 2048, 32, 64)
     assert lib.nm_gemv_gate_up_silu(*args[:3], None, *args[4:], -1, 0, None) == -1
@@ -216,8 +216,8 @@ def test_launch_descriptor_rejections_before_launch():
     d.pos, d.pos_limit = FAKE, 16
     assert _launch(d) == -8                               # no rope table
     d.config_id = 9                                       # tile 2048 rows, fine for head_dim 128
-    e = _desc(config_id=-1, head_dim=256)
-    e.prob[1].head_norm = FAKE                            # h = 1024, th16 tile of 128 rows < head_dim
+    e = _desc(config_id=1, head_dim=256)
+    e.prob[1].head_norm = FAKE                            # th16: a tile of 128 rows < head_dim
     assert _launch(e) == -8
     p = _desc(kind=1, nprob=2, hs=(14336, 14336))
     p.prob[0].pos_stride, p.head_dim = 1, 128
@@ -266,12 +266,22 @@ def test_launch_plan_query():
     def mats(K, h):
         return torch.empty(K // 64 * 32, h, dtype=torch.float16), torch.empty(K // 64, 32, dtype=torch.uint8)
 
+    def summary(p):
+        return p["config_id"], p["splits"], p["blocks"]
+
+    # Llama-3.1-8B: 256-row tiles past 4096 outputs, 8 splits
     qkv = [mats(4096, 4096), mats(4096, 1024), mats(4096, 1024)]
     p = launch_plan(qkv, 32, 64)
-    assert p == {"config_id": 1, "splits": 8, "blocks": (32 + 8 + 8) * 8, "rows_per_split": 256, "chunk_rows": 128}
+    assert p == {"config_id": 3, "splits": 8, "blocks": (16 + 4 + 4) * 8, "rows_per_split": 256, "chunk_rows": 64}
     pair = launch_plan([mats(4096, 14336), mats(4096, 14336)], 32, 64, gate_up=True)
     assert pair["config_id"] == 1 and pair["chunk_rows"] == 32 and pair["blocks"] == 56 * 8
     down = launch_plan([mats(14336, 4096)], 32, 64)
-    assert down["rows_per_split"] == 896 and down["chunk_rows"] == 128
+    assert down["rows_per_split"] == 896 and down["chunk_rows"] == 128 and down["blocks"] == 256
+    # Qwen3 shapes: long columns take up to 12 splits while the grid fits one
+    # workgroup per CU; grids whose last round of workgroups would be mostly
+    # empty take the split count (nearest 8) that fills their rounds best
+    assert summary(launch_plan([mats(17408, 5120)], 32, 64)) == (3, 12, 20 * 12)
+    assert summary(launch_plan([mats(5120, 8192), mats(5120, 1024), mats(5120, 1024)], 32, 64)) == (3, 6, 40 * 6)
+    assert summary(launch_plan([mats(5120, 25600), mats(5120, 25600)], 32, 64, gate_up=True)) == (3, 10, 100 * 10)
     with pytest.raises(_lib.NmSparseLibraryError):
         launch_plan([mats(4096, 1000)], 32, 64)
