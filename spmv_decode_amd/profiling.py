@@ -145,6 +145,62 @@ def stats(stats_csv, bench_json, md_path, cmd):
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 
+def decode_stats(stats_csv, decode_json, md_path, cmd):
+    """Per-token kernel time of a hipGraph decode run from its rocprofv3 stats."""
+    from .decode.model import CONFIGS
+
+    rows = _read(stats_csv)
+    d = json.loads(Path(decode_json).read_text())
+    layers = CONFIGS[d["model"]].n_layers
+    pair = [r for r in rows if ", true, 2, " in r["Name"]]
+    steps = int(pair[0]["Calls"]) // layers  # one gate/up launch per layer and step
+
+    def kind(r):
+        n, per_step = r["Name"], int(r["Calls"]) / steps
+        if per_step < 0.9:
+            return None  # model set-up (random init, packing), not part of a step
+        if "nm_gemv_kernel" in n:
+            if ", 2, " in n:
+                return "sparse GEMV: gate/up pair + RMSNorm + SiLU*mul"
+            return "sparse GEMV: q/k/v + RMSNorm + RoPE + cache write" if n.rstrip().endswith(
+                "true>(nm_hip::Args)") else "sparse GEMV: o or down + residual"
+        if n.startswith("Cijk_"):
+            return "attention product (hipBLASLt)" if per_step > 1.5 else "lm_head (hipBLASLt, dense)"
+        if "softmax" in n:
+            return "attention softmax"
+        return "other (embedding, norm, mask, greedy token, position)"
+
+    per = {}
+    rows = [r for r in rows if kind(r) is not None]
+    for r in rows:
+        c = kind(r)
+        per[c] = per.get(c, 0.0) + float(r["TotalDurationNs"]) / steps / 1e3
+    total = sum(per.values())
+    sp = d["sparse"]
+    lines = [f"# rocprofv3 kernel statistics: hipGraph decode, {d['model']} {sp.get('ratio', '')}, fp16, batch 1", "",
+             "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd,
+             "python -m spmv_decode_amd.profiling decode-stats --csv <stats csv> --decode <json> --command '<the line "
+             "above>' --md <this file>",
+             "```", "",
+             f"{steps} decode steps were profiled (capture warm-up, the {d['prompt']}-token prompt and {d['gen']}",
+             "generated tokens, one graph replay each). Kernel time per step, summed by role: rocprof durations of",
+             "the kernels only (the graph's inter-kernel gaps are not included; the model's set-up kernels are",
+             "left out):", "",
+             "| Role | us per step | Share |", "|---|---|---|"]
+    for c, v in sorted(per.items(), key=lambda kv: -kv[1]):
+        lines.append(f"| {c} | {v:.1f} | {100 * v / total:.1f}% |")
+    lines += [f"| total kernel time | {total:.1f} | |", "",
+              f"The profiled run itself measured {sp['ms_per_token']} ms/token (HIP events around the replays,",
+              "under the profiler).", "",
+              "| Kernel | Calls | Avg (us) | Per step (us) |", "|---|---|---|---|"]
+    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
+        n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
+        n = n if len(n) <= 90 else n[:87] + "..."
+        lines.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                     f"{float(r['TotalDurationNs']) / steps / 1e3:.2f} |")
+    Path(md_path).write_text("\n".join(lines) + "\n")
+
+
 def cpu(bench_json, md_path, cmd):
     """CPU baseline summary from a `bench.py --cpu-detail --cpu-decode` JSON line."""
     b = json.loads(Path(bench_json).read_text())
@@ -190,6 +246,12 @@ def main(argv=None):
     s.add_argument("--csv", required=True)
     s.add_argument("--bench", default=None)
     s.add_argument("--md", required=True)
+    ds = sub.add_parser("decode-stats")
+    ds.add_argument("--csv", required=True)
+    ds.add_argument("--decode", required=True)
+    ds.add_argument("--md", required=True)
+    ds.add_argument("--command", dest="command_line", required=True,
+                    help="the rocprofv3 command line the stats come from")
     a = p.parse_args(argv)
     if a.cmd == "traffic":
         traffic(a.fetch, a.write, a.md, a.json,
@@ -197,6 +259,8 @@ def main(argv=None):
                 "python -u -m spmv_decode_amd.microbench --traffic-probe",
                 "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc --output-format csv -- "
                 "python -u -m spmv_decode_amd.microbench --traffic-probe")
+    elif a.cmd == "decode-stats":
+        decode_stats(a.csv, a.decode, a.md, a.command_line)
     elif a.cmd == "cpu":
         cpu(a.bench, a.md, "python -u bench.py --cpu-detail --cpu-decode > gpurun_out/bench_cpu.json")
     else:
