@@ -81,7 +81,8 @@ constexpr int kPlanCUs = 256;
 //    12 splits while the grid still fits one workgroup per CU;
 //  * a grid of more workgroups than CUs whose last round is mostly empty
 //    (e.g. 320 = 1.25 rounds) waits for the few CUs that run two: then the
-//    split count nearest 8 whose rounds are fullest is taken.
+//    split count in 9..12 whose rounds are fullest is taken, or, when none
+//    fills 80% of its last round, the one in 4..12 that does best.
 // `eff(s)` is the number of splits a request for s splits gets once the rows
 // per split are rounded to whole chunks.
 template <class EffSplits>
@@ -90,17 +91,23 @@ int auto_splits(int tiles, int w, int nmat, EffSplits eff) {
     const double rounds = (double)tiles * eff(s) / kPlanCUs;
     return rounds <= 1.0 ? 1.0 : rounds / ceil(rounds);
   };
-  if (nmat == 1 && w >= 6144 && tiles * 8 <= kPlanCUs) return max(8, min(12, kPlanCUs / tiles));
+  if (nmat == 1 && w >= 6144) {
+    for (int s = 12; s >= 8; --s)
+      if ((long long)tiles * eff(s) <= kPlanCUs) return s;
+  }
   int best = 8;
   double best_balance = balance(8);
   if (best_balance >= 0.8) return best;
-  for (int s : {7, 9, 6, 10, 5, 11, 4, 12}) {  // nearest to 8 first; ties keep the nearer
+  auto consider = [&](int s) {
     const double b = balance(s);
     if (b > best_balance + 1e-9) {
       best = s;
       best_balance = b;
     }
-  }
+  };
+  for (int s = 9; s <= 12; ++s) consider(s);  // ties keep the smaller count
+  if (best_balance >= 0.8) return best;
+  for (int s = 7; s >= 4; --s) consider(s);   // ties keep the larger count
   return best;
 }
 
@@ -308,7 +315,11 @@ int make_spmm_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits,
   if (cfg < 0) {
     const int rc = validate_shape(h, w, nnz, m);
     if (rc != NM_OK) return rc;
-    const bool wide = h >= 8192;
+    // 256-row tiles past 4096 outputs, as the GEMV, except for short columns
+    // at batch > 2 below 8192 outputs; 8-row chunks per lane at batch <= 2, 4
+    // above (the FMA work per loaded word grows with the batch). From sweeps
+    // at the Llama-3.1-8B and Qwen3-14B shapes.
+    const bool wide = h >= 8192 || (h > 4096 && (w >= 6144 || batch <= 2));
     const bool u8 = batch <= 2;
     cfg = (wide ? 2 : 0) + (u8 ? 1 : 0);  // th16_u4, th16_u8, th32_u4, th32_u8
   }
