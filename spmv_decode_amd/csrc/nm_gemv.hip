@@ -61,12 +61,12 @@ int validate_shape(int h, int w, int nnz, int m) {
 // The library's own choice of configuration and split count, from hipGraph
 // sweeps of the decoder's launches on MI355X at the Llama-3.1-8B, Qwen3-14B and
 // Qwen3-32B shapes (h_total: summed output width of the launch). Single
-// matrix: 128-row tiles up to 4096 outputs, 256-row tiles beyond. Gate/up
-// pair: 256-row tiles with 32-row chunks up to 14336 outputs, 64-row chunks
-// beyond.
+// matrix: 128-row tiles up to 4096 outputs, 256-row tiles up to 16384,
+// 512-row tiles beyond. Gate/up pair: 256-row tiles with 32-row chunks up to
+// 14336 outputs, 512-row tiles with 32-row chunks beyond.
 int auto_config(long long h_total, int nmat) {
-  if (nmat == 2) return h_total > 14336 ? 3 : 1;
-  return h_total > 4096 ? 3 : 1;
+  if (nmat == 2) return h_total > 14336 ? 5 : 1;
+  return h_total > 16384 ? 6 : (h_total > 4096 ? 3 : 1);
 }
 
 // Workgroups that run at once, one per CU: an MI355X has 256 CUs. The split

@@ -972,7 +972,9 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_kernel(SpmmArgs a) {
   X(16, 4, true)   /* 0: tile 128, chunk 64 */                                    \
   X(32, 4, true)   /* 1: tile 256, chunk 32 */                                    \
   X(16, 8, true)   /* 2: tile 128, chunk 128 */                                   \
-  X(32, 8, true)   /* 3: tile 256, chunk 64 */
+  X(32, 8, true)   /* 3: tile 256, chunk 64 */                                    \
+  X(64, 4, true)   /* 4: tile 512, chunk 16 */                                    \
+  X(64, 8, true)   /* 5: tile 512, chunk 32 */
 
 #define NM_COUNT_CONFIG(TH, U, NT) +1
 constexpr int kNumConfigs = 0 NM_PLAIN_CONFIGS(NM_COUNT_CONFIG);

@@ -282,6 +282,8 @@ def test_launch_plan_query():
     # empty take the split count (nearest 8) that fills their rounds best
     assert summary(launch_plan([mats(17408, 5120)], 32, 64)) == (3, 12, 20 * 12)
     assert summary(launch_plan([mats(5120, 8192), mats(5120, 1024), mats(5120, 1024)], 32, 64)) == (3, 6, 40 * 6)
-    assert summary(launch_plan([mats(5120, 25600), mats(5120, 25600)], 32, 64, gate_up=True)) == (3, 10, 100 * 10)
+    # the widest launches take 512-row tiles
+    assert summary(launch_plan([mats(5120, 25600), mats(5120, 25600)], 32, 64, gate_up=True)) == (5, 10, 50 * 10)
+    assert summary(launch_plan([mats(5120, 17408)], 32, 64)) == (6, 7, 34 * 7)
     with pytest.raises(_lib.NmSparseLibraryError):
         launch_plan([mats(4096, 1000)], 32, 64)
