@@ -28,11 +28,13 @@ Contents and what pins each function (tests/test_oracle.py):
   fixtures in tests/golden/, written by importing the reference.
 * `nm_oracle.error_metrics`: max_abs, mean_abs, rmse, rel_l2
   (microbench_triton_torchmv.py:408-423). Pinned against hand-computed values.
-* `nm_oracle.expected_exception`: the reference wrapper's and op's argument
-  checks (triton_spmv.py:245-283, src/spmv/nmsparse_op.py:83-86).
-  **Parity unpinned**: the reference wrapper rejects non-CUDA tensors first
-  (triton_spmv.py:245-246) and cannot run without an NVIDIA GPU, so this
-  restatement is checked only by reading.
+* `nm_oracle.expected_exception`: the reference wrapper's argument checks
+  (triton_spmv.py:245-294). Pinned against tests/golden/wrapper_validation.json:
+  the exception type and message the reference wrapper itself raised for 35
+  calls (each check failing alone, valid calls, and pairs of faults that fix
+  the order), written by tests/golden/make_validation_golden.py with the
+  reference imported in the development container (CPU tensors reporting
+  is_cuda, the Triton launch stubbed).
 * `c_oracle` (ctypes binding of oracle/nm_gemv_ref.c): the same GEMV in plain
   C with fp32 FMA in the reference's in-program order and software
   fp16/bf16 conversions. Pinned by exhaustive conversion checks against

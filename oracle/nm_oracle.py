@@ -238,7 +238,7 @@ def error_metrics(ref, out) -> dict:
 
 
 # ---------------------------------------------------------------------------
-# Argument checks of the reference wrapper and op (parity unpinned)
+# Argument checks of the reference wrapper (pinned by tests/golden/wrapper_validation.json)
 # ---------------------------------------------------------------------------
 def expected_exception(spec: dict):
     """Exception type the reference raises for a call described by `spec`, or None.

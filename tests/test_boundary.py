@@ -86,6 +86,48 @@ def test_validation_matches_reference_order(name):
             hip_spmv.validate_args(*args, require_device=False)
 
 
+def _fixture_spec(spec):
+    spec = dict(spec)
+    for k in ("vec_dtype", "mat_dtype", "index_dtype"):
+        spec[k] = getattr(torch, spec[k])
+    return spec
+
+
+WRAPPER_CASES = json.loads((GOLDEN / "wrapper_validation.json").read_text())["cases"]
+
+
+@pytest.mark.parametrize("name", sorted(WRAPPER_CASES))
+def test_validation_matches_reference_fixture(name):
+    """The oracle's restatement and the product's checks against what the
+    reference wrapper raised for the same call (tests/golden/
+    make_validation_golden.py): same exception type, and the same message
+    except where this build differs on purpose (a device check that names
+    HIP, and `arch` also accepting "gfx950")."""
+    case = WRAPPER_CASES[name]
+    spec = _fixture_spec(case["spec"])
+    want = case["raises"]
+    got = O.expected_exception(spec)
+    assert (got.__name__ if got else None) == want
+    vec, md, mi = _spec_tensors(spec)
+    args = (vec, md, mi, spec["w"], spec["h"], spec["bw"], spec["threads"], spec["vw"], spec["minibatch"],
+            spec["vecnum"], spec["arch"])
+    if not all(spec["is_cuda"]):
+        with pytest.raises(ValueError, match="GPU"):  # CPU tensors here: the device check fires first
+            hip_spmv.nmsparse_spmv_forward_hip(*args)
+        return
+    if spec["arch"] == "gfx950":
+        hip_spmv.validate_args(*args, require_device=False)  # accepted by this build (its own target)
+        return
+    if want is None:
+        hip_spmv.validate_args(*args, require_device=False)
+        return
+    exc = {"ValueError": ValueError, "TypeError": TypeError, "NotImplementedError": NotImplementedError}[want]
+    with pytest.raises(exc) as e:
+        hip_spmv.validate_args(*args, require_device=False)
+    if spec["arch"] == "auto" or want != "ValueError" or "arch" not in str(e.value):
+        assert str(e.value) == case["message"]
+
+
 def test_cpu_tensors_rejected_first():
     vec, md, mi = _spec_tensors(_base(vec_dtype=torch.int32))  # dtype also wrong: device check comes first
     with pytest.raises(ValueError, match="GPU"):
