@@ -24,19 +24,21 @@ def _chunk_width(n: int) -> int:
     return 0
 
 
-def greedy_token(logits: torch.Tensor) -> torch.Tensor:
-    """argmax over the last dim of [1, V] logits -> [1] int64, the first index
-    of the maximum like torch.argmax, in two parallel stages: the maximum (and
-    its first index) of each C-wide chunk, then the first chunk holding the
-    largest of those. A single-row torch.argmax over a 128K vocabulary is one
-    workgroup's reduction (~46 us on MI355X)."""
+def greedy_token(logits: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """argmax over the last dim of [1, V] logits -> [1] int64 (written to
+    `out` when given), the first index of the maximum like torch.argmax, in
+    two parallel stages: the maximum (and its first index) of each C-wide
+    chunk, then the first chunk holding the largest of those. A single-row
+    torch.argmax over a 128K vocabulary is one workgroup's reduction (~46 us
+    on MI355X). Four kernels, no host synchronisation (graph capture)."""
     V = logits.shape[-1]
     C = _chunk_width(V)
     if C == 0 or V // C < 2:
-        return torch.argmax(logits, dim=-1)
+        r = torch.argmax(logits, dim=-1)
+        return r if out is None else out.copy_(r.view_as(out))
     vals, idx = logits.reshape(V // C, C).max(dim=1)
     j = torch.argmax(vals).view(1)
-    return j * C + idx.index_select(0, j)  # no host synchronisation (graph capture)
+    return torch.add(idx.index_select(0, j), j, alpha=C, out=out)  # j * C + idx[j]
 
 
 CACHE_ALIGN = 128
@@ -70,9 +72,8 @@ class GraphDecoder:
     @torch.no_grad()
     def _step(self):
         logits = self.model.forward_step(self.token, self.pos)
-        nxt = greedy_token(logits)  # [1]
-        self.tokens.index_copy_(0, self.pos + 1, nxt)
-        self.token.copy_(nxt.view(1, 1))
+        nxt = greedy_token(logits, out=self.token.view(1))  # the next step's input token
+        self.tokens[1:].index_copy_(0, self.pos, nxt)  # tokens[pos + 1]
         self.pos.add_(1)
         return logits
 

@@ -252,6 +252,8 @@ def test_greedy_token_matches_argmax_with_ties(V):
         if trial == 5:
             logits.fill_(1.0)  # all equal: index 0
         assert int(greedy_token(logits)) == int(torch.argmax(logits, dim=-1)), (V, trial)
+        out = torch.full((1,), -1, dtype=torch.long)
+        assert greedy_token(logits, out=out) is out and int(out) == int(torch.argmax(logits, dim=-1)), (V, trial)
 
 
 def test_cache_length_rounds_up_to_the_alignment():
