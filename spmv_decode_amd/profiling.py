@@ -201,6 +201,35 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 
+def decode_table(json_paths):
+    """The decode tables of profiles/decode_*.md: one row per variant of each
+    `bench_decode --json` file, then the speedups over dense."""
+    names = {"llama-3.1-8b": "Llama-3.1-8B", "qwen3-14b": "Qwen3-14B", "qwen3-32b": "Qwen3-32B"}
+    rows, speed = [], []
+    for path in json_paths:
+        d = json.loads(Path(path).read_text())
+        model = names.get(d["model"], d["model"])
+        pg = f"{d['prompt']} / {d['gen']}"
+        ratio = d.get("sparse", {}).get("ratio", "")
+        sparse_bytes = d.get("sparse", {}).get("linear_bytes_per_token")
+        for key, label, nbytes in (("dense", "dense", None), ("sparse", f"{ratio} fused layer", sparse_bytes),
+                                   ("sparse_per_linear", f"{ratio} per-Linear", sparse_bytes)):
+            v = d.get(key)
+            if not v:
+                continue
+            nb = v.get("linear_bytes_per_token", nbytes)
+            rows.append(f"| {model} | {pg} | {label} | {v['ms_per_token']:.4f} | {v['ms_per_token_median_of_16']:.4f} | "
+                        f"{v['tokens_per_s']} | {nb:,} |")
+        if "speedup_sparse_vs_dense" in d:
+            line = f"{model} {ratio}: fused layer {d['speedup_sparse_vs_dense']:.4f}x"
+            if "speedup_sparse_per_linear_vs_dense" in d:
+                line += f", per-Linear {d['speedup_sparse_per_linear_vs_dense']:.4f}x"
+            speed.append(line)
+    head = ["| Model | Prompt / gen | Variant | ms/token (mean) | median of 16-step chunks | tokens/s | "
+            "Linear bytes/token |", "|---|---|---|---|---|---|---|"]
+    return "\n".join(head + rows + [""] + [f"Speedup over dense: {x}." for x in speed]) + "\n"
+
+
 def cpu(bench_json, md_path, cmd):
     """CPU baseline summary from a `bench.py --cpu-detail --cpu-decode` JSON line."""
     b = json.loads(Path(bench_json).read_text())
@@ -246,6 +275,8 @@ def main(argv=None):
     s.add_argument("--csv", required=True)
     s.add_argument("--bench", default=None)
     s.add_argument("--md", required=True)
+    dt = sub.add_parser("decode-table")
+    dt.add_argument("json", nargs="+", help="bench_decode --json files")
     ds = sub.add_parser("decode-stats")
     ds.add_argument("--csv", required=True)
     ds.add_argument("--decode", required=True)
@@ -259,6 +290,8 @@ def main(argv=None):
                 "python -u -m spmv_decode_amd.microbench --traffic-probe",
                 "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc --output-format csv -- "
                 "python -u -m spmv_decode_amd.microbench --traffic-probe")
+    elif a.cmd == "decode-table":
+        print(decode_table(a.json), end="")
     elif a.cmd == "decode-stats":
         decode_stats(a.csv, a.decode, a.md, a.command_line)
     elif a.cmd == "cpu":
