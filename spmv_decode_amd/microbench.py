@@ -391,6 +391,70 @@ def read_ceiling(sizes=(4_206_592, 16_795_648, 58_759_168, 268_435_456, 1 << 30)
     return out
 
 
+STRIPE_SHAPES = {  # name: (rows R = w, outputs h) of the fp16 weights one launch streams, 32:64
+    "q_o": (2048, 4096), "k_v": (2048, 1024), "gate_up": (2048, 14336), "down": (7168, 4096),
+    "gate_up_pair": (2048, 28672),  # gate and up side by side: the pair's bytes
+}
+
+
+def stripe_ceiling(shapes=STRIPE_SHAPES, pool_bytes=2 << 30, reps=10, log=print):
+    """Best time of one launch that only reads the weights of a GEMV launch
+    in the GEMV's pattern (column stripes of 256 B - 2 KB per row, split over
+    rows; roofline_probe.hip: nm_probe_stripe_read), over stripe widths and
+    split counts: the ceiling for this access pattern, graph replay, weights
+    rotated through `pool_bytes`."""
+    import ctypes
+
+    from .build import PROBE_LIB_PATH
+
+    lib = ctypes.CDLL(str(PROBE_LIB_PATH))
+    lib.nm_probe_stripe_read.restype = ctypes.c_int
+    lib.nm_probe_stripe_read.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_int,
+                                         ctypes.c_void_p, ctypes.c_void_p]
+    buf = torch.randint(0, 255, (pool_bytes,), dtype=torch.uint8, device="cuda")
+    sink = torch.zeros(1 << 16, dtype=torch.int32, device="cuda")
+    out = {}
+    for name, (R, h) in shapes.items():
+        nb = R * h * 2
+        C16 = h // 8
+        copies = min(256, max(1, pool_bytes // nb))
+        best = None
+        for sw in (16, 32, 64, 128):
+            for splits in (2, 4, 8, 16, 32):
+                if C16 % sw or R % splits or (C16 // sw) * splits > sink.numel():
+                    continue
+
+                def launch(i, sw=sw, splits=splits):
+                    rc = lib.nm_probe_stripe_read(buf.data_ptr() + i * nb, R, C16, sw, splits, sink.data_ptr(),
+                                                  torch.cuda.current_stream().cuda_stream)
+                    if rc != 0:
+                        raise RuntimeError(f"nm_probe_stripe_read failed: {rc}")
+                us = graph_us_per_launch([lambda i=i: launch(i) for i in range(copies)], reps)
+                if best is None or us < best[0]:
+                    best = (us, sw * 16, splits, (C16 // sw) * splits)
+        out[name] = {"bytes": nb, "us": round(best[0], 3), "GBps": round(nb / best[0] / 1e3, 1),
+                     "stripe_bytes": best[1], "splits": best[2], "workgroups": best[3]}
+        log(f"stripe ceiling {name:13s} {nb / 1e6:7.1f} MB: {best[0]:7.2f} us {nb / best[0] / 1e3:6.0f} GB/s "
+            f"(stripe {best[1]} B, {best[2]} splits, {best[3]} workgroups)")
+    return out
+
+
+def write_stripe_md(res, path, cmd):
+    lines = ["# Read ceiling in the GEMV's access pattern (MI355X, fp16 weights of the Llama-3.1-8B shapes, 32:64)", "",
+             "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
+             "Each row: the fastest launch, over stripe widths (256 B - 2 KB of a row per workgroup, i.e. 128- to",
+             "1024-row output tiles) and split counts (2-32), of a kernel that only reads the launch's weights in",
+             "column stripes as the GEMV does (`roofline_probe.hip: nm_probe_stripe_read`, 8 rows per lane in",
+             "flight). Graph replay over >= 1 GiB of rotated copies, inter-kernel gap included, as for the GEMV",
+             "classes in bench.py. `gate_up_pair` reads gate and up side by side (the pair launch's weight bytes).", "",
+             "| Launch | Weight bytes | us | GB/s | % of 8 TB/s | stripe | splits | workgroups |",
+             "|---|---|---|---|---|---|---|---|"]
+    for name, r in res.items():
+        lines.append(f"| {name} | {r['bytes']:,} | {r['us']:.2f} | {r['GBps']:.0f} | {r['GBps'] / 80:.1f}% | "
+                     f"{r['stripe_bytes']} B | {r['splits']} | {r['workgroups']} |")
+    Path(path).write_text("\n".join(lines) + "\n")
+
+
 def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     """Workload for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
     three copies of a 256 MiB buffer (the known-size calibration kernel), then
@@ -468,12 +532,21 @@ def main(argv=None):
     p.add_argument("--csv", default=None)
     p.add_argument("--json", default=None, help="write the best row per (shape, ratio) as JSON")
     p.add_argument("--read-ceiling", action="store_true", help="measure plain streaming-read launches only")
+    p.add_argument("--stripe-ceiling", action="store_true",
+                   help="measure launches that only read each Llama shape's weights in the GEMV's pattern")
     p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
     a = p.parse_args(argv)
     if a.read_ceiling:
         res = read_ceiling(log=lambda s: print(s, flush=True))
         if a.json:
             Path(a.json).write_text(json.dumps({str(k): v for k, v in res.items()}, indent=1))
+        return 0
+    if a.stripe_ceiling:
+        res = stripe_ceiling(log=lambda s: print(s, flush=True))
+        if a.json:
+            Path(a.json).write_text(json.dumps(res, indent=1))
+        if a.md:
+            write_stripe_md(res, a.md, "python -u -m spmv_decode_amd.microbench --stripe-ceiling --json <json> --md <md>")
         return 0
     if a.traffic_probe:
         traffic_probe(_parse_pairs(a.dims, "x"), log=lambda s: print(s, flush=True))
