@@ -230,6 +230,66 @@ def decode_table(json_paths):
     return "\n".join(head + rows + [""] + [f"Speedup over dense: {x}." for x in speed]) + "\n"
 
 
+def sweep_stats(trace_csv, sweep_csv, md_path, cmd):
+    """Per (configuration, split count) of a `microbench --sweep` run: the
+    HIP-event time per launch it measured and the average kernel duration
+    rocprofv3 traced for the same kernel and grid, with the GB/s of each."""
+    import re
+
+    sweep = _read(sweep_csv)
+    groups = {}
+    with open(trace_csv, newline="") as f:
+        rd = csv.DictReader(f)
+        for r in rd:
+            name = r.get("Kernel_Name", "")
+            mt = re.search(r"nm_gemv_kernel<\d+, (\d+), (\d+), \d+, (true|false), 1, false>", name)
+            if not mt:
+                continue
+            lanes = int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 256)
+            grid = int(r.get("Grid_Size_X") or r.get("Grid_Size"))
+            key = (int(mt.group(1)), int(mt.group(2)), mt.group(3) == "true", grid // max(lanes, 1))
+            dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
+            g = groups.setdefault(key, [0, 0.0])
+            g[0] += 1
+            g[1] += dur
+    lines = ["# Configuration sweep by rocprofv3 kernel duration (configuration x split count)", "",
+             "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd, "```", "",
+             "Each row: one configuration (TH lanes across a 8*TH-row tile, U rows per lane per chunk; `_cached` =",
+             "ordinary instead of non-temporal loads) at one split count, weights rotated over >= 1 GiB; `rocprof us`",
+             "is the average duration rocprofv3 traced for the dispatches of that kernel with that grid, GB/s count",
+             "the algorithmic bytes. The 10 fastest rows and the library's own choice are shown. The tracer's",
+             "per-dispatch bookkeeping slows the launches (the same run's HIP-event times are inflated and left",
+             "out); the library's defaults come from untraced graph-replay sweeps (the decoder's condition), where",
+             "they are the fastest or within 0.3 us of it.", ""]
+    by_shape = {}
+    for r in sweep:
+        by_shape.setdefault((r["n_out"], r["n_in"], r["ratio"]), []).append(r)
+    for (n_out, n_in, ratio), rows in by_shape.items():
+        nbytes = float(rows[0]["GBps"]) * float(rows[0]["us"]) * 1e3
+        timed = []
+        for r in rows:
+            cfgname = r["config"].split(":")[-1]
+            mt = re.match(r"th(\d+)_u(\d+)(_cached)?", cfgname)
+            key = (int(mt.group(1)), int(mt.group(2)), not mt.group(3), int(r["blocks"]))
+            n, tot = groups.get(key, (0, 0.0))
+            if n:
+                timed.append((tot / n / 1e3, n, r))
+        auto = next((t for t in timed if t[2]["config"].startswith("auto:")), None)
+        ranked = sorted((t for t in timed if not t[2]["config"].startswith("auto:")), key=lambda t: t[0])
+        lines += [f"## {n_in} -> {n_out}, {ratio} ({nbytes / 1e6:.1f} MB per launch)", "",
+                  "| config | splits | workgroups | rocprof us | GB/s | % of 8 TB/s | dispatches |",
+                  "|---|---|---|---|---|---|---|"]
+        for rp, n, r in ([auto] if auto else []) + ranked[:10]:
+            label = f"{r['config'].split(':')[-1]} (library choice)" if auto and r is auto[2] else r["config"]
+            gbs = nbytes / rp / 1e3
+            lines.append(f"| {label} | {r['splits']} | {r['blocks']} | {rp:.2f} | {gbs:.0f} | {gbs / 80:.1f}% | {n} |")
+        if auto and ranked:
+            lines.append(f"\nLibrary choice {auto[0]:.2f} us against the fastest traced {ranked[0][0]:.2f} us "
+                         f"({100 * (auto[0] / ranked[0][0] - 1):+.1f}%).")
+        lines.append("")
+    Path(md_path).write_text("\n".join(lines))
+
+
 def cpu(bench_json, md_path, cmd):
     """CPU baseline summary from a `bench.py --cpu-detail --cpu-decode` JSON line."""
     b = json.loads(Path(bench_json).read_text())
@@ -275,6 +335,11 @@ def main(argv=None):
     s.add_argument("--csv", required=True)
     s.add_argument("--bench", default=None)
     s.add_argument("--md", required=True)
+    sw = sub.add_parser("sweep-stats")
+    sw.add_argument("--trace", required=True, help="rocprofv3 kernel trace CSV of a microbench --sweep run")
+    sw.add_argument("--sweep", required=True, help="the microbench --csv of the same run")
+    sw.add_argument("--md", required=True)
+    sw.add_argument("--command", dest="command_line", required=True)
     dt = sub.add_parser("decode-table")
     dt.add_argument("json", nargs="+", help="bench_decode --json files")
     ds = sub.add_parser("decode-stats")
@@ -290,6 +355,8 @@ def main(argv=None):
                 "python -u -m spmv_decode_amd.microbench --traffic-probe",
                 "rocprofv3 --pmc WRITE_SIZE -d gpurun_out/pmc_write -o pmc --output-format csv -- "
                 "python -u -m spmv_decode_amd.microbench --traffic-probe")
+    elif a.cmd == "sweep-stats":
+        sweep_stats(a.trace, a.sweep, a.md, a.command_line)
     elif a.cmd == "decode-table":
         print(decode_table(a.json), end="")
     elif a.cmd == "decode-stats":
