@@ -253,7 +253,9 @@ def sweep_stats(trace_csv, sweep_csv, md_path, cmd):
             g[0] += 1
             g[1] += dur
     lines = ["# Configuration sweep by rocprofv3 kernel duration (configuration x split count)", "",
-             "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd, "```", "",
+             "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd,
+             "python -m spmv_decode_amd.profiling sweep-stats --trace <the kernel trace csv> --sweep <the --csv file> "
+             "--command '<the line above>' --md <this file>", "```", "",
              "Each row: one configuration (TH lanes across a 8*TH-row tile, U rows per lane per chunk; `_cached` =",
              "ordinary instead of non-temporal loads) at one split count, weights rotated over >= 1 GiB; `rocprof us`",
              "is the average duration rocprofv3 traced for the dispatches of that kernel with that grid, GB/s count",
