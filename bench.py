@@ -16,7 +16,8 @@ launches without the fusions (config.plain_fused_step) and the GEMVs as 224
 separate launches (config.unfused_224_launches) are timed too.
 
 Also reported: per-shape average launch time and GB/s for the sparse kernel
-and for dense fp16 F.linear (hipBLASLt preferred) on the same shapes, the
+and for dense fp16 hipBLASLt GEMVs on the same shapes (the faster of its
+x * W^T and W * x problem forms per shape), the
 roofline of the dominant kernel (HIP events on the launch stream), and a CPU
 baseline (the oracle's gather-form GEMV on one layer's weights, host cores).
 Prints ONE JSON line on stdout; progress goes to stderr.
@@ -343,13 +344,14 @@ def main():
         dense_step_us = 0.0
         for cls, names in classes.items():
             K, h = SHAPES[names[0]]
-            us = MB.time_dense(h, K, torch.float16, rotate_bytes=1 << 30, reps=reps)
+            us, form = MB.time_dense(h, K, torch.float16, rotate_bytes=1 << 30, reps=reps, return_form=True)
             b = dense_bytes(K, h)
-            per_dense[cls] = {"us_per_launch": round(us, 3), "GBps": round(b / (us * 1e-6) / 1e9, 1),
+            per_dense[cls] = {"us_per_launch": round(us, 3), "form": form,
+                              "GBps": round(b / (us * 1e-6) / 1e9, 1),
                               "pct_peak": round(100 * b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
                               "speedup_sparse_vs_dense": round(us / per_shape[cls]["us_per_launch"], 3)}
             dense_step_us += us * L * len(names)
-            log(f"dense  {cls:8s}: {us:7.2f} us/launch {per_dense[cls]['GBps']:7.1f} GB/s "
+            log(f"dense  {cls:8s}: {us:7.2f} us/launch ({form}) {per_dense[cls]['GBps']:7.1f} GB/s "
                 f"-> sparse speedup {per_dense[cls]['speedup_sparse_vs_dense']}x")
             torch.cuda.empty_cache()
         sparse_step_us = sum(per_shape[c]["us_per_launch"] * per_shape[c]["launches_per_step"] for c in per_shape)
@@ -395,7 +397,13 @@ def decode_ms_per_token(m, log):
         torch.set_default_dtype(prev)
     init_weights_(model, seed=0)
     prompt = torch.randint(0, LLAMA31_8B.vocab, (128,), generator=torch.Generator().manual_seed(1))
-    dense = run_variant(model, LLAMA31_8B, prompt, 256, "dense", log)
+    dense_by_fusion, forms = {}, {}
+    for mode in ("qkv", "none", "qkv_gate_up"):  # "qkv": the reference's dense model (model.py:198 wqkv)
+        model.set_dense_fusion(mode)
+        forms.update(model.tune_dense_gemv())  # the faster hipBLASLt problem form per dense shape
+        dense_by_fusion[mode] = run_variant(model, LLAMA31_8B, prompt, 256, f"dense ({mode} fused)", log)
+    model.set_dense_fusion("none")
+    dense = dense_by_fusion["qkv"]
     swap_to_nmsparse(model, m, "cuda", seed=0, init="device", keep_dense=False)
     torch.cuda.empty_cache()
     sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)
@@ -405,7 +413,13 @@ def decode_ms_per_token(m, log):
     torch.cuda.empty_cache()
     out = {"model": "llama-3.1-8b (random init)", "prompt": 128, "gen": 256,
            "dense_ms_per_token": dense["ms_per_token"], "sparse_ms_per_token": sparse["ms_per_token"],
+           "dense_launches": "q/k/v fused into one GEMM (the reference's dense model), gate/up/o/down one each; "
+                             "each shape in the faster of hipBLASLt's x*W^T and W*x forms",
+           "dense_gemv_forms": forms,
            "speedup_sparse_vs_dense": round(dense["ms_per_token"] / sparse["ms_per_token"], 4),
+           "dense_ms_per_token_by_fusion": {k: v["ms_per_token"] for k, v in dense_by_fusion.items()},
+           "speedup_sparse_vs_fastest_dense": round(min(v["ms_per_token"] for v in dense_by_fusion.values())
+                                                     / sparse["ms_per_token"], 4),
            "sparse_per_linear_ms_per_token": per_linear["ms_per_token"],
            "speedup_sparse_per_linear_vs_dense": round(dense["ms_per_token"] / per_linear["ms_per_token"], 4),
            "sparse_linear_bytes_per_token": linear_bytes(LLAMA31_8B, m),

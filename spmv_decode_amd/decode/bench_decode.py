@@ -7,12 +7,18 @@ Protocol: random-init weights of the named architecture
 in fp16 on one GPU; the prompt (seeded random token ids) is fed one token per
 graph replay (untimed), then `--gen` greedy decode steps are replayed from one
 captured hipGraph and timed with HIP events. Dense first (nn.Linear ->
-hipBLASLt), then every q/k/v/o/gate/up/down Linear is swapped to
-NmSparseLinear at N:M = (M/2):M with on-device synthetic patterns, and the
-same protocol runs again. Embeddings, norms and lm_head stay dense in both.
+hipBLASLt, q/k/v as one GEMM like the reference's model.py:198 `wqkv`;
+`--dense-fusion` changes that, `--dense-variants` times all three; each
+dense weight shape issued in whichever of hipBLASLt's two problem forms,
+x * W^T or W * x, runs faster on this GPU, `--no-tune` to keep x * W^T),
+then every q/k/v/o/gate/up/down Linear is swapped to NmSparseLinear at
+N:M = (M/2):M with on-device synthetic patterns, and the same protocol runs
+again. Embeddings, norms and lm_head stay dense in both.
 The sparse model runs the fused layer (norms, RoPE, cache write and residuals
 inside the GEMV launches); `--per-linear` also times it with one launch per
-Linear and PyTorch norms/RoPE, the dense model's step structure.
+Linear and PyTorch norms/RoPE (the step structure of the unfused dense
+model), `--grouped` with one q/k/v and one gate/up launch and PyTorch
+norms/RoPE (the structure of the fused dense modes).
 Prints a `RESULT` line per model variant (like the reference benchmarks,
 benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:186-189) and one JSON line.
 """
@@ -68,9 +74,19 @@ def main(argv=None):
     p.add_argument("--gen", type=int, default=256)
     p.add_argument("--seed", type=int, default=0)
     p.add_argument("--no-dense", action="store_true")
+    p.add_argument("--dense-fusion", default="qkv", choices=Decoder.DENSE_FUSIONS,
+                   help="dense baseline's launches: q/k/v fused (the reference's model), none, or q/k/v and gate/up")
+    p.add_argument("--dense-variants", action="store_true",
+                   help="also time the dense model under the other two fusion modes")
+    p.add_argument("--no-tune", action="store_true",
+                   help="issue dense products as nn.Linear does (x * W^T) instead of the faster of the two "
+                        "hipBLASLt problem forms per shape (Decoder.tune_dense_gemv)")
     p.add_argument("--per-linear", action="store_true",
                    help="also time the sparse model with one launch per Linear and PyTorch norms/RoPE (the "
-                        "dense model's step structure, so the ratio isolates the GEMVs)")
+                        "step structure of the unfused dense model, so that ratio isolates the GEMVs)")
+    p.add_argument("--grouped", action="store_true",
+                   help="also time the sparse model with one q/k/v and one gate/up launch and PyTorch norms/RoPE "
+                        "(the step structure of the fused dense modes)")
     p.add_argument("--json", default=None)
     a = p.parse_args(argv)
 
@@ -100,12 +116,30 @@ def main(argv=None):
     res = {"model": cfg.name, "prompt": a.prompt, "gen": a.gen, "dtype": "fp16", "batch": 1,
            "gpu": torch.cuda.get_device_name(dev)}
     if not a.no_dense:
-        d = run_variant(model, cfg, prompt, a.gen, "dense", log)
-        d["linear_bytes_per_token"] = linear_bytes(cfg, 0)
-        res["dense"] = d
-        print(f"RESULT model={cfg.name} dense_float16 prompt={a.prompt} gen={a.gen} "
-              f"decode_ms_per_token={d['ms_per_token']:.6f} median={d['ms_per_token_median_of_16']:.6f}", flush=True)
+        modes = [a.dense_fusion] + ([m for m in Decoder.DENSE_FUSIONS if m != a.dense_fusion]
+                                    if a.dense_variants else [])
+        for mode in modes:
+            model.set_dense_fusion(mode)
+            if not a.no_tune:
+                for shape, r in model.tune_dense_gemv().items():
+                    log(f"dense GEMV {shape}: x*W^T {r['mm']} us, W*x {r['mv']} us -> {r['form']}")
+                    res.setdefault("dense_gemv_forms", {})[shape] = r
+            d = run_variant(model, cfg, prompt, a.gen, f"dense ({mode} fused)", log)
+            d["linear_bytes_per_token"] = linear_bytes(cfg, 0)
+            d["fusion"] = mode
+            if mode == a.dense_fusion:
+                res["dense"] = d
+            else:
+                res.setdefault("dense_variants", {})[mode] = d
+            print(f"RESULT model={cfg.name} dense_float16 fusion={mode} prompt={a.prompt} gen={a.gen} "
+                  f"decode_ms_per_token={d['ms_per_token']:.6f} median={d['ms_per_token_median_of_16']:.6f}",
+                  flush=True)
+        model.set_dense_fusion("none")
     if a.m:
+        if not a.no_tune:  # lm_head stays dense in the sparse model
+            for shape, r in model.tune_dense_gemv().items():
+                log(f"dense GEMV {shape}: x*W^T {r['mm']} us, W*x {r['mv']} us -> {r['form']}")
+                res.setdefault("dense_gemv_forms", {})[shape] = r
         t0 = time.time()
         n = swap_to_nmsparse(model, a.m, "cuda", seed=a.seed, init="device", keep_dense=False)
         gc.collect()
@@ -119,6 +153,8 @@ def main(argv=None):
               f"decode_ms_per_token={s['ms_per_token']:.6f} median={s['ms_per_token_median_of_16']:.6f}", flush=True)
         if "dense" in res:
             res["speedup_sparse_vs_dense"] = round(res["dense"]["ms_per_token"] / s["ms_per_token"], 4)
+            for mode, d in res.get("dense_variants", {}).items():
+                res[f"speedup_sparse_vs_dense_{mode}"] = round(d["ms_per_token"] / s["ms_per_token"], 4)
         if a.per_linear:
             model.set_launch_mode("per_linear")
             u = run_variant(model, cfg, prompt, a.gen, "sparse per-Linear", log)
@@ -129,6 +165,16 @@ def main(argv=None):
                   flush=True)
             if "dense" in res:
                 res["speedup_sparse_per_linear_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
+        if a.grouped:
+            model.set_launch_mode("grouped")
+            u = run_variant(model, cfg, prompt, a.gen, "sparse grouped", log)
+            model.set_launch_mode("fused")
+            res["sparse_grouped"] = u
+            print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) grouped prompt={a.prompt} gen={a.gen} "
+                  f"decode_ms_per_token={u['ms_per_token']:.6f} median={u['ms_per_token_median_of_16']:.6f}",
+                  flush=True)
+            if "dense" in res:
+                res["speedup_sparse_grouped_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
     print(json.dumps(res), flush=True)
     if a.json:
         with open(a.json, "w") as f:

@@ -152,9 +152,36 @@ def linear_into(lin: nn.Module, x2d: torch.Tensor, out: torch.Tensor) -> torch.T
 
         return nmsparse_spmv_forward_hip(x2d, lin.mat_data, lin.mat_index, lin.w, lin.h, lin.block_width, 128,
                                          lin.vec_width, 1, x2d.shape[1], out=out)
+    if type(lin) is nn.Linear and lin.bias is None:
+        return dense_gemv(x2d, lin.weight, getattr(lin, "gemv_form", "mm"), out=out)
     if isinstance(lin, nn.Linear):
         return torch.mm(x2d, lin.weight.t(), out=out)
     return out.copy_(lin(x2d).view_as(out))
+
+
+GEMV_FORMS = ("mm", "mv")
+
+
+def dense_gemv(x2d: torch.Tensor, weight: torch.Tensor, form: str = "mm", out=None) -> torch.Tensor:
+    """y [1, n_out] = x2d [1, K] · weightᵀ through the BLAS library in one of
+    two problem statements, which it serves with different kernels: "mm" (a
+    one-row product x · Wᵀ, what nn.Linear issues) or "mv" (a matrix-vector
+    product W · x). Which is faster depends on the shape (Decoder.tune_dense_gemv)."""
+    if form == "mv":
+        if out is None:
+            return torch.mv(weight, x2d.view(-1)).view(1, -1)
+        torch.mv(weight, x2d.view(-1), out=out.view(-1))
+        return out
+    return torch.mm(x2d, weight.t(), out=out) if out is not None else torch.mm(x2d, weight.t())
+
+
+def project(lin: nn.Module, x: torch.Tensor) -> torch.Tensor:
+    """lin(x) for one row x [..., K]: a bias-free nn.Linear through dense_gemv
+    in its tuned form, any other module (NmSparseLinear included) through its
+    own forward."""
+    if type(lin) is nn.Linear and lin.bias is None and x.numel() == x.shape[-1]:
+        return dense_gemv(x.reshape(1, -1), lin.weight, getattr(lin, "gemv_form", "mm")).view(*x.shape[:-1], -1)
+    return lin(x)
 
 
 def grouped_sparse(mods) -> bool:
@@ -179,6 +206,8 @@ class Attention(nn.Module):
         self.k_proj = nn.Linear(cfg.dim, kvd, bias=False)
         self.v_proj = nn.Linear(cfg.dim, kvd, bias=False)
         self.o_proj = nn.Linear(qd, cfg.dim, bias=False)
+        self.wqkv = None  # fused dense q/k/v weight (Decoder.set_dense_fusion), not a parameter
+        self.wqkv_form = "mm"
         if cfg.qk_norm:
             self.q_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
             self.k_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
@@ -200,6 +229,8 @@ class Attention(nn.Module):
 
             nmsparse_gemv_grouped(x2d, [(p.mat_data, p.mat_index) for p in projs], projs[0].block_width,
                                   projs[0].vec_width, outs=slices)
+        elif self.wqkv is not None and all(type(p) is nn.Linear for p in projs):
+            dense_gemv(x2d, self.wqkv, self.wqkv_form, out=qkv)
         else:
             for proj, sl in zip(projs, slices):
                 linear_into(proj, x2d, sl)
@@ -213,7 +244,7 @@ class Attention(nn.Module):
         k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
         v_cache_t.index_copy_(2, pos, v)
         y = attend(q_pad, k_cache_t, v_cache_t, c, zero)  # [kvh, g, head_dim]
-        return self.o_proj(y.view(1, 1, qd))
+        return project(self.o_proj, y.view(1, 1, qd))
 
 
 class MLP(nn.Module):
@@ -224,6 +255,8 @@ class MLP(nn.Module):
         self.gate_proj = nn.Linear(cfg.dim, cfg.inter, bias=False)
         self.up_proj = nn.Linear(cfg.dim, cfg.inter, bias=False)
         self.down_proj = nn.Linear(cfg.inter, cfg.dim, bias=False)
+        self.w13 = None  # fused dense gate/up weight (Decoder.set_dense_fusion), not a parameter
+        self.w13_form = "mm"
 
     def forward(self, x):
         if self.group_launches and grouped_sparse((self.gate_proj, self.up_proj)):
@@ -232,8 +265,12 @@ class MLP(nn.Module):
             g, u = self.gate_proj, self.up_proj
             act = nmsparse_gate_up_silu(x.view(1, -1), (g.mat_data, g.mat_index), (u.mat_data, u.mat_index),
                                         g.block_width, g.vec_width)
-            return self.down_proj(act.view(1, 1, -1))
-        return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
+            return project(self.down_proj, act.view(1, 1, -1))
+        if self.w13 is not None and type(self.gate_proj) is nn.Linear and type(self.up_proj) is nn.Linear:
+            gu = dense_gemv(x.reshape(1, -1), self.w13, self.w13_form)
+            g, u = gu.chunk(2, dim=1)
+            return project(self.down_proj, (F.silu(g) * u).view(1, 1, -1))
+        return project(self.down_proj, F.silu(project(self.gate_proj, x)) * project(self.up_proj, x))
 
 
 class Block(nn.Module):
@@ -300,6 +337,7 @@ class Decoder(nn.Module):
         self.norm = RMSNorm(cfg.dim, cfg.norm_eps)
         self.lm_head = nn.Linear(cfg.dim, cfg.vocab, bias=False)
         self.max_seq = 0
+        self.gemv_forms = {}  # (n_out, n_in) -> dense_gemv form, filled by tune_dense_gemv
 
     LAUNCH_MODES = ("fused", "grouped", "per_linear")
 
@@ -313,6 +351,79 @@ class Decoder(nn.Module):
         self.fuse_epilogues = mode == "fused"
         for blk in self.layers:
             blk.self_attn.group_launches = blk.mlp.group_launches = mode != "per_linear"
+
+    DENSE_FUSIONS = ("none", "qkv", "qkv_gate_up")
+
+    def set_dense_fusion(self, mode: str) -> None:
+        """How dense (nn.Linear) projections are launched: "none" (one GEMM per
+        Linear), "qkv" (q/k/v as one [q+k+v rows] GEMM, the reference's dense
+        model: model.py:198 `wqkv`, model.py:219) or "qkv_gate_up" (also gate/up
+        as one GEMM). The fused weights are copies taken now, held outside the
+        parameters (so swap_to_nmsparse and state_dict do not see them): change
+        the Linears' weights afterwards and set the mode again. Blocks whose
+        projections are not all nn.Linear ignore them; "none" frees them."""
+        if mode not in self.DENSE_FUSIONS:
+            raise ValueError(f"dense fusion must be one of {self.DENSE_FUSIONS}, got {mode!r}")
+        with torch.no_grad():
+            for blk in self.layers:
+                at, mlp = blk.self_attn, blk.mlp
+                projs = (at.q_proj, at.k_proj, at.v_proj)
+                at.wqkv = (torch.cat([p.weight for p in projs])
+                           if mode != "none" and all(type(p) is nn.Linear for p in projs) else None)
+                pair = (mlp.gate_proj, mlp.up_proj)
+                mlp.w13 = (torch.cat([p.weight for p in pair])
+                           if mode == "qkv_gate_up" and all(type(p) is nn.Linear for p in pair) else None)
+        self._apply_gemv_forms()
+
+    def _dense_gemv_sites(self):
+        """(weight, owner, attribute) for every dense weight the decode step
+        multiplies with dense_gemv: bias-free nn.Linears and the fused copies."""
+        sites = []
+        for blk in self.layers:
+            at, mlp = blk.self_attn, blk.mlp
+            for mod in (at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj):
+                if type(mod) is nn.Linear and mod.bias is None:
+                    sites.append((mod.weight, mod, "gemv_form"))
+            if at.wqkv is not None:
+                sites.append((at.wqkv, at, "wqkv_form"))
+            if mlp.w13 is not None:
+                sites.append((mlp.w13, mlp, "w13_form"))
+        if type(self.lm_head) is nn.Linear and self.lm_head.bias is None:
+            sites.append((self.lm_head.weight, self.lm_head, "gemv_form"))
+        return sites
+
+    def _apply_gemv_forms(self):
+        for w, owner, attr in self._dense_gemv_sites():
+            setattr(owner, attr, self.gemv_forms.get(tuple(w.shape), "mm"))
+
+    def tune_dense_gemv(self, reps: int = 8, warmup: int = 2) -> dict:
+        """Choose, per dense weight shape, the faster dense_gemv form on this
+        GPU: each form is timed over every weight of that shape in the model
+        (all layers in order, so the weights stream from HBM as in a decode
+        step), captured in one hipGraph and replayed `reps` times; the median
+        replay decides. Shapes already tuned are kept. Returns {"n_out x n_in":
+        {"mm": us, "mv": us, "form": ...}} (us per product) for the shapes
+        timed now. Changes only how dense products are issued, not their math
+        (both forms accumulate in fp32; the roundings can differ in the last bit)."""
+        groups = {}
+        for w, _, _ in self._dense_gemv_sites():
+            groups.setdefault(tuple(w.shape), {})[w.data_ptr()] = w
+        report = {}
+        for shape, ws in groups.items():
+            if shape in self.gemv_forms:
+                continue
+            ws = list(ws.values())
+            x = torch.randn(1, shape[1], device=ws[0].device, dtype=ws[0].dtype,
+                            generator=torch.Generator(device=ws[0].device).manual_seed(0))
+            out = torch.empty(1, shape[0], device=ws[0].device, dtype=ws[0].dtype)
+            with torch.no_grad():
+                us = {form: _graph_median_us([lambda w=w, f=form: dense_gemv(x, w, f, out=out) for w in ws], reps,
+                                             warmup) / len(ws) for form in GEMV_FORMS}
+            best = min(GEMV_FORMS, key=us.get)
+            self.gemv_forms[shape] = best
+            report[f"{shape[0]}x{shape[1]}"] = {**{k: round(v, 2) for k, v in us.items()}, "form": best}
+        self._apply_gemv_forms()
+        return report
 
     def setup_cache(self, max_seq: int, device, dtype=torch.float16):
         """Static caches for max_seq positions (see attend for the layouts); the
@@ -352,11 +463,37 @@ class Decoder(nn.Module):
             for i, blk in enumerate(self.layers):
                 fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero,
                                  self.rope)
-            return self.lm_head(self.norm(x)).view(1, -1)
+            return project(self.lm_head, self.norm(x)).view(1, -1)
         freqs = self.rope.index_select(0, pos)
         for i, layer in enumerate(self.layers):
             x = layer(x, freqs, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero)
-        return self.lm_head(self.norm(x)).view(1, -1)
+        return project(self.lm_head, self.norm(x)).view(1, -1)
+
+
+def _graph_median_us(launches, reps: int, warmup: int) -> float:
+    """Median time of one replay of `launches` captured as one hipGraph, in us."""
+    stream = torch.cuda.Stream()
+    stream.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(stream):
+        for fn in launches:  # library handles and workspaces are set up outside the capture
+            fn()
+    torch.cuda.current_stream().wait_stream(stream)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        for fn in launches:
+            fn()
+    for _ in range(warmup):
+        graph.replay()
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        graph.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b) * 1e3)
+    del graph
+    return sorted(times)[len(times) // 2]
 
 
 def init_weights_(model: Decoder, seed: int = 0, std: float = 0.02) -> Decoder:

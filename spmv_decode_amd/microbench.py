@@ -283,16 +283,28 @@ def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60
 
 
 def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda", warmup=3,
-               stats=False):
+               stats=False, form="best", return_form=False):
+    """Dense GEMV y = x * W^T through the BLAS library, weights rotated over
+    `rotate_bytes`, graph-replayed. form: "mm" (a one-row product x * W^T, what
+    nn.Linear issues), "mv" (W * x) or "best" (both timed, the faster kept:
+    the library serves the two with different kernels and neither wins at
+    every shape). Returns us per launch ((median, sd) with stats=True), and
+    with return_form=True also the form that took it: (time, form)."""
+    from .decode.model import dense_gemv
+
     b = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
     copies = max(1, math.ceil(rotate_bytes / b))
     g = torch.Generator(device=device).manual_seed(seed)
     Ws = [(torch.randn(n_out, n_in, generator=g, device=device) * 0.02).to(dtype) for _ in range(copies)]
     x = torch.randn(1, n_in, generator=g, device=device).to(dtype)
     o = torch.empty(1, n_out, dtype=dtype, device=device)
-    us = graph_us_per_launch([lambda W=W: torch.matmul(x, W.t(), out=o) for W in Ws], reps, warmup, stats=stats)
+    res = {}
+    for f in (("mm", "mv") if form == "best" else (form,)):
+        res[f] = graph_us_per_launch([lambda W=W, f=f: dense_gemv(x, W, f, out=o) for W in Ws], reps, warmup,
+                                     stats=stats)
     del Ws
-    return us
+    best = min(res, key=lambda f: res[f][0] if stats else res[f])
+    return (res[best], best) if return_form else res[best]
 
 
 def candidate_splits(case: RotatingCase):
@@ -308,10 +320,11 @@ def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, 
     except Exception:
         pass
     for n_out, n_in in dims:
-        dense_us, dense_sd = (time_dense(n_out, n_in, dtype, rotate_mib << 20, reps, warmup=warmup, stats=True)
-                              if dense else (float("nan"), float("nan")))
+        (dense_us, dense_sd), dense_form = (
+            time_dense(n_out, n_in, dtype, rotate_mib << 20, reps, warmup=warmup, stats=True, return_form=True)
+            if dense else ((float("nan"), float("nan")), ""))
         db = dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8)
-        log(f"--- ({n_out},{n_in}) dense {dense_us:.2f} us {db / dense_us / 1e3:.1f} GB/s")
+        log(f"--- ({n_out},{n_in}) dense {dense_us:.2f} us ({dense_form}) {db / dense_us / 1e3:.1f} GB/s")
         for nnz, m in ratios:
             case = RotatingCase(n_out, n_in, nnz, m, dtype, rotate_mib << 20)
             plan = _lib.plan(n_out, case.w, nnz, m)
@@ -334,7 +347,7 @@ def run(dims, ratios, dtype_name="fp16", sweep=False, rotate_mib=1024, reps=20, 
                        "config": p["config"] if cfg >= 0 else f"auto:{plan['config']}", "splits": p["splits"],
                        "blocks": p["blocks"], "rows_per_split": p["rows_per_split"], "us": round(us, 3),
                        "us_sd": round(sd, 3), "GBps": round(gbs, 1), "pct_peak": round(100 * gbs / HBM_PEAK_GBS, 2),
-                       "dense_us": round(dense_us, 3), "dense_us_sd": round(dense_sd, 3),
+                       "dense_us": round(dense_us, 3), "dense_us_sd": round(dense_sd, 3), "dense_form": dense_form,
                        "dense_GBps": round(dense_bytes(n_in, n_out, torch.finfo(dtype).bits // 8) / dense_us / 1e3, 1),
                        "speedup_vs_dense": round(dense_us / us, 3),
                        "copies": case.copies, **{k: float(f"{v:.3e}") for k, v in err.items()}}
@@ -501,7 +514,8 @@ def write_sweep_md(rows, path, cmd):
              "the 256 MB Infinity Cache serves them); median and stdev over the timed replays, per launch, including",
              "the graph's inter-kernel gap. GB/s counts the algorithmic bytes 2*w*h + w + 2*K + 2*h (dense:",
              "2*K*h + 2*K + 2*h); % of the 8 TB/s HBM peak. Errors are against the fp32 dense matvec on the",
-             "scattered masked weight (the reference microbenchmark's oracle).", "",
+             "scattered masked weight (the reference microbenchmark's oracle). Dense = hipBLASLt in the faster of",
+             "its two problem statements for the shape, x * W^T (`mm`, what nn.Linear issues) or W * x (`mv`).", "",
              "| Shape (K -> h) | N:M | Plan | us (median +- sd) | GB/s | % peak | Dense us | Dense GB/s | Speedup | "
              "max_abs | rel_l2 |", "|---|---|---|---|---|---|---|---|---|---|---|"]
     for r in rows:
@@ -509,7 +523,7 @@ def write_sweep_md(rows, path, cmd):
             continue
         lines.append(f"| {r['n_in']} -> {r['n_out']} | {r['ratio']} | {r['config'][5:]} s{r['splits']} | "
                      f"{r['us']:.2f} +- {r['us_sd']:.2f} | {r['GBps']:.0f} | {r['pct_peak']:.1f}% | "
-                     f"{r['dense_us']:.2f} +- {r['dense_us_sd']:.2f} | {r['dense_GBps']:.0f} | "
+                     f"{r['dense_us']:.2f} +- {r['dense_us_sd']:.2f} ({r.get('dense_form', '')}) | {r['dense_GBps']:.0f} | "
                      f"{r['speedup_vs_dense']:.2f}x | {r['max_abs']:.1e} | {r['rel_l2']:.1e} |")
     Path(path).write_text("\n".join(lines) + "\n")
 

@@ -203,8 +203,11 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
 
 def decode_table(json_paths):
     """The decode tables of profiles/decode_*.md: one row per variant of each
-    `bench_decode --json` file, then the speedups over dense."""
+    `bench_decode --json` file, then the speedups over dense (the headline
+    dense variant, then over the fastest dense fusion mode when several ran)."""
     names = {"llama-3.1-8b": "Llama-3.1-8B", "qwen3-14b": "Qwen3-14B", "qwen3-32b": "Qwen3-32B"}
+    fusion_label = {"qkv": "dense, q/k/v fused", "none": "dense, one GEMM per Linear",
+                    "qkv_gate_up": "dense, q/k/v and gate/up fused"}
     rows, speed = [], []
     for path in json_paths:
         d = json.loads(Path(path).read_text())
@@ -212,9 +215,13 @@ def decode_table(json_paths):
         pg = f"{d['prompt']} / {d['gen']}"
         ratio = d.get("sparse", {}).get("ratio", "")
         sparse_bytes = d.get("sparse", {}).get("linear_bytes_per_token")
-        for key, label, nbytes in (("dense", "dense", None), ("sparse", f"{ratio} fused layer", sparse_bytes),
-                                   ("sparse_per_linear", f"{ratio} per-Linear", sparse_bytes)):
-            v = d.get(key)
+        dense = [("dense", d["dense"])] if d.get("dense") else []
+        dense += [(k, v) for k, v in d.get("dense_variants", {}).items()]
+        variants = [(fusion_label.get(v.get("fusion"), "dense"), v, None) for _, v in dense]
+        variants += [(f"{ratio} fused layer", d.get("sparse"), sparse_bytes),
+                     (f"{ratio} per-Linear", d.get("sparse_per_linear"), sparse_bytes),
+                     (f"{ratio} grouped", d.get("sparse_grouped"), sparse_bytes)]
+        for label, v, nbytes in variants:
             if not v:
                 continue
             nb = v.get("linear_bytes_per_token", nbytes)
@@ -224,6 +231,18 @@ def decode_table(json_paths):
             line = f"{model} {ratio}: fused layer {d['speedup_sparse_vs_dense']:.4f}x"
             if "speedup_sparse_per_linear_vs_dense" in d:
                 line += f", per-Linear {d['speedup_sparse_per_linear_vs_dense']:.4f}x"
+            if "speedup_sparse_grouped_vs_dense" in d:
+                line += f", grouped {d['speedup_sparse_grouped_vs_dense']:.4f}x"
+            hd = fusion_label.get(d["dense"].get("fusion"), "dense")
+            line += f" (over {hd})"
+            if len(dense) > 1 and d.get("sparse"):
+                best_label, best = min(((fusion_label.get(v.get("fusion"), k), v) for k, v in dense),
+                                       key=lambda t: t[1]["ms_per_token"])
+                line += (f"; fused layer over the fastest dense ({best_label}) "
+                         f"{best['ms_per_token'] / d['sparse']['ms_per_token']:.4f}x")
+                for key, lab in (("sparse_per_linear", "per-Linear"), ("sparse_grouped", "grouped")):
+                    if d.get(key):
+                        line += f", {lab} {best['ms_per_token'] / d[key]['ms_per_token']:.4f}x"
             speed.append(line)
     head = ["| Model | Prompt / gen | Variant | ms/token (mean) | median of 16-step chunks | tokens/s | "
             "Linear bytes/token |", "|---|---|---|---|---|---|---|"]

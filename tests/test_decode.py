@@ -124,6 +124,86 @@ def test_linear_like_projection_modules_run_the_decoder():
         torch.testing.assert_close(a, b, rtol=1e-5, atol=1e-5)
 
 
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_dense_fusion_modes_match_per_linear(qk_norm):
+    """Dense q/k/v (and gate/up) as one GEMM give the per-Linear logits; the
+    fused copies are dropped by "none" and ignored once a projection is swapped."""
+    torch.manual_seed(0)
+    model = Decoder(tiny_config(qk_norm=qk_norm)).float()
+    init_weights_(model, seed=6, std=0.05)
+    tokens = torch.tensor([7, 99, 3, 250, 41])
+
+    def run():
+        model.setup_cache(8, "cpu", dtype=torch.float32)
+        with torch.no_grad():
+            return torch.cat([model.forward_step(t.view(1, 1), torch.tensor([i])) for i, t in enumerate(tokens)])
+
+    ref = run()
+    with pytest.raises(ValueError, match="dense fusion"):
+        model.set_dense_fusion("all")
+    model.set_dense_fusion("qkv")
+    at, mlp = model.layers[0].self_attn, model.layers[0].mlp
+    assert at.wqkv.shape == (at.q_proj.out_features + 2 * at.k_proj.out_features, model.cfg.dim)
+    assert mlp.w13 is None and "wqkv" not in dict(model.named_parameters())
+    torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+    model.set_dense_fusion("qkv_gate_up")
+    assert mlp.w13.shape == (2 * model.cfg.inter, model.cfg.dim)
+    torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+    # once a projection is replaced (as swap_to_nmsparse does), its block runs
+    # the replacement, not the fused copy
+    qd = at.q_proj.out_features
+
+    class Zeroed(torch.nn.Module):
+        def forward(self, x):
+            return torch.zeros(*x.shape[:-1], qd, dtype=x.dtype)
+
+    q_dense = at.q_proj
+    at.q_proj = Zeroed()
+    assert not torch.allclose(run(), ref, rtol=1e-3, atol=1e-3)
+    at.q_proj = q_dense
+    torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+    model.set_dense_fusion("none")
+    assert all(b.self_attn.wqkv is None and b.mlp.w13 is None for b in model.layers)
+
+
+def test_dense_gemv_forms_agree_and_are_applied_per_shape():
+    """Both dense_gemv forms compute x·Wᵀ (with and without out=); forms set per
+    shape reach every site of that shape, the fused copies included, and the
+    decoder's logits do not change."""
+    from spmv_decode_amd.decode.model import GEMV_FORMS, dense_gemv
+
+    g = torch.Generator().manual_seed(3)
+    W, x = torch.randn(48, 80, generator=g), torch.randn(1, 80, generator=g)
+    ref = x @ W.t()
+    for form in GEMV_FORMS:
+        torch.testing.assert_close(dense_gemv(x, W, form), ref, rtol=1e-5, atol=1e-5)
+        out = torch.empty(1, 48)
+        assert dense_gemv(x, W, form, out=out) is out
+        torch.testing.assert_close(out, ref, rtol=1e-5, atol=1e-5)
+    model = Decoder(tiny_config(qk_norm=True)).float()
+    init_weights_(model, seed=8, std=0.05)
+    tokens = torch.tensor([3, 14, 159, 26])
+
+    def run():
+        model.setup_cache(8, "cpu", dtype=torch.float32)
+        with torch.no_grad():
+            return torch.cat([model.forward_step(t.view(1, 1), torch.tensor([i])) for i, t in enumerate(tokens)])
+
+    ref = run()
+    c = model.cfg
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+    model.gemv_forms = {(kvd, c.dim): "mv", (c.dim, c.inter): "mv", (c.vocab, c.dim): "mv",
+                        (2 * c.inter, c.dim): "mv"}
+    model.set_dense_fusion("qkv_gate_up")
+    at, mlp = model.layers[1].self_attn, model.layers[1].mlp
+    assert at.k_proj.gemv_form == at.v_proj.gemv_form == "mv" and mlp.down_proj.gemv_form == "mv"
+    assert mlp.gate_proj.gemv_form == "mm" and model.lm_head.gemv_form == "mv"
+    assert mlp.w13_form == "mv" and at.wqkv_form == ("mv" if (qd + 2 * kvd, c.dim) in model.gemv_forms else "mm")
+    torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+    model.set_dense_fusion("none")
+    torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+
+
 def test_swap_applies_to_decoder_layout():
     model = Decoder(tiny_config())
     n = swap_to_nmsparse(model, 8, "cpu", seed=3, keep_dense=False)
@@ -195,6 +275,43 @@ def test_graph_replay_matches_eager_and_masked_dense(gpu):
             assert torch.equal(a, b), rep
     with pytest.raises(RuntimeError, match="static cache"):
         gd.generate(64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("fusion", ["none", "qkv", "qkv_gate_up"])
+def test_tuned_dense_decode_replays_match_eager(gpu, fusion):
+    """The dense baseline as the decode benchmark runs it (fused copies, GEMV
+    forms tuned on the GPU): logits within fp16 tolerance of the untuned
+    per-Linear model, graph replays bit-identical to eager, three times over."""
+    from spmv_decode_amd.decode.model import GEMV_FORMS
+    from spmv_decode_amd.decode.runner import GraphDecoder
+
+    cfg = tiny_config(qk_norm=True)
+    torch.manual_seed(0)
+    model = Decoder(cfg).to("cuda", torch.float16)
+    init_weights_(model, seed=9, std=0.05)
+    prompt = torch.randint(0, cfg.vocab, (4,), generator=torch.Generator().manual_seed(5))
+    base = GraphDecoder(model, 32)
+    base.run_prompt(prompt)
+    ref = [base.eager_step().clone() for _ in range(5)]
+    del base
+    model.set_dense_fusion(fusion)
+    report = model.tune_dense_gemv(reps=3, warmup=1)
+    assert report and all(r["form"] in GEMV_FORMS and r["mm"] > 0 and r["mv"] > 0 for r in report.values())
+    assert model.tune_dense_gemv() == {}  # every shape already tuned
+    eager = GraphDecoder(model, 32)
+    eager.run_prompt(prompt)
+    eager_logits = [eager.eager_step().clone() for _ in range(5)]
+    for a, b in zip(eager_logits, ref):
+        torch.testing.assert_close(a.float(), b.float(), rtol=2e-2, atol=2e-2)
+    gd = GraphDecoder(model, 32)
+    gd.capture()
+    for rep in range(3):
+        gd.run_prompt(prompt)
+        for i in range(5):
+            gd.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(gd.logits, eager_logits[i]), (rep, i)
 
 
 @pytest.mark.gpu
