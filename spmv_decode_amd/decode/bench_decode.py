@@ -136,15 +136,15 @@ def main(argv=None):
                   flush=True)
         model.set_dense_fusion("none")
     if a.m:
-        if not a.no_tune:  # lm_head stays dense in the sparse model
-            for shape, r in model.tune_dense_gemv().items():
-                log(f"dense GEMV {shape}: x*W^T {r['mm']} us, W*x {r['mv']} us -> {r['form']}")
-                res.setdefault("dense_gemv_forms", {})[shape] = r
         t0 = time.time()
         n = swap_to_nmsparse(model, a.m, "cuda", seed=a.seed, init="device", keep_dense=False)
         gc.collect()
         torch.cuda.empty_cache()
         log(f"swapped {n} Linears to {a.m // 2}:{a.m} in {time.time() - t0:.1f} s")
+        if not a.no_tune:  # lm_head stays dense in the sparse model (already tuned if dense ran)
+            for shape, r in model.tune_dense_gemv().items():
+                log(f"dense GEMV {shape}: x*W^T {r['mm']} us, W*x {r['mv']} us -> {r['form']}")
+                res.setdefault("dense_gemv_forms", {})[shape] = r
         s = run_variant(model, cfg, prompt, a.gen, "sparse", log)
         s["linear_bytes_per_token"] = linear_bytes(cfg, a.m)
         s["ratio"] = f"{a.m // 2}:{a.m}"

@@ -170,11 +170,14 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
             return "attention softmax"
         return "other (embedding, norm, mask, greedy token, position)"
 
+    def step_us(r):  # average duration x launches per step (set-up calls of a step kernel left out)
+        return float(r["AverageNs"]) * round(int(r["Calls"]) / steps) / 1e3
+
     per = {}
     rows = [r for r in rows if kind(r) is not None]
     for r in rows:
         c = kind(r)
-        per[c] = per.get(c, 0.0) + float(r["TotalDurationNs"]) / steps / 1e3
+        per[c] = per.get(c, 0.0) + step_us(r)
     total = sum(per.values())
     sp = d["sparse"]
     lines = [f"# rocprofv3 kernel statistics: hipGraph decode, {d['model']} {sp.get('ratio', '')}, fp16, batch 1", "",
@@ -184,8 +187,9 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
              "```", "",
              f"{steps} decode steps were profiled (capture warm-up, the {d['prompt']}-token prompt and {d['gen']}",
              "generated tokens, one graph replay each). Kernel time per step, summed by role: rocprof durations of",
-             "the kernels only (the graph's inter-kernel gaps are not included; the model's set-up kernels are",
-             "left out):", "",
+             "the kernels only (the graph's inter-kernel gaps are not included), each kernel's average duration",
+             "times its launches per step; the model's set-up kernels (random init, packing, the lm_head form",
+             "timing) are left out:", "",
              "| Role | us per step | Share |", "|---|---|---|"]
     for c, v in sorted(per.items(), key=lambda kv: -kv[1]):
         lines.append(f"| {c} | {v:.1f} | {100 * v / total:.1f}% |")
@@ -193,11 +197,10 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
               f"The profiled run itself measured {sp['ms_per_token']} ms/token (HIP events around the replays,",
               "under the profiler).", "",
               "| Kernel | Calls | Avg (us) | Per step (us) |", "|---|---|---|---|"]
-    for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
+    for r in sorted(rows, key=lambda r: -step_us(r))[:12]:
         n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
         n = n if len(n) <= 90 else n[:87] + "..."
-        lines.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
-                     f"{float(r['TotalDurationNs']) / steps / 1e3:.2f} |")
+        lines.append(f"| `{n}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | {step_us(r):.2f} |")
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 

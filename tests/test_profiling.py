@@ -1,0 +1,98 @@
+"""The profile summarisers (spmv_decode_amd.profiling) on synthetic inputs:
+the decode tables and the per-role accounting of a rocprofv3 decode run."""
+import csv
+import json
+
+import pytest
+
+from spmv_decode_amd import profiling as P
+
+
+def _variant(ms, fusion=None):
+    v = {"ms_per_token": ms, "ms_per_token_median_of_16": ms, "tokens_per_s": round(1e3 / ms, 2),
+         "linear_bytes_per_token": 1000}
+    if fusion:
+        v["fusion"] = fusion
+    return v
+
+
+def test_decode_table_rows_and_speedups(tmp_path):
+    d = {"model": "llama-3.1-8b", "prompt": 128, "gen": 256,
+         "dense": _variant(5.0, "qkv"), "dense_variants": {"none": _variant(6.0, "none"),
+                                                           "qkv_gate_up": _variant(4.0, "qkv_gate_up")},
+         "sparse": {**_variant(2.0), "ratio": "32:64", "linear_bytes_per_token": 500},
+         "sparse_per_linear": _variant(4.0), "sparse_grouped": _variant(3.2),
+         "speedup_sparse_vs_dense": 2.5, "speedup_sparse_per_linear_vs_dense": 1.25,
+         "speedup_sparse_grouped_vs_dense": 1.5625}
+    path = tmp_path / "d.json"
+    path.write_text(json.dumps(d))
+    out = P.decode_table([str(path)])
+    lines = out.splitlines()
+    rows = [ln for ln in lines if ln.startswith("| Llama-3.1-8B")]
+    assert [r.split(" | ")[2] for r in rows] == [
+        "dense, q/k/v fused", "dense, one GEMM per Linear", "dense, q/k/v and gate/up fused",
+        "32:64 fused layer", "32:64 per-Linear", "32:64 grouped"]
+    assert "| 2.0000 |" in rows[3] and "| 500 |" in rows[3]
+    speed = lines[-1]
+    assert "fused layer 2.5000x" in speed and "grouped 1.5625x" in speed and "(over dense, q/k/v fused)" in speed
+    # the fastest dense variant is the q/k/v + gate/up one (4.0 ms): 4.0 / 2.0, 4.0 / 4.0, 4.0 / 3.2
+    assert "fastest dense (dense, q/k/v and gate/up fused) 2.0000x, per-Linear 1.0000x, grouped 1.2500x" in speed
+
+
+def test_decode_table_sparse_only(tmp_path):
+    d = {"model": "qwen3-14b", "prompt": 128, "gen": 256, "sparse": {**_variant(4.0), "ratio": "8:16"}}
+    path = tmp_path / "s.json"
+    path.write_text(json.dumps(d))
+    out = P.decode_table([str(path)])
+    assert "| Qwen3-14B | 128 / 256 | 8:16 fused layer | 4.0000 |" in out and "Speedup" not in out
+
+
+def _stats_csv(path, kernels):
+    with open(path, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
+        w.writeheader()
+        for name, calls, avg_us in kernels:
+            w.writerow({"Name": name, "Calls": calls, "TotalDurationNs": calls * avg_us * 1e3,
+                        "AverageNs": avg_us * 1e3, "Percentage": 1.0})
+
+
+@pytest.mark.parametrize("setup_calls", [0, 11])
+def test_decode_stats_roles_per_step(tmp_path, setup_calls):
+    """Roles summed per step from average x launches per step; set-up kernels
+    and the lm_head form timing calls (a few extra launches of a per-step
+    kernel) do not change the per-step figures."""
+    layers, steps = 32, 386  # llama-3.1-8b
+    ls = layers * steps
+    kernels = [
+        ("void nm_hip::nm_gemv_kernel<0, 32, 4, 1, true, 2, true>(nm_hip::Args)", ls, 23.0),
+        ("void nm_hip::nm_gemv_kernel<0, 16, 8, 4, true, 1, false>(nm_hip::Args)", 2 * ls, 10.0),
+        ("void nm_hip::nm_gemv_kernel<0, 32, 8, 1, true, 1, true>(nm_hip::Args)", ls, 9.5),
+        ("Cijk_Alik_Bljk_HHS_MT256x16x32", ls, 8.0),
+        ("Cijk_Ailk_Bljk_HHS_MT16x16x32", ls, 6.0),
+        ("Cijk_Ailk_Bljk_HHS_MT1x4x256", steps + setup_calls, 180.0),
+        ("void softmax_warp_forward<c10::Half>", ls, 5.0),
+        ("void at::native::reduce_kernel<ArgMax>", steps, 5.0),
+        ("void distribution_elementwise_grid_stride_kernel<normal>", 232, 48.0),  # random init: set-up
+    ]
+    _stats_csv(tmp_path / "k.csv", kernels)
+    (tmp_path / "d.json").write_text(json.dumps({"model": "llama-3.1-8b", "prompt": 128, "gen": 256,
+                                                 "sparse": {"ms_per_token": 2.6, "ratio": "32:64"}}))
+    md = tmp_path / "out.md"
+    P.decode_stats(str(tmp_path / "k.csv"), str(tmp_path / "d.json"), str(md), "cmd")
+    text = md.read_text()
+    assert f"{steps} decode steps were profiled" in text
+
+    def role(name):
+        line = next(ln for ln in text.splitlines() if ln.startswith(f"| {name} |"))
+        return float(line.split(" | ")[1])
+
+    assert role("sparse GEMV: gate/up pair + RMSNorm + SiLU*mul") == pytest.approx(32 * 23.0)
+    assert role("sparse GEMV: o or down + residual") == pytest.approx(64 * 10.0)
+    assert role("sparse GEMV: q/k/v + RMSNorm + RoPE + cache write") == pytest.approx(32 * 9.5)
+    assert role("attention product (hipBLASLt)") == pytest.approx(32 * 14.0)
+    assert role("lm_head (hipBLASLt, dense)") == pytest.approx(180.0)
+    assert role("attention softmax") == pytest.approx(32 * 5.0)
+    assert role("other (embedding, norm, mask, greedy token, position)") == pytest.approx(5.0)
+    total = 32 * 23.0 + 640 + 32 * 9.5 + 32 * 14.0 + 180 + 160 + 5
+    assert role("total kernel time") == pytest.approx(total, abs=0.1)
+    assert "distribution_elementwise" not in text
