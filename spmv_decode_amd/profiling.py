@@ -116,7 +116,8 @@ def stats(stats_csv, bench_json, md_path, cmd):
     rows = _read(stats_csv)
     b = json.loads(Path(bench_json).read_text()) if bench_json else None
     lines = ["# rocprofv3 kernel statistics: bench.py (Llama-3.1-8B decode-token sparse GEMVs, 32:64, fp16)", "",
-             "Command (repository root, one MI355X):", "", "```", "export TMPDIR=/tmp", cmd,
+             "Commands (repository root, one MI355X, one call):", "", "```", "export TMPDIR=/tmp",
+             "python -u bench.py > gpurun_out/bench.json", cmd,
              "python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv "
              "--bench gpurun_out/bench.json --md <this file>", "```", "",
              "The run covers the decode-form step graph (q/k/v + RMSNorm + RoPE + cache write, o + residual, gate/up",
@@ -389,8 +390,9 @@ def main(argv=None):
         cpu(a.bench, a.md, "python -u bench.py --cpu-detail --cpu-decode > gpurun_out/bench_cpu.json")
     else:
         stats(a.csv, a.bench, a.md,
-              "rocprofv3 --kernel-trace --stats -d gpurun_out/prof_bench -o bench --output-format csv -- "
-              "python -u bench.py --no-decode --no-cpu")
+              "rocprofv3 --kernel-trace --stats -d /tmp/prof_bench -o bench --output-format csv -- "
+              "python -u bench.py --no-decode --no-cpu && mkdir -p gpurun_out/prof_bench && "
+              "cp $(find /tmp/prof_bench -name bench_kernel_stats.csv) gpurun_out/prof_bench/")
     return 0
 
 
