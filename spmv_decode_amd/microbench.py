@@ -170,13 +170,15 @@ def pair_bytes(gate: RotatingCase, up: RotatingCase) -> int:
     return 2 * (elem * gate.w * gate.n_out + gate.w) + elem * gate.n_in + elem * gate.n_out
 
 
-def decode_form_bytes(cls, nnz=32, m=64, dim=4096, inter=14336, qd=4096, kvd=1024, hd=128) -> int:
+def decode_form_bytes(cls, nnz=32, m=64, dim=4096, inter=14336, qd=4096, kvd=1024, hd=128, qk_norm=False) -> int:
     """Algorithmic bytes of one decode-form launch (fp16): packed weights and
-    index bytes, activations once, norm weights, residual reads, outputs (the
-    k/v outputs are the cache slots written) and the RoPE table row."""
+    index bytes, activations once, norm weights (Qwen3's per-head q/k norms
+    with qk_norm), residual reads, outputs (the k/v outputs are the cache slots
+    written) and the RoPE table row."""
     wd, wi, wq = dim // m * nnz, inter // m * nnz, qd // m * nnz
     if cls == "qkv_decode":
-        return sum(2 * wd * h + wd for h in (qd, kvd, kvd)) + 2 * dim + 2 * dim + 2 * (qd + 2 * kvd) + 8 * (hd // 2)
+        return (sum(2 * wd * h + wd for h in (qd, kvd, kvd)) + 2 * dim + 2 * dim + 2 * (qd + 2 * kvd) + 8 * (hd // 2)
+                + (4 * hd if qk_norm else 0))
     if cls == "o_resid":
         return 2 * wq * dim + wq + 2 * qd + 2 * dim + 2 * dim
     if cls == "gate_up_pair_norm":
@@ -197,8 +199,8 @@ class DecodeForms:
     KV_SLOTS = 512
 
     def __init__(self, nnz=32, m=64, rotate_bytes=1 << 30, dim=4096, inter=14336, n_heads=32, n_kv_heads=8,
-                 head_dim=128, device="cuda", seed=50, min_copies=1):
-        self.nnz, self.m, self.hd = nnz, m, head_dim
+                 head_dim=128, device="cuda", seed=50, min_copies=1, qk_norm=False):
+        self.nnz, self.m, self.hd, self.qk_norm = nnz, m, head_dim, qk_norm
         self.dim, self.inter = dim, inter
         qd, kvd = n_heads * head_dim, n_kv_heads * head_dim
         self.hs = {"q": qd, "kv": kvd}
@@ -225,6 +227,10 @@ class DecodeForms:
         self.h2 = torch.empty(1, dim, dtype=f16, device=device)
         self.ln1 = (torch.rand(dim, generator=g, device=device) + 0.5).to(f16)
         self.ln2 = (torch.rand(dim, generator=g, device=device) + 0.5).to(f16)
+        self.q_norm = self.k_norm = None
+        if qk_norm:  # Qwen3's per-head norms, folded into the q/k/v launch as the decoder does
+            self.q_norm = (torch.rand(head_dim, generator=g, device=device) + 0.5).to(f16)
+            self.k_norm = (torch.rand(head_dim, generator=g, device=device) + 0.5).to(f16)
         self.qo = torch.zeros(n_heads, head_dim + KEY_PAD, dtype=f16, device=device)  # the decoder's query rows
         self.pair_out = torch.empty(1, inter, dtype=f16, device=device)
         S = self.KV_SLOTS
@@ -244,7 +250,7 @@ class DecodeForms:
         if cls == "qkv_decode":
             nmsparse_qkv_decode(self.x, self.q.mats[i], self.k.mats[i], self.v.mats[i], nnz, m, q_out=self.qo,
                                 k_cache_t=self.k_cache, v_cache_t=self.v_cache, pos=self.pos, rope_table=self.rope,
-                                head_dim=self.hd, norm=(self.ln1, 1e-5))
+                                head_dim=self.hd, norm=(self.ln1, 1e-5), q_norm=self.q_norm, k_norm=self.k_norm)
         elif cls == "o_resid":
             nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i], self.h1, residual=self.x)], nnz, m)
         elif cls == "gate_up_pair_norm":
@@ -256,7 +262,8 @@ class DecodeForms:
             raise ValueError(cls)
 
     def bytes(self, cls) -> int:
-        return decode_form_bytes(cls, self.nnz, self.m, self.dim, self.inter, self.hs["q"], self.hs["kv"], self.hd)
+        return decode_form_bytes(cls, self.nnz, self.m, self.dim, self.inter, self.hs["q"], self.hs["kv"], self.hd,
+                                 self.qk_norm)
 
     def time(self, cls, reps=20) -> float:
         return graph_us_per_launch([lambda i=i: self.launch(cls, i) for i in range(self.copies[cls])], reps)
@@ -468,6 +475,65 @@ def write_stripe_md(res, path, cmd):
     Path(path).write_text("\n".join(lines) + "\n")
 
 
+def decode_classes(model, ratios, reps=20, warmup=5, rotate_bytes=1 << 30, log=print):
+    """The decoder's four fused launches (DecodeForms) at one model's shapes,
+    per ratio: us per launch (median of graph replays over >= 1 GiB of rotated
+    weights per class), algorithmic GB/s and % of the 8 TB/s HBM peak, and the
+    sum over one token's launches (layers x 4)."""
+    from .decode.model import CONFIGS
+
+    cfg = CONFIGS[model]
+    res = {}
+    for nnz, m in ratios:
+        forms = DecodeForms(nnz, m, rotate_bytes=rotate_bytes, dim=cfg.dim, inter=cfg.inter, n_heads=cfg.n_heads,
+                            n_kv_heads=cfg.n_kv_heads, head_dim=cfg.head_dim, qk_norm=cfg.qk_norm)
+        per, tok_us, tok_bytes = {}, 0.0, 0
+        for c in DECODE_CLASSES:
+            fns = [lambda i=i, c=c: forms.launch(c, i) for i in range(forms.copies[c])]
+            us, sd = graph_us_per_launch(fns, reps, warmup, stats=True)
+            b = forms.bytes(c)
+            per[c] = {"us": round(us, 3), "us_sd": round(sd, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
+                      "pct_peak": round(b / us / 1e3 / 80.0, 1), "copies": forms.copies[c]}
+            tok_us += us * cfg.n_layers
+            tok_bytes += b * cfg.n_layers
+            log(f"{model} {nnz}:{m} {c:18s}: {us:7.2f} +- {sd:.2f} us {per[c]['GBps']:7.1f} GB/s "
+                f"({per[c]['pct_peak']}%)")
+        res[f"{nnz}:{m}"] = {"classes": per, "token_us": round(tok_us, 1), "token_bytes": tok_bytes,
+                             "token_GBps": round(tok_bytes / tok_us / 1e3, 1),
+                             "token_pct_peak": round(tok_bytes / tok_us / 1e3 / 80.0, 1)}
+        log(f"{model} {nnz}:{m}: one token's {4 * cfg.n_layers} sparse launches {tok_us:.1f} us, "
+            f"{res[f'{nnz}:{m}']['token_GBps']} GB/s")
+        del forms
+        torch.cuda.empty_cache()
+    return res
+
+
+def write_decode_classes_md(model, res, path, cmd):
+    from .decode.model import CONFIGS
+
+    cfg = CONFIGS[model]
+    names = {"qkv_decode": "q/k/v + input RMSNorm + RoPE + KV-cache write" + (" + q/k head norms" if cfg.qk_norm else ""),
+             "o_resid": "o + residual", "gate_up_pair_norm": "gate/up pair + RMSNorm + SiLU*mul",
+             "down_resid": "down + residual"}
+    lines = [f"# Sparse GEMV launches of the fused decoder layer: {cfg.name} shapes (MI355X, fp16, batch 1)", "",
+             "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
+             f"The decoder's four launches per layer at {cfg.name}'s shapes (dim {cfg.dim}, intermediate "
+             f"{cfg.inter}, {cfg.n_heads} query / {cfg.n_kv_heads} KV heads, head_dim {cfg.head_dim}), each",
+             "rotating over >= 1 GiB of distinct packed weights in one hipGraph (so neither L2 nor the 256 MB",
+             "Infinity Cache serves them), the library's default plan; median +- sd over the replays, per launch,",
+             "inter-kernel gap included. GB/s counts the algorithmic bytes of the launch (packed weights and index,",
+             "activations once, norm weights, residual, outputs, RoPE row); % of the 8 TB/s HBM peak. 'Token' sums",
+             f"one decode token's {4 * cfg.n_layers} launches ({cfg.n_layers} layers).", "",
+             "| N:M | Launch | us (median +- sd) | Algorithmic bytes | GB/s | % peak |", "|---|---|---|---|---|---|"]
+    for ratio, r in res.items():
+        for c, v in r["classes"].items():
+            lines.append(f"| {ratio} | {names[c]} | {v['us']:.2f} +- {v['us_sd']:.2f} | {v['bytes']:,} | "
+                         f"{v['GBps']:.0f} | {v['pct_peak']:.1f}% |")
+        lines.append(f"| {ratio} | token ({4 * cfg.n_layers} launches) | {r['token_us']:.1f} | {r['token_bytes']:,} | "
+                     f"{r['token_GBps']:.0f} | {r['token_pct_peak']:.1f}% |")
+    Path(path).write_text("\n".join(lines) + "\n")
+
+
 def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     """Workload for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
     three copies of a 256 MiB buffer (the known-size calibration kernel), then
@@ -549,7 +615,19 @@ def main(argv=None):
     p.add_argument("--stripe-ceiling", action="store_true",
                    help="measure launches that only read each Llama shape's weights in the GEMV's pattern")
     p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
+    p.add_argument("--decode-classes", default=None, metavar="MODEL",
+                   help="time the fused decoder layer's four launches at MODEL's shapes (llama-3.1-8b, qwen3-14b, "
+                        "qwen3-32b) for each --ratios entry")
     a = p.parse_args(argv)
+    if a.decode_classes:
+        res = decode_classes(a.decode_classes, _parse_pairs(a.ratios, ":"), a.reps, a.warmup, a.rotate_mib << 20,
+                             log=lambda s: print(s, flush=True))
+        if a.json:
+            Path(a.json).write_text(json.dumps(res, indent=1))
+        if a.md:
+            write_decode_classes_md(a.decode_classes, res, a.md,
+                                    " ".join(["python -u -m spmv_decode_amd.microbench", *(argv or sys.argv[1:])]))
+        return 0
     if a.read_ceiling:
         res = read_ceiling(log=lambda s: print(s, flush=True))
         if a.json:
