@@ -198,7 +198,8 @@ def test_dense_gemv_forms_agree_and_are_applied_per_shape():
     at, mlp = model.layers[1].self_attn, model.layers[1].mlp
     assert at.k_proj.gemv_form == at.v_proj.gemv_form == "mv" and mlp.down_proj.gemv_form == "mv"
     assert mlp.gate_proj.gemv_form == "mm" and model.lm_head.gemv_form == "mv"
-    assert mlp.w13_form == "mv" and at.wqkv_form == "mm"  # (qd + 2 kvd, dim) has no entry: nn.Linear's form
+    # the fused q/k/v copy takes the form of its own shape, which may coincide with another entry's
+    assert mlp.w13_form == "mv" and at.wqkv_form == model.gemv_forms.get((qd + 2 * kvd, c.dim), "mm")
     torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
     model.set_dense_fusion("none")
     torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
