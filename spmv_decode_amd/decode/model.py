@@ -407,6 +407,8 @@ class Decoder(nn.Module):
         (both forms accumulate in fp32; the roundings can differ in the last bit)."""
         groups = {}
         for w, _, _ in self._dense_gemv_sites():
+            if not w.is_cuda:
+                raise RuntimeError(f"tune_dense_gemv times the products on the GPU; a dense weight is on {w.device}")
             groups.setdefault(tuple(w.shape), {})[w.data_ptr()] = w
         report = {}
         for shape, ws in groups.items():

@@ -203,6 +203,8 @@ def test_dense_gemv_forms_agree_and_are_applied_per_shape():
     torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
     model.set_dense_fusion("none")
     torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+    with pytest.raises(RuntimeError, match="on the GPU"):
+        model.tune_dense_gemv()
 
 
 def test_swap_applies_to_decoder_layout():
