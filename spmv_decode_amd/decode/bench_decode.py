@@ -18,7 +18,10 @@ The sparse model runs the fused layer (norms, RoPE, cache write and residuals
 inside the GEMV launches); `--per-linear` also times it with one launch per
 Linear and PyTorch norms/RoPE (the step structure of the unfused dense
 model), `--grouped` with one q/k/v and one gate/up launch and PyTorch
-norms/RoPE (the structure of the fused dense modes).
+norms/RoPE (the structure of the fused dense modes). `--fixed-ctx 512` times
+the reference benchmark's protocol instead (caches of random values, one
+step at a fixed position replayed; runner.fixed_context_ms) with its
+`RESULT CTX=...` line.
 Prints a `RESULT` line per model variant (like the reference benchmarks,
 benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:186-189) and one JSON line.
 """
@@ -34,7 +37,7 @@ import torch
 
 from ..nmsparse_linear import swap_to_nmsparse
 from .model import CONFIGS, Decoder, init_weights_
-from .runner import GraphDecoder
+from .runner import GraphDecoder, fixed_context_ms
 
 
 def linear_bytes(cfg, m: int) -> int:
@@ -87,6 +90,12 @@ def main(argv=None):
     p.add_argument("--grouped", action="store_true",
                    help="also time the sparse model with one q/k/v and one gate/up launch and PyTorch norms/RoPE "
                         "(the step structure of the fused dense modes)")
+    p.add_argument("--fixed-ctx", type=int, default=0, metavar="CTX",
+                   help="time the reference benchmark's protocol instead: one decode step at position CTX over "
+                        "random-filled caches, replayed (runner.fixed_context_ms)")
+    p.add_argument("--fc-warmup", type=int, default=30)
+    p.add_argument("--fc-repeat", type=int, default=30)
+    p.add_argument("--fc-inner", type=int, default=10)
     p.add_argument("--json", default=None)
     a = p.parse_args(argv)
 
@@ -115,6 +124,28 @@ def main(argv=None):
     prompt = torch.randint(0, cfg.vocab, (a.prompt,), generator=torch.Generator().manual_seed(a.seed + 1))
     res = {"model": cfg.name, "prompt": a.prompt, "gen": a.gen, "dtype": "fp16", "batch": 1,
            "gpu": torch.cuda.get_device_name(dev)}
+    if a.fixed_ctx:
+        res.update(protocol="fixed_context", ctx=a.fixed_ctx, warmup=a.fc_warmup, repeat=a.fc_repeat,
+                   inner=a.fc_inner)
+        del res["prompt"], res["gen"]
+
+    def measure(label, tag):
+        """Time the model as it stands under the selected protocol; print the RESULT line."""
+        if not a.fixed_ctx:
+            v = run_variant(model, cfg, prompt, a.gen, label, log)
+            print(f"RESULT model={cfg.name} {tag} prompt={a.prompt} gen={a.gen} "
+                  f"decode_ms_per_token={v['ms_per_token']:.6f} median={v['ms_per_token_median_of_16']:.6f}",
+                  flush=True)
+            return v
+        r = fixed_context_ms(model, a.fixed_ctx, a.fc_warmup, a.fc_repeat, a.fc_inner)
+        log(f"{label}: fixed context {a.fixed_ctx}, median {r['median']:.4f} ms")
+        print(f"RESULT CTX={a.fixed_ctx} {tag} dtype=float16 measurement=fixed_context_hip_graph "
+              f"warmup={a.fc_warmup} repeat={a.fc_repeat} decode_ms_per_token={r['median']:.6f} "
+              f"mean={r['mean']:.6f} stdev={r['stdev']:.6f}", flush=True)
+        return {"ms_per_token": round(r["median"], 4), "ms_per_token_mean": round(r["mean"], 4),
+                "stdev": round(r["stdev"], 4), "tokens_per_s": round(1e3 / r["median"], 2),
+                "finite_logits": r["finite_logits"]}
+
     if not a.no_dense:
         modes = [a.dense_fusion] + ([m for m in Decoder.DENSE_FUSIONS if m != a.dense_fusion]
                                     if a.dense_variants else [])
@@ -124,16 +155,13 @@ def main(argv=None):
                 for shape, r in model.tune_dense_gemv().items():
                     log(f"dense GEMV {shape}: x*W^T {r['mm']} us, W*x {r['mv']} us -> {r['form']}")
                     res.setdefault("dense_gemv_forms", {})[shape] = r
-            d = run_variant(model, cfg, prompt, a.gen, f"dense ({mode} fused)", log)
+            d = measure(f"dense ({mode} fused)", f"dense_float16 fusion={mode}")
             d["linear_bytes_per_token"] = linear_bytes(cfg, 0)
             d["fusion"] = mode
             if mode == a.dense_fusion:
                 res["dense"] = d
             else:
                 res.setdefault("dense_variants", {})[mode] = d
-            print(f"RESULT model={cfg.name} dense_float16 fusion={mode} prompt={a.prompt} gen={a.gen} "
-                  f"decode_ms_per_token={d['ms_per_token']:.6f} median={d['ms_per_token_median_of_16']:.6f}",
-                  flush=True)
         model.set_dense_fusion("none")
     if a.m:
         t0 = time.time()
@@ -145,34 +173,27 @@ def main(argv=None):
             for shape, r in model.tune_dense_gemv().items():
                 log(f"dense GEMV {shape}: x*W^T {r['mm']} us, W*x {r['mv']} us -> {r['form']}")
                 res.setdefault("dense_gemv_forms", {})[shape] = r
-        s = run_variant(model, cfg, prompt, a.gen, "sparse", log)
+        tag = f"M={a.m}({a.m // 2}:{a.m})"
+        s = measure("sparse", tag)
         s["linear_bytes_per_token"] = linear_bytes(cfg, a.m)
         s["ratio"] = f"{a.m // 2}:{a.m}"
         res["sparse"] = s
-        print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) prompt={a.prompt} gen={a.gen} "
-              f"decode_ms_per_token={s['ms_per_token']:.6f} median={s['ms_per_token_median_of_16']:.6f}", flush=True)
         if "dense" in res:
             res["speedup_sparse_vs_dense"] = round(res["dense"]["ms_per_token"] / s["ms_per_token"], 4)
             for mode, d in res.get("dense_variants", {}).items():
                 res[f"speedup_sparse_vs_dense_{mode}"] = round(d["ms_per_token"] / s["ms_per_token"], 4)
         if a.per_linear:
             model.set_launch_mode("per_linear")
-            u = run_variant(model, cfg, prompt, a.gen, "sparse per-Linear", log)
+            u = measure("sparse per-Linear", f"{tag} per_linear")
             model.set_launch_mode("fused")
             res["sparse_per_linear"] = u
-            print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) per_linear prompt={a.prompt} gen={a.gen} "
-                  f"decode_ms_per_token={u['ms_per_token']:.6f} median={u['ms_per_token_median_of_16']:.6f}",
-                  flush=True)
             if "dense" in res:
                 res["speedup_sparse_per_linear_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
         if a.grouped:
             model.set_launch_mode("grouped")
-            u = run_variant(model, cfg, prompt, a.gen, "sparse grouped", log)
+            u = measure("sparse grouped", f"{tag} grouped")
             model.set_launch_mode("fused")
             res["sparse_grouped"] = u
-            print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) grouped prompt={a.prompt} gen={a.gen} "
-                  f"decode_ms_per_token={u['ms_per_token']:.6f} median={u['ms_per_token_median_of_16']:.6f}",
-                  flush=True)
             if "dense" in res:
                 res["speedup_sparse_grouped_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
     print(json.dumps(res), flush=True)

@@ -53,6 +53,63 @@ def cache_length(max_seq: int) -> int:
     return -(-max_seq // CACHE_ALIGN) * CACHE_ALIGN
 
 
+@torch.no_grad()
+def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 30, inner: int = 10,
+                     seed: int = 1234, token_id: int = 123, device="cuda") -> dict:
+    """The reference benchmark's fixed-context protocol
+    (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:144-189): KV caches for
+    ctx + 1 positions filled with N(0, 0.02), one decode step of `token_id` at
+    position `ctx` (with its greedy next token; the reference samples) captured
+    as one hipGraph, `warmup` replays, then `repeat` samples of `inner`
+    replays each; every replay decodes the same position. Returns the median,
+    mean and stdev of the samples in ms per replay, and the samples."""
+    if min(ctx, warmup, repeat, inner) < 1:
+        raise ValueError("ctx, warmup, repeat and inner must be positive")
+    dev = torch.device(device)
+    hd = model.cfg.head_dim
+    model.setup_cache(cache_length(ctx + 1), dev, dtype=model.embed_tokens.weight.dtype)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for k, v in zip(model.k_cache_t, model.v_cache_t):
+        k[:, :hd].normal_(0.0, 0.02, generator=gen)  # the mask and padding rows stay as set up
+        v.normal_(0.0, 0.02, generator=gen)
+    token = torch.full((1, 1), token_id, dtype=torch.long, device=dev)
+    pos = torch.full((1,), ctx, dtype=torch.long, device=dev)
+    nxt = torch.zeros(1, dtype=torch.long, device=dev)
+
+    def step():
+        logits = model.forward_step(token, pos)
+        greedy_token(logits, out=nxt)
+        return logits
+
+    stream = torch.cuda.Stream(device=dev)
+    stream.wait_stream(torch.cuda.current_stream(dev))
+    with torch.cuda.stream(stream):
+        for _ in range(3):  # workspaces and library handles are created outside the capture
+            step()
+    torch.cuda.current_stream(dev).wait_stream(stream)
+    torch.cuda.synchronize(dev)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=stream):
+        logits = step()
+    for _ in range(warmup):
+        graph.replay()
+    torch.cuda.synchronize(dev)
+    samples = []
+    for _ in range(repeat):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(inner):
+            graph.replay()
+        b.record()
+        b.synchronize()
+        samples.append(a.elapsed_time(b) / inner)
+    finite = bool(torch.isfinite(logits).all().item())
+    del graph
+    return {"median": statistics.median(samples), "mean": statistics.mean(samples),
+            "stdev": statistics.stdev(samples) if repeat > 1 else 0.0, "samples": samples,
+            "finite_logits": finite, "token": int(nxt.item())}
+
+
 class GraphDecoder:
     def __init__(self, model: Decoder, max_seq: int, device="cuda"):
         """max_seq: positions the decode may use (prompt + generated tokens);

@@ -213,10 +213,13 @@ def decode_table(json_paths):
     fusion_label = {"qkv": "dense, q/k/v fused", "none": "dense, one GEMM per Linear",
                     "qkv_gate_up": "dense, q/k/v and gate/up fused"}
     rows, speed = [], []
-    for path in json_paths:
-        d = json.loads(Path(path).read_text())
+    docs = [json.loads(Path(path).read_text()) for path in json_paths]
+    fixed = bool(docs) and all(d.get("protocol") == "fixed_context" for d in docs)
+    if any(d.get("protocol") == "fixed_context" for d in docs) and not fixed:
+        raise SystemExit("decode-table: do not mix fixed-context and generation runs in one table")
+    for d in docs:
         model = names.get(d["model"], d["model"])
-        pg = f"{d['prompt']} / {d['gen']}"
+        pg = f"CTX {d['ctx']}" if fixed else f"{d['prompt']} / {d['gen']}"
         ratio = d.get("sparse", {}).get("ratio", "")
         sparse_bytes = d.get("sparse", {}).get("linear_bytes_per_token")
         dense = [("dense", d["dense"])] if d.get("dense") else []
@@ -229,8 +232,10 @@ def decode_table(json_paths):
             if not v:
                 continue
             nb = v.get("linear_bytes_per_token", nbytes)
-            rows.append(f"| {model} | {pg} | {label} | {v['ms_per_token']:.4f} | {v['ms_per_token_median_of_16']:.4f} | "
-                        f"{v['tokens_per_s']} | {nb:,} |")
+            second = (f"{v['ms_per_token_mean']:.4f} | {v['stdev']:.4f}" if fixed
+                      else f"{v['ms_per_token_median_of_16']:.4f}")
+            rows.append(f"| {model} | {pg} | {label} | {v['ms_per_token']:.4f} | {second} | {v['tokens_per_s']} | "
+                        f"{nb:,} |")
         if "speedup_sparse_vs_dense" in d:
             line = f"{model} {ratio}: fused layer {d['speedup_sparse_vs_dense']:.4f}x"
             if "speedup_sparse_per_linear_vs_dense" in d:
@@ -248,9 +253,55 @@ def decode_table(json_paths):
                     if d.get(key):
                         line += f", {lab} {best['ms_per_token'] / d[key]['ms_per_token']:.4f}x"
             speed.append(line)
-    head = ["| Model | Prompt / gen | Variant | ms/token (mean) | median of 16-step chunks | tokens/s | "
-            "Linear bytes/token |", "|---|---|---|---|---|---|---|"]
+    if fixed:
+        head = ["| Model | Context | Variant | ms/token (median of samples) | mean | stdev | tokens/s | "
+                "Linear bytes/token |", "|---|---|---|---|---|---|---|---|"]
+    else:
+        head = ["| Model | Prompt / gen | Variant | ms/token (mean) | median of 16-step chunks | tokens/s | "
+                "Linear bytes/token |", "|---|---|---|---|---|---|---|"]
     return "\n".join(head + rows + [""] + [f"Speedup over dense: {x}." for x in speed]) + "\n"
+
+
+# The reference's published decode table (README.md:86-119): A100-SXM4-80GB, CTX 512, fp16, batch 1,
+# median ms/token of its fixed-context benchmark; dense, then by M at N = M/2.
+REFERENCE_A100_CTX512 = {
+    "llama-3.1-8b": (10.3904, {4: 8.0753, 8: 8.1507, 16: 6.9512, 32: 6.9400, 64: 6.8521, 128: 7.0335, 256: 7.2585}),
+    "qwen3-14b": (25.0951, {4: 20.3801, 8: 20.4739, 16: 18.0455, 32: 17.8283, 64: 17.6093, 128: 17.9491,
+                            256: 19.1014}),
+    "qwen3-32b": (52.3758, {4: 39.8042, 8: 38.5639, 16: 33.7534, 32: 33.7054, 64: 33.7408, 128: 34.4702,
+                            256: 36.5712}),
+}
+
+
+def fixed_compare(json_paths):
+    """Fixed-context (`bench_decode --fixed-ctx`) results next to the
+    reference's published table: per model, this build's dense (its headline
+    structure) and each ratio's sparse ms/token with the speedup over that
+    dense, then the reference's figures and speedups."""
+    names = {"llama-3.1-8b": "Llama-3.1-8B", "qwen3-14b": "Qwen3-14B", "qwen3-32b": "Qwen3-32B"}
+    dense, sparse = {}, {}
+    for path in json_paths:
+        d = json.loads(Path(path).read_text())
+        if d.get("protocol") != "fixed_context":
+            raise SystemExit(f"fixed-compare: {path} is not a --fixed-ctx run")
+        if d.get("dense"):
+            dense[d["model"]] = d["dense"]["ms_per_token"]
+        if d.get("sparse"):
+            m = int(d["sparse"]["ratio"].split(":")[1])
+            sparse.setdefault(d["model"], {})[m] = d["sparse"]["ms_per_token"]
+    lines = ["| Model | Pattern | This build, MI355X: ms/token | speedup over its dense | Reference, A100: ms/token "
+             "| speedup over its dense |", "|---|---|---|---|---|---|"]
+    for model in sorted(set(dense) | set(sparse), key=list(names).index):
+        rd, rs = REFERENCE_A100_CTX512[model]
+        ours = dense.get(model)
+        lines.append(f"| {names[model]} | dense | {ours:.4f} | 1.000x | {rd:.4f} | 1.000x |" if ours else
+                     f"| {names[model]} | dense | - | - | {rd:.4f} | 1.000x |")
+        for m, v in sorted(sparse.get(model, {}).items()):
+            sp = f"{ours / v:.3f}x" if ours else "-"
+            rv = rs.get(m)
+            ref = f"{rv:.4f} | {rd / rv:.3f}x" if rv else "- | -"
+            lines.append(f"| {names[model]} | {m // 2}:{m} | {v:.4f} | {sp} | {ref} |")
+    return "\n".join(lines) + "\n"
 
 
 def sweep_stats(trace_csv, sweep_csv, md_path, cmd):
@@ -365,6 +416,8 @@ def main(argv=None):
     sw.add_argument("--sweep", required=True, help="the microbench --csv of the same run")
     sw.add_argument("--md", required=True)
     sw.add_argument("--command", dest="command_line", required=True)
+    fcmp = sub.add_parser("fixed-compare")
+    fcmp.add_argument("json", nargs="+", help="bench_decode --fixed-ctx --json files")
     dt = sub.add_parser("decode-table")
     dt.add_argument("json", nargs="+", help="bench_decode --json files")
     ds = sub.add_parser("decode-stats")
@@ -384,6 +437,8 @@ def main(argv=None):
         sweep_stats(a.trace, a.sweep, a.md, a.command_line)
     elif a.cmd == "decode-table":
         print(decode_table(a.json), end="")
+    elif a.cmd == "fixed-compare":
+        print(fixed_compare(a.json), end="")
     elif a.cmd == "decode-stats":
         decode_stats(a.csv, a.decode, a.md, a.command_line)
     elif a.cmd == "cpu":

@@ -318,6 +318,27 @@ def test_tuned_dense_decode_replays_match_eager(gpu, fusion):
 
 
 @pytest.mark.gpu
+def test_fixed_context_protocol_dense_and_sparse(gpu):
+    """The reference benchmark's protocol (one step at a fixed position over
+    random-filled caches, replayed): finite logits, and an eager step at the
+    same position afterwards picks the token the replays picked."""
+    from spmv_decode_amd.decode.runner import fixed_context_ms
+
+    cfg = tiny_config(qk_norm=True)
+    torch.manual_seed(0)
+    model = Decoder(cfg).to("cuda", torch.float16)
+    init_weights_(model, seed=2, std=0.05)
+    for sparse in (False, True):
+        if sparse:
+            swap_to_nmsparse(model, 16, "cuda", seed=3, init="device", keep_dense=False)
+        r = fixed_context_ms(model, 20, warmup=2, repeat=3, inner=2)
+        assert r["finite_logits"] and r["median"] > 0 and len(r["samples"]) == 3
+        with torch.no_grad():
+            logits = model.forward_step(torch.tensor([[123]], device="cuda"), torch.tensor([20], device="cuda"))
+        assert int(torch.argmax(logits, dim=-1)) == r["token"], sparse
+
+
+@pytest.mark.gpu
 def test_restored_compressed_checkpoint_decodes_identically(gpu):
     """A swapped model saved with torch.save and restored into a fresh
     skeleton (weights_only load) produces bit-identical logits."""

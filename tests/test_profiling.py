@@ -47,6 +47,49 @@ def test_decode_table_sparse_only(tmp_path):
     assert "| Qwen3-14B | 128 / 256 | 8:16 fused layer | 4.0000 |" in out and "Speedup" not in out
 
 
+def test_decode_table_fixed_context(tmp_path):
+    fc = lambda ms, **kw: {"ms_per_token": ms, "ms_per_token_mean": ms + 0.01, "stdev": 0.002,  # noqa: E731
+                           "tokens_per_s": round(1e3 / ms, 2), "linear_bytes_per_token": 1000, **kw}
+    d = {"model": "llama-3.1-8b", "protocol": "fixed_context", "ctx": 512, "dense": fc(5.0, fusion="qkv"),
+         "sparse": fc(2.5, ratio="32:64"), "speedup_sparse_vs_dense": 2.0}
+    path = tmp_path / "f.json"
+    path.write_text(json.dumps(d))
+    out = P.decode_table([str(path)])
+    assert "| Model | Context | Variant | ms/token (median of samples) | mean | stdev |" in out
+    assert "| Llama-3.1-8B | CTX 512 | 32:64 fused layer | 2.5000 | 2.5100 | 0.0020 | 400.0 | 1,000 |" in out
+    gen = tmp_path / "g.json"
+    gen.write_text(json.dumps({"model": "qwen3-14b", "prompt": 1, "gen": 2, "sparse": {**_variant(4.0), "ratio": "x"}}))
+    with pytest.raises(SystemExit, match="mix"):
+        P.decode_table([str(path), str(gen)])
+
+
+def test_fixed_compare_against_the_reference_table(tmp_path):
+    fc = lambda ms, **kw: {"ms_per_token": ms, "ms_per_token_mean": ms, "stdev": 0.0,  # noqa: E731
+                           "tokens_per_s": 1.0, **kw}
+    paths = []
+    for name, d in (("d", {"dense": fc(5.0, fusion="qkv")}), ("s4", {"sparse": fc(2.5, ratio="2:4")}),
+                    ("s64", {"sparse": fc(2.0, ratio="32:64")})):
+        path = tmp_path / f"{name}.json"
+        path.write_text(json.dumps({"model": "llama-3.1-8b", "protocol": "fixed_context", "ctx": 512, **d}))
+        paths.append(str(path))
+    out = P.fixed_compare(paths)
+    assert "| Llama-3.1-8B | dense | 5.0000 | 1.000x | 10.3904 | 1.000x |" in out
+    assert "| Llama-3.1-8B | 2:4 | 2.5000 | 2.000x | 8.0753 | 1.287x |" in out
+    assert "| Llama-3.1-8B | 32:64 | 2.0000 | 2.500x | 6.8521 | 1.516x |" in out
+    gen = tmp_path / "g.json"
+    gen.write_text(json.dumps({"model": "llama-3.1-8b", "prompt": 1, "gen": 2}))
+    with pytest.raises(SystemExit, match="not a --fixed-ctx run"):
+        P.fixed_compare([str(gen)])
+
+
+def test_fixed_context_rejects_non_positive_arguments():
+    from spmv_decode_amd.decode.model import Decoder, tiny_config
+    from spmv_decode_amd.decode.runner import fixed_context_ms
+
+    with pytest.raises(ValueError, match="positive"):
+        fixed_context_ms(Decoder(tiny_config()), 0)
+
+
 def _stats_csv(path, kernels):
     with open(path, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=["Name", "Calls", "TotalDurationNs", "AverageNs", "Percentage"])
