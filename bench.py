@@ -386,7 +386,9 @@ def decode_ms_per_token(m, log):
 
     from spmv_decode_amd.decode.bench_decode import linear_bytes, run_variant
     from spmv_decode_amd.decode.model import LLAMA31_8B, Decoder, init_weights_
+    from spmv_decode_amd.decode.runner import fixed_context_ms
     from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
+    from spmv_decode_amd.profiling import REFERENCE_A100_CTX512
 
     prev = torch.get_default_dtype()
     torch.set_default_dtype(torch.float16)
@@ -402,13 +404,17 @@ def decode_ms_per_token(m, log):
         model.set_dense_fusion(mode)
         forms.update(model.tune_dense_gemv())  # the faster hipBLASLt problem form per dense shape
         dense_by_fusion[mode] = run_variant(model, LLAMA31_8B, prompt, 256, f"dense ({mode} fused)", log)
+    model.set_dense_fusion("qkv")
+    fixed_dense = fixed_context_ms(model, 512)  # the reference benchmark's protocol, its dense structure
     model.set_dense_fusion("none")
     dense = dense_by_fusion["qkv"]
     swap_to_nmsparse(model, m, "cuda", seed=0, init="device", keep_dense=False)
     torch.cuda.empty_cache()
     sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)
+    fixed_sparse = fixed_context_ms(model, 512)
     model.set_launch_mode("per_linear")  # the dense model's step structure: isolates the GEMVs
     per_linear = run_variant(model, LLAMA31_8B, prompt, 256, "sparse per-Linear", log)
+    ref_dense, ref_sparse = REFERENCE_A100_CTX512["llama-3.1-8b"]
     del model
     torch.cuda.empty_cache()
     out = {"model": "llama-3.1-8b (random init)", "prompt": 128, "gen": 256,
@@ -423,9 +429,19 @@ def decode_ms_per_token(m, log):
            "sparse_per_linear_ms_per_token": per_linear["ms_per_token"],
            "speedup_sparse_per_linear_vs_dense": round(dense["ms_per_token"] / per_linear["ms_per_token"], 4),
            "sparse_linear_bytes_per_token": linear_bytes(LLAMA31_8B, m),
-           "dense_linear_bytes_per_token": linear_bytes(LLAMA31_8B, 0)}
+           "dense_linear_bytes_per_token": linear_bytes(LLAMA31_8B, 0),
+           "fixed_context_512": {
+               "protocol": "the reference benchmark's (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:144-189): "
+                           "random-filled caches, one step at position 512 replayed, median of 30 x 10 replays",
+               "dense_ms_per_token": round(fixed_dense["median"], 4),
+               "sparse_ms_per_token": round(fixed_sparse["median"], 4),
+               "speedup_sparse_vs_dense": round(fixed_dense["median"] / fixed_sparse["median"], 4),
+               "reference_a100_published": {"dense_ms_per_token": ref_dense, "sparse_ms_per_token": ref_sparse.get(m),
+                                            "speedup": round(ref_dense / ref_sparse[m], 4) if m in ref_sparse else None,
+                                            "source": "README.md:86-93"}}}
     log(f"decode: dense {out['dense_ms_per_token']} ms/token, sparse {out['sparse_ms_per_token']} ms/token, "
-        f"speedup {out['speedup_sparse_vs_dense']}x")
+        f"speedup {out['speedup_sparse_vs_dense']}x; fixed context 512: "
+        f"{out['fixed_context_512']['dense_ms_per_token']} / {out['fixed_context_512']['sparse_ms_per_token']} ms")
     return out
 
 
