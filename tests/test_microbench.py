@@ -81,3 +81,15 @@ def test_decode_classes_times_every_launch_at_a_qwen3_shape(gpu, tmp_path):
     assert r["token_bytes"] == cfg.n_layers * sum(v["bytes"] for v in r["classes"].values())
     assert r["token_us"] == pytest.approx(cfg.n_layers * sum(v["us"] for v in r["classes"].values()), rel=1e-3)
     (tmp_path / "r.json").write_text(json.dumps(res))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N > 1 exits with a message (one-GPU build) before any GPU work."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    root = Path(__file__).resolve().parent.parent
+    r = subprocess.run([sys.executable, str(root / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       timeout=120, cwd=root)
+    assert r.returncode == 2 and "one GPU only" in r.stderr and r.stdout == ""
