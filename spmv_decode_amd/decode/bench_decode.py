@@ -21,7 +21,8 @@ model), `--grouped` with one q/k/v and one gate/up launch and PyTorch
 norms/RoPE (the structure of the fused dense modes). `--fixed-ctx 512` times
 the reference benchmark's protocol instead (caches of random values, one
 step at a fixed position replayed; runner.fixed_context_ms) with its
-`RESULT CTX=...` line.
+`RESULT CTX=...` line; `--compile` runs every variant's step through
+torch.compile first, as the reference benchmark does.
 Prints a `RESULT` line per model variant (like the reference benchmarks,
 benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:186-189) and one JSON line.
 """
@@ -93,6 +94,10 @@ def main(argv=None):
     p.add_argument("--fixed-ctx", type=int, default=0, metavar="CTX",
                    help="time the reference benchmark's protocol instead: one decode step at position CTX over "
                         "random-filled caches, replayed (runner.fixed_context_ms)")
+    p.add_argument("--compile", action="store_true",
+                   help="torch.compile the decode step of every variant before capturing it, as the reference "
+                        "benchmark does (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:152); the sparse launches "
+                        "stay library calls the compiled code calls out to")
     p.add_argument("--fc-warmup", type=int, default=30)
     p.add_argument("--fc-repeat", type=int, default=30)
     p.add_argument("--fc-inner", type=int, default=10)
@@ -129,8 +134,16 @@ def main(argv=None):
                    inner=a.fc_inner)
         del res["prompt"], res["gen"]
 
+    eager_step = model.forward_step
+    if a.compile:
+        res["compiled"] = True
+
     def measure(label, tag):
         """Time the model as it stands under the selected protocol; print the RESULT line."""
+        if a.compile:  # a fresh compilation for each launch configuration
+            torch._dynamo.reset()
+            model.forward_step = torch.compile(eager_step, dynamic=False)
+            tag += " compiled"
         if not a.fixed_ctx:
             v = run_variant(model, cfg, prompt, a.gen, label, log)
             print(f"RESULT model={cfg.name} {tag} prompt={a.prompt} gen={a.gen} "

@@ -165,12 +165,14 @@ GEMV_FORMS = ("mm", "mv")
 def dense_gemv(x2d: torch.Tensor, weight: torch.Tensor, form: str = "mm", out=None) -> torch.Tensor:
     """y [1, n_out] = x2d [1, K] · weightᵀ through the BLAS library in one of
     two problem statements, which it serves with different kernels: "mm" (a
-    one-row product x · Wᵀ, what nn.Linear issues) or "mv" (a matrix-vector
-    product W · x). Which is faster depends on the shape (Decoder.tune_dense_gemv)."""
+    one-row product x · Wᵀ, what nn.Linear issues) or "mv" (the matrix-vector
+    product W · x, stated as a one-column product so that torch.compile also
+    leaves it to the library instead of generating its own kernel). Which is
+    faster depends on the shape (Decoder.tune_dense_gemv)."""
     if form == "mv":
         if out is None:
-            return torch.mv(weight, x2d.view(-1)).view(1, -1)
-        torch.mv(weight, x2d.view(-1), out=out.view(-1))
+            return torch.mm(weight, x2d.view(-1, 1)).view(1, -1)
+        torch.mm(weight, x2d.view(-1, 1), out=out.view(-1, 1))
         return out
     return torch.mm(x2d, weight.t(), out=out) if out is not None else torch.mm(x2d, weight.t())
 
