@@ -379,6 +379,11 @@ def main():
     print(json.dumps(result), flush=True)
 
 
+def _finite(v, digits=4):
+    """v rounded, or None (JSON null) when it is not a finite number."""
+    return round(v, digits) if v == v and abs(v) != float("inf") else None
+
+
 def decode_ms_per_token(m, log):
     """Random-init Llama-3.1-8B, prompt 128 + 256 greedy steps per variant,
     hipGraph replay (spmv_decode_amd.decode.bench_decode protocol)."""
@@ -405,12 +410,16 @@ def decode_ms_per_token(m, log):
         forms.update(model.tune_dense_gemv())  # the faster hipBLASLt problem form per dense shape
         dense_by_fusion[mode] = run_variant(model, LLAMA31_8B, prompt, 256, f"dense ({mode} fused)", log)
     def compiled_fixed(model):
-        """The reference protocol with its torch.compile: compile the step, then capture and replay."""
+        """The reference protocol with its torch.compile: compile the step, then capture and replay.
+        An extra figure: a compiler failure is reported in the JSON, not raised."""
         eager = model.forward_step
         torch._dynamo.reset()
         model.forward_step = torch.compile(eager, dynamic=False)
         try:
             return fixed_context_ms(model, 512)
+        except Exception as exc:  # noqa: BLE001 - torch.compile's failures have no common type
+            log(f"compiled fixed-context decode failed: {type(exc).__name__}: {exc}")
+            return {"median": float("nan"), "error": f"{type(exc).__name__}: {str(exc)[:300]}"}
         finally:
             model.forward_step = eager
             torch._dynamo.reset()
@@ -449,9 +458,10 @@ def decode_ms_per_token(m, log):
                "dense_ms_per_token": round(fixed_dense["median"], 4),
                "sparse_ms_per_token": round(fixed_sparse["median"], 4),
                "speedup_sparse_vs_dense": round(fixed_dense["median"] / fixed_sparse["median"], 4),
-               "compiled": {"dense_ms_per_token": round(fixed_dense_c["median"], 4),
-                            "sparse_ms_per_token": round(fixed_sparse_c["median"], 4),
-                            "speedup_sparse_vs_dense": round(fixed_dense_c["median"] / fixed_sparse_c["median"], 4),
+               "compiled": {"dense_ms_per_token": _finite(fixed_dense_c["median"]),
+                            "sparse_ms_per_token": _finite(fixed_sparse_c["median"]),
+                            "speedup_sparse_vs_dense": _finite(fixed_dense_c["median"] / fixed_sparse_c["median"]),
+                            "errors": [r["error"] for r in (fixed_dense_c, fixed_sparse_c) if "error" in r] or None,
                             "note": "torch.compile of each model's step before capture, as the reference "
                                     "benchmark (its published figures below are compiled)"},
                "reference_a100_published": {"dense_ms_per_token": ref_dense, "sparse_ms_per_token": ref_sparse.get(m),
