@@ -96,6 +96,32 @@ def test_llama_shapes_all_ratios(gpu, shape, nnz, m):
     check_parity(run(x, md, mi, nnz, m), x, md, mi, nnz, m, f"{shape} {nnz}:{m}")
 
 
+QWEN3_SHAPES = {  # (K, h) of the Qwen3-14B and Qwen3-32B Linears, at their benchmark ratios
+    "14b_q_o": (5120, 5120, 32, 64), "14b_k_v": (5120, 1024, 8, 16), "14b_gate_up": (5120, 17408, 32, 64),
+    "14b_down": (17408, 5120, 128, 256), "32b_q": (5120, 8192, 16, 32), "32b_o": (8192, 5120, 16, 32),
+    "32b_gate_up": (5120, 25600, 16, 32), "32b_down": (25600, 5120, 16, 32)}
+
+
+@pytest.mark.parametrize("shape", sorted(QWEN3_SHAPES))
+def test_qwen3_shapes_default_plans(gpu, shape):
+    """The library's default plans at the Qwen3 shapes (the split rule's
+    long-column and round-filling cases, up to 12 splits): GEMV parity, and
+    for the gate/up widths the pair launch with SiLU*mul (pair tiles of 512
+    past 14336 outputs) against the oracle."""
+    from spmv_decode_amd.hip_spmv import nmsparse_gate_up_silu
+
+    K, h, nnz, m = QWEN3_SHAPES[shape]
+    say(f"qwen3 {shape} {K}->{h} {nnz}:{m} plan {_lib.plan(h, K // m * nnz, nnz, m)}")
+    x, md, mi = make_case(K, h, nnz, m, seed=K * 3 + h)
+    check_parity(run(x, md, mi, nnz, m), x, md, mi, nnz, m, shape)
+    if shape.endswith("gate_up"):
+        _, ud, ui = make_case(K, h, nnz, m, seed=K * 3 + h + 1)
+        ref = _silu_ref(x, md, mi, ud, ui, nnz, m)
+        got = nmsparse_gate_up_silu(x, (md, mi), (ud, ui), nnz, m).float().cpu().numpy().reshape(-1)
+        e = O.error_metrics(ref, got)
+        assert np.isfinite(got).all() and e["max_abs"] <= 1e-2 and e["rel_l2"] <= 1e-3, e
+
+
 RAGGED = [  # (K, h, nnz, m): tails in both directions, odd N, tiny and wide
     (16, 128, 2, 4), (12, 384, 3, 4), (2000, 1152, 8, 16), (4096, 1280, 1, 4), (1024, 640, 128, 256),
     (8, 128, 1, 8), (7168, 2176, 5, 7)]
