@@ -449,7 +449,7 @@ def _check_heads(got, ref, dtype, what):
 @pytest.mark.parametrize("qk_norm", [False, True])
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
 @pytest.mark.parametrize("K,nh,kvh,hd,nnz,m", [(4096, 32, 8, 128, 32, 64), (512, 4, 2, 64, 2, 4),
-                                               (5120, 40, 8, 128, 8, 16)], ids=str)
+                                               (5120, 40, 8, 128, 8, 16), (5120, 64, 8, 128, 16, 32)], ids=str)
 def test_qkv_decode_rope_and_cache_write(gpu, K, nh, kvh, hd, nnz, m, dtype, qk_norm, layout):
     """plain: q_out [1, nh*hd], keys [kvh, hd, S], values [kvh, S, hd] (row pos).
     decoder: the decoder's buffers, q_out rows [nh, hd + 8] and keys
