@@ -58,6 +58,19 @@ def test_rows_are_bitwise_the_gemv_of_each_row(gpu, shape):
     check_rows(out, X, md, mi, 32, 64, f"{shape}")
 
 
+@pytest.mark.parametrize("batch", [2, 4, 8])
+@pytest.mark.parametrize("shape", [(5120, 17408), (17408, 5120), (5120, 8192), (25600, 5120)], ids=str)
+def test_default_plans_at_qwen3_shapes(gpu, shape, batch):
+    """The SpMM's default plans (its tile rule for wide and short-column
+    launches, the GEMV's split rule) at Qwen3-14B / Qwen3-32B shapes, every row
+    against the oracle."""
+    K, h = shape
+    _, md, mi = make_case(K, h, 16, 32, seed=K * 7 + h)
+    X = torch.randn(batch, K, generator=torch.Generator(device="cuda").manual_seed(batch), device="cuda").half()
+    say(f"spmm qwen3 {shape} batch {batch} plan {_lib.spmm_plan(batch, h, md.shape[0], 16, 32, -1, 0)}")
+    check_rows(spmm(X, md, mi, 16, 32), X, md, mi, 16, 32, f"{shape} b{batch}")
+
+
 RAGGED = [(16, 128, 2, 4), (12, 384, 3, 4), (2000, 1152, 8, 16), (4096, 1280, 1, 4), (1024, 640, 128, 256),
           (7168, 2176, 5, 7)]
 
