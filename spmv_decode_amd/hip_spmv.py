@@ -87,7 +87,13 @@ def validate_args(vec, mat_data, mat_index, w, h, BLOCK_WIDTH, NUM_THREADS, VEC_
 
 
 def workspace_for(device: torch.device, nbytes: int, stream_ptr: int) -> torch.Tensor:
-    """A zero-initialised uint8 workspace of at least `nbytes` for (device, stream)."""
+    """A zero-initialised uint8 workspace of at least `nbytes` for (device, stream).
+
+    During graph capture on a stream that has none of its own, another
+    stream's workspace on the device is borrowed (a capture cannot zero a new
+    one without recording a fill): replays of that graph must then not overlap
+    GEMVs on the lending stream, whose counters and partials they share. Warm
+    up on the capture stream itself (as decode.runner does) to avoid sharing."""
     key = (device.index, int(stream_ptr))
     ws = _workspaces.get(key)
     if ws is not None and ws.numel() >= nbytes:
