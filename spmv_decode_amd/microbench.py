@@ -534,6 +534,45 @@ def write_decode_classes_md(model, res, path, cmd):
     Path(path).write_text("\n".join(lines) + "\n")
 
 
+def pair_sweep(nnz=32, m=64, splits_list=(4, 6, 7, 8, 9, 10, 12, 14, 16), reps=20, warmup=5, log=print):
+    """The decoder's gate/up pair launch (RMSNorm + SiLU*mul, Llama-3.1-8B
+    shapes) under every pair configuration x split count, weights rotated over
+    >= 1 GiB, graph replay; rows in the --sweep CSV layout (config named
+    `pair_th{TH}_u{U}` from the plan: TH from the tile count, U from the chunk)."""
+    from .hip_spmv import launch_plan, nmsparse_gate_up_silu
+
+    forms = DecodeForms(nnz, m)
+    h, K = forms.inter, forms.dim
+    nbytes = forms.bytes("gate_up_pair_norm")
+    n = forms.copies["gate_up_pair_norm"]
+    rows, seen = [], set()
+    for cfg in [-1, *range(_lib.load().nm_num_gate_up_configs())]:
+        for sp in ((0,) if cfg < 0 else splits_list):
+            plan = launch_plan([forms.gate.mats[0], forms.up.mats[0]], nnz, m, gate_up=True, config_id=cfg,
+                               splits=sp)
+            tiles = plan["blocks"] // plan["splits"]
+            th = -(-h // tiles) // 8  # tiles = ceil(h / (8 TH)), exact for the TH in the table at these h
+            u = plan["chunk_rows"] * th // 256
+            key = (plan["config_id"], plan["splits"])
+            if cfg >= 0 and key in seen:
+                continue
+            seen.add(key)
+
+            def launch(i, cfg=cfg, sp=sp):
+                nmsparse_gate_up_silu(forms.h1, forms.gate.mats[i], forms.up.mats[i], nnz, m, out=forms.pair_out,
+                                      norm=(forms.ln2, 1e-5), config_id=cfg, splits=sp)
+
+            us = graph_us_per_launch([lambda i=i: launch(i) for i in range(n)], reps, warmup)
+            name = ("auto:" if cfg < 0 else "") + f"pair_th{th}_u{u}"
+            rows.append({"config": name, "config_id": plan["config_id"], "n_out": h, "n_in": K,
+                         "ratio": f"{nnz}:{m}", "splits": plan["splits"], "blocks": plan["blocks"],
+                         "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1), "nmat": 2})
+            log(f"pair {name} s={plan['splits']} blocks {plan['blocks']}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
+    del forms
+    torch.cuda.empty_cache()
+    return rows
+
+
 def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     """Workload for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
     three copies of a 256 MiB buffer (the known-size calibration kernel), then
@@ -615,10 +654,22 @@ def main(argv=None):
     p.add_argument("--stripe-ceiling", action="store_true",
                    help="measure launches that only read each Llama shape's weights in the GEMV's pattern")
     p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
+    p.add_argument("--pair-sweep", action="store_true",
+                   help="time the decoder's gate/up pair launch under every pair configuration x split count "
+                        "(Llama-3.1-8B shapes, the first --ratios entry); --csv for profiling sweep-stats")
     p.add_argument("--decode-classes", default=None, metavar="MODEL",
                    help="time the fused decoder layer's four launches at MODEL's shapes (llama-3.1-8b, qwen3-14b, "
                         "qwen3-32b) for each --ratios entry")
     a = p.parse_args(argv)
+    if a.pair_sweep:
+        nnz, m = _parse_pairs(a.ratios, ":")[0]
+        rows = pair_sweep(nnz, m, reps=a.reps, warmup=a.warmup, log=lambda s: print(s, flush=True))
+        if a.csv:
+            with open(a.csv, "w", newline="") as f:
+                wr = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
+                wr.writeheader()
+                wr.writerows(rows)
+        return 0
     if a.decode_classes:
         res = decode_classes(a.decode_classes, _parse_pairs(a.ratios, ":"), a.reps, a.warmup, a.rotate_mib << 20,
                              log=lambda s: print(s, flush=True))

@@ -139,3 +139,34 @@ def test_decode_stats_roles_per_step(tmp_path, setup_calls):
     total = 32 * 23.0 + 640 + 32 * 9.5 + 32 * 14.0 + 180 + 160 + 5
     assert role("total kernel time") == pytest.approx(total, abs=0.1)
     assert "distribution_elementwise" not in text
+
+
+def test_sweep_stats_joins_pair_rows_to_the_pair_kernel(tmp_path):
+    """A pair sweep row (pair_th32_u4, 448 workgroups) takes the duration of
+    the traced NMAT=2 kernel with that grid, not a single-matrix kernel's."""
+    trace = tmp_path / "trace.csv"
+    with open(trace, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=["Kernel_Name", "Workgroup_Size_X", "Grid_Size_X", "Start_Timestamp",
+                                          "End_Timestamp"])
+        w.writeheader()
+        for name, grid, dur in (("nm_gemv_kernel<0, 32, 4, 1, true, 2, true>(nm_hip::Args)", 448 * 256, 22_000),
+                                ("nm_gemv_kernel<0, 32, 4, 1, true, 1, false>(nm_hip::Args)", 448 * 256, 11_000),
+                                ("nm_gemv_kernel<0, 64, 8, 1, true, 2, true>(nm_hip::Args)", 448 * 256, 24_000)):
+            for i in range(3):
+                w.writerow({"Kernel_Name": name, "Workgroup_Size_X": 256, "Grid_Size_X": grid,
+                            "Start_Timestamp": 1000 * i, "End_Timestamp": 1000 * i + dur})
+    sweep = tmp_path / "sweep.csv"
+    rows = [{"config": "auto:pair_th32_u4", "config_id": 1, "n_out": 14336, "n_in": 4096, "ratio": "32:64",
+             "splits": 8, "blocks": 448, "us": 24.0, "GBps": 4895.4, "nmat": 2},
+            {"config": "pair_th64_u8", "config_id": 5, "n_out": 14336, "n_in": 4096, "ratio": "32:64",
+             "splits": 16, "blocks": 448, "us": 25.0, "GBps": 4699.6, "nmat": 2}]
+    with open(sweep, "w", newline="") as f:
+        w = csv.DictWriter(f, fieldnames=list(rows[0]))
+        w.writeheader()
+        w.writerows(rows)
+    md = tmp_path / "s.md"
+    P.sweep_stats(str(trace), str(sweep), str(md), "cmd")
+    text = md.read_text()
+    assert "gate/up pair + RMSNorm + SiLU*mul, 4096 -> 2 x 14336" in text
+    assert "| pair_th32_u4 (library choice) | 8 | 448 | 22.00 |" in text
+    assert "| pair_th64_u8 | 16 | 448 | 24.00 |" in text
