@@ -243,21 +243,23 @@ class DecodeForms:
         self.copies = {"qkv_decode": cq, "o_resid": self.o.copies, "gate_up_pair_norm": cp,
                        "down_resid": self.down.copies}
 
-    def launch(self, cls, i):
+    def launch(self, cls, i, config_id=-1, splits=0):
         from .hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
 
         nnz, m = self.nnz, self.m
+        kw = dict(config_id=config_id, splits=splits)
         if cls == "qkv_decode":
             nmsparse_qkv_decode(self.x, self.q.mats[i], self.k.mats[i], self.v.mats[i], nnz, m, q_out=self.qo,
                                 k_cache_t=self.k_cache, v_cache_t=self.v_cache, pos=self.pos, rope_table=self.rope,
-                                head_dim=self.hd, norm=(self.ln1, 1e-5), q_norm=self.q_norm, k_norm=self.k_norm)
+                                head_dim=self.hd, norm=(self.ln1, 1e-5), q_norm=self.q_norm, k_norm=self.k_norm, **kw)
         elif cls == "o_resid":
-            nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i], self.h1, residual=self.x)], nnz, m)
+            nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i], self.h1, residual=self.x)], nnz, m, **kw)
         elif cls == "gate_up_pair_norm":
             nmsparse_gate_up_silu(self.h1, self.gate.mats[i], self.up.mats[i], nnz, m, out=self.pair_out,
-                                  norm=(self.ln2, 1e-5))
+                                  norm=(self.ln2, 1e-5), **kw)
         elif cls == "down_resid":
-            nmsparse_gemv_launch(self.act, [GemvProblem(*self.down.mats[i], self.h2, residual=self.h1)], nnz, m)
+            nmsparse_gemv_launch(self.act, [GemvProblem(*self.down.mats[i], self.h2, residual=self.h1)], nnz, m,
+                                 **kw)
         else:
             raise ValueError(cls)
 
@@ -534,40 +536,51 @@ def write_decode_classes_md(model, res, path, cmd):
     Path(path).write_text("\n".join(lines) + "\n")
 
 
-def pair_sweep(nnz=32, m=64, splits_list=(4, 6, 7, 8, 9, 10, 12, 14, 16), reps=20, warmup=5, log=print):
-    """The decoder's gate/up pair launch (RMSNorm + SiLU*mul, Llama-3.1-8B
-    shapes) under every pair configuration x split count, weights rotated over
-    >= 1 GiB, graph replay; rows in the --sweep CSV layout (config named
-    `pair_th{TH}_u{U}` from the plan: TH from the tile count, U from the chunk)."""
-    from .hip_spmv import launch_plan, nmsparse_gate_up_silu
+def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8, 9, 10, 12, 14, 16), reps=20,
+                 warmup=5, log=print):
+    """One of the decoder's fused launches at the Llama-3.1-8B shapes under
+    every configuration x split count (weights rotated over >= 1 GiB, graph
+    replay): "gate_up_pair_norm" (the pair configurations) or "qkv_decode"
+    (the plain configurations, grouped q/k/v with the input RMSNorm, RoPE and
+    cache write). Rows in the --sweep CSV layout, the configuration named from
+    the plan (TH from the tile count, U from the chunk; `pair_` for the pair),
+    with the kernel's NMAT and NORM so that profiling sweep-stats can match
+    them to the traced kernels."""
+    from .hip_spmv import launch_plan
 
     forms = DecodeForms(nnz, m)
-    h, K = forms.inter, forms.dim
-    nbytes = forms.bytes("gate_up_pair_norm")
-    n = forms.copies["gate_up_pair_norm"]
+    pair = cls == "gate_up_pair_norm"
+    if not pair and cls != "qkv_decode":
+        raise ValueError(f"launch_sweep: {cls!r} is not a fused decoder launch with its own plan")
+    mats = [forms.gate.mats[0], forms.up.mats[0]] if pair else [forms.q.mats[0], forms.k.mats[0], forms.v.mats[0]]
+    hs = [forms.inter] if pair else [int(md.shape[1]) for md, _ in mats]
+    nbytes = forms.bytes(cls)
+    n = forms.copies[cls]
+    n_cfg = _lib.load().nm_num_gate_up_configs() if pair else _lib.num_configs()
     rows, seen = [], set()
-    for cfg in [-1, *range(_lib.load().nm_num_gate_up_configs())]:
+    for cfg in [-1, *range(n_cfg)]:
         for sp in ((0,) if cfg < 0 else splits_list):
-            plan = launch_plan([forms.gate.mats[0], forms.up.mats[0]], nnz, m, gate_up=True, config_id=cfg,
-                               splits=sp)
-            tiles = plan["blocks"] // plan["splits"]
-            th = -(-h // tiles) // 8  # tiles = ceil(h / (8 TH)), exact for the TH in the table at these h
-            u = plan["chunk_rows"] * th // 256
+            plan = launch_plan(mats, nnz, m, gate_up=pair, config_id=cfg, splits=sp)
             key = (plan["config_id"], plan["splits"])
             if cfg >= 0 and key in seen:
                 continue
             seen.add(key)
+            tiles = plan["blocks"] // plan["splits"]
+            th = next(t for t in (16, 32, 64, 128, 256) if sum(-(-h // (8 * t)) for h in hs) == tiles)
+            u = plan["chunk_rows"] * th // 256
+            cached = not pair and "cached" in _lib.describe(plan["config_id"])
+            name = ("auto:" if cfg < 0 else "") + ("pair_" if pair else "") + f"th{th}_u{u}" + ("_cached" if cached
+                                                                                           else "")
 
             def launch(i, cfg=cfg, sp=sp):
-                nmsparse_gate_up_silu(forms.h1, forms.gate.mats[i], forms.up.mats[i], nnz, m, out=forms.pair_out,
-                                      norm=(forms.ln2, 1e-5), config_id=cfg, splits=sp)
+                forms.launch(cls, i, config_id=cfg, splits=sp)
 
             us = graph_us_per_launch([lambda i=i: launch(i) for i in range(n)], reps, warmup)
-            name = ("auto:" if cfg < 0 else "") + f"pair_th{th}_u{u}"
-            rows.append({"config": name, "config_id": plan["config_id"], "n_out": h, "n_in": K,
+            rows.append({"config": name, "config_id": plan["config_id"], "n_out": sum(hs), "n_in": forms.dim,
                          "ratio": f"{nnz}:{m}", "splits": plan["splits"], "blocks": plan["blocks"],
-                         "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1), "nmat": 2})
-            log(f"pair {name} s={plan['splits']} blocks {plan['blocks']}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
+                         "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1), "nmat": 2 if pair else 1,
+                         "norm": 1})
+            log(f"{cls} {name} s={plan['splits']} blocks {plan['blocks']}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
     del forms
     torch.cuda.empty_cache()
     return rows
@@ -657,13 +670,17 @@ def main(argv=None):
     p.add_argument("--pair-sweep", action="store_true",
                    help="time the decoder's gate/up pair launch under every pair configuration x split count "
                         "(Llama-3.1-8B shapes, the first --ratios entry); --csv for profiling sweep-stats")
+    p.add_argument("--qkv-sweep", action="store_true",
+                   help="the same for the decoder's q/k/v launch (norm, RoPE, cache write) and the plain "
+                        "configurations")
     p.add_argument("--decode-classes", default=None, metavar="MODEL",
                    help="time the fused decoder layer's four launches at MODEL's shapes (llama-3.1-8b, qwen3-14b, "
                         "qwen3-32b) for each --ratios entry")
     a = p.parse_args(argv)
-    if a.pair_sweep:
+    if a.pair_sweep or a.qkv_sweep:
         nnz, m = _parse_pairs(a.ratios, ":")[0]
-        rows = pair_sweep(nnz, m, reps=a.reps, warmup=a.warmup, log=lambda s: print(s, flush=True))
+        rows = launch_sweep("gate_up_pair_norm" if a.pair_sweep else "qkv_decode", nnz, m, reps=a.reps,
+                            warmup=a.warmup, log=lambda s: print(s, flush=True))
         if a.csv:
             with open(a.csv, "w", newline="") as f:
                 wr = csv.DictWriter(f, fieldnames=list(rows[0].keys()))

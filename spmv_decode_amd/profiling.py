@@ -319,13 +319,13 @@ def sweep_stats(trace_csv, sweep_csv, md_path, cmd):
         for r in rd:
             name = r.get("Kernel_Name", "")
             # plain single-matrix launches (NMAT 1, no norm) and the gate/up pair with its norm (NMAT 2)
-            mt = re.search(r"nm_gemv_kernel<\d+, (\d+), (\d+), \d+, (true|false), (1, false|2, true)>", name)
+            mt = re.search(r"nm_gemv_kernel<\d+, (\d+), (\d+), \d+, (true|false), (\d), (true|false)>", name)
             if not mt:
                 continue
             lanes = int(r.get("Workgroup_Size_X") or r.get("Workgroup_Size") or 256)
             grid = int(r.get("Grid_Size_X") or r.get("Grid_Size"))
-            nmat = int(mt.group(4)[0])
-            key = (int(mt.group(1)), int(mt.group(2)), mt.group(3) == "true", grid // max(lanes, 1), nmat)
+            key = (int(mt.group(1)), int(mt.group(2)), mt.group(3) == "true", grid // max(lanes, 1),
+                   int(mt.group(4)), mt.group(5) == "true")
             dur = int(r["End_Timestamp"]) - int(r["Start_Timestamp"])
             g = groups.setdefault(key, [0, 0.0])
             g[0] += 1
@@ -350,14 +350,17 @@ def sweep_stats(trace_csv, sweep_csv, md_path, cmd):
         for r in rows:
             cfgname = r["config"].split(":")[-1]
             mt = re.match(r"(?:pair_)?th(\d+)_u(\d+)(_cached)?", cfgname)
-            key = (int(mt.group(1)), int(mt.group(2)), not mt.group(3), int(r["blocks"]), int(r.get("nmat") or 1))
+            key = (int(mt.group(1)), int(mt.group(2)), not mt.group(3), int(r["blocks"]), int(r.get("nmat") or 1),
+                   bool(int(r.get("norm") or 0)))
             n, tot = groups.get(key, (0, 0.0))
             if n:
                 timed.append((tot / n / 1e3, n, r))
         auto = next((t for t in timed if t[2]["config"].startswith("auto:")), None)
         ranked = sorted((t for t in timed if not t[2]["config"].startswith("auto:")), key=lambda t: t[0])
         pair = any(str(r.get("nmat")) == "2" for r in rows)
-        title = f"gate/up pair + RMSNorm + SiLU*mul, {n_in} -> 2 x {n_out}" if pair else f"{n_in} -> {n_out}"
+        normed = any(str(r.get("norm")) == "1" for r in rows)
+        title = (f"gate/up pair + RMSNorm + SiLU*mul, {n_in} -> 2 x {n_out}" if pair else
+                 f"q/k/v + RMSNorm + RoPE + cache write, {n_in} -> {n_out}" if normed else f"{n_in} -> {n_out}")
         lines += [f"## {title}, {ratio} ({nbytes / 1e6:.1f} MB per launch)", "",
                   "| config | splits | workgroups | rocprof us | GB/s | % of 8 TB/s | dispatches |",
                   "|---|---|---|---|---|---|---|"]

@@ -157,9 +157,9 @@ def test_sweep_stats_joins_pair_rows_to_the_pair_kernel(tmp_path):
                             "Start_Timestamp": 1000 * i, "End_Timestamp": 1000 * i + dur})
     sweep = tmp_path / "sweep.csv"
     rows = [{"config": "auto:pair_th32_u4", "config_id": 1, "n_out": 14336, "n_in": 4096, "ratio": "32:64",
-             "splits": 8, "blocks": 448, "us": 24.0, "GBps": 4895.4, "nmat": 2},
+             "splits": 8, "blocks": 448, "us": 24.0, "GBps": 4895.4, "nmat": 2, "norm": 1},
             {"config": "pair_th64_u8", "config_id": 5, "n_out": 14336, "n_in": 4096, "ratio": "32:64",
-             "splits": 16, "blocks": 448, "us": 25.0, "GBps": 4699.6, "nmat": 2}]
+             "splits": 16, "blocks": 448, "us": 25.0, "GBps": 4699.6, "nmat": 2, "norm": 1}]
     with open(sweep, "w", newline="") as f:
         w = csv.DictWriter(f, fieldnames=list(rows[0]))
         w.writeheader()
