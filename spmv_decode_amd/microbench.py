@@ -548,10 +548,10 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
     them to the traced kernels."""
     from .hip_spmv import launch_plan
 
-    forms = DecodeForms(nnz, m)
     pair = cls == "gate_up_pair_norm"
     if not pair and cls != "qkv_decode":
         raise ValueError(f"launch_sweep: {cls!r} is not a fused decoder launch with its own plan")
+    forms = DecodeForms(nnz, m)
     mats = [forms.gate.mats[0], forms.up.mats[0]] if pair else [forms.q.mats[0], forms.k.mats[0], forms.v.mats[0]]
     hs = [forms.inter] if pair else [int(md.shape[1]) for md, _ in mats]
     nbytes = forms.bytes(cls)

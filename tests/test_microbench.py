@@ -83,6 +83,11 @@ def test_decode_classes_times_every_launch_at_a_qwen3_shape(gpu, tmp_path):
     (tmp_path / "r.json").write_text(json.dumps(res))
 
 
+def test_launch_sweep_takes_the_fused_launches_only():
+    with pytest.raises(ValueError, match="fused decoder launch"):
+        MB.launch_sweep("o_resid")
+
+
 def test_bench_refuses_more_than_one_gpu():
     """bench.py --gpus N > 1 exits with a message (one-GPU build) before any GPU work."""
     import subprocess
