@@ -14,16 +14,22 @@ must start at zero, plus fp32 split-K partials). One zero-initialised
 workspace is kept per (device, stream) and reused by every call on that
 stream; it is grown outside of graph capture only, and retired workspaces are
 kept alive so that captured graphs never see their memory reused. Calls on
-different streams use different workspaces. During hipGraph capture a call
-uses the capture stream's workspace, or any initialised workspace of the
-device that is large enough (the graph must then not be replayed concurrently
-with eager calls on the stream that owns it); call the op once eagerly on the
-device before capturing, as the reference's benchmarks do per shape
-(benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:134-144).
+different streams use different workspaces, and no call ever uses another
+stream's. During hipGraph capture a call uses the capture stream's own
+workspace when a warm-up call on that stream created one large enough (the
+reference's benchmarks warm every shape up before capturing,
+benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:134-144); replays then share it
+with eager calls on the capture stream, so they must be ordered with them.
+Otherwise the capture gets a workspace of its own, allocated inside the
+capture from the graph's memory pool with its counters cleared by a fill
+kernel recorded in the graph (one fill node per replay, as the reference's
+per-call `torch.zeros` scratch, triton_spmv.py:285); it is keyed by the HIP
+capture id, so two graphs never share one.
 """
 from __future__ import annotations
 
 import ctypes
+import os
 import warnings
 
 import torch
@@ -39,6 +45,29 @@ _KNOWN_ARCH = ("auto", "a100", "sm80", "generic", "default", "gfx950")
 _MIN_WORKSPACE = _lib.NM_TICKET_BYTES + (16 << 20)
 _workspaces: dict[tuple[int, int], torch.Tensor] = {}
 _retired: list[torch.Tensor] = []
+# Workspaces owned by a capture in progress: (device, capture id) -> tensors from
+# the capture's pool (the last one is grown into). Dropped once no capture is
+# active: the graph's pool then keeps the memory for its replays, as it does
+# for every intermediate tensor of the capture.
+_capture_workspaces: dict[tuple[int, int], list[torch.Tensor]] = {}
+_hip_rt = None
+
+
+def capture_id(stream_ptr: int) -> int:
+    """Id of the hipGraph capture in progress on `stream_ptr` (hipStreamGetCaptureInfo
+    of the HIP runtime torch has loaded); 0 when the stream is not capturing."""
+    global _hip_rt
+    if _hip_rt is None:
+        lib = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD)  # the runtime already in the process
+        fn = lib.hipStreamGetCaptureInfo
+        fn.restype = ctypes.c_int
+        fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_ulonglong)]
+        _hip_rt = fn
+    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
+    rc = _hip_rt(ctypes.c_void_p(int(stream_ptr)), ctypes.byref(status), ctypes.byref(cid))
+    if rc != 0:
+        raise _lib.NmSparseLibraryError(f"hipStreamGetCaptureInfo failed with status {rc}")
+    return int(cid.value) if status.value == 1 else 0  # hipStreamCaptureStatusActive
 
 
 def validate_args(vec, mat_data, mat_index, w, h, BLOCK_WIDTH, NUM_THREADS, VEC_WIDTH, minibatch, vecNum,
@@ -87,28 +116,38 @@ def validate_args(vec, mat_data, mat_index, w, h, BLOCK_WIDTH, NUM_THREADS, VEC_
 
 
 def workspace_for(device: torch.device, nbytes: int, stream_ptr: int) -> torch.Tensor:
-    """A zero-initialised uint8 workspace of at least `nbytes` for (device, stream).
+    """A uint8 workspace of at least `nbytes` for a launch on (device, stream)
+    whose arrival counters (its first NM_TICKET_BYTES) are zero.
 
-    During graph capture on a stream that has none of its own, another
-    stream's workspace on the device is borrowed (a capture cannot zero a new
-    one without recording a fill): replays of that graph must then not overlap
-    GEMVs on the lending stream, whose counters and partials they share. Warm
-    up on the capture stream itself (as decode.runner does) to avoid sharing."""
+    Outside capture: the stream's own zero-initialised workspace (grown when
+    too small). During capture: the capture stream's own workspace if one
+    large enough exists, else one owned by this capture (see the module
+    docstring); never another stream's."""
     key = (device.index, int(stream_ptr))
     ws = _workspaces.get(key)
+    capturing = torch.cuda.is_current_stream_capturing() if (_capture_workspaces or ws is None
+                                                             or ws.numel() < nbytes) else False
+    if not capturing and _capture_workspaces:
+        _capture_workspaces.clear()  # no capture in progress: the graphs' pools own those now
     if ws is not None and ws.numel() >= nbytes:
         return ws
-    if torch.cuda.is_current_stream_capturing():
-        for (dev, _), cand in _workspaces.items():
-            if dev == device.index and cand.numel() >= nbytes:
-                return cand
-        warnings.warn(
-            "nmsparse: no initialised workspace for this device during graph capture; allocating one "
-            "inside the graph (an extra fill node). Call the op once eagerly before capturing.",
-            RuntimeWarning,
-            stacklevel=3,
-        )
-        return torch.zeros(nbytes, dtype=torch.uint8, device=device)
+    if capturing:
+        ckey = (device.index, capture_id(stream_ptr))
+        owned = _capture_workspaces.setdefault(ckey, [])
+        if owned and owned[-1].numel() >= nbytes:
+            return owned[-1]
+        if not owned:
+            warnings.warn(
+                "nmsparse: graph capture on a stream without a warmed-up workspace; the capture gets its own, "
+                "cleared by a fill node in the graph on every replay. Call the op once eagerly on the capture "
+                "stream before capturing to avoid it.",
+                RuntimeWarning,
+                stacklevel=3,
+            )
+        cws = torch.empty(max(int(nbytes), _MIN_WORKSPACE), dtype=torch.uint8, device=device)
+        cws[:_lib.NM_TICKET_BYTES].zero_()  # a fill kernel, recorded in the graph
+        owned.append(cws)  # earlier ones stay referenced: launches recorded before still use them
+        return cws
     if ws is not None:
         _retired.append(ws)
     ws = torch.zeros(max(int(nbytes), _MIN_WORKSPACE), dtype=torch.uint8, device=device)

@@ -12,9 +12,14 @@ and output shape rule as `gemv`.
 
 Backend selection keeps the reference's `NM_KERNEL` contract of refusing
 unknown values (src/spmv/nmsparse_op.py:20-22). Unset, "hip" and
-"triton_ptx" all select the one shared-mask HIP kernel. "guarded", "fp16" and
-"fp16_split" name per-row-index CUDA backends whose sources are absent from
-the reference; they raise instead of silently changing layout.
+"triton_ptx" all select the one shared-mask HIP kernel. `_mode` reads
+"triton_ptx" under NM_KERNEL=triton_ptx, as the reference module sets it
+(src/spmv/nmsparse_op.py:29-32): the reference's benchmarks refuse any other
+value (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:95), and in that mode the
+shared-mask layout they check for is the one this kernel serves. Otherwise
+`_mode` is "hip". "guarded", "fp16" and "fp16_split" name per-row-index CUDA
+backends whose sources are absent from the reference; they raise instead of
+silently changing layout.
 """
 from __future__ import annotations
 
@@ -32,7 +37,7 @@ if _kernel in ("guarded", "fp16", "fp16_split"):
         f"NM_KERNEL={_kernel!r} selects a per-row-index CUDA backend that this MI355X build does not "
         "provide; leave NM_KERNEL unset (or set it to 'hip' / 'triton_ptx') for the shared-mask HIP kernel"
     )
-_mode = "hip"
+_mode = "triton_ptx" if _kernel == "triton_ptx" else "hip"
 
 
 @torch.library.custom_op("nmsparse::gemv", mutates_args=())

@@ -210,7 +210,8 @@ def _run_py(code, **env):
 
 def test_nm_kernel_env_contract():
     imp = "import spmv_decode_amd.nmsparse_op as m; print(m._mode)"
-    assert _run_py(imp, NM_KERNEL="triton_ptx").stdout.strip() == "hip"
+    assert _run_py(imp, NM_KERNEL="triton_ptx").stdout.strip() == "triton_ptx"
+    assert _run_py(imp).stdout.strip() == "hip"
     assert _run_py(imp, NM_KERNEL="hip").stdout.strip() == "hip"
     r = _run_py(imp, NM_KERNEL="bogus")
     assert r.returncode != 0 and "refusing silent fallback" in r.stderr
@@ -225,6 +226,21 @@ def test_flat_import_shims():
     r = _run_py(code)
     assert r.returncode == 0, r.stderr
     assert r.stdout.split() == ["spmv_decode_amd.nmsparse_linear", "hip", "nmsparse_spmv_forward_hip"]
+
+
+def test_reference_harness_mode_check_passes_through_the_flat_imports():
+    """The reference benchmarks import `nmsparse_op` flat under NM_KERNEL=triton_ptx and
+    refuse to run unless `nmsparse_op._mode == "triton_ptx"`
+    (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:95); the shared-mask layout branch of
+    `_make_sparse` is the one that mode selects (src/spmv/nmsparse_linear.py:11,22)."""
+    code = ("import sys; sys.path.insert(0, 'spmv_decode_amd/compat'); import nmsparse_op, nmsparse_linear as s\n"
+            "if nmsparse_op._mode != 'triton_ptx':\n"
+            "    raise RuntimeError('This benchmark requires NM_KERNEL=triton_ptx')\n"
+            "md, mi, w, nnz = s._make_sparse(256, 128, 16, 0, 'cpu')\n"
+            "print(nmsparse_op._mode, tuple(mi.shape), mi.dtype)")
+    r = _run_py(code, NM_KERNEL="triton_ptx")
+    assert r.returncode == 0, r.stderr
+    assert r.stdout.split() == ["triton_ptx", "(16,", "8)", "torch.uint8"]
 
 
 # ---------------------------------------------------------------------------
@@ -364,3 +380,48 @@ def test_swap_rejects_unknown_layout_and_places_blocks():
         nmsparse_linear.swap_to_nmsparse(model, 4, "cpu")
     stack = _Stack(_HfBlock, 2, 128, 128, 256)
     assert nmsparse_linear.swap_to_nmsparse(stack, 4, "cuda", block_devices=["cpu", "cpu"]) == 14
+
+
+# ---------------------------------------------------------------------------
+# workspaces: per stream, never lent to another stream's capture
+# ---------------------------------------------------------------------------
+def test_workspace_for_never_lends_another_streams_workspace(monkeypatch):
+    """Eager calls get their stream's own zeroed workspace; a capture uses the capture
+    stream's own warmed workspace or one owned by that capture (keyed by capture id,
+    counters cleared, earlier ones kept while the capture lasts), never another
+    stream's. The reference's per-call scratch is always capture-private
+    (triton_spmv.py:285). Run on CPU tensors with the capture state simulated."""
+    from spmv_decode_amd import _lib
+    from spmv_decode_amd import hip_spmv as H
+
+    dev = torch.device("cpu")
+    monkeypatch.setattr(H, "_workspaces", {})
+    monkeypatch.setattr(H, "_capture_workspaces", {})
+    monkeypatch.setattr(H, "_retired", [])
+    state = {"on": False, "id": 0}
+    monkeypatch.setattr(torch.cuda, "is_current_stream_capturing", lambda: state["on"])
+    monkeypatch.setattr(H, "capture_id", lambda stream: state["id"])
+    T = _lib.NM_TICKET_BYTES
+
+    a = H.workspace_for(dev, 1000, 11)  # eager, stream 11
+    assert a.numel() >= H._MIN_WORKSPACE and not a.any()
+    assert H.workspace_for(dev, 1000, 11) is a
+    state.update(on=True, id=5)  # capture 5 on stream 22, which has no workspace of its own
+    with pytest.warns(RuntimeWarning, match="warmed-up workspace"):
+        c = H.workspace_for(dev, 1000, 22)
+    assert c is not a and not c[:T].any()
+    assert H.workspace_for(dev, 1000, 22) is c  # reused within the capture
+    big = H.workspace_for(dev, H._MIN_WORKSPACE + 64, 22)  # grows; the first stays referenced
+    assert big is not c and big.numel() >= H._MIN_WORKSPACE + 64 and not big[:T].any()
+    assert [t is u for t, u in zip(H._capture_workspaces[(None, 5)], (c, big))] == [True, True]
+    assert H.workspace_for(dev, 1000, 11) is a  # a capture on stream 11 uses its warmed workspace
+    state.update(id=6)  # a second capture on stream 22: a workspace of its own
+    with pytest.warns(RuntimeWarning, match="warmed-up workspace"):
+        d = H.workspace_for(dev, 1000, 22)
+    assert d is not c and d is not big
+    state.update(on=False, id=0)  # captures over: their pools own their workspaces
+    e = H.workspace_for(dev, 1000, 22)
+    assert not H._capture_workspaces and all(e is not t for t in (a, c, big, d))
+    assert H._workspaces[(None, 22)] is e and not e.any()
+    grown = H.workspace_for(dev, 2 * H._MIN_WORKSPACE, 11)  # eager growth retires the old one
+    assert grown is not a and H._retired[-1] is a and not grown.any()

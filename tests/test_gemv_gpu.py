@@ -214,6 +214,77 @@ def test_graph_capture_replays_match_eager(gpu):
         torch.cuda.synchronize()
 
 
+def test_capture_without_warmup_owns_its_workspace(gpu):
+    """A capture on a stream that never ran a GEMV gets a workspace of its own
+    (allocated in the capture, counters cleared by a fill node): two such graphs
+    on one stream, replayed in turn with eager GEMVs between, each match eager,
+    and neither borrows the default stream's workspace."""
+    cases = [make_case(K, h, 32, 64, seed=20 + i) for i, (K, h) in enumerate(LLAMA_SHAPES.values())]
+    eager = [run(x, md, mi, 32, 64).clone() for x, md, mi in cases]
+    torch.cuda.synchronize()
+    default_ws = hip_spmv._workspaces[(gpu.index or 0, torch.cuda.current_stream().cuda_stream)]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    graphs, outs = [], []
+    for half in (cases[:2], cases[2:]):
+        g = torch.cuda.CUDAGraph()
+        with pytest.warns(RuntimeWarning, match="warmed-up workspace"):
+            with torch.cuda.graph(g, stream=s):
+                outs.append([run(x, md, mi, 32, 64) for x, md, mi in half])
+        graphs.append(g)
+    assert (gpu.index or 0, s.cuda_stream) not in hip_spmv._workspaces
+    ref = [eager[:2], eager[2:]]
+    for rep in range(3):
+        for gi, (g, o, e) in enumerate(zip(graphs, outs, ref)):
+            say(f"no-warm-up graph {gi} replay {rep}")
+            for t in o:
+                t.zero_()
+            g.replay()
+            torch.cuda.synchronize()
+            for t, u in zip(o, e):
+                assert torch.equal(t, u), (rep, gi)
+            x, md, mi = cases[rep]
+            assert torch.equal(run(x, md, mi, 32, 64), eager[rep])
+            torch.cuda.synchronize()
+    assert not hip_spmv._capture_workspaces  # released to the graphs' pools after the captures
+    assert not default_ws[: _lib.NM_TICKET_BYTES].any()
+
+
+@pytest.mark.parametrize("m", [4, 64, 256])
+def test_fused_wqkv_width_default_plan(gpu, m):
+    """gpt-fast fuses q/k/v into one 4096 -> 6144 Linear (model.py:196-198, 219), which
+    the reference's swap turns into one NmSparseLinear; its default plan (256-row tiles
+    past 4096 outputs) against the oracle, through the module and the op."""
+    lin = nmsparse_linear.NmSparseLinear(6144, 4096, m, 11, "cuda")
+    say(f"wqkv 4096->6144 {m // 2}:{m} plan {_lib.plan(6144, lin.w, m // 2, m)}")
+    x = torch.randn(1, 1, 4096, generator=torch.Generator(device="cuda").manual_seed(m), device=gpu).half()
+    y = lin(x)
+    assert y.shape == (1, 1, 6144)
+    check_parity(y.reshape(1, -1), x.reshape(1, -1), lin.mat_data, lin.mat_index, m // 2, m, f"wqkv {m}")
+
+
+def test_make_sparse_digests_on_this_box(gpu):
+    """The synthetic weights NmSparseLinear draws on this machine are the reference's
+    own (fixtures written by importing src/spmv/nmsparse_linear.py): every digest case,
+    computed with this box's torch, whose version is printed."""
+    import hashlib
+    import json
+    from pathlib import Path
+
+    fx = json.loads((Path(__file__).parent / "golden" / "make_sparse.json").read_text())
+    say(f"torch {torch.__version__} on this box; fixtures written with torch {fx['meta']['torch']}")
+    for case in fx["digests"]:
+        md, mi, w, nnz = nmsparse_linear._make_sparse(case["K"], case["N"], case["M"], case["seed"], "cpu")
+        tag = (case["K"], case["N"], case["M"], case["seed"])
+        assert (w, nnz) == (case["w"], case["nnz"]), tag
+        assert hashlib.sha256(md.view(torch.int16).numpy().tobytes()).hexdigest() == case["mat_data_sha256"], tag
+        assert hashlib.sha256(mi.numpy().tobytes()).hexdigest() == case["mat_index_sha256"], tag
+    # and the module on the GPU holds exactly those buffers
+    c0 = fx["digests"][0]
+    lin = nmsparse_linear.NmSparseLinear(c0["N"], c0["K"], c0["M"], c0["seed"], "cuda")
+    assert hashlib.sha256(lin.mat_data.cpu().view(torch.int16).numpy().tobytes()).hexdigest() == c0["mat_data_sha256"]
+
+
 def test_op_and_module_on_gpu(gpu):
     lin = nmsparse_linear.NmSparseLinear(1024, 4096, 64, 3, "cuda")
     x = torch.randn(1, 1, 4096, device=gpu, dtype=torch.float16)
