@@ -69,6 +69,7 @@ extern "C" {
 #define NM_ERR_WORKSPACE (-6)        /* workspace missing or too small */
 #define NM_ERR_BAD_CONFIG (-7)       /* explicit config id / split count rejected */
 #define NM_ERR_BAD_EPILOGUE (-8)     /* input-norm / residual / head-layout arguments rejected */
+#define NM_ERR_STATIC_SCRATCH (-9)   /* launch needs more than NM_STATIC_SCRATCH_BYTES (static entry point) */
 
 /* Element type codes for the *_ex entry point and nm_gemv_workspace_bytes. */
 #define NM_DTYPE_F16 0
@@ -229,6 +230,28 @@ size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);
 int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int* out_splits, int* out_blocks,
                         int* out_rows_per_split, int* out_chunk_rows);
 int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream);
+
+/*
+ * nm_gemv_launch without a workspace argument: the launch's counters and
+ * split-K partials live in a scratch array of NM_STATIC_SCRATCH_BYTES that the
+ * library holds in static device memory, one copy per GPU for the life of the
+ * process. No counterpart in the reference (whose scratch comes from the
+ * caching allocator per call, triton_spmv.py:285): it is for callers that
+ * cannot allocate device memory -- code that must not call hipMalloc, such as
+ * hipGraph capture without a memory pool, tight serving loops and harnesses
+ * that forbid allocation. It allocates nothing and frees nothing. Same
+ * descriptor, results and checks as nm_gemv_launch (the same kernels and
+ * plans, so outputs are bit-identical to it); a launch whose
+ * nm_gemv_launch_workspace_bytes(desc) exceeds NM_STATIC_SCRATCH_BYTES is
+ * rejected with NM_ERR_STATIC_SCRATCH before anything runs. The counters start
+ * at zero and every launch leaves them zero. All calls on one GPU share its
+ * array: calls that may overlap on one GPU (different streams without
+ * ordering) race and must not be made. The first call on each GPU looks the
+ * array's address up (hipGetSymbolAddress, which may load the library's device
+ * code): make it outside graph capture. The stream's device is the one used.
+ */
+#define NM_STATIC_SCRATCH_BYTES (NM_TICKET_BYTES + (16 << 20))
+int nm_gemv_launch_static(const nm_gemv_launch_desc* desc, void* stream);
 
 /*
  * Small-batch SpMM: out[b, :] = W x[b, :] for 1 <= batch <= NM_MAX_BATCH

@@ -24,9 +24,11 @@ NM_ERR = {
     -6: "NM_ERR_WORKSPACE",
     -7: "NM_ERR_BAD_CONFIG",
     -8: "NM_ERR_BAD_EPILOGUE",
+    -9: "NM_ERR_STATIC_SCRATCH",
 }
 NM_KIND_GROUPED, NM_KIND_GATE_UP = 0, 1
 NM_MAX_BATCH = 8
+NM_STATIC_SCRATCH_BYTES = NM_TICKET_BYTES + (16 << 20)
 
 _vp = ctypes.c_void_p
 _i = ctypes.c_int
@@ -71,6 +73,7 @@ ABI = {
     "nm_num_gate_up_configs": (_i, []),
     "nm_gemv_launch_workspace_bytes": (_sz, [_descp]),
     "nm_gemv_launch": (_i, [_descp, _vp, _sz, _vp]),
+    "nm_gemv_launch_static": (_i, [_descp, _vp]),
     "nm_gemv_launch_plan": (_i, [_descp, _ip, _ip, _ip, _ip, _ip]),
     "nm_spmm_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "nm_spmm": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
@@ -80,7 +83,7 @@ ABI = {
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
 }
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _lib = None
 _lock = threading.Lock()

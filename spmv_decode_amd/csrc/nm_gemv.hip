@@ -3,6 +3,8 @@
 // argument validation and the C ABI declared in include/nmsparse_hip.h. The
 // kernels are in nm_gemv_kernel.h (instantiated by nm_gemv_inst.hip).
 
+#include <mutex>
+
 #include "nm_gemv_kernel.h"
 
 namespace nm_hip {
@@ -166,9 +168,11 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
 }
 
 // Validate a launch descriptor, plan it and launch. Every entry point of the
-// C ABI goes through here.
+// C ABI goes through here. With `workspace_needed` it only plans (and reports
+// the workspace size); with `validate_only` it runs every check and returns
+// before launching.
 int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes, void* stream,
-           size_t* workspace_needed) {
+           size_t* workspace_needed, bool validate_only = false) {
   if (d.dtype < NM_DTYPE_F16 || d.dtype > NM_DTYPE_F32) return NM_ERR_BAD_CONFIG;
   if (d.kind != NM_KIND_GROUPED && d.kind != NM_KIND_GATE_UP) return NM_ERR_BAD_CONFIG;
   const bool pair = d.kind == NM_KIND_GATE_UP;
@@ -223,6 +227,7 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   }
   if (any_pos && (!d.pos || d.pos_limit <= 0)) return NM_ERR_BAD_EPILOGUE;
   if (any_rope && !d.rope_table) return NM_ERR_BAD_EPILOGUE;
+  if (validate_only) return NM_OK;
 
   Args a;
   memset(&a, 0, sizeof(a));
@@ -369,6 +374,63 @@ int launch_spmm(int dtype, const void* x, long long x_row_stride, int batch, con
 }  // namespace
 }  // namespace nm_hip
 
+// Scratch of nm_gemv_launch_static: arrival counters (the first
+// NM_TICKET_BYTES), then split-K partials, in static device memory. Each GPU
+// the library runs on holds its own copy until the process ends. In host code
+// `scratch` names a host-side stand-in, not device memory: host code uses only
+// the per-device address that hipGetSymbolAddress returns for it.
+static __device__ __align__(256) unsigned char scratch[NM_STATIC_SCRATCH_BYTES];
+
+namespace nm_hip {
+namespace {
+
+// Zero n 32-bit words (the scratch's counters, once per device before its
+// first use; a kernel rather than a memset node, so it is also safe to record).
+__global__ void clear_words(uint32_t* p, int n) {
+  const int i = (int)(blockIdx.x * blockDim.x + threadIdx.x);
+  if (i < n) p[i] = 0u;
+}
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch[kMaxDevices];  // per-device address of `scratch`, set once
+
+// The address of this GPU's scratch (the stream's device, or the current
+// device for the null stream), looked up on the first call for that device,
+// whose counters are then cleared on `stream`.
+int static_scratch(void* stream, void** out) {
+  int dev = 0;
+  hipError_t e = stream ? hipStreamGetDevice(static_cast<hipStream_t>(stream), &dev) : hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return NM_ERR_BAD_CONFIG;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch[dev]) {
+    int cur = 0;
+    if ((e = hipGetDevice(&cur)) != hipSuccess) return (int)e;
+    if (cur != dev && (e = hipSetDevice(dev)) != hipSuccess) return (int)e;
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e == hipSuccess && p && ((uintptr_t)p & 255u) == 0) {
+      constexpr int kWords = NM_TICKET_BYTES / 4;
+      hipLaunchKernelGGL(clear_words, dim3((kWords + 255) / 256), dim3(256), 0, static_cast<hipStream_t>(stream),
+                         static_cast<uint32_t*>(p), kWords);
+      e = hipGetLastError();
+    }
+    if (cur != dev) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess) return (int)e;
+    if (!p || ((uintptr_t)p & 255u) != 0) return NM_ERR_MISALIGNED;
+    g_scratch[dev] = p;
+  }
+  *out = g_scratch[dev];
+  return NM_OK;
+}
+
+}  // namespace
+}  // namespace nm_hip
+
 using namespace nm_hip;
 
 // ---------------------------------------------------------------------------
@@ -490,6 +552,22 @@ int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t work
   return launch(*desc, workspace, workspace_bytes, stream, nullptr);
 }
 
+int nm_gemv_launch_static(const nm_gemv_launch_desc* desc, void* stream) {
+  if (!desc) return NM_ERR_NULL_POINTER;
+  size_t need = 0;
+  int rc = launch(*desc, nullptr, 0, nullptr, &need);  // plan only
+  if (rc != NM_OK) return rc;
+  if (need > (size_t)NM_STATIC_SCRATCH_BYTES) return NM_ERR_STATIC_SCRATCH;
+  // Every argument check before the first HIP call (a 256-byte aligned stand-in
+  // for the scratch address, never dereferenced).
+  rc = launch(*desc, reinterpret_cast<void*>((uintptr_t)256), NM_STATIC_SCRATCH_BYTES, stream, nullptr, true);
+  if (rc != NM_OK) return rc;
+  void* ptr = nullptr;
+  rc = static_scratch(stream, &ptr);
+  if (rc != NM_OK) return rc;
+  return launch(*desc, ptr, NM_STATIC_SCRATCH_BYTES, stream, nullptr);
+}
+
 size_t nm_spmm_workspace_bytes(int batch, int h, int w, int nnz, int m, int config_id, int splits) {
   Plan p;
   return make_spmm_plan(batch, h, w, nnz, m, config_id, splits, &p) == NM_OK ? p.workspace : 0;
@@ -556,6 +634,9 @@ const char* nm_strerror(int code) {
     case NM_ERR_MISALIGNED: return "mat_data/out must be 16-byte aligned, workspace 256-byte aligned";
     case NM_ERR_WORKSPACE: return "workspace missing or smaller than the *_workspace_bytes() value";
     case NM_ERR_BAD_CONFIG: return "unknown dtype, launch kind, config id or split count";
+    case NM_ERR_STATIC_SCRATCH:
+      return "the launch needs more workspace than the static scratch holds (NM_STATIC_SCRATCH_BYTES); use "
+             "nm_gemv_launch with a workspace";
     case NM_ERR_BAD_EPILOGUE:
       return "input-norm / residual / head-layout arguments rejected (contiguous 16-byte aligned vec for the "
              "norm; head_dim a multiple of 64 dividing h and the tile; pos and rope table when used)";

@@ -287,3 +287,28 @@ def test_launch_plan_query():
     assert summary(launch_plan([mats(5120, 17408)], 32, 64)) == (6, 7, 34 * 7)
     with pytest.raises(_lib.NmSparseLibraryError):
         launch_plan([mats(4096, 1000)], 32, 64)
+
+
+def test_static_scratch_entry_rejections_before_any_hip_call():
+    """nm_gemv_launch_static checks everything before it looks up its scratch:
+    a missing descriptor, a rejected shape, a launch whose workspace exceeds
+    NM_STATIC_SCRATCH_BYTES and bad pointers all return without a HIP call."""
+    lib = _lib.load()
+    assert lib.nm_gemv_launch_static(None, None) == -1
+    d = _lib.NmGemvLaunchDesc()
+    d.dtype, d.kind, d.nprob, d.vec_stride, d.vec = 0, 0, 1, 1, FAKE
+    d.w, d.nnz, d.m, d.config_id, d.splits = 8192, 32, 64, -1, 0
+    d.prob[0].mat_data, d.prob[0].mat_index, d.prob[0].out, d.prob[0].h = FAKE, FAKE, FAKE, 100
+    assert lib.nm_gemv_launch_static(ctypes.byref(d), None) == -3
+    d.prob[0].h = 128256
+    d.splits = 40  # 37 splits x 128256 fp32 partials: more than the static scratch
+    assert lib.nm_gemv_launch_workspace_bytes(ctypes.byref(d)) > _lib.NM_STATIC_SCRATCH_BYTES
+    assert lib.nm_gemv_launch_static(ctypes.byref(d), None) == -9
+    d.splits = 0
+    assert 0 < lib.nm_gemv_launch_workspace_bytes(ctypes.byref(d)) <= _lib.NM_STATIC_SCRATCH_BYTES
+    d.prob[0].out = FAKE + 8
+    assert lib.nm_gemv_launch_static(ctypes.byref(d), None) == -5
+    d.prob[0].out = None
+    assert lib.nm_gemv_launch_static(ctypes.byref(d), None) == -1
+    assert f"#define NM_STATIC_SCRATCH_BYTES (NM_TICKET_BYTES + (16 << 20))" in HEADER.read_text()
+    assert _lib.NM_STATIC_SCRATCH_BYTES == _lib.NM_TICKET_BYTES + (16 << 20)
