@@ -178,11 +178,18 @@ def dense_gemv(x2d: torch.Tensor, weight: torch.Tensor, form: str = "mm", out=No
 
 
 def project(lin: nn.Module, x: torch.Tensor) -> torch.Tensor:
-    """lin(x) for one row x [..., K]: a bias-free nn.Linear through dense_gemv
-    in its tuned form, any other module (NmSparseLinear included) through its
-    own forward."""
-    if type(lin) is nn.Linear and lin.bias is None and x.numel() == x.shape[-1]:
-        return dense_gemv(x.reshape(1, -1), lin.weight, getattr(lin, "gemv_form", "mm")).view(*x.shape[:-1], -1)
+    """lin(x) for one row x [..., K] as one launch of its own: a bias-free
+    nn.Linear through dense_gemv in its tuned form, an NmSparseLinear through
+    its op (never through a sibling group's shared launch), any other module
+    through its own forward."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    if x.numel() == x.shape[-1]:
+        if type(lin) is nn.Linear and lin.bias is None:
+            return dense_gemv(x.reshape(1, -1), lin.weight, getattr(lin, "gemv_form", "mm")).view(*x.shape[:-1], -1)
+        if isinstance(lin, NmSparseLinear):
+            return torch.ops.nmsparse.gemv(x, lin.mat_data, lin.mat_index, lin.w, lin.h, lin.block_width,
+                                           lin.vec_width)
     return lin(x)
 
 
@@ -199,6 +206,7 @@ def grouped_sparse(mods) -> bool:
 
 class Attention(nn.Module):
     group_launches = True  # one q/k/v launch when all three are sparse (Decoder.set_launch_mode)
+    call_modules = False   # every projection through its module's forward (Decoder.set_launch_mode)
 
     def __init__(self, cfg: DecoderConfig):
         super().__init__()
@@ -233,6 +241,8 @@ class Attention(nn.Module):
                                   projs[0].vec_width, outs=slices)
         elif self.wqkv is not None and all(type(p) is nn.Linear for p in projs):
             dense_gemv(x2d, self.wqkv, self.wqkv_form, out=qkv)
+        elif self.call_modules:  # as model code that knows nothing of the swap calls them
+            torch.cat([p(x) for p in projs], dim=-1, out=qkv.view(1, 1, -1))
         else:
             for proj, sl in zip(projs, slices):
                 linear_into(proj, x2d, sl)
@@ -246,11 +256,14 @@ class Attention(nn.Module):
         k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
         v_cache_t.index_copy_(2, pos, v)
         y = attend(q_pad, k_cache_t, v_cache_t, c, zero)  # [kvh, g, head_dim]
+        if self.call_modules:
+            return self.o_proj(y.view(1, 1, qd))
         return project(self.o_proj, y.view(1, 1, qd))
 
 
 class MLP(nn.Module):
     group_launches = True  # one gate/up launch when both are sparse (Decoder.set_launch_mode)
+    call_modules = False   # every projection through its module's forward (Decoder.set_launch_mode)
 
     def __init__(self, cfg: DecoderConfig):
         super().__init__()
@@ -261,6 +274,8 @@ class MLP(nn.Module):
         self.w13_form = "mm"
 
     def forward(self, x):
+        if self.call_modules:
+            return self.down_proj(F.silu(self.gate_proj(x)) * self.up_proj(x))
         if self.group_launches and grouped_sparse((self.gate_proj, self.up_proj)):
             from ..hip_spmv import nmsparse_gate_up_silu
 
@@ -341,18 +356,22 @@ class Decoder(nn.Module):
         self.max_seq = 0
         self.gemv_forms = {}  # (n_out, n_in) -> dense_gemv form, filled by tune_dense_gemv
 
-    LAUNCH_MODES = ("fused", "grouped", "per_linear")
+    LAUNCH_MODES = ("fused", "grouped", "per_linear", "modules")
 
     def set_launch_mode(self, mode: str) -> None:
         """How sparse projections are launched: "fused" (the fused layer, the
         default), "grouped" (one q/k/v and one gate/up launch, norms and RoPE
-        in PyTorch) or "per_linear" (one launch per Linear, like the
-        reference's decode step and the dense model)."""
+        in PyTorch), "per_linear" (one launch per Linear, like the reference's
+        decode step and the dense model) or "modules" (each projection called
+        as a module, lin(x), as model code written for dense Linears does: an
+        NmSparseLinear then runs its own forward, so q/k/v and gate/up share a
+        launch when swap_to_nmsparse tied them, else one launch each)."""
         if mode not in self.LAUNCH_MODES:
             raise ValueError(f"launch mode must be one of {self.LAUNCH_MODES}, got {mode!r}")
         self.fuse_epilogues = mode == "fused"
         for blk in self.layers:
-            blk.self_attn.group_launches = blk.mlp.group_launches = mode != "per_linear"
+            blk.self_attn.group_launches = blk.mlp.group_launches = mode in ("fused", "grouped")
+            blk.self_attn.call_modules = blk.mlp.call_modules = mode == "modules"
 
     DENSE_FUSIONS = ("none", "qkv", "qkv_gate_up")
 

@@ -29,9 +29,10 @@ bit-exact with the reference; the default is the bit-exact CPU stream.
 Beyond the reference: `NmSparseLinear.from_dense` / `pack_dense` build the
 packed buffers from a real dense weight and a shared N:M mask (a pure gather);
 `index_from_pruned` / `NmSparseLinear.from_pruned` recover the shared mask of
-an already N:M-pruned dense weight, and `swap_to_nmsparse(...,
-from_weights=True)` swaps a pruned checkpoint's own weights instead of
-synthetic ones. `NmSparseLinear.empty` builds a module with uninitialised
+an already N:M-pruned dense weight; `NmSparseLinear.to_dense` scatters the
+packed weights back (the masked dense weight the module computes with); and
+`swap_to_nmsparse(..., from_weights=True)` swaps a pruned checkpoint's own
+weights instead of synthetic ones. `NmSparseLinear.empty` builds a module with uninitialised
 buffers for `load_state_dict` (the packed buffers are ordinary state_dict
 entries, `mat_data` and `mat_index`).
 """
@@ -201,6 +202,18 @@ class NmSparseLinear(nn.Module):
         self.h, self.w, self.block_width, self.vec_width = N, banks * nnz, nnz, M
         return self
 
+    def to_dense(self, dtype=None) -> torch.Tensor:
+        """The dense [N, K] weight this module computes with: the packed weights
+        scattered back to their input columns, zeros elsewhere (the inverse of
+        pack_dense, a pure scatter: bit-exact). `dtype` converts the result."""
+        banks, nnz = self.mat_index.shape
+        K = banks * self.vec_width
+        pos = (torch.arange(banks * nnz, device=self.mat_index.device) // nnz) * self.vec_width \
+            + self.mat_index.reshape(-1).long()
+        dense = torch.zeros(self.h, K, dtype=dtype or self.mat_data.dtype, device=self.mat_data.device)
+        dense[:, pos.to(dense.device)] = self.mat_data.t().to(dense.dtype)
+        return dense
+
     def _prefill_weight(self, device):
         if self.weight is not None:
             return self.weight
@@ -218,11 +231,92 @@ class NmSparseLinear(nn.Module):
             if not self._has_dense() or (SPARSE_BATCH == "1" and rows <= SPARSE_BATCH_MAX_ROWS):
                 return torch.ops.nmsparse.spmm(x, *args)
         if x.shape[-2] == 1:
+            group = self.__dict__.get("_siblings")
+            if group is not None and not torch.compiler.is_compiling():
+                y = group.output(self, x)
+                if y is not None:
+                    return y
             return torch.ops.nmsparse.gemv(x, *args)
         return F.linear(x, self._prefill_weight(x.device))
 
     def extra_repr(self) -> str:
         return f"h={self.h}, w={self.w}, N:M={self.block_width}:{self.vec_width}"
+
+
+class SiblingLaunch:
+    """Sparse Linears of one block that read the same input (q/k/v, gate/up),
+    computed by one grouped launch (hip_spmv.nmsparse_gemv_grouped) instead of
+    one launch each, without any change to the model code that calls them.
+
+    The first member called with a one-row input launches the grouped GEMV for
+    every member and keeps the other members' outputs; a member then called
+    with the very same input tensor (same object, unchanged version counter)
+    takes its output, once. Any other call (another input, a repeated member,
+    more than one row, a dtype or device the grouped launch does not take, or
+    torch.compile tracing) goes through the member's own op as before, so the
+    results never depend on the call order, only the last bit of a sum may
+    (the grouped plan splits the columns like a launch of the summed width).
+    The bookkeeping is on the host, so under hipGraph capture the graph holds
+    the one grouped launch and the siblings read its outputs. The group holds
+    the input tensor it launched for until the next launch, so that tensor's
+    memory cannot be reused under it. No reference counterpart: the reference
+    launches every Linear on its own (src/spmv/nmsparse_linear.py:62-68).
+    """
+
+    def __init__(self, members):
+        if not 2 <= len(members) <= 4:
+            raise ValueError("a sibling group takes 2 to 4 Linears")
+        m0 = members[0]
+        for m in members:
+            if not isinstance(m, NmSparseLinear) or (m.w, m.block_width, m.vec_width) != (
+                    m0.w, m0.block_width, m0.vec_width):
+                raise ValueError("siblings must be NmSparseLinear with the same K and N:M")
+        self.members = list(members)
+        self._x = None
+        self._version = -1
+        self._pending = {}
+
+    def _usable(self, x) -> bool:
+        md = self.members[0].mat_data
+        return (x.is_cuda and x.dtype == md.dtype and x.device == md.device and x.is_contiguous()
+                and x.numel() == x.shape[-1] and all(m.mat_data.device == md.device for m in self.members))
+
+    def output(self, member, x):
+        """member(x) from the group's launch, or None when the group does not
+        serve this call (the member then launches on its own)."""
+        if not self._usable(x):
+            return None
+        i = next(j for j, m in enumerate(self.members) if m is member)
+        if self._x is x and self._version == x._version and i in self._pending:
+            return self._pending.pop(i)
+        from .hip_spmv import nmsparse_gemv_grouped
+
+        m0 = self.members[0]
+        outs = [torch.empty(*x.shape[:-1], m.h, dtype=x.dtype, device=x.device) for m in self.members]
+        nmsparse_gemv_grouped(x.view(1, -1), [(m.mat_data, m.mat_index) for m in self.members], m0.block_width,
+                              m0.vec_width, outs=[o.view(1, -1) for o in outs])
+        self._x, self._version = x, x._version
+        self._pending = {j: o for j, o in enumerate(outs) if j != i}
+        return outs[i]
+
+
+def tie_siblings(*members) -> SiblingLaunch:
+    """Make `members` (NmSparseLinear of one block reading the same input) one
+    SiblingLaunch; returns it. Replaces any group they were in."""
+    group = SiblingLaunch(members)
+    for m in members:
+        m.__dict__["_siblings"] = group  # a plain attribute: not a submodule, not in the state_dict
+    return group
+
+
+def untie_siblings(model) -> int:
+    """Drop every sibling group in `model` (each Linear launches on its own
+    again); returns the number of Linears untied."""
+    n = 0
+    for mod in model.modules():
+        if mod.__dict__.pop("_siblings", None) is not None:
+            n += 1
+    return n
 
 
 # Decoder-block layouts: (sub-module attribute, Linear names in swap order).
@@ -237,6 +331,11 @@ _MLP_LAYOUTS = (
     ("feed_forward", ("w1", "w3", "w2")),
     ("mlp", ("gate_proj", "up_proj", "down_proj")),
 )
+
+
+# Linears of a layout that read the same input: tied by swap_to_nmsparse.
+_SIBLINGS = {"wqkv": None, "q_proj": ("q_proj", "k_proj", "v_proj"), "w1": ("w1", "w3"),
+             "gate_proj": ("gate_proj", "up_proj")}
 
 
 def _resolve_layout(blk, layouts, kind):
@@ -273,7 +372,7 @@ def _swap_linears(submodule, names, M, device, seed, cnt, init=None, keep_dense=
 
 
 def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None, keep_dense=None,
-                     from_weights=False):
+                     from_weights=False, tie=True):
     """Swap every attention and MLP Linear of `model.layers` to NmSparseLinear.
 
     Blocks are visited in order, attention before MLP, Linears in layout
@@ -281,9 +380,12 @@ def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None,
     optionally gives one device (index or "cuda:N") per block. Returns the
     number of swapped Linears. Keyword-only extras of this build: `init`
     ("reference" | "device", default from NM_SYNTH_INIT), `keep_dense`
-    (default: not NM_DECODE_ONLY) and `from_weights` (pack each Linear's own
+    (default: not NM_DECODE_ONLY), `from_weights` (pack each Linear's own
     weight, which must already be 50% M-group pruned with a shared mask,
-    instead of drawing synthetic weights; seeds are then unused).
+    instead of drawing synthetic weights; seeds are then unused) and `tie`
+    (default True: the Linears of a block that read the same input, q/k/v
+    and gate/up (w1/w3), become one SiblingLaunch, so the unchanged model
+    code runs them as one grouped launch; untie_siblings undoes it).
     """
     cnt = 0
     for i, blk in enumerate(model.layers):
@@ -291,11 +393,14 @@ def swap_to_nmsparse(model, M, device, seed=0, block_devices=None, *, init=None,
         if block_devices is not None:
             d = block_devices[i]
             blk_device = d if isinstance(d, str) else f"cuda:{d}"
-        attn, attn_names = _resolve_layout(blk, _ATTENTION_LAYOUTS, "attention")
-        cnt = _swap_linears(attn, attn_names, M, blk_device, seed, cnt, init, keep_dense, from_weights)
-        mlp, mlp_names = _resolve_layout(blk, _MLP_LAYOUTS, "feed-forward")
-        cnt = _swap_linears(mlp, mlp_names, M, blk_device, seed, cnt, init, keep_dense, from_weights)
+        for layouts, kind in ((_ATTENTION_LAYOUTS, "attention"), (_MLP_LAYOUTS, "feed-forward")):
+            sub, names = _resolve_layout(blk, layouts, kind)
+            cnt = _swap_linears(sub, names, M, blk_device, seed, cnt, init, keep_dense, from_weights)
+            sibs = _SIBLINGS.get(names[0])
+            if tie and sibs:
+                tie_siblings(*(getattr(sub, n) for n in sibs))
     return cnt
 
 
-__all__ = ["NmSparseLinear", "swap_to_nmsparse", "pack_dense", "index_from_pruned", "_make_sparse"]
+__all__ = ["NmSparseLinear", "swap_to_nmsparse", "pack_dense", "index_from_pruned", "_make_sparse", "SiblingLaunch",
+           "tie_siblings", "untie_siblings"]

@@ -32,6 +32,19 @@ def test_mask_recovered_and_packing_reproduces_the_weight(M):
     assert torch.equal(back.view(torch.int16), W.view(torch.int16))  # bit for bit, signed zeros included
 
 
+@pytest.mark.parametrize("M", [4, 64])
+def test_to_dense_is_the_oracle_scatter(M):
+    """NmSparseLinear.to_dense equals the oracle's scatter (microbench_triton_torchmv.py:145-164)
+    bit for bit, and packing it again gives the module's buffers back."""
+    lin = NmSparseLinear(384, 4 * M, M, 3, "cpu")
+    dense = lin.to_dense()
+    ref = O.scatter(lin.mat_data, lin.mat_index, M // 2, M, 4 * M)
+    assert dense.shape == (384, 4 * M) and torch.equal(dense.view(torch.int16), ref.view(torch.int16))
+    assert torch.equal(pack_dense(dense, lin.mat_index, M).view(torch.int16), lin.mat_data.view(torch.int16))
+    assert lin.to_dense(torch.float32).dtype == torch.float32
+    assert torch.equal(lin.to_dense(torch.float32), ref.float())
+
+
 def test_all_zero_kept_positions_are_completed_deterministically():
     W, mi = _pruned(128, 64, 8, seed=3)
     pos = (torch.arange(mi.numel()) // 4) * 8 + mi.reshape(-1).long()

@@ -371,10 +371,81 @@ def test_launch_modes_are_validated_and_applied():
         model.set_launch_mode("fast")
     model.set_launch_mode("per_linear")
     assert not model.fuse_epilogues and not model.layers[0].self_attn.group_launches
+    assert not model.layers[0].self_attn.call_modules
     model.set_launch_mode("grouped")
     assert not model.fuse_epilogues and model.layers[1].mlp.group_launches
+    model.set_launch_mode("modules")
+    at, mlp = model.layers[1].self_attn, model.layers[1].mlp
+    assert not model.fuse_epilogues and not at.group_launches and at.call_modules and mlp.call_modules
     model.set_launch_mode("fused")
-    assert model.fuse_epilogues
+    assert model.fuse_epilogues and not at.call_modules
+
+
+def test_modules_mode_runs_the_same_dense_model():
+    """"modules" calls every projection as a module; on a dense model it computes
+    the per-Linear logits."""
+    torch.manual_seed(0)
+    model = Decoder(tiny_config(qk_norm=True)).float()
+    init_weights_(model, seed=12, std=0.05)
+    tokens = torch.tensor([9, 8, 400, 33])
+
+    def run():
+        model.setup_cache(8, "cpu", dtype=torch.float32)
+        with torch.no_grad():
+            return torch.cat([model.forward_step(t.view(1, 1), torch.tensor([i])) for i, t in enumerate(tokens)])
+
+    model.set_launch_mode("per_linear")
+    ref = run()
+    model.set_launch_mode("modules")
+    torch.testing.assert_close(run(), ref, rtol=1e-5, atol=1e-5)
+
+
+def test_swap_ties_the_siblings_of_each_layout():
+    """q/k/v and gate/up (gpt-fast: w1/w3) of each block become one sibling group;
+    the group is neither a submodule nor in the state_dict; untie_siblings drops it;
+    tie=False leaves every Linear on its own."""
+    import torch.nn as nn
+
+    from spmv_decode_amd.nmsparse_linear import SiblingLaunch, untie_siblings
+
+    model = Decoder(tiny_config())
+    swap_to_nmsparse(model, 8, "cpu", seed=1, keep_dense=False)
+    for blk in model.layers:
+        at, mlp = blk.self_attn, blk.mlp
+        g = at.q_proj.__dict__["_siblings"]
+        assert isinstance(g, SiblingLaunch) and g.members == [at.q_proj, at.k_proj, at.v_proj]
+        assert at.k_proj.__dict__["_siblings"] is g and "_siblings" not in at.o_proj.__dict__
+        g2 = mlp.up_proj.__dict__["_siblings"]
+        assert g2.members == [mlp.gate_proj, mlp.up_proj] and "_siblings" not in mlp.down_proj.__dict__
+    assert all(not isinstance(m, SiblingLaunch) for m in model.modules())
+    model2 = Decoder(tiny_config())
+    swap_to_nmsparse(model2, 8, "cpu", seed=1, keep_dense=False, tie=False)
+    assert all("_siblings" not in m.__dict__ for m in model2.modules())
+    sd, sd2 = model.state_dict(), model2.state_dict()
+    assert list(sd) == list(sd2)  # ties add no state; the swapped buffers are the same seeded draws
+    assert all(torch.equal(sd[k], sd2[k]) for k in sd if ".mat_" in k)
+    assert untie_siblings(model) == 5 * model.cfg.n_layers
+    assert all("_siblings" not in m.__dict__ for m in model.modules())
+
+    class GptFastBlock(nn.Module):  # gpt-fast's layout: fused wqkv, MLP w1/w3/w2
+        def __init__(self):
+            super().__init__()
+            self.attention = nn.Module()
+            self.attention.wqkv, self.attention.wo = nn.Linear(128, 384, bias=False), nn.Linear(128, 128, bias=False)
+            self.feed_forward = nn.Module()
+            ff = self.feed_forward
+            ff.w1, ff.w3 = nn.Linear(128, 256, bias=False), nn.Linear(128, 256, bias=False)
+            ff.w2 = nn.Linear(256, 128, bias=False)
+
+    stack = nn.Module()
+    stack.layers = nn.ModuleList([GptFastBlock(), GptFastBlock()])
+    assert swap_to_nmsparse(stack, 8, "cpu", seed=0, keep_dense=False) == 10
+    ff = stack.layers[1].feed_forward
+    assert ff.w1.__dict__["_siblings"].members == [ff.w1, ff.w3]
+    assert "_siblings" not in stack.layers[1].attention.wqkv.__dict__
+    with pytest.raises(ValueError, match="same K"):
+        from spmv_decode_amd.nmsparse_linear import tie_siblings
+        tie_siblings(ff.w1, ff.w2)
 
 
 @pytest.mark.parametrize("V", [128256, 151936, 512, 1000, 97])

@@ -641,10 +641,68 @@ def test_decoder_fused_layer_matches_grouped_and_per_linear_paths(gpu, qk_norm):
         finally:
             mdl.set_launch_mode("fused")
 
-    fused, grouped, per_linear = run("fused"), run("grouped"), run("per_linear")
-    for a, b, c in zip(fused, grouped, per_linear):
+    fused, grouped, per_linear, modules = run("fused"), run("grouped"), run("per_linear"), run("modules")
+    for a, b, c, d in zip(fused, grouped, per_linear, modules):
         torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
         torch.testing.assert_close(b, c, rtol=2e-2, atol=2e-2)
+        torch.testing.assert_close(d, c, rtol=2e-2, atol=2e-2)
+
+
+def test_tied_siblings_against_the_oracle(gpu, monkeypatch):
+    """Linears tied by swap_to_nmsparse (q/k/v here) called one after another on
+    the same input run as ONE grouped launch, in any call order, each output
+    within the oracle bar and equal to the grouped launch's; a new input object
+    or an in-place change of the input launches afresh (never a stale output);
+    inputs the group does not take fall back to the member's own op; under
+    hipGraph capture the graph holds the grouped launch and its replays follow
+    the captured input buffer's new contents."""
+    from spmv_decode_amd.nmsparse_linear import NmSparseLinear, tie_siblings
+
+    K, M = 4096, 64
+    mods = [NmSparseLinear(h, K, M, 30 + i, "cuda", init="device") for i, h in enumerate((4096, 1024, 1024))]
+    tie_siblings(*mods)
+    launches = []
+    real = hip_spmv.nmsparse_gemv_grouped
+    monkeypatch.setattr(hip_spmv, "nmsparse_gemv_grouped", lambda *a, **k: launches.append(1) or real(*a, **k))
+    g = torch.Generator(device="cuda").manual_seed(4)
+    x = torch.randn(1, 1, K, generator=g, device="cuda").half()
+    outs = {i: mods[i](x) for i in (1, 0, 2)}  # k first: it launches for all three
+    assert len(launches) == 1
+    ref = real(x.view(1, -1), [(m.mat_data, m.mat_index) for m in mods], 32, 64)
+    for i, mod in enumerate(mods):
+        assert outs[i].shape == (1, 1, mod.h) and torch.equal(outs[i].view(1, -1), ref[i])
+        check_parity(outs[i].view(1, -1), x.view(1, -1), mod.mat_data, mod.mat_index, 32, 64, f"tied {i}")
+    x2 = x.clone()  # same values, another object: launched afresh
+    assert torch.equal(mods[2](x2), outs[2]) and len(launches) == 2
+    assert torch.equal(mods[2](x2), outs[2]) and len(launches) == 3  # v again: no second hand-out
+    y_q = mods[0](x)  # launches for x (k, v pending) ...
+    x.mul_(2)  # ... then the input changes in place: k must see the new values
+    y_k = mods[1](x)
+    assert len(launches) == 5 and torch.equal(y_q, outs[0])
+    check_parity(y_k.view(1, -1), x.view(1, -1), mods[1].mat_data, mods[1].mat_index, 32, 64, "k after x*2")
+    xb = x.view(1, K).bfloat16()  # a dtype the group does not take: each member's own op
+    assert mods[0](xb).dtype == torch.bfloat16 and len(launches) == 5
+    # graph capture of the three calls on a static input
+    xs = torch.zeros(1, 1, K, dtype=torch.float16, device="cuda")
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):  # warm-up on the capture stream
+        [m(xs) for m in mods]
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    n0 = len(launches)
+    with torch.cuda.graph(graph, stream=st):
+        gouts = [m(xs) for m in mods]
+    assert len(launches) == n0 + 1
+    for rep in range(3):
+        say(f"tied siblings graph replay {rep}")
+        xs.copy_(torch.randn(1, 1, K, generator=g, device="cuda").half())
+        graph.replay()
+        torch.cuda.synchronize()
+        for i, mod in enumerate(mods):
+            check_parity(gouts[i].view(1, -1), xs.view(1, -1), mod.mat_data, mod.mat_index, 32, 64, f"graph {rep} {i}")
+        assert torch.equal(mods[1](x.clone()), y_k)  # eager work between the replays
+        torch.cuda.synchronize()
 
 
 def test_module_under_torch_compile_matches_eager(gpu):
