@@ -18,10 +18,12 @@ The sparse model runs the fused layer (norms, RoPE, cache write and residuals
 inside the GEMV launches); `--per-linear` also times it with one launch per
 Linear and PyTorch norms/RoPE (the step structure of the unfused dense
 model), `--grouped` with one q/k/v and one gate/up launch and PyTorch
-norms/RoPE (the structure of the fused dense modes). `--fixed-ctx 512` times
+norms/RoPE (the structure of the fused dense modes), `--modules` as unmodified
+model code calls it (each projection a module call; swap_to_nmsparse's ties
+give q/k/v and gate/up one launch each). `--fixed-ctx 512` times
 the reference benchmark's protocol instead (caches of random values, one
-step at a fixed position replayed; runner.fixed_context_ms) with its
-`RESULT CTX=...` line; `--compile` runs every variant's step through
+step at a fixed position replayed, the next token sampled as the reference
+does; runner.fixed_context_ms) with its `RESULT CTX=...` line; `--compile` runs every variant's step through
 torch.compile first, as the reference benchmark does.
 Prints a `RESULT` line per model variant (like the reference benchmarks,
 benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:186-189) and one JSON line.
@@ -91,6 +93,9 @@ def main(argv=None):
     p.add_argument("--grouped", action="store_true",
                    help="also time the sparse model with one q/k/v and one gate/up launch and PyTorch norms/RoPE "
                         "(the step structure of the fused dense modes)")
+    p.add_argument("--modules", action="store_true",
+                   help="also time the sparse model as unmodified model code runs it: every projection called as a "
+                        "module, q/k/v and gate/up sharing a launch through swap_to_nmsparse's ties")
     p.add_argument("--fixed-ctx", type=int, default=0, metavar="CTX",
                    help="time the reference benchmark's protocol instead: one decode step at position CTX over "
                         "random-filled caches, replayed (runner.fixed_context_ms)")
@@ -209,6 +214,13 @@ def main(argv=None):
             res["sparse_grouped"] = u
             if "dense" in res:
                 res["speedup_sparse_grouped_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
+        if a.modules:
+            model.set_launch_mode("modules")
+            u = measure("sparse modules", f"{tag} modules")
+            model.set_launch_mode("fused")
+            res["sparse_modules"] = u
+            if "dense" in res:
+                res["speedup_sparse_modules_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
     print(json.dumps(res), flush=True)
     if a.json:
         with open(a.json, "w") as f:

@@ -315,29 +315,27 @@ def fusable(block: Block) -> bool:
 
 def fused_block_step(blk: Block, x2d, k_cache_t, v_cache_t, pos, q_pad, zero, rope):
     """One fused sparse layer on the residual stream x2d [1, dim], updated in
-    place. rope: complex64 [S, head_dim/2] table of the cache's positions;
-    caches, q_pad and zero as in attend."""
-    from ..hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
-
+    place. rope: fp32 [S, head_dim/2, 2] (cos, sin) table of the cache's
+    positions; caches, q_pad and zero as in attend. Four launches, each a
+    `torch.ops.nmsparse` op (so torch.compile traces the step whole)."""
     at, mlp = blk.self_attn, blk.mlp
     c = at.cfg
     qd = c.n_heads * c.head_dim
     ln1, ln2 = blk.input_layernorm, blk.post_attention_layernorm
     qp, kp, vp = at.q_proj, at.k_proj, at.v_proj
-    nmsparse_qkv_decode(x2d, (qp.mat_data, qp.mat_index), (kp.mat_data, kp.mat_index), (vp.mat_data, vp.mat_index),
-                        qp.block_width, qp.vec_width, q_out=q_pad, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
-                        rope_table=rope, head_dim=c.head_dim, norm=(ln1.weight, ln1.eps),
-                        q_norm=at.q_norm.weight if c.qk_norm else None,
-                        k_norm=at.k_norm.weight if c.qk_norm else None, head_eps=c.norm_eps)
+    ops = torch.ops.nmsparse
+    ops.qkv_decode(x2d, qp.mat_data, qp.mat_index, kp.mat_data, kp.mat_index, vp.mat_data, vp.mat_index,
+                   qp.block_width, qp.vec_width, q_pad, k_cache_t, v_cache_t, pos, rope, c.head_dim, ln1.weight,
+                   ln1.eps, at.q_norm.weight if c.qk_norm else None, at.k_norm.weight if c.qk_norm else None,
+                   c.norm_eps)
     y = attend(q_pad, k_cache_t, v_cache_t, c, zero).view(1, qd)
     o = at.o_proj
-    nmsparse_gemv_launch(y, [GemvProblem(o.mat_data, o.mat_index, x2d, residual=x2d)], o.block_width, o.vec_width)
+    ops.gemv_add_(y, o.mat_data, o.mat_index, o.block_width, o.vec_width, x2d)
     gp, up = mlp.gate_proj, mlp.up_proj
-    act = nmsparse_gate_up_silu(x2d, (gp.mat_data, gp.mat_index), (up.mat_data, up.mat_index), gp.block_width,
-                                gp.vec_width, norm=(ln2.weight, ln2.eps))
+    act = ops.gate_up_silu(x2d, gp.mat_data, gp.mat_index, up.mat_data, up.mat_index, gp.block_width, gp.vec_width,
+                           ln2.weight, ln2.eps)
     d = mlp.down_proj
-    nmsparse_gemv_launch(act, [GemvProblem(d.mat_data, d.mat_index, x2d, residual=x2d)], d.block_width,
-                         d.vec_width)
+    ops.gemv_add_(act, d.mat_data, d.mat_index, d.block_width, d.vec_width, x2d)
     return x2d
 
 
@@ -467,6 +465,7 @@ class Decoder(nn.Module):
         t = torch.arange(max_seq, dtype=torch.float64)
         ang = torch.outer(t, rope_inv_freq(c))
         self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
+        self.rope_real = torch.view_as_real(self.rope)  # the same table as fp32 (cos, sin) pairs
         self.positions = torch.arange(max_seq, device=device)
 
     def reset_cache(self):
@@ -480,12 +479,16 @@ class Decoder(nn.Module):
         -> logits [1, vocab]. No host synchronisation."""
         x = self.embed_tokens(token)  # [1, 1, dim]
         # causal mask of this step in every layer's key cache: 0 up to pos, -inf after
-        torch.where((self.positions <= pos).expand_as(self.k_mask), self.zero, self.neg_inf, out=self.k_mask)
+        keep = (self.positions <= pos).expand_as(self.k_mask)
+        if torch.compiler.is_compiling():  # the tracer takes no strided out=; the compiler fuses the copy
+            self.k_mask.copy_(torch.where(keep, self.zero, self.neg_inf))
+        else:
+            torch.where(keep, self.zero, self.neg_inf, out=self.k_mask)
         if self.fuse_epilogues and all(fusable(b) and b.self_attn.group_launches for b in self.layers):
             x2d = x.view(1, -1)
             for i, blk in enumerate(self.layers):
                 fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero,
-                                 self.rope)
+                                 self.rope_real)
             return project(self.lm_head, self.norm(x)).view(1, -1)
         freqs = self.rope.index_select(0, pos)
         for i, layer in enumerate(self.layers):

@@ -53,16 +53,27 @@ def cache_length(max_seq: int) -> int:
     return -(-max_seq // CACHE_ALIGN) * CACHE_ALIGN
 
 
+def sample_token(logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+    """The reference's sampling step (generate.py:46-63;
+    benchmarks/bench_qwen_31_14b_fp16_fixed_ptx.py:356-357): softmax of the
+    logits in fp32, cast back to the logits' dtype, one multinomial draw from
+    torch's device generator (graph-safe); writes the token id into `out` [1]."""
+    probs = torch.softmax(logits.float(), dim=-1).to(logits.dtype)
+    return out.copy_(torch.multinomial(probs, num_samples=1).view(1))
+
+
 @torch.no_grad()
 def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 30, inner: int = 10,
-                     seed: int = 1234, token_id: int = 123, device="cuda") -> dict:
+                     seed: int = 1234, token_id: int = 123, device="cuda", sample: bool = True) -> dict:
     """The reference benchmark's fixed-context protocol
     (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:144-189): KV caches for
     ctx + 1 positions filled with N(0, 0.02), one decode step of `token_id` at
-    position `ctx` (with its greedy next token; the reference samples) captured
-    as one hipGraph, `warmup` replays, then `repeat` samples of `inner`
-    replays each; every replay decodes the same position. Returns the median,
-    mean and stdev of the samples in ms per replay, and the samples."""
+    position `ctx`, with the next token sampled as the reference's step does
+    (softmax + multinomial, sample_token; `sample=False`: greedy), captured as
+    one hipGraph, `warmup` replays, then `repeat` samples of `inner` replays
+    each; every replay decodes the same position. Returns the median, mean and
+    stdev of the samples in ms per replay, the samples, the last replay's
+    logits (fp32, host), their greedy token and the last sampled token."""
     if min(ctx, warmup, repeat, inner) < 1:
         raise ValueError("ctx, warmup, repeat and inner must be positive")
     dev = torch.device(device)
@@ -78,7 +89,10 @@ def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 3
 
     def step():
         logits = model.forward_step(token, pos)
-        greedy_token(logits, out=nxt)
+        if sample:
+            sample_token(logits, out=nxt)
+        else:
+            greedy_token(logits, out=nxt)
         return logits
 
     stream = torch.cuda.Stream(device=dev)
@@ -104,10 +118,12 @@ def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 3
         b.synchronize()
         samples.append(a.elapsed_time(b) / inner)
     finite = bool(torch.isfinite(logits).all().item())
+    host_logits = logits.float().cpu()
     del graph
     return {"median": statistics.median(samples), "mean": statistics.mean(samples),
             "stdev": statistics.stdev(samples) if repeat > 1 else 0.0, "samples": samples,
-            "finite_logits": finite, "token": int(nxt.item())}
+            "finite_logits": finite, "token": int(torch.argmax(host_logits, dim=-1)), "logits": host_logits,
+            "sampled_token": int(nxt.item()) if sample else None, "sampling": "multinomial" if sample else "greedy"}
 
 
 class GraphDecoder:

@@ -10,6 +10,15 @@ fp16 if needed, the result is cast back to x.dtype and reshaped to
 of rows, NM_MAX_BATCH per launch of the small-batch SpMM kernel, same casts
 and output shape rule as `gemv`.
 
+The fused decode-layer launches are ops too, so that torch.compile traces a
+decode step that uses them without graph breaks (no reference counterpart;
+they replace the PyTorch operations around the reference's sparse Linears):
+`nmsparse::qkv_decode` (q/k/v with the input RMSNorm, Qwen3's head norms,
+RoPE and the KV-cache write; mutates the query buffer and both caches),
+`nmsparse::gemv_add_` (out += W x, the residual add inside the GEMV; mutates
+out) and `nmsparse::gate_up_silu` (silu(W_gate x) * (W_up x) with the input
+RMSNorm folded in). They take fp16/bf16/fp32 inputs as they are (no casts).
+
 Backend selection keeps the reference's `NM_KERNEL` contract of refusing
 unknown values (src/spmv/nmsparse_op.py:20-22). Unset, "hip" and
 "triton_ptx" all select the one shared-mask HIP kernel. `_mode` reads
@@ -27,7 +36,10 @@ import os
 
 import torch
 
-from .hip_spmv import nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip
+from typing import Optional
+
+from .hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode,
+                       nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip)
 
 _kernel = os.environ.get("NM_KERNEL", "")
 if _kernel not in ("", "hip", "triton_ptx", "guarded", "fp16", "fp16_split"):
@@ -76,4 +88,54 @@ def _(x, mat_data, mat_index, w, h, block_width, vec_width):
     return x.new_empty((*x.shape[:-1], int(h)))
 
 
-__all__ = ["gemv", "spmm"]
+@torch.library.custom_op("nmsparse::qkv_decode", mutates_args=("q_out", "k_cache_t", "v_cache_t"))
+def qkv_decode(x: torch.Tensor, q_data: torch.Tensor, q_index: torch.Tensor, k_data: torch.Tensor,
+               k_index: torch.Tensor, v_data: torch.Tensor, v_index: torch.Tensor, block_width: int, vec_width: int,
+               q_out: torch.Tensor, k_cache_t: torch.Tensor, v_cache_t: torch.Tensor, pos: torch.Tensor,
+               rope_table: torch.Tensor, head_dim: int, norm_weight: Optional[torch.Tensor], norm_eps: float,
+               q_norm: Optional[torch.Tensor], k_norm: Optional[torch.Tensor], head_eps: float) -> None:
+    """hip_spmv.nmsparse_qkv_decode with transposed key and value caches
+    ([kv_heads, >= head_dim, S] and [kv_heads, head_dim, S]) and rope_table
+    fp32 [S', head_dim / 2, 2] (S' >= S)."""
+    nmsparse_qkv_decode(x.view(1, -1), (q_data, q_index), (k_data, k_index), (v_data, v_index), int(block_width),
+                        int(vec_width), q_out=q_out, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
+                        rope_table=rope_table, head_dim=int(head_dim),
+                        norm=None if norm_weight is None else (norm_weight, float(norm_eps)), q_norm=q_norm,
+                        k_norm=k_norm, head_eps=float(head_eps))
+
+
+@qkv_decode.register_fake
+def _(x, q_data, q_index, k_data, k_index, v_data, v_index, block_width, vec_width, q_out, k_cache_t, v_cache_t,
+      pos, rope_table, head_dim, norm_weight, norm_eps, q_norm, k_norm, head_eps):
+    return None
+
+
+@torch.library.custom_op("nmsparse::gemv_add_", mutates_args=("out",))
+def gemv_add_(x: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor, block_width: int, vec_width: int,
+              out: torch.Tensor) -> None:
+    """out [1, h] += W_sparse x, added in fp32 inside the launch before the one
+    rounding (the residual add of a decoder layer, in place)."""
+    nmsparse_gemv_launch(x.view(1, -1), [GemvProblem(mat_data, mat_index, out, residual=out)], int(block_width),
+                         int(vec_width))
+
+
+@gemv_add_.register_fake
+def _(x, mat_data, mat_index, block_width, vec_width, out):
+    return None
+
+
+@torch.library.custom_op("nmsparse::gate_up_silu", mutates_args=())
+def gate_up_silu(x: torch.Tensor, gate_data: torch.Tensor, gate_index: torch.Tensor, up_data: torch.Tensor,
+                 up_index: torch.Tensor, block_width: int, vec_width: int, norm_weight: Optional[torch.Tensor],
+                 norm_eps: float) -> torch.Tensor:
+    """silu(W_gate x') * (W_up x') -> [1, h], x' = RMSNorm(x) when norm_weight is given."""
+    return nmsparse_gate_up_silu(x.view(1, -1), (gate_data, gate_index), (up_data, up_index), int(block_width),
+                                 int(vec_width), norm=None if norm_weight is None else (norm_weight, float(norm_eps)))
+
+
+@gate_up_silu.register_fake
+def _(x, gate_data, gate_index, up_data, up_index, block_width, vec_width, norm_weight, norm_eps):
+    return x.new_empty((1, gate_data.shape[1]))
+
+
+__all__ = ["gemv", "spmm", "qkv_decode", "gemv_add_", "gate_up_silu"]

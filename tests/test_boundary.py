@@ -194,6 +194,21 @@ def test_op_fake_impl_shapes():
         assert y.dtype == torch.bfloat16
 
 
+def test_fused_decode_ops_schemas_and_fakes():
+    """The fused decode launches are ops (so a compiled step traces them): their
+    mutated arguments are declared, gate_up_silu's fake output is [1, h]."""
+    from torch._subclasses.fake_tensor import FakeTensorMode
+
+    assert "Tensor(a9!) q_out" in str(torch.ops.nmsparse.qkv_decode.default._schema)
+    assert "Tensor(a5!) out" in str(torch.ops.nmsparse.gemv_add_.default._schema)
+    with FakeTensorMode():
+        x = torch.empty(1, 4096, dtype=torch.float16)
+        md = torch.empty(2048, 14336, dtype=torch.float16)
+        mi = torch.empty(64, 32, dtype=torch.uint8)
+        y = torch.ops.nmsparse.gate_up_silu(x, md, mi, md, mi, 32, 64, torch.empty(4096, dtype=torch.float16), 1e-5)
+        assert tuple(y.shape) == (1, 14336) and y.dtype == torch.float16
+
+
 def test_op_rejects_more_than_one_row():
     x = torch.zeros(1, 2, 256, dtype=torch.float16)
     md = torch.zeros(128, 256, dtype=torch.float16)
