@@ -501,14 +501,17 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
     //    The handoff uses agent-scope atomics only, never an agent-scope
     //    fence: on gfx950 such a fence writes back and invalidates the whole
     //    L2 of the workgroup's XCD (buffer_wbl2 / buffer_inv), which costs
-    //    more than the GEMV itself. Each partial is published with a
-    //    returning atomic swap: its result comes back only after the swap has
-    //    been performed at the device coherence point, and each lane waits
-    //    for all of its results (vmcnt(0)) before the barrier. Lane 0 then
-    //    counts the arrival; the last arrival reads every partial with
-    //    agent-scope atomic loads (sc1, coherent across XCDs) in split order,
-    //    so the sum is deterministic.
-    float sink = 0.0f;
+    //    more than the GEMV itself, and exists to make non-atomic data
+    //    coherent; every word shared here is written and read by agent-scope
+    //    atomics. Each partial is published with an agent-scope atomic swap
+    //    (relaxed, result unused: the no-return global_atomic_swap, performed
+    //    at the agent's coherence point like every agent-scope RMW), and each
+    //    lane waits for the completion of all of them (vmcnt counts
+    //    no-return atomics on gfx9-family GPUs) before the barrier. Lane 0
+    //    then counts the arrival (a returning agent-scope add); the last
+    //    arrival, ordered after its add's returned value, reads every partial
+    //    with agent-scope atomic loads (sc1) in split order, so the sum is
+    //    deterministic.
 #pragma unroll
     for (int q = 0; q < NMAT; ++q) {
       float* part = a.prob[NMAT == 1 ? p : q].partial + (size_t)split * (size_t)h;
@@ -517,12 +520,9 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
         const int o = tid + j * kBlock;
         const int r = tile * HT + o;
         if (o < HT && r < h)
-          sink += __hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          (void)__hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    // Consume the swap results (a.splits is never negative) so the compiler
-    // keeps the returning form of the instruction.
-    if (a.splits < 0) static_cast<T*>(P.out)[tid] = E::from_f32(sink);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {
@@ -855,7 +855,6 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_kernel(SpmmArgs a) {
 
   // 6. Split-K handoff (as nm_gemv_kernel; partials [split, batch, h]).
   if (a.splits > 1) {
-    float sink = 0.0f;
 #pragma unroll
     for (int b = 0; b < NB; ++b) {
       if (b >= a.batch) break;
@@ -865,10 +864,9 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_kernel(SpmmArgs a) {
         const int o = tid + j * kBlock;
         const int r = tile * HT + o;
         if (o < HT && r < h)
-          sink += __hip_atomic_exchange(part + r, tsum[b][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          (void)__hip_atomic_exchange(part + r, tsum[b][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
     }
-    if (a.splits < 0) static_cast<T*>(a.out)[tid] = E::from_f32(sink);
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
     if (tid == 0) {

@@ -732,3 +732,69 @@ def test_module_under_torch_compile_matches_eager(gpu):
         got = compiled(x)
         torch.cuda.synchronize()
         assert torch.equal(got, eager)
+
+
+def test_split_k_handoff_soak_2000_replays(gpu):
+    """The split-K handoff orders its partials by hardware completion (no-return
+    agent-scope atomic swaps waited for with vmcnt, a returning agent-scope ticket
+    add, agent-scope loads after it), not by a language-level happens-before. A
+    rare visibility miss would show as a wrong sum, not a fault, so: the four
+    decode launch classes at the Llama-3.1-8B shapes (32:64; 8 splits each,
+    192-448 workgroups over every XCD) in one hipGraph, made idempotent (fixed
+    position, residuals read from other buffers than they write), replayed 2000
+    times; every replay's outputs bitwise equal to the first replay's, checked
+    after each replay, stopping at the first mismatch; the first replay's down
+    output within the oracle bar."""
+    from spmv_decode_amd.decode.model import KEY_PAD
+    from spmv_decode_amd.hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch,
+                                          nmsparse_qkv_decode)
+
+    g = torch.Generator(device="cuda").manual_seed(11)
+    mats = {}
+    for i, (name, K, h) in enumerate((("q", 4096, 4096), ("k", 4096, 1024), ("v", 4096, 1024), ("o", 4096, 4096),
+                                      ("gate", 4096, 14336), ("up", 4096, 14336), ("down", 14336, 4096))):
+        _, md, mi = make_case(K, h, 32, 64, seed=100 + i)
+        mats[name] = (md, mi)
+    S = 256
+    x = torch.randn(1, 4096, generator=g, device="cuda").half()
+    attn = torch.randn(1, 4096, generator=g, device="cuda").half()
+    ln1, ln2 = ((torch.rand(4096, generator=g, device="cuda") + 0.5).half() for _ in range(2))
+    q_out = torch.zeros(32, 128 + KEY_PAD, dtype=torch.float16, device="cuda")
+    kc = torch.zeros(8, 128 + KEY_PAD, S, dtype=torch.float16, device="cuda")
+    vc = torch.zeros(8, 128, S, dtype=torch.float16, device="cuda")
+    ang = torch.outer(torch.arange(S, dtype=torch.float64), torch.rand(64, dtype=torch.float64))
+    rope = torch.view_as_real(torch.polar(torch.ones_like(ang), ang).to(torch.complex64)).cuda()
+    pos = torch.tensor([S // 3], device="cuda")
+    h1, h2 = torch.empty_like(x), torch.empty_like(x)
+    act = torch.empty(1, 14336, dtype=torch.float16, device="cuda")
+
+    def layer():
+        nmsparse_qkv_decode(x, mats["q"], mats["k"], mats["v"], 32, 64, q_out=q_out, k_cache_t=kc, v_cache_t=vc,
+                            pos=pos, rope_table=rope, head_dim=128, norm=(ln1, 1e-5))
+        nmsparse_gemv_launch(attn, [GemvProblem(*mats["o"], h1, residual=x)], 32, 64)
+        nmsparse_gate_up_silu(h1, mats["gate"], mats["up"], 32, 64, out=act, norm=(ln2, 1e-5))
+        nmsparse_gemv_launch(act, [GemvProblem(*mats["down"], h2, residual=h1)], 32, 64)
+
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        layer()
+    torch.cuda.current_stream().wait_stream(st)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=st):
+        layer()
+    outs = (q_out, kc, vc, h1, act, h2)
+    graph.replay()
+    torch.cuda.synchronize()
+    first = [t.clone() for t in outs]
+    ref = O.gemv_f64(act.cpu(), mats["down"][0].cpu(), mats["down"][1].cpu(), 32, 64) + h1.float().cpu().numpy()[0]
+    e = O.error_metrics(ref, h2.float().cpu().numpy().reshape(-1))
+    assert e["max_abs"] <= 1e-2 and e["rel_l2"] <= 1e-3, e
+    for rep in range(1, 2000):
+        graph.replay()
+        torch.cuda.synchronize()
+        for t, f, name in zip(outs, first, ("q", "k cache", "v cache", "o+resid", "gate/up", "down+resid")):
+            if not torch.equal(t, f):
+                pytest.fail(f"replay {rep}: {name} differs from the first replay")
+        if rep % 500 == 0:
+            say(f"handoff soak: {rep} replays bit-identical")
