@@ -221,6 +221,17 @@ def main(argv=None):
             res["sparse_modules"] = u
             if "dense" in res:
                 res["speedup_sparse_modules_vs_dense"] = round(res["dense"]["ms_per_token"] / u["ms_per_token"], 4)
+    structure = {}  # each sparse launch structure over the dense model with the same launches per layer
+    dv = {res["dense"]["fusion"]: res["dense"]} if res.get("dense") else {}
+    dv.update({k: v for k, v in res.get("dense_variants", {}).items()})
+    for key, dense_mode, label in (("sparse", "qkv", "fused_vs_dense_qkv_fused"),
+                                   ("sparse_per_linear", "none", "per_linear_vs_dense_per_linear"),
+                                   ("sparse_modules", "none", "modules_vs_dense_per_linear"),
+                                   ("sparse_grouped", "qkv_gate_up", "grouped_vs_dense_qkv_gate_up_fused")):
+        if res.get(key) and dense_mode in dv:
+            structure[label] = round(dv[dense_mode]["ms_per_token"] / res[key]["ms_per_token"], 4)
+    if structure:
+        res["speedup_structure_matched"] = structure
     print(json.dumps(res), flush=True)
     if a.json:
         with open(a.json, "w") as f:

@@ -227,7 +227,9 @@ def decode_table(json_paths):
         variants = [(fusion_label.get(v.get("fusion"), "dense"), v, None) for _, v in dense]
         variants += [(f"{ratio} fused layer", d.get("sparse"), sparse_bytes),
                      (f"{ratio} per-Linear", d.get("sparse_per_linear"), sparse_bytes),
-                     (f"{ratio} grouped", d.get("sparse_grouped"), sparse_bytes)]
+                     (f"{ratio} grouped", d.get("sparse_grouped"), sparse_bytes),
+                     (f"{ratio} unmodified model (module calls, tied q/k/v and gate/up)", d.get("sparse_modules"),
+                      sparse_bytes)]
         if d.get("compiled"):
             variants = [(f"{label}, compiled", v, nb) for label, v, nb in variants]
         for label, v, nbytes in variants:
@@ -244,6 +246,8 @@ def decode_table(json_paths):
                 line += f", per-Linear {d['speedup_sparse_per_linear_vs_dense']:.4f}x"
             if "speedup_sparse_grouped_vs_dense" in d:
                 line += f", grouped {d['speedup_sparse_grouped_vs_dense']:.4f}x"
+            if "speedup_sparse_modules_vs_dense" in d:
+                line += f", unmodified model {d['speedup_sparse_modules_vs_dense']:.4f}x"
             hd = fusion_label.get(d["dense"].get("fusion"), "dense")
             line += f" (over {hd})"
             if len(dense) > 1 and d.get("sparse"):
@@ -251,9 +255,13 @@ def decode_table(json_paths):
                                        key=lambda t: t[1]["ms_per_token"])
                 line += (f"; fused layer over the fastest dense ({best_label}) "
                          f"{best['ms_per_token'] / d['sparse']['ms_per_token']:.4f}x")
-                for key, lab in (("sparse_per_linear", "per-Linear"), ("sparse_grouped", "grouped")):
+                for key, lab in (("sparse_per_linear", "per-Linear"), ("sparse_grouped", "grouped"),
+                                 ("sparse_modules", "unmodified model")):
                     if d.get(key):
                         line += f", {lab} {best['ms_per_token'] / d[key]['ms_per_token']:.4f}x"
+            if d.get("speedup_structure_matched"):
+                line += "; structure-matched: " + ", ".join(
+                    f"{k.replace('_', ' ')} {v:.4f}x" for k, v in d["speedup_structure_matched"].items())
             speed.append(line)
     if fixed:
         head = ["| Model | Context | Variant | ms/token (median of samples) | mean | stdev | tokens/s | "

@@ -39,6 +39,22 @@ def test_decode_table_rows_and_speedups(tmp_path):
     assert "fastest dense (dense, q/k/v and gate/up fused) 2.0000x, per-Linear 1.0000x, grouped 1.2500x" in speed
 
 
+def test_decode_table_unmodified_model_row_and_structure_matched_ratios(tmp_path):
+    d = {"model": "llama-3.1-8b", "prompt": 128, "gen": 256,
+         "dense": _variant(5.0, "qkv"), "dense_variants": {"none": _variant(6.0, "none")},
+         "sparse": {**_variant(2.0), "ratio": "32:64"}, "sparse_modules": _variant(3.75),
+         "speedup_sparse_vs_dense": 2.5, "speedup_sparse_modules_vs_dense": 1.3333,
+         "speedup_structure_matched": {"fused_vs_dense_qkv_fused": 2.5, "modules_vs_dense_per_linear": 1.6}}
+    path = tmp_path / "m.json"
+    path.write_text(json.dumps(d))
+    out = P.decode_table([str(path)])
+    rows = [ln for ln in out.splitlines() if ln.startswith("| Llama-3.1-8B")]
+    assert rows[-1].split(" | ")[2] == "32:64 unmodified model (module calls, tied q/k/v and gate/up)"
+    speed = out.splitlines()[-1]
+    assert "unmodified model 1.3333x" in speed and "fastest dense (dense, q/k/v fused) 2.5000x" in speed
+    assert "structure-matched: fused vs dense qkv fused 2.5000x, modules vs dense per linear 1.6000x" in speed
+
+
 def test_decode_table_sparse_only(tmp_path):
     d = {"model": "qwen3-14b", "prompt": 128, "gen": 256, "sparse": {**_variant(4.0), "ratio": "8:16"}}
     path = tmp_path / "s.json"
