@@ -53,13 +53,24 @@ def cache_length(max_seq: int) -> int:
     return -(-max_seq // CACHE_ALIGN) * CACHE_ALIGN
 
 
-def sample_token(logits: torch.Tensor, out: torch.Tensor) -> torch.Tensor:
+def sample_token(logits: torch.Tensor, out: torch.Tensor, generator: torch.Generator | None = None) -> torch.Tensor:
     """The reference's sampling step (generate.py:46-63;
-    benchmarks/bench_qwen_31_14b_fp16_fixed_ptx.py:356-357): softmax of the
-    logits in fp32, cast back to the logits' dtype, one multinomial draw from
-    torch's device generator (graph-safe); writes the token id into `out` [1]."""
+    benchmarks/bench_qwen_31_14b_fp16_fixed_ptx.py:356-357): the softmax of the
+    logits in fp32, cast back to the logits' dtype, and one draw from that
+    categorical distribution, written into `out` [1].
+
+    The draw is the exponential race that torch.multinomial itself uses for
+    one sample: with E_i ~ Exp(1) independent, argmax_i p_i / E_i is
+    distributed as Categorical(p) (the Gumbel-max trick, exponentiated). It is
+    written here with graph-safe pieces, torch's device generator
+    (`exponential_`) and the two-stage greedy_token argmax, because
+    torch.multinomial first checks its input with vocabulary-wide max/min
+    reductions whose multi-block form clears its semaphores with memset nodes
+    when captured; replayed, those gave wrong results on MI355X and the check's
+    device-side assert then aborted the run."""
     probs = torch.softmax(logits.float(), dim=-1).to(logits.dtype)
-    return out.copy_(torch.multinomial(probs, num_samples=1).view(1))
+    race = torch.empty(probs.shape, dtype=torch.float32, device=probs.device).exponential_(generator=generator)
+    return greedy_token(probs.float() / race, out=out)
 
 
 @torch.no_grad()

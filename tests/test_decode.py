@@ -536,3 +536,61 @@ def test_greedy_token_in_a_captured_graph(gpu):
         g.replay()
         torch.cuda.synchronize()
         assert int(out) == int(torch.argmax(logits, dim=-1)), rep
+
+
+def test_sample_token_draws_from_the_softmax_distribution():
+    """The exponential race (argmax p / E, E ~ Exp(1)) samples Categorical(softmax(logits)):
+    on the CPU, 40000 draws over 5 classes land within 5 standard errors of the
+    softmax probabilities (a wrong race, e.g. argmax p * E or argmax E, does not)."""
+    from spmv_decode_amd.decode.runner import sample_token
+
+    logits = torch.tensor([[2.0, 1.0, 0.0, -1.0, 0.5]]).half()
+    p = torch.softmax(logits.float(), dim=-1).half().float().view(-1)
+    p = p / p.sum()
+    g = torch.Generator().manual_seed(7)
+    n = 40000
+    counts = torch.zeros(5)
+    out = torch.zeros(1, dtype=torch.long)
+    for _ in range(n):
+        counts[int(sample_token(logits, out, generator=g))] += 1
+    freq = counts / n
+    se = (p * (1 - p) / n).sqrt()
+    assert ((freq - p).abs() <= 5 * se).all(), (freq, p)
+
+
+@pytest.mark.gpu
+def test_sample_token_in_a_captured_graph_over_many_replays(gpu):
+    """sample_token captured in a hipGraph at Qwen3's vocabulary (151936) and replayed
+    400 times, eager multi-block reductions and synchronisations between replays:
+    a dominant logit is drawn every time, and two equal logits split about evenly
+    (within 5 standard errors); no replay asserts or faults."""
+    from spmv_decode_amd.decode.runner import sample_token
+
+    V = 151936
+    logits = torch.randn(1, V, device="cuda", generator=torch.Generator(device="cuda").manual_seed(1)).half()
+    out = torch.zeros(1, dtype=torch.long, device="cuda")
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        sample_token(logits, out)
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=s):
+        sample_token(logits, out)
+    big = torch.randn(1 << 22, device="cuda")
+    for case, (hot, n) in enumerate((([777], 200), ([5, 150000], 400))):
+        logits.copy_(torch.randn(1, V, device="cuda").half())
+        logits[0, hot] = 40.0  # the rest is negligible: exp(-40) per token
+        counts = {}
+        for rep in range(n):
+            g.replay()
+            torch.cuda.synchronize()
+            t = int(out)
+            counts[t] = counts.get(t, 0) + 1
+            if rep % 50 == 0:
+                assert torch.isfinite(big.sum())  # eager multi-block work between replays
+        assert set(counts) <= set(hot), (case, counts)
+        if len(hot) == 2:
+            se = (0.25 / n) ** 0.5
+            assert abs(counts.get(hot[0], 0) / n - 0.5) <= 5 * se, counts
