@@ -491,8 +491,9 @@ def decode_ms_per_token(m, log):
            "dense_linear_bytes_per_token": linear_bytes(LLAMA31_8B, 0),
            "fixed_context_512": {
                "protocol": "the reference benchmark's (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:144-189): "
-                           "random-filled caches, one step at position 512 with the next token sampled (softmax + "
-                           "multinomial, generate.py:46-63) replayed, median of 30 x 10 replays",
+                           "random-filled caches, one step at position 512 with the next token sampled (softmax, one "
+                           "categorical draw as generate.py:46-63 makes with multinomial; drawn by the exponential "
+                           "race) replayed, median of 30 x 10 replays",
                "dense_ms_per_token": round(fc["qkv"], 4),
                "dense_ms_per_token_by_fusion": {k: round(v, 4) for k, v in fc.items()},
                "sparse_ms_per_token": round(fixed_sparse["median"], 4),

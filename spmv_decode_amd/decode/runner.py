@@ -80,7 +80,7 @@ def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 3
     (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:144-189): KV caches for
     ctx + 1 positions filled with N(0, 0.02), one decode step of `token_id` at
     position `ctx`, with the next token sampled as the reference's step does
-    (softmax + multinomial, sample_token; `sample=False`: greedy), captured as
+    (softmax, one categorical draw: sample_token; `sample=False`: greedy), captured as
     one hipGraph, `warmup` replays, then `repeat` samples of `inner` replays
     each; every replay decodes the same position. Returns the median, mean and
     stdev of the samples in ms per replay, the samples, the last replay's
@@ -134,7 +134,7 @@ def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 3
     return {"median": statistics.median(samples), "mean": statistics.mean(samples),
             "stdev": statistics.stdev(samples) if repeat > 1 else 0.0, "samples": samples,
             "finite_logits": finite, "token": int(torch.argmax(host_logits, dim=-1)), "logits": host_logits,
-            "sampled_token": int(nxt.item()) if sample else None, "sampling": "multinomial" if sample else "greedy"}
+            "sampled_token": int(nxt.item()) if sample else None, "sampling": "categorical" if sample else "greedy"}
 
 
 class GraphDecoder:

@@ -228,8 +228,8 @@ def decode_table(json_paths):
         variants += [(f"{ratio} fused layer", d.get("sparse"), sparse_bytes),
                      (f"{ratio} per-Linear", d.get("sparse_per_linear"), sparse_bytes),
                      (f"{ratio} grouped", d.get("sparse_grouped"), sparse_bytes),
-                     (f"{ratio} unmodified model (module calls, tied q/k/v and gate/up)", d.get("sparse_modules"),
-                      sparse_bytes)]
+                     (f"{ratio} unmodified model (module calls, " + ("each its own launch" if d.get("compiled")
+                      else "tied q/k/v and gate/up") + ")", d.get("sparse_modules"), sparse_bytes)]
         if d.get("compiled"):
             variants = [(f"{label}, compiled", v, nb) for label, v, nb in variants]
         for label, v, nbytes in variants:

@@ -365,7 +365,7 @@ def test_compiled_step_is_one_graph_and_matches_eager(gpu):
         finally:
             model.forward_step = eager_step
             torch._dynamo.reset()
-        assert got["finite_logits"] and got["sampling"] == "multinomial" and 0 <= got["sampled_token"] < cfg.vocab
+        assert got["finite_logits"] and got["sampling"] == "categorical" and 0 <= got["sampled_token"] < cfg.vocab
         torch.testing.assert_close(got["logits"], ref["logits"], rtol=2e-2, atol=2e-2)
         top2 = torch.topk(ref["logits"].view(-1), 2).values
         if float(top2[0] - top2[1]) > 4e-2:

@@ -55,6 +55,18 @@ def test_decode_table_unmodified_model_row_and_structure_matched_ratios(tmp_path
     assert "structure-matched: fused vs dense qkv fused 2.5000x, modules vs dense per linear 1.6000x" in speed
 
 
+def test_decode_table_compiled_unmodified_model_row_names_no_ties(tmp_path):
+    """Under torch.compile the sibling ties stand aside: the row must not claim them."""
+    fixed = lambda ms: {**_variant(ms), "ms_per_token_mean": ms, "stdev": 0.01}  # noqa: E731
+    d = {"model": "qwen3-14b", "protocol": "fixed_context", "ctx": 512, "compiled": True,
+         "sparse": {**fixed(4.0), "ratio": "32:64"}, "sparse_modules": fixed(6.5)}
+    path = tmp_path / "c.json"
+    path.write_text(json.dumps(d))
+    rows = [ln for ln in P.decode_table([str(path)]).splitlines() if ln.startswith("| Qwen3-14B")]
+    assert [r.split(" | ")[2] for r in rows] == [
+        "32:64 fused layer, compiled", "32:64 unmodified model (module calls, each its own launch), compiled"]
+
+
 def test_decode_table_sparse_only(tmp_path):
     d = {"model": "qwen3-14b", "prompt": 128, "gen": 256, "sparse": {**_variant(4.0), "ratio": "8:16"}}
     path = tmp_path / "s.json"
