@@ -184,6 +184,23 @@ int nm_num_gate_up_configs(void);
  *    slot, replacing the cache update (KVCache.update, model.py:114-123); nothing is stored
  *    when *pos is outside [0, pos_limit). The residual is added last.
  *
+ *  - Split-K carry between consecutive launches of a decoder layer (replaces
+ *    the residual add after o_proj / down_proj, model.py:186-187, moved into
+ *    the next launch): carry_out != NULL makes a producer, one plain GEMV
+ *    (grouped kind, nprob 1, no norm, residual or heads; prob[0].out unused)
+ *    that leaves its fp32 split partials [splits, h] in carry_out (splits as
+ *    nm_gemv_launch_plan reports) and reduces nothing. carry_in != NULL makes
+ *    a consumer (norm_weight required, 16-byte aligned; K = the producer's h;
+ *    m a multiple of 4) whose
+ *    input is x = round(sum over the carry_splits (<= 16) partials, in split
+ *    order, + vec): bit for bit what the producer with residual vec would
+ *    have written. The consumer writes x to vec_out ([K], not vec) and
+ *    otherwise runs as with vec = x, except that the input norm's mean(x^2)
+ *    is summed per split slice (a different fp32 summation order). Its plan
+ *    puts whole groups of nnz columns, at most 512, spanning at most 1024
+ *    positions of K, in each split; shapes that cannot are rejected with
+ *    NM_ERR_BAD_EPILOGUE.
+ *
  * For NM_KIND_GATE_UP, nprob is 2 (prob[0] gate, prob[1] up, same h); the
  * output, residual and h are prob[0]'s, and no heads fusion is allowed.
  * Workspace: nm_gemv_launch_workspace_bytes(desc) (0 if the shape is
@@ -221,12 +238,16 @@ typedef struct nm_gemv_launch_desc {
   int w, nnz, m;
   int config_id, splits;       /* as nm_gemv_ex (pair configs for the gate/up kind) */
   nm_gemv_problem prob[4];
+  float* carry_out;            /* NULL or [splits, h] fp32: producer */
+  const float* carry_in;       /* NULL or [carry_splits, K] fp32: consumer */
+  void* vec_out;               /* consumer: [K] receives its finished input */
+  int carry_splits;
 } nm_gemv_launch_desc;
 
 size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);
-/* The plan of such a launch (only the kind, counts, sizes, config_id and
- * splits of desc are read): configuration, splits, workgroups, compressed
- * rows per split and rows per chunk. */
+/* The plan of such a launch (only the kind, counts, sizes, config_id,
+ * splits and whether carry_in is set are read): configuration, splits,
+ * workgroups, compressed rows per split and rows per chunk. */
 int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int* out_splits, int* out_blocks,
                         int* out_rows_per_split, int* out_chunk_rows);
 int nm_gemv_launch(const nm_gemv_launch_desc* desc, void* workspace, size_t workspace_bytes, void* stream);

@@ -51,7 +51,8 @@ class NmGemvLaunchDesc(ctypes.Structure):
     _fields_ = [("dtype", _i), ("kind", _i), ("nprob", _i), ("vec_stride", _i), ("vec", _vp),
                 ("norm_weight", _vp), ("norm_eps", ctypes.c_float), ("head_norm_eps", ctypes.c_float),
                 ("head_dim", _i), ("pos_limit", _i), ("pos", _vp), ("rope_table", _vp), ("w", _i), ("nnz", _i),
-                ("m", _i), ("config_id", _i), ("splits", _i), ("prob", NmGemvProblem * 4)]
+                ("m", _i), ("config_id", _i), ("splits", _i), ("prob", NmGemvProblem * 4), ("carry_out", _vp),
+                ("carry_in", _vp), ("vec_out", _vp), ("carry_splits", _i)]
 
 
 _descp = ctypes.POINTER(NmGemvLaunchDesc)
@@ -83,7 +84,7 @@ ABI = {
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
 }
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _lib = None
 _lock = threading.Lock()

@@ -46,6 +46,7 @@ struct Plan {
   int blocks;
   size_t ticket_off[kMaxProblems];   // in uint32 units from the workspace start
   size_t partial_off[kMaxProblems];  // in bytes from the workspace start
+  size_t ssq_off;                    // carried input: per-workgroup ssq slots, bytes from the start
   size_t workspace;
 };
 
@@ -118,7 +119,7 @@ int auto_splits(int tiles, int w, int nmat, EffSplits eff) {
 // problem in its first NM_TICKET_BYTES and then nmat * splits * h floats of
 // partial sums per problem.
 int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg, int splits, Plan* p,
-              int max_rows = kMaxRows, int batch = 1) {
+              int max_rows = kMaxRows, int batch = 1, int row_align = 1) {
   if (nprob < 1 || nprob > kMaxProblems || (nmat == 2 && nprob != 1)) return NM_ERR_BAD_SHAPE;
   long long h_total = 0;
   for (int i = 0; i < nprob; ++i) {
@@ -132,11 +133,15 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
   const Config& c = nmat == 2 ? kDualConfigs[cfg] : kConfigs[cfg];
   const int HT = c.th * kVec;
   const int CH = (kBlock / c.th) * c.u;
+  // Rows per split: whole chunks, and whole multiples of row_align (a carried
+  // input needs whole groups of nnz columns per split).
+  int AL = CH;
+  while (AL % row_align != 0) AL += CH;
   auto rows_for = [&](int s) {
     if (s > w) s = w;
-    int r = ceil_div(ceil_div(w, s), CH) * CH;
-    if (r > max_rows) r = max_rows;
-    return r < CH ? CH : r;
+    int r = ceil_div(ceil_div(w, s), AL) * AL;
+    if (r > max_rows) r = max_rows >= AL ? (max_rows / AL) * AL : AL;
+    return r < AL ? AL : r;
   };
   if (splits <= 0) {
     int tiles = 0;
@@ -146,6 +151,7 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
   const int rows = rows_for(splits);
   splits = ceil_div(w, rows);
   p->cfg = cfg;
+  p->ssq_off = 0;
   p->splits = splits;
   p->rows_per_split = rows;
   p->nprob = nprob;
@@ -182,9 +188,22 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   int hs[kMaxProblems];
   for (int i = 0; i < nprob; ++i) hs[i] = d.prob[i].h;
   if (pair && d.prob[1].h != d.prob[0].h) return NM_ERR_BAD_SHAPE;
+  const bool carry_in = d.carry_in != nullptr;
+  const bool carry_out = d.carry_out != nullptr;
+  if (carry_in && carry_out) return NM_ERR_BAD_EPILOGUE;
+  if (d.nnz <= 0) return NM_ERR_BAD_SHAPE;
   Plan p;
-  int rc = make_plan(nprob, hs, d.w, d.nnz, d.m, nmat, d.config_id, d.splits, &p);
+  // A consumer's plan: whole groups of columns per split, at most 512 (the
+  // carried-input kernels cover gather slots 0 and 1).
+  int rc = make_plan(nprob, hs, d.w, d.nnz, d.m, nmat, d.config_id, d.splits, &p, carry_in ? 2 * kBlock : kMaxRows,
+                     1, carry_in ? d.nnz : 1);
   if (rc != NM_OK) return rc;
+  if (carry_in) {
+    // The ssq slots follow the partials: one float per workgroup.
+    p.workspace = (p.workspace + 255) & ~(size_t)255;
+    p.ssq_off = p.workspace;
+    if (p.splits > 1) p.workspace += (size_t)p.blocks * sizeof(float);
+  }
   if (workspace_needed) {
     *workspace_needed = p.workspace;
     return NM_OK;
@@ -193,12 +212,12 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   for (int i = 0; i < d.nprob; ++i)
     if (!d.prob[i].mat_data || !d.prob[i].mat_index) return NM_ERR_NULL_POINTER;
   for (int i = 0; i < nprob; ++i)
-    if (!d.prob[i].out) return NM_ERR_NULL_POINTER;
+    if (!d.prob[i].out && !carry_out) return NM_ERR_NULL_POINTER;
   if (d.vec_stride < 1) return NM_ERR_BAD_SHAPE;
   for (int i = 0; i < d.nprob; ++i)
     if (((uintptr_t)d.prob[i].mat_data & 15u) != 0) return NM_ERR_MISALIGNED;
   for (int i = 0; i < nprob; ++i)
-    if (((uintptr_t)d.prob[i].out & 15u) != 0) return NM_ERR_MISALIGNED;
+    if (!carry_out && ((uintptr_t)d.prob[i].out & 15u) != 0) return NM_ERR_MISALIGNED;
   if (((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
   if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
 
@@ -227,6 +246,26 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   }
   if (any_pos && (!d.pos || d.pos_limit <= 0)) return NM_ERR_BAD_EPILOGUE;
   if (any_rope && !d.rope_table) return NM_ERR_BAD_EPILOGUE;
+  if (carry_out) {
+    // One plain GEMV: its epilogue moves into the consumer.
+    const nm_gemv_problem& q = d.prob[0];
+    if (pair || d.nprob != 1 || d.norm_weight || q.residual || q.head_norm || q.rope || q.head_stride ||
+        q.elem_stride || q.pos_stride)
+      return NM_ERR_BAD_EPILOGUE;
+    if (((uintptr_t)d.carry_out & 15u) != 0) return NM_ERR_MISALIGNED;
+  }
+  if (carry_in) {
+    if (!d.norm_weight || !d.vec_out) return NM_ERR_BAD_EPILOGUE;
+    if (d.carry_splits < 1 || d.carry_splits > kMaxCarry || d.m % 4 != 0) return NM_ERR_BAD_EPILOGUE;
+    if (p.rows_per_split % d.nnz != 0 || gather_slot(p.rows_per_split) > 1) return NM_ERR_BAD_EPILOGUE;
+    const long long slice = (long long)(p.rows_per_split / d.nnz) * d.m;  // K positions a split reads
+    if (slice > 4 * kBlock) return NM_ERR_BAD_EPILOGUE;
+    if (((uintptr_t)d.carry_in & 15u) != 0 || ((uintptr_t)d.vec_out & 15u) != 0 ||
+        ((uintptr_t)d.norm_weight & 15u) != 0)
+      return NM_ERR_MISALIGNED;
+    const uintptr_t vo = (uintptr_t)d.vec_out, vi = (uintptr_t)d.vec;
+    if (vo < vi + (size_t)K * esize && vi < vo + (size_t)K * esize) return NM_ERR_BAD_EPILOGUE;  // overlap
+  }
   if (validate_only) return NM_OK;
 
   Args a;
@@ -268,7 +307,14 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
     P.partial = reinterpret_cast<float*>(ws + p.partial_off[src] +
                                          (size_t)i * (pair ? (size_t)p.splits * (size_t)hs[0] * 4 : 0));
   }
-  const KernelFn fn = kernel_table(d.dtype, pair)[p.cfg].fn[gather_slot(p.rows_per_split)][d.norm_weight ? 1 : 0];
+  a.carry_out = d.carry_out;
+  a.carry_in = d.carry_in;
+  a.vec_out = d.vec_out;
+  a.carry_splits = d.carry_splits;
+  a.ssq_slots = carry_in ? reinterpret_cast<float*>(ws + p.ssq_off) : nullptr;
+  const int variant = carry_in ? (d.carry_splits <= 8 ? 2 : 3) : (d.norm_weight ? 1 : 0);
+  const KernelFn fn = kernel_table(d.dtype, pair)[p.cfg].fn[gather_slot(p.rows_per_split)][variant];
+  if (!fn) return NM_ERR_BAD_EPILOGUE;
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, static_cast<hipStream_t>(stream), a);
   hipError_t e = hipGetLastError();
   return e == hipSuccess ? NM_OK : (int)e;
@@ -536,7 +582,10 @@ int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int
   int hs[kMaxProblems];
   for (int i = 0; i < nprob; ++i) hs[i] = desc->prob[i].h;
   Plan p;
-  const int rc = make_plan(nprob, hs, desc->w, desc->nnz, desc->m, pair ? 2 : 1, desc->config_id, desc->splits, &p);
+  const bool carry_in = desc->carry_in != nullptr;
+  if (desc->nnz <= 0) return NM_ERR_BAD_SHAPE;
+  const int rc = make_plan(nprob, hs, desc->w, desc->nnz, desc->m, pair ? 2 : 1, desc->config_id, desc->splits, &p,
+                           carry_in ? 2 * kBlock : kMaxRows, 1, carry_in ? desc->nnz : 1);
   if (rc != NM_OK) return rc;
   const Config& c = pair ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
   if (out_config_id) *out_config_id = p.cfg;

@@ -10,10 +10,14 @@
 
 namespace nm_hip {
 
-#define NM_ROW_N(TH, U, G, NT, NM) \
-  {&nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, false>, &nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, true>}
+#define NM_KERNEL_V(TH, U, G, NT, NM, NORM, CARRY) &nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, NORM, CARRY>
+#define NM_ROW_N(TH, U, G, NT, NM)                                                                         \
+  {NM_KERNEL_V(TH, U, G, NT, NM, false, 0), NM_KERNEL_V(TH, U, G, NT, NM, true, 0),                       \
+   NM_KERNEL_V(TH, U, G, NT, NM, true, 8), NM_KERNEL_V(TH, U, G, NT, NM, true, 16)}
+#define NM_ROW_W(TH, U, G, NT, NM) \
+  {NM_KERNEL_V(TH, U, G, NT, NM, false, 0), NM_KERNEL_V(TH, U, G, NT, NM, true, 0), nullptr, nullptr}
 #define NM_ROW(NM, TH, U, NT) \
-  {{NM_ROW_N(TH, U, 1, NT, NM), NM_ROW_N(TH, U, 2, NT, NM), NM_ROW_N(TH, U, 4, NT, NM), NM_ROW_N(TH, U, 8, NT, NM)}},
+  {{NM_ROW_N(TH, U, 1, NT, NM), NM_ROW_N(TH, U, 2, NT, NM), NM_ROW_W(TH, U, 4, NT, NM), NM_ROW_W(TH, U, 8, NT, NM)}},
 #define NM_PLAIN_ROW(TH, U, NT) NM_ROW(1, TH, U, NT)
 #define NM_PAIR_ROW(TH, U, NT) NM_ROW(2, TH, U, NT)
 

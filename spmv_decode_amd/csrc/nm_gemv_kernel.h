@@ -44,7 +44,7 @@ constexpr int kBlock = 256;        // lanes per workgroup
 constexpr int kVec = 8;            // output rows per lane
 constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
 constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
-constexpr int kAbiVersion = 6;
+constexpr int kAbiVersion = 7;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -169,7 +169,20 @@ struct Args {
   int rows_per_split;  // multiple of the chunk height, <= kMaxRows
   int nprob;           // NMAT == 1: problems in the grid; NMAT == 2: 2 (gate, up)
   Problem prob[kMaxProblems];
+  // Split-K carry between two launches of a decoder chain (null when unused).
+  // A producer (one plain GEMV) leaves its fp32 split partials [splits, h] in
+  // carry_out and writes nothing else. A consumer (CARRY) takes as its input
+  // vector round_T(sum_s carry_in[s, :] + vec), the producer's epilogue with
+  // vec as the residual, writes that vector to vec_out and runs as usual.
+  float* carry_out;
+  const float* carry_in;     // [carry_splits, K]
+  void* vec_out;             // [K]
+  float* ssq_slots;          // [grid] per-workgroup sums of squares of its input slice
+  int carry_splits;
 };
+
+// Most producer splits a consumer reads (their partials are requested at once).
+constexpr int kMaxCarry = 16;
 
 __device__ inline float silu(float g) { return g / (1.0f + expf(-g)); }
 
@@ -222,7 +235,12 @@ __device__ inline float word_ssq(const u32x4 raw, bool ok, float acc) {
 // NMAT == 2: each workgroup streams the same tile/split of prob[0] (gate) and
 // prob[1] (up), both of width prob[0].h, and the output prob[0].out receives
 // silu(gate) * up, computed in fp32 and rounded once.
-template <int DT, int TH, int U, int G, bool NT, int NMAT, bool NORM>
+// CARRY > 0 (with NORM, at most 512 compressed columns per split, whole
+// groups per split, at most CARRY producer splits): the input vector is
+// finished from the previous launch's split partials (Args::carry_in). Each workgroup builds only the slice of K its
+// columns read, [k0, k0 + kn), in LDS, and its sum of squares; the tile's
+// last arrival adds the slices' sums in split order for the input norm.
+template <int DT, int TH, int U, int G, bool NT, int NMAT, bool NORM, int CARRY>
 __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   using E = Elem<DT>;
   typedef typename E::scalar T;
@@ -235,11 +253,18 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   static_assert(U % 4 == 0, "U must be a multiple of 4 (ds_read_b128)");
   static_assert(XR % CH == 0, "chunk must divide the split");
   static_assert(NMAT == 1 || NMAT == 2, "one matrix, or the gate/up pair");
+  static_assert(!CARRY || (NORM && G <= 2 && CARRY <= kMaxCarry),
+                "a carried input comes with the input norm, <= 512 columns per split");
 
   constexpr int kWaves = kBlock / 64;
   constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
+  // Carried input: a slice of at most kCarryLen positions of K, four adjacent
+  // ones per lane (a split of 512 columns at half density).
+  constexpr int kCarryLen = 4 * kBlock;
+  typedef T t4 __attribute__((ext_vector_type(4)));
   __shared__ __attribute__((aligned(16))) float xs[NMAT][XR];
   __shared__ __attribute__((aligned(16))) float red[NMAT][TK * HT];
+  __shared__ __attribute__((aligned(16))) float hs[CARRY ? kCarryLen : 4];  // slice of x * g
   __shared__ float wsum[kOutPerLane * kWaves];  // per-wave sums of the head norms
   __shared__ float nsum[kWaves];                // per-wave sums of the input norm
   __shared__ int is_last;
@@ -296,6 +321,28 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
 #pragma unroll
     for (int j = 0; j < G; ++j) gidx[q][j] = (int)mi[q][c0 + min(tid + j * kBlock, cw - 1)];
 
+  // 1b. Carried input: the split's columns are whole groups (c0 and cw are
+  //     multiples of nnz; the host checks), so they read the slice
+  //     [k0, k0 + kn) of K, and the splits' slices partition K. Every producer
+  //     split's partial (at most CARRY, addresses clamped to the last), the
+  //     residual and the norm weight at four adjacent positions per lane
+  //     (16-byte loads of the partials), requested before the first weight
+  //     chunk so that they do not wait behind it (vmcnt is in order).
+  const int k0 = CARRY ? (c0 / a.nnz) * a.m : 0;
+  const int kn = CARRY ? (cw / a.nnz) * a.m : 4;  // a multiple of 4 (m is; host check), <= kCarryLen
+  float4 cpart[CARRY ? CARRY : 1];
+  t4 cres, cgw;
+  if constexpr (CARRY > 0) {
+    const int kc = k0 + min(4 * tid, kn - 4);
+#pragma unroll
+    for (int s = 0; s < CARRY; ++s) {
+      const int ss = min(s, a.carry_splits - 1);
+      cpart[s] = *reinterpret_cast<const float4*>(a.carry_in + (size_t)ss * (size_t)a.K + (size_t)kc);
+    }
+    cres = *reinterpret_cast<const t4*>(static_cast<const T*>(a.vec) + kc);
+    cgw = *reinterpret_cast<const t4*>(static_cast<const T*>(a.norm_w) + kc);
+  }
+
   // 2. The first chunk of weights goes in flight before the activation loads.
   auto load_chunk = [&](u32x4 (&dst)[NMAT][U][W], int k) {
 #pragma unroll
@@ -341,19 +388,60 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
       const int c = c0 + min(t, cw - 1);
       const int pos = (c / a.nnz) * a.m + gidx[q][j];
       gok[q][j] = (t < cw) && (pos < a.K);
-      graw[q][j] = vx[(long long)(gok[q][j] ? pos : 0) * a.vec_stride];
-      if constexpr (NORM) wraw[q][j] = gx[gok[q][j] ? pos : 0];
+      if constexpr (CARRY) {
+        graw[q][j] = 0;
+        wraw[q][j] = 0;
+      } else {
+        graw[q][j] = vx[(long long)(gok[q][j] ? pos : 0) * a.vec_stride];
+        if constexpr (NORM) wraw[q][j] = gx[gok[q][j] ? pos : 0];
+      }
     }
   // The words of vec for mean(x^2) (contiguous, 16-byte aligned, K * size a
   // multiple of 16 with a norm; the host checks) are requested now and
   // summed after the main loop, so they never delay the weight stream.
-  constexpr int kSsqWords = NORM ? 3 : 1;  // per lane: K * sizeof(T) <= 12 KiB in flight
+  constexpr int kSsqWords = (NORM && !CARRY) ? 3 : 1;  // per lane: K * sizeof(T) <= 12 KiB in flight
   const u32x4* __restrict__ xw = static_cast<const u32x4*>(a.vec);
   const int nw = (int)(((long long)a.K * (long long)sizeof(T)) / 16);
   u32x4 sraw[kSsqWords];
-  if constexpr (NORM) {
+  if constexpr (NORM && !CARRY) {
 #pragma unroll
     for (int i = 0; i < kSsqWords; ++i) sraw[i] = xw[min(i * kBlock + tid, nw - 1)];
+  }
+  // Carried input: finish the slice, x = round_T(sum of the producer's
+  // partials in split order + residual) -- the producer's own epilogue, so x
+  // is bit-identical to what it would have written --, keep x * g in LDS and
+  // sum x^2 over the slice. The first tile's workgroups of each split write
+  // their slice of x to vec_out.
+  float ssq_carry = 0.0f;
+  if constexpr (CARRY) {
+    float sum[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+    for (int s = 0; s < (CARRY ? CARRY : 1); ++s) {
+      if (s < a.carry_splits) {
+        sum[0] += cpart[s].x;
+        sum[1] += cpart[s].y;
+        sum[2] += cpart[s].z;
+        sum[3] += cpart[s].w;
+      }
+    }
+    const int kl = 4 * tid;
+    if (kl < kn) {
+      t4 hv;
+      float4 xg;
+      float f[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        hv[e] = E::from_f32(sum[e] + E::to_f32(cres[e]));
+        f[e] = E::to_f32(hv[e]);
+        ssq_carry = __builtin_fmaf(f[e], f[e], ssq_carry);
+      }
+      xg.x = f[0] * E::to_f32(cgw[0]);
+      xg.y = f[1] * E::to_f32(cgw[1]);
+      xg.z = f[2] * E::to_f32(cgw[2]);
+      xg.w = f[3] * E::to_f32(cgw[3]);
+      *reinterpret_cast<float4*>(&hs[kl]) = xg;
+      if (p == 0 && tile == 0) *reinterpret_cast<t4*>(static_cast<T*>(a.vec_out) + k0 + kl) = hv;
+    }
   }
   // Single-matrix launches request chunk 1 here, behind the gather: the
   // barrier below then waits for chunk 0 and the gather only, and chunk 1
@@ -363,15 +451,23 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   constexpr bool kEarlyChunk1 = NMAT == 1;
   if constexpr (kEarlyChunk1) load_chunk(bufB, 1);
   __builtin_amdgcn_sched_barrier(0);  // every gather request before the first use of one
+  if constexpr (CARRY) __syncthreads();  // the slice is in LDS
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
 #pragma unroll
     for (int j = 0; j < G; ++j) {
-      const float xv = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
-      if constexpr (NORM) {
-        xs[q][tid + j * kBlock] = xv * E::to_f32(wraw[q][j]);
+      if constexpr (CARRY) {
+        const int t = tid + j * kBlock;
+        const int cl = min(t, cw - 1);  // column within the split
+        const int li = (cl / a.nnz) * a.m + gidx[q][j];  // < kn for positions below m
+        xs[q][t] = (gok[q][j] && li < kn) ? hs[li] : 0.0f;
       } else {
-        xs[q][tid + j * kBlock] = xv;
+        const float xv = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
+        if constexpr (NORM) {
+          xs[q][tid + j * kBlock] = xv * E::to_f32(wraw[q][j]);
+        } else {
+          xs[q][tid + j * kBlock] = xv;
+        }
       }
     }
   __syncthreads();
@@ -465,20 +561,26 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
   }
   if constexpr (NORM) {
     float ssq = 0.0f;
+    if constexpr (CARRY) {
+      ssq = ssq_carry;
+    } else {
 #pragma unroll
-    for (int i = 0; i < kSsqWords; ++i) ssq = word_ssq<DT>(sraw[i], i * kBlock + tid < nw, ssq);
-    for (int base = kSsqWords * kBlock; base < nw; base += kBlock)  // K * sizeof(T) > 12 KiB only
-      ssq = word_ssq<DT>(xw[min(base + tid, nw - 1)], base + tid < nw, ssq);
+      for (int i = 0; i < kSsqWords; ++i) ssq = word_ssq<DT>(sraw[i], i * kBlock + tid < nw, ssq);
+      for (int base = kSsqWords * kBlock; base < nw; base += kBlock)  // K * sizeof(T) > 12 KiB only
+        ssq = word_ssq<DT>(xw[min(base + tid, nw - 1)], base + tid < nw, ssq);
+    }
     ssq = wave_sum(ssq);
     if ((tid & 63) == 0) nsum[tid >> 6] = ssq;
   }
   __syncthreads();
   float s_in = 1.0f;
+  float slice_ssq = 0.0f;  // CARRY: this split's share of sum(x^2)
   if constexpr (NORM) {
     float t = 0.0f;
 #pragma unroll
     for (int i = 0; i < kWaves; ++i) t += nsum[i];
-    s_in = rsqrtf(t / (float)a.K + a.norm_eps);
+    slice_ssq = t;
+    if (!CARRY || a.splits == 1) s_in = rsqrtf(t / (float)a.K + a.norm_eps);
   }
 
   float tsum[NMAT][kOutPerLane];
@@ -494,6 +596,21 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
       }
       tsum[q][j] = s;
     }
+
+  // A producer leaves its partial tile for the next launch (which reads it
+  // after this grid has completed) and is done: no handoff, no epilogue.
+  if constexpr (NMAT == 1 && !CARRY) {
+    if (a.carry_out != nullptr) {
+      float* part = a.carry_out + (size_t)split * (size_t)h;
+#pragma unroll
+      for (int j = 0; j < kOutPerLane; ++j) {
+        const int o = tid + j * kBlock;
+        const int r = tile * HT + o;
+        if (o < HT && r < h) part[r] = tsum[0][j];
+      }
+      return;
+    }
+  }
 
   uint32_t* tickets = P.tickets;
   if (a.splits > 1) {
@@ -522,6 +639,10 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
         if (o < HT && r < h)
           (void)__hip_atomic_exchange(part + r, tsum[q][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       }
+    }
+    if constexpr (CARRY) {
+      if (tid == 0)
+        (void)__hip_atomic_exchange(a.ssq_slots + blockIdx.x, slice_ssq, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
     __syncthreads();
@@ -573,9 +694,15 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
         pp[q][j] = a.prob[NMAT == 1 ? p : q].partial + r;
         sacc[q][j] = 0.0f;
       }
+    // CARRY: the splits' slice sums of squares (slot of the workgroup of
+    // split s = its grid index) are read in the same round trip, summed in
+    // split order.
+    const float* slot = CARRY ? a.ssq_slots + P.block_begin + tile : nullptr;
+    float ssq_all = 0.0f;
     int sp = 0;
     for (; sp + 8 <= a.splits; sp += 8) {
       float t8[NMAT][kOutPerLane][8];
+      float n8[8];
 #pragma unroll
       for (int q = 0; q < NMAT; ++q)
 #pragma unroll
@@ -584,25 +711,40 @@ __global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
           for (int i = 0; i < 8; ++i)
             t8[q][j][i] = __hip_atomic_load(pp[q][j] + (size_t)(sp + i) * (size_t)h, __ATOMIC_RELAXED,
                                             __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (CARRY) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i)
+          n8[i] = __hip_atomic_load(slot + (size_t)(sp + i) * (size_t)tiles, __ATOMIC_RELAXED,
+                                    __HIP_MEMORY_SCOPE_AGENT);
+      }
 #pragma unroll
       for (int q = 0; q < NMAT; ++q)
 #pragma unroll
         for (int j = 0; j < kOutPerLane; ++j)
 #pragma unroll
           for (int i = 0; i < 8; ++i) sacc[q][j] += t8[q][j][i];
+      if constexpr (CARRY) {
+#pragma unroll
+        for (int i = 0; i < 8; ++i) ssq_all += n8[i];
+      }
     }
     for (; sp < a.splits; ++sp) {
       float t1[NMAT][kOutPerLane];
+      float n1 = 0.0f;
 #pragma unroll
       for (int q = 0; q < NMAT; ++q)
 #pragma unroll
         for (int j = 0; j < kOutPerLane; ++j)
           t1[q][j] = __hip_atomic_load(pp[q][j] + (size_t)sp * (size_t)h, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if constexpr (CARRY)
+        n1 = __hip_atomic_load(slot + (size_t)sp * (size_t)tiles, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int q = 0; q < NMAT; ++q)
 #pragma unroll
         for (int j = 0; j < kOutPerLane; ++j) sacc[q][j] += t1[q][j];
+      if constexpr (CARRY) ssq_all += n1;
     }
+    if constexpr (CARRY) s_in = rsqrtf(ssq_all / (float)a.K + a.norm_eps);
 #pragma unroll
     for (int q = 0; q < NMAT; ++q)
 #pragma unroll
@@ -982,9 +1124,11 @@ constexpr int kNumDualConfigs = 0 NM_PAIR_CONFIGS(NM_COUNT_CONFIG);
 typedef void (*KernelFn)(Args);
 
 // The kernels of one configuration and element type:
-// fn[gather slot: 256, 512, 1024, 2048 columns per split][input norm].
+// fn[gather slot: 256, 512, 1024, 2048 columns per split][variant: plain,
+// input norm, input norm with a carried input of <= 8 or <= 16 producer
+// splits (slots 0-1 only, else null)].
 struct KernelRow {
-  KernelFn fn[4][2];
+  KernelFn fn[4][4];
 };
 
 // SpMM configurations: the plain ids 0-3 (th16/th32 x u4/u8, non-temporal).

@@ -339,6 +339,82 @@ def fused_block_step(blk: Block, x2d, k_cache_t, v_cache_t, pos, q_pad, zero, ro
     return x2d
 
 
+def carry_supported(layers) -> bool:
+    """True when the fused layers can hand o_proj's and down_proj's split-K
+    reduction to the next launch (fused_layers_carried): every layer has the
+    first one's shapes, both producers leave at most 16 splits, and both
+    consumers' plans (whole groups of columns per split, at most 512 columns
+    and 1024 positions of K per split, M a multiple of 4) take a carried
+    input. Mirrors the library's checks, so that the choice is made once,
+    before any launch, rather than by a launch failing."""
+    from ..hip_spmv import carry_splits, launch_plan
+
+    if not layers or not all(fusable(b) for b in layers):
+        return False
+
+    def shapes(b):
+        at, mlp = b.self_attn, b.mlp
+        return tuple(tuple(m.mat_data.shape) + (m.block_width, m.vec_width) for m in
+                     (at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj))
+
+    first = shapes(layers[0])
+    if any(shapes(b) != first for b in layers[1:]):
+        return False
+    at, mlp = layers[0].self_attn, layers[0].mlp
+    nnz, m = at.q_proj.block_width, at.q_proj.vec_width
+    if m % 4 or any(x.block_width != nnz or x.vec_width != m for x in (at.o_proj, mlp.gate_proj, mlp.down_proj)):
+        return False
+    for prod in (at.o_proj, mlp.down_proj):
+        if carry_splits(prod.mat_data, prod.mat_index, nnz, m) > 16:
+            return False
+    for mats, pair in (((at.q_proj, at.k_proj, at.v_proj), False), ((mlp.gate_proj, mlp.up_proj), True)):
+        plan = launch_plan([(x.mat_data, x.mat_index) for x in mats], nnz, m, gate_up=pair, carried=True)
+        rows = plan["rows_per_split"]
+        if rows % nnz or rows > 512 or (rows // nnz) * m > 1024:
+            return False
+    return True
+
+
+def fused_layers_carried(layers, x2d, h2d, carry_o, carry_d, k_caches, v_caches, pos, q_pad, zero, rope):
+    """The fused sparse layers with the split-K reduction of o_proj and
+    down_proj carried into the next launch: o_proj and down_proj leave their
+    fp32 split partials (carry_o / carry_d) and end without a handoff; the
+    gate/up launch finishes h = x + o_proj(y) (the same rounding as o +
+    residual) from them, writes h to h2d and runs on it; the next layer's
+    q/k/v launch finishes x = h + down_proj(act) into x2d likewise. The first
+    layer's q/k/v reads x2d (the embeddings) and the last layer's down_proj
+    adds its residual itself. x2d and h2d are [1, dim]; the final residual
+    stream is returned (h2d). Four launches per layer, as fused_block_step."""
+    ops = torch.ops.nmsparse
+    n = len(layers)
+    for i, blk in enumerate(layers):
+        at, mlp = blk.self_attn, blk.mlp
+        c = at.cfg
+        ln1, ln2 = blk.input_layernorm, blk.post_attention_layernorm
+        qp, kp, vp = at.q_proj, at.k_proj, at.v_proj
+        qn = at.q_norm.weight if c.qk_norm else None
+        kn = at.k_norm.weight if c.qk_norm else None
+        qkv = (qp.mat_data, qp.mat_index, kp.mat_data, kp.mat_index, vp.mat_data, vp.mat_index, qp.block_width,
+               qp.vec_width, q_pad, k_caches[i], v_caches[i], pos, rope, c.head_dim, ln1.weight, ln1.eps, qn, kn,
+               c.norm_eps)
+        if i == 0:
+            ops.qkv_decode(x2d, *qkv)
+        else:
+            ops.qkv_decode_carried(h2d, carry_d, x2d, *qkv)
+        y = attend(q_pad, k_caches[i], v_caches[i], c, zero).view(1, c.n_heads * c.head_dim)
+        o = at.o_proj
+        ops.gemv_partials_(y, o.mat_data, o.mat_index, o.block_width, o.vec_width, carry_o)
+        gp, up = mlp.gate_proj, mlp.up_proj
+        act = ops.gate_up_silu_carried(x2d, carry_o, h2d, gp.mat_data, gp.mat_index, up.mat_data, up.mat_index,
+                                       gp.block_width, gp.vec_width, ln2.weight, ln2.eps)
+        d = mlp.down_proj
+        if i + 1 < n:
+            ops.gemv_partials_(act, d.mat_data, d.mat_index, d.block_width, d.vec_width, carry_d)
+        else:
+            ops.gemv_add_(act, d.mat_data, d.mat_index, d.block_width, d.vec_width, h2d)
+    return h2d
+
+
 class Decoder(nn.Module):
     """Decoder stack with a static KV cache; `model.layers` is what
     `swap_to_nmsparse` walks."""
@@ -347,6 +423,10 @@ class Decoder(nn.Module):
         super().__init__()
         self.cfg = cfg
         self.fuse_epilogues = True
+        # Fused sparse layers: carry o_proj's / down_proj's split-K reduction
+        # into the next launch where the shapes allow (fused_layers_carried).
+        self.carry_splitk = True
+        self._carry = None  # (key, x2d-independent buffers) set up by _carry_buffers
         self.embed_tokens = nn.Embedding(cfg.vocab, cfg.dim)
         self.layers = nn.ModuleList(Block(cfg) for _ in range(cfg.n_layers))
         self.norm = RMSNorm(cfg.dim, cfg.norm_eps)
@@ -467,6 +547,41 @@ class Decoder(nn.Module):
         self.rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(device)
         self.rope_real = torch.view_as_real(self.rope)  # the same table as fp32 (cos, sin) pairs
         self.positions = torch.arange(max_seq, device=device)
+        self._carry = None
+        self.prepare_decode()
+
+    def prepare_decode(self) -> None:
+        """Set up what the fused sparse step needs beyond the caches: the
+        buffers of fused_layers_carried (the h stream and the fp32 partials of
+        o_proj and down_proj), when the layers support the carry. Run by every
+        eager step (cheap once done; redone when the layers' shapes change) and
+        by the runners before capturing or compiling a step: a step traced by
+        torch.compile uses what was prepared before it, and the plain fused
+        layers when nothing was."""
+        if not self.layers or not hasattr(self, "q_pad"):
+            return
+        at, mlp = self.layers[0].self_attn, self.layers[0].mlp
+        o, d = at.o_proj, mlp.down_proj
+        dev, dt = self.q_pad.device, self.q_pad.dtype
+        def shape(mod):
+            md = getattr(mod, "mat_data", None)
+            return (type(mod).__name__, tuple(md.shape) if isinstance(md, torch.Tensor) else None)
+
+        key = (dev, dt, len(self.layers),
+               tuple(shape(mod) for b in self.layers for mod in (b.self_attn.o_proj, b.mlp.down_proj, b.mlp.gate_proj)))
+        if self._carry is not None and self._carry[0] == key:
+            return
+        if dev.type != "cuda" or not carry_supported(self.layers):
+            self._carry = (key, None)
+            return
+        from ..hip_spmv import carry_splits
+
+        so = carry_splits(o.mat_data, o.mat_index, o.block_width, o.vec_width)
+        sd = carry_splits(d.mat_data, d.mat_index, d.block_width, d.vec_width)
+        dim = self.cfg.dim
+        self._carry = (key, (torch.empty(1, dim, device=dev, dtype=dt),
+                             torch.empty(so, dim, device=dev, dtype=torch.float32),
+                             torch.empty(sd, dim, device=dev, dtype=torch.float32)))
 
     def reset_cache(self):
         """Zero every cached key and value (the mask rows are rewritten by each step)."""
@@ -486,6 +601,13 @@ class Decoder(nn.Module):
             torch.where(keep, self.zero, self.neg_inf, out=self.k_mask)
         if self.fuse_epilogues and all(fusable(b) and b.self_attn.group_launches for b in self.layers):
             x2d = x.view(1, -1)
+            if not torch.compiler.is_compiling():
+                self.prepare_decode()
+            bufs = self._carry[1] if (self.carry_splitk and self._carry is not None) else None
+            if bufs is not None:
+                h2d = fused_layers_carried(self.layers, x2d, *bufs, self.k_cache_t, self.v_cache_t, pos, self.q_pad,
+                                           self.zero, self.rope_real)
+                return project(self.lm_head, self.norm(h2d.view(1, 1, -1))).view(1, -1)
             for i, blk in enumerate(self.layers):
                 fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero,
                                  self.rope_real)

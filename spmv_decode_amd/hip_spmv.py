@@ -321,11 +321,14 @@ class GemvProblem:
         self.residual, self.head_norm, self.rope, self.layout = residual, head_norm, bool(rope), layout
 
 
-def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1, splits=0) -> dict:
+def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1, splits=0, carried=False) -> dict:
     """The library's plan for a launch over `problems` ((mat_data, mat_index)
     pairs): configuration, splits, grid, compressed rows per split and rows
-    per chunk (the rows a workgroup streams first)."""
+    per chunk (the rows a workgroup streams first). `carried`: the plan of a
+    launch with a carried input (nmsparse_gemv_launch's carry_in)."""
     desc = _lib.NmGemvLaunchDesc()
+    if carried:
+        desc.carry_in = 16  # only its presence is read by the planner
     desc.dtype, desc.kind = _lib.NM_DTYPE_F16, _lib.NM_KIND_GATE_UP if gate_up else _lib.NM_KIND_GROUPED
     desc.nprob = len(problems)
     w = problems[0][0].shape[0]
@@ -340,7 +343,8 @@ def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1
 
 
 def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, norm=None, head_dim=0,
-                         head_eps=1e-6, pos=None, pos_limit=None, rope_table=None, config_id=-1, splits=0):
+                         head_eps=1e-6, pos=None, pos_limit=None, rope_table=None, config_id=-1, splits=0,
+                         carry_out=None, carry_in=None, vec_out=None):
     """One launch of 1-4 GEMVs that share `vec` [1, K] (or the gate/up pair),
     with the fusions of include/nmsparse_hip.h's nm_gemv_launch.
 
@@ -351,6 +355,13 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
     complex64 [S, head_dim/2]) when used; positions outside [0, pos_limit)
     store nothing (pos_limit defaults to the rope table's length). Returns the
     list of outputs (the pair: one). Outputs left as None are allocated ([1, h]).
+
+    Split-K carry (a decoder chain's residual add moved into the next
+    launch): `carry_out` (fp32 [splits, h], splits from `launch_plan`) makes
+    this one plain GEMV leave its unreduced split partials there (nothing is
+    returned); `carry_in` (fp32 [S, K]: a producer's partials) with `vec_out`
+    ([K] of vec.dtype, not vec) makes the launch's input round(sum of the
+    partials + vec), written to vec_out; it needs `norm`.
     """
     n = len(problems)
     if gate_up and n != 2:
@@ -364,7 +375,7 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
     if gate_up and problems[0].mat_data.shape != problems[1].mat_data.shape:
         raise ValueError(f"gate {tuple(problems[0].mat_data.shape)} and up {tuple(problems[1].mat_data.shape)} "
                          "must have the same shape")
-    n_out = 1 if gate_up else n
+    n_out = 0 if carry_out is not None else (1 if gate_up else n)
     desc = _lib.NmGemvLaunchDesc()
     desc.dtype = _DTYPE_CODE[vec.dtype]
     desc.kind = _lib.NM_KIND_GATE_UP if gate_up else _lib.NM_KIND_GROUPED
@@ -440,6 +451,28 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
             P.head_norm = pr.head_norm.data_ptr()
         P.rope = int(pr.rope)
     desc.pos_limit = pos_limit
+    if carry_out is not None:
+        if (carry_out.dtype != torch.float32 or not carry_out.is_contiguous() or carry_out.device != vec.device
+                or carry_out.data_ptr() % 16):
+            raise ValueError("carry_out must be a contiguous, 16-byte aligned fp32 tensor on vec.device")
+        plan = launch_plan([(pr.mat_data, pr.mat_index) for pr in problems], BLOCK_WIDTH, VEC_WIDTH,
+                           gate_up=gate_up, config_id=config_id, splits=splits)
+        if carry_out.numel() != plan["splits"] * int(problems[0].mat_data.shape[1]):
+            raise ValueError(f"carry_out holds {carry_out.numel()} floats, the producer leaves "
+                             f"{plan['splits']} x {int(problems[0].mat_data.shape[1])}")
+        desc.carry_out = carry_out.data_ptr()
+    if carry_in is not None:
+        if carry_in.dtype != torch.float32 or carry_in.dim() != 2 or carry_in.shape[1] != K \
+                or not carry_in.is_contiguous() or carry_in.device != vec.device or carry_in.data_ptr() % 16:
+            raise ValueError(f"carry_in must be a contiguous, 16-byte aligned fp32 [splits, {K}] tensor on vec.device")
+        if vec_out is None:
+            raise ValueError("a carried input needs vec_out")
+        _check_vector(vec_out, K, vec, "vec_out")
+        if vec_out.data_ptr() % 16:
+            raise ValueError("vec_out must be 16-byte aligned")
+        desc.carry_in, desc.carry_splits, desc.vec_out = carry_in.data_ptr(), carry_in.shape[0], vec_out.data_ptr()
+    elif vec_out is not None:
+        raise ValueError("vec_out is the output of a carried input (carry_in)")
     lib = _lib.load()
     need = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(desc))
     if need == 0:
@@ -473,20 +506,38 @@ def nmsparse_gemv_grouped(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, n
 
 
 def nmsparse_gate_up_silu(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, *, out=None, norm=None, residual=None,
-                          config_id=-1, splits=0):
+                          config_id=-1, splits=0, carry_in=None, vec_out=None):
     """silu(W_gate @ vec) * (W_up @ vec) for two N:M-sparse [w, h] weights in one
     launch; `gate` and `up` are (mat_data, mat_index) pairs. fp32 throughout,
     one rounding to vec.dtype. Returns [1, h]. `norm` = (weight [K], eps)
-    applies an RMSNorm to vec first; `residual` ([h]) is added last."""
+    applies an RMSNorm to vec first; `residual` ([h]) is added last.
+    `carry_in` / `vec_out`: the input is round(sum of a producer's partials +
+    vec), written to vec_out (nmsparse_gemv_launch)."""
     (gd, gi), (ud, ui) = gate, up
     probs = [GemvProblem(gd, gi, out, residual=residual), GemvProblem(ud, ui)]
     return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, gate_up=True, norm=norm, config_id=config_id,
-                                splits=splits)[0]
+                                splits=splits, carry_in=carry_in, vec_out=vec_out)[0]
+
+
+def carry_splits(mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH) -> int:
+    """Split count of the plain GEMV `mat_data` as a producer: the rows of
+    the fp32 [splits, h] partials buffer nmsparse_gemv_partials fills."""
+    return launch_plan([(mat_data, mat_index)], BLOCK_WIDTH, VEC_WIDTH)["splits"]
+
+
+def nmsparse_gemv_partials(vec, mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH, carry):
+    """The GEMV W @ vec left unreduced: its fp32 split partials go to `carry`
+    [splits, h] (splits = carry_splits(...)), for a following launch that takes
+    round(sum of them + residual) as its input (carry_in=carry). The split-K
+    reduction and the residual add of a decoder layer's o_proj / down_proj
+    move into that launch, so this one ends without a split-K handoff."""
+    nmsparse_gemv_launch(vec, [GemvProblem(mat_data, mat_index)], BLOCK_WIDTH, VEC_WIDTH, carry_out=carry)
+    return carry
 
 
 def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_t, v_cache=None, v_cache_t=None,
                         pos, rope_table, head_dim, norm=None, q_norm=None, k_norm=None, head_eps=1e-6, config_id=-1,
-                        splits=0):
+                        splits=0, carry_in=None, vec_out=None):
     """The q/k/v projections of one decode step in one launch.
 
     q, k, v are (mat_data, mat_index) pairs sharing `vec` [1, K]. Writes the
@@ -498,7 +549,8 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
     `v_cache_t` [kv_heads, head_dim, S] at column pos (exactly one of the two;
     the decoder keeps both caches transposed). `norm` = (weight [K], eps) is
     the layer's input RMSNorm; `q_norm` / `k_norm` ([head_dim]) are Qwen3's
-    per-head norms.
+    per-head norms. `carry_in` / `vec_out`: the input is round(sum of a
+    producer's partials + vec), written to vec_out (nmsparse_gemv_launch).
     """
     kvh, kd, S = k_cache_t.shape
     hd = head_dim
@@ -529,9 +581,9 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
              GemvProblem(v[0], v[1], vc, layout=v_layout)]
     return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, norm=norm, head_dim=head_dim,
                                 head_eps=head_eps, pos=pos, rope_table=rt[:S], config_id=config_id,
-                                splits=splits)
+                                splits=splits, carry_in=carry_in, vec_out=vec_out)
 
 
 __all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
            "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "nmsparse_spmm_forward_hip",
-           "GemvProblem", "launch_plan", "validate_args", "workspace_for"]
+           "nmsparse_gemv_partials", "carry_splits", "GemvProblem", "launch_plan", "validate_args", "workspace_for"]

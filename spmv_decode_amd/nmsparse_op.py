@@ -18,6 +18,10 @@ RoPE and the KV-cache write; mutates the query buffer and both caches),
 `nmsparse::gemv_add_` (out += W x, the residual add inside the GEMV; mutates
 out) and `nmsparse::gate_up_silu` (silu(W_gate x) * (W_up x) with the input
 RMSNorm folded in). They take fp16/bf16/fp32 inputs as they are (no casts).
+The split-K carry between a layer's launches adds `nmsparse::gemv_partials_`
+(a GEMV left as fp32 split partials; mutates its carry buffer) and the
+`_carried` forms of the q/k/v and gate/up launches, which finish their input
+from those partials and the residual stream (mutating vec_out).
 
 Backend selection keeps the reference's `NM_KERNEL` contract of refusing
 unknown values (src/spmv/nmsparse_op.py:20-22). Unset, "hip" and
@@ -38,8 +42,8 @@ import torch
 
 from typing import Optional
 
-from .hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode,
-                       nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip)
+from .hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_gemv_partials,
+                       nmsparse_qkv_decode, nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip)
 
 _kernel = os.environ.get("NM_KERNEL", "")
 if _kernel not in ("", "hip", "triton_ptx", "guarded", "fp16", "fp16_split"):
@@ -138,4 +142,56 @@ def _(x, gate_data, gate_index, up_data, up_index, block_width, vec_width, norm_
     return x.new_empty((1, gate_data.shape[1]))
 
 
-__all__ = ["gemv", "spmm", "qkv_decode", "gemv_add_", "gate_up_silu"]
+@torch.library.custom_op("nmsparse::gemv_partials_", mutates_args=("carry",))
+def gemv_partials_(x: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor, block_width: int,
+                   vec_width: int, carry: torch.Tensor) -> None:
+    """W_sparse x left as fp32 split partials in carry [splits, h], for the
+    next launch to finish (hip_spmv.nmsparse_gemv_partials)."""
+    nmsparse_gemv_partials(x.view(1, -1), mat_data, mat_index, int(block_width), int(vec_width), carry)
+
+
+@gemv_partials_.register_fake
+def _(x, mat_data, mat_index, block_width, vec_width, carry):
+    return None
+
+
+@torch.library.custom_op("nmsparse::qkv_decode_carried", mutates_args=("q_out", "k_cache_t", "v_cache_t", "vec_out"))
+def qkv_decode_carried(x: torch.Tensor, carry: torch.Tensor, vec_out: torch.Tensor, q_data: torch.Tensor,
+                       q_index: torch.Tensor, k_data: torch.Tensor, k_index: torch.Tensor, v_data: torch.Tensor,
+                       v_index: torch.Tensor, block_width: int, vec_width: int, q_out: torch.Tensor,
+                       k_cache_t: torch.Tensor, v_cache_t: torch.Tensor, pos: torch.Tensor, rope_table: torch.Tensor,
+                       head_dim: int, norm_weight: torch.Tensor, norm_eps: float, q_norm: Optional[torch.Tensor],
+                       k_norm: Optional[torch.Tensor], head_eps: float) -> None:
+    """qkv_decode on the input round(sum of carry's partials + x), which is
+    also written to vec_out (x: the residual stream before the producer)."""
+    nmsparse_qkv_decode(x.view(1, -1), (q_data, q_index), (k_data, k_index), (v_data, v_index), int(block_width),
+                        int(vec_width), q_out=q_out, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
+                        rope_table=rope_table, head_dim=int(head_dim), norm=(norm_weight, float(norm_eps)),
+                        q_norm=q_norm, k_norm=k_norm, head_eps=float(head_eps), carry_in=carry,
+                        vec_out=vec_out.view(1, -1))
+
+
+@qkv_decode_carried.register_fake
+def _(x, carry, vec_out, q_data, q_index, k_data, k_index, v_data, v_index, block_width, vec_width, q_out, k_cache_t,
+      v_cache_t, pos, rope_table, head_dim, norm_weight, norm_eps, q_norm, k_norm, head_eps):
+    return None
+
+
+@torch.library.custom_op("nmsparse::gate_up_silu_carried", mutates_args=("vec_out",))
+def gate_up_silu_carried(x: torch.Tensor, carry: torch.Tensor, vec_out: torch.Tensor, gate_data: torch.Tensor,
+                         gate_index: torch.Tensor, up_data: torch.Tensor, up_index: torch.Tensor, block_width: int,
+                         vec_width: int, norm_weight: torch.Tensor, norm_eps: float) -> torch.Tensor:
+    """gate_up_silu on the input round(sum of carry's partials + x), which is
+    also written to vec_out."""
+    return nmsparse_gate_up_silu(x.view(1, -1), (gate_data, gate_index), (up_data, up_index), int(block_width),
+                                 int(vec_width), norm=(norm_weight, float(norm_eps)), carry_in=carry,
+                                 vec_out=vec_out.view(1, -1))
+
+
+@gate_up_silu_carried.register_fake
+def _(x, carry, vec_out, gate_data, gate_index, up_data, up_index, block_width, vec_width, norm_weight, norm_eps):
+    return x.new_empty((1, gate_data.shape[1]))
+
+
+__all__ = ["gemv", "spmm", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_", "qkv_decode_carried",
+           "gate_up_silu_carried"]

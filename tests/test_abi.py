@@ -312,3 +312,60 @@ def test_static_scratch_entry_rejections_before_any_hip_call():
     assert lib.nm_gemv_launch_static(ctypes.byref(d), None) == -1
     assert f"#define NM_STATIC_SCRATCH_BYTES (NM_TICKET_BYTES + (16 << 20))" in HEADER.read_text()
     assert _lib.NM_STATIC_SCRATCH_BYTES == _lib.NM_TICKET_BYTES + (16 << 20)
+
+
+def test_split_k_carry_rejections_and_plans_before_launch():
+    """The carry descriptor fields: producer and consumer roles, their limits
+    and the consumer's plan (whole groups, <= 512 columns and <= 1024
+    positions of K per split), all decided on the host."""
+    import torch
+
+    from spmv_decode_amd.hip_spmv import launch_plan
+
+    lib = _lib.load()
+    pair = dict(kind=1, nprob=2, hs=(14336, 14336), norm_weight=FAKE)
+    ok = dict(carry_in=FAKE, carry_splits=8, vec_out=FAKE + 0x100000)
+    # a consumer needs the input norm, 1..16 producer splits, M a multiple of 4, vec_out apart from vec
+    assert _launch(_desc(**{**pair, "norm_weight": None}, **ok)) == -8
+    assert _launch(_desc(**pair, **{**ok, "carry_splits": 0})) == -8
+    assert _launch(_desc(**pair, **{**ok, "carry_splits": 17})) == -8
+    assert _launch(_desc(**pair, **{**ok, "vec_out": None})) == -8
+    assert _launch(_desc(**pair, **{**ok, "vec_out": FAKE})) == -8                  # overlaps vec
+    assert _launch(_desc(**pair, **{**ok, "vec_out": FAKE + 0x100008})) == -5       # misaligned
+    assert _launch(_desc(**pair, **{**ok, "carry_in": FAKE + 4})) == -5
+    assert _launch(_desc(**{**pair, "norm_weight": FAKE + 2}, **ok)) == -5
+    assert _launch(_desc(**pair, **ok, m=6, nnz=3, w=2040)) == -8                    # M not a multiple of 4
+    # a split of more than 1024 positions of K (1:4 density, 512 columns) cannot carry
+    assert _launch(_desc(**pair, **ok, nnz=16, m=64, w=1024, splits=2)) == -8
+    # producer and consumer at once; a producer is one plain GEMV without epilogue
+    assert _launch(_desc(**pair, **ok, carry_out=FAKE)) == -8
+    prod = dict(nprob=1, hs=(4096,), carry_out=FAKE)
+    assert _launch(_desc(**prod, norm_weight=FAKE)) == -8
+    d = _desc(**prod)
+    d.prob[0].residual = FAKE
+    assert _launch(d) == -8
+    d = _desc(**prod)
+    d.prob[0].rope, d.head_dim = 1, 128
+    assert _launch(d) == -8
+    d = _desc(**prod)
+    d.carry_out = FAKE + 4
+    assert _launch(d) == -5
+    # the consumer's workspace adds one float per workgroup for the slices' sums of squares
+    plain = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(_desc(**pair)))
+    carried = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(_desc(**pair, **ok)))
+    assert carried >= plain + 56 * 8 * 4
+
+    def mats(K, h, nnz=32, m=64):
+        return (torch.empty(K // m * nnz, h, dtype=torch.float16), torch.empty(K // m, nnz, dtype=torch.uint8))
+
+    # consumer plans of the decoder shapes: whole groups, <= 512 columns, <= 1024 positions per split
+    for K, hs, nnz, m, gate_up in ((4096, (14336, 14336), 32, 64, True), (4096, (4096, 1024, 1024), 32, 64, False),
+                                   (5120, (17408, 17408), 32, 64, True), (5120, (5120, 1024, 1024), 32, 64, False),
+                                   (5120, (25600, 25600), 16, 32, True), (5120, (8192, 1024, 1024), 16, 32, False),
+                                   (4096, (14336, 14336), 128, 256, True), (4096, (4096, 1024, 1024), 2, 4, False)):
+        p = launch_plan([mats(K, h, nnz, m) for h in hs], nnz, m, gate_up=gate_up, carried=True)
+        rows = p["rows_per_split"]
+        assert rows % nnz == 0 and rows % p["chunk_rows"] == 0 and rows <= 512 and rows // nnz * m <= 1024, (K, hs, p)
+    # the Llama-3.1-8B consumers keep the plain plans
+    assert launch_plan([mats(4096, 14336)] * 2, 32, 64, gate_up=True, carried=True) == launch_plan(
+        [mats(4096, 14336)] * 2, 32, 64, gate_up=True)

@@ -631,8 +631,9 @@ def test_decoder_fused_layer_matches_grouped_and_per_linear_paths(gpu, qk_norm):
     assert all(dm.fusable(b) for b in mdl.layers)
     toks = [3, 5, 7, 9, 11]
 
-    def run(mode):
+    def run(mode, carry=True):
         mdl.set_launch_mode(mode)
+        mdl.carry_splitk = carry
         try:
             mdl.setup_cache(16, "cuda", dtype=torch.float16)
             with torch.no_grad():
@@ -640,9 +641,16 @@ def test_decoder_fused_layer_matches_grouped_and_per_linear_paths(gpu, qk_norm):
                         for i, t in enumerate(toks)]
         finally:
             mdl.set_launch_mode("fused")
+            mdl.carry_splitk = True
 
-    fused, grouped, per_linear, modules = run("fused"), run("grouped"), run("per_linear"), run("modules")
-    for a, b, c, d in zip(fused, grouped, per_linear, modules):
+    fused = run("fused")
+    assert mdl._carry is not None and mdl._carry[1] is not None  # the fused layers carried the split-K sums
+    plain = run("fused", carry=False)
+    grouped, per_linear, modules = run("grouped"), run("per_linear"), run("modules")
+    for a, p, b, c, d in zip(fused, plain, grouped, per_linear, modules):
+        # the carried and the plain fused layers round the same values the same
+        # way; only the input norm's mean of squares is summed in another order
+        torch.testing.assert_close(a, p, rtol=2e-3, atol=2e-3)
         torch.testing.assert_close(a, b, rtol=2e-2, atol=2e-2)
         torch.testing.assert_close(b, c, rtol=2e-2, atol=2e-2)
         torch.testing.assert_close(d, c, rtol=2e-2, atol=2e-2)
