@@ -4,16 +4,21 @@
 
 One step = every sparse GEMV of one Llama-3.1-8B decode token at 32:64, as the
 decoder launches them: per layer one q/k/v launch with the input RMSNorm,
-RoPE and KV-cache write fused in, o with the residual add, one gate/up pair
-launch with the post-attention RMSNorm and the SiLU*mul epilogue, and down
-with the residual add (4 launches x 32 layers), over 32 layers' distinct
+RoPE and KV-cache write fused in, o, one gate/up pair launch with the
+post-attention RMSNorm and the SiLU*mul epilogue, and down (4 launches x 32
+layers), with the split-K carry of the decoder's fused path: o and down leave
+their fp32 split partials, and the gate/up launch and the next layer's q/k/v
+launch finish their input from them and the residual stream (the residual
+adds); the last down adds its residual itself. Over 32 layers' distinct
 packed weights (7.0 GB resident in HBM, far beyond the 256 MB Infinity Cache),
 fp16, batch 1, captured once in a hipGraph and replayed. `value` is the
 algorithmic bytes of the step (2*w*h weights + w index bytes per matrix,
 2*K activations once per launch, norm weights, residual reads, 2*h outputs
-per output vector, the RoPE table row) divided by the step time. The same
-launches without the fusions (config.plain_fused_step) and the GEMVs as 224
-separate launches (config.unfused_224_launches) are timed too.
+per output vector, the RoPE table row; the split partials passed between
+launches are not counted) divided by the step time. The same layer without
+the carry (o and down with the residual add, config.fused_step_without_carry),
+without any fusion (config.plain_fused_step) and the GEMVs as 224 separate
+launches (config.unfused_224_launches) are timed too.
 
 Also reported: per-shape average launch time and GB/s for the sparse kernel
 and for dense fp16 hipBLASLt GEMVs on the same shapes (the faster of its
@@ -138,7 +143,7 @@ def main():
 
     from spmv_decode_amd.decode.model import KEY_PAD
     from spmv_decode_amd.hip_spmv import GemvProblem
-    from spmv_decode_amd.microbench import DECODE_CLASSES, decode_form_bytes
+    from spmv_decode_amd.microbench import CARRIED_CLASSES, DECODE_CLASSES, decode_form_bytes
 
     # decode-form buffers: residual stream, attention output, norms, KV cache, RoPE table, position
     S = 512
@@ -166,6 +171,34 @@ def main():
         hip_spmv.nmsparse_gemv_launch(act, [GemvProblem(*lay["down_proj"], h2, residual=h1)], nnz, m)
 
     decode_bytes = L * sum(decode_form_bytes(c, nnz, m) for c in DECODE_CLASSES)
+
+    # the decoder's fused path: the split-K carry between the launches
+    co = torch.zeros(hip_spmv.carry_splits(*layers[0]["o_proj"], nnz, m), 4096, device=dev)
+    cd = torch.zeros(hip_spmv.carry_splits(*layers[0]["down_proj"], nnz, m), 4096, device=dev)
+    xa, hb = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(2))
+
+    def carried_layer(li):
+        # q/k/v finishes the previous down's partials (the first layer reads x_res), o leaves its partials,
+        # gate/up finishes them, down leaves its partials (the last one adds its residual)
+        lay = layers[li]
+        qkv = dict(q_out=qo, k_cache_t=kcs[li], v_cache_t=vcs[li], pos=pos, rope_table=rope, head_dim=128,
+                   norm=(ln1, 1e-5))
+        if li == 0:
+            hip_spmv.nmsparse_qkv_decode(x_res, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, **qkv)
+        else:
+            hip_spmv.nmsparse_qkv_decode(hb, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, carry_in=cd,
+                                         vec_out=xa, **qkv)
+        hip_spmv.nmsparse_gemv_partials(attn, *lay["o_proj"], nnz, m, co)
+        hip_spmv.nmsparse_gate_up_silu(x_res if li == 0 else xa, lay["gate_proj"], lay["up_proj"], nnz, m, out=act,
+                                       norm=(ln2, 1e-5), carry_in=co, vec_out=hb)
+        if li + 1 < L:
+            hip_spmv.nmsparse_gemv_partials(act, *lay["down_proj"], nnz, m, cd)
+        else:
+            hip_spmv.nmsparse_gemv_launch(act, [GemvProblem(*lay["down_proj"], h2, residual=hb)], nnz, m)
+
+    carried_bytes = (L * sum(decode_form_bytes(c, nnz, m) for c in CARRIED_CLASSES)
+                     - decode_form_bytes("qkv_decode_carried", nnz, m) + decode_form_bytes("qkv_decode", nnz, m)
+                     - decode_form_bytes("down_partials", nnz, m) + decode_form_bytes("down_resid", nnz, m))
 
     w4, w14 = 4096 // m * nnz, 14336 // m * nnz
     fused_bytes_layer = (
@@ -204,13 +237,16 @@ def main():
         return start.elapsed_time(end) / args.steps
 
     # ---- the timed step: one decode token's sparse GEMVs as the decoder runs them
-    ms_per_step = time_step(lambda: [decode_layer(li) for li in range(L)])
-    value = decode_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"decode-form step ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
+    ms_per_step = time_step(lambda: [carried_layer(li) for li in range(L)])
+    value = carried_bytes / (ms_per_step * 1e-3) / 1e9
+    log(f"decode step, carried ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
-    written = [act, qo, h1, h2, kcs[0][:, :, S // 2], vcs[0][:, :, S // 2]]
+    written = [act, qo, xa, hb, h2, kcs[1][:, :, S // 2], vcs[1][:, :, S // 2]]
     if not all(bool(torch.isfinite(o.float()).all()) for o in written):
         raise RuntimeError("non-finite GEMV output")
+    ms_nocarry = time_step(lambda: [decode_layer(li) for li in range(L)])
+    nocarry_value = decode_bytes / (ms_nocarry * 1e-3) / 1e9
+    log(f"decode step without the carry ({4 * L} launches) {ms_nocarry:.4f} ms -> {nocarry_value:.1f} GB/s")
     ms_plain = time_step(lambda: [fused_layer(li) for li in range(L)])
     plain_value = fused_bytes / (ms_plain * 1e-3) / 1e9
     log(f"plain fused step ({4 * L} launches, no norm/RoPE/residual fusions) {ms_plain:.4f} ms -> "
@@ -234,13 +270,19 @@ def main():
         "data": "synthetic (seeded on-device N(0,0.02) weights, random in-group patterns, N(0,1) activations)",
         "config": {
             "workload": f"Llama-3.1-8B decode-token sparse GEMVs at {nnz}:{m}: {L} layers x (q/k/v + input "
-                        "RMSNorm + RoPE + KV-cache write, o + residual, gate/up pair + RMSNorm + SiLU*mul, down + "
-                        "residual), batch 1, fp16, hipGraph replay, distinct resident weights per layer",
+                        "RMSNorm + RoPE + KV-cache write, o, gate/up pair + RMSNorm + SiLU*mul, down), the residual "
+                        "adds and o's / down's split-K reductions carried into the next launch, batch 1, fp16, "
+                        "hipGraph replay, distinct resident weights per layer",
             "ratio": f"{nnz}:{m}",
             "layers": L,
             "launches_per_step": 4 * L,
-            "algorithmic_bytes_per_step": decode_bytes,
+            "algorithmic_bytes_per_step": carried_bytes,
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
+            "fused_step_without_carry": {"ms_per_step": round(ms_nocarry, 5), "GBps": round(nocarry_value, 2),
+                                         "algorithmic_bytes_per_step": decode_bytes,
+                                         "launches": "q/k/v + norm/RoPE/cache, o + residual, gate/up pair + norm + "
+                                                     "SiLU*mul, down + residual: every launch reduces its own "
+                                                     "split-K partials"},
             "plain_fused_step": {"ms_per_step": round(ms_plain, 5), "GBps": round(plain_value, 2),
                                  "algorithmic_bytes_per_step": fused_bytes,
                                  "launches": "grouped q/k/v, o, gate/up pair with SiLU*mul, down (no norm, RoPE, "
@@ -275,28 +317,33 @@ def main():
             f"({per_shape[cls]['pct_peak']}%) {plan} x{case.copies} copies")
         del case
         torch.cuda.empty_cache()
-    # the step's launch classes (decode forms), weights rotated over >= 1 GiB
+    # the step's launch classes (decode forms, carried as in the step, and without the carry), weights rotated
+    # over >= 1 GiB each
     forms = MB.DecodeForms(nnz, m, rotate_bytes=1 << 30)
-    fused = {}
-    for c in DECODE_CLASSES:
+    per_class = {}
+    for c in CARRIED_CLASSES + DECODE_CLASSES:
         us = forms.time(c, reps=reps)
         b = forms.bytes(c)
-        fused[c] = {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": b,
-                    "GBps": round(b / (us * 1e-6) / 1e9, 1), "pct_peak": round(100 * b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
-                    "rotated_copies": forms.copies[c]}
-        log(f"decode class {c:18s}: {us:7.2f} us/launch {fused[c]['GBps']:7.1f} GB/s ({fused[c]['pct_peak']}%)")
+        per_class[c] = {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": b,
+                        "GBps": round(b / (us * 1e-6) / 1e9, 1),
+                        "pct_peak": round(100 * b / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 1),
+                        "rotated_copies": forms.copies[c]}
+        log(f"decode class {c:26s}: {us:7.2f} us/launch {per_class[c]['GBps']:7.1f} GB/s "
+            f"({per_class[c]['pct_peak']}%)")
     del forms
     torch.cuda.empty_cache()
+    fused = {c: per_class[c] for c in CARRIED_CLASSES}
     # dominant kernel: largest share of the step
     dom = max(fused, key=lambda c: fused[c]["us_per_launch"] * fused[c]["launches_per_step"])
     d = fused[dom]
     kernel_name = {
-        "gate_up_pair_norm": "nm_gemv_kernel<fp16, pair_th32_u4, NMAT=2, NORM> (gate/up pair + RMSNorm + SiLU*mul, "
-                             "K=4096 h=14336)",
-        "qkv_decode": "nm_gemv_kernel<fp16, th16_u8, NORM> (q/k/v + RMSNorm + RoPE + cache write, K=4096 "
-                      "h=4096+1024+1024)",
-        "down_resid": "nm_gemv_kernel<fp16, th16_u8> (down + residual, K=14336 h=4096)",
-        "o_resid": "nm_gemv_kernel<fp16, th16_u8> (o + residual, K=4096 h=4096)"}[dom]
+        "gate_up_pair_norm_carried": "nm_gemv_kernel<fp16, pair_th64_u4, NMAT=2, NORM, CARRY=8> (gate/up pair + "
+                                     "RMSNorm + SiLU*mul, input finished from o_proj's split partials + residual, "
+                                     "K=4096 h=14336)",
+        "qkv_decode_carried": "nm_gemv_kernel<fp16, th32_u8, NORM, CARRY=8> (q/k/v + RMSNorm + RoPE + cache write, "
+                              "input finished from down_proj's split partials + residual, K=4096 h=4096+1024+1024)",
+        "down_partials": "nm_gemv_kernel<fp16, th16_u8> (down, split partials left, K=14336 h=4096)",
+        "o_partials": "nm_gemv_kernel<fp16, th16_u8> (o, split partials left, K=4096 h=4096)"}[dom]
     result["roofline"] = {
         "bound": "hbm",
         "achieved": d["GBps"],
@@ -309,6 +356,7 @@ def main():
         "us_per_launch": d["us_per_launch"],
     }
     result["per_launch_class"] = fused
+    result["per_launch_class_without_carry"] = {c: per_class[c] for c in DECODE_CLASSES}
     traffic_file = ROOT / "profiles" / "traffic.json"
     if traffic_file.exists():
         t = json.loads(traffic_file.read_text()).get(f"{dom}_{nnz}:{m}")

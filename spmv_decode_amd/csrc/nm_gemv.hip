@@ -66,9 +66,12 @@ int validate_shape(int h, int w, int nnz, int m) {
 // Qwen3-32B shapes (h_total: summed output width of the launch). Single
 // matrix: 128-row tiles up to 4096 outputs, 256-row tiles up to 16384,
 // 512-row tiles beyond. Gate/up pair: 256-row tiles with 32-row chunks up to
-// 14336 outputs, 512-row tiles with 32-row chunks beyond.
-int auto_config(long long h_total, int nmat) {
-  if (nmat == 2) return h_total > 14336 ? 5 : 1;
+// 14336 outputs, 512-row tiles with 32-row chunks beyond; with a carried
+// input, 512-row tiles with 16-row chunks (half the workgroups of 256-row
+// tiles, so half the carried partials read: 23.0 against 24.3 us at the
+// Llama-3.1-8B shape).
+int auto_config(long long h_total, int nmat, bool carried) {
+  if (nmat == 2) return carried ? 4 : (h_total > 14336 ? 5 : 1);
   return h_total > 16384 ? 6 : (h_total > 4096 ? 3 : 1);
 }
 
@@ -88,8 +91,28 @@ constexpr int kPlanCUs = 256;
 //    fills 80% of its last round, the one in 4..12 that does best.
 // `eff(s)` is the number of splits a request for s splits gets once the rows
 // per split are rounded to whole chunks.
+//  * a gate/up pair of 512-row tiles (a carried input, or wider than 14336
+//    outputs) takes one round of workgroups: the largest split count whose
+//    grid has at most 7/8 of the CUs' workgroups, else the smallest grid of
+//    at most one per CU (sweeps: a second round of a few workgroups costs
+//    4-9 us; Qwen3-14B 33.1 us at 6 splits against 34.5 at 7, Qwen3-32B 44.1
+//    at 4 against 46.6 at 10).
 template <class EffSplits>
-int auto_splits(int tiles, int w, int nmat, EffSplits eff) {
+int auto_splits(int tiles, int w, int nmat, EffSplits eff, bool one_round) {
+  if (one_round) {
+    for (int s = 16; s >= 2; --s)
+      if ((long long)tiles * eff(s) <= kPlanCUs * 7 / 8) return s;
+    int best = 0;
+    long long fewest = kPlanCUs + 1;
+    for (int s = 2; s <= 16; ++s) {
+      const long long blocks = (long long)tiles * eff(s);
+      if (blocks < fewest) {
+        fewest = blocks;
+        best = s;
+      }
+    }
+    if (best) return best;
+  }
   auto balance = [&](int s) {
     const double rounds = (double)tiles * eff(s) / kPlanCUs;
     return rounds <= 1.0 ? 1.0 : rounds / ceil(rounds);
@@ -119,7 +142,7 @@ int auto_splits(int tiles, int w, int nmat, EffSplits eff) {
 // problem in its first NM_TICKET_BYTES and then nmat * splits * h floats of
 // partial sums per problem.
 int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg, int splits, Plan* p,
-              int max_rows = kMaxRows, int batch = 1, int row_align = 1) {
+              int max_rows = kMaxRows, int batch = 1, int row_align = 1, bool carried = false) {
   if (nprob < 1 || nprob > kMaxProblems || (nmat == 2 && nprob != 1)) return NM_ERR_BAD_SHAPE;
   long long h_total = 0;
   for (int i = 0; i < nprob; ++i) {
@@ -128,7 +151,7 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
     h_total += hs[i];
   }
   const int ncfg = nmat == 2 ? kNumDualConfigs : kNumConfigs;
-  if (cfg < 0) cfg = auto_config(h_total, nmat);
+  if (cfg < 0) cfg = auto_config(h_total, nmat, carried);
   if (cfg >= ncfg) return NM_ERR_BAD_CONFIG;
   const Config& c = nmat == 2 ? kDualConfigs[cfg] : kConfigs[cfg];
   const int HT = c.th * kVec;
@@ -146,7 +169,8 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
   if (splits <= 0) {
     int tiles = 0;
     for (int i = 0; i < nprob; ++i) tiles += ceil_div(hs[i], HT);
-    splits = auto_splits(tiles, w, nmat, [&](int s) { return ceil_div(w, rows_for(s)); });
+    const bool one_round = nmat == 2 && c.th == 64 && (carried || h_total > 14336);
+    splits = auto_splits(tiles, w, nmat, [&](int s) { return ceil_div(w, rows_for(s)); }, one_round);
   }
   const int rows = rows_for(splits);
   splits = ceil_div(w, rows);
@@ -196,7 +220,7 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   // A consumer's plan: whole groups of columns per split, at most 512 (the
   // carried-input kernels cover gather slots 0 and 1).
   int rc = make_plan(nprob, hs, d.w, d.nnz, d.m, nmat, d.config_id, d.splits, &p, carry_in ? 2 * kBlock : kMaxRows,
-                     1, carry_in ? d.nnz : 1);
+                     1, carry_in ? d.nnz : 1, carry_in);
   if (rc != NM_OK) return rc;
   if (carry_in) {
     // The ssq slots follow the partials: one float per workgroup.
@@ -585,7 +609,7 @@ int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int
   const bool carry_in = desc->carry_in != nullptr;
   if (desc->nnz <= 0) return NM_ERR_BAD_SHAPE;
   const int rc = make_plan(nprob, hs, desc->w, desc->nnz, desc->m, pair ? 2 : 1, desc->config_id, desc->splits, &p,
-                           carry_in ? 2 * kBlock : kMaxRows, 1, carry_in ? desc->nnz : 1);
+                           carry_in ? 2 * kBlock : kMaxRows, 1, carry_in ? desc->nnz : 1, carry_in);
   if (rc != NM_OK) return rc;
   const Config& c = pair ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
   if (out_config_id) *out_config_id = p.cfg;

@@ -185,6 +185,16 @@ def decode_form_bytes(cls, nnz=32, m=64, dim=4096, inter=14336, qd=4096, kvd=102
         return 2 * (2 * wd * inter + wd) + 2 * dim + 2 * dim + 2 * inter
     if cls == "down_resid":
         return 2 * wi * dim + wi + 2 * inter + 2 * dim + 2 * dim
+    # split-K carry: the producers read weights, index and input only; each
+    # consumer also reads the residual stream and writes the finished vector
+    # (the split partials passed between them are not counted, as the
+    # partials of every split-K launch are not)
+    if cls == "o_partials":
+        return 2 * wq * dim + wq + 2 * qd
+    if cls == "down_partials":
+        return 2 * wi * dim + wi + 2 * inter
+    if cls in ("qkv_decode_carried", "gate_up_pair_norm_carried"):
+        return decode_form_bytes(cls[:-len("_carried")], nnz, m, dim, inter, qd, kvd, hd, qk_norm) + 2 * dim
     raise ValueError(cls)
 
 
@@ -242,6 +252,14 @@ class DecodeForms:
         self.pos = torch.tensor([S // 2], device=device)
         self.copies = {"qkv_decode": cq, "o_resid": self.o.copies, "gate_up_pair_norm": cp,
                        "down_resid": self.down.copies}
+        self.copies.update({"qkv_decode_carried": cq, "o_partials": self.o.copies, "gate_up_pair_norm_carried": cp,
+                            "down_partials": self.down.copies})
+        # split-K carry: the producers' fp32 partials and the consumers' finished vectors
+        from .hip_spmv import carry_splits
+
+        self.carry_o = torch.zeros(carry_splits(*self.o.mats[0], nnz, m), dim, device=device)
+        self.carry_d = torch.zeros(carry_splits(*self.down.mats[0], nnz, m), dim, device=device)
+        self.x_fin, self.h_fin = (torch.empty(1, dim, dtype=f16, device=device) for _ in range(2))
 
     def launch(self, cls, i, config_id=-1, splits=0):
         from .hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
@@ -260,6 +278,18 @@ class DecodeForms:
         elif cls == "down_resid":
             nmsparse_gemv_launch(self.act, [GemvProblem(*self.down.mats[i], self.h2, residual=self.h1)], nnz, m,
                                  **kw)
+        elif cls == "o_partials":
+            nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i])], nnz, m, carry_out=self.carry_o, **kw)
+        elif cls == "gate_up_pair_norm_carried":
+            nmsparse_gate_up_silu(self.x, self.gate.mats[i], self.up.mats[i], nnz, m, out=self.pair_out,
+                                  norm=(self.ln2, 1e-5), carry_in=self.carry_o, vec_out=self.h_fin, **kw)
+        elif cls == "down_partials":
+            nmsparse_gemv_launch(self.act, [GemvProblem(*self.down.mats[i])], nnz, m, carry_out=self.carry_d, **kw)
+        elif cls == "qkv_decode_carried":
+            nmsparse_qkv_decode(self.x, self.q.mats[i], self.k.mats[i], self.v.mats[i], nnz, m, q_out=self.qo,
+                                k_cache_t=self.k_cache, v_cache_t=self.v_cache, pos=self.pos, rope_table=self.rope,
+                                head_dim=self.hd, norm=(self.ln1, 1e-5), q_norm=self.q_norm, k_norm=self.k_norm,
+                                carry_in=self.carry_d, vec_out=self.x_fin, **kw)
         else:
             raise ValueError(cls)
 
@@ -272,6 +302,9 @@ class DecodeForms:
 
 
 DECODE_CLASSES = ("qkv_decode", "o_resid", "gate_up_pair_norm", "down_resid")
+# The same layer with the split-K carry (the decoder's default fused path):
+# o and down leave their partials, gate/up and the next q/k/v finish them.
+CARRIED_CLASSES = ("qkv_decode_carried", "o_partials", "gate_up_pair_norm_carried", "down_partials")
 
 
 def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60) -> float:
@@ -477,34 +510,39 @@ def write_stripe_md(res, path, cmd):
     Path(path).write_text("\n".join(lines) + "\n")
 
 
-def decode_classes(model, ratios, reps=20, warmup=5, rotate_bytes=1 << 30, log=print):
+def decode_classes(model, ratios, reps=20, warmup=5, rotate_bytes=1 << 30, log=print, classes=None):
     """The decoder's four fused launches (DecodeForms) at one model's shapes,
     per ratio: us per launch (median of graph replays over >= 1 GiB of rotated
     weights per class), algorithmic GB/s and % of the 8 TB/s HBM peak, and the
-    sum over one token's launches (layers x 4)."""
+    sum over one token's launches (layers x 4). With the carried classes in
+    `classes`, the token sum of the layer with the split-K carry too."""
     from .decode.model import CONFIGS
 
     cfg = CONFIGS[model]
+    classes = tuple(classes or DECODE_CLASSES)
     res = {}
     for nnz, m in ratios:
         forms = DecodeForms(nnz, m, rotate_bytes=rotate_bytes, dim=cfg.dim, inter=cfg.inter, n_heads=cfg.n_heads,
                             n_kv_heads=cfg.n_kv_heads, head_dim=cfg.head_dim, qk_norm=cfg.qk_norm)
-        per, tok_us, tok_bytes = {}, 0.0, 0
-        for c in DECODE_CLASSES:
+        per = {}
+        for c in classes:
             fns = [lambda i=i, c=c: forms.launch(c, i) for i in range(forms.copies[c])]
             us, sd = graph_us_per_launch(fns, reps, warmup, stats=True)
             b = forms.bytes(c)
             per[c] = {"us": round(us, 3), "us_sd": round(sd, 3), "bytes": b, "GBps": round(b / us / 1e3, 1),
                       "pct_peak": round(b / us / 1e3 / 80.0, 1), "copies": forms.copies[c]}
-            tok_us += us * cfg.n_layers
-            tok_bytes += b * cfg.n_layers
-            log(f"{model} {nnz}:{m} {c:18s}: {us:7.2f} +- {sd:.2f} us {per[c]['GBps']:7.1f} GB/s "
+            log(f"{model} {nnz}:{m} {c:26s}: {us:7.2f} +- {sd:.2f} us {per[c]['GBps']:7.1f} GB/s "
                 f"({per[c]['pct_peak']}%)")
-        res[f"{nnz}:{m}"] = {"classes": per, "token_us": round(tok_us, 1), "token_bytes": tok_bytes,
-                             "token_GBps": round(tok_bytes / tok_us / 1e3, 1),
-                             "token_pct_peak": round(tok_bytes / tok_us / 1e3 / 80.0, 1)}
-        log(f"{model} {nnz}:{m}: one token's {4 * cfg.n_layers} sparse launches {tok_us:.1f} us, "
-            f"{res[f'{nnz}:{m}']['token_GBps']} GB/s")
+        r = {"classes": per}
+        for tag, group in (("token", DECODE_CLASSES), ("token_carried", CARRIED_CLASSES)):
+            if all(c in per for c in group):
+                t_us = sum(per[c]["us"] for c in group) * cfg.n_layers
+                t_b = sum(per[c]["bytes"] for c in group) * cfg.n_layers
+                r[tag] = {"us": round(t_us, 1), "bytes": t_b, "GBps": round(t_b / t_us / 1e3, 1),
+                          "pct_peak": round(t_b / t_us / 1e3 / 80.0, 1)}
+                log(f"{model} {nnz}:{m}: one token's {4 * cfg.n_layers} sparse launches ({tag}) {t_us:.1f} us, "
+                    f"{r[tag]['GBps']} GB/s")
+        res[f"{nnz}:{m}"] = r
         del forms
         torch.cuda.empty_cache()
     return res
@@ -514,9 +552,11 @@ def write_decode_classes_md(model, res, path, cmd):
     from .decode.model import CONFIGS
 
     cfg = CONFIGS[model]
-    names = {"qkv_decode": "q/k/v + input RMSNorm + RoPE + KV-cache write" + (" + q/k head norms" if cfg.qk_norm else ""),
-             "o_resid": "o + residual", "gate_up_pair_norm": "gate/up pair + RMSNorm + SiLU*mul",
-             "down_resid": "down + residual"}
+    qkv = "q/k/v + input RMSNorm + RoPE + KV-cache write" + (" + q/k head norms" if cfg.qk_norm else "")
+    names = {"qkv_decode": qkv, "o_resid": "o + residual", "gate_up_pair_norm": "gate/up pair + RMSNorm + SiLU*mul",
+             "down_resid": "down + residual", "qkv_decode_carried": qkv + ", carried input",
+             "o_partials": "o, partials left", "gate_up_pair_norm_carried": "gate/up pair + RMSNorm + SiLU*mul, carried input",
+             "down_partials": "down, partials left"}
     lines = [f"# Sparse GEMV launches of the fused decoder layer: {cfg.name} shapes (MI355X, fp16, batch 1)", "",
              "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
              f"The decoder's four launches per layer at {cfg.name}'s shapes (dim {cfg.dim}, intermediate "
@@ -525,33 +565,48 @@ def write_decode_classes_md(model, res, path, cmd):
              "Infinity Cache serves them), the library's default plan; median +- sd over the replays, per launch,",
              "inter-kernel gap included. GB/s counts the algorithmic bytes of the launch (packed weights and index,",
              "activations once, norm weights, residual, outputs, RoPE row); % of the 8 TB/s HBM peak. 'Token' sums",
-             f"one decode token's {4 * cfg.n_layers} launches ({cfg.n_layers} layers).", "",
+             f"one decode token's {4 * cfg.n_layers} launches ({cfg.n_layers} layers); 'carried' rows are the layer",
+             "with the split-K carry (o and down leave their fp32 partials; gate/up and the next q/k/v finish",
+             "them, reading the residual and writing the finished vector; the partials are not counted).", "",
              "| N:M | Launch | us (median +- sd) | Algorithmic bytes | GB/s | % peak |", "|---|---|---|---|---|---|"]
     for ratio, r in res.items():
         for c, v in r["classes"].items():
             lines.append(f"| {ratio} | {names[c]} | {v['us']:.2f} +- {v['us_sd']:.2f} | {v['bytes']:,} | "
                          f"{v['GBps']:.0f} | {v['pct_peak']:.1f}% |")
-        lines.append(f"| {ratio} | token ({4 * cfg.n_layers} launches) | {r['token_us']:.1f} | {r['token_bytes']:,} | "
-                     f"{r['token_GBps']:.0f} | {r['token_pct_peak']:.1f}% |")
+        for tag, label in (("token", "token"), ("token_carried", "token, carried")):
+            if tag in r:
+                t = r[tag]
+                lines.append(f"| {ratio} | {label} ({4 * cfg.n_layers} launches) | {t['us']:.1f} | {t['bytes']:,} | "
+                             f"{t['GBps']:.0f} | {t['pct_peak']:.1f}% |")
     Path(path).write_text("\n".join(lines) + "\n")
 
 
 def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8, 9, 10, 12, 14, 16), reps=20,
-                 warmup=5, log=print):
+                 warmup=5, log=print, model=None):
     """One of the decoder's fused launches at the Llama-3.1-8B shapes under
     every configuration x split count (weights rotated over >= 1 GiB, graph
     replay): "gate_up_pair_norm" (the pair configurations) or "qkv_decode"
     (the plain configurations, grouped q/k/v with the input RMSNorm, RoPE and
-    cache write). Rows in the --sweep CSV layout, the configuration named from
-    the plan (TH from the tile count, U from the chunk; `pair_` for the pair),
-    with the kernel's NMAT and NORM so that profiling sweep-stats can match
-    them to the traced kernels."""
+    cache write), or either with "_carried" (its input finished from the
+    producer's split partials; plans that cannot carry are skipped). Rows in
+    the --sweep CSV layout, the configuration named from the plan (TH from the
+    tile count, U from the chunk; `pair_` for the pair), with the kernel's NMAT
+    and NORM so that profiling sweep-stats can match them to the traced
+    kernels."""
     from .hip_spmv import launch_plan
 
-    pair = cls == "gate_up_pair_norm"
-    if not pair and cls != "qkv_decode":
+    carried = cls.endswith("_carried")
+    pair = cls.startswith("gate_up_pair_norm")
+    if cls not in ("gate_up_pair_norm", "qkv_decode", "gate_up_pair_norm_carried", "qkv_decode_carried"):
         raise ValueError(f"launch_sweep: {cls!r} is not a fused decoder launch with its own plan")
-    forms = DecodeForms(nnz, m)
+    if model:  # another model's shapes (default: Llama-3.1-8B)
+        from .decode.model import CONFIGS
+
+        c = CONFIGS[model]
+        forms = DecodeForms(nnz, m, dim=c.dim, inter=c.inter, n_heads=c.n_heads, n_kv_heads=c.n_kv_heads,
+                            head_dim=c.head_dim, qk_norm=c.qk_norm)
+    else:
+        forms = DecodeForms(nnz, m)
     mats = [forms.gate.mats[0], forms.up.mats[0]] if pair else [forms.q.mats[0], forms.k.mats[0], forms.v.mats[0]]
     hs = [forms.inter] if pair else [int(md.shape[1]) for md, _ in mats]
     nbytes = forms.bytes(cls)
@@ -560,7 +615,7 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
     rows, seen = [], set()
     for cfg in [-1, *range(n_cfg)]:
         for sp in ((0,) if cfg < 0 else splits_list):
-            plan = launch_plan(mats, nnz, m, gate_up=pair, config_id=cfg, splits=sp)
+            plan = launch_plan(mats, nnz, m, gate_up=pair, config_id=cfg, splits=sp, carried=carried)
             key = (plan["config_id"], plan["splits"])
             if cfg >= 0 and key in seen:
                 continue
@@ -575,6 +630,12 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
             def launch(i, cfg=cfg, sp=sp):
                 forms.launch(cls, i, config_id=cfg, splits=sp)
 
+            if carried:
+                try:
+                    launch(0)
+                except _lib.NmSparseLibraryError:
+                    log(f"{cls} {name} s={plan['splits']}: this plan cannot take a carried input, skipped")
+                    continue
             us = graph_us_per_launch([lambda i=i: launch(i) for i in range(n)], reps, warmup)
             rows.append({"config": name, "config_id": plan["config_id"], "n_out": sum(hs), "n_in": forms.dim,
                          "ratio": f"{nnz}:{m}", "splits": plan["splits"], "blocks": plan["blocks"],
@@ -590,7 +651,8 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     """Workload for `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE` passes:
     three copies of a 256 MiB buffer (the known-size calibration kernel), then
     three GEMV launches per shape, each on distinct weights, then three grouped
-    q/k/v launches and three gate/up pair launches at the Llama-3.1-8B shapes."""
+    q/k/v launches and three gate/up pair launches at the Llama-3.1-8B shapes,
+    then three of each decoder-layer launch, plain and carried."""
     x = torch.empty(128 << 20, dtype=torch.float16, device="cuda").normal_()
     y = torch.empty_like(x)
     for _ in range(3):
@@ -617,11 +679,11 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     del g, u
     log("traffic probe: grouped q/k/v and gate/up pair done")
     forms = DecodeForms(nnz, m, rotate_bytes=0, min_copies=3)
-    for cls in DECODE_CLASSES:
+    for cls in DECODE_CLASSES + CARRIED_CLASSES:
         for i in range(3):
             forms.launch(cls, i)
         torch.cuda.synchronize()
-    log("traffic probe: decode-form launches done")
+    log("traffic probe: decode-form launches (plain and carried) done")
 
 
 def write_sweep_md(rows, path, cmd):
@@ -676,11 +738,19 @@ def main(argv=None):
     p.add_argument("--decode-classes", default=None, metavar="MODEL",
                    help="time the fused decoder layer's four launches at MODEL's shapes (llama-3.1-8b, qwen3-14b, "
                         "qwen3-32b) for each --ratios entry")
+    p.add_argument("--model", default=None,
+                   help="with --pair-sweep / --qkv-sweep: that model's shapes (qwen3-14b, qwen3-32b; default "
+                        "llama-3.1-8b)")
+    p.add_argument("--carried", action="store_true",
+                   help="with --decode-classes: also the four launches of the layer with the split-K carry "
+                        "(o and down leave their partials, gate/up and q/k/v finish them); with --pair-sweep / "
+                        "--qkv-sweep: sweep the launch with a carried input")
     a = p.parse_args(argv)
     if a.pair_sweep or a.qkv_sweep:
         nnz, m = _parse_pairs(a.ratios, ":")[0]
-        rows = launch_sweep("gate_up_pair_norm" if a.pair_sweep else "qkv_decode", nnz, m, reps=a.reps,
-                            warmup=a.warmup, log=lambda s: print(s, flush=True))
+        cls = ("gate_up_pair_norm" if a.pair_sweep else "qkv_decode") + ("_carried" if a.carried else "")
+        rows = launch_sweep(cls, nnz, m, reps=a.reps, warmup=a.warmup, log=lambda s: print(s, flush=True),
+                            model=a.model)
         if a.csv:
             with open(a.csv, "w", newline="") as f:
                 wr = csv.DictWriter(f, fieldnames=list(rows[0].keys()))
@@ -689,7 +759,8 @@ def main(argv=None):
         return 0
     if a.decode_classes:
         res = decode_classes(a.decode_classes, _parse_pairs(a.ratios, ":"), a.reps, a.warmup, a.rotate_mib << 20,
-                             log=lambda s: print(s, flush=True))
+                             log=lambda s: print(s, flush=True),
+                             classes=DECODE_CLASSES + CARRIED_CLASSES if a.carried else DECODE_CLASSES)
         if a.json:
             Path(a.json).write_text(json.dumps(res, indent=1))
         if a.md:

@@ -34,6 +34,10 @@ PROBE_CLASSES = [
     ("o_resid_32:64", None, None, None, "o + residual add (decode form)"),
     ("gate_up_pair_norm_32:64", None, None, None, "gate/up pair + input RMSNorm (decode form)"),
     ("down_resid_32:64", None, None, None, "down + residual add (decode form)"),
+    ("qkv_decode_carried_32:64", None, None, None, "q/k/v decode form, input carried from down's partials"),
+    ("o_partials_32:64", None, None, None, "o, split partials left for the next launch"),
+    ("gate_up_pair_norm_carried_32:64", None, None, None, "gate/up pair + RMSNorm, input carried from o's partials"),
+    ("down_partials_32:64", None, None, None, "down, split partials left for the next launch"),
 ]
 
 
@@ -95,8 +99,9 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
              "The probe copies a 256 MiB fp16 buffer three times (the known-size calibration kernel), then launches",
              "each class three times on distinct weights with the library's default plan. Kernel template arguments:",
              "<dtype (0 = fp16), TH (tile = 8*TH rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT",
-             "(2 = gate/up pair), NORM (input RMSNorm folded into the gather)>. The decode-form classes are the",
-             "launches bench.py times as its step (microbench.DecodeForms).",
+             "(2 = gate/up pair), NORM (input RMSNorm folded into the gather), CARRY (most producer splits a carried",
+             "input reads; 0 = none)>. The decode-form classes are the launches of the decoder's fused layer",
+             "(microbench.DecodeForms); bench.py times the carried ones as its step.",
              "",
              f"Calibration: the 256 MiB copy reads {sum(fcopy) / len(fcopy):.1f} KiB by FETCH_SIZE (true "
              f"{CALIBRATION_BYTES // 1024} KiB) -> fetch scale {fscale:.4f}; it writes {sum(wcopy) / len(wcopy):.1f} KiB "
@@ -105,7 +110,8 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
              "|---|---|---|---|---|---|", *table, "",
              "Extra fetch over the algorithmic bytes is the index bytes and activations re-read by every output tile",
              "of a split plus the partial sums read back by the last workgroup of each tile; extra writes are the fp32",
-             "split-K partials (8 splits x h x 4 B per matrix). No weight byte is fetched twice.",
+             "split-K partials (8 splits x h x 4 B per matrix). A carried launch also fetches the producer's partials",
+             "(splits x K x 4 B, once per XCD's L2), and a producer writes them. No weight byte is fetched twice.",
              "`profiles/traffic.json` holds the same numbers; bench.py reports `bytes_per_launch` of the dominant",
              "launch class as `roofline.traffic`."]
     Path(md_path).write_text("\n".join(lines) + "\n")
@@ -120,12 +126,15 @@ def stats(stats_csv, bench_json, md_path, cmd):
              "python -u bench.py > gpurun_out/bench.json", cmd,
              "python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv "
              "--bench gpurun_out/bench.json --md <this file>", "```", "",
-             "The run covers the decode-form step graph (q/k/v + RMSNorm + RoPE + cache write, o + residual, gate/up",
-             "pair + RMSNorm + SiLU*mul, down + residual per layer), the plain fused step, the 224-launch step graph,",
-             "per-class rotation graphs (>= 1 GiB of distinct weights each), the small-batch SpMM graphs and the dense",
+             "The run covers the decode step graph with the split-K carry (per layer: q/k/v + RMSNorm + RoPE + cache",
+             "write finishing the previous down's partials, o leaving its partials, gate/up pair + RMSNorm + SiLU*mul",
+             "finishing o's, down leaving its partials), the same step without the carry (o and down + residual), the",
+             "plain fused step, the 224-launch step graph, per-class rotation graphs (>= 1 GiB of distinct weights",
+             "each, carried and plain classes), the small-batch SpMM graphs and the dense",
              "hipBLASLt baseline graphs. `nm_gemv_kernel` template arguments: <dtype (0 = fp16), TH (tile = 8*TH",
              "rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair), NORM (input",
-             "RMSNorm)>; `nm_spmm_kernel`: <dtype, TH, U, G, NT, batch rows per launch>.", "",
+             "RMSNorm), CARRY (most producer splits of a carried input; 0 = none)>; `nm_spmm_kernel`: <dtype, TH, U,",
+             "G, NT, batch rows per launch>.", "",
              "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
         n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
@@ -138,11 +147,14 @@ def stats(stats_csv, bench_json, md_path, cmd):
         lines += ["", f"Unprofiled `python bench.py` from the same call: value {b['value']} GB/s, ms_per_step "
                       f"{b['ms_per_step']}; dominant launch class: {rf.get('kernel')} at {rf.get('us_per_launch')} us "
                       f"per launch (HIP events over graph replays, {rf.get('achieved')} GB/s, frac {rf.get('frac')})."]
-        pair_norm = [r for r in pair if r["Name"].rstrip().endswith("true>(nm_hip::Args)")]
-        if pair_norm:
-            lines.append(f"rocprof average kernel duration of the gate/up pair + RMSNorm kernel: "
-                         f"{float(pair_norm[0]['AverageNs']) / 1e3:.2f} us (the replay-timed figure also includes the "
-                         "inter-kernel gap of the graph).")
+        for r in pair:
+            n = r["Name"]
+            if ", 2, true, " not in n:
+                continue
+            what = "with a carried input" if ", 2, true, 0>" not in n else "with its own input"
+            lines.append(f"rocprof average kernel duration of the gate/up pair + RMSNorm kernel {what}: "
+                         f"{float(r['AverageNs']) / 1e3:.2f} us over {r['Calls']} calls (the replay-timed figure also "
+                         "includes the inter-kernel gap of the graph).")
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 
@@ -154,17 +166,18 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
     d = json.loads(Path(decode_json).read_text())
     layers = CONFIGS[d["model"]].n_layers
     pair = [r for r in rows if ", true, 2, " in r["Name"]]
-    steps = int(pair[0]["Calls"]) // layers  # one gate/up launch per layer and step
+    steps = sum(int(r["Calls"]) for r in pair) // layers  # one gate/up launch per layer and step
 
     def kind(r):
         n, per_step = r["Name"], int(r["Calls"]) / steps
         if per_step < 0.9:
             return None  # model set-up (random init, packing), not part of a step
         if "nm_gemv_kernel" in n:
-            if ", 2, " in n:
+            if ", true, 2, " in n:
                 return "sparse GEMV: gate/up pair + RMSNorm + SiLU*mul"
-            return "sparse GEMV: q/k/v + RMSNorm + RoPE + cache write" if n.rstrip().endswith(
-                "true>(nm_hip::Args)") else "sparse GEMV: o or down + residual"
+            # <dtype, TH, U, G, NT, NMAT, NORM, CARRY>: the input norm marks the q/k/v launch
+            return ("sparse GEMV: q/k/v + RMSNorm + RoPE + cache write" if ", 1, true, " in n
+                    else "sparse GEMV: o or down (+ residual, or partials left)")
         if n.startswith("Cijk_"):
             return "attention product (hipBLASLt)" if per_step > 1.5 else "lm_head (hipBLASLt, dense)"
         if "softmax" in n:

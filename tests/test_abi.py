@@ -282,8 +282,11 @@ def test_launch_plan_query():
     # empty take the split count (nearest 8) that fills their rounds best
     assert summary(launch_plan([mats(17408, 5120)], 32, 64)) == (3, 12, 20 * 12)
     assert summary(launch_plan([mats(5120, 8192), mats(5120, 1024), mats(5120, 1024)], 32, 64)) == (3, 6, 40 * 6)
-    # the widest launches take 512-row tiles
-    assert summary(launch_plan([mats(5120, 25600), mats(5120, 25600)], 32, 64, gate_up=True)) == (5, 10, 50 * 10)
+    # the widest launches take 512-row tiles; a pair of them one round of workgroups (<= 7/8 of the CUs)
+    assert summary(launch_plan([mats(5120, 25600), mats(5120, 25600)], 32, 64, gate_up=True)) == (5, 4, 50 * 4)
+    assert summary(launch_plan([mats(5120, 17408), mats(5120, 17408)], 32, 64, gate_up=True)) == (5, 6, 34 * 6)
+    # with a carried input the pair takes 512-row tiles at every width (half the carried reads of 256-row tiles)
+    assert summary(launch_plan([mats(4096, 14336)] * 2, 32, 64, gate_up=True, carried=True)) == (4, 8, 28 * 8)
     assert summary(launch_plan([mats(5120, 17408)], 32, 64)) == (6, 7, 34 * 7)
     with pytest.raises(_lib.NmSparseLibraryError):
         launch_plan([mats(4096, 1000)], 32, 64)
@@ -353,7 +356,7 @@ def test_split_k_carry_rejections_and_plans_before_launch():
     # the consumer's workspace adds one float per workgroup for the slices' sums of squares
     plain = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(_desc(**pair)))
     carried = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(_desc(**pair, **ok)))
-    assert carried >= plain + 56 * 8 * 4
+    assert carried == plain + 28 * 8 * 4  # the carried plan: 28 tiles of 512 rows x 8 splits
 
     def mats(K, h, nnz=32, m=64):
         return (torch.empty(K // m * nnz, h, dtype=torch.float16), torch.empty(K // m, nnz, dtype=torch.uint8))
@@ -366,6 +369,6 @@ def test_split_k_carry_rejections_and_plans_before_launch():
         p = launch_plan([mats(K, h, nnz, m) for h in hs], nnz, m, gate_up=gate_up, carried=True)
         rows = p["rows_per_split"]
         assert rows % nnz == 0 and rows % p["chunk_rows"] == 0 and rows <= 512 and rows // nnz * m <= 1024, (K, hs, p)
-    # the Llama-3.1-8B consumers keep the plain plans
-    assert launch_plan([mats(4096, 14336)] * 2, 32, 64, gate_up=True, carried=True) == launch_plan(
-        [mats(4096, 14336)] * 2, 32, 64, gate_up=True)
+    # the Llama-3.1-8B q/k/v consumer keeps the plain plan
+    qkv = [mats(4096, h) for h in (4096, 1024, 1024)]
+    assert launch_plan(qkv, 32, 64, carried=True) == launch_plan(qkv, 32, 64)

@@ -38,6 +38,16 @@ def test_decode_form_bytes_are_the_gemvs_plus_their_extra_operands():
     # the pair: two weight/index streams, x once, the norm weight, one SiLU*mul output
     assert f("gate_up_pair_norm") == 2 * g(4096, 14336) - 2 * 4096 - 2 * 14336 + 2 * 4096
     assert f("down_resid") == g(14336, 4096) + 2 * 4096
+    # split-K carry: the producers read weights, index and input only; the
+    # consumers add the residual read and the finished vector's write, so a
+    # carried layer moves the plain layer's bytes less o's output write and
+    # the pair's read of it (2 x 2 x dim)
+    assert f("o_partials") == g(4096, 4096) - 2 * 4096
+    assert f("down_partials") == g(14336, 4096) - 2 * 4096
+    assert f("gate_up_pair_norm_carried") == f("gate_up_pair_norm") + 2 * 4096
+    assert f("qkv_decode_carried") == f("qkv_decode") + 2 * 4096
+    plain = sum(f(c) for c in MB.DECODE_CLASSES)
+    assert sum(f(c) for c in MB.CARRIED_CLASSES) == plain - 2 * 2 * 4096
     with pytest.raises(ValueError):
         MB.decode_form_bytes("lm_head")
 
@@ -45,14 +55,15 @@ def test_decode_form_bytes_are_the_gemvs_plus_their_extra_operands():
 def test_parse_pairs_and_summary_writers(tmp_path):
     assert MB._parse_pairs("4096x4096,1024x4096", "x") == [(4096, 4096), (1024, 4096)]
     assert MB._parse_pairs("2:4,32:64,", ":") == [(2, 4), (32, 64)]
+    tok = {"us": 256.0, "bytes": 128_000_000, "GBps": 500.0, "pct_peak": 6.2}
     res = {"32:64": {"classes": {c: {"us": 2.0, "us_sd": 0.1, "bytes": 1_000_000, "GBps": 500.0, "pct_peak": 6.2,
-                                     "copies": 3} for c in MB.DECODE_CLASSES},
-                     "token_us": 256.0, "token_bytes": 128_000_000, "token_GBps": 500.0, "token_pct_peak": 6.2}}
+                                     "copies": 3} for c in MB.DECODE_CLASSES + MB.CARRIED_CLASSES},
+                     "token": tok, "token_carried": tok}}
     md = tmp_path / "dc.md"
     MB.write_decode_classes_md("qwen3-14b", res, md, "python -u -m spmv_decode_amd.microbench --decode-classes x")
     text = md.read_text()
     assert "--decode-classes x" in text and "+ q/k head norms" in text and "160 launches" in text
-    assert text.count("| 32:64 |") == 5
+    assert text.count("| 32:64 |") == 10 and "token, carried (160 launches)" in text
     rows = [{"config": "auto:th16_u8", "n_in": 4096, "n_out": 4096, "ratio": "32:64", "splits": 8, "us": 7.2,
              "us_sd": 0.05, "GBps": 2333.0, "pct_peak": 29.2, "dense_us": 11.9, "dense_us_sd": 0.1, "dense_form": "mv",
              "dense_GBps": 2800.0, "speedup_vs_dense": 1.65, "max_abs": 1e-3, "rel_l2": 2e-4},
@@ -71,15 +82,17 @@ def test_decode_classes_times_every_launch_at_a_qwen3_shape(gpu, tmp_path):
     from spmv_decode_amd.decode.model import CONFIGS
 
     cfg = CONFIGS["qwen3-14b"]
-    res = MB.decode_classes("qwen3-14b", [(32, 64)], reps=3, warmup=1, rotate_bytes=0, log=lambda s: None)
+    res = MB.decode_classes("qwen3-14b", [(32, 64)], reps=3, warmup=1, rotate_bytes=0, log=lambda s: None,
+                            classes=MB.DECODE_CLASSES + MB.CARRIED_CLASSES)
     r = res["32:64"]
-    assert set(r["classes"]) == set(MB.DECODE_CLASSES)
+    assert set(r["classes"]) == set(MB.DECODE_CLASSES + MB.CARRIED_CLASSES)
     for c, v in r["classes"].items():
         assert v["us"] > 0 and v["copies"] == 1
         assert v["bytes"] == MB.decode_form_bytes(c, 32, 64, cfg.dim, cfg.inter, cfg.n_heads * cfg.head_dim,
                                                   cfg.n_kv_heads * cfg.head_dim, cfg.head_dim, True)
-    assert r["token_bytes"] == cfg.n_layers * sum(v["bytes"] for v in r["classes"].values())
-    assert r["token_us"] == pytest.approx(cfg.n_layers * sum(v["us"] for v in r["classes"].values()), rel=1e-3)
+    for tag, group in (("token", MB.DECODE_CLASSES), ("token_carried", MB.CARRIED_CLASSES)):
+        assert r[tag]["bytes"] == cfg.n_layers * sum(r["classes"][c]["bytes"] for c in group)
+        assert r[tag]["us"] == pytest.approx(cfg.n_layers * sum(r["classes"][c]["us"] for c in group), rel=1e-3)
     (tmp_path / "r.json").write_text(json.dumps(res))
 
 
