@@ -240,8 +240,17 @@ __device__ inline float word_ssq(const u32x4 raw, bool ok, float acc) {
 // finished from the previous launch's split partials (Args::carry_in). Each workgroup builds only the slice of K its
 // columns read, [k0, k0 + kn), in LDS, and its sum of squares; the tile's
 // last arrival adds the slices' sums in split order for the input norm.
+//
+// The gate/up pair kernels may use up to half the register file per lane (at
+// most 2 waves per SIMD, i.e. two workgroups per CU at once, as many as the
+// library's pair plans place): left to its occupancy heuristics the compiler fits the pair without
+// the input norm into 135 registers, too few to keep both weight chunks of
+// U = 8 rows in flight, and that kernel then ran 25-35% slower than the same
+// pair with the norm (Qwen3-14B 45.3 against 34.1 us, Qwen3-32B 61.5 against
+// 45.7); with the bound both fit, and both run alike.
 template <int DT, int TH, int U, int G, bool NT, int NMAT, bool NORM, int CARRY>
-__global__ __launch_bounds__(kBlock) void nm_gemv_kernel(Args a) {
+__global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, NMAT == 2 ? 2 : 8)))
+void nm_gemv_kernel(Args a) {
   using E = Elem<DT>;
   typedef typename E::scalar T;
   constexpr int W = E::kWords;
