@@ -54,6 +54,18 @@ def _read(path):
     return list(csv.DictReader(open(path)))
 
 
+def gemv_args(name: str):
+    """The template arguments of an nm_gemv_kernel name, <dtype, TH, U, G, NT,
+    NMAT, NORM, CARRY>, as a dict (None for any other kernel)."""
+    if "nm_gemv_kernel<" not in name:
+        return None
+    a = name[name.index("nm_gemv_kernel<") + len("nm_gemv_kernel<"):]
+    a = [v.strip() for v in a[:a.index(">")].split(",")]
+    keys = ("dtype", "th", "u", "g", "nt", "nmat", "norm", "carry")
+    d = dict(zip(keys, a))
+    return {k: (v == "true" if k in ("nt", "norm") else int(v)) for k, v in d.items()}
+
+
 def _gemv_dispatches(rows):
     out = []
     for r in rows:
@@ -143,15 +155,15 @@ def stats(stats_csv, bench_json, md_path, cmd):
                      f"{float(r['MaxNs']) / 1e3:.2f} | {float(r['Percentage']):.1f}% |")
     if b:
         rf = b.get("roofline", {})
-        pair = [r for r in rows if ", true, 2, " in r["Name"]]
+        pair = [r for r in rows if (gemv_args(r["Name"]) or {}).get("nmat") == 2]
         lines += ["", f"Unprofiled `python bench.py` from the same call: value {b['value']} GB/s, ms_per_step "
                       f"{b['ms_per_step']}; dominant launch class: {rf.get('kernel')} at {rf.get('us_per_launch')} us "
                       f"per launch (HIP events over graph replays, {rf.get('achieved')} GB/s, frac {rf.get('frac')})."]
         for r in pair:
-            n = r["Name"]
-            if ", 2, true, " not in n:
+            g = gemv_args(r["Name"])
+            if not g["norm"]:
                 continue
-            what = "with a carried input" if ", 2, true, 0>" not in n else "with its own input"
+            what = "with a carried input" if g.get("carry") else "with its own input"
             lines.append(f"rocprof average kernel duration of the gate/up pair + RMSNorm kernel {what}: "
                          f"{float(r['AverageNs']) / 1e3:.2f} us over {r['Calls']} calls (the replay-timed figure also "
                          "includes the inter-kernel gap of the graph).")
@@ -165,18 +177,19 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
     rows = _read(stats_csv)
     d = json.loads(Path(decode_json).read_text())
     layers = CONFIGS[d["model"]].n_layers
-    pair = [r for r in rows if ", true, 2, " in r["Name"]]
+    pair = [r for r in rows if (gemv_args(r["Name"]) or {}).get("nmat") == 2]
     steps = sum(int(r["Calls"]) for r in pair) // layers  # one gate/up launch per layer and step
 
     def kind(r):
         n, per_step = r["Name"], int(r["Calls"]) / steps
         if per_step < 0.9:
             return None  # model set-up (random init, packing), not part of a step
-        if "nm_gemv_kernel" in n:
-            if ", true, 2, " in n:
+        g = gemv_args(n)
+        if g is not None:
+            if g["nmat"] == 2:
                 return "sparse GEMV: gate/up pair + RMSNorm + SiLU*mul"
-            # <dtype, TH, U, G, NT, NMAT, NORM, CARRY>: the input norm marks the q/k/v launch
-            return ("sparse GEMV: q/k/v + RMSNorm + RoPE + cache write" if ", 1, true, " in n
+            # the input norm marks the q/k/v launch
+            return ("sparse GEMV: q/k/v + RMSNorm + RoPE + cache write" if g["norm"]
                     else "sparse GEMV: o or down (+ residual, or partials left)")
         if n.startswith("Cijk_"):
             return "attention product (hipBLASLt)" if per_step > 1.5 else "lm_head (hipBLASLt, dense)"

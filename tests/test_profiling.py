@@ -137,7 +137,8 @@ def test_decode_stats_roles_per_step(tmp_path, setup_calls):
     kernels = [
         # the carried layer: every gate/up and all but the first q/k/v read a carried input
         ("void nm_hip::nm_gemv_kernel<0, 32, 4, 1, true, 2, true, 8>(nm_hip::Args)", ls, 23.0),
-        ("void nm_hip::nm_gemv_kernel<0, 16, 8, 4, true, 1, false, 0>(nm_hip::Args)", 2 * ls, 10.0),
+        ("void nm_hip::nm_gemv_kernel<0, 16, 8, 4, true, 1, false, 0>(nm_hip::Args)", ls, 10.0),  # down
+        ("void nm_hip::nm_gemv_kernel<0, 16, 8, 1, true, 1, false, 0>(nm_hip::Args)", ls, 10.0),  # o (G=1, NT)
         ("void nm_hip::nm_gemv_kernel<0, 32, 8, 1, true, 1, true, 8>(nm_hip::Args)", ls - steps, 9.5),
         ("void nm_hip::nm_gemv_kernel<0, 32, 8, 1, true, 1, true, 0>(nm_hip::Args)", steps, 9.5),
         ("Cijk_Alik_Bljk_HHS_MT256x16x32", ls, 8.0),
