@@ -2,7 +2,9 @@
 split-K partials live in the library's static device scratch. Its outputs must
 equal nm_gemv_launch's (same kernels, same plans) bit for bit, call after call
 on the shared scratch, the second call smaller than the first; the plain GEMV
-is also checked against the float64 oracle (max-abs 1e-2, rel-L2 1e-3)."""
+is also checked against the float64 oracle (max-abs 1e-2, rel-L2 1e-3), and a
+split-K carry producer / consumer pair runs through it as through the
+workspace entry point."""
 import ctypes
 
 import pytest
@@ -97,3 +99,44 @@ def test_static_entry_rejects_what_does_not_fit(gpu):
     assert rc == -9 and "static scratch" in _lib.strerror(rc)
     torch.cuda.synchronize()
     assert not o.any()
+
+
+def test_static_entry_carried_chain(gpu):
+    """o_proj as a split-K carry producer, then the gate/up pair finishing its
+    input from the partials, both through the static scratch: the finished
+    vector and the pair's output equal the workspace entry point's bit for bit
+    (the consumer's per-workgroup norm slots live in the scratch too)."""
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    g = torch.Generator(device="cuda").manual_seed(9)
+    y = torch.randn(1, 4096, generator=g, device="cuda").half()
+    x = torch.randn(1, 4096, generator=g, device="cuda").half()
+    ln = (torch.rand(4096, generator=g, device="cuda") + 0.5).half()
+    o = _case(4096, 4096, 32, 64, 21)
+    gate, up = _case(4096, 14336, 32, 64, 22), _case(4096, 14336, 32, 64, 23)
+    results = []
+    for static in (False, True):
+        say(f"carried chain through the {'static scratch' if static else 'workspace entry point'}")
+        prod = _desc(y, [o], [], 32, 64)
+        splits = ctypes.c_int()
+        _lib.check(lib.nm_gemv_launch_plan(ctypes.byref(prod), None, ctypes.byref(splits), None, None, None), "plan")
+        carry = torch.full((splits.value, 4096), float("nan"), device="cuda")
+        prod.carry_out = carry.data_ptr()
+        h = torch.full((1, 4096), float("nan"), dtype=torch.float16, device="cuda")
+        act = torch.full((1, 14336), float("nan"), dtype=torch.float16, device="cuda")
+        cons = _desc(x, [gate, up], [act], 32, 64, gate_up=True, norm=ln)
+        cons.carry_in, cons.carry_splits, cons.vec_out = carry.data_ptr(), splits.value, h.data_ptr()
+        for d in (prod, cons):
+            if static:
+                _lib.check(lib.nm_gemv_launch_static(ctypes.byref(d), stream), "nm_gemv_launch_static")
+            else:
+                need = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(d))
+                assert 0 < need <= _lib.NM_STATIC_SCRATCH_BYTES
+                ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+                _lib.check(lib.nm_gemv_launch(ctypes.byref(d), ws.data_ptr(), need, stream), "nm_gemv_launch")
+                torch.cuda.synchronize()
+                assert not ws[: _lib.NM_TICKET_BYTES].any()
+        torch.cuda.synchronize()
+        assert torch.isfinite(h.float()).all() and torch.isfinite(act.float()).all()
+        results.append((h, act))
+    assert torch.equal(results[0][0], results[1][0]) and torch.equal(results[0][1], results[1][1])
