@@ -568,7 +568,9 @@ class Decoder(nn.Module):
             return (type(mod).__name__, tuple(md.shape) if isinstance(md, torch.Tensor) else None)
 
         key = (dev, dt, len(self.layers),
-               tuple(shape(mod) for b in self.layers for mod in (b.self_attn.o_proj, b.mlp.down_proj, b.mlp.gate_proj)))
+               tuple(shape(mod) for b in self.layers for mod in (b.self_attn.q_proj, b.self_attn.k_proj,
+                                                                  b.self_attn.v_proj, b.self_attn.o_proj,
+                                                                  b.mlp.gate_proj, b.mlp.up_proj, b.mlp.down_proj)))
         if self._carry is not None and self._carry[0] == key:
             return
         if dev.type != "cuda" or not carry_supported(self.layers):

@@ -594,3 +594,28 @@ def test_sample_token_in_a_captured_graph_over_many_replays(gpu):
         if len(hot) == 2:
             se = (0.25 / n) ** 0.5
             assert abs(counts.get(hot[0], 0) / n - 0.5) <= 5 * se, counts
+
+
+def test_carry_is_chosen_only_where_the_plans_take_it():
+    """carry_supported (host-only planning, no kernel runs): the swapped tiny
+    decoder can carry o_proj's and down_proj's split-K sums into the next
+    launch; a dense decoder, a decoder whose layers differ in shape, and an
+    M that is not a multiple of 4 cannot. The buffers are only set up on a GPU
+    device (prepare_decode)."""
+    from spmv_decode_amd.decode.model import carry_supported
+
+    cfg = tiny_config()
+    dense = Decoder(cfg)
+    assert not carry_supported(dense.layers)
+    sparse = Decoder(cfg)
+    swap_to_nmsparse(sparse, 8, "cpu", seed=1, keep_dense=False)
+    assert carry_supported(sparse.layers)
+    odd = Decoder(cfg)
+    swap_to_nmsparse(odd, 8, "cpu", seed=1, keep_dense=False)
+    odd.layers[1].mlp.down_proj = NmSparseLinear.empty(cfg.dim, 2 * cfg.inter, 8, "cpu")
+    assert not carry_supported(odd.layers)
+    m2 = Decoder(cfg)
+    swap_to_nmsparse(m2, 2, "cpu", seed=1, keep_dense=False)  # 1:2, M = 2
+    assert not carry_supported(m2.layers)
+    sparse.setup_cache(16, "cpu", dtype=torch.float32)
+    assert sparse._carry is not None and sparse._carry[1] is None  # no carry buffers off the GPU
