@@ -7,8 +7,10 @@ microbench_triton_torchmv.py, re-designed for MI355X).
 Differences from the reference harness (microbench_triton_torchmv.py:218-364):
 * Weights are rotated over enough distinct copies (default >= 1 GiB) that
   every timed launch streams from HBM, not from the 256 MB Infinity Cache.
-* Launches are captured in a hipGraph and replayed; time per launch is the
-  replay time divided by the number of launches (HIP events on the stream).
+* Launches are captured in a hipGraph (the rotation repeated to >= 64
+  launches, as many as a decode step's graph holds) and replayed; time per
+  launch is the replay time divided by the number of launches (HIP events on
+  the stream).
 * `--sweep` times every kernel configuration and split count of the static
   table (the replacement for Triton autotuning, triton_spmv.py:40-55,
   122-148) and reports the fastest; the library's own choice is `cfg=-1`.
@@ -79,9 +81,17 @@ class RotatingCase:
                                          out=self.out, config_id=config_id, splits=splits)
 
 
-def graph_us_per_launch(launches, reps=20, warmup=3, stream=None, stats=False):
-    """Capture `launches` (callables) in one hipGraph; median replay time / len in
-    us (with stats=True: (median, sample stdev) over the `reps` replays)."""
+def graph_us_per_launch(launches, reps=20, warmup=3, stream=None, stats=False, min_launches=64):
+    """Capture `launches` (callables) in one hipGraph, the list repeated until
+    the graph holds at least `min_launches` launches; median replay time per
+    launch in us (with stats=True: (median, sample stdev) over the `reps`
+    replays). A replay's own fixed cost (the graph launch and its first
+    dispatch, a few us) is thereby spread over as many launches as in a decode
+    step's graph (128 GEMV launches for Llama-3.1-8B) instead of over a short
+    rotation (9 copies of the gate/up pair per GiB); repeating the rotation
+    keeps every copy's reuse distance >= the rotated bytes."""
+    launches = list(launches)
+    seq = launches * max(1, math.ceil(min_launches / len(launches)))
     stream = stream or torch.cuda.Stream()
     stream.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(stream):
@@ -91,7 +101,7 @@ def graph_us_per_launch(launches, reps=20, warmup=3, stream=None, stats=False):
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=stream):
-        for fn in launches:
+        for fn in seq:
             fn()
     for _ in range(warmup):
         g.replay()
@@ -103,7 +113,7 @@ def graph_us_per_launch(launches, reps=20, warmup=3, stream=None, stats=False):
         g.replay()
         e.record()
         e.synchronize()
-        samples.append(s.elapsed_time(e) * 1e3 / len(launches))
+        samples.append(s.elapsed_time(e) * 1e3 / len(seq))
     del g
     med = statistics.median(samples)
     if stats:
@@ -561,9 +571,9 @@ def write_decode_classes_md(model, res, path, cmd):
              "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
              f"The decoder's four launches per layer at {cfg.name}'s shapes (dim {cfg.dim}, intermediate "
              f"{cfg.inter}, {cfg.n_heads} query / {cfg.n_kv_heads} KV heads, head_dim {cfg.head_dim}), each",
-             "rotating over >= 1 GiB of distinct packed weights in one hipGraph (so neither L2 nor the 256 MB",
-             "Infinity Cache serves them), the library's default plan; median +- sd over the replays, per launch,",
-             "inter-kernel gap included. GB/s counts the algorithmic bytes of the launch (packed weights and index,",
+             "rotating over >= 1 GiB of distinct packed weights in one hipGraph of >= 64 launches (so neither L2 nor",
+             "the 256 MB Infinity Cache serves them), the library's default plan; median +- sd over the replays, per",
+             "launch, inter-kernel gap included. GB/s counts the algorithmic bytes of the launch (packed weights and index,",
              "activations once, norm weights, residual, outputs, RoPE row); % of the 8 TB/s HBM peak. 'Token' sums",
              f"one decode token's {4 * cfg.n_layers} launches ({cfg.n_layers} layers); 'carried' rows are the layer",
              "with the split-K carry (o and down leave their fp32 partials; gate/up and the next q/k/v finish",
@@ -690,8 +700,8 @@ def write_sweep_md(rows, path, cmd):
     """Markdown table of the library's own plan (`auto:` rows) per (shape, ratio)."""
     lines = ["# N:M sparse GEMV vs dense hipBLASLt per shape and ratio (MI355X, fp16, batch 1)", "",
              "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
-             "Each (shape, ratio) rotates over >= 1 GiB of distinct packed weights in one hipGraph (so neither L2 nor",
-             "the 256 MB Infinity Cache serves them); median and stdev over the timed replays, per launch, including",
+             "Each (shape, ratio) rotates over >= 1 GiB of distinct packed weights in one hipGraph of >= 64 launches",
+             "(so neither L2 nor the 256 MB Infinity Cache serves them); median and stdev over the timed replays, per launch, including",
              "the graph's inter-kernel gap. GB/s counts the algorithmic bytes 2*w*h + w + 2*K + 2*h (dense:",
              "2*K*h + 2*K + 2*h); % of the 8 TB/s HBM peak. Errors are against the fp32 dense matvec on the",
              "scattered masked weight (the reference microbenchmark's oracle). Dense = hipBLASLt in the faster of",

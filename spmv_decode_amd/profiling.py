@@ -158,15 +158,16 @@ def stats(stats_csv, bench_json, md_path, cmd):
         pair = [r for r in rows if (gemv_args(r["Name"]) or {}).get("nmat") == 2]
         lines += ["", f"Unprofiled `python bench.py` from the same call: value {b['value']} GB/s, ms_per_step "
                       f"{b['ms_per_step']}; dominant launch class: {rf.get('kernel')} at {rf.get('us_per_launch')} us "
-                      f"per launch (HIP events over graph replays, {rf.get('achieved')} GB/s, frac {rf.get('frac')})."]
+                      f"per launch (HIP events over replays of a graph of >= 64 of its launches, {rf.get('achieved')} "
+                      f"GB/s, frac {rf.get('frac')})."]
         for r in pair:
             g = gemv_args(r["Name"])
             if not g["norm"]:
                 continue
             what = "with a carried input" if g.get("carry") else "with its own input"
             lines.append(f"rocprof average kernel duration of the gate/up pair + RMSNorm kernel {what}: "
-                         f"{float(r['AverageNs']) / 1e3:.2f} us over {r['Calls']} calls (the replay-timed figure also "
-                         "includes the inter-kernel gap of the graph).")
+                         f"{float(r['AverageNs']) / 1e3:.2f} us over {r['Calls']} calls (the kernel alone, in the traced "
+                         "run; the replay-timed figure is the interval per launch in the untraced one, gap included).")
     Path(md_path).write_text("\n".join(lines) + "\n")
 
 
