@@ -189,7 +189,10 @@ int nm_num_gate_up_configs(void);
  *    the next launch): carry_out != NULL makes a producer, one plain GEMV
  *    (grouped kind, nprob 1, no norm, residual or heads; prob[0].out unused)
  *    that leaves its fp32 split partials [splits, h] in carry_out (splits as
- *    nm_gemv_launch_plan reports) and reduces nothing. carry_in != NULL makes
+ *    nm_gemv_launch_plan reports for the descriptor with carry_out set: with
+ *    no handoff to pay for, a producer whose default plan would leave a
+ *    quarter of the CUs idle takes 128-row tiles and more splits, at most 16)
+ *    and reduces nothing. carry_in != NULL makes
  *    a consumer (norm_weight required, 16-byte aligned; K = the producer's h;
  *    m a multiple of 4) whose
  *    input is x = round(sum over the carry_splits (<= 16) partials, in split
@@ -246,7 +249,7 @@ typedef struct nm_gemv_launch_desc {
 
 size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);
 /* The plan of such a launch (only the kind, counts, sizes, config_id,
- * splits and whether carry_in is set are read): configuration, splits,
+ * splits and whether carry_in and carry_out are set are read): configuration, splits,
  * workgroups, compressed rows per split and rows per chunk. */
 int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int* out_splits, int* out_blocks,
                         int* out_rows_per_split, int* out_chunk_rows);

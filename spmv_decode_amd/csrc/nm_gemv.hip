@@ -197,6 +197,35 @@ int make_plan(int nprob, const int* hs, int w, int nnz, int m, int nmat, int cfg
   return NM_OK;
 }
 
+// The plan of a launch described by `d`. A producer (carry_out: one GEMV whose
+// split-K reduction moves into the next launch) has no handoff, so more
+// splits cost it only the partials its consumer reads: where the default plan
+// would leave a quarter of the CUs or more idle (the Qwen3-14B / Qwen3-32B
+// o_proj: 20 tiles of 256 rows x 8 splits, 160 workgroups), it takes 128-row
+// tiles and the most splits (<= kMaxCarry) that fit one workgroup per CU
+// (sweeps: 7.13 -> 6.52 us and 9.28 -> 8.81 us, its consumer then reading 5
+// or 6 splits instead of 8). A consumer's plan puts whole groups of columns,
+// at most 512, in each split (the carried-input kernels cover gather slots 0
+// and 1).
+constexpr int kProducerConfig = 1;  // th16_u8: 128-row tiles, 128-row chunks
+
+int plan_desc(const nm_gemv_launch_desc& d, int nprob, const int* hs, int nmat, Plan* p) {
+  const bool carry_in = d.carry_in != nullptr;
+  int rc = make_plan(nprob, hs, d.w, d.nnz, d.m, nmat, d.config_id, d.splits, p, carry_in ? 2 * kBlock : kMaxRows,
+                     1, carry_in ? d.nnz : 1, carry_in);
+  const bool producer = d.carry_out != nullptr && nmat == 1 && nprob == 1 && !carry_in;
+  if (rc != NM_OK || !producer || d.config_id >= 0 || d.splits > 0 || p->blocks > kPlanCUs * 3 / 4) return rc;
+  for (int s = kMaxCarry; s >= 2; --s) {
+    Plan q;
+    if (make_plan(1, hs, d.w, d.nnz, d.m, 1, kProducerConfig, s, &q) == NM_OK && q.splits <= kMaxCarry &&
+        q.blocks <= kPlanCUs) {
+      if (q.blocks > p->blocks) *p = q;
+      break;
+    }
+  }
+  return NM_OK;
+}
+
 // Validate a launch descriptor, plan it and launch. Every entry point of the
 // C ABI goes through here. With `workspace_needed` it only plans (and reports
 // the workspace size); with `validate_only` it runs every check and returns
@@ -217,10 +246,7 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   if (carry_in && carry_out) return NM_ERR_BAD_EPILOGUE;
   if (d.nnz <= 0) return NM_ERR_BAD_SHAPE;
   Plan p;
-  // A consumer's plan: whole groups of columns per split, at most 512 (the
-  // carried-input kernels cover gather slots 0 and 1).
-  int rc = make_plan(nprob, hs, d.w, d.nnz, d.m, nmat, d.config_id, d.splits, &p, carry_in ? 2 * kBlock : kMaxRows,
-                     1, carry_in ? d.nnz : 1, carry_in);
+  int rc = plan_desc(d, nprob, hs, nmat, &p);
   if (rc != NM_OK) return rc;
   if (carry_in) {
     // The ssq slots follow the partials: one float per workgroup.
@@ -606,10 +632,8 @@ int nm_gemv_launch_plan(const nm_gemv_launch_desc* desc, int* out_config_id, int
   int hs[kMaxProblems];
   for (int i = 0; i < nprob; ++i) hs[i] = desc->prob[i].h;
   Plan p;
-  const bool carry_in = desc->carry_in != nullptr;
   if (desc->nnz <= 0) return NM_ERR_BAD_SHAPE;
-  const int rc = make_plan(nprob, hs, desc->w, desc->nnz, desc->m, pair ? 2 : 1, desc->config_id, desc->splits, &p,
-                           carry_in ? 2 * kBlock : kMaxRows, 1, carry_in ? desc->nnz : 1, carry_in);
+  const int rc = plan_desc(*desc, nprob, hs, pair ? 2 : 1, &p);
   if (rc != NM_OK) return rc;
   const Config& c = pair ? kDualConfigs[p.cfg] : kConfigs[p.cfg];
   if (out_config_id) *out_config_id = p.cfg;

@@ -321,14 +321,18 @@ class GemvProblem:
         self.residual, self.head_norm, self.rope, self.layout = residual, head_norm, bool(rope), layout
 
 
-def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1, splits=0, carried=False) -> dict:
+def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1, splits=0, carried=False,
+                producer=False) -> dict:
     """The library's plan for a launch over `problems` ((mat_data, mat_index)
     pairs): configuration, splits, grid, compressed rows per split and rows
     per chunk (the rows a workgroup streams first). `carried`: the plan of a
-    launch with a carried input (nmsparse_gemv_launch's carry_in)."""
+    launch with a carried input (nmsparse_gemv_launch's carry_in);
+    `producer`: of one that leaves its partials (carry_out)."""
     desc = _lib.NmGemvLaunchDesc()
     if carried:
         desc.carry_in = 16  # only its presence is read by the planner
+    if producer:
+        desc.carry_out = 16
     desc.dtype, desc.kind = _lib.NM_DTYPE_F16, _lib.NM_KIND_GATE_UP if gate_up else _lib.NM_KIND_GROUPED
     desc.nprob = len(problems)
     w = problems[0][0].shape[0]
@@ -456,7 +460,7 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
                 or carry_out.data_ptr() % 16):
             raise ValueError("carry_out must be a contiguous, 16-byte aligned fp32 tensor on vec.device")
         plan = launch_plan([(pr.mat_data, pr.mat_index) for pr in problems], BLOCK_WIDTH, VEC_WIDTH,
-                           gate_up=gate_up, config_id=config_id, splits=splits)
+                           gate_up=gate_up, config_id=config_id, splits=splits, producer=True)
         if carry_out.numel() != plan["splits"] * int(problems[0].mat_data.shape[1]):
             raise ValueError(f"carry_out holds {carry_out.numel()} floats, the producer leaves "
                              f"{plan['splits']} x {int(problems[0].mat_data.shape[1])}")
@@ -522,7 +526,7 @@ def nmsparse_gate_up_silu(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, *, out=None, no
 def carry_splits(mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH) -> int:
     """Split count of the plain GEMV `mat_data` as a producer: the rows of
     the fp32 [splits, h] partials buffer nmsparse_gemv_partials fills."""
-    return launch_plan([(mat_data, mat_index)], BLOCK_WIDTH, VEC_WIDTH)["splits"]
+    return launch_plan([(mat_data, mat_index)], BLOCK_WIDTH, VEC_WIDTH, producer=True)["splits"]
 
 
 def nmsparse_gemv_partials(vec, mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH, carry):

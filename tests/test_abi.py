@@ -372,3 +372,16 @@ def test_split_k_carry_rejections_and_plans_before_launch():
     # the Llama-3.1-8B q/k/v consumer keeps the plain plan
     qkv = [mats(4096, h) for h in (4096, 1024, 1024)]
     assert launch_plan(qkv, 32, 64, carried=True) == launch_plan(qkv, 32, 64)
+    # a producer whose plan would leave a quarter of the CUs idle takes 128-row tiles and more splits
+    # (Qwen3-14B / Qwen3-32B o_proj); the Llama-3.1-8B o_proj and every down_proj keep their plans
+    for K, h, nnz, m, want in ((5120, 5120, 32, 64, (1, 5, 200)), (8192, 5120, 16, 32, (1, 6, 240)),
+                               (4096, 4096, 32, 64, None), (14336, 4096, 32, 64, None), (17408, 5120, 32, 64, None)):
+        plain = launch_plan([mats(K, h, nnz, m)], nnz, m)
+        prod = launch_plan([mats(K, h, nnz, m)], nnz, m, producer=True)
+        got = (prod["config_id"], prod["splits"], prod["blocks"])
+        assert got == (want or (plain["config_id"], plain["splits"], plain["blocks"])), (K, h, plain, prod)
+        if want:
+            assert plain["blocks"] <= 192 < prod["blocks"] <= 256 and prod["splits"] <= 16
+    # explicit configurations and split counts are kept as asked
+    p = launch_plan([mats(5120, 5120)], 32, 64, producer=True, config_id=3, splits=8)
+    assert (p["config_id"], p["splits"], p["blocks"]) == (3, 8, 160)

@@ -44,15 +44,22 @@ def _finish_reference(y, md, mi, x, nnz, m, cfg=-1, splits=0):
 
 
 def _carry(y, md, mi, nnz, m, cfg=-1, splits=0):
-    plan = launch_plan([(md, mi)], nnz, m, config_id=cfg, splits=splits)
+    """The producer's partials and the (config, splits) request under which
+    the plain launch partitions the columns exactly as the producer did: the
+    request itself when explicit, else the producer's own plan (a producer may
+    plan differently from the plain launch), checked to re-plan identically."""
+    plan = launch_plan([(md, mi)], nnz, m, config_id=cfg, splits=splits, producer=True)
     carry = torch.empty(plan["splits"], md.shape[1], dtype=torch.float32, device="cuda")
     nmsparse_gemv_launch(y, [GemvProblem(md, mi)], nnz, m, config_id=cfg, splits=splits, carry_out=carry)
-    return carry
+    req = (cfg, splits) if (cfg, splits) != (-1, 0) else (plan["config_id"], plan["splits"])
+    again = launch_plan([(md, mi)], nnz, m, config_id=req[0], splits=req[1])
+    assert (again["config_id"], again["rows_per_split"]) == (plan["config_id"], plan["rows_per_split"]), (plan, again)
+    return carry, plan, req
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32], ids=str)
-@pytest.mark.parametrize("dim,inter,nnz,m", [(4096, 14336, 32, 64), (1024, 384, 2, 4), (2048, 1024, 128, 256)],
-                         ids=str)
+@pytest.mark.parametrize("dim,inter,nnz,m", [(4096, 14336, 32, 64), (1024, 384, 2, 4), (2048, 1024, 128, 256),
+                                             (5120, 17408, 32, 64)], ids=str)
 def test_gate_up_consumer_finishes_the_producer_bitwise(gpu, dim, inter, nnz, m, dtype):
     y, od, oi, x = _producer(dim, dim, nnz, m, dtype, seed=dim + nnz)
     _, gd, gi = make_case(dim, inter, nnz, m, seed=dim + 1, dtype=dtype)
@@ -61,8 +68,10 @@ def test_gate_up_consumer_finishes_the_producer_bitwise(gpu, dim, inter, nnz, m,
     # producer plans: the library's (8 splits), one split, and 11-12 splits of
     # 512-row tiles (the consumer kernel that reads up to 16)
     for pcfg, psplits in ((-1, 0), (-1, 1), (5, 12)):
-        ref_h = _finish_reference(y, od, oi, x, nnz, m, pcfg, psplits)
-        carry = _carry(y, od, oi, nnz, m, pcfg, psplits)
+        carry, plan, req = _carry(y, od, oi, nnz, m, pcfg, psplits)
+        ref_h = _finish_reference(y, od, oi, x, nnz, m, *req)
+        if dim == 5120 and pcfg < 0 and psplits == 0:  # the Qwen3-14B o_proj: a producer plan of its own
+            assert (plan["config_id"], plan["splits"], plan["blocks"]) == (1, 5, 200), plan
         if pcfg == 5:
             assert carry.shape[0] > 8
         xn = O.rms_norm_f64(ref_h.cpu().reshape(-1), lnw.cpu(), 1e-5)
@@ -93,8 +102,8 @@ def test_qkv_consumer_finishes_down_proj_bitwise(gpu, dim, inter, nh, kvh, nnz, 
     writes as the consumer; outputs against the float64 oracle."""
     hd = 128 if dim >= 4096 else 64
     act, dd, di, x = _producer(inter, dim, nnz, m, dtype, seed=inter + nnz)
-    ref_x = _finish_reference(act, dd, di, x, nnz, m)
-    carry = _carry(act, dd, di, nnz, m)
+    carry, _, req = _carry(act, dd, di, nnz, m)
+    ref_x = _finish_reference(act, dd, di, x, nnz, m, *req)
     g = torch.Generator(device="cuda").manual_seed(dim)
     q = make_case(dim, nh * hd, nnz, m, seed=7, dtype=dtype)[1:]
     k = make_case(dim, kvh * hd, nnz, m, seed=8, dtype=dtype)[1:]

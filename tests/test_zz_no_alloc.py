@@ -118,6 +118,7 @@ def test_static_entry_carried_chain(gpu):
     for static in (False, True):
         say(f"carried chain through the {'static scratch' if static else 'workspace entry point'}")
         prod = _desc(y, [o], [], 32, 64)
+        prod.carry_out = 16  # a producer's plan is asked for with carry_out set (only its presence is read)
         splits = ctypes.c_int()
         _lib.check(lib.nm_gemv_launch_plan(ctypes.byref(prod), None, ctypes.byref(splits), None, None, None), "plan")
         carry = torch.full((splits.value, 4096), float("nan"), device="cuda")
