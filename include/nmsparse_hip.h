@@ -197,7 +197,8 @@ int nm_num_gate_up_configs(void);
  *    m a multiple of 4) whose
  *    input is x = round(sum over the carry_splits (<= 16) partials, in split
  *    order, + vec): bit for bit what the producer with residual vec would
- *    have written. The consumer writes x to vec_out ([K], not vec) and
+ *    have written. The consumer writes x to vec_out ([K], apart from vec and
+ *    carry_in) and
  *    otherwise runs as with vec = x, except that the input norm's mean(x^2)
  *    is summed per split slice (a different fp32 summation order). Its plan
  *    puts whole groups of nnz columns, at most 512, spanning at most 1024

@@ -315,6 +315,10 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
       return NM_ERR_MISALIGNED;
     const uintptr_t vo = (uintptr_t)d.vec_out, vi = (uintptr_t)d.vec;
     if (vo < vi + (size_t)K * esize && vi < vo + (size_t)K * esize) return NM_ERR_BAD_EPILOGUE;  // overlap
+    // vec_out is written while other workgroups still read carry_in.
+    const uintptr_t ci = (uintptr_t)d.carry_in;
+    const size_t in_bytes = (size_t)d.carry_splits * (size_t)K * sizeof(float);
+    if (vo < ci + in_bytes && ci < vo + (size_t)K * esize) return NM_ERR_BAD_EPILOGUE;
   }
   if (validate_only) return NM_OK;
 

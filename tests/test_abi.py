@@ -334,6 +334,7 @@ def test_split_k_carry_rejections_and_plans_before_launch():
     assert _launch(_desc(**pair, **{**ok, "carry_splits": 17})) == -8
     assert _launch(_desc(**pair, **{**ok, "vec_out": None})) == -8
     assert _launch(_desc(**pair, **{**ok, "vec_out": FAKE})) == -8                  # overlaps vec
+    assert _launch(_desc(**pair, **{**ok, "carry_in": FAKE + 0x100000 - 16})) == -8  # vec_out inside carry_in
     assert _launch(_desc(**pair, **{**ok, "vec_out": FAKE + 0x100008})) == -5       # misaligned
     assert _launch(_desc(**pair, **{**ok, "carry_in": FAKE + 4})) == -5
     assert _launch(_desc(**{**pair, "norm_weight": FAKE + 2}, **ok)) == -5
