@@ -563,9 +563,11 @@ class Decoder(nn.Module):
         at, mlp = self.layers[0].self_attn, self.layers[0].mlp
         o, d = at.o_proj, mlp.down_proj
         dev, dt = self.q_pad.device, self.q_pad.dtype
-        def shape(mod):
-            md = getattr(mod, "mat_data", None)
-            return (type(mod).__name__, tuple(md.shape) if isinstance(md, torch.Tensor) else None)
+        def shape(mod):  # what the plans depend on: packed shapes and the N:M ratio
+            md, mi = getattr(mod, "mat_data", None), getattr(mod, "mat_index", None)
+            return (type(mod).__name__, tuple(md.shape) if isinstance(md, torch.Tensor) else None,
+                    tuple(mi.shape) if isinstance(mi, torch.Tensor) else None, getattr(mod, "block_width", None),
+                    getattr(mod, "vec_width", None))
 
         key = (dev, dt, len(self.layers),
                tuple(shape(mod) for b in self.layers for mod in (b.self_attn.q_proj, b.self_attn.k_proj,

@@ -619,3 +619,14 @@ def test_carry_is_chosen_only_where_the_plans_take_it():
     assert not carry_supported(m2.layers)
     sparse.setup_cache(16, "cpu", dtype=torch.float32)
     assert sparse._carry is not None and sparse._carry[1] is None  # no carry buffers off the GPU
+    # the buffers' key follows what the plans depend on: repacked as 2:4 instead of 4:8 (the packed
+    # weights keep their shapes at half density), the decision is taken again
+    key = sparse._carry[0]
+    for blk in sparse.layers:
+        for lin in (blk.self_attn.q_proj, blk.self_attn.k_proj, blk.self_attn.v_proj, blk.self_attn.o_proj,
+                    blk.mlp.gate_proj, blk.mlp.up_proj, blk.mlp.down_proj):
+            assert (lin.block_width, lin.vec_width) == (4, 8)
+            lin.block_width, lin.vec_width = 2, 4
+            lin.mat_index = lin.mat_index.reshape(-1, 2)
+    sparse.prepare_decode()
+    assert sparse._carry[0] != key
