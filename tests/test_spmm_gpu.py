@@ -143,3 +143,43 @@ def test_graph_capture_replays(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
         _ = spmm(X, md, mi, nnz, m)  # eager work between replays
+
+
+def test_split_k_handoff_soak_1000_replays(gpu):
+    """The SpMM publishes its partials with agent-scope atomic stores (the GEMV
+    with atomic swaps) and orders them by hardware completion (vmcnt wait, a
+    returning agent-scope ticket add, agent-scope loads after it). A rare
+    visibility miss would show as a wrong sum, not a fault, so: batch 8 gate
+    (448 workgroups), batch 8 down (256) and batch 4 q/o at the Llama-3.1-8B
+    shapes (8 splits each) in one hipGraph, replayed 1000 times; every replay
+    bitwise equal to the per-row GEMV (swap handoff) of the same plan, checked
+    after each replay, stopping at the first mismatch."""
+    cases = []
+    for i, (K, h, batch) in enumerate(((4096, 14336, 8), (14336, 4096, 8), (4096, 4096, 4))):
+        _, md, mi = make_case(K, h, 32, 64, seed=40 + i)
+        X = torch.randn(batch, K, device="cuda").half()
+        p = _lib.spmm_plan(batch, h, md.shape[0], 32, 64)
+        assert p["splits"] == 8, p
+        ref = torch.cat([run(X[b:b + 1], md, mi, 32, 64, config_id=p["config_id"], splits=p["splits"])
+                         for b in range(batch)])
+        cases.append((X, md, mi, torch.empty(batch, h, dtype=torch.float16, device="cuda"), ref))
+
+    def launches():
+        for X, md, mi, out, _ in cases:
+            spmm(X, md, mi, 32, 64, out=out)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        launches()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            launches()
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(1000):
+        g.replay()
+        torch.cuda.synchronize()
+        for k, (_, _, _, out, ref) in enumerate(cases):
+            if not torch.equal(out, ref.view(out.shape)):
+                pytest.fail(f"replay {rep}: case {k} differs from the per-row GEMV")
