@@ -364,15 +364,18 @@ def main():
             result["roofline"]["traffic"] = t.get("bytes_per_launch")
     result["per_shape_sparse"] = per_shape
 
-    # ---- batch > 1: the small-batch SpMM, per row vs the batch-1 GEMV ---------
+    # ---- batch > 1: the small-batch SpMM (up to 8 rows) and the matrix-core
+    #      SpMM (16-64 rows, one launch plus its activation gather), per row vs
+    #      the batch-1 GEMV ------------------------------------------------------
     spmm = {}
     for cls in ("q_o", "gate_up", "down"):
         K, h = SHAPES[classes[cls][0]]
         b1 = per_shape[cls]["us_per_launch"]
         rows = {}
-        for batch in (2, 4, 8):
+        for batch in (2, 4, 8, 16, 32, 64):
             us = MB.time_spmm(h, K, nnz, m, batch, reps=reps)
-            rows[str(batch)] = {"us_per_launch": round(us, 3), "us_per_row": round(us / batch, 3),
+            rows[str(batch)] = {"kernel": "small-batch" if batch <= 8 else "matrix-core",
+                                "us_per_launch": round(us, 3), "us_per_row": round(us / batch, 3),
                                 "speedup_per_row_vs_batch1": round(b1 * batch / us, 3),
                                 "weight_GBps": round(sparse_bytes(K, h, nnz, m) / (us * 1e-6) / 1e9, 1)}
             log(f"spmm {cls:8s} batch {batch}: {us:7.2f} us/launch, {us / batch:6.2f} us/row "

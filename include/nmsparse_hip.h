@@ -300,6 +300,29 @@ int nm_spmm_plan(int batch, int h, int w, int nnz, int m, int config_id, int spl
                  int* out_splits, int* out_blocks, int* out_rows_per_block);
 
 /*
+ * Matrix-core SpMM: the same product for 1 <= batch <= NM_MC_MAX_BATCH rows
+ * in one pass over the packed weights, fp16 and bf16 only
+ * (v_mfma_f32_16x16x32_f16 / _bf16: fp32 accumulation, one rounding to the
+ * element type at the end, like nm_spmm; the order of the sums differs, so
+ * rows are not bit-identical to nm_gemv_ex). Meant for more than
+ * NM_MAX_BATCH rows (prefill chunks, batched serving), where nm_spmm needs a
+ * launch per 8 rows. x rows x_row_stride >= K elements apart, out rows
+ * out_row_stride >= h apart; mat_data and out 16-byte aligned, workspace
+ * 256-byte aligned with zeroed arrival counters (as nm_gemv_ex).
+ * config_id: 0..2 (output tiles of 64, 128, 256 columns) or < 0 for the
+ * library's choice; splits <= 0 likewise. No reference counterpart (the
+ * reference op rejects rows != 1, src/spmv/nmsparse_op.py:83-86, and its
+ * module runs them through a dense F.linear, src/spmv/nmsparse_linear.py:62-68).
+ */
+#define NM_MC_MAX_BATCH 64
+size_t nm_spmm_mc_workspace_bytes(int batch, int h, int w, int nnz, int m, int config_id, int splits);
+int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
+               const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace,
+               size_t workspace_bytes, int h, int w, int nnz, int m, int config_id, int splits, void* stream);
+int nm_spmm_mc_plan(int batch, int h, int w, int nnz, int m, int config_id, int splits, int* out_config_id,
+                    int* out_splits, int* out_blocks, int* out_rows_per_block);
+
+/*
  * Configuration introspection. nm_config_describe writes a short text such as
  * "th32_u8" into buf (ids nm_num_configs() + j describe pair configuration j);
  * nm_gemv_plan reports the configuration and split count the library would

@@ -28,6 +28,7 @@ NM_ERR = {
 }
 NM_KIND_GROUPED, NM_KIND_GATE_UP = 0, 1
 NM_MAX_BATCH = 8
+NM_MC_MAX_BATCH = 64
 NM_STATIC_SCRATCH_BYTES = NM_TICKET_BYTES + (16 << 20)
 
 _vp = ctypes.c_void_p
@@ -79,6 +80,9 @@ ABI = {
     "nm_spmm_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "nm_spmm": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_spmm_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
+    "nm_spmm_mc_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
+    "nm_spmm_mc": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
+    "nm_spmm_mc_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_config_describe": (_i, [_i, ctypes.c_char_p, _i]),
     "nm_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_strerror": (ctypes.c_char_p, [_i]),
@@ -149,6 +153,19 @@ def spmm_plan(batch: int, h: int, w: int, nnz: int, m: int, config_id: int = -1,
     check(rc, "nm_spmm_plan")
     return {"config_id": cfg.value, "splits": sp.value, "blocks": blocks.value, "rows_per_split": rows.value,
             "config": describe(cfg.value)}
+
+
+MC_CONFIGS = ("mc_h64", "mc_h128", "mc_h256")  # matrix-core SpMM: output tile columns
+
+
+def spmm_mc_plan(batch: int, h: int, w: int, nnz: int, m: int, config_id: int = -1, splits: int = 0) -> dict:
+    """Configuration, split count, grid size and rows per split of a matrix-core SpMM launch."""
+    cfg, sp, blocks, rows = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = load().nm_spmm_mc_plan(batch, h, w, nnz, m, config_id, splits, ctypes.byref(cfg), ctypes.byref(sp),
+                                ctypes.byref(blocks), ctypes.byref(rows))
+    check(rc, "nm_spmm_mc_plan")
+    return {"config_id": cfg.value, "splits": sp.value, "blocks": blocks.value, "rows_per_split": rows.value,
+            "config": MC_CONFIGS[cfg.value]}
 
 
 def describe(config_id: int) -> str:

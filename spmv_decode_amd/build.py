@@ -4,8 +4,8 @@
 
 The library is a plain C-ABI shared object (include/nmsparse_hip.h) compiled
 by hipcc from spmv_decode_amd/csrc/: nm_gemv.hip (host side and C ABI) and
-nm_gemv_inst.hip once per element type (the kernels), compiled in parallel
-and linked; nothing links against torch.
+nm_gemv_inst.hip once per element type (the kernels) and nm_spmm_mc.hip (the
+matrix-core SpMM), compiled in parallel and linked; nothing links against torch.
 """
 from __future__ import annotations
 
@@ -21,7 +21,8 @@ PKG = Path(__file__).resolve().parent
 ROOT = PKG.parent
 CSRC = PKG / "csrc"
 # (source, extra defines): the host side, then the kernels of each element type.
-UNITS = [(CSRC / "nm_gemv.hip", []), *[(CSRC / "nm_gemv_inst.hip", [f"-DNM_INST_DTYPE={dt}"]) for dt in (0, 1, 2)]]
+UNITS = [(CSRC / "nm_gemv.hip", []), *[(CSRC / "nm_gemv_inst.hip", [f"-DNM_INST_DTYPE={dt}"]) for dt in (0, 1, 2)],
+         (CSRC / "nm_spmm_mc.hip", [])]
 LIB_PATH = PKG / "libnmsparse_hip.so"
 # Measurement-only streaming-read kernel used by the microbenchmark.
 PROBE_SOURCES = [PKG / "csrc" / "roofline_probe.hip"]

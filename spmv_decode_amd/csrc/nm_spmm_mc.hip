@@ -1,0 +1,414 @@
+// nm_spmm_mc.hip — the matrix-core SpMM: out[b, :] = W x[b, :] for
+// NM_MAX_BATCH < batch <= NM_MC_MAX_BATCH activation rows (prefill chunks,
+// batched serving) over the shared-mask N:M packed weights, fp16 and bf16,
+// on gfx950's v_mfma_f32_16x16x32_{f16,bf16}. The C ABI (nm_spmm_mc*) is
+// declared in include/nmsparse_hip.h.
+//
+// out[b, r] = RNE_T( sum_c f32(mat_data[c, r]) * f32(x[b, (c/nnz)*m + mat_index[c]]) )
+//
+// is the GEMM out = Xg W of the gathered activations Xg[b, c] (batch x w)
+// and the packed weights W = mat_data (w x h): the shared mask makes the
+// gather one index per compressed column for every row. Past 8 rows the
+// small-batch SpMM's FMAs (rows x 8 per 16-B weight word) and its one launch
+// per 8 rows dominate; here each weight word is read from HBM once per
+// launch and multiplied on the matrix cores for all rows.
+//
+//  * A first kernel gathers the activations once per call, Xg[b, c] =
+//    x[b, (c/nnz)*m + mat_index[c]], into the workspace ([batch, wp], wp = w
+//    rounded up to whole 64-column chunks, zero past w).
+//  * The main kernel: a workgroup (256 lanes = 4 wave64) owns an output tile
+//    of HT columns r and all BT >= batch rows (16, 32 or 64), over one split
+//    of the compressed columns c. The 4 waves split the tile into BT/16 row
+//    blocks x 64/BT column ranges (each activation row block is loaded by
+//    as few waves as possible); a wave keeps its 16 rows x HT*BT/64 columns
+//    as 16 x 16 fp32 accumulator blocks in registers. Chunks of 64 compressed columns (two
+//    MFMA K steps): the weight rows [64 x HT] are loaded 16 B per lane
+//    (non-temporal) and staged through LDS, two buffers; the activation
+//    operands come straight from Xg, 16 B per lane and row block. Two chunks
+//    are in flight in registers while one is multiplied.
+//  * MFMA operands: the activation block is K-contiguous in Xg; the weight
+//    block, stored with the outputs contiguous, is read transposed with
+//    ds_read_b64_tr_b16 (lane l of a 16-lane group receives element l of
+//    each of the 4 rows the group addresses, 4 consecutive elements per lane).
+//  * Split-K as the small-batch SpMM: partials [split, batch, h] published
+//    with agent-scope atomic stores, an agent-scope arrival counter per tile,
+//    the last arrival sums the partials in split order and rounds to T.
+//    Deterministic for a given plan; not bit-identical to the GEMV (the
+//    matrix core's dot products have their own order).
+#include "nm_gemv_kernel.h"
+
+namespace nm_hip {
+namespace {
+
+constexpr int kMcCK = 64;         // compressed columns per chunk: two MFMA K steps of 32
+constexpr int kMcNumConfigs = 3;  // output tile HT = 64, 128, 256
+static_assert(NM_MC_MAX_BATCH == 64, "batch tiles of 16, 32 and 64 rows");
+
+typedef short s4 __attribute__((ext_vector_type(4)));
+typedef short s8 __attribute__((ext_vector_type(8)));
+typedef float f4 __attribute__((ext_vector_type(4)));
+typedef _Float16 h8 __attribute__((ext_vector_type(8)));
+typedef __bf16 b8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) s4 lds_s4;
+
+template <int DT>
+__device__ inline f4 mfma16x16x32(s8 a, s8 b, f4 c);
+template <>
+__device__ inline f4 mfma16x16x32<NM_DTYPE_F16>(s8 a, s8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(h8, a), __builtin_bit_cast(h8, b), c, 0, 0, 0);
+}
+template <>
+__device__ inline f4 mfma16x16x32<NM_DTYPE_BF16>(s8 a, s8 b, f4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(b8, a), __builtin_bit_cast(b8, b), c, 0, 0, 0);
+}
+
+// MFMA 16x16x32 register layout (gfx950; checked on the GPU): A[16 x 32]:
+// lane l holds row l % 16, K elements 8*(l/16) .. +7; B[32 x 16]: column
+// l % 16, K elements 8*(l/16) .. +7; D[16 x 16]: column l % 16, rows
+// 4*(l/16) .. +3.
+template <int DT, int BT, int HT>
+__global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
+  using E = Elem<DT>;
+  typedef typename E::scalar T;  // 16-bit storage
+  constexpr int WM = BT / 16;               // waves along the rows (one 16-row block each)
+  constexpr int WN = 4 / WM;                // waves along the output columns
+  constexpr int MB = 1;                     // 16-row blocks per wave
+  constexpr int NW = HT / WN;               // output columns per wave
+  constexpr int NBK = NW / 16;              // 16-column blocks per wave
+  constexpr int LPR = HT / 8;               // lanes per weight row (16 B each)
+  constexpr int RPI = kBlock / LPR;         // weight rows per load
+  constexpr int NI = kMcCK / RPI;           // weight loads per lane per chunk
+  constexpr int WSTR = HT + 16;             // LDS weight row stride (elements)
+  constexpr int KS = kMcCK / 32;            // MFMA K steps per chunk
+  static_assert(NBK >= 1 && NI >= 1 && RPI * NI == kMcCK, "tile shape");
+
+  __shared__ __attribute__((aligned(16))) T ws[2][kMcCK * WSTR];
+  __shared__ int is_last;
+
+  const int h = a.h;
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6;
+  const int rb = 16 * (wave % WM);  // the wave's first batch row
+  const int cb = NW * (wave / WM);  // the wave's first column within the tile
+  const int lg = (tid & 63) >> 4;
+  const int li = tid & 15;
+  const int tile = (int)blockIdx.x % a.tiles;
+  const int split = (int)blockIdx.x / a.tiles;
+  const int c0 = split * a.rows_per_split;
+  const int cw = min(a.rows_per_split, a.w - c0);
+  const int nch = (cw + kMcCK - 1) / kMcCK;  // c0 + nch * kMcCK <= wp (rows_per_split: whole chunks)
+
+  // Weight rows: lane tid loads 16 B of row wrow + i * RPI of each chunk
+  // (rows past the split re-read its last row and are zeroed in LDS;
+  // columns past h read the last 8 columns and feed only outputs >= h).
+  const T* __restrict__ md = static_cast<const T*>(a.mat_data);
+  const int wrow = tid / LPR;
+  const int wcol = (tid % LPR) * 8;
+  const int gcol = min(tile * HT + wcol, h - 8);
+  auto load_w = [&](u32x4 (&dst)[NI], int k) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const int r = c0 + min(k * kMcCK + wrow + i * RPI, cw - 1);
+      dst[i] = load16<true>(reinterpret_cast<const u32x4*>(md + (size_t)r * (size_t)h + gcol));
+    }
+  };
+  // Gathered activations (row-major [batch, wp], zero past w): the A
+  // operand of the wave's row block is 16 B of row rb + li at column 8*lg of
+  // the chunk, loaded straight into registers (rows past the batch read its last
+  // row: they feed only outputs that are not written).
+  const T* __restrict__ xg = static_cast<const T*>(a.x);
+  auto load_a = [&](u32x4 (&dst)[MB][KS], int k) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks)
+        dst[mb][ks] = *reinterpret_cast<const u32x4*>(
+            xg + (size_t)min(rb + 16 * mb + li, a.batch - 1) * (size_t)a.x_row_stride +
+            (size_t)(c0 + k * kMcCK + 32 * ks + 8 * lg));
+  };
+  u32x4 wA[NI], wB[NI], aA[MB][KS], aB[MB][KS];
+  load_w(wA, 0);
+  load_a(aA, 0);
+  load_w(wB, min(1, nch - 1));
+  load_a(aB, min(1, nch - 1));
+
+  auto store = [&](const u32x4 (&wr)[NI], int k, int buf) {
+#pragma unroll
+    for (int i = 0; i < NI; ++i) {
+      const bool ok = k * kMcCK + wrow + i * RPI < cw;
+      *reinterpret_cast<u32x4*>(&ws[buf][(wrow + i * RPI) * WSTR + wcol]) = ok ? wr[i] : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+
+  f4 acc[MB][NBK];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb) acc[mb][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  auto compute = [&](const u32x4 (&af)[MB][KS], int buf) {
+#pragma unroll
+    for (int ks = 0; ks < KS; ++ks)
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb) {
+        // Lane t of group lg addresses row 32*ks + 8*lg + t/4 (then + 4),
+        // columns n0 + 4*(t%4) .. +3; it receives column n0 + t of the
+        // group's rows.
+        const T* p = &ws[buf][(32 * ks + 8 * lg + (li >> 2)) * WSTR + cb + 16 * nb + 4 * (li & 3)];
+        const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)p);
+        const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s4*)(p + 4 * WSTR));
+        const s8 bf = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+          acc[mb][nb] = mfma16x16x32<DT>(__builtin_bit_cast(s8, af[mb][ks]), bf, acc[mb][nb]);
+      }
+  };
+
+  // Buffer b holds chunk k (k % 2 == b); the barrier after each store also
+  // orders the previous reads of the other buffer before its next store.
+  // Loads past the split's last chunk re-read it (never used).
+  for (int k = 0; k < nch; k += 2) {
+    store(wA, k, 0);
+    __syncthreads();
+    u32x4 a0[MB][KS];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) a0[mb][ks] = aA[mb][ks];
+    load_w(wA, min(k + 2, nch - 1));
+    load_a(aA, min(k + 2, nch - 1));
+    compute(a0, 0);
+    if (k + 1 < nch) {
+      store(wB, k + 1, 1);
+      __syncthreads();
+      u32x4 a1[MB][KS];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int ks = 0; ks < KS; ++ks) a1[mb][ks] = aB[mb][ks];
+      load_w(wB, min(k + 3, nch - 1));
+      load_a(aB, min(k + 3, nch - 1));
+      compute(a1, 1);
+    }
+  }
+
+  // acc[mb][nb][j]: batch row rb + 16*mb + 4*lg + j, output column
+  // tile*HT + cb + 16*nb + li.
+  const int rcol = tile * HT + cb + li;
+  if (a.splits > 1) {
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const int b = rb + 16 * mb + 4 * lg + j;
+          const int r = rcol + 16 * nb;
+          if (b < a.batch && r < h)
+            __hip_atomic_store(a.partial + ((size_t)split * (size_t)a.batch + (size_t)b) * (size_t)h + r,
+                               acc[mb][nb][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
+    if (tid == 0) {
+      const uint32_t prev = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED,
+                                                   __HIP_MEMORY_SCOPE_AGENT);
+      is_last = (prev == (uint32_t)(a.splits - 1)) ? 1 : 0;
+    }
+    __syncthreads();
+    if (!is_last) return;
+    // Every split's partials of the lane's outputs, one split per round trip,
+    // summed in split order (clamped addresses for outputs that are unused).
+    const size_t step = (size_t)a.batch * (size_t)h;
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[mb][nb][j] = 0.0f;
+    for (int sp = 0; sp < a.splits; ++sp) {
+      const float* ps = a.partial + (size_t)sp * step;
+      float t[MB][NBK][4];
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+            t[mb][nb][j] = __hip_atomic_load(ps + (size_t)min(rb + 16 * mb + 4 * lg + j, a.batch - 1) * (size_t)h +
+                                                 min(rcol + 16 * nb, h - 1),
+                                             __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j) acc[mb][nb][j] += t[mb][nb][j];
+    }
+  }
+
+  T* __restrict__ out = static_cast<T*>(a.out);
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int b = rb + 16 * mb + 4 * lg + j;
+        const int r = rcol + 16 * nb;
+        if (b < a.batch && r < h) out[(long long)b * a.out_row_stride + r] = E::from_f32(acc[mb][nb][j]);
+      }
+  if (a.splits > 1 && tid == 0) {
+    __hip_atomic_store(&a.tickets[tile], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
+}
+
+// The gathered activations: xg[b, c] = x[b, (c/nnz)*m + mat_index[c]] for
+// c < w, zero for positions outside x and for w <= c < wp (rows wp apart).
+template <typename T>
+__global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const T* __restrict__ x, long long x_row_stride,
+                                                            int batch, const uint8_t* __restrict__ mat_index, int w,
+                                                            int wp, int nnz, int m, int K, T* __restrict__ xg) {
+  const long long i = (long long)blockIdx.x * kBlock + threadIdx.x;
+  if (i >= (long long)batch * wp) return;
+  const int b = (int)(i / wp);
+  const int c = (int)(i % wp);
+  T v = T(0);
+  if (c < w) {
+    const int p = (c / nnz) * m + (int)mat_index[c];
+    if (p < K) v = x[(long long)b * x_row_stride + p];
+  }
+  xg[i] = v;
+}
+
+typedef void (*McFn)(SpmmArgs);
+
+// fn[config: HT = 64, 128, 256][batch tile: 16, 32, 64 rows]
+#define NM_MC_ROW(DT, HT) {&nm_spmm_mc_kernel<DT, 16, HT>, &nm_spmm_mc_kernel<DT, 32, HT>, &nm_spmm_mc_kernel<DT, 64, HT>}
+const McFn kMcKernelsF16[kMcNumConfigs][3] = {NM_MC_ROW(NM_DTYPE_F16, 64), NM_MC_ROW(NM_DTYPE_F16, 128),
+                                              NM_MC_ROW(NM_DTYPE_F16, 256)};
+const McFn kMcKernelsBF16[kMcNumConfigs][3] = {NM_MC_ROW(NM_DTYPE_BF16, 64), NM_MC_ROW(NM_DTYPE_BF16, 128),
+                                               NM_MC_ROW(NM_DTYPE_BF16, 256)};
+#undef NM_MC_ROW
+
+constexpr int kMcTileCols[kMcNumConfigs] = {64, 128, 256};
+constexpr int kMcCUs = 256;  // MI355X compute units; split counts aim at about this many workgroups
+
+inline int ceil_div_mc(int a, int b) { return (a + b - 1) / b; }
+
+struct McPlan {
+  int cfg, splits, rows, tiles, blocks, wp;
+  size_t xg_off, workspace;
+};
+
+// Plan (from sweeps at the Llama-3.1-8B and Qwen3-14B shapes, 16-64 rows):
+// cfg < 0 takes 64-column tiles above 32 rows or up to 4096 outputs, 128
+// otherwise; splits <= 0 the fewest that give about one workgroup per CU and
+// at most 1024 columns per split, at most 8 (the partials grow with the
+// rows); each split whole chunks of 64 columns. Workspace: arrival counters, the partials
+// [splits, batch, h] fp32 when splits > 1, then the gathered activations
+// [batch, wp] (wp = w rounded up to whole chunks).
+int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, McPlan* p) {
+  if (batch < 1 || batch > NM_MC_MAX_BATCH) return NM_ERR_BAD_SHAPE;
+  if (h <= 0 || w <= 0 || nnz <= 0 || m <= 0 || m > 256 || nnz > m) return NM_ERR_BAD_SHAPE;
+  if (h % 128 != 0) return NM_ERR_H_NOT_MULTIPLE_128;
+  if (w % nnz != 0) return NM_ERR_W_NOT_MULTIPLE_NNZ;
+  if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
+  if (cfg < 0) cfg = (batch > 32 || h <= 4096) ? 0 : 1;
+  if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
+  const int HT = kMcTileCols[cfg];
+  const int tiles = ceil_div_mc(h, HT);
+  const int wp = ceil_div_mc(w, kMcCK) * kMcCK;
+  if (splits <= 0) {
+    splits = ceil_div_mc(kMcCUs, tiles);
+    if (splits < ceil_div_mc(w, 1024)) splits = ceil_div_mc(w, 1024);
+    if (splits > 8) splits = 8;
+  }
+  if (splits > wp / kMcCK) splits = wp / kMcCK;
+  const int rows = ceil_div_mc(ceil_div_mc(w, splits), kMcCK) * kMcCK;
+  splits = ceil_div_mc(w, rows);
+  if (tiles > kMaxTickets || (long long)tiles * splits > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
+  p->cfg = cfg;
+  p->splits = splits;
+  p->rows = rows;
+  p->tiles = tiles;
+  p->blocks = tiles * splits;
+  p->wp = wp;
+  const size_t part = splits > 1 ? (size_t)splits * (size_t)batch * (size_t)h * sizeof(float) : (size_t)0;
+  p->xg_off = ((size_t)NM_TICKET_BYTES + part + 255) / 256 * 256;
+  p->workspace = p->xg_off + (size_t)batch * (size_t)wp * 2;
+  return NM_OK;
+}
+
+}  // namespace
+}  // namespace nm_hip
+
+using namespace nm_hip;
+
+extern "C" {
+
+size_t nm_spmm_mc_workspace_bytes(int batch, int h, int w, int nnz, int m, int config_id, int splits) {
+  McPlan p;
+  return make_mc_plan(batch, h, w, nnz, m, config_id, splits, &p) == NM_OK ? p.workspace : 0;
+}
+
+int nm_spmm_mc_plan(int batch, int h, int w, int nnz, int m, int config_id, int splits, int* out_config_id,
+                    int* out_splits, int* out_blocks, int* out_rows_per_block) {
+  McPlan p;
+  const int rc = make_mc_plan(batch, h, w, nnz, m, config_id, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (out_config_id) *out_config_id = p.cfg;
+  if (out_splits) *out_splits = p.splits;
+  if (out_blocks) *out_blocks = p.blocks;
+  if (out_rows_per_block) *out_rows_per_block = p.rows;
+  return NM_OK;
+}
+
+int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
+               const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace, size_t workspace_bytes,
+               int h, int w, int nnz, int m, int config_id, int splits, void* stream) {
+  if (dtype != NM_DTYPE_F16 && dtype != NM_DTYPE_BF16) return NM_ERR_BAD_CONFIG;
+  McPlan p;
+  const int rc = make_mc_plan(batch, h, w, nnz, m, config_id, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (!x || !mat_data || !mat_index || !out || !workspace) return NM_ERR_NULL_POINTER;
+  const long long K = (long long)(w / nnz) * (long long)m;
+  if (x_row_stride < K || out_row_stride < h) return NM_ERR_BAD_SHAPE;
+  if (((uintptr_t)mat_data & 15u) != 0 || ((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
+  if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* xg = static_cast<char*>(workspace) + p.xg_off;
+  const long long gathered = (long long)batch * (long long)p.wp;
+  const unsigned gblocks = (unsigned)((gathered + kBlock - 1) / kBlock);
+  hipLaunchKernelGGL(nm_gather_mc_kernel<uint16_t>, dim3(gblocks), dim3(kBlock), 0, st,
+                     static_cast<const uint16_t*>(x), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K,
+                     static_cast<uint16_t*>(xg));  // both element types are 16-bit: a copy of bits
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  SpmmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = xg;
+  a.x_row_stride = p.wp;
+  a.mat_data = mat_data;
+  a.mat_index = mat_index;
+  a.out = out;
+  a.out_row_stride = out_row_stride;
+  a.tickets = static_cast<uint32_t*>(workspace);
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + NM_TICKET_BYTES);
+  a.batch = batch;
+  a.h = h;
+  a.tiles = p.tiles;
+  a.w = w;
+  a.nnz = nnz;
+  a.m = m;
+  a.K = (int)K;
+  a.splits = p.splits;
+  a.rows_per_split = p.rows;
+  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : 2);
+  const McFn fn = (dtype == NM_DTYPE_F16 ? kMcKernelsF16 : kMcKernelsBF16)[p.cfg][bt];
+  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, a);
+  e = hipGetLastError();
+  return e == hipSuccess ? NM_OK : (int)e;
+}
+
+}  // extern "C"

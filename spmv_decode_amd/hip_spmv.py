@@ -233,15 +233,24 @@ def _aligned(md):
 
 
 def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1,
-                              splits=0):
+                              splits=0, matrix_cores=None):
     """out[..., r, :] = W_sparse @ x[..., r, :] for every row of x ([..., rows, K]),
-    NM_MAX_BATCH rows per launch, each launch streaming the packed weights once.
+    each launch streaming the packed weights once.
 
     Same layout and limits as nmsparse_spmv_forward_hip; rows may be any
     number >= 1. Returns [..., rows, h] in x.dtype (or writes `out`, a
-    contiguous tensor of that shape). With the same config_id and splits,
-    each row equals the batch-1 GEMV of that row bit for bit when at most 1024
-    compressed columns fall in a split (see _lib.spmm_plan).
+    contiguous tensor of that shape).
+
+    Two kernels: the small-batch SpMM (NM_MAX_BATCH rows per launch; with
+    the same config_id and splits each row equals the batch-1 GEMV of that
+    row bit for bit when at most 1024 compressed columns fall in a split, see
+    _lib.spmm_plan) and, for fp16 / bf16, the matrix-core SpMM
+    (NM_MC_MAX_BATCH rows per launch; fp32 accumulation in the matrix cores'
+    own order, see _lib.spmm_mc_plan). matrix_cores=None takes the matrix
+    cores for more than NM_MAX_BATCH rows of a 16-bit type when config_id
+    and splits are left to the library, else the small-batch kernel;
+    True / False forces one kernel (True needs fp16 or bf16). config_id and
+    splits are those of the kernel that runs.
     """
     if not (x.is_cuda and mat_data.is_cuda and mat_index.is_cuda):
         raise ValueError("x, mat_data, and mat_index must be GPU (HIP) tensors")
@@ -274,10 +283,18 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
         raise ValueError(f"out must be a contiguous, 16-byte aligned {(*lead, h)} tensor of x.dtype")
     if rows == 0:
         return out
+    sixteen = x.dtype in (torch.float16, torch.bfloat16)
+    if matrix_cores is None:
+        matrix_cores = sixteen and rows > _lib.NM_MAX_BATCH and config_id < 0 and splits <= 0
+    elif matrix_cores and not sixteen:
+        raise TypeError("the matrix-core SpMM takes fp16 or bf16")
     md = _aligned(mat_data)
     lib = _lib.load()
-    nb = min(rows, _lib.NM_MAX_BATCH)
-    need = lib.nm_spmm_workspace_bytes(nb, h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
+    if matrix_cores:
+        per, fn, ws_fn, name = _lib.NM_MC_MAX_BATCH, lib.nm_spmm_mc, lib.nm_spmm_mc_workspace_bytes, "nm_spmm_mc"
+    else:
+        per, fn, ws_fn, name = _lib.NM_MAX_BATCH, lib.nm_spmm, lib.nm_spmm_workspace_bytes, "nm_spmm"
+    need = ws_fn(min(rows, per), h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
     if need == 0:
         raise ValueError("spmm shape outside what libnmsparse_hip supports")
     o2d = out.view(rows, h)
@@ -286,12 +303,12 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     with torch.cuda.device(device):
         stream = torch.cuda.current_stream(device).cuda_stream
         ws = workspace_for(device, need, stream)
-        for r0 in range(0, rows, _lib.NM_MAX_BATCH):
-            b = min(_lib.NM_MAX_BATCH, rows - r0)
-            rc = lib.nm_spmm(_DTYPE_CODE[x.dtype], x2d.data_ptr() + r0 * K * esize, K, b, md.data_ptr(),
-                             mat_index.data_ptr(), o2d.data_ptr() + r0 * h * esize, h, ws.data_ptr(), ws.numel(),
-                             h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits), stream)
-            _lib.check(rc, "nm_spmm")
+        for r0 in range(0, rows, per):
+            b = min(per, rows - r0)
+            rc = fn(_DTYPE_CODE[x.dtype], x2d.data_ptr() + r0 * K * esize, K, b, md.data_ptr(), mat_index.data_ptr(),
+                    o2d.data_ptr() + r0 * h * esize, h, ws.data_ptr(), ws.numel(), h, w, BLOCK_WIDTH, VEC_WIDTH,
+                    int(config_id), int(splits), stream)
+            _lib.check(rc, name)
     return out
 
 

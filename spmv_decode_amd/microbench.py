@@ -318,7 +318,8 @@ CARRIED_CLASSES = ("qkv_decode_carried", "o_partials", "gate_up_pair_norm_carrie
 
 
 def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60) -> float:
-    """us per small-batch SpMM launch of `batch` rows, weights rotated."""
+    """us per SpMM call of `batch` rows (the library's kernel choice: the
+    small-batch SpMM up to 8 rows, the matrix-core SpMM above), weights rotated."""
     from .hip_spmv import nmsparse_spmm_forward_hip
 
     case = RotatingCase(n_out, n_in, nnz, m, rotate_bytes=rotate_bytes, seed=seed)

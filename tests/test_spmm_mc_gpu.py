@@ -1,0 +1,134 @@
+"""GPU parity of the matrix-core SpMM (nm_spmm_mc: 9-64 rows per launch,
+fp16 / bf16) against the oracle, at the Llama-3.1-8B and Qwen3 shapes, on
+ragged shapes (a last chunk shorter than 32 columns, a last tile past h,
+positions outside x), every configuration and split count, strided rows
+through the C ABI, graph replay and the automatic routing."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import say
+from spmv_decode_amd import _lib, hip_spmv, nmsparse_linear
+from test_gemv_gpu import make_case
+from test_spmm_gpu import check_rows
+
+pytestmark = pytest.mark.gpu
+
+
+def mc(X, md, mi, nnz, m, **kw):
+    w, h = md.shape
+    return hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, h, nnz, m, matrix_cores=True, **kw)
+
+
+@pytest.mark.parametrize("batch", [9, 16, 24, 33, 64])
+@pytest.mark.parametrize("shape", [(4096, 14336), (14336, 4096), (4096, 4096), (4096, 1024)], ids=str)
+def test_llama_shapes_default_plan(gpu, shape, batch):
+    K, h = shape
+    _, md, mi = make_case(K, h, 32, 64, seed=K + h + batch)
+    X = torch.randn(batch, K, generator=torch.Generator(device="cuda").manual_seed(batch), device="cuda").half()
+    say(f"spmm_mc {shape} batch {batch} plan {_lib.spmm_mc_plan(batch, h, md.shape[0], 32, 64)}")
+    check_rows(mc(X, md, mi, 32, 64), X, md, mi, 32, 64, f"{shape} b{batch}")
+
+
+@pytest.mark.parametrize("shape", [(5120, 17408), (17408, 5120), (5120, 25600), (25600, 5120)], ids=str)
+def test_qwen3_shapes(gpu, shape):
+    K, h = shape
+    _, md, mi = make_case(K, h, 16, 32, seed=K * 3 + h)
+    X = torch.randn(40, K, generator=torch.Generator(device="cuda").manual_seed(h), device="cuda").half()
+    say(f"spmm_mc qwen3 {shape} plan {_lib.spmm_mc_plan(40, h, md.shape[0], 16, 32)}")
+    check_rows(mc(X, md, mi, 16, 32), X, md, mi, 16, 32, f"{shape}")
+
+
+# (K, h, nnz, m): w = (K/m)*nnz of 8, 9, 500, 1024, 2800 and 6144 columns, h an odd multiple of 128.
+RAGGED = [(16, 128, 2, 4), (12, 384, 3, 4), (1000, 384, 4, 8), (4096, 1280, 1, 4), (7168, 2176, 5, 7),
+          (24576, 640, 2, 8)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+def test_ragged_shapes_configs_and_splits(gpu, dtype):
+    for K, h, nnz, m in RAGGED:
+        _, md, mi = make_case(K, h, nnz, m, seed=K + 5 * h, dtype=dtype)
+        w = md.shape[0]
+        for batch in (9, 17, 40, 64):
+            X = torch.randn(batch, K, device="cuda").to(dtype)
+            for cfg, splits in ((-1, 0), (0, 1), (1, 3), (2, 2), (2, 0), (0, 64)):
+                p = _lib.spmm_mc_plan(batch, h, w, nnz, m, cfg, splits)
+                say(f"spmm_mc {dtype} K{K} h{h} {nnz}:{m} batch {batch} cfg {cfg} splits {splits} -> {p}")
+                check_rows(mc(X, md, mi, nnz, m, config_id=cfg, splits=splits), X, md, mi, nnz, m,
+                           f"{dtype} {K}x{h} {nnz}:{m} b{batch} cfg{cfg} s{splits}")
+
+
+def test_more_than_64_rows_and_determinism(gpu):
+    K, h = 4096, 4096
+    _, md, mi = make_case(K, h, 32, 64, seed=77)
+    X = torch.randn(150, K, device="cuda").half()
+    say("spmm_mc 150 rows")
+    y = mc(X, md, mi, 32, 64)
+    check_rows(y, X, md, mi, 32, 64, "150 rows")
+    for _ in range(3):
+        assert torch.equal(mc(X, md, mi, 32, 64), y)
+    # the first 64 rows are one launch of their own: the same bits alone
+    assert torch.equal(mc(X[:64].contiguous(), md, mi, 32, 64), y[:64])
+
+
+def test_c_abi_row_strides(gpu):
+    """x and out with padded rows through the C ABI directly."""
+    K, h, nnz, m, B = 4096, 4096, 32, 64, 20
+    _, md, mi = make_case(K, h, nnz, m, seed=6)
+    xs, os_ = K + 64, h + 128
+    Xp = torch.randn(B, xs, device="cuda").half()
+    outp = torch.full((B, os_), 7.0, device="cuda").half()
+    lib = _lib.load()
+    need = lib.nm_spmm_mc_workspace_bytes(B, h, md.shape[0], nnz, m, -1, 0)
+    ws = torch.zeros(need, dtype=torch.uint8, device="cuda")
+    say("spmm_mc strided rows")
+    rc = lib.nm_spmm_mc(0, Xp.data_ptr(), xs, B, md.data_ptr(), mi.data_ptr(), outp.data_ptr(), os_, ws.data_ptr(),
+                        need, h, md.shape[0], nnz, m, -1, 0, torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "nm_spmm_mc")
+    torch.cuda.synchronize()
+    check_rows(outp[:, :h].contiguous(), Xp[:, :K].contiguous(), md, mi, nnz, m, "strided")
+    assert bool((outp[:, h:] == 7.0).all())  # padding untouched
+    with pytest.raises(_lib.NmSparseLibraryError):  # fp32 has no matrix-core path
+        _lib.check(lib.nm_spmm_mc(2, Xp.data_ptr(), xs, B, md.data_ptr(), mi.data_ptr(), outp.data_ptr(), os_,
+                                  ws.data_ptr(), need, h, md.shape[0], nnz, m, -1, 0, 0), "nm_spmm_mc")
+
+
+def test_auto_routing_and_module(gpu):
+    K, h = 2048, 1024
+    _, md, mi = make_case(K, h, 16, 32, seed=9)
+    w = md.shape[0]
+    X = torch.randn(12, K, device="cuda").half()
+    auto = hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, h, 16, 32)
+    assert torch.equal(auto, mc(X, md, mi, 16, 32))  # > 8 rows of fp16: the matrix cores
+    valu = hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, h, 16, 32, matrix_cores=False)
+    check_rows(valu, X, md, mi, 16, 32, "valu 12 rows")
+    lin = nmsparse_linear.NmSparseLinear(1024, 2048, 16, 3, "cuda", init="device")
+    x = torch.randn(2, 30, 2048, device="cuda").half()
+    say("module 60 rows")
+    y = lin(x)
+    check_rows(y.reshape(-1, 1024), x.reshape(-1, 2048), lin.mat_data, lin.mat_index, 8, 16, "module 60 rows")
+    with pytest.raises(TypeError):
+        mc(X.float(), md.float(), mi, 16, 32)
+
+
+def test_graph_capture_replays(gpu):
+    K, h, nnz, m = 4096, 14336, 32, 64
+    _, md, mi = make_case(K, h, nnz, m, seed=10)
+    X = torch.randn(48, K, device="cuda").half()
+    eager = mc(X, md, mi, nnz, m)
+    out = torch.empty_like(eager)
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        mc(X, md, mi, nnz, m, out=out)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            mc(X, md, mi, nnz, m, out=out)
+    torch.cuda.current_stream().wait_stream(s)
+    for rep in range(4):
+        out.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, eager), rep
+        _ = mc(X, md, mi, nnz, m)  # eager work between replays
