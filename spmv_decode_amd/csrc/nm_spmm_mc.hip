@@ -264,21 +264,33 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
 }
 
 // The gathered activations: xg[b, c] = x[b, (c/nnz)*m + mat_index[c]] for
-// c < w, zero for positions outside x and for w <= c < wp (rows wp apart).
-template <typename T>
-__global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const T* __restrict__ x, long long x_row_stride,
+// c < w, zero for positions outside x and for w <= c < wp (rows wp apart,
+// wp a multiple of 8). Lane i writes 8 consecutive columns of one row as one
+// 16-B store.
+__global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __restrict__ x, long long x_row_stride,
                                                             int batch, const uint8_t* __restrict__ mat_index, int w,
-                                                            int wp, int nnz, int m, int K, T* __restrict__ xg) {
+                                                            int wp, int nnz, int m, int K, uint16_t* __restrict__ xg) {
   const long long i = (long long)blockIdx.x * kBlock + threadIdx.x;
-  if (i >= (long long)batch * wp) return;
-  const int b = (int)(i / wp);
-  const int c = (int)(i % wp);
-  T v = T(0);
-  if (c < w) {
-    const int p = (c / nnz) * m + (int)mat_index[c];
-    if (p < K) v = x[(long long)b * x_row_stride + p];
+  const int per_row = wp / 8;
+  if (i >= (long long)batch * per_row) return;
+  const int b = (int)(i / per_row);
+  const int c0 = (int)(i % per_row) * 8;
+  const uint16_t* __restrict__ xr = x + (long long)b * x_row_stride;
+  uint16_t v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const int c = c0 + e;
+    const int cc = c < w ? c : w - 1;  // clamped: the load stays in range
+    const int p = (cc / nnz) * m + (int)mat_index[cc];
+    const uint16_t t = xr[p < K ? p : 0];
+    v[e] = (c < w && p < K) ? t : (uint16_t)0;
   }
-  xg[i] = v;
+  u32x4 word;
+  word.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
+  word.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
+  word.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
+  word.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
+  *reinterpret_cast<u32x4*>(xg + (long long)b * wp + c0) = word;
 }
 
 typedef void (*McFn)(SpmmArgs);
@@ -378,11 +390,11 @@ int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, cons
   if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* xg = static_cast<char*>(workspace) + p.xg_off;
-  const long long gathered = (long long)batch * (long long)p.wp;
+  const long long gathered = (long long)batch * (long long)(p.wp / 8);
   const unsigned gblocks = (unsigned)((gathered + kBlock - 1) / kBlock);
-  hipLaunchKernelGGL(nm_gather_mc_kernel<uint16_t>, dim3(gblocks), dim3(kBlock), 0, st,
+  hipLaunchKernelGGL(nm_gather_mc_kernel, dim3(gblocks), dim3(kBlock), 0, st,
                      static_cast<const uint16_t*>(x), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K,
-                     static_cast<uint16_t*>(xg));  // both element types are 16-bit: a copy of bits
+                     static_cast<uint16_t*>(xg));  // fp16 and bf16 alike: a copy of 16-bit words
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   SpmmArgs a;
