@@ -270,11 +270,11 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
 __global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __restrict__ x, long long x_row_stride,
                                                             int batch, const uint8_t* __restrict__ mat_index, int w,
                                                             int wp, int nnz, int m, int K, uint16_t* __restrict__ xg) {
-  const long long i = (long long)blockIdx.x * kBlock + threadIdx.x;
-  const int per_row = wp / 8;
-  if (i >= (long long)batch * per_row) return;
-  const int b = (int)(i / per_row);
-  const int c0 = (int)(i % per_row) * 8;
+  const int per_row = wp / 8;  // batch * per_row < 2^31 (host)
+  const int i = (int)blockIdx.x * kBlock + (int)threadIdx.x;
+  if (i >= batch * per_row) return;
+  const int b = i / per_row;
+  const int c0 = (i - b * per_row) * 8;
   const uint16_t* __restrict__ xr = x + (long long)b * x_row_stride;
   uint16_t v[8];
 #pragma unroll
@@ -326,6 +326,7 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   if (h % 128 != 0) return NM_ERR_H_NOT_MULTIPLE_128;
   if (w % nnz != 0) return NM_ERR_W_NOT_MULTIPLE_NNZ;
   if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
+  if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   if (cfg < 0) cfg = (batch > 32 || h <= 4096) ? 0 : 1;
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
   const int HT = kMcTileCols[cfg];
