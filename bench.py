@@ -479,6 +479,34 @@ def decode_ms_per_token(m, log):
             model.forward_step = eager
             torch._dynamo.reset()
 
+    def prefill_ms(model, reps=10):
+        """The prompt's GPU time in one Decoder.prefill pass (every Linear over its 128 rows: hipBLASLt for
+        the dense model, the sparse model's SpMM on the matrix cores in launches of 64 rows), captured as a
+        hipGraph after an eager warm-up; median of reps replays."""
+        from spmv_decode_amd.decode.runner import cache_length
+
+        model.setup_cache(cache_length(prompt.numel() + 1), torch.device("cuda"), dtype=torch.float16)
+        ids = prompt.cuda()
+        st = torch.cuda.Stream()
+        st.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(st):
+            model.prefill(ids)
+        torch.cuda.current_stream().wait_stream(st)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=st):
+            model.prefill(ids)
+        times = []
+        for _ in range(reps):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            g.replay()
+            b.record()
+            b.synchronize()
+            times.append(a.elapsed_time(b))
+        del g
+        return round(sorted(times)[len(times) // 2], 4)
+
     dense_by_fusion, forms, fixed_dense, fixed_dense_c = {}, {}, {}, {}
     for mode in ("qkv", "none", "qkv_gate_up"):  # "qkv": the reference's dense model (model.py:198 wqkv)
         model.set_dense_fusion(mode)
@@ -488,8 +516,12 @@ def decode_ms_per_token(m, log):
         fixed_dense_c[mode] = compiled_fixed(model, fixed_dense[mode])
     model.set_dense_fusion("none")
     dense = dense_by_fusion["qkv"]
+    prefill_dense = prefill_ms(model)
     swap_to_nmsparse(model, m, "cuda", seed=0, init="device", keep_dense=False)
     torch.cuda.empty_cache()
+    prefill_sparse = prefill_ms(model)
+    log(f"prefill of the {prompt.numel()}-token prompt in one pass: dense {prefill_dense} ms, "
+        f"sparse {prefill_sparse} ms ({prefill_dense / prefill_sparse:.3f}x)")
     sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)
     fixed_sparse = fixed_context_ms(model, 512)
     fixed_sparse_c = compiled_fixed(model, fixed_sparse)
@@ -512,6 +544,11 @@ def decode_ms_per_token(m, log):
         return _finite(a / b)
 
     out = {"model": "llama-3.1-8b (random init)", "prompt": 128, "gen": 256,
+           "prefill_one_pass": {"dense_ms": prefill_dense, "sparse_ms": prefill_sparse,
+                                "speedup_sparse_vs_dense": ratio(prefill_dense, prefill_sparse),
+                                "what": "the 128-token prompt through Decoder.prefill as one hipGraph: every "
+                                        "Linear over 128 rows (dense: hipBLASLt; sparse: the matrix-core SpMM, "
+                                        "two launches of 64 rows each), causal attention in PyTorch"},
            "dense_ms_per_token": dense["ms_per_token"], "sparse_ms_per_token": sparse["ms_per_token"],
            "dense_launches": "q/k/v fused into one GEMM (the reference's dense model), gate/up/o/down one each; "
                              "each shape in the faster of hipBLASLt's x*W^T and W*x forms",

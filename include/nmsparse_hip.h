@@ -323,6 +323,17 @@ int nm_spmm_mc_plan(int batch, int h, int w, int nnz, int m, int config_id, int 
                     int* out_splits, int* out_blocks, int* out_rows_per_block);
 
 /*
+ * The gathered activations alone: out[r, c] = x[r, (c/nnz)*m + mat_index[c]]
+ * for c < w, zero for out_row_stride > c >= w (fp16 / bf16; out 16-byte
+ * aligned, out_row_stride a multiple of 8 and >= w rounded up to 8). With
+ * it, more rows than NM_MC_MAX_BATCH are a plain GEMM of out [rows, w] and
+ * mat_data [w, h] for a BLAS library (the Python layer uses hipBLASLt
+ * through torch.matmul). No reference counterpart.
+ */
+int nm_gather_columns(int dtype, const void* x, long long x_row_stride, int rows, const uint8_t* mat_index, int w,
+                      int nnz, int m, void* out, long long out_row_stride, void* stream);
+
+/*
  * Configuration introspection. nm_config_describe writes a short text such as
  * "th32_u8" into buf (ids nm_num_configs() + j describe pair configuration j);
  * nm_gemv_plan reports the configuration and split count the library would

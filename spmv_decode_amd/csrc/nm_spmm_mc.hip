@@ -377,6 +377,26 @@ int nm_spmm_mc_plan(int batch, int h, int w, int nnz, int m, int config_id, int 
   return NM_OK;
 }
 
+int nm_gather_columns(int dtype, const void* x, long long x_row_stride, int rows, const uint8_t* mat_index, int w,
+                      int nnz, int m, void* out, long long out_row_stride, void* stream) {
+  if (dtype != NM_DTYPE_F16 && dtype != NM_DTYPE_BF16) return NM_ERR_BAD_CONFIG;
+  if (rows < 1 || w <= 0 || nnz <= 0 || m <= 0 || m > 256 || nnz > m || w % nnz != 0) return NM_ERR_BAD_SHAPE;
+  if (!x || !mat_index || !out) return NM_ERR_NULL_POINTER;
+  const long long K = (long long)(w / nnz) * (long long)m;
+  const long long wp = ((long long)w + 7) / 8 * 8;
+  if (K > 0x7fffffffLL || x_row_stride < K || out_row_stride < wp || out_row_stride % 8 != 0 ||
+      out_row_stride > 0x7fffffffLL || (long long)rows * (out_row_stride / 8) > 0x7fffffffLL)
+    return NM_ERR_BAD_SHAPE;
+  if (((uintptr_t)out & 15u) != 0) return NM_ERR_MISALIGNED;
+  // rows of out_row_stride elements: every column past w is written as zero
+  const long long lanes = (long long)rows * (out_row_stride / 8);
+  hipLaunchKernelGGL(nm_gather_mc_kernel, dim3((unsigned)((lanes + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+                     static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), x_row_stride, rows,
+                     mat_index, w, (int)out_row_stride, nnz, m, (int)K, static_cast<uint16_t*>(out));
+  const hipError_t e = hipGetLastError();
+  return e == hipSuccess ? NM_OK : (int)e;
+}
+
 int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
                const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace, size_t workspace_bytes,
                int h, int w, int nnz, int m, int config_id, int splits, void* stream) {

@@ -193,6 +193,36 @@ def project(lin: nn.Module, x: torch.Tensor) -> torch.Tensor:
     return lin(x)
 
 
+def project_rows(lin: nn.Module, x2d: torch.Tensor) -> torch.Tensor:
+    """lin(x) for every row of x2d [rows, K] -> [rows, h]: an NmSparseLinear
+    through the SpMM on its packed weights (the small-batch kernel up to 8
+    rows, the matrix-core kernel above for fp16 / bf16), even when it also
+    holds a dense weight; any other module through its own forward."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    if isinstance(lin, NmSparseLinear):
+        from ..hip_spmv import nmsparse_spmm_forward_hip
+
+        return nmsparse_spmm_forward_hip(x2d, lin.mat_data, lin.mat_index, lin.w, lin.h, lin.block_width,
+                                         lin.vec_width)
+    return lin(x2d)
+
+
+def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n_kv_heads: int) -> torch.Tensor:
+    """softmax(q kᵀ / sqrt(d) + causal mask) v over P positions, grouped query
+    heads: q [P, n_heads, d], k and v [P, kv_heads, d] -> [P, n_heads * d].
+    Scores in fp32 (every operand contiguous before each batched product)."""
+    P, nh, d = q.shape
+    g = nh // n_kv_heads
+    qh = q.transpose(0, 1).float().contiguous()                                # [nh, P, d]
+    kt = k.permute(1, 2, 0).float().repeat_interleave(g, 0).contiguous()       # [nh, d, P]
+    vh = v.transpose(0, 1).float().repeat_interleave(g, 0).contiguous()        # [nh, P, d]
+    scores = torch.bmm(qh, kt) * (1.0 / math.sqrt(d))
+    mask = torch.ones(P, P, dtype=torch.bool, device=q.device).triu(1)
+    probs = torch.softmax(scores.masked_fill(mask, float("-inf")), dim=-1)
+    return torch.bmm(probs, vh).transpose(0, 1).reshape(P, nh * d).to(q.dtype)
+
+
 def grouped_sparse(mods) -> bool:
     """True when every module is an NmSparseLinear with the same w and N:M, so
     they can share one launch (grouped GEMV, or the gate/up pair)."""
@@ -592,6 +622,40 @@ class Decoder(nn.Module):
         self.k_store[:, :, :self.cfg.head_dim].zero_()
         for v in self.v_cache_t:
             v.zero_()
+
+    @torch.no_grad()
+    def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
+        """The prompt in one pass: tokens [P] int64 at positions 0 .. P-1 on
+        the device. Every Linear sees all P rows (sparse ones through the SpMM:
+        project_rows), causal attention over the prompt in PyTorch
+        (causal_attention), keys and values written to the static caches at
+        positions 0 .. P-1 as the decode steps write them. Returns the logits
+        of position P-1 [1, vocab]; decoding continues at position P (each
+        step rewrites the mask rows itself)."""
+        c = self.cfg
+        ids = tokens.view(-1)
+        P = ids.numel()
+        if P < 1 or P > self.max_seq:
+            raise ValueError(f"prompt of {P} tokens for a cache of {self.max_seq} positions")
+        hd = c.head_dim
+        x = self.embed_tokens(ids)  # [P, dim]
+        freqs = self.rope[:P].view(P, 1, -1)
+        for i, blk in enumerate(self.layers):
+            at, mlp = blk.self_attn, blk.mlp
+            h = blk.input_layernorm(x)
+            q = project_rows(at.q_proj, h).view(P, c.n_heads, hd)
+            k = project_rows(at.k_proj, h).view(P, c.n_kv_heads, hd)
+            v = project_rows(at.v_proj, h).view(P, c.n_kv_heads, hd)
+            if c.qk_norm:
+                q, k = at.q_norm(q), at.k_norm(k)
+            q, k = rotate(q, freqs), rotate(k, freqs)
+            self.k_cache_t[i][:, :hd, :P].copy_(k.permute(1, 2, 0))
+            self.v_cache_t[i][:, :, :P].copy_(v.permute(1, 2, 0))
+            x = x + project_rows(at.o_proj, causal_attention(q, k, v, c.n_kv_heads))
+            h = blk.post_attention_layernorm(x)
+            act = F.silu(project_rows(mlp.gate_proj, h)) * project_rows(mlp.up_proj, h)
+            x = x + project_rows(mlp.down_proj, act)
+        return project(self.lm_head, self.norm(x[-1:].view(1, 1, -1))).view(1, -1)
 
     def forward_step(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:
         """One decode step: token [1, 1] int64 and pos [1] int64 on the device

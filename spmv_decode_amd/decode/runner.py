@@ -203,12 +203,24 @@ class GraphDecoder:
         self.graph.replay()
 
     @torch.no_grad()
-    def run_prompt(self, prompt_ids: torch.Tensor):
-        """Feed prompt tokens one step at a time (untimed). After the last one
-        `token` holds the first generated token."""
+    def run_prompt(self, prompt_ids: torch.Tensor, batched: bool = False):
+        """Feed the prompt (untimed): one step per token, or with batched=True
+        all tokens in one Decoder.prefill pass. After it `token` holds the
+        first generated token and `pos` the prompt length."""
         ids = prompt_ids.to(self.device).view(-1)
         self.reset(int(0))
         self.tokens[0] = ids[0]
+        if batched:
+            self._advance(ids.numel())
+            logits = self.model.prefill(ids)
+            if self.graph is not None:  # self.logits is the captured step's output buffer: keep it
+                self.logits.copy_(logits)
+            else:
+                self.logits = logits
+            nxt = greedy_token(logits, out=self.token.view(1))
+            self.tokens[ids.numel():ids.numel() + 1].copy_(nxt)
+            self.pos.fill_(ids.numel())
+            return
         for i in range(ids.numel()):
             self.token.copy_(ids[i].view(1, 1))
             self.replay() if self.graph is not None else self.eager_step()

@@ -247,10 +247,14 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     _lib.spmm_plan) and, for fp16 / bf16, the matrix-core SpMM
     (NM_MC_MAX_BATCH rows per launch; fp32 accumulation in the matrix cores'
     own order, see _lib.spmm_mc_plan). matrix_cores=None takes the matrix
-    cores for more than NM_MAX_BATCH rows of a 16-bit type when config_id
-    and splits are left to the library, else the small-batch kernel;
-    True / False forces one kernel (True needs fp16 or bf16). config_id and
-    splits are those of the kernel that runs.
+    cores for NM_MAX_BATCH < rows <= NM_MC_MAX_BATCH of a 16-bit type when
+    config_id and splits are left to the library, and beyond that the
+    gathered activations (nm_gather_columns, [rows, w]) times mat_data as one
+    hipBLASLt GEMM (torch.matmul: a plain GEMM over half the input width,
+    faster than launches of 64 rows on the matrix-core kernel); else the
+    small-batch kernel. True / False forces one of the two HIP kernels (True
+    needs fp16 or bf16). config_id and splits are those of the kernel that
+    runs.
     """
     if not (x.is_cuda and mat_data.is_cuda and mat_index.is_cuda):
         raise ValueError("x, mat_data, and mat_index must be GPU (HIP) tensors")
@@ -284,12 +288,24 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     if rows == 0:
         return out
     sixteen = x.dtype in (torch.float16, torch.bfloat16)
+    library_gemm = False
     if matrix_cores is None:
         matrix_cores = sixteen and rows > _lib.NM_MAX_BATCH and config_id < 0 and splits <= 0
+        library_gemm = matrix_cores and rows > _lib.NM_MC_MAX_BATCH
     elif matrix_cores and not sixteen:
         raise TypeError("the matrix-core SpMM takes fp16 or bf16")
     md = _aligned(mat_data)
     lib = _lib.load()
+    if library_gemm:
+        wp = (w + 7) // 8 * 8
+        with torch.cuda.device(x.device):
+            xg = torch.empty(rows, wp, dtype=x.dtype, device=x.device)
+            rc = lib.nm_gather_columns(_DTYPE_CODE[x.dtype], x2d.data_ptr(), K, rows, mat_index.data_ptr(), w,
+                                       BLOCK_WIDTH, VEC_WIDTH, xg.data_ptr(), wp,
+                                       torch.cuda.current_stream(x.device).cuda_stream)
+            _lib.check(rc, "nm_gather_columns")
+            torch.matmul(xg[:, :w], md, out=out.view(rows, h))
+        return out
     if matrix_cores:
         per, fn, ws_fn, name = _lib.NM_MC_MAX_BATCH, lib.nm_spmm_mc, lib.nm_spmm_mc_workspace_bytes, "nm_spmm_mc"
     else:

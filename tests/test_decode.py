@@ -92,6 +92,37 @@ def test_cached_decode_matches_full_sequence_reference(qk_norm):
     torch.testing.assert_close(torch.stack(got), ref, rtol=1e-4, atol=1e-4)
 
 
+@pytest.mark.parametrize("qk_norm", [False, True])
+def test_prefill_matches_full_sequence_reference_and_steps(qk_norm):
+    """Decoder.prefill (the prompt in one pass) against the independent
+    full-sequence reference at the last position; its caches equal the ones
+    the per-token steps write; the step after it gives the same logits."""
+    torch.manual_seed(0)
+    model = Decoder(tiny_config(qk_norm=qk_norm)).float()
+    init_weights_(model, seed=4, std=0.05)
+    T = 9
+    tokens = torch.randint(0, model.cfg.vocab, (T,), generator=torch.Generator().manual_seed(6))
+    hd = model.cfg.head_dim
+    with torch.no_grad():
+        ref = _reference_logits(model, tokens)
+        model.setup_cache(16, "cpu", dtype=torch.float32)
+        got = model.prefill(tokens)
+        torch.testing.assert_close(got[0], ref[-1], rtol=1e-4, atol=1e-4)
+        kv = ([k[:, :hd, :T].clone() for k in model.k_cache_t], [v[:, :, :T].clone() for v in model.v_cache_t])
+        after = model.forward_step(tokens[:1].view(1, 1), torch.tensor([T]))
+        model.setup_cache(16, "cpu", dtype=torch.float32)
+        for t in range(T):
+            model.forward_step(tokens[t].view(1, 1), torch.tensor([t]))
+        for a, b in zip(kv[0], model.k_cache_t):
+            torch.testing.assert_close(a, b[:, :hd, :T], rtol=1e-5, atol=1e-5)
+        for a, b in zip(kv[1], model.v_cache_t):
+            torch.testing.assert_close(a, b[:, :, :T], rtol=1e-5, atol=1e-5)
+        step = model.forward_step(tokens[:1].view(1, 1), torch.tensor([T]))
+        torch.testing.assert_close(after, step, rtol=1e-4, atol=1e-4)
+        with pytest.raises(ValueError):
+            model.prefill(torch.zeros(17, dtype=torch.long))
+
+
 def test_linear_like_projection_modules_run_the_decoder():
     """Projections that are neither nn.Linear nor NmSparseLinear (e.g. a
     CPU gather-form module) go through their own forward: same logits as the
@@ -278,6 +309,49 @@ def test_graph_replay_matches_eager_and_masked_dense(gpu):
             assert torch.equal(a, b), rep
     with pytest.raises(RuntimeError, match="static cache"):
         gd.generate(64)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("prompt_len", [5, 24, 70])
+def test_sparse_prefill_matches_per_token_prompt(gpu, prompt_len):
+    """The sparse model's one-pass prompt (every projection through the SpMM:
+    5 rows on the small-batch kernel, 24 and 70 on the matrix cores) against
+    feeding the prompt one step at a time: last-position logits and the KV
+    caches within fp16 tolerance, and the masked dense twin's prefill within
+    the same tolerance; decoding after either continues with the same logits
+    (graph replay)."""
+    from spmv_decode_amd.decode.runner import GraphDecoder
+
+    cfg = tiny_config(qk_norm=True)
+    dense, sparse = _masked_pair(cfg, 8)
+    prompt = torch.randint(0, cfg.vocab, (prompt_len,), generator=torch.Generator().manual_seed(prompt_len))
+    hd = cfg.head_dim
+    step = GraphDecoder(sparse, 96)
+    step.run_prompt(prompt)
+    step_logits = step.logits.clone()
+    caches = ([k[:, :hd, :prompt_len].clone() for k in sparse.k_cache_t],
+              [v[:, :, :prompt_len].clone() for v in sparse.v_cache_t])
+    nxt_step = [step.eager_step().clone() for _ in range(3)]
+    one = GraphDecoder(sparse, 96)
+    one.capture()
+    one.run_prompt(prompt, batched=True)
+    torch.testing.assert_close(one.logits.float(), step_logits.float(), rtol=2e-2, atol=2e-2)
+    assert int(one.pos) == prompt_len and one.host_pos == prompt_len
+    for a, b in zip(caches[0], sparse.k_cache_t):
+        torch.testing.assert_close(a.float(), b[:, :hd, :prompt_len].float(), rtol=2e-2, atol=2e-2)
+    for a, b in zip(caches[1], sparse.v_cache_t):
+        torch.testing.assert_close(a.float(), b[:, :, :prompt_len].float(), rtol=2e-2, atol=2e-2)
+    if int(one.token) == int(step.tokens[prompt_len]):  # same first token: the continuations compare
+        nxt_one = []
+        for _ in range(3):
+            one.replay()
+            nxt_one.append(one.logits.clone())
+        torch.cuda.synchronize()
+        for a, b in zip(nxt_one, nxt_step):
+            torch.testing.assert_close(a.float(), b.float(), rtol=2e-2, atol=2e-2)
+    dref = GraphDecoder(dense, 96)
+    dref.run_prompt(prompt, batched=True)
+    torch.testing.assert_close(dref.logits.float(), step_logits.float(), rtol=2e-2, atol=2e-2)
 
 
 @pytest.mark.gpu

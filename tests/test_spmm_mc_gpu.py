@@ -71,6 +71,29 @@ def test_more_than_64_rows_and_determinism(gpu):
     assert torch.equal(mc(X[:64].contiguous(), md, mi, 32, 64), y[:64])
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+def test_more_than_64_rows_gather_and_library_gemm(gpu, dtype):
+    """Past NM_MC_MAX_BATCH rows the automatic route gathers the activations
+    (nm_gather_columns) and multiplies them with mat_data in one hipBLASLt
+    GEMM: the oracle bar at Llama-3.1-8B shapes and a ragged one, and the
+    gather alone bit-exact against a PyTorch index_select."""
+    for K, h, nnz, m, rows in ((4096, 14336, 32, 64, 128), (14336, 4096, 32, 64, 96), (1000, 384, 4, 8, 200)):
+        _, md, mi = make_case(K, h, nnz, m, seed=K + rows, dtype=dtype)
+        w = md.shape[0]
+        X = torch.randn(rows, K, device="cuda").to(dtype)
+        say(f"spmm gather + library gemm {dtype} K{K} h{h} {nnz}:{m} rows {rows}")
+        check_rows(hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, h, nnz, m), X, md, mi, nnz, m,
+                   f"{dtype} {K}x{h} rows {rows}")
+        wp = (w + 7) // 8 * 8
+        xg = torch.full((rows, wp + 8), 3.0, device="cuda").to(dtype)
+        rc = _lib.load().nm_gather_columns(0 if dtype == torch.float16 else 1, X.data_ptr(), K, rows, mi.data_ptr(),
+                                           w, nnz, m, xg.data_ptr(), wp + 8, torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "nm_gather_columns")
+        pos = (torch.arange(w, device="cuda") // nnz) * m + mi.reshape(-1).long()
+        assert torch.equal(xg[:, :w], X.index_select(1, pos))
+        assert bool((xg[:, w:] == 0).all())
+
+
 def test_c_abi_row_strides(gpu):
     """x and out with padded rows through the C ABI directly."""
     K, h, nnz, m, B = 4096, 4096, 32, 64, 20
