@@ -480,9 +480,10 @@ def decode_ms_per_token(m, log):
             torch._dynamo.reset()
 
     def prefill_ms(model, reps=10):
-        """The prompt's GPU time in one Decoder.prefill pass (every Linear over its 128 rows: hipBLASLt for
-        the dense model, the sparse model's SpMM on the matrix cores in launches of 64 rows), captured as a
-        hipGraph after an eager warm-up; median of reps replays."""
+        """The prompt's GPU time in one Decoder.prefill pass (every Linear over its 128 rows: hipBLASLt on the
+        dense weights for the dense model; for the sparse one the gathered activations [128, w] times the
+        packed weights as one hipBLASLt GEMM), captured as a hipGraph after an eager warm-up; median of reps
+        replays."""
         from spmv_decode_amd.decode.runner import cache_length
 
         model.setup_cache(cache_length(prompt.numel() + 1), torch.device("cuda"), dtype=torch.float16)
@@ -547,8 +548,9 @@ def decode_ms_per_token(m, log):
            "prefill_one_pass": {"dense_ms": prefill_dense, "sparse_ms": prefill_sparse,
                                 "speedup_sparse_vs_dense": ratio(prefill_dense, prefill_sparse),
                                 "what": "the 128-token prompt through Decoder.prefill as one hipGraph: every "
-                                        "Linear over 128 rows (dense: hipBLASLt; sparse: the matrix-core SpMM, "
-                                        "two launches of 64 rows each), causal attention in PyTorch"},
+                                        "Linear over 128 rows (dense: hipBLASLt on the dense weights; sparse: "
+                                        "nm_gather_columns + one hipBLASLt GEMM over the packed weights, half the "
+                                        "input width), causal attention in PyTorch"},
            "dense_ms_per_token": dense["ms_per_token"], "sparse_ms_per_token": sparse["ms_per_token"],
            "dense_launches": "q/k/v fused into one GEMM (the reference's dense model), gate/up/o/down one each; "
                              "each shape in the faster of hipBLASLt's x*W^T and W*x forms",
