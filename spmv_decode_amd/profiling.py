@@ -142,11 +142,13 @@ def stats(stats_csv, bench_json, md_path, cmd):
              "write finishing the previous down's partials, o leaving its partials, gate/up pair + RMSNorm + SiLU*mul",
              "finishing o's, down leaving its partials), the same step without the carry (o and down + residual), the",
              "plain fused step, the 224-launch step graph, per-class rotation graphs (>= 1 GiB of distinct weights",
-             "each, carried and plain classes), the small-batch SpMM graphs and the dense",
+             "each, carried and plain classes), the SpMM graphs (batch 2-8: small-batch kernel; 16-64: the",
+             "activation gather + the matrix-core kernel) and the dense",
              "hipBLASLt baseline graphs. `nm_gemv_kernel` template arguments: <dtype (0 = fp16), TH (tile = 8*TH",
              "rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair), NORM (input",
              "RMSNorm), CARRY (most producer splits of a carried input; 0 = none)>; `nm_spmm_kernel`: <dtype, TH, U,",
-             "G, NT, batch rows per launch>.", "",
+             "G, NT, batch rows per launch>; `nm_spmm_mc_kernel`: <dtype, batch rows per tile, output columns",
+             "per tile>.", "",
              "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
         n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
