@@ -155,3 +155,42 @@ def test_graph_capture_replays(gpu):
         torch.cuda.synchronize()
         assert torch.equal(out, eager), rep
         _ = mc(X, md, mi, nnz, m)  # eager work between replays
+
+
+def test_split_k_handoff_soak_500_replays(gpu):
+    """The matrix-core SpMM's split-K handoff (agent-scope atomic-store
+    publish, ticket, ordered partial reads) under repetition: gate/up, down
+    and q/o at the Llama-3.1-8B shapes with 48 rows (2-8 splits, 256-448
+    workgroups) in one hipGraph, replayed 500 times, every replay bitwise
+    equal to the first, stopping at the first mismatch."""
+    cases = []
+    for i, (K, h) in enumerate(((4096, 14336), (14336, 4096), (4096, 4096))):
+        _, md, mi = make_case(K, h, 32, 64, seed=90 + i)
+        X = torch.randn(48, K, device="cuda").half()
+        p = _lib.spmm_mc_plan(48, h, md.shape[0], 32, 64)
+        assert p["splits"] > 1, p
+        cases.append((X, md, mi, torch.empty(48, h, dtype=torch.float16, device="cuda")))
+
+    def launches():
+        for X, md, mi, out in cases:
+            mc(X, md, mi, 32, 64, out=out)
+
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        launches()
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            launches()
+    torch.cuda.current_stream().wait_stream(s)
+    g.replay()
+    torch.cuda.synchronize()
+    first = [c[3].clone() for c in cases]
+    check_rows(first[0], cases[0][0], cases[0][1], cases[0][2], 32, 64, "soak gate/up")
+    for rep in range(1, 500):
+        g.replay()
+        torch.cuda.synchronize()
+        for k, c in enumerate(cases):
+            if not torch.equal(c[3], first[k]):
+                pytest.fail(f"replay {rep}: case {k} differs from the first replay")
