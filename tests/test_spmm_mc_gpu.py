@@ -49,7 +49,7 @@ def test_ragged_shapes_configs_and_splits(gpu, dtype):
     for K, h, nnz, m in RAGGED:
         _, md, mi = make_case(K, h, nnz, m, seed=K + 5 * h, dtype=dtype)
         w = md.shape[0]
-        for batch in (9, 17, 40, 64):
+        for batch in (3, 9, 17, 40, 64):
             X = torch.randn(batch, K, device="cuda").to(dtype)
             for cfg, splits in ((-1, 0), (0, 1), (1, 3), (2, 2), (2, 0), (0, 64)):
                 p = _lib.spmm_mc_plan(batch, h, w, nnz, m, cfg, splits)
