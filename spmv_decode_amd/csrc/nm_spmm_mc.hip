@@ -313,11 +313,13 @@ struct McPlan {
   size_t xg_off, workspace;
 };
 
-// Plan (from sweeps at the Llama-3.1-8B and Qwen3-14B shapes, 16-64 rows):
-// cfg < 0 takes 64-column tiles above 32 rows or up to 4096 outputs, 128
-// otherwise; splits <= 0 the fewest that give about one workgroup per CU and
-// at most 1024 columns per split, at most 8 (the partials grow with the
-// rows); each split whole chunks of 64 columns. Workspace: arrival counters, the partials
+// Plan (fitted to a grid of tile widths x split counts at the Llama-3.1-8B,
+// Qwen3-14B and Qwen3-32B shapes, 16-64 rows: within 3% of each shape's best
+// on average): cfg < 0 takes 64-column tiles up to 4096 outputs unless the
+// input is deep (w > 4096) at <= 16 rows, 128-column tiles otherwise; splits
+// <= 0 about one workgroup per CU (256 / tiles, rounded), at least w / 2048,
+// at most 8 (the partials grow with the rows); each split whole chunks of 64
+// columns. Workspace: arrival counters, the partials
 // [splits, batch, h] fp32 when splits > 1, then the gathered activations
 // [batch, wp] (wp = w rounded up to whole chunks).
 int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, McPlan* p) {
@@ -327,14 +329,15 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   if (w % nnz != 0) return NM_ERR_W_NOT_MULTIPLE_NNZ;
   if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
-  if (cfg < 0) cfg = (batch > 32 || h <= 4096) ? 0 : 1;
+  if (cfg < 0) cfg = (h <= 4096 && !(w > 4096 && batch <= 16)) ? 0 : 1;
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
   const int HT = kMcTileCols[cfg];
   const int tiles = ceil_div_mc(h, HT);
   const int wp = ceil_div_mc(w, kMcCK) * kMcCK;
   if (splits <= 0) {
-    splits = ceil_div_mc(kMcCUs, tiles);
-    if (splits < ceil_div_mc(w, 1024)) splits = ceil_div_mc(w, 1024);
+    splits = (kMcCUs + tiles / 2) / tiles;
+    if (splits < ceil_div_mc(w, 2048)) splits = ceil_div_mc(w, 2048);
+    if (splits < 1) splits = 1;
     if (splits > 8) splits = 8;
   }
   if (splits > wp / kMcCK) splits = wp / kMcCK;
