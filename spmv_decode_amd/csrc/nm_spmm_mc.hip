@@ -217,17 +217,53 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
     }
     __syncthreads();
     if (!is_last) return;
-    // Every split's partials of the lane's outputs, one split per round trip,
+    // Every split's partials of the lane's outputs, GS splits per round trip,
     // summed in split order (clamped addresses for outputs that are unused).
+    // At most 32 loads in flight per lane: more raised the register count of
+    // the 64 x 128 tile to one wave per SIMD and slowed it down. A split's
+    // base is uniform; the lane keeps 32-bit offsets (batch * h < 2^31,
+    // checked by the plan).
+    constexpr int NOUT = MB * NBK * 4;
+    constexpr int GS = NOUT >= 32 ? 1 : (32 / NOUT >= 8 ? 8 : 32 / NOUT);
     const size_t step = (size_t)a.batch * (size_t)h;
+    int roff[MB][4], coff[NBK];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) roff[mb][j] = min(rb + 16 * mb + 4 * lg + j, a.batch - 1) * h;
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb) coff[nb] = min(rcol + 16 * nb, h - 1);
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
       for (int nb = 0; nb < NBK; ++nb)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[mb][nb][j] = 0.0f;
-    for (int sp = 0; sp < a.splits; ++sp) {
-      const float* ps = a.partial + (size_t)sp * step;
+    int sp = 0;
+    for (; sp + GS <= a.splits; sp += GS) {
+      float t[MB][NBK][4][GS];
+#pragma unroll
+      for (int i = 0; i < GS; ++i) {
+        const float* ps = a.partial + (size_t)(sp + i) * step;
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+              t[mb][nb][j][i] = __hip_atomic_load(ps + (roff[mb][j] + coff[nb]), __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      }
+#pragma unroll
+      for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb)
+#pragma unroll
+          for (int j = 0; j < 4; ++j)
+#pragma unroll
+            for (int i = 0; i < GS; ++i) acc[mb][nb][j] += t[mb][nb][j][i];
+    }
+    for (; sp < a.splits; ++sp) {
       float t[MB][NBK][4];
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -235,8 +271,7 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
         for (int nb = 0; nb < NBK; ++nb)
 #pragma unroll
           for (int j = 0; j < 4; ++j)
-            t[mb][nb][j] = __hip_atomic_load(ps + (size_t)min(rb + 16 * mb + 4 * lg + j, a.batch - 1) * (size_t)h +
-                                                 min(rcol + 16 * nb, h - 1),
+            t[mb][nb][j] = __hip_atomic_load(a.partial + (size_t)sp * step + (roff[mb][j] + coff[nb]),
                                              __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 #pragma unroll
       for (int mb = 0; mb < MB; ++mb)
@@ -329,6 +364,7 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   if (w % nnz != 0) return NM_ERR_W_NOT_MULTIPLE_NNZ;
   if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
+  if ((long long)batch * (long long)h > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;  // the reduction's 32-bit offsets
   if (cfg < 0) cfg = (h <= 4096 && !(w > 4096 && batch <= 16)) ? 0 : 1;
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
   const int HT = kMcTileCols[cfg];
