@@ -156,7 +156,8 @@ def spmm_plan(batch: int, h: int, w: int, nnz: int, m: int, config_id: int = -1,
             "config": describe(cfg.value)}
 
 
-MC_CONFIGS = ("mc_h64", "mc_h128", "mc_h256")  # matrix-core SpMM: output tile columns
+MC_CONFIGS = ("mc_h64", "mc_h128", "mc_h256",  # matrix-core SpMM: output tile columns; weights staged
+              "mc_h64_dma", "mc_h128_dma", "mc_h256_dma")  # through registers (0-2) or DMA into LDS (3-5)
 
 
 def spmm_mc_plan(batch: int, h: int, w: int, nnz: int, m: int, config_id: int = -1, splits: int = 0) -> dict:

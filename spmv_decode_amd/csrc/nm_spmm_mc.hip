@@ -41,7 +41,7 @@ namespace nm_hip {
 namespace {
 
 constexpr int kMcCK = 64;         // compressed columns per chunk: two MFMA K steps of 32
-constexpr int kMcNumConfigs = 3;  // output tile HT = 64, 128, 256
+constexpr int kMcNumConfigs = 6;  // output tile HT = 64, 128, 256; register-staged (0-2) or DMA (3-5) weights
 static_assert(NM_MC_MAX_BATCH == 64, "batch tiles of 16, 32 and 64 rows");
 
 typedef short s4 __attribute__((ext_vector_type(4)));
@@ -66,7 +66,48 @@ __device__ inline f4 mfma16x16x32<NM_DTYPE_BF16>(s8 a, s8 b, f4 c) {
 // lane l holds row l % 16, K elements 8*(l/16) .. +7; B[32 x 16]: column
 // l % 16, K elements 8*(l/16) .. +7; D[16 x 16]: column l % 16, rows
 // 4*(l/16) .. +3.
-template <int DT, int BT, int HT>
+// LDS stages of the DMA variant per tile width: about 64 KB of weight chunks
+// in flight per workgroup (S - 1 chunks of 64 x HT 16-bit weights).
+constexpr int mc_stages(int ht) { return ht == 64 ? 8 : (ht == 128 ? 5 : 3); }
+constexpr int kMcNtAux = 2;  // cache policy of the weight DMA: non-temporal
+
+// Inline asm with register constraints exists only in the device pass (the
+// host pass of a kernel template would otherwise reject it and drop the stub).
+template <int N>
+__device__ inline void mc_wait_vm() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+#endif
+}
+
+// Two transposed 16-bit reads, rows 0-3 and 4-7 of a 16-lane group (the
+// second OFF bytes further), without a wait: see mc_lds_wait.
+template <int OFF>
+__device__ inline void mc_read_tr_pair(s4& lo, s4& hi, uint32_t addr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %2 offset:%3"
+               : "=&v"(lo), "=&v"(hi)
+               : "v"(addr), "n"(OFF));
+#endif
+}
+
+__device__ inline void mc_lds_wait() {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+#endif
+}
+
+// Orders every later use of v after the preceding mc_lds_wait.
+__device__ inline void mc_after_wait(s4& v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" : "+v"(v));
+#endif
+}
+
+typedef __attribute__((address_space(3))) void lds_void;
+typedef __attribute__((address_space(3))) char lds_char;
+
+template <int DT, int BT, int HT, bool DMA>
 __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   using E = Elem<DT>;
   typedef typename E::scalar T;  // 16-bit storage
@@ -82,7 +123,12 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   constexpr int KS = kMcCK / 32;            // MFMA K steps per chunk
   static_assert(NBK >= 1 && NI >= 1 && RPI * NI == kMcCK, "tile shape");
 
-  __shared__ __attribute__((aligned(16))) T ws[2][kMcCK * WSTR];
+  constexpr int S = mc_stages(HT);           // DMA variant: LDS stages
+  constexpr int RB = HT * 2;                 // DMA variant: bytes per LDS weight row (no padding)
+  constexpr int SB = kMcCK * RB;             // DMA variant: bytes per stage
+  constexpr int kLdsBytes = DMA ? S * SB : 2 * kMcCK * WSTR * (int)sizeof(T);
+  __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
+  T(*ws)[kMcCK * WSTR] = reinterpret_cast<T(*)[kMcCK * WSTR]>(lds);
   __shared__ int is_last;
 
   const int h = a.h;
@@ -126,6 +172,108 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
             xg + (size_t)min(rb + 16 * mb + li, a.batch - 1) * (size_t)a.x_row_stride +
             (size_t)(c0 + k * kMcCK + 32 * ks + 8 * lg));
   };
+  f4 acc[MB][NBK];
+#pragma unroll
+  for (int mb = 0; mb < MB; ++mb)
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb) acc[mb][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  if constexpr (DMA) {
+#if defined(__HIP_DEVICE_COMPILE__)  // device code only: the host pass needs just the kernel's stub
+    // Weight chunks go from HBM straight into a ring of S LDS stages
+    // (global_load_lds_dwordx4: no registers held while in flight), S - 1
+    // chunks ahead of the one multiplied; the activation operands of the same
+    // chunks are loaded into a register ring in the same order, so that one
+    // in-order vmcnt wait covers both. Lane tid fills 16 B at byte
+    // i * kBlock * 16 + tid * 16 of a stage: row wrow + i * RPI, physical slot
+    // tid % LPR, which holds logical 16-B column slot (tid % LPR) ^ sw(row),
+    // sw(row) = 2 * (row & 3); the four rows one 16-lane transposed read
+    // addresses then fall in four distinct 32-B bank groups without padding.
+    constexpr int OPS = NI + MB * KS;  // vector memory instructions per lane per chunk
+    static_assert((S - 1) * OPS < 64, "vmcnt is a 6-bit counter");
+    static_assert(RPI % 4 == 0, "the rows a lane fills share their swizzle");
+    static_assert(S * SB <= 160 * 1024, "LDS");
+    const int gcol_d = min(tile * HT + 8 * ((tid % LPR) ^ (2 * (wrow & 3))), h - 8);
+    u32x4 aR[S][MB][KS];
+    // Every step issues the same instructions (a static vmcnt count, and no
+    // branch for the compiler's own waits to merge): rows past the split
+    // re-read its last row (zeroed in LDS once landed, below), chunks past its
+    // last read that one row again (a few cache lines; never multiplied).
+    auto issue = [&](int k, int s) {
+      const bool live = k < nch;
+#pragma unroll
+      for (int i = 0; i < NI; ++i) {
+        const int r = live ? min(k * kMcCK + wrow + i * RPI, cw - 1) : cw - 1;
+        __builtin_amdgcn_global_load_lds(md + (size_t)(c0 + r) * (size_t)h + gcol_d,
+                                         (lds_void*)(lds + s * SB + i * kBlock * 16 + wave * 1024), 16, 0, kMcNtAux);
+      }
+      load_a(aR[s], min(k, nch - 1));
+    };
+    // The lane's transposed-read address (LDS bytes) of 16-column block nb,
+    // stage 0, K step 0: row rr = 8 * lg + li / 4 (and rr + 4), logical
+    // columns cb + 16 * nb + 4 * (li & 3) .. + 3.
+    const int rr = 8 * lg + (li >> 2);
+    const uint32_t lds0 = (uint32_t)(uintptr_t)(lds_char*)lds;
+    uint32_t rd[NBK];
+#pragma unroll
+    for (int nb = 0; nb < NBK; ++nb) {
+      const int lc = (cb + 16 * nb) / 8 + ((li & 3) >> 1);
+      rd[nb] = lds0 + (uint32_t)(rr * RB + (lc ^ (2 * (rr & 3))) * 16 + (li & 1) * 8);
+    }
+    // The reads are inline asm: the compiler cannot tell the DMA stages
+    // apart and would wait for every DMA in flight before each LDS read.
+    // Their results are used only after the lgkmcnt wait (the empty asm
+    // statements order each result after it).
+    auto compute_d = [&](const u32x4 (&af)[MB][KS], int s) {
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        s4 lo[NBK], hi[NBK];
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb) {
+          const uint32_t ad = rd[nb] + (uint32_t)(s * SB + ks * 32 * RB);
+          mc_read_tr_pair<4 * RB>(lo[nb], hi[nb], ad);
+        }
+        mc_lds_wait();
+#pragma unroll
+        for (int nb = 0; nb < NBK; ++nb) {
+          mc_after_wait(lo[nb]);
+          mc_after_wait(hi[nb]);
+          const s8 bf = {lo[nb][0], lo[nb][1], lo[nb][2], lo[nb][3], hi[nb][0], hi[nb][1], hi[nb][2], hi[nb][3]};
+#pragma unroll
+          for (int mb = 0; mb < MB; ++mb)
+            acc[mb][nb] = mfma16x16x32<DT>(__builtin_bit_cast(s8, af[mb][ks]), bf, acc[mb][nb]);
+        }
+      }
+    };
+#pragma unroll
+    for (int s = 0; s < S - 1; ++s) issue(s, s);
+    for (int k0 = 0;; k0 += S) {
+#pragma unroll
+      for (int s = 0; s < S; ++s) {
+        if (k0 + s >= nch) goto mc_dma_done;
+        // chunk k0 + s: this lane's loads have landed once at most the
+        // S - 2 later chunks' are in flight; after the barrier every lane's
+        // have, and every wave is done with the stage read last step.
+        mc_wait_vm<(S - 2) * OPS>();
+        __builtin_amdgcn_s_barrier();
+        if ((k0 + s + 1) * kMcCK > cw) {
+          // the split's ragged last chunk: its rows past cw hold row cw - 1
+          const int z0 = cw - (k0 + s) * kMcCK;
+#pragma unroll
+          for (int i = 0; i < NI; ++i)
+            if (wrow + i * RPI >= z0)
+              *reinterpret_cast<u32x4*>(lds + s * SB + i * kBlock * 16 + tid * 16) = u32x4{0u, 0u, 0u, 0u};
+          mc_lds_wait();
+          __builtin_amdgcn_s_barrier();
+        }
+        issue(k0 + s + S - 1, (s + S - 1) % S);
+        compute_d(aR[s], s);
+      }
+    }
+  mc_dma_done:
+    mc_wait_vm<0>();  // no DMA into this workgroup's LDS outlives it
+#endif
+  } else {
   u32x4 wA[NI], wB[NI], aA[MB][KS], aB[MB][KS];
   load_w(wA, 0);
   load_a(aA, 0);
@@ -139,12 +287,6 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
       *reinterpret_cast<u32x4*>(&ws[buf][(wrow + i * RPI) * WSTR + wcol]) = ok ? wr[i] : u32x4{0u, 0u, 0u, 0u};
     }
   };
-
-  f4 acc[MB][NBK];
-#pragma unroll
-  for (int mb = 0; mb < MB; ++mb)
-#pragma unroll
-    for (int nb = 0; nb < NBK; ++nb) acc[mb][nb] = f4{0.0f, 0.0f, 0.0f, 0.0f};
 
   auto compute = [&](const u32x4 (&af)[MB][KS], int buf) {
 #pragma unroll
@@ -190,6 +332,7 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
       load_a(aB, min(k + 3, nch - 1));
       compute(a1, 1);
     }
+  }
   }
 
   // acc[mb][nb][j]: batch row rb + 16*mb + 4*lg + j, output column
@@ -331,14 +474,17 @@ __global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __
 typedef void (*McFn)(SpmmArgs);
 
 // fn[config: HT = 64, 128, 256][batch tile: 16, 32, 64 rows]
-#define NM_MC_ROW(DT, HT) {&nm_spmm_mc_kernel<DT, 16, HT>, &nm_spmm_mc_kernel<DT, 32, HT>, &nm_spmm_mc_kernel<DT, 64, HT>}
-const McFn kMcKernelsF16[kMcNumConfigs][3] = {NM_MC_ROW(NM_DTYPE_F16, 64), NM_MC_ROW(NM_DTYPE_F16, 128),
-                                              NM_MC_ROW(NM_DTYPE_F16, 256)};
-const McFn kMcKernelsBF16[kMcNumConfigs][3] = {NM_MC_ROW(NM_DTYPE_BF16, 64), NM_MC_ROW(NM_DTYPE_BF16, 128),
-                                               NM_MC_ROW(NM_DTYPE_BF16, 256)};
+#define NM_MC_ROW(DT, HT, DMA) \
+  {&nm_spmm_mc_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_kernel<DT, 32, HT, DMA>, &nm_spmm_mc_kernel<DT, 64, HT, DMA>}
+#define NM_MC_TABLE(DT)                                                                                    \
+  {NM_MC_ROW(DT, 64, false), NM_MC_ROW(DT, 128, false), NM_MC_ROW(DT, 256, false), NM_MC_ROW(DT, 64, true), \
+   NM_MC_ROW(DT, 128, true), NM_MC_ROW(DT, 256, true)}
+const McFn kMcKernelsF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_F16);
+const McFn kMcKernelsBF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_BF16);
+#undef NM_MC_TABLE
 #undef NM_MC_ROW
 
-constexpr int kMcTileCols[kMcNumConfigs] = {64, 128, 256};
+constexpr int kMcTileCols[kMcNumConfigs] = {64, 128, 256, 64, 128, 256};
 constexpr int kMcCUs = 256;  // MI355X compute units; split counts aim at about this many workgroups
 
 inline int ceil_div_mc(int a, int b) { return (a + b - 1) / b; }
@@ -349,9 +495,11 @@ struct McPlan {
 };
 
 // Plan (fitted to a grid of tile widths x split counts at the Llama-3.1-8B,
-// Qwen3-14B and Qwen3-32B shapes, 16-64 rows: within 3% of each shape's best
-// on average): cfg < 0 takes 64-column tiles up to 4096 outputs unless the
-// input is deep (w > 4096) at <= 16 rows, 128-column tiles otherwise; splits
+// Qwen3-14B and Qwen3-32B shapes, 16-64 rows, then to the DMA configurations
+// at the Llama-3.1-8B shapes): cfg < 0 takes register-staged 64-column tiles
+// up to 1024 outputs (16 tiles: the deeper DMA ring does not pay there),
+// DMA-staged 64-column tiles up to 4096 outputs over w <= 4096, DMA-staged
+// 128-column tiles otherwise; splits
 // <= 0 about one workgroup per CU (256 / tiles, rounded), at least w / 2048,
 // at most 8 (the partials grow with the rows); each split whole chunks of 64
 // columns. Workspace: arrival counters, the partials
@@ -365,7 +513,7 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)h > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;  // the reduction's 32-bit offsets
-  if (cfg < 0) cfg = (h <= 4096 && !(w > 4096 && batch <= 16)) ? 0 : 1;
+  if (cfg < 0) cfg = h <= 1024 ? 0 : (h <= 4096 && w <= 4096 ? 3 : 4);
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
   const int HT = kMcTileCols[cfg];
   const int tiles = ceil_div_mc(h, HT);

@@ -51,7 +51,8 @@ def test_ragged_shapes_configs_and_splits(gpu, dtype):
         w = md.shape[0]
         for batch in (3, 9, 17, 40, 64):
             X = torch.randn(batch, K, device="cuda").to(dtype)
-            for cfg, splits in ((-1, 0), (0, 1), (1, 3), (2, 2), (2, 0), (0, 64)):
+            for cfg, splits in ((-1, 0), (0, 1), (1, 3), (2, 2), (2, 0), (0, 64), (3, 0), (3, 1), (4, 3), (4, 64),
+                                (5, 2), (5, 0)):
                 p = _lib.spmm_mc_plan(batch, h, w, nnz, m, cfg, splits)
                 say(f"spmm_mc {dtype} K{K} h{h} {nnz}:{m} batch {batch} cfg {cfg} splits {splits} -> {p}")
                 check_rows(mc(X, md, mi, nnz, m, config_id=cfg, splits=splits), X, md, mi, nnz, m,
