@@ -148,7 +148,7 @@ def stats(stats_csv, bench_json, md_path, cmd):
              "rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair), NORM (input",
              "RMSNorm), CARRY (most producer splits of a carried input; 0 = none)>; `nm_spmm_kernel`: <dtype, TH, U,",
              "G, NT, batch rows per launch>; `nm_spmm_mc_kernel`: <dtype, batch rows per tile, output columns",
-             "per tile>.", "",
+             "per tile, weights DMA-staged into LDS>.", "",
              "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
     for r in sorted(rows, key=lambda r: -float(r["TotalDurationNs"]))[:12]:
         n = r["Name"].replace("void nm_hip::", "").replace("(nm_hip::Args)", "")
