@@ -68,6 +68,75 @@ def dense_bytes(K: int, h: int) -> int:
     return 2 * K * h + 2 * K + 2 * h
 
 
+def carried_gemv_chain(layers, cfg, nnz, m, dev, gen, S=512):
+    """One decode token's sparse GEMV launches as the decoder's fused path
+    issues them, over `layers` (one dict per layer: Linear name -> (mat_data,
+    mat_index)) at the shapes of `cfg` (a DecoderConfig): per layer q/k/v with
+    the input RMSNorm (and Qwen3's q/k head norms), RoPE and the KV-cache write,
+    o leaving its split partials, the gate/up pair finishing them with the
+    residual (+ RMSNorm, SiLU*mul), down leaving its partials for the next
+    layer's q/k/v (the last down adds its residual itself). Synthetic
+    activations, norm weights, caches of S positions and RoPE table; the
+    position is S // 2. Returns (step function, algorithmic bytes per step,
+    tensors the step writes)."""
+    import torch
+
+    from spmv_decode_amd import hip_spmv
+    from spmv_decode_amd.decode.model import KEY_PAD
+    from spmv_decode_amd.hip_spmv import GemvProblem
+    from spmv_decode_amd.microbench import CARRIED_CLASSES, decode_form_bytes
+
+    L = len(layers)
+    dim, inter, hd = cfg.dim, cfg.inter, cfg.head_dim
+    qd, kvd = cfg.n_heads * hd, cfg.n_kv_heads * hd
+    eps = cfg.norm_eps
+    f16 = dict(dtype=torch.float16, device=dev)
+    x_res = torch.randn(1, dim, generator=gen, device=dev).to(torch.float16)
+    attn = torch.randn(1, qd, generator=gen, device=dev).to(torch.float16)
+    qo = torch.zeros(cfg.n_heads, hd + KEY_PAD, **f16)  # the decoder's query rows
+    ln1, ln2 = ((torch.rand(dim, generator=gen, device=dev) + 0.5).to(torch.float16) for _ in range(2))
+    qn, kn = ((torch.rand(hd, generator=gen, device=dev) + 0.5).to(torch.float16) if cfg.qk_norm else None
+              for _ in range(2))
+    kcs = [torch.zeros(cfg.n_kv_heads, hd + KEY_PAD, S, **f16) for _ in range(L)]
+    vcs = [torch.zeros(cfg.n_kv_heads, hd, S, **f16) for _ in range(L)]
+    ang = torch.outer(torch.arange(S, dtype=torch.float64),
+                      1.0 / (cfg.rope_theta ** (torch.arange(hd // 2, dtype=torch.float64) * 2.0 / hd)))
+    rope = torch.polar(torch.ones_like(ang), ang).to(torch.complex64).to(dev)
+    pos = torch.tensor([S // 2], device=dev)
+    act = torch.empty(1, inter, **f16)
+    h2, xa, hb = (torch.empty(1, dim, **f16) for _ in range(3))
+    co = torch.zeros(hip_spmv.carry_splits(*layers[0]["o_proj"], nnz, m), dim, device=dev)
+    cd = torch.zeros(hip_spmv.carry_splits(*layers[0]["down_proj"], nnz, m), dim, device=dev)
+
+    def layer(li):
+        lay = layers[li]
+        qkv = dict(q_out=qo, k_cache_t=kcs[li], v_cache_t=vcs[li], pos=pos, rope_table=rope, head_dim=hd,
+                   norm=(ln1, eps), q_norm=qn, k_norm=kn, head_eps=eps)
+        if li == 0:
+            hip_spmv.nmsparse_qkv_decode(x_res, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, **qkv)
+        else:
+            hip_spmv.nmsparse_qkv_decode(hb, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, carry_in=cd,
+                                         vec_out=xa, **qkv)
+        hip_spmv.nmsparse_gemv_partials(attn, *lay["o_proj"], nnz, m, co)
+        hip_spmv.nmsparse_gate_up_silu(x_res if li == 0 else xa, lay["gate_proj"], lay["up_proj"], nnz, m, out=act,
+                                       norm=(ln2, eps), carry_in=co, vec_out=hb)
+        if li + 1 < L:
+            hip_spmv.nmsparse_gemv_partials(act, *lay["down_proj"], nnz, m, cd)
+        else:
+            hip_spmv.nmsparse_gemv_launch(act, [GemvProblem(*lay["down_proj"], h2, residual=hb)], nnz, m)
+
+    def step():
+        for li in range(L):
+            layer(li)
+
+    dims = dict(dim=dim, inter=inter, qd=qd, kvd=kvd, hd=hd, qk_norm=cfg.qk_norm)
+    nbytes = (L * sum(decode_form_bytes(c, nnz, m, **dims) for c in CARRIED_CLASSES)
+              - decode_form_bytes("qkv_decode_carried", nnz, m, **dims) + decode_form_bytes("qkv_decode", nnz, m, **dims)
+              - decode_form_bytes("down_partials", nnz, m, **dims) + decode_form_bytes("down_resid", nnz, m, **dims))
+    written = [act, qo, xa, hb, h2, kcs[-1][:, :, S // 2], vcs[-1][:, :, S // 2]]
+    return step, nbytes, written
+
+
 def parse_args():
     p = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     p.add_argument("--gpus", type=int, default=1)
@@ -84,7 +153,8 @@ def parse_args():
     p.add_argument("--cpu-decode", action="store_true",
                    help="also time a CPU Llama-3.1-8B decode step (the decoder code, every Linear via CPU-B)")
     p.add_argument("--only-step", action="store_true", help="time only the sparse step (for profiling)")
-    p.add_argument("--no-decode", action="store_true", help="skip the end-to-end Llama-3.1-8B decode")
+    p.add_argument("--no-decode", action="store_true", help="skip the end-to-end decodes")
+    p.add_argument("--no-qwen3", action="store_true", help="skip the Qwen3-14B / Qwen3-32B decodes (configs 4-5)")
     return p.parse_args()
 
 
@@ -173,32 +243,9 @@ def main():
     decode_bytes = L * sum(decode_form_bytes(c, nnz, m) for c in DECODE_CLASSES)
 
     # the decoder's fused path: the split-K carry between the launches
-    co = torch.zeros(hip_spmv.carry_splits(*layers[0]["o_proj"], nnz, m), 4096, device=dev)
-    cd = torch.zeros(hip_spmv.carry_splits(*layers[0]["down_proj"], nnz, m), 4096, device=dev)
-    xa, hb = (torch.empty(1, 4096, dtype=torch.float16, device=dev) for _ in range(2))
+    from spmv_decode_amd.decode.model import LLAMA31_8B
 
-    def carried_layer(li):
-        # q/k/v finishes the previous down's partials (the first layer reads x_res), o leaves its partials,
-        # gate/up finishes them, down leaves its partials (the last one adds its residual)
-        lay = layers[li]
-        qkv = dict(q_out=qo, k_cache_t=kcs[li], v_cache_t=vcs[li], pos=pos, rope_table=rope, head_dim=128,
-                   norm=(ln1, 1e-5))
-        if li == 0:
-            hip_spmv.nmsparse_qkv_decode(x_res, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, **qkv)
-        else:
-            hip_spmv.nmsparse_qkv_decode(hb, lay["q_proj"], lay["k_proj"], lay["v_proj"], nnz, m, carry_in=cd,
-                                         vec_out=xa, **qkv)
-        hip_spmv.nmsparse_gemv_partials(attn, *lay["o_proj"], nnz, m, co)
-        hip_spmv.nmsparse_gate_up_silu(x_res if li == 0 else xa, lay["gate_proj"], lay["up_proj"], nnz, m, out=act,
-                                       norm=(ln2, 1e-5), carry_in=co, vec_out=hb)
-        if li + 1 < L:
-            hip_spmv.nmsparse_gemv_partials(act, *lay["down_proj"], nnz, m, cd)
-        else:
-            hip_spmv.nmsparse_gemv_launch(act, [GemvProblem(*lay["down_proj"], h2, residual=hb)], nnz, m)
-
-    carried_bytes = (L * sum(decode_form_bytes(c, nnz, m) for c in CARRIED_CLASSES)
-                     - decode_form_bytes("qkv_decode_carried", nnz, m) + decode_form_bytes("qkv_decode", nnz, m)
-                     - decode_form_bytes("down_partials", nnz, m) + decode_form_bytes("down_resid", nnz, m))
+    carried_step, carried_bytes, carried_written = carried_gemv_chain(layers, LLAMA31_8B, nnz, m, dev, gen, S=S)
 
     w4, w14 = 4096 // m * nnz, 14336 // m * nnz
     fused_bytes_layer = (
@@ -237,12 +284,11 @@ def main():
         return start.elapsed_time(end) / args.steps
 
     # ---- the timed step: one decode token's sparse GEMVs as the decoder runs them
-    ms_per_step = time_step(lambda: [carried_layer(li) for li in range(L)])
+    ms_per_step = time_step(carried_step)
     value = carried_bytes / (ms_per_step * 1e-3) / 1e9
     log(f"decode step, carried ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
-    written = [act, qo, xa, hb, h2, kcs[1][:, :, S // 2], vcs[1][:, :, S // 2]]
-    if not all(bool(torch.isfinite(o.float()).all()) for o in written):
+    if not all(bool(torch.isfinite(o.float()).all()) for o in carried_written):
         raise RuntimeError("non-finite GEMV output")
     ms_nocarry = time_step(lambda: [decode_layer(li) for li in range(L)])
     nocarry_value = decode_bytes / (ms_nocarry * 1e-3) / 1e9
@@ -427,6 +473,12 @@ def main():
         layers.clear()  # the closures above share this list: clearing it frees the weights
         torch.cuda.empty_cache()
         result["decode"] = decode_ms_per_token(m, log)
+        if not args.no_qwen3:
+            result["decode_qwen3"] = decode_qwen3(log)
+        # torch.compile's worker pool (started by the compiled fixed-context runs) must not outlive the bench
+        from torch._inductor.async_compile import shutdown_compile_workers
+
+        shutdown_compile_workers()
     print(json.dumps(result), flush=True)
 
 
@@ -444,7 +496,7 @@ def decode_ms_per_token(m, log):
 
     from spmv_decode_amd.decode.bench_decode import linear_bytes, run_variant
     from spmv_decode_amd.decode.model import LLAMA31_8B, Decoder, init_weights_
-    from spmv_decode_amd.decode.runner import fixed_context_ms
+    from spmv_decode_amd.decode.runner import fixed_context_logits_fp32, fixed_context_ms, logits_envelope
     from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
     from spmv_decode_amd.profiling import REFERENCE_A100_CTX512
 
@@ -458,19 +510,25 @@ def decode_ms_per_token(m, log):
     init_weights_(model, seed=0)
     prompt = torch.randint(0, LLAMA31_8B.vocab, (128,), generator=torch.Generator().manual_seed(1))
 
-    def compiled_fixed(model, eager_ref):
-        """The reference protocol with its torch.compile: compile the step, then capture and replay;
-        the compiled step's logits are compared with the eager step's (eager_ref). An extra figure:
-        a compiler failure is reported in the JSON, not raised."""
+    envelope_failures = []
+
+    def compiled_fixed(model, eager_ref, ref32, label):
+        """The reference protocol with its torch.compile: compile the step, then capture and replay.
+        The compiled step's logits must stay within the fp16 envelope of the eager step's (eager_ref),
+        judged against the fp32 reference ref32 of the same step (runner.logits_envelope); a step outside
+        it is collected in envelope_failures and fails the bench. A compiler failure is reported in the
+        JSON, not raised (the compiled figures are then null)."""
         eager = model.forward_step
         torch._dynamo.reset()
         model.forward_step = torch.compile(eager, dynamic=False)
         try:
             r = fixed_context_ms(model, 512)
             diff = (r["logits"] - eager_ref["logits"]).abs().max().item()
-            rel = ((r["logits"] - eager_ref["logits"]).norm() / eager_ref["logits"].norm()).item()
-            r["matches_eager"] = {"max_abs_logit_diff": round(diff, 5), "rel_l2": float(f"{rel:.3e}"),
-                                  "same_greedy_token": r["token"] == eager_ref["token"]}
+            r["matches_eager"] = {"max_abs_logit_diff": round(diff, 5),
+                                  **logits_envelope(eager_ref["logits"], r["logits"], ref32)}
+            log(f"{label} compiled vs eager: {r['matches_eager']}")
+            if not r["matches_eager"]["within"]:
+                envelope_failures.append((label, r["matches_eager"]))
             return r
         except Exception as exc:  # noqa: BLE001 - torch.compile's failures have no common type
             log(f"compiled fixed-context decode failed: {type(exc).__name__}: {exc}")
@@ -509,12 +567,13 @@ def decode_ms_per_token(m, log):
         return round(sorted(times)[len(times) // 2], 4)
 
     dense_by_fusion, forms, fixed_dense, fixed_dense_c = {}, {}, {}, {}
+    ref32_dense = fixed_context_logits_fp32(model, 512)  # the dense step in fp32: the envelope's reference
     for mode in ("qkv", "none", "qkv_gate_up"):  # "qkv": the reference's dense model (model.py:198 wqkv)
         model.set_dense_fusion(mode)
         forms.update(model.tune_dense_gemv())  # the faster hipBLASLt problem form per dense shape
         dense_by_fusion[mode] = run_variant(model, LLAMA31_8B, prompt, 256, f"dense ({mode} fused)", log)
         fixed_dense[mode] = fixed_context_ms(model, 512)  # the reference benchmark's protocol
-        fixed_dense_c[mode] = compiled_fixed(model, fixed_dense[mode])
+        fixed_dense_c[mode] = compiled_fixed(model, fixed_dense[mode], ref32_dense, f"dense ({mode} fused)")
     model.set_dense_fusion("none")
     dense = dense_by_fusion["qkv"]
     prefill_dense = prefill_ms(model)
@@ -525,7 +584,8 @@ def decode_ms_per_token(m, log):
         f"sparse {prefill_sparse} ms ({prefill_dense / prefill_sparse:.3f}x)")
     sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)
     fixed_sparse = fixed_context_ms(model, 512)
-    fixed_sparse_c = compiled_fixed(model, fixed_sparse)
+    ref32_sparse = fixed_context_logits_fp32(model, 512)
+    fixed_sparse_c = compiled_fixed(model, fixed_sparse, ref32_sparse, "sparse")
     variants = {}
     for mode in ("per_linear", "grouped", "modules"):
         model.set_launch_mode(mode)
@@ -593,8 +653,13 @@ def decode_ms_per_token(m, log):
                             "sparse_ms_per_token": _finite(fixed_sparse_c["median"]),
                             "speedup_sparse_vs_dense": ratio(fcc["qkv"], fixed_sparse_c["median"]),
                             "speedup_sparse_vs_fastest_dense": ratio(fastest_fcc, fixed_sparse_c["median"]),
-                            "matches_eager": {"dense": fixed_dense_c["qkv"].get("matches_eager"),
-                                              "sparse": fixed_sparse_c.get("matches_eager")},
+                            "matches_eager": {**{f"dense_{k}": v.get("matches_eager")
+                                                 for k, v in fixed_dense_c.items()},
+                                              "sparse": fixed_sparse_c.get("matches_eager"),
+                                              "rule": "each compiled step's logits within 2*e16 + 1e-3 (rel-L2) of "
+                                                      "the same step in fp32 and within 3*e16 + 1e-3 of the eager "
+                                                      "fp16 step, e16 = the eager fp16 step's rel-L2 from fp32; "
+                                                      "the bench fails otherwise"},
                             "errors": [r["error"] for r in (*fixed_dense_c.values(), fixed_sparse_c)
                                        if "error" in r] or None,
                             "note": "torch.compile of each model's step before capture, as the reference "
@@ -606,12 +671,123 @@ def decode_ms_per_token(m, log):
            "headline": {"speedup": ratio(fastest_fcc, fixed_sparse_c["median"]),
                         "what": "sparse over the fastest of the three dense launch structures, both compiled, "
                                 "under the reference benchmark's fixed-context protocol (CTX 512, sampling)"}}
+    if envelope_failures:
+        raise RuntimeError(f"compiled fixed-context step outside the fp16 envelope of the eager step: "
+                           f"{envelope_failures}")
     log(f"decode: dense {out['dense_ms_per_token']} ms/token, sparse {out['sparse_ms_per_token']} ms/token "
         f"({out['speedup_sparse_vs_dense']}x), unmodified model after the swap "
         f"{variants['modules']['ms_per_token']} ms ({out['speedup_sparse_modules_vs_dense']}x), per-Linear "
         f"{variants['per_linear']['ms_per_token']} ms; fixed context 512: {round(fc['qkv'], 4)} / "
         f"{round(fixed_sparse['median'], 4)} ms (compiled {_finite(fcc['qkv'])} / "
         f"{_finite(fixed_sparse_c['median'])} ms; over the fastest compiled dense {out['headline']['speedup']}x)")
+    return out
+
+
+QWEN3_DECODE = (  # BASELINE configs 4 and 5: (model, M, prompt tokens, generated tokens)
+    ("qwen3-14b", 64, 128, 256),
+    ("qwen3-32b", 32, 512, 512),
+)
+
+
+def decode_qwen3(log, steps=20, warmup=5):
+    """Configs 4-5: random-init Qwen3-14B at 32:64 and Qwen3-32B at 16:32, fp16,
+    batch 1. Per model: the dense model under each of its three launch
+    structures (one GEMM per Linear, q/k/v fused, q/k/v and gate/up fused; every
+    dense shape in hipBLASLt's faster problem form) and the fused sparse decoder,
+    each the prompt in one Decoder.prefill pass (untimed) then the generated
+    tokens by hipGraph replay (ms/token: the mean over them); the speedup over
+    the fastest dense structure; and one token's sparse GEMV launches as the
+    decoder issues them (4 per layer, the split-K carry, over the model's own
+    resident weights) timed alone by graph replay: ms and algorithmic GB/s."""
+    import gc
+
+    import torch
+
+    from spmv_decode_amd.decode.bench_decode import linear_bytes, run_variant
+    from spmv_decode_amd.decode.model import CONFIGS, Decoder, init_weights_
+    from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
+    from spmv_decode_amd.profiling import REFERENCE_A100_CTX512
+
+    dev = torch.device("cuda:0")
+    out = {}
+    for name, M, P, G in QWEN3_DECODE:
+        cfg = CONFIGS[name]
+        nnz = M // 2
+        t0 = time.time()
+        prev = torch.get_default_dtype()
+        torch.set_default_dtype(torch.float16)
+        try:
+            with torch.device(dev):
+                model = Decoder(cfg)
+        finally:
+            torch.set_default_dtype(prev)
+        init_weights_(model, seed=0)
+        model.eval()
+        prompt = torch.randint(0, cfg.vocab, (P,), generator=torch.Generator().manual_seed(1))
+        log(f"{name}: dense model built in {time.time() - t0:.1f} s")
+        dense = {}
+        for mode in ("qkv", "none", "qkv_gate_up"):
+            model.set_dense_fusion(mode)
+            model.tune_dense_gemv()
+            dense[mode] = run_variant(model, cfg, prompt, G, f"{name} dense ({mode} fused)", log,
+                                      batched_prompt=True)
+        model.set_dense_fusion("none")
+        swap_to_nmsparse(model, M, "cuda", seed=0, init="device", keep_dense=False)
+        gc.collect()
+        torch.cuda.empty_cache()
+        sparse = run_variant(model, cfg, prompt, G, f"{name} sparse {nnz}:{M}", log, batched_prompt=True)
+        layers = [{n: (getattr(sub, n).mat_data, getattr(sub, n).mat_index)
+                   for sub, names in ((blk.self_attn, ("q_proj", "k_proj", "v_proj", "o_proj")),
+                                      (blk.mlp, ("gate_proj", "up_proj", "down_proj"))) for n in names}
+                  for blk in model.layers]
+        step, nbytes, written = carried_gemv_chain(layers, cfg, nnz, M, dev, torch.Generator(device=dev).manual_seed(3))
+        stream = torch.cuda.Stream(device=dev)
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            step()
+        torch.cuda.current_stream().wait_stream(stream)
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g, stream=stream):
+            step()
+        for _ in range(warmup):
+            g.replay()
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(steps):
+            g.replay()
+        b.record()
+        b.synchronize()
+        step_ms = a.elapsed_time(b) / steps
+        if not all(bool(torch.isfinite(o.float()).all()) for o in written):
+            raise RuntimeError(f"{name}: non-finite GEMV output in the step")
+        del g, layers, step, written
+        ms = {k: v["ms_per_token"] for k, v in dense.items()}
+        fastest = min(ms, key=ms.get)
+        ref_dense, ref_sparse = REFERENCE_A100_CTX512.get(name, (None, {}))
+        out[name] = {
+            "ratio": f"{nnz}:{M}", "prompt": P, "gen": G, "layers": cfg.n_layers,
+            "dense_ms_per_token_by_fusion": ms, "fastest_dense": fastest,
+            "sparse_ms_per_token": sparse["ms_per_token"],
+            "speedup_sparse_vs_fastest_dense": round(ms[fastest] / sparse["ms_per_token"], 4),
+            "speedup_sparse_vs_dense_qkv_fused": round(ms["qkv"] / sparse["ms_per_token"], 4),
+            "finite_logits": sparse["finite_logits"] and all(v["finite_logits"] for v in dense.values()),
+            "sparse_linear_bytes_per_token": linear_bytes(cfg, M), "dense_linear_bytes_per_token": linear_bytes(cfg, 0),
+            "gemv_step": {"launches": 4 * cfg.n_layers, "ms": round(step_ms, 5), "algorithmic_bytes": nbytes,
+                          "GBps": round(nbytes / step_ms / 1e6, 1),
+                          "pct_hbm_peak": round(100 * nbytes / step_ms / 1e6 / HBM_PEAK_GBS, 2)},
+            "reference_a100_published_fixed_ctx512": {
+                "dense_ms_per_token": ref_dense, "sparse_ms_per_token": ref_sparse.get(M),
+                "note": "the reference's A100 table (README.md:99-121), fixed-context protocol (CTX 512), not this "
+                        "generation protocol"},
+        }
+        log(f"{name} {nnz}:{M}: dense {ms} ms/token, sparse {sparse['ms_per_token']} ms/token "
+            f"({out[name]['speedup_sparse_vs_fastest_dense']}x over the fastest dense); GEMV step "
+            f"{out[name]['gemv_step']}")
+        del model
+        gc.collect()
+        torch.cuda.empty_cache()
     return out
 
 

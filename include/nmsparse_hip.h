@@ -349,6 +349,16 @@ int nm_gemv_plan(int h, int w, int nnz, int m, int config_id, int splits,
 /* Human-readable text for a status code returned above. */
 const char* nm_strerror(int code);
 
+/*
+ * Capture state of `stream` as the HIP runtime this library links reports it
+ * (hipStreamGetCaptureInfo): *out_id receives the id of the graph capture in
+ * progress on the stream, or 0 when the stream is not capturing. Returns 0 or
+ * the hipError_t. No reference counterpart: the Python layer keys the
+ * workspaces of launches recorded into a capture by this id, through the
+ * runtime the library itself uses (whatever its soname).
+ */
+int nm_stream_capture_id(void* stream, unsigned long long* out_id);
+
 /* ABI version of this header (bumped on any signature change). */
 int nm_abi_version(void);
 

@@ -88,8 +88,9 @@ ABI = {
     "nm_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_strerror": (ctypes.c_char_p, [_i]),
     "nm_abi_version": (_i, []),
+    "nm_stream_capture_id": (_i, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _lib = None
 _lock = threading.Lock()

@@ -315,10 +315,35 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
       return NM_ERR_MISALIGNED;
     const uintptr_t vo = (uintptr_t)d.vec_out, vi = (uintptr_t)d.vec;
     if (vo < vi + (size_t)K * esize && vi < vo + (size_t)K * esize) return NM_ERR_BAD_EPILOGUE;  // overlap
-    // vec_out is written while other workgroups still read carry_in.
-    const uintptr_t ci = (uintptr_t)d.carry_in;
-    const size_t in_bytes = (size_t)d.carry_splits * (size_t)K * sizeof(float);
-    if (vo < ci + in_bytes && ci < vo + (size_t)K * esize) return NM_ERR_BAD_EPILOGUE;
+    // Tile 0's workgroups write vec_out while the other workgroups still read
+    // every input of the launch and write its outputs: vec_out must overlap
+    // none of them.
+    const size_t vo_bytes = (size_t)K * esize;
+    auto clash = [&](const void* ptr, size_t bytes) {
+      const uintptr_t b = (uintptr_t)ptr;
+      return ptr != nullptr && bytes > 0 && vo < b + bytes && b < vo + vo_bytes;
+    };
+    if (clash(d.carry_in, (size_t)d.carry_splits * (size_t)K * sizeof(float)) || clash(d.norm_weight, vo_bytes) ||
+        clash(workspace, workspace_bytes) || clash(d.pos, sizeof(long long)) ||
+        clash(d.rope_table, (size_t)(d.pos_limit > 0 ? d.pos_limit : 0) * (size_t)(d.head_dim / 2) * 2 * sizeof(float)))
+      return NM_ERR_BAD_EPILOGUE;
+    for (int i = 0; i < d.nprob; ++i) {
+      const nm_gemv_problem& q = d.prob[i];
+      if (clash(q.mat_data, (size_t)d.w * (size_t)q.h * esize) || clash(q.mat_index, (size_t)d.w))
+        return NM_ERR_BAD_EPILOGUE;
+    }
+    for (int i = 0; i < nprob; ++i) {
+      const nm_gemv_problem& q = d.prob[i];
+      size_t out_elems = (size_t)q.h;
+      if (q.head_stride != 0 || q.elem_stride != 0 || q.pos_stride != 0) {
+        const long long hd = d.head_dim;
+        out_elems = (size_t)((q.h / hd - 1) * q.head_stride + (hd - 1) * q.elem_stride +
+                             (long long)(d.pos_limit > 1 ? d.pos_limit - 1 : 0) * q.pos_stride + 1);
+      }
+      if (clash(q.out, out_elems * esize) || clash(q.residual, (size_t)q.h * esize) ||
+          clash(q.head_norm, (size_t)(d.head_dim > 0 ? d.head_dim : 0) * esize))
+        return NM_ERR_BAD_EPILOGUE;
+    }
   }
   if (validate_only) return NM_OK;
 
@@ -748,5 +773,15 @@ const char* nm_strerror(int code) {
 }
 
 int nm_abi_version(void) { return kAbiVersion; }
+
+int nm_stream_capture_id(void* stream, unsigned long long* out_id) {
+  if (!out_id) return NM_ERR_NULL_POINTER;
+  hipStreamCaptureStatus status = hipStreamCaptureStatusNone;
+  unsigned long long id = 0;
+  const hipError_t err = hipStreamGetCaptureInfo(static_cast<hipStream_t>(stream), &status, &id);
+  if (err != hipSuccess) return (int)err;
+  *out_id = status == hipStreamCaptureStatusActive ? id : 0ull;
+  return NM_OK;
+}
 
 }  // extern "C"

@@ -58,12 +58,15 @@ def linear_bytes(cfg, m: int) -> int:
     return total * cfg.n_layers
 
 
-def run_variant(model, cfg, prompt, gen, label, log):
+def run_variant(model, cfg, prompt, gen, label, log, batched_prompt=False):
+    """Capture the decode step, feed the prompt (untimed; one graph replay per
+    token, or with batched_prompt one Decoder.prefill pass), then time `gen`
+    greedy steps by graph replay."""
     dec = GraphDecoder(model, prompt.numel() + gen)
     t0 = time.time()
     dec.capture()
     log(f"{label}: captured decode step in {time.time() - t0:.1f} s")
-    dec.run_prompt(prompt)
+    dec.run_prompt(prompt, batched=batched_prompt)
     ids, ms_mean, ms_median = dec.generate(gen)
     ok = bool(torch.isfinite(dec.logits).all().item())
     del dec

@@ -463,6 +463,7 @@ class Decoder(nn.Module):
         self.lm_head = nn.Linear(cfg.dim, cfg.vocab, bias=False)
         self.max_seq = 0
         self.gemv_forms = {}  # (n_out, n_in) -> dense_gemv form, filled by tune_dense_gemv
+        self.dense_fusion = "none"  # set_dense_fusion's mode
 
     LAUNCH_MODES = ("fused", "grouped", "per_linear", "modules")
 
@@ -493,6 +494,7 @@ class Decoder(nn.Module):
         projections are not all nn.Linear ignore them; "none" frees them."""
         if mode not in self.DENSE_FUSIONS:
             raise ValueError(f"dense fusion must be one of {self.DENSE_FUSIONS}, got {mode!r}")
+        self.dense_fusion = mode
         with torch.no_grad():
             for blk in self.layers:
                 at, mlp = blk.self_attn, blk.mlp

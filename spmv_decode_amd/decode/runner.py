@@ -73,6 +73,73 @@ def sample_token(logits: torch.Tensor, out: torch.Tensor, generator: torch.Gener
     return greedy_token(probs.float() / race, out=out)
 
 
+def _fill_fixed_context(model: Decoder, ctx: int, seed: int, dev: torch.device) -> None:
+    """The fixed-context protocol's caches: ctx + 1 positions (rounded up by
+    cache_length) of the model's dtype, keys and values N(0, 0.02) from a
+    seeded device generator, layer by layer (the mask and padding rows stay as
+    set up)."""
+    hd = model.cfg.head_dim
+    model.setup_cache(cache_length(ctx + 1), dev, dtype=model.embed_tokens.weight.dtype)
+    gen = torch.Generator(device=dev).manual_seed(seed)
+    for k, v in zip(model.k_cache_t, model.v_cache_t):
+        k[:, :hd].normal_(0.0, 0.02, generator=gen)
+        v.normal_(0.0, 0.02, generator=gen)
+
+
+@torch.no_grad()
+def fixed_context_logits_fp32(model: Decoder, ctx: int, seed: int = 1234, token_id: int = 123,
+                              device="cuda") -> torch.Tensor:
+    """The logits of fixed_context_ms's step computed in fp32 throughout: the
+    same weights and cache values (drawn in the model's dtype exactly as
+    fixed_context_ms draws them, then widened, which is exact), every
+    activation fp32, one eager step. The fp32 reference against which the
+    fp16 steps (eager and compiled) are held (fp16 rounding envelope). The
+    model is widened in place for the step and narrowed back afterwards (an
+    exact round trip: every weight is an fp16 value); its dense fusion copies
+    are rebuilt both ways. Returns fp32 logits [1, vocab] on the host."""
+    dev = torch.device(device)
+    dt = model.embed_tokens.weight.dtype
+    hd = model.cfg.head_dim
+    _fill_fixed_context(model, ctx, seed, dev)
+    keys = model.k_store[:, :, :hd].clone()
+    vals = [v.clone() for v in model.v_cache_t]
+    fusion = model.dense_fusion
+    try:
+        model.float()
+        model.set_dense_fusion(fusion)
+        model.setup_cache(cache_length(ctx + 1), dev, dtype=torch.float32)
+        model.k_store[:, :, :hd].copy_(keys)
+        for v, src in zip(model.v_cache_t, vals):
+            v.copy_(src)
+        del keys, vals
+        token = torch.full((1, 1), token_id, dtype=torch.long, device=dev)
+        pos = torch.full((1,), ctx, dtype=torch.long, device=dev)
+        logits = model.forward_step(token, pos).float().cpu()
+    finally:
+        model.to(dt)
+        model.set_dense_fusion(fusion)
+        model.setup_cache(cache_length(ctx + 1), dev, dtype=dt)
+    return logits
+
+
+def logits_envelope(eager16: torch.Tensor, other16: torch.Tensor, ref32: torch.Tensor) -> dict:
+    """Whether `other16` (e.g. the compiled step's logits) stays within the
+    fp16 envelope of `eager16` (the eager step's), both judged against the
+    fp32 reference `ref32` of the same step: e16 = rel-L2(eager16, ref32) is
+    what fp16 rounding costs at this depth; `other16` must be within
+    2 * e16 + 1e-3 of ref32 and within 3 * e16 + 1e-3 of eager16 (the rule of
+    the full-depth decode parity tests). Relative L2 over the vocabulary."""
+    def rel(a, b):
+        return float((a.float() - b.float()).norm() / b.float().norm())
+
+    e16 = rel(eager16, ref32)
+    to_ref, to_eager = rel(other16, ref32), rel(other16, eager16)
+    ok = to_ref <= 2 * e16 + 1e-3 and to_eager <= 3 * e16 + 1e-3
+    return {"within": ok, "e16_eager_vs_fp32": float(f"{e16:.3e}"), "rel_l2_vs_fp32": float(f"{to_ref:.3e}"),
+            "rel_l2_vs_eager": float(f"{to_eager:.3e}"),
+            "same_greedy_token": int(torch.argmax(other16)) == int(torch.argmax(eager16))}
+
+
 @torch.no_grad()
 def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 30, inner: int = 10,
                      seed: int = 1234, token_id: int = 123, device="cuda", sample: bool = True) -> dict:
@@ -88,12 +155,7 @@ def fixed_context_ms(model: Decoder, ctx: int, warmup: int = 30, repeat: int = 3
     if min(ctx, warmup, repeat, inner) < 1:
         raise ValueError("ctx, warmup, repeat and inner must be positive")
     dev = torch.device(device)
-    hd = model.cfg.head_dim
-    model.setup_cache(cache_length(ctx + 1), dev, dtype=model.embed_tokens.weight.dtype)
-    gen = torch.Generator(device=dev).manual_seed(seed)
-    for k, v in zip(model.k_cache_t, model.v_cache_t):
-        k[:, :hd].normal_(0.0, 0.02, generator=gen)  # the mask and padding rows stay as set up
-        v.normal_(0.0, 0.02, generator=gen)
+    _fill_fixed_context(model, ctx, seed, dev)
     token = torch.full((1, 1), token_id, dtype=torch.long, device=dev)
     pos = torch.full((1,), ctx, dtype=torch.long, device=dev)
     nxt = torch.zeros(1, dtype=torch.long, device=dev)

@@ -29,7 +29,6 @@ capture id, so two graphs never share one.
 from __future__ import annotations
 
 import ctypes
-import os
 import warnings
 
 import torch
@@ -50,24 +49,17 @@ _retired: list[torch.Tensor] = []
 # active: the graph's pool then keeps the memory for its replays, as it does
 # for every intermediate tensor of the capture.
 _capture_workspaces: dict[tuple[int, int], list[torch.Tensor]] = {}
-_hip_rt = None
 
 
 def capture_id(stream_ptr: int) -> int:
-    """Id of the hipGraph capture in progress on `stream_ptr` (hipStreamGetCaptureInfo
-    of the HIP runtime torch has loaded); 0 when the stream is not capturing."""
-    global _hip_rt
-    if _hip_rt is None:
-        lib = ctypes.CDLL("libamdhip64.so.7", mode=os.RTLD_NOLOAD)  # the runtime already in the process
-        fn = lib.hipStreamGetCaptureInfo
-        fn.restype = ctypes.c_int
-        fn.argtypes = [ctypes.c_void_p, ctypes.POINTER(ctypes.c_int), ctypes.POINTER(ctypes.c_ulonglong)]
-        _hip_rt = fn
-    status, cid = ctypes.c_int(0), ctypes.c_ulonglong(0)
-    rc = _hip_rt(ctypes.c_void_p(int(stream_ptr)), ctypes.byref(status), ctypes.byref(cid))
+    """Id of the hipGraph capture in progress on `stream_ptr`, 0 when the stream
+    is not capturing (nm_stream_capture_id: hipStreamGetCaptureInfo of the HIP
+    runtime the library links, so no runtime soname is assumed here)."""
+    cid = ctypes.c_ulonglong(0)
+    rc = _lib.load().nm_stream_capture_id(ctypes.c_void_p(int(stream_ptr)), ctypes.byref(cid))
     if rc != 0:
         raise _lib.NmSparseLibraryError(f"hipStreamGetCaptureInfo failed with status {rc}")
-    return int(cid.value) if status.value == 1 else 0  # hipStreamCaptureStatusActive
+    return int(cid.value)
 
 
 def validate_args(vec, mat_data, mat_index, w, h, BLOCK_WIDTH, NUM_THREADS, VEC_WIDTH, minibatch, vecNum,

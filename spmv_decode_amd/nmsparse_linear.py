@@ -39,6 +39,7 @@ entries, `mat_data` and `mat_index`).
 from __future__ import annotations
 
 import os
+import warnings
 
 import torch
 import torch.nn as nn
@@ -261,6 +262,20 @@ class SiblingLaunch:
     the input tensor it launched for until the next launch, so that tensor's
     memory cannot be reused under it. No reference counterpart: the reference
     launches every Linear on its own (src/spmv/nmsparse_linear.py:62-68).
+
+    Inference tensors (created under torch.inference_mode(), as the
+    reference's benchmarks run: benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:87)
+    carry no version counter, so for them "the very same input" means the same
+    tensor object only: an in-place change of that tensor between two
+    members' calls is not seen (the later member gets the output computed
+    before the change). Model code that modifies a Linear's input in place
+    between its siblings' calls should untie them (untie_siblings).
+
+    When a launch leaves outputs that no member claims before the next launch
+    (siblings fed different inputs, e.g. cross-attention's q from the decoder
+    and k/v from the encoder), the grouped launch streamed those members'
+    weights for nothing; the group warns once (RuntimeWarning) and keeps
+    serving calls, so results are unaffected.
     """
 
     def __init__(self, members):
@@ -275,6 +290,7 @@ class SiblingLaunch:
         self._x = None
         self._version = -1
         self._pending = {}
+        self._warned = False
 
     def _usable(self, x) -> bool:
         md = self.members[0].mat_data
@@ -287,15 +303,24 @@ class SiblingLaunch:
         if not self._usable(x):
             return None
         i = next(j for j, m in enumerate(self.members) if m is member)
-        if self._x is x and self._version == x._version and i in self._pending:
+        version = None if x.is_inference() else x._version  # inference tensors have no version counter
+        if self._x is x and self._version == version and i in self._pending:
             return self._pending.pop(i)
+        if self._pending and not self._warned:
+            self._warned = True
+            names = ", ".join(str(j) for j in sorted(self._pending))
+            warnings.warn(
+                f"nmsparse: a SiblingLaunch of {len(self.members)} Linears launched again while member(s) {names} "
+                "had not taken their outputs of its previous launch (siblings called with different inputs?); "
+                "those weights were streamed for nothing. Results are unaffected; untie_siblings(model) makes "
+                "every Linear launch on its own.", RuntimeWarning, stacklevel=3)
         from .hip_spmv import nmsparse_gemv_grouped
 
         m0 = self.members[0]
         outs = [torch.empty(*x.shape[:-1], m.h, dtype=x.dtype, device=x.device) for m in self.members]
         nmsparse_gemv_grouped(x.view(1, -1), [(m.mat_data, m.mat_index) for m in self.members], m0.block_width,
                               m0.vec_width, outs=[o.view(1, -1) for o in outs])
-        self._x, self._version = x, x._version
+        self._x, self._version = x, version
         self._pending = {j: o for j, o in enumerate(outs) if j != i}
         return outs[i]
 

@@ -317,6 +317,67 @@ def test_static_scratch_entry_rejections_before_any_hip_call():
     assert _lib.NM_STATIC_SCRATCH_BYTES == _lib.NM_TICKET_BYTES + (16 << 20)
 
 
+def test_carried_vec_out_must_not_overlap_any_launch_buffer():
+    """A carried consumer's tile-0 workgroups write vec_out while the other
+    workgroups still read the launch's inputs and write its outputs, so the
+    host rejects (NM_ERR_BAD_EPILOGUE) a vec_out that overlaps any of them:
+    norm weight, every matrix and index, every output (plain or heads
+    layout), residual, head norm, RoPE table, position, workspace, carry_in."""
+    VO = FAKE + (1 << 36)
+    K = 4096  # w = 2048 at 32:64
+    ok = dict(carry_in=FAKE, carry_splits=8, vec_out=VO)
+    pair = dict(kind=1, nprob=2, hs=(14336, 14336), norm_weight=FAKE)
+    inside = VO + 2 * K - 16   # the last 16 bytes of vec_out
+
+    def pair_with(**fields):
+        d = _desc(**pair, **ok)
+        for k, v in fields.items():
+            if k.startswith("p0_") or k.startswith("p1_"):
+                setattr(d.prob[int(k[1])], k[3:], v)
+            else:
+                setattr(d, k, v)
+        return d
+
+    def rejected(d):
+        return _lib.load().nm_gemv_launch_workspace_bytes(ctypes.byref(d)) > 0 and _launch(d) == -8
+
+    assert rejected(pair_with(norm_weight=inside))
+    assert rejected(pair_with(p0_mat_data=VO - 2 * 2048 * 14336 + 16))  # the gate matrix's last bytes
+    assert rejected(pair_with(p1_mat_data=inside))                       # the up matrix
+    assert rejected(pair_with(p1_mat_index=VO - 2048 + 16))
+    assert rejected(pair_with(p0_out=VO - 2 * 14336 + 16))               # the pair's output
+    assert rejected(pair_with(p0_residual=inside))
+    assert _launch(_desc(**pair, **ok), ws_bytes=(1 << 36) + 16) == -8   # the workspace at FAKE reaches vec_out
+    assert not rejected(pair_with(norm_weight=VO - 2 * K))             # ends where vec_out begins
+    assert not rejected(pair_with(p0_out=VO - 2 * 14336))
+    assert not rejected(pair_with(p0_residual=VO + 2 * K))             # begins where vec_out ends
+    # q/k/v consumer with heads layouts, head norms, the RoPE table and the position
+    qkv = dict(kind=0, nprob=3, hs=(4096, 1024, 1024), norm_weight=FAKE, head_dim=128, pos=FAKE, pos_limit=512,
+               rope_table=FAKE)
+
+    def qkv_with(**fields):
+        d = _desc(**qkv, **ok)
+        for i in range(3):
+            d.prob[i].rope = int(i < 2)
+        d.prob[1].head_stride, d.prob[1].elem_stride, d.prob[1].pos_stride = 160 * 512, 512, 1  # key cache
+        for k, v in fields.items():
+            if k[0] == "p" and k[2] == "_":
+                setattr(d.prob[int(k[1])], k[3:], v)
+            else:
+                setattr(d, k, v)
+        return d
+
+    assert _launch(qkv_with(), ws_bytes=1 << 20) != -8
+    # the key cache [8, 160, 512] ends at (7 * 160 * 512 + 127 * 512 + 511 + 1) elements past its base
+    extent = 2 * (7 * 160 * 512 + 127 * 512 + 512)
+    assert _launch(qkv_with(p1_out=VO - extent + 16), ws_bytes=1 << 20) == -8
+    assert _launch(qkv_with(p1_out=VO - extent), ws_bytes=1 << 20) != -8
+    assert _launch(qkv_with(p0_head_norm=VO - 2 * 128 + 16), ws_bytes=1 << 20) == -8
+    assert _launch(qkv_with(rope_table=VO - 512 * 64 * 8 + 16), ws_bytes=1 << 20) == -8
+    assert _launch(qkv_with(pos=VO), ws_bytes=1 << 20) == -8
+    assert _launch(qkv_with(p2_out=inside), ws_bytes=1 << 20) == -8
+
+
 def test_split_k_carry_rejections_and_plans_before_launch():
     """The carry descriptor fields: producer and consumer roles, their limits
     and the consumer's plan (whole groups, <= 512 columns and <= 1024
@@ -327,15 +388,16 @@ def test_split_k_carry_rejections_and_plans_before_launch():
 
     lib = _lib.load()
     pair = dict(kind=1, nprob=2, hs=(14336, 14336), norm_weight=FAKE)
-    ok = dict(carry_in=FAKE, carry_splits=8, vec_out=FAKE + 0x100000)
+    VO = FAKE + (1 << 36)  # far from every other placeholder range
+    ok = dict(carry_in=FAKE, carry_splits=8, vec_out=VO)
     # a consumer needs the input norm, 1..16 producer splits, M a multiple of 4, vec_out apart from vec
     assert _launch(_desc(**{**pair, "norm_weight": None}, **ok)) == -8
     assert _launch(_desc(**pair, **{**ok, "carry_splits": 0})) == -8
     assert _launch(_desc(**pair, **{**ok, "carry_splits": 17})) == -8
     assert _launch(_desc(**pair, **{**ok, "vec_out": None})) == -8
     assert _launch(_desc(**pair, **{**ok, "vec_out": FAKE})) == -8                  # overlaps vec
-    assert _launch(_desc(**pair, **{**ok, "carry_in": FAKE + 0x100000 - 16})) == -8  # vec_out inside carry_in
-    assert _launch(_desc(**pair, **{**ok, "vec_out": FAKE + 0x100008})) == -5       # misaligned
+    assert _launch(_desc(**pair, **{**ok, "carry_in": VO - 16})) == -8              # vec_out inside carry_in
+    assert _launch(_desc(**pair, **{**ok, "vec_out": VO + 8})) == -5                # misaligned
     assert _launch(_desc(**pair, **{**ok, "carry_in": FAKE + 4})) == -5
     assert _launch(_desc(**{**pair, "norm_weight": FAKE + 2}, **ok)) == -5
     assert _launch(_desc(**pair, **ok, m=6, nnz=3, w=2040)) == -8                    # M not a multiple of 4

@@ -556,6 +556,59 @@ def test_swap_ties_the_siblings_of_each_layout():
         tie_siblings(ff.w1, ff.w2)
 
 
+def test_sibling_bookkeeping_under_inference_mode_and_the_waste_warning(monkeypatch):
+    """The sibling group's host bookkeeping with the grouped launch replaced by a
+    CPU stand-in (the launch itself needs a GPU): inference tensors, which have
+    no version counter, are matched by identity (the reference's benchmarks run
+    under torch.inference_mode(): benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:87),
+    so q/k/v of one input are one launch there too; a launch that leaves outputs
+    unclaimed before the next one warns once (siblings fed different inputs)."""
+    import warnings
+
+    from spmv_decode_amd import hip_spmv
+    from spmv_decode_amd.nmsparse_linear import NmSparseLinear, SiblingLaunch, tie_siblings
+
+    mods = [NmSparseLinear(h, 64, 8, 40 + i, "cpu") for i, h in enumerate((128, 256, 128))]
+    dense = [m.to_dense(torch.float32) for m in mods]
+    launches = []
+
+    def grouped(vec, problems, nnz, m, outs):
+        launches.append(vec)
+        for (md, mi), o in zip(problems, outs):
+            j = next(k for k, mod in enumerate(mods) if mod.mat_data is md)
+            o.copy_((vec.float() @ dense[j].t()).to(o.dtype))
+        return outs
+
+    monkeypatch.setattr(hip_spmv, "nmsparse_gemv_grouped", grouped)
+    monkeypatch.setattr(SiblingLaunch, "_usable", lambda self, x: True)
+    tie_siblings(*mods)
+    g = torch.Generator().manual_seed(0)
+    with torch.inference_mode():
+        x = torch.randn(1, 1, 64, generator=g).half()
+        assert x.is_inference()
+        outs = [m(x) for m in mods]  # no "Inference tensors do not track version counter"
+        assert len(launches) == 1
+        for o, d in zip(outs, dense):
+            assert torch.equal(o.view(-1), (x.view(1, -1).float() @ d.t()).half().view(-1))
+        x2 = torch.randn(1, 1, 64, generator=g).half()
+        with warnings.catch_warnings():
+            warnings.simplefilter("error")  # every output was claimed: no warning
+            mods[1](x2), mods[0](x2), mods[2](x2)
+        assert len(launches) == 2
+    # outside inference mode the version counter still guards against in-place changes
+    x3 = torch.randn(1, 1, 64, generator=g).half()
+    mods[0](x3)
+    x3.mul_(2)
+    with pytest.warns(RuntimeWarning, match="streamed for nothing"):
+        y = mods[1](x3)  # relaunch: k and v of the first launch were never claimed
+    assert len(launches) == 4
+    assert torch.equal(y.view(-1), (x3.view(1, -1).float() @ dense[1].t()).half().view(-1))
+    with warnings.catch_warnings():
+        warnings.simplefilter("error")  # warned once per group
+        mods[0](x3.clone()), mods[0](x3.clone())
+    assert len(launches) == 6
+
+
 @pytest.mark.parametrize("V", [128256, 151936, 512, 1000, 97])
 def test_greedy_token_matches_argmax_with_ties(V):
     """The two-stage greedy argmax returns torch.argmax's index (the first

@@ -16,6 +16,14 @@ and rounding alone cost at this depth; every fp16 sparse structure must stay
 within twice that plus 1e-3, and two fp16 structures within three times that
 plus 1e-3 of each other. A wrong index, term or fusion moves the logits by
 orders of magnitude more.
+
+The configurations' own context lengths (test_decode_parity_at_the_configs_context):
+Llama-3.1-8B 32:64 with config 3's 128-token prompt in a 384-position cache and
+Qwen3-32B 16:32 with config 5's 512-token prompt in a 1024-position cache; the
+prompt through Decoder.prefill (every sparse Linear through the SpMM), then
+graph-replayed steps at positions 128+ / 512+, bitwise equal to the eager steps
+from the same caches, and every launch structure and both dense twins, each
+prefilled the same way, held to the same envelope at those positions.
 """
 import dataclasses
 import gc
@@ -176,6 +184,97 @@ def test_full_depth_decode_parity(gpu, name, M, layers):
     assert e16 < 0.05, e16  # the fp16 model tracks fp32 at this depth at all
     bound = 2 * e16 + 1e-3
     for k in ("fused", "per_linear", "grouped"):
+        assert err[k] <= bound, (k, err[k], bound)
+    assert cross <= 3 * e16 + 1e-3, cross
+    assert to_dense16 <= 3 * e16 + 1e-3, to_dense16
+    del model
+    _free()
+
+
+LONG_CASES = [  # (model, M, prompt tokens, positions): BASELINE configs 3 and 5
+    ("llama-3.1-8b", 64, 128, 128 + 256),
+    ("qwen3-32b", 32, 512, 512 + 512),
+]
+LONG_STEPS = 6
+
+
+@torch.no_grad()
+def prefilled_then_steps(model, prompt, fed, positions):
+    """Decoder.prefill of `prompt` into a cache for `positions`, then eager steps
+    feeding fed[i] at position P + i; fp32 logits [1 + len(fed), vocab], the
+    prompt's last position first."""
+    model.setup_cache(cache_length(positions), "cuda", dtype=model.embed_tokens.weight.dtype)
+    P = prompt.numel()
+    out = [model.prefill(prompt.to("cuda")).float().view(-1)]
+    for i in range(fed.numel()):
+        out.append(model.forward_step(fed[i].view(1, 1), torch.tensor([P + i], device="cuda")).float().view(-1))
+    return torch.stack(out)
+
+
+@pytest.mark.parametrize("name,M,P,positions", LONG_CASES, ids=lambda v: str(v))
+def test_decode_parity_at_the_configs_context(gpu, name, M, P, positions):
+    """Decode at the positions the benchmark configurations run at: the mask
+    rows of caches rounded up to whole 128 positions, the causal mask rewritten
+    every step, prefill-written keys and values (reference protocol:
+    benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:141-142,164-165,181-182)."""
+    cfg = CONFIGS[name]
+    tag = f"{name} {M // 2}:{M} prompt {P} positions {positions}"
+    _free()
+    say(f"{tag}: building the sparse model")
+    model = sparse_model(cfg, M, seed=M + P)
+    prompt = torch.randint(0, cfg.vocab, (P,), generator=torch.Generator().manual_seed(P))
+    gd = GraphDecoder(model, positions)
+    assert model.max_seq == cache_length(positions)
+    say(f"{tag}: prefill, then {LONG_STEPS} eager steps")
+    gd.run_prompt(prompt, batched=True)
+    prefill_logits = gd.logits.float().view(-1).clone()
+    snap_k, snap_v = model.k_store.clone(), [v.clone() for v in model.v_cache_t]
+    snap_tok, snap_tokens = gd.token.clone(), gd.tokens.clone()
+    eager = [gd.eager_step().clone() for _ in range(LONG_STEPS)]
+    assert all(bool(torch.isfinite(e).all()) for e in eager)
+    fed = gd.tokens[P:P + LONG_STEPS].clone()
+    eager_tokens = gd.tokens[P:P + LONG_STEPS + 1].clone()
+    say(f"{tag}: graph replays from the same caches")
+    gd.capture()
+    model.k_store.copy_(snap_k)
+    for v, sv in zip(model.v_cache_t, snap_v):
+        v.copy_(sv)
+    gd.token.copy_(snap_tok)
+    gd.tokens.copy_(snap_tokens)
+    gd.pos.fill_(P)
+    gd.host_pos = P
+    for i in range(LONG_STEPS):
+        gd.replay()
+        torch.cuda.synchronize()
+        assert torch.isfinite(gd.logits).all(), i
+        assert torch.equal(gd.logits, eager[i]), f"graph replay at position {P + i} differs from eager"
+    assert torch.equal(gd.tokens[P:P + LONG_STEPS + 1], eager_tokens)
+    del gd, snap_k, snap_v
+    _free()
+    logits = {"eager": torch.cat((prefill_logits.view(1, -1), torch.stack([e.float().view(-1) for e in eager])))}
+    for mode in Decoder.LAUNCH_MODES:
+        say(f"{tag}: prefill + teacher-forced {mode}")
+        model.set_launch_mode(mode)
+        logits[mode] = prefilled_then_steps(model, prompt, fed, positions)
+    model.set_launch_mode("fused")
+    for dtype in (torch.float32, torch.float16):
+        say(f"{tag}: masked dense twin {dtype}")
+        twin = dense_twin(model, dtype)
+        logits[f"dense_{str(dtype)[6:]}"] = prefilled_then_steps(twin, prompt, fed, positions)
+        del twin
+        _free()
+    ref = logits.pop("dense_float32")
+    e16 = rel_l2(logits["dense_float16"], ref)
+    err = {k: rel_l2(v, ref) for k, v in logits.items()}
+    cross = rel_l2(logits["fused"], logits["per_linear"])
+    to_dense16 = rel_l2(logits["eager"], logits["dense_float16"])
+    say(f"{tag}: rel-L2 of logits vs the fp32 dense twin (worst of the prefill and {LONG_STEPS} steps): "
+        + ", ".join(f"{k} {v:.2e}" for k, v in err.items())
+        + f"; fused vs per-Linear {cross:.2e}; eager vs fp16 dense twin {to_dense16:.2e}")
+    assert all(torch.isfinite(v).all() for v in logits.values())
+    assert e16 < 0.05, e16
+    bound = 2 * e16 + 1e-3
+    for k in ("eager", "fused", "per_linear", "grouped", "modules"):
         assert err[k] <= bound, (k, err[k], bound)
     assert cross <= 3 * e16 + 1e-3, cross
     assert to_dense16 <= 3 * e16 + 1e-3, to_dense16

@@ -250,6 +250,29 @@ def test_capture_without_warmup_owns_its_workspace(gpu):
     assert not default_ws[: _lib.NM_TICKET_BYTES].any()
 
 
+def test_capture_id_through_the_library(gpu):
+    """hip_spmv.capture_id asks the library's own HIP runtime (nm_stream_capture_id):
+    0 outside a capture, the same non-zero id throughout one capture, a new id for
+    the next capture on the same stream."""
+    s = torch.cuda.Stream()
+    assert hip_spmv.capture_id(s.cuda_stream) == 0
+    ids = []
+    for _ in range(2):
+        g = torch.cuda.CUDAGraph()
+        x = torch.zeros(16, device=gpu)
+        with torch.cuda.graph(g, stream=s):
+            first = hip_spmv.capture_id(s.cuda_stream)
+            x.add_(1.0)
+            assert hip_spmv.capture_id(s.cuda_stream) == first
+        ids.append(first)
+        g.replay()
+        torch.cuda.synchronize()
+        assert bool((x == 1.0).all())
+        del g
+    assert ids[0] != 0 and ids[1] != 0 and ids[0] != ids[1], ids
+    assert hip_spmv.capture_id(s.cuda_stream) == 0
+
+
 @pytest.mark.parametrize("m", [4, 64, 256])
 def test_fused_wqkv_width_default_plan(gpu, m):
     """gpt-fast fuses q/k/v into one 4096 -> 6144 Linear (model.py:196-198, 219), which
@@ -682,7 +705,8 @@ def test_tied_siblings_against_the_oracle(gpu, monkeypatch):
         check_parity(outs[i].view(1, -1), x.view(1, -1), mod.mat_data, mod.mat_index, 32, 64, f"tied {i}")
     x2 = x.clone()  # same values, another object: launched afresh
     assert torch.equal(mods[2](x2), outs[2]) and len(launches) == 2
-    assert torch.equal(mods[2](x2), outs[2]) and len(launches) == 3  # v again: no second hand-out
+    with pytest.warns(RuntimeWarning, match="streamed for nothing"):  # q and k of that launch never claimed
+        assert torch.equal(mods[2](x2), outs[2]) and len(launches) == 3  # v again: no second hand-out
     y_q = mods[0](x)  # launches for x (k, v pending) ...
     x.mul_(2)  # ... then the input changes in place: k must see the new values
     y_k = mods[1](x)
@@ -711,6 +735,42 @@ def test_tied_siblings_against_the_oracle(gpu, monkeypatch):
             check_parity(gouts[i].view(1, -1), xs.view(1, -1), mod.mat_data, mod.mat_index, 32, 64, f"graph {rep} {i}")
         assert torch.equal(mods[1](x.clone()), y_k)  # eager work between the replays
         torch.cuda.synchronize()
+
+
+def test_swapped_model_decodes_under_inference_mode(gpu):
+    """The reference's benchmarks swap the model and run it under
+    torch.inference_mode() (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:87,
+    132-140): the swapped decoder with its q/k/v and gate/up tied, every
+    projection called as a module, decodes one-row steps there with one grouped
+    launch per tied group, and its logits equal the same steps under no_grad."""
+    from spmv_decode_amd.decode.model import Decoder, init_weights_, tiny_config
+    from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
+
+    cfg = tiny_config(qk_norm=True)
+    model = Decoder(cfg).to(device="cuda", dtype=torch.float16)
+    init_weights_(model, seed=3)
+    swap_to_nmsparse(model, 16, "cuda", seed=5, init="device", keep_dense=False)
+    model.set_launch_mode("modules")
+    tokens = torch.randint(0, cfg.vocab, (6,), generator=torch.Generator().manual_seed(2)).cuda()
+
+    def run():
+        model.setup_cache(8, "cuda", dtype=torch.float16)
+        return torch.cat([model.forward_step(t.view(1, 1), torch.tensor([i], device="cuda"))
+                          for i, t in enumerate(tokens)])
+
+    with torch.no_grad():
+        ref = run()
+    real = hip_spmv.nmsparse_gemv_grouped
+    launches = []
+    hip_spmv.nmsparse_gemv_grouped = lambda *a, **k: launches.append(1) or real(*a, **k)
+    try:
+        with torch.inference_mode():
+            got = run()
+    finally:
+        hip_spmv.nmsparse_gemv_grouped = real
+    torch.cuda.synchronize()
+    assert len(launches) == 2 * cfg.n_layers * tokens.numel()  # q/k/v and gate/up: one launch each
+    assert torch.equal(got, ref)
 
 
 def test_module_under_torch_compile_matches_eager(gpu):
