@@ -590,9 +590,33 @@ def decode_ms_per_token(m, log):
     for mode in ("per_linear", "grouped", "modules"):
         model.set_launch_mode(mode)
         variants[mode] = run_variant(model, LLAMA31_8B, prompt, 256, f"sparse {mode}", log)
+    # the unmodified model (every projection a module call) compiled: the compile pass groups its siblings
+    model.set_launch_mode("modules")
+    fixed_mod = fixed_context_ms(model, 512)
+    fixed_mod_c = compiled_fixed(model, fixed_mod, ref32_sparse, "sparse unmodified model (HF names)")
     model.set_launch_mode("fused")
     ref_dense, ref_sparse = REFERENCE_A100_CTX512["llama-3.1-8b"]
     del model
+    torch.cuda.empty_cache()
+    # the same under gpt-fast's names (the reference benchmark's model: fused wqkv, w1/w3/w2)
+    t0 = time.time()
+    prev = torch.get_default_dtype()
+    torch.set_default_dtype(torch.float16)
+    try:
+        with torch.device("cuda:0"):
+            gf = Decoder(LLAMA31_8B, layout="gpt-fast")
+    finally:
+        torch.set_default_dtype(prev)
+    init_weights_(gf, seed=0)
+    fixed_gf_dense = fixed_context_ms(gf, 512)
+    fixed_gf_dense_c = compiled_fixed(gf, fixed_gf_dense, fixed_context_logits_fp32(gf, 512), "dense (gpt-fast names)")
+    swap_to_nmsparse(gf, m, "cuda", seed=0, init="device", keep_dense=False)
+    torch.cuda.empty_cache()
+    fixed_gf = fixed_context_ms(gf, 512)
+    fixed_gf_c = compiled_fixed(gf, fixed_gf, fixed_context_logits_fp32(gf, 512), "sparse unmodified model (gpt-fast names)")
+    log(f"gpt-fast-named model: dense {fixed_gf_dense['median']:.4f} ms (compiled {fixed_gf_dense_c['median']:.4f}), "
+        f"sparse {fixed_gf['median']:.4f} ms (compiled {fixed_gf_c['median']:.4f}) in {time.time() - t0:.0f} s")
+    del gf
     torch.cuda.empty_cache()
     ms = {k: v["ms_per_token"] for k, v in dense_by_fusion.items()}
     fastest_dense = min(ms.values())
@@ -668,6 +692,26 @@ def decode_ms_per_token(m, log):
                "reference_a100_published": {"dense_ms_per_token": ref_dense, "sparse_ms_per_token": ref_sparse.get(m),
                                             "speedup": round(ref_dense / ref_sparse[m], 4) if m in ref_sparse else None,
                                             "source": "README.md:86-93"}},
+           "compiled_unmodified_model": {
+               "protocol": "the fixed-context protocol above, torch.compile (inductor, fullgraph) of the step of the "
+                           "model as written for dense Linears, swapped by swap_to_nmsparse: every projection a module "
+                           "call; the compile pass (spmv_decode_amd/compile_pass.py) turns each layer's sibling gemv "
+                           "calls into one grouped q/k/v launch (HF names) and one gate/up pair launch with SiLU*mul",
+               "hf_names": {"sparse_ms_per_token": _finite(fixed_mod_c["median"]),
+                            "eager_sparse_ms_per_token": round(fixed_mod["median"], 4),
+                            "speedup_vs_fastest_compiled_dense": ratio(fastest_fcc, fixed_mod_c["median"]),
+                            "matches_eager": fixed_mod_c.get("matches_eager")},
+               "gpt_fast_names": {"dense_ms_per_token": _finite(fixed_gf_dense_c["median"]),
+                                  "sparse_ms_per_token": _finite(fixed_gf_c["median"]),
+                                  "speedup_vs_its_dense": ratio(fixed_gf_dense_c["median"], fixed_gf_c["median"]),
+                                  "speedup_vs_fastest_compiled_dense": ratio(min(fastest_fcc,
+                                                                                 fixed_gf_dense_c["median"]),
+                                                                             fixed_gf_c["median"]),
+                                  "eager_dense_ms_per_token": round(fixed_gf_dense["median"], 4),
+                                  "eager_sparse_ms_per_token": round(fixed_gf["median"], 4),
+                                  "matches_eager": {"dense": fixed_gf_dense_c.get("matches_eager"),
+                                                    "sparse": fixed_gf_c.get("matches_eager")}},
+               "errors": [r["error"] for r in (fixed_mod_c, fixed_gf_dense_c, fixed_gf_c) if "error" in r] or None},
            "headline": {"speedup": ratio(fastest_fcc, fixed_sparse_c["median"]),
                         "what": "sparse over the fastest of the three dense launch structures, both compiled, "
                                 "under the reference benchmark's fixed-context protocol (CTX 512, sampling)"}}

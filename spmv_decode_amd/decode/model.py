@@ -33,6 +33,11 @@ kernel costs a few microseconds: the q/k/v projections write into slices of
 one buffer, so the rotary embedding runs once over queries and keys; the
 attention scale and causal mask are folded into one batched product.
 
+`Decoder(cfg, layout="gpt-fast")` names the layers as gpt-fast does (the
+reference benchmark's model.py: `attention.wqkv` / `wo`, `feed_forward.w1` /
+`w3` / `w2`, `attention_norm`, `ffn_norm`); those layers call every projection
+as a module, as unmodified model code does.
+
 When every projection of every layer is an `NmSparseLinear` (after
 `swap_to_nmsparse`), `forward_step` runs the fused layer instead
 (`fuse_epilogues`, on by default): the input RMSNorm, Qwen3's q/k norms, the
@@ -276,19 +281,29 @@ class Attention(nn.Module):
         else:
             for proj, sl in zip(projs, slices):
                 linear_into(proj, x2d, sl)
-        qk = qkv[0, :qd + kvd].view(c.n_heads + c.n_kv_heads, c.head_dim)
-        if c.qk_norm:
-            qk = torch.cat((self.q_norm(qk[:c.n_heads]), self.k_norm(qk[c.n_heads:])))
-        qk = rotate(qk, freqs)
-        q, k = qk[:c.n_heads], qk[c.n_heads:]
-        v = qkv[0, qd + kvd:].view(c.n_kv_heads, c.head_dim, 1)
-        q_pad[:, :c.head_dim].copy_(q)
-        k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
-        v_cache_t.index_copy_(2, pos, v)
-        y = attend(q_pad, k_cache_t, v_cache_t, c, zero)  # [kvh, g, head_dim]
+        y = attention_core(self, qkv, freqs, k_cache_t, v_cache_t, pos, q_pad, zero)  # [kvh, g, head_dim]
         if self.call_modules:
             return self.o_proj(y.view(1, 1, qd))
         return project(self.o_proj, y.view(1, 1, qd))
+
+
+def attention_core(at, qkv, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
+    """The attention of one decode token from its projections qkv [1, q + k + v]
+    (at: the attention module, for its config and Qwen3's q/k norms): head
+    norms, rotary embedding, the cache write at `pos`, attend. Returns
+    [kv_heads, g, head_dim]."""
+    c = at.cfg
+    qd, kvd = c.n_heads * c.head_dim, c.n_kv_heads * c.head_dim
+    qk = qkv[0, :qd + kvd].view(c.n_heads + c.n_kv_heads, c.head_dim)
+    if c.qk_norm:
+        qk = torch.cat((at.q_norm(qk[:c.n_heads]), at.k_norm(qk[c.n_heads:])))
+    qk = rotate(qk, freqs)
+    q, k = qk[:c.n_heads], qk[c.n_heads:]
+    v = qkv[0, qd + kvd:].view(c.n_kv_heads, c.head_dim, 1)
+    q_pad[:, :c.head_dim].copy_(q)
+    k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
+    v_cache_t.index_copy_(2, pos, v)
+    return attend(q_pad, k_cache_t, v_cache_t, c, zero)
 
 
 class MLP(nn.Module):
@@ -333,11 +348,64 @@ class Block(nn.Module):
         return h + self.mlp(self.post_attention_layernorm(h))
 
 
+class GptFastAttention(nn.Module):
+    """Attention under gpt-fast's names (the reference's model.py:191-246): one
+    fused `wqkv` Linear [q + k + v rows] and `wo`; Qwen3's q/k norms when the
+    config has them. Same math as Attention; every projection is a module call,
+    as unmodified gpt-fast code makes it."""
+
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.cfg = cfg
+        qd, kvd = cfg.n_heads * cfg.head_dim, cfg.n_kv_heads * cfg.head_dim
+        self.wqkv = nn.Linear(cfg.dim, qd + 2 * kvd, bias=False)
+        self.wo = nn.Linear(qd, cfg.dim, bias=False)
+        if cfg.qk_norm:
+            self.q_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
+            self.k_norm = RMSNorm(cfg.head_dim, cfg.norm_eps)
+
+    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
+        y = attention_core(self, self.wqkv(x).view(1, -1), freqs, k_cache_t, v_cache_t, pos, q_pad, zero)
+        return self.wo(y.view(1, 1, -1))
+
+
+class GptFastFeedForward(nn.Module):
+    """The SiLU-gated MLP under gpt-fast's names (the reference's model.py:248-256):
+    w2(silu(w1(x)) * w3(x)), each a module call."""
+
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.w1 = nn.Linear(cfg.dim, cfg.inter, bias=False)
+        self.w3 = nn.Linear(cfg.dim, cfg.inter, bias=False)
+        self.w2 = nn.Linear(cfg.inter, cfg.dim, bias=False)
+
+    def forward(self, x):
+        return self.w2(F.silu(self.w1(x)) * self.w3(x))
+
+
+class GptFastBlock(nn.Module):
+    """A decoder layer under gpt-fast's names (the reference's model.py:177-189):
+    attention_norm, attention, ffn_norm, feed_forward."""
+
+    def __init__(self, cfg: DecoderConfig):
+        super().__init__()
+        self.attention_norm = RMSNorm(cfg.dim, cfg.norm_eps)
+        self.attention = GptFastAttention(cfg)
+        self.ffn_norm = RMSNorm(cfg.dim, cfg.norm_eps)
+        self.feed_forward = GptFastFeedForward(cfg)
+
+    def forward(self, x, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
+        h = x + self.attention(self.attention_norm(x), freqs, k_cache_t, v_cache_t, pos, q_pad, zero)
+        return h + self.feed_forward(self.ffn_norm(h))
+
+
 def fusable(block: Block) -> bool:
     """True when the block's projections can run as the fused sparse layer:
     q/k/v and gate/up each share one launch, o and down are sparse too."""
     from ..nmsparse_linear import NmSparseLinear
 
+    if not isinstance(block, Block):
+        return False
     at, mlp = block.self_attn, block.mlp
     return (grouped_sparse((at.q_proj, at.k_proj, at.v_proj)) and grouped_sparse((mlp.gate_proj, mlp.up_proj))
             and isinstance(at.o_proj, NmSparseLinear) and isinstance(mlp.down_proj, NmSparseLinear))
@@ -447,18 +515,29 @@ def fused_layers_carried(layers, x2d, h2d, carry_o, carry_d, k_caches, v_caches,
 
 class Decoder(nn.Module):
     """Decoder stack with a static KV cache; `model.layers` is what
-    `swap_to_nmsparse` walks."""
+    `swap_to_nmsparse` walks. layout="hf" (default) builds Hugging Face-named
+    blocks (Block: self_attn.{q,k,v,o}_proj, mlp.{gate,up,down}_proj), which
+    every launch mode and the fused sparse layer serve; layout="gpt-fast"
+    builds gpt-fast-named blocks (GptFastBlock: attention.wqkv / wo,
+    feed_forward.w1 / w3 / w2, the reference benchmark's model), which always
+    call their projections as modules (the unmodified-model path)."""
 
-    def __init__(self, cfg: DecoderConfig):
+    LAYOUTS = ("hf", "gpt-fast")
+
+    def __init__(self, cfg: DecoderConfig, layout: str = "hf"):
         super().__init__()
+        if layout not in self.LAYOUTS:
+            raise ValueError(f"layout must be one of {self.LAYOUTS}, got {layout!r}")
         self.cfg = cfg
+        self.layout = layout
         self.fuse_epilogues = True
         # Fused sparse layers: carry o_proj's / down_proj's split-K reduction
         # into the next launch where the shapes allow (fused_layers_carried).
         self.carry_splitk = True
         self._carry = None  # (key, x2d-independent buffers) set up by _carry_buffers
         self.embed_tokens = nn.Embedding(cfg.vocab, cfg.dim)
-        self.layers = nn.ModuleList(Block(cfg) for _ in range(cfg.n_layers))
+        block = Block if layout == "hf" else GptFastBlock
+        self.layers = nn.ModuleList(block(cfg) for _ in range(cfg.n_layers))
         self.norm = RMSNorm(cfg.dim, cfg.norm_eps)
         self.lm_head = nn.Linear(cfg.dim, cfg.vocab, bias=False)
         self.max_seq = 0
@@ -479,6 +558,8 @@ class Decoder(nn.Module):
             raise ValueError(f"launch mode must be one of {self.LAUNCH_MODES}, got {mode!r}")
         self.fuse_epilogues = mode == "fused"
         for blk in self.layers:
+            if not isinstance(blk, Block):
+                continue  # gpt-fast blocks always call their projections as modules
             blk.self_attn.group_launches = blk.mlp.group_launches = mode in ("fused", "grouped")
             blk.self_attn.call_modules = blk.mlp.call_modules = mode == "modules"
 
@@ -497,6 +578,8 @@ class Decoder(nn.Module):
         self.dense_fusion = mode
         with torch.no_grad():
             for blk in self.layers:
+                if not isinstance(blk, Block):
+                    continue  # gpt-fast blocks: wqkv is one Linear already
                 at, mlp = blk.self_attn, blk.mlp
                 projs = (at.q_proj, at.k_proj, at.v_proj)
                 at.wqkv = (torch.cat([p.weight for p in projs])
@@ -511,6 +594,8 @@ class Decoder(nn.Module):
         multiplies with dense_gemv: bias-free nn.Linears and the fused copies."""
         sites = []
         for blk in self.layers:
+            if not isinstance(blk, Block):
+                continue  # gpt-fast blocks call nn.Linear's own forward
             at, mlp = blk.self_attn, blk.mlp
             for mod in (at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj):
                 if type(mod) is nn.Linear and mod.bias is None:
@@ -592,6 +677,9 @@ class Decoder(nn.Module):
         layers when nothing was."""
         if not self.layers or not hasattr(self, "q_pad"):
             return
+        if not all(isinstance(b, Block) for b in self.layers):
+            self._carry = ("gpt-fast", None)  # the fused path needs q/k/v as separate matrices
+            return
         at, mlp = self.layers[0].self_attn, self.layers[0].mlp
         o, d = at.o_proj, mlp.down_proj
         dev, dt = self.q_pad.device, self.q_pad.dtype
@@ -642,21 +730,30 @@ class Decoder(nn.Module):
         hd = c.head_dim
         x = self.embed_tokens(ids)  # [P, dim]
         freqs = self.rope[:P].view(P, 1, -1)
+        qd, kvd = c.n_heads * hd, c.n_kv_heads * hd
         for i, blk in enumerate(self.layers):
-            at, mlp = blk.self_attn, blk.mlp
-            h = blk.input_layernorm(x)
-            q = project_rows(at.q_proj, h).view(P, c.n_heads, hd)
-            k = project_rows(at.k_proj, h).view(P, c.n_kv_heads, hd)
-            v = project_rows(at.v_proj, h).view(P, c.n_kv_heads, hd)
+            if isinstance(blk, Block):
+                at, mlp = blk.self_attn, blk.mlp
+                ln1, ln2, o_proj = blk.input_layernorm, blk.post_attention_layernorm, at.o_proj
+                gate, up, down = mlp.gate_proj, mlp.up_proj, mlp.down_proj
+                h = ln1(x)
+                q, k, v = (project_rows(p, h) for p in (at.q_proj, at.k_proj, at.v_proj))
+            else:  # gpt-fast names
+                at, ff = blk.attention, blk.feed_forward
+                ln1, ln2, o_proj = blk.attention_norm, blk.ffn_norm, at.wo
+                gate, up, down = ff.w1, ff.w3, ff.w2
+                h = ln1(x)
+                q, k, v = project_rows(at.wqkv, h).split([qd, kvd, kvd], dim=-1)
+            q, k, v = q.reshape(P, c.n_heads, hd), k.reshape(P, c.n_kv_heads, hd), v.reshape(P, c.n_kv_heads, hd)
             if c.qk_norm:
                 q, k = at.q_norm(q), at.k_norm(k)
             q, k = rotate(q, freqs), rotate(k, freqs)
             self.k_cache_t[i][:, :hd, :P].copy_(k.permute(1, 2, 0))
             self.v_cache_t[i][:, :, :P].copy_(v.permute(1, 2, 0))
-            x = x + project_rows(at.o_proj, causal_attention(q, k, v, c.n_kv_heads))
-            h = blk.post_attention_layernorm(x)
-            act = F.silu(project_rows(mlp.gate_proj, h)) * project_rows(mlp.up_proj, h)
-            x = x + project_rows(mlp.down_proj, act)
+            x = x + project_rows(o_proj, causal_attention(q, k, v, c.n_kv_heads))
+            h = ln2(x)
+            act = F.silu(project_rows(gate, h)) * project_rows(up, h)
+            x = x + project_rows(down, act)
         return project(self.lm_head, self.norm(x[-1:].view(1, 1, -1))).view(1, -1)
 
     def forward_step(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:

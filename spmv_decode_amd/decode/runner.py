@@ -91,12 +91,19 @@ def fixed_context_logits_fp32(model: Decoder, ctx: int, seed: int = 1234, token_
                               device="cuda") -> torch.Tensor:
     """The logits of fixed_context_ms's step computed in fp32 throughout: the
     same weights and cache values (drawn in the model's dtype exactly as
-    fixed_context_ms draws them, then widened, which is exact), every
-    activation fp32, one eager step. The fp32 reference against which the
-    fp16 steps (eager and compiled) are held (fp16 rounding envelope). The
+    fixed_context_ms draws them, then widened, which is exact), every sparse
+    projection replaced for the step by an fp32 nn.Linear holding its masked
+    dense weight (NmSparseLinear.to_dense: the packed weights scattered back),
+    every activation fp32, one eager step. The fp32 reference against which
+    the fp16 steps (eager and compiled) are held (fp16 rounding envelope). The
     model is widened in place for the step and narrowed back afterwards (an
-    exact round trip: every weight is an fp16 value); its dense fusion copies
-    are rebuilt both ways. Returns fp32 logits [1, vocab] on the host."""
+    exact round trip: every weight is an fp16 value), its sparse projections
+    put back and its dense fusion copies rebuilt. Returns fp32 logits
+    [1, vocab] on the host."""
+    import torch.nn as nn
+
+    from ..nmsparse_linear import NmSparseLinear
+
     dev = torch.device(device)
     dt = model.embed_tokens.weight.dtype
     hd = model.cfg.head_dim
@@ -104,7 +111,15 @@ def fixed_context_logits_fp32(model: Decoder, ctx: int, seed: int = 1234, token_
     keys = model.k_store[:, :, :hd].clone()
     vals = [v.clone() for v in model.v_cache_t]
     fusion = model.dense_fusion
+    swapped = []
     try:
+        for mod in list(model.modules()):
+            for name, child in list(mod.named_children()):
+                if isinstance(child, NmSparseLinear):
+                    dense = nn.Linear(1, 1, bias=False, device="meta")
+                    dense.weight = nn.Parameter(child.to_dense(torch.float32), requires_grad=False)
+                    setattr(mod, name, dense)
+                    swapped.append((mod, name, child))
         model.float()
         model.set_dense_fusion(fusion)
         model.setup_cache(cache_length(ctx + 1), dev, dtype=torch.float32)
@@ -116,6 +131,8 @@ def fixed_context_logits_fp32(model: Decoder, ctx: int, seed: int = 1234, token_
         pos = torch.full((1,), ctx, dtype=torch.long, device=dev)
         logits = model.forward_step(token, pos).float().cpu()
     finally:
+        for mod, name, child in swapped:
+            setattr(mod, name, child)
         model.to(dt)
         model.set_dense_fusion(fusion)
         model.setup_cache(cache_length(ctx + 1), dev, dtype=dt)

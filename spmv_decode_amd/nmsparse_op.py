@@ -23,6 +23,12 @@ The split-K carry between a layer's launches adds `nmsparse::gemv_partials_`
 `_carried` forms of the q/k/v and gate/up launches, which finish their input
 from those partials and the residual stream (mutating vec_out).
 
+`nmsparse::gemv_grouped` (one launch for 2-4 gemv calls on the same input)
+and `nmsparse::gemv_silu_mul` (silu(gemv gate) * gemv up in one launch) are
+what the torch.compile pass of compile_pass.py rewrites sibling `gemv` calls
+into, so that unmodified model code compiled with torch.compile gets one
+q/k/v and one gate/up launch per layer (no reference counterpart).
+
 Backend selection keeps the reference's `NM_KERNEL` contract of refusing
 unknown values (src/spmv/nmsparse_op.py:20-22). Unset, "hip" and
 "triton_ptx" all select the one shared-mask HIP kernel. `_mode` reads
@@ -42,8 +48,9 @@ import torch
 
 from typing import Optional
 
-from .hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_gemv_partials,
-                       nmsparse_qkv_decode, nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip)
+from .hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_grouped, nmsparse_gemv_launch,
+                       nmsparse_gemv_partials, nmsparse_qkv_decode, nmsparse_spmm_forward_hip,
+                       nmsparse_spmv_forward_hip)
 
 _kernel = os.environ.get("NM_KERNEL", "")
 if _kernel not in ("", "hip", "triton_ptx", "guarded", "fp16", "fp16_split"):
@@ -89,6 +96,55 @@ def spmm(x: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor,
 
 @spmm.register_fake
 def _(x, mat_data, mat_index, w, h, block_width, vec_width):
+    return x.new_empty((*x.shape[:-1], int(h)))
+
+
+def _decode_rows(x: torch.Tensor, name: str) -> torch.Tensor:
+    """x as one fp16 row [1, K], with gemv's rows check and cast."""
+    K = x.shape[-1]
+    x2d = x.reshape(-1, K).contiguous()
+    if x2d.shape[0] != 1:
+        raise RuntimeError(f"nmsparse {name} only supports decode (rows==1), got {tuple(x2d.shape)}")
+    return x2d if x2d.dtype == torch.float16 else x2d.to(torch.float16)
+
+
+def _fp16(t: torch.Tensor) -> torch.Tensor:
+    return t if t.dtype == torch.float16 else t.to(torch.float16)
+
+
+@torch.library.custom_op("nmsparse::gemv_grouped", mutates_args=())
+def gemv_grouped(x: torch.Tensor, mat_data: list[torch.Tensor], mat_index: list[torch.Tensor], w: int,
+                 h: list[int], block_width: int, vec_width: int) -> list[torch.Tensor]:
+    """[gemv(x, mat_data[i], mat_index[i], w, h[i], ...) for i] as one launch
+    (2-4 problems sharing x, w and N:M; hip_spmv.nmsparse_gemv_grouped), with
+    gemv's rows check, casts and output shapes. What the compile pass
+    (compile_pass.group_sibling_gemvs) puts in place of sibling gemv calls."""
+    xh = _decode_rows(x, "gemv_grouped")
+    outs = nmsparse_gemv_grouped(xh, [(_fp16(md), mi) for md, mi in zip(mat_data, mat_index)], int(block_width),
+                                 int(vec_width))
+    return [o.to(dtype=x.dtype).reshape(*x.shape[:-1], int(hi)) for o, hi in zip(outs, h)]
+
+
+@gemv_grouped.register_fake
+def _(x, mat_data, mat_index, w, h, block_width, vec_width):
+    return [x.new_empty((*x.shape[:-1], int(hi))) for hi in h]
+
+
+@torch.library.custom_op("nmsparse::gemv_silu_mul", mutates_args=())
+def gemv_silu_mul(x: torch.Tensor, gate_data: torch.Tensor, gate_index: torch.Tensor, up_data: torch.Tensor,
+                  up_index: torch.Tensor, w: int, h: int, block_width: int, vec_width: int) -> torch.Tensor:
+    """silu(gemv(x, gate)) * gemv(x, up) as one launch of the gate/up pair
+    kernel (fp32 sums, SiLU and product, one rounding to fp16), with gemv's
+    rows check, casts and output shape. What the compile pass puts in place of
+    a SiLU-gated pair of sibling gemv calls."""
+    xh = _decode_rows(x, "gemv_silu_mul")
+    y = nmsparse_gate_up_silu(xh, (_fp16(gate_data), gate_index), (_fp16(up_data), up_index), int(block_width),
+                              int(vec_width))
+    return y.to(dtype=x.dtype).reshape(*x.shape[:-1], int(h))
+
+
+@gemv_silu_mul.register_fake
+def _(x, gate_data, gate_index, up_data, up_index, w, h, block_width, vec_width):
     return x.new_empty((*x.shape[:-1], int(h)))
 
 
@@ -193,5 +249,5 @@ def _(x, carry, vec_out, gate_data, gate_index, up_data, up_index, block_width, 
     return x.new_empty((1, gate_data.shape[1]))
 
 
-__all__ = ["gemv", "spmm", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_", "qkv_decode_carried",
+__all__ = ["gemv", "spmm", "gemv_grouped", "gemv_silu_mul", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_", "qkv_decode_carried",
            "gate_up_silu_carried"]

@@ -757,3 +757,50 @@ def test_carry_is_chosen_only_where_the_plans_take_it():
             lin.mat_index = lin.mat_index.reshape(-1, 2)
     sparse.prepare_decode()
     assert sparse._carry[0] != key
+
+
+def test_fixed_context_fp32_reference_and_envelope():
+    """The fp32 reference of the fixed-context step (runner.fixed_context_logits_fp32)
+    of a sparse model is its masked dense twin's step in fp32 on the same cache
+    values, and the model comes back unchanged (fp16, its NmSparseLinear
+    modules and ties); logits_envelope accepts what rounds like the eager step
+    and rejects a planted error."""
+    from spmv_decode_amd.decode.runner import _fill_fixed_context, fixed_context_logits_fp32, logits_envelope
+    from spmv_decode_amd.nmsparse_linear import NmSparseLinear
+
+    cfg = tiny_config(qk_norm=True)
+    model = Decoder(cfg).half()
+    init_weights_(model, seed=2)
+    swap_to_nmsparse(model, 8, "cpu", seed=4, keep_dense=False)
+    before = {k: v.clone() for k, v in model.state_dict().items()}
+    ref = fixed_context_logits_fp32(model, 20, device="cpu")
+    after = model.state_dict()
+    assert list(after) == list(before) and all(torch.equal(after[k], before[k]) for k in before)
+    assert after["layers.0.self_attn.q_proj.mat_data"].dtype == torch.float16
+    assert isinstance(model.layers[0].mlp.up_proj, NmSparseLinear)
+    assert model.layers[0].mlp.up_proj.__dict__["_siblings"].members[0] is model.layers[0].mlp.gate_proj
+    # the same step by hand: an fp32 dense twin on the same (fp16-drawn) caches
+    twin = Decoder(cfg)
+    sd = {k: v.float() for k, v in before.items() if ".mat_" not in k}
+    for i, blk in enumerate(model.layers):
+        for sub, names in (("self_attn", ("q_proj", "k_proj", "v_proj", "o_proj")),
+                           ("mlp", ("gate_proj", "up_proj", "down_proj"))):
+            for n in names:
+                sd[f"layers.{i}.{sub}.{n}.weight"] = getattr(getattr(blk, sub), n).to_dense(torch.float32)
+    twin.load_state_dict(sd)
+    _fill_fixed_context(model, 20, 1234, torch.device("cpu"))
+    keys, vals = model.k_store[:, :, :cfg.head_dim].float(), [v.float() for v in model.v_cache_t]
+    twin.setup_cache(model.max_seq, "cpu", dtype=torch.float32)
+    twin.k_store[:, :, :cfg.head_dim].copy_(keys)
+    for v, s in zip(twin.v_cache_t, vals):
+        v.copy_(s)
+    with torch.no_grad():
+        want = twin.forward_step(torch.full((1, 1), 123), torch.tensor([20]))
+    torch.testing.assert_close(ref, want, rtol=1e-6, atol=1e-6)
+    # the envelope: an fp16 rounding of the reference passes, a planted error does not
+    e16 = ref.half().float() + 1e-3 * torch.randn(ref.shape, generator=torch.Generator().manual_seed(0))
+    ok = logits_envelope(e16, ref.half().float(), ref)
+    assert ok["within"] and ok["same_greedy_token"] in (True, False)
+    bad = ref.clone()
+    bad[0, :50] += 10 * ref.abs().max()
+    assert not logits_envelope(e16, bad, ref)["within"]

@@ -773,6 +773,61 @@ def test_swapped_model_decodes_under_inference_mode(gpu):
     assert torch.equal(got, ref)
 
 
+@pytest.mark.parametrize("layout", ["hf", "gpt-fast"])
+def test_compiled_unmodified_model_groups_siblings(gpu, layout, monkeypatch):
+    """The unmodified model (every projection called as a module) after the swap,
+    compiled with inductor (fullgraph, as the reference benchmark compiles its
+    step: benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:155): the compile pass
+    gives each layer 4 launches (HF names: q/k/v grouped, o, the gate/up pair
+    with SiLU*mul, down; gpt-fast names: wqkv, wo, the w1/w3 pair, w2), counted
+    at the library calls of one compiled step, and its logits agree with the
+    eager steps' (which launch through the sibling ties) within fp16 rounding."""
+    from spmv_decode_amd import nmsparse_op
+    from spmv_decode_amd.decode.model import Decoder, init_weights_, tiny_config
+    from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
+
+    cfg = tiny_config(qk_norm=True, n_layers=3)
+    model = Decoder(cfg, layout=layout).to(device="cuda", dtype=torch.float16)
+    init_weights_(model, seed=7)
+    swap_to_nmsparse(model, 16, "cuda", seed=9, init="device", keep_dense=False)
+    model.set_launch_mode("modules")
+    tokens = torch.randint(0, cfg.vocab, (5,), generator=torch.Generator().manual_seed(4)).cuda()
+
+    def run(step):
+        model.setup_cache(8, "cuda", dtype=torch.float16)
+        return torch.cat([step(t.view(1, 1), torch.tensor([i], device="cuda")) for i, t in enumerate(tokens)])
+
+    with torch.no_grad():
+        eager = run(model.forward_step)
+        torch._dynamo.reset()
+        compiled = torch.compile(model.forward_step, fullgraph=True, dynamic=False)
+        try:
+            say(f"compiling the {layout} step")
+            run(compiled)  # compile once
+            counts = {}
+            for name in ("nmsparse_spmv_forward_hip", "nmsparse_gemv_grouped", "nmsparse_gate_up_silu"):
+                real = getattr(nmsparse_op, name)
+
+                def counted(*a, _real=real, _name=name, **k):
+                    counts[_name] = counts.get(_name, 0) + 1
+                    return _real(*a, **k)
+
+                monkeypatch.setattr(nmsparse_op, name, counted)
+            got = run(compiled)
+        finally:
+            torch._dynamo.reset()
+    torch.cuda.synchronize()
+    L, T = cfg.n_layers, tokens.numel()
+    want = ({"nmsparse_gemv_grouped": L * T, "nmsparse_gate_up_silu": L * T, "nmsparse_spmv_forward_hip": 2 * L * T}
+            if layout == "hf" else {"nmsparse_gate_up_silu": L * T, "nmsparse_spmv_forward_hip": 3 * L * T})
+    assert counts == want, counts
+    assert torch.isfinite(got).all()
+    rel = float((got.float() - eager.float()).norm() / eager.float().norm())
+    say(f"{layout}: compiled vs eager logits rel-L2 {rel:.2e}")
+    assert rel <= 5e-3, rel
+    torch.testing.assert_close(got.float(), eager.float(), rtol=2e-2, atol=2e-2)
+
+
 def test_module_under_torch_compile_matches_eager(gpu):
     """The reference benchmarks compile the model around the op
     (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:155): a full-graph
