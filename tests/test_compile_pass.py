@@ -135,6 +135,7 @@ def test_installed_pass_runs_inside_inductor(monkeypatch):
         return n
 
     monkeypatch.setattr(compile_pass, "group_sibling_gemvs", spy)
+    monkeypatch.setattr(ic, "force_disable_caches", True)  # a cached compile would not run the pass again
     q, k, v = (NmSparseLinear(h, 128, 8, i, "cpu") for i, h in enumerate((256, 128, 128)))
     w1, w3, w2 = NmSparseLinear(256, 128, 8, 5, "cpu"), NmSparseLinear(256, 128, 8, 6, "cpu"), \
         NmSparseLinear(128, 256, 8, 7, "cpu")
