@@ -424,6 +424,10 @@ def main():
                                 "us_per_launch": round(us, 3), "us_per_row": round(us / batch, 3),
                                 "speedup_per_row_vs_batch1": round(b1 * batch / us, 3),
                                 "weight_GBps": round(sparse_bytes(K, h, nnz, m) / (us * 1e-6) / 1e9, 1)}
+            if batch > 8:  # the library route beside it: gather + one hipBLASLt GEMM of [batch, w] x [w, h]
+                lib_us = MB.time_gather_gemm(h, K, nnz, m, batch, reps=reps)
+                rows[str(batch)]["gather_plus_hipblaslt_us"] = round(lib_us, 3)
+                rows[str(batch)]["speedup_vs_gather_plus_hipblaslt"] = round(lib_us / us, 3)
             log(f"spmm {cls:8s} batch {batch}: {us:7.2f} us/launch, {us / batch:6.2f} us/row "
                 f"({rows[str(batch)]['speedup_per_row_vs_batch1']}x per row vs batch 1)")
         spmm[cls] = rows

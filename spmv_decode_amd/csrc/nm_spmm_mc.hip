@@ -67,7 +67,10 @@ __device__ inline f4 mfma16x16x32<NM_DTYPE_BF16>(s8 a, s8 b, f4 c) {
 // l % 16, K elements 8*(l/16) .. +7; D[16 x 16]: column l % 16, rows
 // 4*(l/16) .. +3.
 // LDS stages of the DMA variant per tile width: about 64 KB of weight chunks
-// in flight per workgroup (S - 1 chunks of 64 x HT 16-bit weights).
+// in flight per workgroup (S - 1 chunks of 64 x HT 16-bit weights), at most
+// 80 KB of LDS, so that two workgroups fit in a CU. (Rings of about 128 KB,
+// one workgroup per CU, measured no faster: the per-CU request pipeline, not
+// the bytes in flight, bounds the stream.)
 constexpr int mc_stages(int ht) { return ht == 64 ? 8 : (ht == 128 ? 5 : 3); }
 constexpr int kMcNtAux = 2;  // cache policy of the weight DMA: non-temporal
 
@@ -127,9 +130,13 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   constexpr int RB = HT * 2;                 // DMA variant: bytes per LDS weight row (no padding)
   constexpr int SB = kMcCK * RB;             // DMA variant: bytes per stage
   constexpr int kLdsBytes = DMA ? S * SB : 2 * kMcCK * WSTR * (int)sizeof(T);
+  // The whole static LDS is the weight staging (the split-K tail reuses its
+  // first word once every wave is past the main loop): at 80 KB per
+  // workgroup two of them fit in a CU's 160 KB, which one more word would
+  // prevent.
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   T(*ws)[kMcCK * WSTR] = reinterpret_cast<T(*)[kMcCK * WSTR]>(lds);
-  __shared__ int is_last;
+  int& is_last = *reinterpret_cast<int*>(lds);
 
   const int h = a.h;
   const int tid = threadIdx.x;
@@ -158,19 +165,26 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
       dst[i] = load16<true>(reinterpret_cast<const u32x4*>(md + (size_t)r * (size_t)h + gcol));
     }
   };
-  // Gathered activations (row-major [batch, wp], zero past w): the A
-  // operand of the wave's row block is 16 B of row rb + li at column 8*lg of
-  // the chunk, loaded straight into registers (rows past the batch read its last
-  // row: they feed only outputs that are not written).
+  // Gathered activations, stored by the gather in MFMA operand order: the A
+  // operand of row block j (16 rows) for K step ks of chunk q (global chunk
+  // index) is one contiguous 1 KB fragment at ((q * KS + ks) * RBK + j) * 512
+  // elements, lane l's 16 B at l * 8 (row 16 j + l % 16, compressed columns
+  // 64 q + 32 ks + 8 (l / 16) .. + 7; rows past the batch and columns past w
+  // zero). RBK (row blocks stored) comes in x_row_stride. One wave's operand
+  // load is 8 whole cache lines instead of 16 half ones of a row-major
+  // [batch, w] array.
   const T* __restrict__ xg = static_cast<const T*>(a.x);
+  const int rbk_n = (int)a.x_row_stride;
+  const int lane = tid & 63;
   auto load_a = [&](u32x4 (&dst)[MB][KS], int k) {
 #pragma unroll
     for (int mb = 0; mb < MB; ++mb)
 #pragma unroll
-      for (int ks = 0; ks < KS; ++ks)
-        dst[mb][ks] = *reinterpret_cast<const u32x4*>(
-            xg + (size_t)min(rb + 16 * mb + li, a.batch - 1) * (size_t)a.x_row_stride +
-            (size_t)(c0 + k * kMcCK + 32 * ks + 8 * lg));
+      for (int ks = 0; ks < KS; ++ks) {
+        const int rbk = min((rb >> 4) + mb, rbk_n - 1);
+        const size_t frag = ((size_t)(c0 / kMcCK + k) * KS + ks) * (size_t)rbk_n + (size_t)rbk;
+        dst[mb][ks] = *reinterpret_cast<const u32x4*>(xg + frag * 512 + (size_t)lane * 8);
+      }
   };
   f4 acc[MB][NBK];
 #pragma unroll
@@ -352,7 +366,7 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
                                acc[mb][nb][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         }
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-    __syncthreads();
+    __syncthreads();  // also: every wave's staging reads and DMAs are done, so is_last may take the first word
     if (tid == 0) {
       const uint32_t prev = __hip_atomic_fetch_add(&a.tickets[tile], 1u, __ATOMIC_RELAXED,
                                                    __HIP_MEMORY_SCOPE_AGENT);
@@ -441,19 +455,33 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   }
 }
 
-// The gathered activations: xg[b, c] = x[b, (c/nnz)*m + mat_index[c]] for
-// c < w, zero for positions outside x and for w <= c < wp (rows wp apart,
-// wp a multiple of 8). Lane i writes 8 consecutive columns of one row as one
-// 16-B store.
+// The gathered activations xg[b, c] = x[b, (c/nnz)*m + mat_index[c]] for
+// c < w, zero for positions outside x, for w <= c < wp and for rows past the
+// batch. Lane i writes 8 consecutive columns of one row as one 16-B store:
+// row-major (FRAG = false: rows wp apart, wp a multiple of 8; `batch` rows)
+// or in the matrix-core kernel's operand order (FRAG = true: lane i fills
+// 16-B slot i of the fragments described at nm_spmm_mc_kernel's load_a; wp
+// a multiple of 64; rbk row blocks of 16 rows).
+template <bool FRAG>
 __global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __restrict__ x, long long x_row_stride,
                                                             int batch, const uint8_t* __restrict__ mat_index, int w,
-                                                            int wp, int nnz, int m, int K, uint16_t* __restrict__ xg) {
-  const int per_row = wp / 8;  // batch * per_row < 2^31 (host)
+                                                            int wp, int nnz, int m, int K, int rbk,
+                                                            uint16_t* __restrict__ xg) {
+  const int per_row = wp / 8;  // rows * per_row < 2^31 (host)
   const int i = (int)blockIdx.x * kBlock + (int)threadIdx.x;
-  if (i >= batch * per_row) return;
-  const int b = i / per_row;
-  const int c0 = (i - b * per_row) * 8;
-  const uint16_t* __restrict__ xr = x + (long long)b * x_row_stride;
+  if (i >= (FRAG ? 16 * rbk : batch) * per_row) return;
+  int b, c0;
+  if (FRAG) {  // slot i: fragment i / 64 = (chunk * 2 + ks) * rbk + j, lane l = i % 64
+    const int f = i >> 6, l = i & 63;
+    const int j = f % rbk, qk = f / rbk;
+    b = 16 * j + (l & 15);
+    c0 = 32 * qk + 8 * (l >> 4);
+  } else {
+    b = i / per_row;
+    c0 = (i - b * per_row) * 8;
+  }
+  const bool row_ok = b < batch;
+  const uint16_t* __restrict__ xr = x + (long long)(row_ok ? b : 0) * x_row_stride;
   uint16_t v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
@@ -461,14 +489,14 @@ __global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __
     const int cc = c < w ? c : w - 1;  // clamped: the load stays in range
     const int p = (cc / nnz) * m + (int)mat_index[cc];
     const uint16_t t = xr[p < K ? p : 0];
-    v[e] = (c < w && p < K) ? t : (uint16_t)0;
+    v[e] = (row_ok && c < w && p < K) ? t : (uint16_t)0;
   }
   u32x4 word;
   word.x = (uint32_t)v[0] | ((uint32_t)v[1] << 16);
   word.y = (uint32_t)v[2] | ((uint32_t)v[3] << 16);
   word.z = (uint32_t)v[4] | ((uint32_t)v[5] << 16);
   word.w = (uint32_t)v[6] | ((uint32_t)v[7] << 16);
-  *reinterpret_cast<u32x4*>(xg + (long long)b * wp + c0) = word;
+  *reinterpret_cast<u32x4*>(xg + (FRAG ? (long long)i * 8 : (long long)b * wp + c0)) = word;
 }
 
 typedef void (*McFn)(SpmmArgs);
@@ -494,17 +522,24 @@ struct McPlan {
   size_t xg_off, workspace;
 };
 
-// Plan (fitted to a grid of tile widths x split counts at the Llama-3.1-8B,
-// Qwen3-14B and Qwen3-32B shapes, 16-64 rows, then to the DMA configurations
-// at the Llama-3.1-8B shapes): cfg < 0 takes register-staged 64-column tiles
-// up to 1024 outputs (16 tiles: the deeper DMA ring does not pay there),
-// DMA-staged 64-column tiles up to 4096 outputs over w <= 4096, DMA-staged
-// 128-column tiles otherwise; splits
-// <= 0 about one workgroup per CU (256 / tiles, rounded), at least w / 2048,
-// at most 8 (the partials grow with the rows); each split whole chunks of 64
-// columns. Workspace: arrival counters, the partials
-// [splits, batch, h] fp32 when splits > 1, then the gathered activations
-// [batch, wp] (wp = w rounded up to whole chunks).
+// Plan, fitted to graph-replay sweeps of the DMA configurations x 1-8 splits
+// at the Llama-3.1-8B, Qwen3-14B and Qwen3-32B shapes, 16 / 32 / 64 rows.
+// Up to 1024 outputs: register-staged 64-column tiles, about one workgroup
+// per CU (256 / tiles splits, at most 8). Otherwise the DMA-staged tile width
+// and split count are chosen together: the grid of the most workgroups that
+// still runs in one round (at most one per CU; a second round of a few
+// workgroups costs more than it brings), ties broken by
+//  * splits of at most 2560 compressed rows (deep K runs slower per split);
+//  * up to 16 rows: 128-column tiles, then 256, then 64 (the 64 x 64 tile
+//    reads as many activation bytes per chunk as weight bytes);
+//  * past 16 rows: fewer splits (their partials, [splits, batch, h] fp32,
+//    grow with the rows), then 128-, 64-, 256-column tiles;
+// and past 32 rows a plan whose partials would reach a quarter of the weight
+// bytes gives way to the widest grid without splits, when that has at least
+// half its workgroups. Each split is whole chunks of 64 columns. Workspace:
+// arrival counters, the partials [splits, batch, h] fp32 when splits > 1,
+// then the gathered activations in operand order (ceil(batch / 16) blocks of
+// 16 rows x wp columns, wp = w rounded up to whole chunks).
 int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, McPlan* p) {
   if (batch < 1 || batch > NM_MC_MAX_BATCH) return NM_ERR_BAD_SHAPE;
   if (h <= 0 || w <= 0 || nnz <= 0 || m <= 0 || m > 256 || nnz > m) return NM_ERR_BAD_SHAPE;
@@ -513,20 +548,63 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)h > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;  // the reduction's 32-bit offsets
-  if (cfg < 0) cfg = h <= 1024 ? 0 : (h <= 4096 && w <= 4096 ? 3 : 4);
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
-  const int HT = kMcTileCols[cfg];
-  const int tiles = ceil_div_mc(h, HT);
   const int wp = ceil_div_mc(w, kMcCK) * kMcCK;
-  if (splits <= 0) {
-    splits = (kMcCUs + tiles / 2) / tiles;
-    if (splits < ceil_div_mc(w, 2048)) splits = ceil_div_mc(w, 2048);
-    if (splits < 1) splits = 1;
-    if (splits > 8) splits = 8;
+  // (tiles, splits, rows per split) of a configuration and a requested split count
+  auto shape_of = [&](int c, int sp, int* tiles_out, int* rows_out) {
+    if (sp > wp / kMcCK) sp = wp / kMcCK;
+    const int r = ceil_div_mc(ceil_div_mc(w, sp), kMcCK) * kMcCK;
+    *tiles_out = ceil_div_mc(h, kMcTileCols[c]);
+    *rows_out = r;
+    return ceil_div_mc(w, r);
+  };
+  if (cfg < 0 && h <= 1024) cfg = 0;
+  if (cfg >= 0 && cfg < 3 && splits <= 0) {  // register-staged: about one workgroup per CU
+    const int t = ceil_div_mc(h, kMcTileCols[cfg]);
+    splits = (kMcCUs + t / 2) / t;
+    splits = splits < 1 ? 1 : (splits > 8 ? 8 : splits);
+  } else if (cfg < 0 || splits <= 0) {
+    // search the DMA configurations (or the given one) x split counts (or the given one)
+    const int c_lo = cfg < 0 ? 3 : cfg, c_hi = cfg < 0 ? 5 : cfg;
+    const int s_lo = splits > 0 ? splits : 1, s_hi = splits > 0 ? splits : 8;
+    const int pref_small[3] = {2, 0, 1};  // ranks of HT = 64, 128, 256 up to 16 rows (lower is better)
+    const int pref_large[3] = {1, 0, 2};  // past 16 rows
+    int best_c = -1, best_s = 0, best_b = 0, best_r = 0, free_c = -1, free_b = 0;
+    auto better = [&](int c, int sp, int b, int r) {
+      if (best_c < 0) return true;
+      const bool fits = b <= kMcCUs, best_fits = best_b <= kMcCUs;
+      if (fits != best_fits) return fits;
+      if (!fits) return b < best_b;  // nothing fits one round: the smallest grid
+      if (b != best_b) return b > best_b;
+      const bool deep = r > 2560, best_deep = best_r > 2560;
+      if (deep != best_deep) return !deep;
+      if (batch > 16 && sp != best_s) return sp < best_s;
+      const int* pref = batch > 16 ? pref_large : pref_small;
+      return pref[c - 3] < pref[best_c - 3];
+    };
+    for (int c = c_lo; c <= c_hi; ++c)
+      for (int sp = s_lo; sp <= s_hi; ++sp) {
+        int t, r;
+        const int se = shape_of(c, sp, &t, &r);
+        if (se != sp && splits <= 0) continue;  // the same grid as a smaller request
+        const long long b = (long long)t * se;
+        if (b > 0x7fffffffLL) continue;
+        if (better(c, se, (int)b, r)) {
+          best_c = c, best_s = se, best_b = (int)b, best_r = r;
+        }
+        if (se == 1 && b <= kMcCUs && b > free_b) free_c = c, free_b = (int)b;
+      }
+    if (best_c < 0) return NM_ERR_BAD_SHAPE;
+    const long long part4 = 4LL * best_s * batch;  // partials written and read, relative to 2 * w weight bytes
+    if (batch > 32 && splits <= 0 && best_s > 1 && part4 * 4 >= (long long)w && free_c >= 0 && 2 * free_b >= best_b) {
+      best_c = free_c;
+      best_s = 1;
+    }
+    cfg = best_c;
+    splits = best_s;
   }
-  if (splits > wp / kMcCK) splits = wp / kMcCK;
-  const int rows = ceil_div_mc(ceil_div_mc(w, splits), kMcCK) * kMcCK;
-  splits = ceil_div_mc(w, rows);
+  int tiles, rows;
+  splits = shape_of(cfg, splits, &tiles, &rows);
   if (tiles > kMaxTickets || (long long)tiles * splits > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   p->cfg = cfg;
   p->splits = splits;
@@ -536,7 +614,7 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   p->wp = wp;
   const size_t part = splits > 1 ? (size_t)splits * (size_t)batch * (size_t)h * sizeof(float) : (size_t)0;
   p->xg_off = ((size_t)NM_TICKET_BYTES + part + 255) / 256 * 256;
-  p->workspace = p->xg_off + (size_t)batch * (size_t)wp * 2;
+  p->workspace = p->xg_off + (size_t)ceil_div_mc(batch, 16) * 16 * (size_t)wp * 2;
   return NM_OK;
 }
 
@@ -577,9 +655,9 @@ int nm_gather_columns(int dtype, const void* x, long long x_row_stride, int rows
   if (((uintptr_t)out & 15u) != 0) return NM_ERR_MISALIGNED;
   // rows of out_row_stride elements: every column past w is written as zero
   const long long lanes = (long long)rows * (out_row_stride / 8);
-  hipLaunchKernelGGL(nm_gather_mc_kernel, dim3((unsigned)((lanes + kBlock - 1) / kBlock)), dim3(kBlock), 0,
+  hipLaunchKernelGGL(nm_gather_mc_kernel<false>, dim3((unsigned)((lanes + kBlock - 1) / kBlock)), dim3(kBlock), 0,
                      static_cast<hipStream_t>(stream), static_cast<const uint16_t*>(x), x_row_stride, rows,
-                     mat_index, w, (int)out_row_stride, nnz, m, (int)K, static_cast<uint16_t*>(out));
+                     mat_index, w, (int)out_row_stride, nnz, m, (int)K, 0, static_cast<uint16_t*>(out));
   const hipError_t e = hipGetLastError();
   return e == hipSuccess ? NM_OK : (int)e;
 }
@@ -598,17 +676,18 @@ int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, cons
   if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
   hipStream_t st = static_cast<hipStream_t>(stream);
   void* xg = static_cast<char*>(workspace) + p.xg_off;
-  const long long gathered = (long long)batch * (long long)(p.wp / 8);
+  const int rbk = ceil_div_mc(batch, 16);  // row blocks of 16 stored (operand order, zero rows past the batch)
+  const long long gathered = (long long)16 * rbk * (long long)(p.wp / 8);
   const unsigned gblocks = (unsigned)((gathered + kBlock - 1) / kBlock);
-  hipLaunchKernelGGL(nm_gather_mc_kernel, dim3(gblocks), dim3(kBlock), 0, st,
-                     static_cast<const uint16_t*>(x), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K,
+  hipLaunchKernelGGL(nm_gather_mc_kernel<true>, dim3(gblocks), dim3(kBlock), 0, st,
+                     static_cast<const uint16_t*>(x), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K, rbk,
                      static_cast<uint16_t*>(xg));  // fp16 and bf16 alike: a copy of 16-bit words
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
   SpmmArgs a;
   memset(&a, 0, sizeof(a));
   a.x = xg;
-  a.x_row_stride = p.wp;
+  a.x_row_stride = rbk;  // operand-order activations: the row blocks stored
   a.mat_data = mat_data;
   a.mat_index = mat_index;
   a.out = out;

@@ -335,6 +335,31 @@ def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60
     return us
 
 
+def time_gather_gemm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60) -> float:
+    """us per call of the library route for the same product: the gathered
+    activations (nm_gather_columns, [batch, w]) times the packed weights as one
+    hipBLASLt GEMM (torch.matmul), weights rotated as in time_spmm."""
+    from . import _lib
+
+    case = RotatingCase(n_out, n_in, nnz, m, rotate_bytes=rotate_bytes, seed=seed)
+    X = torch.randn(batch, n_in, device="cuda").to(case.dtype)
+    out = torch.empty(batch, n_out, dtype=case.dtype, device="cuda")
+    wp = (case.w + 7) // 8 * 8
+    xg = torch.empty(batch, wp, dtype=case.dtype, device="cuda")
+    lib = _lib.load()
+
+    def launch(i):
+        md, mi = case.mats[i]
+        rc = lib.nm_gather_columns(_lib.NM_DTYPE_F16, X.data_ptr(), n_in, batch, mi.data_ptr(), case.w, nnz, m,
+                                   xg.data_ptr(), wp, torch.cuda.current_stream().cuda_stream)
+        _lib.check(rc, "nm_gather_columns")
+        torch.matmul(xg[:, :case.w], md, out=out)
+
+    us = graph_us_per_launch([lambda i=i: launch(i) for i in range(case.copies)], reps)
+    del case
+    return us
+
+
 def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda", warmup=3,
                stats=False, form="best", return_form=False):
     """Dense GEMV y = x * W^T through the BLAS library, weights rotated over
@@ -694,7 +719,21 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
         for i in range(3):
             forms.launch(cls, i)
         torch.cuda.synchronize()
+    del forms
     log("traffic probe: decode-form launches (plain and carried) done")
+    from .hip_spmv import nmsparse_spmm_forward_hip
+    from .profiling import SPMM_PROBE_CLASSES
+
+    for key, K, h, rows, kind, _ in SPMM_PROBE_CLASSES:
+        case = RotatingCase(h, K, nnz, m, rotate_bytes=0, min_copies=3, seed=30)
+        X = torch.randn(rows, K, device="cuda").half()
+        out = torch.empty(rows, h, dtype=torch.float16, device="cuda")
+        for i in range(3):
+            md, mi = case.mats[i]
+            nmsparse_spmm_forward_hip(X, md, mi, case.w, h, nnz, m, out=out, matrix_cores=kind == "mc")
+        torch.cuda.synchronize()
+        del case
+        log(f"traffic probe: {key} done")
 
 
 def write_sweep_md(rows, path, cmd):

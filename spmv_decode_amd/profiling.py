@@ -41,6 +41,36 @@ PROBE_CLASSES = [
 ]
 
 
+# SpMM calls of the traffic probe, after the GEMV classes: (key, K, h, rows, kernel, description); "mc" calls
+# launch the operand-order gather and then the matrix-core kernel, "small" calls the small-batch kernel.
+SPMM_PROBE_CLASSES = [
+    ("spmm8_gate_up_32:64", 4096, 14336, 8, "small", "gate or up, 8 rows (small-batch SpMM)"),
+    ("spmm8_down_32:64", 14336, 4096, 8, "small", "down, 8 rows (small-batch SpMM)"),
+    ("mc16_gate_up_32:64", 4096, 14336, 16, "mc", "gate or up, 16 rows (matrix-core SpMM)"),
+    ("mc64_gate_up_32:64", 4096, 14336, 64, "mc", "gate or up, 64 rows (matrix-core SpMM)"),
+    ("mc16_down_32:64", 14336, 4096, 16, "mc", "down, 16 rows (matrix-core SpMM)"),
+    ("mc64_down_32:64", 14336, 4096, 64, "mc", "down, 64 rows (matrix-core SpMM)"),
+]
+
+
+def spmm_algorithmic(K, h, rows, nnz=32, m=64):
+    """Algorithmic bytes of one SpMM call: packed weights and index bytes once,
+    every row's activations and outputs."""
+    w = K // m * nnz
+    return 2 * w * h + w + rows * (2 * K + 2 * h)
+
+
+def _spmm_dispatches(rows):
+    out = []
+    for r in rows:
+        n = r["Kernel_Name"]
+        for k in ("nm_spmm_mc_kernel", "nm_gather_mc_kernel", "nm_spmm_kernel"):
+            if k + "<" in n:
+                out.append((k + n[n.index("<", n.index(k)):n.index(">", n.index(k)) + 1], float(r["Counter_Value"])))
+                break
+    return out
+
+
 def _algorithmic(K, hs, nmat, nnz=32, m=64, key=None):
     if K is None:  # a decode-form class
         from .microbench import decode_form_bytes
@@ -102,6 +132,32 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
                    "fetch_scale": round(fscale, 5), "write_scale": round(wscale, 5)}
         table.append(f"| {desc} | `nm_gemv_kernel{kern}` | {alg:,} | {round(fetch):,} | {round(write):,} | "
                      f"{(fetch + write) / alg:.4f} |")
+    sf, sw = _spmm_dispatches(frows), _spmm_dispatches(wrows)
+    per_call = {"small": 1, "mc": 2}
+    need = sum(3 * per_call[c[4]] for c in SPMM_PROBE_CLASSES)
+    if len(sf) != need or len(sw) != need:
+        raise SystemExit(f"expected {need} SpMM dispatches per pass, got {len(sf)}/{len(sw)}")
+    spmm_table, i = [], 0
+    for key, K, h, nrows, kind, desc in SPMM_PROBE_CLASSES:
+        n = per_call[kind]
+        fcalls = [sf[i + j * n:i + (j + 1) * n] for j in range(3)]
+        wcalls = [sw[i + j * n:i + (j + 1) * n] for j in range(3)]
+        i += 3 * n
+        alg = spmm_algorithmic(K, h, nrows)
+        parts = []
+        for d in range(n):  # per kernel of the call: average over the three calls
+            kern = fcalls[0][d][0]
+            fb = sum(c[d][1] for c in fcalls) / 3 * fscale * 1024
+            wb = sum(c[d][1] for c in wcalls) / 3 * wscale * 1024
+            parts.append((kern, fb, wb))
+        fetch, write = sum(p[1] for p in parts), sum(p[2] for p in parts)
+        js[key] = {"kernels": {k: {"fetch_bytes": round(f), "write_bytes": round(wv)} for k, f, wv in parts},
+                   "fetch_bytes": round(fetch), "write_bytes": round(write), "bytes_per_call": round(fetch + write),
+                   "algorithmic_bytes": alg}
+        for kern, fb, wb in parts:
+            spmm_table.append(f"| {desc} | `{kern}` | | {round(fb):,} | {round(wb):,} | |")
+        spmm_table.append(f"| {desc}: the call | | {alg:,} | {round(fetch):,} | {round(write):,} | "
+                          f"{(fetch + write) / alg:.4f} |")
     lines = ["# HBM traffic per launch: rocprofv3 FETCH_SIZE / WRITE_SIZE (Llama-3.1-8B shapes, 32:64, fp16)", "",
              "Commands (repository root, one MI355X; each counter in its own run), then the summary:", "", "```",
              "export TMPDIR=/tmp", fetch_cmd, write_cmd,
@@ -125,7 +181,17 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
              "split-K partials (8 splits x h x 4 B per matrix). A carried launch also fetches the producer's partials",
              "(splits x K x 4 B, once per XCD's L2), and a producer writes them. No weight byte is fetched twice.",
              "`profiles/traffic.json` holds the same numbers; bench.py reports `bytes_per_launch` of the dominant",
-             "launch class as `roofline.traffic`."]
+             "launch class as `roofline.traffic`.", "",
+             "## SpMM calls (batch > 1)", "",
+             "Three calls each on distinct weights, the library's default plans. A matrix-core call is two kernels: the",
+             "gather of the activations into operand order (`nm_gather_mc_kernel<true>`) and the main kernel. The",
+             "algorithmic bytes of a call count the packed weights and index bytes once and every row's activations",
+             "and outputs.", "",
+             "| Call | Kernel | Algorithmic bytes | Fetched (scaled) | Written (scaled) | Traffic / algorithmic |",
+             "|---|---|---|---|---|---|", *spmm_table, "",
+             "Over the algorithmic bytes: the fp32 split-K partials ([splits, rows, h], written once and read back by",
+             "each tile's last workgroup), and for the matrix-core calls the gathered activations (written by the",
+             "gather, then read by the main kernel: from L2 mostly, FETCH_SIZE counts only what reaches HBM)."]
     Path(md_path).write_text("\n".join(lines) + "\n")
     Path(json_path).write_text(json.dumps(js, indent=1) + "\n")
 

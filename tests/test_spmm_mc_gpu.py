@@ -161,20 +161,22 @@ def test_graph_capture_replays(gpu):
 def test_split_k_handoff_soak_500_replays(gpu):
     """The matrix-core SpMM's split-K handoff (agent-scope atomic-store
     publish, ticket, ordered partial reads) under repetition: gate/up, down
-    and q/o at the Llama-3.1-8B shapes with 48 rows (2-8 splits, 256-448
+    and q/o at the Llama-3.1-8B shapes with 48 rows (2-4 splits, 224-256
     workgroups) in one hipGraph, replayed 500 times, every replay bitwise
     equal to the first, stopping at the first mismatch."""
     cases = []
-    for i, (K, h) in enumerate(((4096, 14336), (14336, 4096), (4096, 4096))):
+    # (K, h, config, splits): gate/up on the 128-column DMA tiles with 2 splits (its default plan at 48 rows
+    # has none), down and q/o on their default plans (4 splits each)
+    for i, (K, h, cfg, splits) in enumerate(((4096, 14336, 4, 2), (14336, 4096, -1, 0), (4096, 4096, -1, 0))):
         _, md, mi = make_case(K, h, 32, 64, seed=90 + i)
         X = torch.randn(48, K, device="cuda").half()
-        p = _lib.spmm_mc_plan(48, h, md.shape[0], 32, 64)
+        p = _lib.spmm_mc_plan(48, h, md.shape[0], 32, 64, cfg, splits)
         assert p["splits"] > 1, p
-        cases.append((X, md, mi, torch.empty(48, h, dtype=torch.float16, device="cuda")))
+        cases.append((X, md, mi, torch.empty(48, h, dtype=torch.float16, device="cuda"), cfg, splits))
 
     def launches():
-        for X, md, mi, out in cases:
-            mc(X, md, mi, 32, 64, out=out)
+        for X, md, mi, out, cfg, splits in cases:
+            mc(X, md, mi, 32, 64, out=out, config_id=cfg, splits=splits)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
