@@ -205,6 +205,32 @@ int nm_num_gate_up_configs(void);
  *    positions of K, in each split; shapes that cannot are rejected with
  *    NM_ERR_BAD_EPILOGUE.
  *
+ *  - Accumulated carry (the reference's relaxed fp32 atomic accumulation,
+ *    triton_spmv.py:209-214, used as the medium between two launches; the
+ *    order of the additions, hence the last bits of the sums, varies from run
+ *    to run). carry_accumulate != 0 with carry_out:
+ *      * a plain producer (as above) adds its partial tile into carry_out[0, :]
+ *        ([h] fp32, zero before the launch) instead of writing its split's
+ *        row; a consumer then reads it with carry_splits = 1;
+ *      * the gate/up pair (with or without carry_in) becomes a producer too:
+ *        it adds gate's and up's raw sums (the input norm's scale not applied)
+ *        into carry_out[0, h) and [h, 2h) ([2h + 16] fp32, the sums zero
+ *        before the launch) and stores its input's sum of squares in
+ *        carry_out[2h + split] (one per split with a carried input, whose
+ *        plan must then have at most 16 splits; the whole sum in
+ *        carry_out[2h] otherwise; nothing without norm_weight); prob[0].out
+ *        is unused. The pair is a producer only in this form.
+ *    silu_in != NULL (grouped kind, nprob 1, no norm_weight or carry_in; vec
+ *    unused and may be NULL): the input is x[k] = round(silu(s * G[k]) *
+ *    (s * U[k])), G = silu_in[0, K), U = silu_in[K, 2K), s = 1 / sqrt(sum of
+ *    silu_in[2K, 2K + silu_ssq_n) / silu_k + silu_eps) (s = 1 when silu_ssq_n
+ *    is 0; silu_ssq_n <= 16; silu_in apart from every other buffer of the
+ *    launch): the gate/up pair's epilogue, done where down_proj gathers its
+ *    input. zero_buf != NULL ([zero_len] fp32, 16-byte aligned,
+ *    zero_len a multiple of 4, apart from every other buffer of the launch)
+ *    is cleared by the launch: the accumulator a later launch adds into. No
+ *    reference counterpart for silu_in and zero_buf.
+ *
  * For NM_KIND_GATE_UP, nprob is 2 (prob[0] gate, prob[1] up, same h); the
  * output, residual and h are prob[0]'s, and no heads fusion is allowed.
  * Workspace: nm_gemv_launch_workspace_bytes(desc) (0 if the shape is
@@ -246,6 +272,13 @@ typedef struct nm_gemv_launch_desc {
   const float* carry_in;       /* NULL or [carry_splits, K] fp32: consumer */
   void* vec_out;               /* consumer: [K] receives its finished input */
   int carry_splits;
+  int carry_accumulate;        /* producer: 1 = add into carry_out (accumulated carry) */
+  float* zero_buf;             /* NULL or [zero_len] fp32 cleared by the launch */
+  int zero_len;
+  const float* silu_in;        /* NULL or [2K + silu_ssq_n] fp32: the SiLU-product input */
+  int silu_ssq_n;
+  int silu_k;
+  float silu_eps;
 } nm_gemv_launch_desc;
 
 size_t nm_gemv_launch_workspace_bytes(const nm_gemv_launch_desc* desc);

@@ -53,7 +53,9 @@ class NmGemvLaunchDesc(ctypes.Structure):
                 ("norm_weight", _vp), ("norm_eps", ctypes.c_float), ("head_norm_eps", ctypes.c_float),
                 ("head_dim", _i), ("pos_limit", _i), ("pos", _vp), ("rope_table", _vp), ("w", _i), ("nnz", _i),
                 ("m", _i), ("config_id", _i), ("splits", _i), ("prob", NmGemvProblem * 4), ("carry_out", _vp),
-                ("carry_in", _vp), ("vec_out", _vp), ("carry_splits", _i)]
+                ("carry_in", _vp), ("vec_out", _vp), ("carry_splits", _i), ("carry_accumulate", _i),
+                ("zero_buf", _vp), ("zero_len", _i), ("silu_in", _vp), ("silu_ssq_n", _i), ("silu_k", _i),
+                ("silu_eps", ctypes.c_float)]
 
 
 _descp = ctypes.POINTER(NmGemvLaunchDesc)
@@ -90,7 +92,7 @@ ABI = {
     "nm_abi_version": (_i, []),
     "nm_stream_capture_id": (_i, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _lib = None
 _lock = threading.Lock()

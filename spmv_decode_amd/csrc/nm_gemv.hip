@@ -226,6 +226,53 @@ int plan_desc(const nm_gemv_launch_desc& d, int nprob, const int* hs, int nmat, 
   return NM_OK;
 }
 
+// Whether [ptr, ptr + bytes) overlaps a buffer the launch described by `d`
+// reads or writes other than vec (norm weight, matrices and indices,
+// outputs, residuals, head norms, RoPE table, position, workspace, carried
+// input and output, SiLU-product input, vec_out, zero_buf), leaving out the
+// descriptor field `self` (the buffer being checked: &d.vec_out, &d.zero_buf
+// or &d.silu_in).
+bool overlaps_launch(const nm_gemv_launch_desc& d, int nprob, int K, size_t esize, const void* workspace,
+                     size_t workspace_bytes, int splits, const void* self, const void* ptr, size_t bytes) {
+  const uintptr_t v0 = (uintptr_t)ptr;
+  auto clash_field = [&](const void* field, const void* other, size_t n) {
+    const uintptr_t b = (uintptr_t)other;
+    return field != self && other != nullptr && n > 0 && v0 < b + n && b < v0 + bytes;
+  };
+  auto clash = [&](const void* other, size_t n) { return clash_field(nullptr, other, n); };
+  const size_t slice_k = (size_t)K * esize;
+  const size_t rope_bytes = (size_t)(d.pos_limit > 0 ? d.pos_limit : 0) * (size_t)(d.head_dim / 2) * 2 * sizeof(float);
+  if (clash(d.carry_in, (size_t)d.carry_splits * (size_t)K * sizeof(float)) || clash(d.norm_weight, slice_k) ||
+      clash(workspace, workspace_bytes) || clash(d.pos, sizeof(long long)) || clash(d.rope_table, rope_bytes) ||
+      clash_field(&d.vec_out, d.vec_out, slice_k) ||
+      clash_field(&d.zero_buf, d.zero_buf, (size_t)(d.zero_len > 0 ? d.zero_len : 0) * sizeof(float)) ||
+      clash_field(&d.silu_in, d.silu_in,
+                  (size_t)(2 * (size_t)K + (size_t)(d.silu_ssq_n > 0 ? d.silu_ssq_n : 0)) * sizeof(float)))
+    return true;
+  for (int i = 0; i < d.nprob; ++i) {
+    const nm_gemv_problem& q = d.prob[i];
+    if (clash(q.mat_data, (size_t)d.w * (size_t)q.h * esize) || clash(q.mat_index, (size_t)d.w)) return true;
+  }
+  const bool pair = d.kind == NM_KIND_GATE_UP;
+  if (d.carry_out) {  // a producer writes its partials (an accumulating one a row, the pair 2h + 16 floats)
+    const size_t n = pair ? 2 * (size_t)d.prob[0].h + 16 : (size_t)(d.carry_accumulate ? 1 : splits) * (size_t)d.prob[0].h;
+    if (clash(d.carry_out, n * sizeof(float))) return true;
+  }
+  for (int i = 0; i < nprob; ++i) {
+    const nm_gemv_problem& q = d.prob[i];
+    size_t out_elems = (size_t)q.h;
+    if (q.head_stride != 0 || q.elem_stride != 0 || q.pos_stride != 0) {
+      const long long hd = d.head_dim > 0 ? d.head_dim : 1;
+      out_elems = (size_t)((q.h / hd - 1) * q.head_stride + (hd - 1) * q.elem_stride +
+                           (long long)(d.pos_limit > 1 ? d.pos_limit - 1 : 0) * q.pos_stride + 1);
+    }
+    if ((!d.carry_out && clash(q.out, out_elems * esize)) || clash(q.residual, (size_t)q.h * esize) ||
+        clash(q.head_norm, (size_t)(d.head_dim > 0 ? d.head_dim : 0) * esize))
+      return true;
+  }
+  return false;
+}
+
 // Validate a launch descriptor, plan it and launch. Every entry point of the
 // C ABI goes through here. With `workspace_needed` it only plans (and reports
 // the workspace size); with `validate_only` it runs every check and returns
@@ -243,11 +290,18 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   if (pair && d.prob[1].h != d.prob[0].h) return NM_ERR_BAD_SHAPE;
   const bool carry_in = d.carry_in != nullptr;
   const bool carry_out = d.carry_out != nullptr;
-  if (carry_in && carry_out) return NM_ERR_BAD_EPILOGUE;
+  const bool silu_in = d.silu_in != nullptr;
+  // a carried input and a producer at once: only the accumulating gate/up pair
+  if (carry_in && carry_out && !(pair && d.carry_accumulate)) return NM_ERR_BAD_EPILOGUE;
+  if (d.carry_accumulate && !carry_out) return NM_ERR_BAD_EPILOGUE;
+  if (pair && carry_out && !d.carry_accumulate) return NM_ERR_BAD_EPILOGUE;  // the pair's only producer form
   if (d.nnz <= 0) return NM_ERR_BAD_SHAPE;
   Plan p;
   int rc = plan_desc(d, nprob, hs, nmat, &p);
   if (rc != NM_OK) return rc;
+  // the accumulating pair with a carried input stores one sum of squares per
+  // split in the 16 slots after its sums
+  if (pair && carry_out && carry_in && p.splits > 16) return NM_ERR_BAD_EPILOGUE;
   if (carry_in) {
     // The ssq slots follow the partials: one float per workgroup.
     p.workspace = (p.workspace + 255) & ~(size_t)255;
@@ -258,7 +312,7 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
     *workspace_needed = p.workspace;
     return NM_OK;
   }
-  if (!d.vec || !workspace) return NM_ERR_NULL_POINTER;
+  if ((!d.vec && !silu_in) || !workspace) return NM_ERR_NULL_POINTER;
   for (int i = 0; i < d.nprob; ++i)
     if (!d.prob[i].mat_data || !d.prob[i].mat_index) return NM_ERR_NULL_POINTER;
   for (int i = 0; i < nprob; ++i)
@@ -297,12 +351,32 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   if (any_pos && (!d.pos || d.pos_limit <= 0)) return NM_ERR_BAD_EPILOGUE;
   if (any_rope && !d.rope_table) return NM_ERR_BAD_EPILOGUE;
   if (carry_out) {
-    // One plain GEMV: its epilogue moves into the consumer.
     const nm_gemv_problem& q = d.prob[0];
-    if (pair || d.nprob != 1 || d.norm_weight || q.residual || q.head_norm || q.rope || q.head_stride ||
-        q.elem_stride || q.pos_stride)
-      return NM_ERR_BAD_EPILOGUE;
+    if (pair) {
+      // the accumulating pair: raw sums and the norm's sum of squares go to the consumer
+      if (q.residual) return NM_ERR_BAD_EPILOGUE;
+    } else if (d.nprob != 1 || d.norm_weight || q.residual || q.head_norm || q.rope || q.head_stride ||
+               q.elem_stride || q.pos_stride) {
+      return NM_ERR_BAD_EPILOGUE;  // one plain GEMV: its epilogue moves into the consumer
+    }
     if (((uintptr_t)d.carry_out & 15u) != 0) return NM_ERR_MISALIGNED;
+  }
+  if (silu_in) {
+    const nm_gemv_problem& q = d.prob[0];
+    if (pair || d.nprob != 1 || d.norm_weight || carry_in || q.head_norm || q.rope || q.head_stride ||
+        q.elem_stride || q.pos_stride || d.silu_ssq_n < 0 || d.silu_ssq_n > 16 ||
+        (d.silu_ssq_n > 0 && d.silu_k <= 0) || !(d.silu_eps >= 0.0f))
+      return NM_ERR_BAD_EPILOGUE;
+    if (((uintptr_t)d.silu_in & 15u) != 0) return NM_ERR_MISALIGNED;
+    // every workgroup gathers from silu_in while others write the launch's
+    // outputs (or add into carry_out): it must overlap none of them
+    if (overlaps_launch(d, nprob, K, esize, workspace, workspace_bytes, p.splits, &d.silu_in, d.silu_in,
+                        (2 * (size_t)K + (size_t)d.silu_ssq_n) * sizeof(float)))
+      return NM_ERR_BAD_EPILOGUE;
+  }
+  if (d.zero_buf) {
+    if (d.zero_len <= 0 || d.zero_len % 4 != 0) return NM_ERR_BAD_EPILOGUE;
+    if (((uintptr_t)d.zero_buf & 15u) != 0) return NM_ERR_MISALIGNED;
   }
   if (carry_in) {
     if (!d.norm_weight || !d.vec_out) return NM_ERR_BAD_EPILOGUE;
@@ -318,33 +392,16 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
     // Tile 0's workgroups write vec_out while the other workgroups still read
     // every input of the launch and write its outputs: vec_out must overlap
     // none of them.
-    const size_t vo_bytes = (size_t)K * esize;
-    auto clash = [&](const void* ptr, size_t bytes) {
-      const uintptr_t b = (uintptr_t)ptr;
-      return ptr != nullptr && bytes > 0 && vo < b + bytes && b < vo + vo_bytes;
-    };
-    if (clash(d.carry_in, (size_t)d.carry_splits * (size_t)K * sizeof(float)) || clash(d.norm_weight, vo_bytes) ||
-        clash(workspace, workspace_bytes) || clash(d.pos, sizeof(long long)) ||
-        clash(d.rope_table, (size_t)(d.pos_limit > 0 ? d.pos_limit : 0) * (size_t)(d.head_dim / 2) * 2 * sizeof(float)))
+    if (overlaps_launch(d, nprob, K, esize, workspace, workspace_bytes, p.splits, &d.vec_out, d.vec_out,
+                        (size_t)K * esize))
       return NM_ERR_BAD_EPILOGUE;
-    for (int i = 0; i < d.nprob; ++i) {
-      const nm_gemv_problem& q = d.prob[i];
-      if (clash(q.mat_data, (size_t)d.w * (size_t)q.h * esize) || clash(q.mat_index, (size_t)d.w))
-        return NM_ERR_BAD_EPILOGUE;
-    }
-    for (int i = 0; i < nprob; ++i) {
-      const nm_gemv_problem& q = d.prob[i];
-      size_t out_elems = (size_t)q.h;
-      if (q.head_stride != 0 || q.elem_stride != 0 || q.pos_stride != 0) {
-        const long long hd = d.head_dim;
-        out_elems = (size_t)((q.h / hd - 1) * q.head_stride + (hd - 1) * q.elem_stride +
-                             (long long)(d.pos_limit > 1 ? d.pos_limit - 1 : 0) * q.pos_stride + 1);
-      }
-      if (clash(q.out, out_elems * esize) || clash(q.residual, (size_t)q.h * esize) ||
-          clash(q.head_norm, (size_t)(d.head_dim > 0 ? d.head_dim : 0) * esize))
-        return NM_ERR_BAD_EPILOGUE;
-    }
   }
+  // The buffer this launch clears must not be one it reads or writes.
+  if (d.zero_buf && ((d.vec && (uintptr_t)d.zero_buf < (uintptr_t)d.vec + (size_t)K * esize &&
+                      (uintptr_t)d.vec < (uintptr_t)d.zero_buf + (size_t)d.zero_len * 4) ||
+                     overlaps_launch(d, nprob, K, esize, workspace, workspace_bytes, p.splits, &d.zero_buf, d.zero_buf,
+                                     (size_t)d.zero_len * sizeof(float))))
+    return NM_ERR_BAD_EPILOGUE;
   if (validate_only) return NM_OK;
 
   Args a;
@@ -391,7 +448,16 @@ int launch(const nm_gemv_launch_desc& d, void* workspace, size_t workspace_bytes
   a.vec_out = d.vec_out;
   a.carry_splits = d.carry_splits;
   a.ssq_slots = carry_in ? reinterpret_cast<float*>(ws + p.ssq_off) : nullptr;
-  const int variant = carry_in ? (d.carry_splits <= 8 ? 2 : 3) : (d.norm_weight ? 1 : 0);
+  a.carry_acc = d.carry_accumulate;
+  a.zero_buf = d.zero_buf;
+  a.zero_len = d.zero_len;
+  a.silu_in = d.silu_in;
+  a.silu_ssq_n = d.silu_ssq_n;
+  a.silu_k = d.silu_k;
+  a.silu_eps = d.silu_eps;
+  const int variant = silu_in    ? kVarSilu
+                      : carry_in ? (d.carry_splits == 1 ? kVarCarry1 : (d.carry_splits <= 8 ? kVarCarry8 : kVarCarry16))
+                                 : (d.norm_weight ? kVarNorm : kVarPlain);
   const KernelFn fn = kernel_table(d.dtype, pair)[p.cfg].fn[gather_slot(p.rows_per_split)][variant];
   if (!fn) return NM_ERR_BAD_EPILOGUE;
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, static_cast<hipStream_t>(stream), a);

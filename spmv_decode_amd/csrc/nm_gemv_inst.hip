@@ -10,12 +10,19 @@
 
 namespace nm_hip {
 
-#define NM_KERNEL_V(TH, U, G, NT, NM, NORM, CARRY) &nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, NORM, CARRY>
+#define NM_KERNEL_V(TH, U, G, NT, NM, NORM, CARRY, SILU) \
+  &nm_gemv_kernel<NM_INST_DTYPE, TH, U, G, NT, NM, NORM, CARRY, SILU>
+// variants (Variant in nm_gemv_kernel.h): plain, norm, carried 8 / 16 / 1, SiLU-product input (SILUK: the
+// kernel for single-matrix rows, nullptr for the pair)
+#define NM_SILU_1(TH, U, G, NT) NM_KERNEL_V(TH, U, G, NT, 1, false, 0, true)
+#define NM_SILU_2(TH, U, G, NT) nullptr
 #define NM_ROW_N(TH, U, G, NT, NM)                                                                         \
-  {NM_KERNEL_V(TH, U, G, NT, NM, false, 0), NM_KERNEL_V(TH, U, G, NT, NM, true, 0),                       \
-   NM_KERNEL_V(TH, U, G, NT, NM, true, 8), NM_KERNEL_V(TH, U, G, NT, NM, true, 16)}
-#define NM_ROW_W(TH, U, G, NT, NM) \
-  {NM_KERNEL_V(TH, U, G, NT, NM, false, 0), NM_KERNEL_V(TH, U, G, NT, NM, true, 0), nullptr, nullptr}
+  {NM_KERNEL_V(TH, U, G, NT, NM, false, 0, false), NM_KERNEL_V(TH, U, G, NT, NM, true, 0, false),         \
+   NM_KERNEL_V(TH, U, G, NT, NM, true, 8, false),  NM_KERNEL_V(TH, U, G, NT, NM, true, 16, false),        \
+   NM_KERNEL_V(TH, U, G, NT, NM, true, 1, false),  NM_SILU_##NM(TH, U, G, NT)}
+#define NM_ROW_W(TH, U, G, NT, NM)                                                                 \
+  {NM_KERNEL_V(TH, U, G, NT, NM, false, 0, false), NM_KERNEL_V(TH, U, G, NT, NM, true, 0, false), \
+   nullptr, nullptr, nullptr, NM_SILU_##NM(TH, U, G, NT)}
 #define NM_ROW(NM, TH, U, NT) \
   {{NM_ROW_N(TH, U, 1, NT, NM), NM_ROW_N(TH, U, 2, NT, NM), NM_ROW_W(TH, U, 4, NT, NM), NM_ROW_W(TH, U, 8, NT, NM)}},
 #define NM_PLAIN_ROW(TH, U, NT) NM_ROW(1, TH, U, NT)

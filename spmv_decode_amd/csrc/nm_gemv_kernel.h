@@ -44,7 +44,7 @@ constexpr int kBlock = 256;        // lanes per workgroup
 constexpr int kVec = 8;            // output rows per lane
 constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
 constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
-constexpr int kAbiVersion = 8;
+constexpr int kAbiVersion = 9;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
@@ -179,6 +179,30 @@ struct Args {
   void* vec_out;             // [K]
   float* ssq_slots;          // [grid] per-workgroup sums of squares of its input slice
   int carry_splits;
+  // Accumulated carry (the reference's relaxed fp32 atomic accumulation,
+  // triton_spmv.py:209-214, as the medium between two launches; the sums'
+  // order, hence their last bits, then varies from run to run):
+  //  * carry_acc with a plain producer: every split adds its partial tile
+  //    into carry_out[0, :] (fp32 atomic add, agent scope) instead of
+  //    writing its own row, so a consumer reads one row (carry_splits = 1);
+  //  * carry_acc with the gate/up pair (carry_out set): the pair ends after
+  //    its tile reduction, adding gate's and up's raw sums (without the input
+  //    norm's scale) into carry_out[0, h) and [h, 2h), and storing its input's
+  //    sum of squares in carry_out[2h + split] (with a carried input each
+  //    split's share; otherwise the whole sum, split 0 only);
+  //  * silu_in (a plain GEMV): the input is x[k] = round_T(silu(s G[k]) *
+  //    (s U[k])) with G = silu_in[0, K), U = silu_in[K, 2K) and s =
+  //    rsqrt(sum(silu_in[2K, 2K + silu_ssq_n)) / silu_k + silu_eps), or 1 when
+  //    silu_ssq_n == 0: the pair's epilogue, done where its output is read;
+  //  * zero_buf: zero_len floats this launch clears (an accumulator a later
+  //    launch adds into; the launches between them order the two).
+  int carry_acc;
+  float* zero_buf;
+  int zero_len;
+  const float* silu_in;
+  int silu_ssq_n;
+  int silu_k;
+  float silu_eps;
 };
 
 // Most producer splits a consumer reads (their partials are requested at once).
@@ -248,7 +272,7 @@ __device__ inline float word_ssq(const u32x4 raw, bool ok, float acc) {
 // U = 8 rows in flight, and that kernel then ran 25-35% slower than the same
 // pair with the norm (Qwen3-14B 45.3 against 34.1 us, Qwen3-32B 61.5 against
 // 45.7); with the bound both fit, and both run alike.
-template <int DT, int TH, int U, int G, bool NT, int NMAT, bool NORM, int CARRY>
+template <int DT, int TH, int U, int G, bool NT, int NMAT, bool NORM, int CARRY, bool SILU>
 __global__ __launch_bounds__(kBlock) __attribute__((amdgpu_waves_per_eu(1, NMAT == 2 ? 2 : 8)))
 void nm_gemv_kernel(Args a) {
   using E = Elem<DT>;
@@ -264,6 +288,7 @@ void nm_gemv_kernel(Args a) {
   static_assert(NMAT == 1 || NMAT == 2, "one matrix, or the gate/up pair");
   static_assert(!CARRY || (NORM && G <= 2 && CARRY <= kMaxCarry),
                 "a carried input comes with the input norm, <= 512 columns per split");
+  static_assert(!SILU || (NMAT == 1 && !NORM && !CARRY), "the SiLU-product input feeds a plain GEMV");
 
   constexpr int kWaves = kBlock / 64;
   constexpr int kOutPerLane = (HT + kBlock - 1) / kBlock;
@@ -389,6 +414,7 @@ void nm_gemv_kernel(Args a) {
   T graw[NMAT][G];
   T wraw[NMAT][G];
   bool gok[NMAT][G];
+  float sg[SILU ? G : 1], su[SILU ? G : 1];  // SILU: the pair's raw gate and up sums at the gathered positions
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
 #pragma unroll
@@ -400,11 +426,19 @@ void nm_gemv_kernel(Args a) {
       if constexpr (CARRY) {
         graw[q][j] = 0;
         wraw[q][j] = 0;
+      } else if constexpr (SILU) {
+        const int pc = gok[q][j] ? pos : 0;
+        sg[j] = a.silu_in[pc];
+        su[j] = a.silu_in[a.K + pc];
       } else {
         graw[q][j] = vx[(long long)(gok[q][j] ? pos : 0) * a.vec_stride];
         if constexpr (NORM) wraw[q][j] = gx[gok[q][j] ? pos : 0];
       }
     }
+  // SiLU-product input: the producer's sums of squares (one per lane, summed
+  // in slot order below).
+  float sq_slot = 0.0f;
+  if constexpr (SILU) sq_slot = a.silu_ssq_n > 0 ? a.silu_in[2 * a.K + min(tid & 63, a.silu_ssq_n - 1)] : 0.0f;
   // The words of vec for mean(x^2) (contiguous, 16-byte aligned, K * size a
   // multiple of 16 with a norm; the host checks) are requested now and
   // summed after the main loop, so they never delay the weight stream.
@@ -461,6 +495,15 @@ void nm_gemv_kernel(Args a) {
   if constexpr (kEarlyChunk1) load_chunk(bufB, 1);
   __builtin_amdgcn_sched_barrier(0);  // every gather request before the first use of one
   if constexpr (CARRY) __syncthreads();  // the slice is in LDS
+  float s_silu = 1.0f;
+  if constexpr (SILU) {
+    if (a.silu_ssq_n > 0) {
+      const int b = __builtin_bit_cast(int, sq_slot);
+      float t = 0.0f;
+      for (int i = 0; i < a.silu_ssq_n; ++i) t += __builtin_bit_cast(float, __builtin_amdgcn_readlane(b, i));
+      s_silu = rsqrtf(t / (float)a.silu_k + a.silu_eps);
+    }
+  }
 #pragma unroll
   for (int q = 0; q < NMAT; ++q)
 #pragma unroll
@@ -470,6 +513,10 @@ void nm_gemv_kernel(Args a) {
         const int cl = min(t, cw - 1);  // column within the split
         const int li = (cl / a.nnz) * a.m + gidx[q][j];  // < kn for positions below m
         xs[q][t] = (gok[q][j] && li < kn) ? hs[li] : 0.0f;
+      } else if constexpr (SILU) {
+        // the pair's epilogue: silu(s g) * (s u) in fp32, one rounding to T
+        const float xv = E::to_f32(E::from_f32(silu(sg[j] * s_silu) * (su[j] * s_silu)));
+        xs[q][tid + j * kBlock] = gok[q][j] ? xv : 0.0f;
       } else {
         const float xv = gok[q][j] ? E::to_f32(graw[q][j]) : 0.0f;
         if constexpr (NORM) {
@@ -560,6 +607,17 @@ void nm_gemv_kernel(Args a) {
     }
   }
 
+  // 4b. An accumulator a later launch adds into is cleared here, behind the
+  //     weight stream (its stores would otherwise hold up the first waits):
+  //     workgroup b clears its share of zero_len floats (16-byte stores).
+  if (a.zero_buf != nullptr) {
+    const int per = (((a.zero_len + (int)gridDim.x - 1) / (int)gridDim.x) + 3) & ~3;
+    const int z0 = (int)blockIdx.x * per;
+    const int z1 = min(z0 + per, a.zero_len);
+    for (int i = z0 + 4 * tid; i < z1; i += 4 * kBlock)
+      *reinterpret_cast<float4*>(a.zero_buf + i) = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+
   // 5. Reduce the TK lane-rows of the tile through LDS (fixed order), and
   //    the input norm's sum of squares (fixed order too).
 #pragma unroll
@@ -610,12 +668,46 @@ void nm_gemv_kernel(Args a) {
   // after this grid has completed) and is done: no handoff, no epilogue.
   if constexpr (NMAT == 1 && !CARRY) {
     if (a.carry_out != nullptr) {
+      if (a.carry_acc) {  // accumulated: every split adds into row 0
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j) {
+          const int o = tid + j * kBlock;
+          const int r = tile * HT + o;
+          if (o < HT && r < h)
+            (void)__hip_atomic_fetch_add(a.carry_out + r, tsum[0][j], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
+        return;
+      }
       float* part = a.carry_out + (size_t)split * (size_t)h;
 #pragma unroll
       for (int j = 0; j < kOutPerLane; ++j) {
         const int o = tid + j * kBlock;
         const int r = tile * HT + o;
         if (o < HT && r < h) part[r] = tsum[0][j];
+      }
+      return;
+    }
+  }
+  // The gate/up pair as an accumulated producer: its raw sums go to the
+  // consumer (which applies the input norm's scale and the SiLU product when
+  // it gathers them), the input's sum of squares to slot 2h + split; no
+  // handoff, no epilogue.
+  if constexpr (NMAT == 2) {
+    if (a.carry_out != nullptr) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q)
+#pragma unroll
+        for (int j = 0; j < kOutPerLane; ++j) {
+          const int o = tid + j * kBlock;
+          const int r = tile * HT + o;
+          if (o < HT && r < h)
+            (void)__hip_atomic_fetch_add(a.carry_out + (size_t)q * (size_t)h + r, tsum[q][j], __ATOMIC_RELAXED,
+                                         __HIP_MEMORY_SCOPE_AGENT);
+        }
+      if constexpr (NORM) {
+        if (tid == 0 && tile == 0 && (CARRY || split == 0))
+          (void)__hip_atomic_exchange(a.carry_out + 2 * (size_t)h + split, slice_ssq, __ATOMIC_RELAXED,
+                                      __HIP_MEMORY_SCOPE_AGENT);
       }
       return;
     }
@@ -1139,9 +1231,11 @@ typedef void (*KernelFn)(Args);
 // The kernels of one configuration and element type:
 // fn[gather slot: 256, 512, 1024, 2048 columns per split][variant: plain,
 // input norm, input norm with a carried input of <= 8 or <= 16 producer
-// splits (slots 0-1 only, else null)].
+// splits or of one accumulated row (slots 0-1 only, else null), the
+// SiLU-product input (single-matrix configurations only, else null)].
+enum Variant { kVarPlain = 0, kVarNorm, kVarCarry8, kVarCarry16, kVarCarry1, kVarSilu, kNumVariants };
 struct KernelRow {
-  KernelFn fn[4][4];
+  KernelFn fn[4][kNumVariants];
 };
 
 // SpMM configurations: the plain ids 0-3 (th16/th32 x u4/u8, non-temporal).

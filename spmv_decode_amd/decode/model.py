@@ -425,7 +425,7 @@ def fused_block_step(blk: Block, x2d, k_cache_t, v_cache_t, pos, q_pad, zero, ro
     ops.qkv_decode(x2d, qp.mat_data, qp.mat_index, kp.mat_data, kp.mat_index, vp.mat_data, vp.mat_index,
                    qp.block_width, qp.vec_width, q_pad, k_cache_t, v_cache_t, pos, rope, c.head_dim, ln1.weight,
                    ln1.eps, at.q_norm.weight if c.qk_norm else None, at.k_norm.weight if c.qk_norm else None,
-                   c.norm_eps)
+                   c.norm_eps, None)
     y = attend(q_pad, k_cache_t, v_cache_t, c, zero).view(1, qd)
     o = at.o_proj
     ops.gemv_add_(y, o.mat_data, o.mat_index, o.block_width, o.vec_width, x2d)
@@ -496,9 +496,9 @@ def fused_layers_carried(layers, x2d, h2d, carry_o, carry_d, k_caches, v_caches,
                qp.vec_width, q_pad, k_caches[i], v_caches[i], pos, rope, c.head_dim, ln1.weight, ln1.eps, qn, kn,
                c.norm_eps)
         if i == 0:
-            ops.qkv_decode(x2d, *qkv)
+            ops.qkv_decode(x2d, *qkv, None)
         else:
-            ops.qkv_decode_carried(h2d, carry_d, x2d, *qkv)
+            ops.qkv_decode_carried(h2d, carry_d, x2d, *qkv, None)
         y = attend(q_pad, k_caches[i], v_caches[i], c, zero).view(1, c.n_heads * c.head_dim)
         o = at.o_proj
         ops.gemv_partials_(y, o.mat_data, o.mat_index, o.block_width, o.vec_width, carry_o)
@@ -511,6 +511,70 @@ def fused_layers_carried(layers, x2d, h2d, carry_o, carry_d, k_caches, v_caches,
         else:
             ops.gemv_add_(act, d.mat_data, d.mat_index, d.block_width, d.vec_width, h2d)
     return h2d
+
+
+def fused_layers_accumulated(layers, x2d, h2d, acc_op, acc_d, ssq_n, k_caches, v_caches, pos, q_pad, zero, rope):
+    """The fused sparse layers with an accumulated carry: o_proj, the gate/up
+    pair and down_proj are producers whose workgroups add their partial sums
+    into one fp32 row with atomics (the reference's accumulation medium,
+    triton_spmv.py:209-214), and the next launch finishes the epilogue as it
+    gathers its input: gate/up finishes h = x + o_proj(y) from acc_o, down_proj
+    takes silu(s G) * (s U) from acc_p (the pair's raw sums and sums of
+    squares, ssq_n of them), the next q/k/v finishes x = h + down_proj(act)
+    from acc_d. acc_o [dim] and acc_p [2 * inter + 16] are one fp32 buffer
+    acc_op, which each layer's q/k/v launch clears (after their last readers,
+    the previous gate/up and down); the gate/up launch clears acc_d [1, dim]
+    (after q/k/v read it). Clearing acc_p in o_proj instead measured 35-40 us
+    slower per Llama-3.1-8B step: o_proj is short and its clearing stores
+    delay its adds. The order of the atomic adds varies, so the sums' last
+    bits (and, through the roundings, the outputs') vary from run to run.
+    x2d, h2d, caches, pos, q_pad, zero and rope as for fused_layers_carried;
+    the final residual stream is returned (h2d)."""
+    ops = torch.ops.nmsparse
+    n = len(layers)
+    dim = x2d.shape[-1]
+    acc_o, acc_p = acc_op[:dim].view(1, dim), acc_op[dim:]
+    for i, blk in enumerate(layers):
+        at, mlp = blk.self_attn, blk.mlp
+        c = at.cfg
+        ln1, ln2 = blk.input_layernorm, blk.post_attention_layernorm
+        qp, kp, vp = at.q_proj, at.k_proj, at.v_proj
+        qn = at.q_norm.weight if c.qk_norm else None
+        kn = at.k_norm.weight if c.qk_norm else None
+        qkv = (qp.mat_data, qp.mat_index, kp.mat_data, kp.mat_index, vp.mat_data, vp.mat_index, qp.block_width,
+               qp.vec_width, q_pad, k_caches[i], v_caches[i], pos, rope, c.head_dim, ln1.weight, ln1.eps, qn, kn,
+               c.norm_eps)
+        if i == 0:
+            ops.qkv_decode(x2d, *qkv, acc_op)
+        else:
+            ops.qkv_decode_carried(h2d, acc_d, x2d, *qkv, acc_op)
+        y = attend(q_pad, k_caches[i], v_caches[i], c, zero).view(1, c.n_heads * c.head_dim)
+        o = at.o_proj
+        ops.gemv_accumulate_(y, o.mat_data, o.mat_index, o.block_width, o.vec_width, acc_o, None)
+        gp, up = mlp.gate_proj, mlp.up_proj
+        ops.gate_up_accumulate_(x2d, acc_o, h2d, gp.mat_data, gp.mat_index, up.mat_data, up.mat_index,
+                                gp.block_width, gp.vec_width, ln2.weight, ln2.eps, acc_p, acc_d)
+        d = mlp.down_proj
+        if i + 1 < n:
+            ops.gemv_silu_accumulate_(acc_p, d.mat_data, d.mat_index, d.block_width, d.vec_width, ssq_n, dim, ln2.eps,
+                                      acc_d, None)
+        else:
+            ops.gemv_silu_add_(acc_p, d.mat_data, d.mat_index, d.block_width, d.vec_width, ssq_n, dim, ln2.eps, h2d)
+    return h2d
+
+
+def accumulate_supported(layers) -> bool:
+    """True when the fused layers can run fused_layers_accumulated: the split
+    carry's conditions (carry_supported) and an accumulating gate/up pair of
+    at most 16 splits with its carried input (one sum of squares per split)."""
+    from ..hip_spmv import gate_up_ssq_slots
+
+    if not carry_supported(layers):
+        return False
+    mlp = layers[0].mlp
+    gp, up = mlp.gate_proj, mlp.up_proj
+    return gate_up_ssq_slots((gp.mat_data, gp.mat_index), (up.mat_data, up.mat_index), gp.block_width,
+                             gp.vec_width, carried=True) <= 16
 
 
 class Decoder(nn.Module):
@@ -532,8 +596,13 @@ class Decoder(nn.Module):
         self.layout = layout
         self.fuse_epilogues = True
         # Fused sparse layers: carry o_proj's / down_proj's split-K reduction
-        # into the next launch where the shapes allow (fused_layers_carried).
+        # into the next launch where the shapes allow. carry_mode "split"
+        # (fused_layers_carried: fp32 split partials, bit-reproducible) or
+        # "accumulate" (fused_layers_accumulated: fp32 atomic adds into one
+        # row, the gate/up pair a producer too; the sums' last bits vary
+        # from run to run).
         self.carry_splitk = True
+        self.carry_mode = "split"
         self._carry = None  # (key, x2d-independent buffers) set up by _carry_buffers
         self.embed_tokens = nn.Embedding(cfg.vocab, cfg.dim)
         block = Block if layout == "hf" else GptFastBlock
@@ -545,6 +614,7 @@ class Decoder(nn.Module):
         self.dense_fusion = "none"  # set_dense_fusion's mode
 
     LAUNCH_MODES = ("fused", "grouped", "per_linear", "modules")
+    CARRY_MODES = ("split", "accumulate")
 
     def set_launch_mode(self, mode: str) -> None:
         """How sparse projections are launched: "fused" (the fused layer, the
@@ -670,7 +740,11 @@ class Decoder(nn.Module):
     def prepare_decode(self) -> None:
         """Set up what the fused sparse step needs beyond the caches: the
         buffers of fused_layers_carried (the h stream and the fp32 partials of
-        o_proj and down_proj), when the layers support the carry. Run by every
+        o_proj and down_proj) or, with carry_mode "accumulate", of
+        fused_layers_accumulated (the h stream, the fp32 accumulators of
+        o_proj and the gate/up pair in one buffer, down_proj's, and the pair's
+        count of sums of squares), when the layers
+        support the carry. Run by every
         eager step (cheap once done; redone when the layers' shapes change) and
         by the runners before capturing or compiling a step: a step traced by
         torch.compile uses what was prepared before it, and the plain fused
@@ -689,20 +763,32 @@ class Decoder(nn.Module):
                     tuple(mi.shape) if isinstance(mi, torch.Tensor) else None, getattr(mod, "block_width", None),
                     getattr(mod, "vec_width", None))
 
-        key = (dev, dt, len(self.layers),
+        key = (dev, dt, len(self.layers), self.carry_mode,
                tuple(shape(mod) for b in self.layers for mod in (b.self_attn.q_proj, b.self_attn.k_proj,
                                                                   b.self_attn.v_proj, b.self_attn.o_proj,
                                                                   b.mlp.gate_proj, b.mlp.up_proj, b.mlp.down_proj)))
         if self._carry is not None and self._carry[0] == key:
             return
-        if dev.type != "cuda" or not carry_supported(self.layers):
+        if self.carry_mode not in self.CARRY_MODES:
+            raise ValueError(f"carry_mode must be one of {self.CARRY_MODES}, got {self.carry_mode!r}")
+        accumulate = self.carry_mode == "accumulate"
+        if dev.type != "cuda" or not (accumulate_supported if accumulate else carry_supported)(self.layers):
             self._carry = (key, None)
             return
-        from ..hip_spmv import carry_splits
+        from ..hip_spmv import carry_splits, gate_up_ssq_slots
 
+        dim = self.cfg.dim
+        if accumulate:
+            gp, up = mlp.gate_proj, mlp.up_proj
+            inter = gp.mat_data.shape[1]
+            ssq_n = gate_up_ssq_slots((gp.mat_data, gp.mat_index), (up.mat_data, up.mat_index), gp.block_width,
+                                      gp.vec_width, carried=True)
+            f32 = dict(device=dev, dtype=torch.float32)
+            self._carry = (key, (torch.empty(1, dim, device=dev, dtype=dt), torch.empty(dim + 2 * inter + 16, **f32),
+                                 torch.empty(1, dim, **f32), ssq_n))
+            return
         so = carry_splits(o.mat_data, o.mat_index, o.block_width, o.vec_width)
         sd = carry_splits(d.mat_data, d.mat_index, d.block_width, d.vec_width)
-        dim = self.cfg.dim
         self._carry = (key, (torch.empty(1, dim, device=dev, dtype=dt),
                              torch.empty(so, dim, device=dev, dtype=torch.float32),
                              torch.empty(sd, dim, device=dev, dtype=torch.float32)))
@@ -772,8 +858,9 @@ class Decoder(nn.Module):
                 self.prepare_decode()
             bufs = self._carry[1] if (self.carry_splitk and self._carry is not None) else None
             if bufs is not None:
-                h2d = fused_layers_carried(self.layers, x2d, *bufs, self.k_cache_t, self.v_cache_t, pos, self.q_pad,
-                                           self.zero, self.rope_real)
+                run = fused_layers_accumulated if len(bufs) == 4 else fused_layers_carried
+                h2d = run(self.layers, x2d, *bufs, self.k_cache_t, self.v_cache_t, pos, self.q_pad, self.zero,
+                          self.rope_real)
                 return project(self.lm_head, self.norm(h2d.view(1, 1, -1))).view(1, -1)
             for i, blk in enumerate(self.layers):
                 fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero,

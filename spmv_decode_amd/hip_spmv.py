@@ -373,7 +373,8 @@ def launch_plan(problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, config_id=-1
 
 def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False, norm=None, head_dim=0,
                          head_eps=1e-6, pos=None, pos_limit=None, rope_table=None, config_id=-1, splits=0,
-                         carry_out=None, carry_in=None, vec_out=None):
+                         carry_out=None, carry_in=None, vec_out=None, carry_accumulate=False, zero=None,
+                         silu_in=None, silu_ssq_n=0, silu_k=0, silu_eps=0.0):
     """One launch of 1-4 GEMVs that share `vec` [1, K] (or the gate/up pair),
     with the fusions of include/nmsparse_hip.h's nm_gemv_launch.
 
@@ -391,6 +392,17 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
     returned); `carry_in` (fp32 [S, K]: a producer's partials) with `vec_out`
     ([K] of vec.dtype, not vec) makes the launch's input round(sum of the
     partials + vec), written to vec_out; it needs `norm`.
+
+    Accumulated carry (nm_gemv_launch_desc.carry_accumulate; the sums' last
+    bits then vary from run to run): with `carry_accumulate=True` a plain
+    producer adds its partials into `carry_out` (fp32 [1, h], zero before
+    the launch) and the gate/up pair (carried input or not) becomes a
+    producer adding its raw gate and up sums into `carry_out` (fp32 [2h + 16]:
+    sums, then the input's sums of squares). `silu_in` (fp32 [2K + 16], a
+    pair's accumulator; vec may then be None) makes the input of one plain
+    GEMV round(silu(s G) * (s U)) with s from the first `silu_ssq_n` sums of
+    squares, `silu_k` and `silu_eps`. `zero` (fp32, a multiple of 4
+    elements) is cleared by the launch.
     """
     n = len(problems)
     if gate_up and n != 2:
@@ -398,6 +410,16 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
     if not 1 <= n <= 4:
         raise ValueError("a fused launch takes 1 to 4 problems")
     w = problems[0].mat_data.shape[0]
+    if silu_in is not None:
+        if vec is not None:
+            raise ValueError("a SiLU-product input replaces vec: pass vec=None")
+        md0 = problems[0].mat_data
+        K = (w // BLOCK_WIDTH) * VEC_WIDTH
+        if (silu_in.dtype != torch.float32 or not silu_in.is_contiguous() or silu_in.device != md0.device
+                or silu_in.numel() < 2 * K + max(int(silu_ssq_n), 0) or silu_in.data_ptr() % 16):
+            raise ValueError(f"silu_in must be a contiguous, 16-byte aligned fp32 tensor of >= 2K + ssq_n "
+                             f"({2 * K} + {silu_ssq_n}) elements on the weights' device")
+        vec = silu_in.view(md0.dtype)[:K].view(1, K)  # carries K, dtype and device only: desc.vec stays null
     K = vec.shape[-1]
     for pr in problems:
         validate_args(vec, pr.mat_data, pr.mat_index, w, pr.mat_data.shape[1], BLOCK_WIDTH, 128, VEC_WIDTH, 1, K)
@@ -484,12 +506,24 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
         if (carry_out.dtype != torch.float32 or not carry_out.is_contiguous() or carry_out.device != vec.device
                 or carry_out.data_ptr() % 16):
             raise ValueError("carry_out must be a contiguous, 16-byte aligned fp32 tensor on vec.device")
-        plan = launch_plan([(pr.mat_data, pr.mat_index) for pr in problems], BLOCK_WIDTH, VEC_WIDTH,
-                           gate_up=gate_up, config_id=config_id, splits=splits, producer=True)
-        if carry_out.numel() != plan["splits"] * int(problems[0].mat_data.shape[1]):
-            raise ValueError(f"carry_out holds {carry_out.numel()} floats, the producer leaves "
-                             f"{plan['splits']} x {int(problems[0].mat_data.shape[1])}")
+        h0 = int(problems[0].mat_data.shape[1])
+        if carry_accumulate:
+            want = 2 * h0 + 16 if gate_up else h0
+            if carry_out.numel() != want:
+                raise ValueError(f"an accumulating producer adds into {want} floats, carry_out holds "
+                                 f"{carry_out.numel()}")
+        else:
+            if gate_up:
+                raise ValueError("the gate/up pair is a producer only with carry_accumulate")
+            plan = launch_plan([(pr.mat_data, pr.mat_index) for pr in problems], BLOCK_WIDTH, VEC_WIDTH,
+                               gate_up=gate_up, config_id=config_id, splits=splits, producer=True)
+            if carry_out.numel() != plan["splits"] * h0:
+                raise ValueError(f"carry_out holds {carry_out.numel()} floats, the producer leaves "
+                                 f"{plan['splits']} x {h0}")
         desc.carry_out = carry_out.data_ptr()
+        desc.carry_accumulate = int(bool(carry_accumulate))
+    elif carry_accumulate:
+        raise ValueError("carry_accumulate needs carry_out")
     if carry_in is not None:
         if carry_in.dtype != torch.float32 or carry_in.dim() != 2 or carry_in.shape[1] != K \
                 or not carry_in.is_contiguous() or carry_in.device != vec.device or carry_in.data_ptr() % 16:
@@ -502,6 +536,15 @@ def nmsparse_gemv_launch(vec, problems, BLOCK_WIDTH, VEC_WIDTH, *, gate_up=False
         desc.carry_in, desc.carry_splits, desc.vec_out = carry_in.data_ptr(), carry_in.shape[0], vec_out.data_ptr()
     elif vec_out is not None:
         raise ValueError("vec_out is the output of a carried input (carry_in)")
+    if silu_in is not None:
+        desc.vec = None
+        desc.silu_in, desc.silu_ssq_n, desc.silu_k = silu_in.data_ptr(), int(silu_ssq_n), int(silu_k)
+        desc.silu_eps = float(silu_eps)
+    if zero is not None:
+        if (zero.dtype != torch.float32 or not zero.is_contiguous() or zero.device != vec.device or zero.numel() % 4
+                or zero.data_ptr() % 16 or zero.numel() == 0):
+            raise ValueError("zero must be a contiguous, 16-byte aligned fp32 tensor of a multiple of 4 elements")
+        desc.zero_buf, desc.zero_len = zero.data_ptr(), zero.numel()
     lib = _lib.load()
     need = lib.nm_gemv_launch_workspace_bytes(ctypes.byref(desc))
     if need == 0:
@@ -564,9 +607,63 @@ def nmsparse_gemv_partials(vec, mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH, car
     return carry
 
 
+def gate_up_ssq_slots(gate, up, BLOCK_WIDTH, VEC_WIDTH, *, carried: bool, norm: bool = True) -> int:
+    """Sums of squares the accumulating gate/up pair leaves after its sums
+    (nmsparse_gate_up_accumulate): one per split of its plan with a carried
+    input, one without, none without an input norm."""
+    if not norm:
+        return 0
+    if not carried:
+        return 1
+    return launch_plan([gate, up], BLOCK_WIDTH, VEC_WIDTH, gate_up=True, carried=True)["splits"]
+
+
+def nmsparse_gemv_accumulate(vec, mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH, acc, *, zero=None, silu_in=None,
+                             silu_ssq_n=0, silu_k=0, silu_eps=0.0):
+    """acc [1, h] (fp32, zero beforehand) += W @ vec, each split adding its
+    partial tile with fp32 atomics (accumulated carry: the order of the adds,
+    hence the sum's last bits, varies from run to run). A following launch
+    reads acc as a one-row carry (carry_in=acc). `silu_in` (an accumulating
+    gate/up pair's buffer; vec None) makes the input that pair's SiLU
+    product; `zero` is cleared by the launch."""
+    nmsparse_gemv_launch(vec, [GemvProblem(mat_data, mat_index)], BLOCK_WIDTH, VEC_WIDTH, carry_out=acc,
+                         carry_accumulate=True, zero=zero, silu_in=silu_in, silu_ssq_n=silu_ssq_n, silu_k=silu_k,
+                         silu_eps=silu_eps)
+    return acc
+
+
+def nmsparse_gate_up_accumulate(vec, gate, up, BLOCK_WIDTH, VEC_WIDTH, acc, *, norm=None, carry_in=None,
+                                vec_out=None, zero=None) -> int:
+    """The gate/up pair as an accumulating producer: gate's and up's raw sums
+    (W_gate x * g, W_up x * g with x the input and g the norm weight) are
+    added into acc[0, h) and acc[h, 2h) (fp32 [2h + 16], the sums zero
+    beforehand) and the input's sums of squares stored after them; a
+    following GEMV applies the norm's scale and silu(gate) * up as it gathers
+    its input (nmsparse_gemv_silu). Returns the number of sums of squares
+    stored (that GEMV's silu_ssq_n). carry_in / vec_out as for
+    nmsparse_gate_up_silu; `zero` is cleared by the launch."""
+    (gd, gi), (ud, ui) = gate, up
+    nmsparse_gemv_launch(vec, [GemvProblem(gd, gi), GemvProblem(ud, ui)], BLOCK_WIDTH, VEC_WIDTH, gate_up=True,
+                         norm=norm, carry_in=carry_in, vec_out=vec_out, carry_out=acc, carry_accumulate=True,
+                         zero=zero)
+    return gate_up_ssq_slots(gate, up, BLOCK_WIDTH, VEC_WIDTH, carried=carry_in is not None, norm=norm is not None)
+
+
+def nmsparse_gemv_silu(silu_in, mat_data, mat_index, BLOCK_WIDTH, VEC_WIDTH, *, ssq_n, silu_k, silu_eps, out=None,
+                       residual=None, zero=None):
+    """W @ x (+ residual) with x = round(silu(s G) * (s U)) gathered from an
+    accumulating gate/up pair's buffer silu_in ([2K + 16] fp32: G, U, then
+    ssq_n sums of squares; s = rsqrt(sum of them / silu_k + silu_eps), 1 when
+    ssq_n is 0): the pair's epilogue done where its output is read. Returns
+    [1, h] of the weights' dtype."""
+    return nmsparse_gemv_launch(None, [GemvProblem(mat_data, mat_index, out, residual=residual)], BLOCK_WIDTH,
+                                VEC_WIDTH, silu_in=silu_in, silu_ssq_n=ssq_n, silu_k=silu_k, silu_eps=silu_eps,
+                                zero=zero)[0]
+
+
 def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_t, v_cache=None, v_cache_t=None,
                         pos, rope_table, head_dim, norm=None, q_norm=None, k_norm=None, head_eps=1e-6, config_id=-1,
-                        splits=0, carry_in=None, vec_out=None):
+                        splits=0, carry_in=None, vec_out=None, zero=None):
     """The q/k/v projections of one decode step in one launch.
 
     q, k, v are (mat_data, mat_index) pairs sharing `vec` [1, K]. Writes the
@@ -579,7 +676,8 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
     the decoder keeps both caches transposed). `norm` = (weight [K], eps) is
     the layer's input RMSNorm; `q_norm` / `k_norm` ([head_dim]) are Qwen3's
     per-head norms. `carry_in` / `vec_out`: the input is round(sum of a
-    producer's partials + vec), written to vec_out (nmsparse_gemv_launch).
+    producer's partials + vec), written to vec_out (nmsparse_gemv_launch);
+    `zero` (fp32) is cleared by the launch.
     """
     kvh, kd, S = k_cache_t.shape
     hd = head_dim
@@ -610,9 +708,10 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
              GemvProblem(v[0], v[1], vc, layout=v_layout)]
     return nmsparse_gemv_launch(vec, probs, BLOCK_WIDTH, VEC_WIDTH, norm=norm, head_dim=head_dim,
                                 head_eps=head_eps, pos=pos, rope_table=rt[:S], config_id=config_id,
-                                splits=splits, carry_in=carry_in, vec_out=vec_out)
+                                splits=splits, carry_in=carry_in, vec_out=vec_out, zero=zero)
 
 
 __all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
            "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "nmsparse_spmm_forward_hip",
-           "nmsparse_gemv_partials", "carry_splits", "GemvProblem", "launch_plan", "validate_args", "workspace_for"]
+           "nmsparse_gemv_partials", "carry_splits", "GemvProblem", "launch_plan", "validate_args", "workspace_for",
+           "nmsparse_gemv_accumulate", "nmsparse_gate_up_accumulate", "nmsparse_gemv_silu", "gate_up_ssq_slots"]

@@ -21,7 +21,13 @@ RMSNorm folded in). They take fp16/bf16/fp32 inputs as they are (no casts).
 The split-K carry between a layer's launches adds `nmsparse::gemv_partials_`
 (a GEMV left as fp32 split partials; mutates its carry buffer) and the
 `_carried` forms of the q/k/v and gate/up launches, which finish their input
-from those partials and the residual stream (mutating vec_out).
+from those partials and the residual stream (mutating vec_out). The
+accumulated carry (fp32 atomic adds into one row; sums' last bits vary from
+run to run) adds `nmsparse::gemv_accumulate_`, `nmsparse::gate_up_accumulate_`
+(the pair as a producer of raw sums), `nmsparse::gemv_silu_accumulate_` and
+`nmsparse::gemv_silu_add_` (down_proj taking the pair's SiLU product as it
+gathers its input), and the `zero` argument of the q/k/v ops (an accumulator
+cleared by the launch).
 
 `nmsparse::gemv_grouped` (one launch for 2-4 gemv calls on the same input)
 and `nmsparse::gemv_silu_mul` (silu(gemv gate) * gemv up in one launch) are
@@ -48,9 +54,9 @@ import torch
 
 from typing import Optional
 
-from .hip_spmv import (GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_grouped, nmsparse_gemv_launch,
-                       nmsparse_gemv_partials, nmsparse_qkv_decode, nmsparse_spmm_forward_hip,
-                       nmsparse_spmv_forward_hip)
+from .hip_spmv import (GemvProblem, nmsparse_gate_up_accumulate, nmsparse_gate_up_silu, nmsparse_gemv_accumulate,
+                       nmsparse_gemv_grouped, nmsparse_gemv_launch, nmsparse_gemv_partials, nmsparse_gemv_silu,
+                       nmsparse_qkv_decode, nmsparse_spmm_forward_hip, nmsparse_spmv_forward_hip)
 
 _kernel = os.environ.get("NM_KERNEL", "")
 if _kernel not in ("", "hip", "triton_ptx", "guarded", "fp16", "fp16_split"):
@@ -148,25 +154,27 @@ def _(x, gate_data, gate_index, up_data, up_index, w, h, block_width, vec_width)
     return x.new_empty((*x.shape[:-1], int(h)))
 
 
-@torch.library.custom_op("nmsparse::qkv_decode", mutates_args=("q_out", "k_cache_t", "v_cache_t"))
+@torch.library.custom_op("nmsparse::qkv_decode", mutates_args=("q_out", "k_cache_t", "v_cache_t", "zero"))
 def qkv_decode(x: torch.Tensor, q_data: torch.Tensor, q_index: torch.Tensor, k_data: torch.Tensor,
                k_index: torch.Tensor, v_data: torch.Tensor, v_index: torch.Tensor, block_width: int, vec_width: int,
                q_out: torch.Tensor, k_cache_t: torch.Tensor, v_cache_t: torch.Tensor, pos: torch.Tensor,
                rope_table: torch.Tensor, head_dim: int, norm_weight: Optional[torch.Tensor], norm_eps: float,
-               q_norm: Optional[torch.Tensor], k_norm: Optional[torch.Tensor], head_eps: float) -> None:
+               q_norm: Optional[torch.Tensor], k_norm: Optional[torch.Tensor], head_eps: float,
+               zero: Optional[torch.Tensor]) -> None:
     """hip_spmv.nmsparse_qkv_decode with transposed key and value caches
     ([kv_heads, >= head_dim, S] and [kv_heads, head_dim, S]) and rope_table
-    fp32 [S', head_dim / 2, 2] (S' >= S)."""
+    fp32 [S', head_dim / 2, 2] (S' >= S); `zero` (fp32) is cleared by the
+    launch (an accumulator of the accumulated carry)."""
     nmsparse_qkv_decode(x.view(1, -1), (q_data, q_index), (k_data, k_index), (v_data, v_index), int(block_width),
                         int(vec_width), q_out=q_out, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
                         rope_table=rope_table, head_dim=int(head_dim),
                         norm=None if norm_weight is None else (norm_weight, float(norm_eps)), q_norm=q_norm,
-                        k_norm=k_norm, head_eps=float(head_eps))
+                        k_norm=k_norm, head_eps=float(head_eps), zero=zero)
 
 
 @qkv_decode.register_fake
 def _(x, q_data, q_index, k_data, k_index, v_data, v_index, block_width, vec_width, q_out, k_cache_t, v_cache_t,
-      pos, rope_table, head_dim, norm_weight, norm_eps, q_norm, k_norm, head_eps):
+      pos, rope_table, head_dim, norm_weight, norm_eps, q_norm, k_norm, head_eps, zero):
     return None
 
 
@@ -211,25 +219,27 @@ def _(x, mat_data, mat_index, block_width, vec_width, carry):
     return None
 
 
-@torch.library.custom_op("nmsparse::qkv_decode_carried", mutates_args=("q_out", "k_cache_t", "v_cache_t", "vec_out"))
+@torch.library.custom_op("nmsparse::qkv_decode_carried",
+                         mutates_args=("q_out", "k_cache_t", "v_cache_t", "vec_out", "zero"))
 def qkv_decode_carried(x: torch.Tensor, carry: torch.Tensor, vec_out: torch.Tensor, q_data: torch.Tensor,
                        q_index: torch.Tensor, k_data: torch.Tensor, k_index: torch.Tensor, v_data: torch.Tensor,
                        v_index: torch.Tensor, block_width: int, vec_width: int, q_out: torch.Tensor,
                        k_cache_t: torch.Tensor, v_cache_t: torch.Tensor, pos: torch.Tensor, rope_table: torch.Tensor,
                        head_dim: int, norm_weight: torch.Tensor, norm_eps: float, q_norm: Optional[torch.Tensor],
-                       k_norm: Optional[torch.Tensor], head_eps: float) -> None:
+                       k_norm: Optional[torch.Tensor], head_eps: float, zero: Optional[torch.Tensor]) -> None:
     """qkv_decode on the input round(sum of carry's partials + x), which is
-    also written to vec_out (x: the residual stream before the producer)."""
+    also written to vec_out (x: the residual stream before the producer);
+    carry [S, K] fp32 (S = 1: an accumulated carry)."""
     nmsparse_qkv_decode(x.view(1, -1), (q_data, q_index), (k_data, k_index), (v_data, v_index), int(block_width),
                         int(vec_width), q_out=q_out, k_cache_t=k_cache_t, v_cache_t=v_cache_t, pos=pos,
                         rope_table=rope_table, head_dim=int(head_dim), norm=(norm_weight, float(norm_eps)),
                         q_norm=q_norm, k_norm=k_norm, head_eps=float(head_eps), carry_in=carry,
-                        vec_out=vec_out.view(1, -1))
+                        vec_out=vec_out.view(1, -1), zero=zero)
 
 
 @qkv_decode_carried.register_fake
 def _(x, carry, vec_out, q_data, q_index, k_data, k_index, v_data, v_index, block_width, vec_width, q_out, k_cache_t,
-      v_cache_t, pos, rope_table, head_dim, norm_weight, norm_eps, q_norm, k_norm, head_eps):
+      v_cache_t, pos, rope_table, head_dim, norm_weight, norm_eps, q_norm, k_norm, head_eps, zero):
     return None
 
 
@@ -249,5 +259,68 @@ def _(x, carry, vec_out, gate_data, gate_index, up_data, up_index, block_width, 
     return x.new_empty((1, gate_data.shape[1]))
 
 
-__all__ = ["gemv", "spmm", "gemv_grouped", "gemv_silu_mul", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_", "qkv_decode_carried",
-           "gate_up_silu_carried"]
+@torch.library.custom_op("nmsparse::gemv_accumulate_", mutates_args=("acc", "zero"))
+def gemv_accumulate_(x: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor, block_width: int,
+                     vec_width: int, acc: torch.Tensor, zero: Optional[torch.Tensor]) -> None:
+    """acc [1, h] fp32 += W_sparse x with fp32 atomics (accumulated carry;
+    hip_spmv.nmsparse_gemv_accumulate); `zero` is cleared by the launch."""
+    nmsparse_gemv_accumulate(x.view(1, -1), mat_data, mat_index, int(block_width), int(vec_width), acc, zero=zero)
+
+
+@gemv_accumulate_.register_fake
+def _(x, mat_data, mat_index, block_width, vec_width, acc, zero):
+    return None
+
+
+@torch.library.custom_op("nmsparse::gate_up_accumulate_", mutates_args=("vec_out", "acc", "zero"))
+def gate_up_accumulate_(x: torch.Tensor, carry: Optional[torch.Tensor], vec_out: Optional[torch.Tensor],
+                        gate_data: torch.Tensor, gate_index: torch.Tensor, up_data: torch.Tensor,
+                        up_index: torch.Tensor, block_width: int, vec_width: int, norm_weight: torch.Tensor,
+                        norm_eps: float, acc: torch.Tensor, zero: Optional[torch.Tensor]) -> None:
+    """The gate/up pair adding its raw sums and leaving its input's sums of
+    squares in acc [2h + 16] fp32 (hip_spmv.nmsparse_gate_up_accumulate), on
+    the input round(sum of carry's partials + x) written to vec_out when carry
+    is given, else on x."""
+    nmsparse_gate_up_accumulate(x.view(1, -1), (gate_data, gate_index), (up_data, up_index), int(block_width),
+                                int(vec_width), acc, norm=(norm_weight, float(norm_eps)), carry_in=carry,
+                                vec_out=None if vec_out is None else vec_out.view(1, -1), zero=zero)
+
+
+@gate_up_accumulate_.register_fake
+def _(x, carry, vec_out, gate_data, gate_index, up_data, up_index, block_width, vec_width, norm_weight, norm_eps, acc,
+      zero):
+    return None
+
+
+@torch.library.custom_op("nmsparse::gemv_silu_accumulate_", mutates_args=("acc", "zero"))
+def gemv_silu_accumulate_(silu_in: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor, block_width: int,
+                          vec_width: int, ssq_n: int, silu_k: int, silu_eps: float, acc: torch.Tensor,
+                          zero: Optional[torch.Tensor]) -> None:
+    """acc [1, h] fp32 += W_sparse x with fp32 atomics, x the SiLU product of
+    an accumulating gate/up pair's buffer silu_in (hip_spmv.nmsparse_gemv_silu)."""
+    nmsparse_gemv_accumulate(None, mat_data, mat_index, int(block_width), int(vec_width), acc, zero=zero,
+                             silu_in=silu_in, silu_ssq_n=int(ssq_n), silu_k=int(silu_k), silu_eps=float(silu_eps))
+
+
+@gemv_silu_accumulate_.register_fake
+def _(silu_in, mat_data, mat_index, block_width, vec_width, ssq_n, silu_k, silu_eps, acc, zero):
+    return None
+
+
+@torch.library.custom_op("nmsparse::gemv_silu_add_", mutates_args=("out",))
+def gemv_silu_add_(silu_in: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor, block_width: int,
+                   vec_width: int, ssq_n: int, silu_k: int, silu_eps: float, out: torch.Tensor) -> None:
+    """out [1, h] += W_sparse x (one rounding), x the SiLU product of an
+    accumulating gate/up pair's buffer silu_in (hip_spmv.nmsparse_gemv_silu)."""
+    nmsparse_gemv_silu(silu_in, mat_data, mat_index, int(block_width), int(vec_width), ssq_n=int(ssq_n),
+                       silu_k=int(silu_k), silu_eps=float(silu_eps), out=out, residual=out)
+
+
+@gemv_silu_add_.register_fake
+def _(silu_in, mat_data, mat_index, block_width, vec_width, ssq_n, silu_k, silu_eps, out):
+    return None
+
+
+__all__ = ["gemv", "spmm", "gemv_grouped", "gemv_silu_mul", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_",
+           "qkv_decode_carried", "gate_up_silu_carried", "gemv_accumulate_", "gate_up_accumulate_",
+           "gemv_silu_accumulate_", "gemv_silu_add_"]

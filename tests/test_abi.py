@@ -17,6 +17,18 @@ HEADER = ROOT / "include" / "nmsparse_hip.h"
 FAKE = 0x10000  # 256-byte aligned placeholder address, never dereferenced
 
 
+def _gpu_visible() -> bool:
+    import torch
+
+    return torch.cuda.device_count() > 0  # counts devices without initialising HIP
+
+
+# A descriptor these checks accept goes on to hipLaunchKernelGGL with the
+# placeholder pointers: with no GPU that call fails, on a GPU the kernel would
+# run on them. The module is for machines without one.
+pytestmark = pytest.mark.skipif(_gpu_visible(), reason="placeholder-pointer launches need a machine without a GPU")
+
+
 def _declared_functions():
     text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
     return set(re.findall(r"\b(nm_[a-z0-9_]+)\s*\(", text))
@@ -448,3 +460,78 @@ def test_split_k_carry_rejections_and_plans_before_launch():
     # explicit configurations and split counts are kept as asked
     p = launch_plan([mats(5120, 5120)], 32, 64, producer=True, config_id=3, splits=8)
     assert (p["config_id"], p["splits"], p["blocks"]) == (3, 8, 160)
+
+
+def test_accumulated_carry_rejections_before_launch():
+    """The accumulated carry's descriptor fields: carry_accumulate needs
+    carry_out; the gate/up pair is a producer only in that form, without a
+    residual, and with a carried input at most 16 splits (one sum of squares
+    per split); the SiLU-product input feeds one plain GEMV without norm,
+    carried input or heads fusions, 16-byte aligned, with 0..16 sums of
+    squares, silu_k > 0 when it has some and eps >= 0 (vec may then be null);
+    zero_buf is 16-byte aligned, a positive multiple of 4 floats, apart from
+    every buffer of the launch."""
+    VO = FAKE + (1 << 36)
+    ACC = FAKE + (1 << 38)
+    h = 14336
+    pair = dict(kind=1, nprob=2, hs=(h, h), norm_weight=FAKE)
+    carried = dict(carry_in=FAKE, carry_splits=1, vec_out=VO)
+
+    def accepted(d):  # every check passed: the launch itself fails (no GPU here)
+        return _launch(d) not in (-1, -2, -5, -6, -7, -8)
+
+    # carry_accumulate without carry_out; the pair as a producer without it, or with a residual
+    assert _launch(_desc(nprob=1, hs=(4096,), carry_accumulate=1)) == -8
+    assert _launch(_desc(**pair, carry_out=ACC)) == -8
+    d = _desc(**pair, carry_out=ACC, carry_accumulate=1)
+    d.prob[0].residual = FAKE
+    assert _launch(d) == -8
+    assert accepted(_desc(**pair, carry_out=ACC, carry_accumulate=1))
+    assert accepted(_desc(**pair, **carried, carry_out=ACC, carry_accumulate=1))
+    assert accepted(_desc(nprob=1, hs=(4096,), carry_out=ACC, carry_accumulate=1))
+    # a carried pair of more than 16 splits has no room for its sums of squares; as a plain consumer it runs
+    big = dict(w=16384, **{**carried, "carry_splits": 1})
+    assert accepted(_desc(**pair, **big))
+    assert _launch(_desc(**pair, **big, carry_out=ACC, carry_accumulate=1)) == -8
+    # the pair's buffer [2h + 16] must not overlap its other buffers
+    assert _launch(_desc(**pair, **carried, carry_out=VO - 16, carry_accumulate=1)) == -8
+    assert _launch(_desc(**pair, **carried, carry_out=ACC, carry_accumulate=1,
+                         zero_buf=ACC + 4 * (2 * h + 12), zero_len=4)) == -8
+    assert accepted(_desc(**pair, **carried, carry_out=ACC, carry_accumulate=1,
+                          zero_buf=ACC + 4 * (2 * h + 16), zero_len=4))
+    # the SiLU-product input: one plain GEMV, K = 4096 (w 2048 at 32:64), vec unused
+    silu = dict(nprob=1, hs=(4096,), vec=None, silu_in=ACC, silu_ssq_n=4, silu_k=4096, silu_eps=1e-5)
+    assert accepted(_desc(**silu))
+    assert accepted(_desc(**silu, carry_out=VO, carry_accumulate=1))
+    assert _launch(_desc(**silu, norm_weight=FAKE)) == -8
+    assert _launch(_desc(**silu, **carried)) == -8
+    assert _launch(_desc(**{**silu, "nprob": 2, "hs": (4096, 4096)})) == -8
+    assert _launch(_desc(**{**pair, "vec": None}, silu_in=ACC, silu_ssq_n=1, silu_k=4096)) == -8
+    assert _launch(_desc(**{**silu, "silu_ssq_n": 17})) == -8
+    assert _launch(_desc(**{**silu, "silu_ssq_n": -1})) == -8
+    assert _launch(_desc(**{**silu, "silu_k": 0})) == -8
+    assert accepted(_desc(**{**silu, "silu_k": 0, "silu_ssq_n": 0}))
+    assert _launch(_desc(**{**silu, "silu_eps": -1.0})) == -8
+    assert _launch(_desc(**{**silu, "silu_in": ACC + 8})) == -5
+    d = _desc(**silu)
+    d.prob[0].rope, d.head_dim = 1, 128
+    assert _launch(d) == -8
+    d = _desc(**silu)
+    d.prob[0].out = ACC + 4 * 100  # the output inside silu_in [2K + 4]
+    assert _launch(d) == -8
+    # zero_buf: shape, alignment, and apart from vec, outputs and every other buffer
+    plain = dict(nprob=1, hs=(4096,))
+    Z = FAKE + (1 << 40)
+    assert accepted(_desc(**plain, zero_buf=Z, zero_len=4096))
+    assert _launch(_desc(**plain, zero_buf=Z, zero_len=0)) == -8
+    assert _launch(_desc(**plain, zero_buf=Z, zero_len=6)) == -8
+    assert _launch(_desc(**plain, zero_buf=Z + 4, zero_len=4)) == -5
+    assert _launch(_desc(**plain, zero_buf=FAKE, zero_len=4)) == -8          # vec (and the matrix, output)
+    d = _desc(**plain, zero_buf=Z, zero_len=4096)
+    d.prob[0].out = Z + 4096 * 4 - 16                                         # the buffer's last 16 bytes
+    assert _launch(d) == -8
+    d.prob[0].out = Z + 4096 * 4
+    assert accepted(d)
+    assert _launch(_desc(**plain, zero_buf=Z, zero_len=4096, carry_out=Z + 4 * 4092, carry_accumulate=1)) == -8
+    assert _launch(_desc(**silu, zero_buf=ACC + 4 * 8192, zero_len=4)) == -8  # the sums of squares of silu_in
+    assert accepted(_desc(**silu, zero_buf=ACC + 4 * 8196, zero_len=4))

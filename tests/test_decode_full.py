@@ -162,6 +162,11 @@ def test_full_depth_decode_parity(gpu, name, M, layers):
         logits[mode] = teacher_forced(model, seq, PROMPT)
     model.set_launch_mode("fused")
     assert torch.equal(logits["fused"], eager)  # the same computation, fed the same tokens
+    say(f"{tag}: teacher-forced fused, accumulated carry")
+    model.carry_mode = "accumulate"
+    logits["fused_accumulate"] = teacher_forced(model, seq, PROMPT)
+    assert len(model._carry[1]) == 4  # the accumulated layers ran
+    model.carry_mode = "split"
     for dtype in (torch.float32, torch.float16):
         say(f"{tag}: masked dense twin {dtype}")
         twin = dense_twin(model, dtype)
@@ -183,7 +188,7 @@ def test_full_depth_decode_parity(gpu, name, M, layers):
     assert all(torch.isfinite(v).all() for v in logits.values())
     assert e16 < 0.05, e16  # the fp16 model tracks fp32 at this depth at all
     bound = 2 * e16 + 1e-3
-    for k in ("fused", "per_linear", "grouped"):
+    for k in ("fused", "fused_accumulate", "per_linear", "grouped"):
         assert err[k] <= bound, (k, err[k], bound)
     assert cross <= 3 * e16 + 1e-3, cross
     assert to_dense16 <= 3 * e16 + 1e-3, to_dense16
