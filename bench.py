@@ -5,20 +5,23 @@
 One step = every sparse GEMV of one Llama-3.1-8B decode token at 32:64, as the
 decoder launches them: per layer one q/k/v launch with the input RMSNorm,
 RoPE and KV-cache write fused in, o, one gate/up pair launch with the
-post-attention RMSNorm and the SiLU*mul epilogue, and down (4 launches x 32
-layers), with the split-K carry of the decoder's fused path: o and down leave
-their fp32 split partials, and the gate/up launch and the next layer's q/k/v
-launch finish their input from them and the residual stream (the residual
-adds); the last down adds its residual itself. Over 32 layers' distinct
-packed weights (7.0 GB resident in HBM, far beyond the 256 MB Infinity Cache),
-fp16, batch 1, captured once in a hipGraph and replayed. `value` is the
-algorithmic bytes of the step (2*w*h weights + w index bytes per matrix,
-2*K activations once per launch, norm weights, residual reads, 2*h outputs
-per output vector, the RoPE table row; the split partials passed between
-launches are not counted) divided by the step time. The same layer without
-the carry (o and down with the residual add, config.fused_step_without_carry),
-without any fusion (config.plain_fused_step) and the GEMVs as 224 separate
-launches (config.unfused_224_launches) are timed too.
+post-attention RMSNorm, and down (4 launches x 32 layers), with the
+accumulated carry of the decoder's default fused path: o, the gate/up pair
+and down add their split-K sums into fp32 rows with atomics (as the reference
+kernel accumulates), and the next launch finishes the epilogue as it gathers
+its input: gate/up the residual add and RMSNorm, down the SiLU*mul, the next
+layer's q/k/v the residual add and RMSNorm; the last down adds its residual
+itself. Over 32 layers' distinct packed weights (7.0 GB resident in HBM, far
+beyond the 256 MB Infinity Cache), fp16, batch 1, captured once in a hipGraph
+and replayed. `value` is the algorithmic bytes of the step (2*w*h weights +
+w index bytes per matrix, 2*K activations once per launch, norm weights,
+residual reads, 2*h outputs per output vector, the RoPE table row; the fp32
+rows passed between launches are not counted) divided by the step time. The
+same layer with the bit-reproducible split carry (config.split_carry_step),
+without a carry (o and down with the residual add,
+config.fused_step_without_carry), without any fusion (config.plain_fused_step)
+and the GEMVs as 224 separate launches (config.unfused_224_launches) are
+timed too.
 
 Also reported: per-shape average launch time and GB/s for the sparse kernel
 and for dense fp16 hipBLASLt GEMVs on the same shapes (the faster of its
@@ -244,7 +247,7 @@ def main():
 
     from spmv_decode_amd.decode.model import KEY_PAD
     from spmv_decode_amd.hip_spmv import GemvProblem
-    from spmv_decode_amd.microbench import CARRIED_CLASSES, DECODE_CLASSES, decode_form_bytes
+    from spmv_decode_amd.microbench import ACCUMULATED_CLASSES, CARRIED_CLASSES, DECODE_CLASSES, decode_form_bytes
 
     # decode-form buffers: residual stream, attention output, norms, KV cache, RoPE table, position
     S = 512
@@ -276,9 +279,10 @@ def main():
     # the decoder's fused path: the split-K carry between the launches
     from spmv_decode_amd.decode.model import LLAMA31_8B
 
-    carried_step, carried_bytes, carried_written = carried_gemv_chain(layers, LLAMA31_8B, nnz, m, dev, gen, S=S)
-    acc_step, acc_bytes, acc_written = carried_gemv_chain(layers, LLAMA31_8B, nnz, m, dev, gen, S=S,
-                                                          carry="accumulate")
+    # the decoder's default fused path: the accumulated carry; the bit-reproducible split carry beside it
+    step_fn, step_bytes_carried, step_written = carried_gemv_chain(layers, LLAMA31_8B, nnz, m, dev, gen, S=S,
+                                                                   carry="accumulate")
+    split_step, split_bytes, split_written = carried_gemv_chain(layers, LLAMA31_8B, nnz, m, dev, gen, S=S)
 
     w4, w14 = 4096 // m * nnz, 14336 // m * nnz
     fused_bytes_layer = (
@@ -317,17 +321,17 @@ def main():
         return start.elapsed_time(end) / args.steps
 
     # ---- the timed step: one decode token's sparse GEMVs as the decoder runs them
-    ms_per_step = time_step(carried_step)
-    value = carried_bytes / (ms_per_step * 1e-3) / 1e9
-    log(f"decode step, carried ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
+    ms_per_step = time_step(step_fn)
+    value = step_bytes_carried / (ms_per_step * 1e-3) / 1e9
+    log(f"decode step, accumulated carry ({4 * L} launches) {ms_per_step:.4f} ms -> {value:.1f} GB/s "
         f"({100 * value / HBM_PEAK_GBS:.1f}% of {HBM_PEAK_GBS:.0f})")
-    if not all(bool(torch.isfinite(o.float()).all()) for o in carried_written):
+    if not all(bool(torch.isfinite(o.float()).all()) for o in step_written):
         raise RuntimeError("non-finite GEMV output")
-    ms_acc = time_step(acc_step)
-    acc_value = acc_bytes / (ms_acc * 1e-3) / 1e9
-    log(f"decode step, accumulated carry ({4 * L} launches) {ms_acc:.4f} ms -> {acc_value:.1f} GB/s")
-    if not all(bool(torch.isfinite(o.float()).all()) for o in acc_written):
-        raise RuntimeError("non-finite GEMV output (accumulated carry)")
+    ms_split = time_step(split_step)
+    split_value = split_bytes / (ms_split * 1e-3) / 1e9
+    log(f"decode step, split carry ({4 * L} launches) {ms_split:.4f} ms -> {split_value:.1f} GB/s")
+    if not all(bool(torch.isfinite(o.float()).all()) for o in split_written):
+        raise RuntimeError("non-finite GEMV output (split carry)")
     ms_nocarry = time_step(lambda: [decode_layer(li) for li in range(L)])
     nocarry_value = decode_bytes / (ms_nocarry * 1e-3) / 1e9
     log(f"decode step without the carry ({4 * L} launches) {ms_nocarry:.4f} ms -> {nocarry_value:.1f} GB/s")
@@ -354,22 +358,23 @@ def main():
         "data": "synthetic (seeded on-device N(0,0.02) weights, random in-group patterns, N(0,1) activations)",
         "config": {
             "workload": f"Llama-3.1-8B decode-token sparse GEMVs at {nnz}:{m}: {L} layers x (q/k/v + input "
-                        "RMSNorm + RoPE + KV-cache write, o, gate/up pair + RMSNorm + SiLU*mul, down), the residual "
-                        "adds and o's / down's split-K reductions carried into the next launch, batch 1, fp16, "
-                        "hipGraph replay, distinct resident weights per layer",
+                        "RMSNorm + RoPE + KV-cache write, o, gate/up pair + RMSNorm + SiLU*mul, down), the decoder's "
+                        "default fused path: o, the gate/up pair and down accumulate their split-K sums into fp32 "
+                        "rows with atomics (the reference kernel's accumulation) and the next launch finishes the "
+                        "epilogue (residual add, RMSNorm, SiLU*mul), batch 1, fp16, hipGraph replay, distinct "
+                        "resident weights per layer",
             "ratio": f"{nnz}:{m}",
             "layers": L,
             "launches_per_step": 4 * L,
-            "algorithmic_bytes_per_step": carried_bytes,
+            "algorithmic_bytes_per_step": step_bytes_carried,
             "pct_hbm_peak": round(100 * value / HBM_PEAK_GBS, 2),
-            "accumulated_carry_step": {"ms_per_step": round(ms_acc, 5), "GBps": round(acc_value, 2),
-                                       "algorithmic_bytes_per_step": acc_bytes,
-                                       "speedup_vs_split_carry": round(ms_per_step / ms_acc, 4),
-                                       "launches": "the same 4 launches per layer with Decoder.carry_mode "
-                                                   "'accumulate': o, the gate/up pair and down add into fp32 rows "
-                                                   "with atomics, the pair's SiLU product formed where down gathers "
-                                                   "it; the sums' order, so their last bits, vary from run to run "
-                                                   "(the timed step keeps the bit-reproducible split carry)"},
+            "split_carry_step": {"ms_per_step": round(ms_split, 5), "GBps": round(split_value, 2),
+                                 "algorithmic_bytes_per_step": split_bytes,
+                                 "timed_step_speedup_over_it": round(ms_split / ms_per_step, 4),
+                                 "launches": "the same 4 launches per layer with Decoder.carry_mode 'split': o and "
+                                             "down leave fp32 split partials that gate/up and the next q/k/v sum in "
+                                             "split order (bit-reproducible run to run, unlike the accumulated "
+                                             "carry of the timed step, whose atomic adds' order varies)"},
             "fused_step_without_carry": {"ms_per_step": round(ms_nocarry, 5), "GBps": round(nocarry_value, 2),
                                          "algorithmic_bytes_per_step": decode_bytes,
                                          "launches": "q/k/v + norm/RoPE/cache, o + residual, gate/up pair + norm + "
@@ -413,7 +418,7 @@ def main():
     # over >= 1 GiB each
     forms = MB.DecodeForms(nnz, m, rotate_bytes=1 << 30)
     per_class = {}
-    for c in CARRIED_CLASSES + DECODE_CLASSES:
+    for c in ACCUMULATED_CLASSES + CARRIED_CLASSES + DECODE_CLASSES:
         us = forms.time(c, reps=reps)
         b = forms.bytes(c)
         per_class[c] = {"launches_per_step": L, "us_per_launch": round(us, 3), "bytes_per_launch": b,
@@ -424,11 +429,19 @@ def main():
             f"({per_class[c]['pct_peak']}%)")
     del forms
     torch.cuda.empty_cache()
-    fused = {c: per_class[c] for c in CARRIED_CLASSES}
+    fused = {c: per_class[c] for c in ACCUMULATED_CLASSES}
     # dominant kernel: largest share of the step
     dom = max(fused, key=lambda c: fused[c]["us_per_launch"] * fused[c]["launches_per_step"])
     d = fused[dom]
     kernel_name = {
+        "gate_up_pair_acc": "nm_gemv_kernel<fp16, pair_th64_u4, NMAT=2, NORM, CARRY=1> (gate/up pair + RMSNorm, input "
+                            "finished from o_proj's accumulated row + residual, raw gate/up sums added into an fp32 "
+                            "row, K=4096 h=14336)",
+        "qkv_decode_acc": "nm_gemv_kernel<fp16, th32_u8, NORM, CARRY=1> (q/k/v + RMSNorm + RoPE + cache write, input "
+                          "finished from down_proj's accumulated row + residual, K=4096 h=4096+1024+1024)",
+        "down_silu_acc": "nm_gemv_kernel<fp16, th16_u8, SILU> (down on the pair's SiLU product, adding into an fp32 "
+                         "row, K=14336 h=4096)",
+        "o_acc": "nm_gemv_kernel<fp16, th16_u8> (o, adding into an fp32 row, K=4096 h=4096)",
         "gate_up_pair_norm_carried": "nm_gemv_kernel<fp16, pair_th64_u4, NMAT=2, NORM, CARRY=8> (gate/up pair + "
                                      "RMSNorm + SiLU*mul, input finished from o_proj's split partials + residual, "
                                      "K=4096 h=14336)",
@@ -448,6 +461,7 @@ def main():
         "us_per_launch": d["us_per_launch"],
     }
     result["per_launch_class"] = fused
+    result["per_launch_class_split_carry"] = {c: per_class[c] for c in CARRIED_CLASSES}
     result["per_launch_class_without_carry"] = {c: per_class[c] for c in DECODE_CLASSES}
     traffic_file = ROOT / "profiles" / "traffic.json"
     if traffic_file.exists():
@@ -636,18 +650,18 @@ def decode_ms_per_token(m, log):
     fixed_sparse = fixed_context_ms(model, 512)
     ref32_sparse = fixed_context_logits_fp32(model, 512)
     fixed_sparse_c = compiled_fixed(model, fixed_sparse, ref32_sparse, "sparse")
-    # the accumulated carry (Decoder.carry_mode "accumulate": atomic fp32 rows between the launches)
-    model.carry_mode = "accumulate"
+    # the bit-reproducible split carry (Decoder.carry_mode "split") beside the default accumulated carry
+    model.carry_mode = "split"
     try:
-        sparse_acc = run_variant(model, LLAMA31_8B, prompt, 256, "sparse, accumulated carry", log)
-        fixed_acc = fixed_context_ms(model, 512)
-        acc_env = logits_envelope(fixed_sparse["logits"], fixed_acc["logits"], ref32_sparse)
-        log(f"accumulated carry vs split carry, fixed context: {acc_env}")
-        if not acc_env["within"]:
-            envelope_failures.append(("sparse accumulated carry (eager)", acc_env))
-        fixed_acc_c = compiled_fixed(model, fixed_acc, ref32_sparse, "sparse accumulated carry")
+        sparse_split = run_variant(model, LLAMA31_8B, prompt, 256, "sparse, split carry", log)
+        fixed_split = fixed_context_ms(model, 512)
+        split_env = logits_envelope(fixed_split["logits"], fixed_sparse["logits"], ref32_sparse)
+        log(f"accumulated carry vs split carry, fixed context: {split_env}")
+        if not split_env["within"]:
+            envelope_failures.append(("sparse accumulated carry vs split carry (eager)", split_env))
+        fixed_split_c = compiled_fixed(model, fixed_split, ref32_sparse, "sparse split carry")
     finally:
-        model.carry_mode = "split"
+        model.carry_mode = "accumulate"
     variants = {}
     for mode in ("per_linear", "grouped", "modules"):
         model.set_launch_mode(mode)
@@ -704,17 +718,17 @@ def decode_ms_per_token(m, log):
            "speedup_sparse_vs_dense": round(dense["ms_per_token"] / sparse["ms_per_token"], 4),
            "dense_ms_per_token_by_fusion": ms,
            "speedup_sparse_vs_fastest_dense": round(fastest_dense / sparse["ms_per_token"], 4),
-           "accumulated_carry": {
-               "sparse_ms_per_token": sparse_acc["ms_per_token"],
-               "speedup_vs_split_carry": round(sparse["ms_per_token"] / sparse_acc["ms_per_token"], 4),
-               "fixed_context_512_ms_per_token": round(fixed_acc["median"], 4),
-               "fixed_context_512_compiled_ms_per_token": _finite(fixed_acc_c["median"]),
-               "matches_split_carry": acc_env,
-               "compiled_matches_eager": fixed_acc_c.get("matches_eager"),
-               "note": "Decoder.carry_mode 'accumulate': o_proj, the gate/up pair and down_proj add into fp32 rows "
-                       "with atomics (the reference kernel's accumulation) and the next launch finishes the "
-                       "epilogue; the adds' order varies, so logits vary in their last bits from run to run; the "
-                       "default stays the bit-reproducible split carry"},
+           "split_carry": {
+               "sparse_ms_per_token": sparse_split["ms_per_token"],
+               "default_speedup_over_it": round(sparse_split["ms_per_token"] / sparse["ms_per_token"], 4),
+               "fixed_context_512_ms_per_token": round(fixed_split["median"], 4),
+               "fixed_context_512_compiled_ms_per_token": _finite(fixed_split_c["median"]),
+               "accumulated_matches_split": split_env,
+               "compiled_matches_eager": fixed_split_c.get("matches_eager"),
+               "note": "Decoder.carry_mode 'split': o_proj and down_proj leave fp32 split partials that the next "
+                       "launch sums in split order, so logits are bit-reproducible run to run and graph replay to "
+                       "eager; the default 'accumulate' (every other sparse figure here) adds into fp32 rows with "
+                       "atomics, as the reference kernel accumulates, and its logits vary in the last bits"},
            "sparse_ms_per_token_by_launch_mode": {"fused": sparse["ms_per_token"],
                                                   **{k: v["ms_per_token"] for k, v in variants.items()}},
            "sparse_per_linear_ms_per_token": variants["per_linear"]["ms_per_token"],
@@ -814,8 +828,8 @@ def decode_qwen3(log, steps=20, warmup=5):
     each the prompt in one Decoder.prefill pass (untimed) then the generated
     tokens by hipGraph replay (ms/token: the mean over them); the speedup over
     the fastest dense structure; and one token's sparse GEMV launches as the
-    decoder issues them (4 per layer, the split-K carry, over the model's own
-    resident weights) timed alone by graph replay: ms and algorithmic GB/s."""
+    decoder issues them (4 per layer, the accumulated carry, over the model's
+    own resident weights) timed alone by graph replay: ms and algorithmic GB/s."""
     import gc
 
     import torch
@@ -857,7 +871,8 @@ def decode_qwen3(log, steps=20, warmup=5):
                    for sub, names in ((blk.self_attn, ("q_proj", "k_proj", "v_proj", "o_proj")),
                                       (blk.mlp, ("gate_proj", "up_proj", "down_proj"))) for n in names}
                   for blk in model.layers]
-        step, nbytes, written = carried_gemv_chain(layers, cfg, nnz, M, dev, torch.Generator(device=dev).manual_seed(3))
+        step, nbytes, written = carried_gemv_chain(layers, cfg, nnz, M, dev, torch.Generator(device=dev).manual_seed(3),
+                                                   carry="accumulate")
         stream = torch.cuda.Stream(device=dev)
         stream.wait_stream(torch.cuda.current_stream())
         with torch.cuda.stream(stream):

@@ -596,13 +596,14 @@ class Decoder(nn.Module):
         self.layout = layout
         self.fuse_epilogues = True
         # Fused sparse layers: carry o_proj's / down_proj's split-K reduction
-        # into the next launch where the shapes allow. carry_mode "split"
-        # (fused_layers_carried: fp32 split partials, bit-reproducible) or
-        # "accumulate" (fused_layers_accumulated: fp32 atomic adds into one
-        # row, the gate/up pair a producer too; the sums' last bits vary
-        # from run to run).
+        # into the next launch where the shapes allow. carry_mode
+        # "accumulate" (default; fused_layers_accumulated: fp32 atomic adds
+        # into one row as the reference kernel accumulates, the gate/up pair
+        # a producer too; the sums' last bits vary from run to run) or
+        # "split" (fused_layers_carried: fp32 split partials summed in split
+        # order, bit-reproducible run to run and graph replay to eager).
         self.carry_splitk = True
-        self.carry_mode = "split"
+        self.carry_mode = "accumulate"
         self._carry = None  # (key, x2d-independent buffers) set up by _carry_buffers
         self.embed_tokens = nn.Embedding(cfg.vocab, cfg.dim)
         block = Block if layout == "hf" else GptFastBlock

@@ -205,6 +205,12 @@ def decode_form_bytes(cls, nnz=32, m=64, dim=4096, inter=14336, qd=4096, kvd=102
         return 2 * wi * dim + wi + 2 * inter
     if cls in ("qkv_decode_carried", "gate_up_pair_norm_carried"):
         return decode_form_bytes(cls[:-len("_carried")], nnz, m, dim, inter, qd, kvd, hd, qk_norm) + 2 * dim
+    # accumulated carry: the same work as the split carry's launch in the same place (the fp32 rows passed
+    # between them are not counted, as split partials are not)
+    same = {"qkv_decode_acc": "qkv_decode_carried", "o_acc": "o_partials",
+            "gate_up_pair_acc": "gate_up_pair_norm_carried", "down_silu_acc": "down_partials"}
+    if cls in same:
+        return decode_form_bytes(same[cls], nnz, m, dim, inter, qd, kvd, hd, qk_norm)
     raise ValueError(cls)
 
 
@@ -270,6 +276,16 @@ class DecodeForms:
         self.carry_o = torch.zeros(carry_splits(*self.o.mats[0], nnz, m), dim, device=device)
         self.carry_d = torch.zeros(carry_splits(*self.down.mats[0], nnz, m), dim, device=device)
         self.x_fin, self.h_fin = (torch.empty(1, dim, dtype=f16, device=device) for _ in range(2))
+        # accumulated carry: o's and the pair's rows in one buffer (cleared by q/k/v), down's row (cleared by
+        # the pair), as the decoder keeps them
+        from .hip_spmv import gate_up_ssq_slots
+
+        self.copies.update({"qkv_decode_acc": cq, "o_acc": self.o.copies, "gate_up_pair_acc": cp,
+                            "down_silu_acc": self.down.copies})
+        self.acc_op = torch.zeros(dim + 2 * inter + 16, device=device)
+        self.acc_o, self.acc_p = self.acc_op[:dim].view(1, dim), self.acc_op[dim:]
+        self.acc_d = torch.zeros(1, dim, device=device)
+        self.ssq_n = gate_up_ssq_slots(self.gate.mats[0], self.up.mats[0], nnz, m, carried=True)
 
     def launch(self, cls, i, config_id=-1, splits=0):
         from .hip_spmv import GemvProblem, nmsparse_gate_up_silu, nmsparse_gemv_launch, nmsparse_qkv_decode
@@ -300,6 +316,22 @@ class DecodeForms:
                                 k_cache_t=self.k_cache, v_cache_t=self.v_cache, pos=self.pos, rope_table=self.rope,
                                 head_dim=self.hd, norm=(self.ln1, 1e-5), q_norm=self.q_norm, k_norm=self.k_norm,
                                 carry_in=self.carry_d, vec_out=self.x_fin, **kw)
+        elif cls == "qkv_decode_acc":
+            nmsparse_qkv_decode(self.x, self.q.mats[i], self.k.mats[i], self.v.mats[i], nnz, m, q_out=self.qo,
+                                k_cache_t=self.k_cache, v_cache_t=self.v_cache, pos=self.pos, rope_table=self.rope,
+                                head_dim=self.hd, norm=(self.ln1, 1e-5), q_norm=self.q_norm, k_norm=self.k_norm,
+                                carry_in=self.acc_d, vec_out=self.x_fin, zero=self.acc_op, **kw)
+        elif cls == "o_acc":
+            nmsparse_gemv_launch(self.attn, [GemvProblem(*self.o.mats[i])], nnz, m, carry_out=self.acc_o,
+                                 carry_accumulate=True, **kw)
+        elif cls == "gate_up_pair_acc":
+            nmsparse_gemv_launch(self.x, [GemvProblem(*self.gate.mats[i]), GemvProblem(*self.up.mats[i])], nnz, m,
+                                 gate_up=True, norm=(self.ln2, 1e-5), carry_in=self.acc_o, vec_out=self.h_fin,
+                                 carry_out=self.acc_p, carry_accumulate=True, zero=self.acc_d, **kw)
+        elif cls == "down_silu_acc":
+            nmsparse_gemv_launch(None, [GemvProblem(*self.down.mats[i])], nnz, m, carry_out=self.acc_d,
+                                 carry_accumulate=True, silu_in=self.acc_p, silu_ssq_n=self.ssq_n, silu_k=self.dim,
+                                 silu_eps=1e-5, **kw)
         else:
             raise ValueError(cls)
 
@@ -312,9 +344,12 @@ class DecodeForms:
 
 
 DECODE_CLASSES = ("qkv_decode", "o_resid", "gate_up_pair_norm", "down_resid")
-# The same layer with the split-K carry (the decoder's default fused path):
+# The same layer with the split-K carry (Decoder.carry_mode "split", bit-reproducible):
 # o and down leave their partials, gate/up and the next q/k/v finish them.
 CARRIED_CLASSES = ("qkv_decode_carried", "o_partials", "gate_up_pair_norm_carried", "down_partials")
+# The same layer with the accumulated carry (the decoder's default, Decoder.carry_mode "accumulate"): o,
+# the gate/up pair and down add into fp32 rows; gate/up, down and the next q/k/v finish them.
+ACCUMULATED_CLASSES = ("qkv_decode_acc", "o_acc", "gate_up_pair_acc", "down_silu_acc")
 
 
 def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60) -> float:
@@ -570,7 +605,8 @@ def decode_classes(model, ratios, reps=20, warmup=5, rotate_bytes=1 << 30, log=p
             log(f"{model} {nnz}:{m} {c:26s}: {us:7.2f} +- {sd:.2f} us {per[c]['GBps']:7.1f} GB/s "
                 f"({per[c]['pct_peak']}%)")
         r = {"classes": per}
-        for tag, group in (("token", DECODE_CLASSES), ("token_carried", CARRIED_CLASSES)):
+        for tag, group in (("token", DECODE_CLASSES), ("token_carried", CARRIED_CLASSES),
+                           ("token_accumulated", ACCUMULATED_CLASSES)):
             if all(c in per for c in group):
                 t_us = sum(per[c]["us"] for c in group) * cfg.n_layers
                 t_b = sum(per[c]["bytes"] for c in group) * cfg.n_layers
@@ -592,7 +628,10 @@ def write_decode_classes_md(model, res, path, cmd):
     names = {"qkv_decode": qkv, "o_resid": "o + residual", "gate_up_pair_norm": "gate/up pair + RMSNorm + SiLU*mul",
              "down_resid": "down + residual", "qkv_decode_carried": qkv + ", carried input",
              "o_partials": "o, partials left", "gate_up_pair_norm_carried": "gate/up pair + RMSNorm + SiLU*mul, carried input",
-             "down_partials": "down, partials left"}
+             "down_partials": "down, partials left", "qkv_decode_acc": qkv + ", input from an accumulated row",
+             "o_acc": "o, adding into an fp32 row", "gate_up_pair_acc": "gate/up pair + RMSNorm, input from o's row, "
+                                                                   "adding its sums into an fp32 row",
+             "down_silu_acc": "down on the pair's SiLU product, adding into an fp32 row"}
     lines = [f"# Sparse GEMV launches of the fused decoder layer: {cfg.name} shapes (MI355X, fp16, batch 1)", "",
              "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
              f"The decoder's four launches per layer at {cfg.name}'s shapes (dim {cfg.dim}, intermediate "
@@ -603,13 +642,16 @@ def write_decode_classes_md(model, res, path, cmd):
              "activations once, norm weights, residual, outputs, RoPE row); % of the 8 TB/s HBM peak. 'Token' sums",
              f"one decode token's {4 * cfg.n_layers} launches ({cfg.n_layers} layers); 'carried' rows are the layer",
              "with the split-K carry (o and down leave their fp32 partials; gate/up and the next q/k/v finish",
-             "them, reading the residual and writing the finished vector; the partials are not counted).", "",
+             "them, reading the residual and writing the finished vector; the partials are not counted);",
+             "'accumulated' rows are the layer with the accumulated carry (the decoder's default: o, the gate/up",
+             "pair and down add into fp32 rows, the next launch finishes them; the rows are not counted).", "",
              "| N:M | Launch | us (median +- sd) | Algorithmic bytes | GB/s | % peak |", "|---|---|---|---|---|---|"]
     for ratio, r in res.items():
         for c, v in r["classes"].items():
             lines.append(f"| {ratio} | {names[c]} | {v['us']:.2f} +- {v['us_sd']:.2f} | {v['bytes']:,} | "
                          f"{v['GBps']:.0f} | {v['pct_peak']:.1f}% |")
-        for tag, label in (("token", "token"), ("token_carried", "token, carried")):
+        for tag, label in (("token", "token"), ("token_carried", "token, carried"),
+                           ("token_accumulated", "token, accumulated carry")):
             if tag in r:
                 t = r[tag]
                 lines.append(f"| {ratio} | {label} ({4 * cfg.n_layers} launches) | {t['us']:.1f} | {t['bytes']:,} | "
@@ -715,12 +757,12 @@ def traffic_probe(shapes=DEFAULT_DIMS, nnz=32, m=64, log=print):
     del g, u
     log("traffic probe: grouped q/k/v and gate/up pair done")
     forms = DecodeForms(nnz, m, rotate_bytes=0, min_copies=3)
-    for cls in DECODE_CLASSES + CARRIED_CLASSES:
+    for cls in DECODE_CLASSES + CARRIED_CLASSES + ACCUMULATED_CLASSES:
         for i in range(3):
             forms.launch(cls, i)
         torch.cuda.synchronize()
     del forms
-    log("traffic probe: decode-form launches (plain and carried) done")
+    log("traffic probe: decode-form launches (plain, split carry, accumulated carry) done")
     from .hip_spmv import nmsparse_spmm_forward_hip
     from .profiling import SPMM_PROBE_CLASSES
 
@@ -810,7 +852,8 @@ def main(argv=None):
     if a.decode_classes:
         res = decode_classes(a.decode_classes, _parse_pairs(a.ratios, ":"), a.reps, a.warmup, a.rotate_mib << 20,
                              log=lambda s: print(s, flush=True),
-                             classes=DECODE_CLASSES + CARRIED_CLASSES if a.carried else DECODE_CLASSES)
+                             classes=(DECODE_CLASSES + CARRIED_CLASSES + ACCUMULATED_CLASSES if a.carried
+                                      else DECODE_CLASSES))
         if a.json:
             Path(a.json).write_text(json.dumps(res, indent=1))
         if a.md:

@@ -38,6 +38,12 @@ PROBE_CLASSES = [
     ("o_partials_32:64", None, None, None, "o, split partials left for the next launch"),
     ("gate_up_pair_norm_carried_32:64", None, None, None, "gate/up pair + RMSNorm, input carried from o's partials"),
     ("down_partials_32:64", None, None, None, "down, split partials left for the next launch"),
+    ("qkv_decode_acc_32:64", None, None, None, "q/k/v decode form, input carried from down's accumulated row; "
+                                               "clears o's and the pair's rows"),
+    ("o_acc_32:64", None, None, None, "o, adding into an fp32 row (accumulated carry)"),
+    ("gate_up_pair_acc_32:64", None, None, None, "gate/up pair + RMSNorm, input carried from o's row, adding its raw "
+                                                 "sums into an fp32 row; clears down's row"),
+    ("down_silu_acc_32:64", None, None, None, "down, input the pair's SiLU product, adding into an fp32 row"),
 ]
 
 
@@ -86,14 +92,14 @@ def _read(path):
 
 def gemv_args(name: str):
     """The template arguments of an nm_gemv_kernel name, <dtype, TH, U, G, NT,
-    NMAT, NORM, CARRY>, as a dict (None for any other kernel)."""
+    NMAT, NORM, CARRY, SILU>, as a dict (None for any other kernel)."""
     if "nm_gemv_kernel<" not in name:
         return None
     a = name[name.index("nm_gemv_kernel<") + len("nm_gemv_kernel<"):]
     a = [v.strip() for v in a[:a.index(">")].split(",")]
-    keys = ("dtype", "th", "u", "g", "nt", "nmat", "norm", "carry")
+    keys = ("dtype", "th", "u", "g", "nt", "nmat", "norm", "carry", "silu")
     d = dict(zip(keys, a))
-    return {k: (v == "true" if k in ("nt", "norm") else int(v)) for k, v in d.items()}
+    return {k: (v == "true" if k in ("nt", "norm", "silu") else int(v)) for k, v in d.items()}
 
 
 def _gemv_dispatches(rows):
@@ -169,7 +175,8 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
              "<dtype (0 = fp16), TH (tile = 8*TH rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT",
              "(2 = gate/up pair), NORM (input RMSNorm folded into the gather), CARRY (most producer splits a carried",
              "input reads; 0 = none)>. The decode-form classes are the launches of the decoder's fused layer",
-             "(microbench.DecodeForms); bench.py times the carried ones as its step.",
+             "(microbench.DecodeForms): plain, with the split carry and with the accumulated carry (`_acc`; the",
+             "decoder's default, which bench.py times as its step).",
              "",
              f"Calibration: the 256 MiB copy reads {sum(fcopy) / len(fcopy):.1f} KiB by FETCH_SIZE (true "
              f"{CALIBRATION_BYTES // 1024} KiB) -> fetch scale {fscale:.4f}; it writes {sum(wcopy) / len(wcopy):.1f} KiB "
@@ -179,7 +186,9 @@ def traffic(fetch_csv, write_csv, md_path, json_path, fetch_cmd, write_cmd):
              "Extra fetch over the algorithmic bytes is the index bytes and activations re-read by every output tile",
              "of a split plus the partial sums read back by the last workgroup of each tile; extra writes are the fp32",
              "split-K partials (8 splits x h x 4 B per matrix). A carried launch also fetches the producer's partials",
-             "(splits x K x 4 B, once per XCD's L2), and a producer writes them. No weight byte is fetched twice.",
+             "(splits x K x 4 B, once per XCD's L2), and a producer writes them. An accumulating producer's adds",
+             "are performed at the memory side (agent scope) and counted as writes of the fp32 rows; the launch",
+             "that clears a row writes it once more. No weight byte is fetched twice.",
              "`profiles/traffic.json` holds the same numbers; bench.py reports `bytes_per_launch` of the dominant",
              "launch class as `roofline.traffic`.", "",
              "## SpMM calls (batch > 1)", "",
@@ -204,15 +213,18 @@ def stats(stats_csv, bench_json, md_path, cmd):
              "python -u bench.py > gpurun_out/bench.json", cmd,
              "python -m spmv_decode_amd.profiling stats --csv gpurun_out/prof_bench/bench_kernel_stats.csv "
              "--bench gpurun_out/bench.json --md <this file>", "```", "",
-             "The run covers the decode step graph with the split-K carry (per layer: q/k/v + RMSNorm + RoPE + cache",
-             "write finishing the previous down's partials, o leaving its partials, gate/up pair + RMSNorm + SiLU*mul",
-             "finishing o's, down leaving its partials), the same step without the carry (o and down + residual), the",
-             "plain fused step, the 224-launch step graph, per-class rotation graphs (>= 1 GiB of distinct weights",
-             "each, carried and plain classes), the SpMM graphs (batch 2-8: small-batch kernel; 16-64: the",
-             "activation gather + the matrix-core kernel) and the dense",
+             "The run covers the decode step graph with the accumulated carry (the timed step; per layer: q/k/v +",
+             "RMSNorm + RoPE + cache write finishing the previous down's fp32 row, o adding into its row, the gate/up",
+             "pair + RMSNorm finishing o's row and adding its raw sums into its own, down on the pair's SiLU product",
+             "adding into its row), the same step with the split carry (o and down leave split partials, gate/up",
+             "and q/k/v finish them), without a carry (o and down + residual), the plain fused step, the 224-launch",
+             "step graph, per-class rotation graphs (>= 1 GiB of distinct weights each: accumulated, split-carried",
+             "and plain classes), the SpMM graphs (batch 2-8: small-batch kernel; 16-64: the activation gather + the",
+             "matrix-core kernel) and the dense",
              "hipBLASLt baseline graphs. `nm_gemv_kernel` template arguments: <dtype (0 = fp16), TH (tile = 8*TH",
              "rows), U (rows per lane per chunk), G (gather width / 256), NT, NMAT (2 = gate/up pair), NORM (input",
-             "RMSNorm), CARRY (most producer splits of a carried input; 0 = none)>; `nm_spmm_kernel`: <dtype, TH, U,",
+             "RMSNorm), CARRY (most producer splits of a carried input, 1 = an accumulated row; 0 = none), SILU",
+             "(input the gate/up pair's SiLU product)>; `nm_spmm_kernel`: <dtype, TH, U,",
              "G, NT, batch rows per launch>; `nm_spmm_mc_kernel`: <dtype, batch rows per tile, output columns",
              "per tile, weights DMA-staged into LDS>.", "",
              "| Kernel | Calls | Avg (us) | Min (us) | Max (us) | Share of GPU time |", "|---|---|---|---|---|---|"]
@@ -232,7 +244,8 @@ def stats(stats_csv, bench_json, md_path, cmd):
             g = gemv_args(r["Name"])
             if not g["norm"]:
                 continue
-            what = "with a carried input" if g.get("carry") else "with its own input"
+            what = ("with its input finished from an accumulated row (the timed step's)" if g.get("carry") == 1 else
+                    "with its input finished from split partials" if g.get("carry") else "with its own input")
             lines.append(f"rocprof average kernel duration of the gate/up pair + RMSNorm kernel {what}: "
                          f"{float(r['AverageNs']) / 1e3:.2f} us over {r['Calls']} calls (the kernel alone, in the traced "
                          "run; the replay-timed figure is the interval per launch in the untraced one, gap included).")

@@ -282,6 +282,7 @@ def test_graph_replay_matches_eager_and_masked_dense(gpu):
 
     cfg = tiny_config(qk_norm=True)
     dense, sparse = _masked_pair(cfg, 8)
+    sparse.carry_mode = "split"  # the bit-reproducible carry (the accumulated one varies in the last bits)
     prompt = torch.randint(0, cfg.vocab, (5,), generator=torch.Generator().manual_seed(3))
     # eager reference tokens and logits
     eager = GraphDecoder(sparse, 32)
@@ -465,6 +466,7 @@ def test_restored_compressed_checkpoint_decodes_identically(gpu):
     b.load_state_dict(torch.load(buf, weights_only=True))
     outs = []
     for mdl in (a, b):
+        mdl.carry_mode = "split"  # bit-reproducible run to run
         mdl.setup_cache(8, "cuda", dtype=torch.float16)
         with torch.no_grad():
             outs.append([mdl.forward_step(torch.tensor([[t]], device="cuda"), torch.tensor([i], device="cuda"))

@@ -152,6 +152,7 @@ def test_full_depth_decode_parity(gpu, name, M, layers):
     _free()
     say(f"{tag}: building the sparse model")
     model = sparse_model(cfg, M, seed=M + cfg.n_layers)
+    model.carry_mode = "split"  # graph replay bit-identical to eager; the accumulated carry is checked below
     prompt = torch.randint(0, cfg.vocab, (PROMPT,), generator=torch.Generator().manual_seed(M))
     say(f"{tag}: eager vs graph replay, {STEPS} steps")
     seq, eager = graph_matches_eager(model, prompt, STEPS)
@@ -227,6 +228,7 @@ def test_decode_parity_at_the_configs_context(gpu, name, M, P, positions):
     _free()
     say(f"{tag}: building the sparse model")
     model = sparse_model(cfg, M, seed=M + P)
+    model.carry_mode = "split"  # graph replay bit-identical to eager; the accumulated carry is checked below
     prompt = torch.randint(0, cfg.vocab, (P,), generator=torch.Generator().manual_seed(P))
     gd = GraphDecoder(model, positions)
     assert model.max_seq == cache_length(positions)
@@ -262,6 +264,11 @@ def test_decode_parity_at_the_configs_context(gpu, name, M, P, positions):
         model.set_launch_mode(mode)
         logits[mode] = prefilled_then_steps(model, prompt, fed, positions)
     model.set_launch_mode("fused")
+    say(f"{tag}: prefill + teacher-forced fused, accumulated carry")
+    model.carry_mode = "accumulate"
+    logits["fused_accumulate"] = prefilled_then_steps(model, prompt, fed, positions)
+    assert len(model._carry[1]) == 4  # the accumulated layers ran
+    model.carry_mode = "split"
     for dtype in (torch.float32, torch.float16):
         say(f"{tag}: masked dense twin {dtype}")
         twin = dense_twin(model, dtype)
@@ -279,7 +286,7 @@ def test_decode_parity_at_the_configs_context(gpu, name, M, P, positions):
     assert all(torch.isfinite(v).all() for v in logits.values())
     assert e16 < 0.05, e16
     bound = 2 * e16 + 1e-3
-    for k in ("eager", "fused", "per_linear", "grouped", "modules"):
+    for k in ("eager", "fused", "fused_accumulate", "per_linear", "grouped", "modules"):
         assert err[k] <= bound, (k, err[k], bound)
     assert cross <= 3 * e16 + 1e-3, cross
     assert to_dense16 <= 3 * e16 + 1e-3, to_dense16
