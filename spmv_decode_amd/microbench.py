@@ -673,9 +673,11 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
     kernels."""
     from .hip_spmv import launch_plan
 
-    carried = cls.endswith("_carried")
-    pair = cls.startswith("gate_up_pair_norm")
-    if cls not in ("gate_up_pair_norm", "qkv_decode", "gate_up_pair_norm_carried", "qkv_decode_carried"):
+    carried = cls.endswith("_carried") or cls in ("gate_up_pair_acc", "qkv_decode_acc")
+    pair = cls.startswith("gate_up_pair")
+    single = {"o_acc": "o", "down_silu_acc": "down"}.get(cls)  # accumulating producers: one matrix
+    if cls not in ("gate_up_pair_norm", "qkv_decode", "gate_up_pair_norm_carried", "qkv_decode_carried",
+                   "gate_up_pair_acc", "qkv_decode_acc", "o_acc", "down_silu_acc"):
         raise ValueError(f"launch_sweep: {cls!r} is not a fused decoder launch with its own plan")
     if model:  # another model's shapes (default: Llama-3.1-8B)
         from .decode.model import CONFIGS
@@ -685,7 +687,11 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
                             head_dim=c.head_dim, qk_norm=c.qk_norm)
     else:
         forms = DecodeForms(nnz, m)
-    mats = [forms.gate.mats[0], forms.up.mats[0]] if pair else [forms.q.mats[0], forms.k.mats[0], forms.v.mats[0]]
+    if single:
+        mats = [getattr(forms, single).mats[0]]
+    else:
+        mats = ([forms.gate.mats[0], forms.up.mats[0]] if pair
+                else [forms.q.mats[0], forms.k.mats[0], forms.v.mats[0]])
     hs = [forms.inter] if pair else [int(md.shape[1]) for md, _ in mats]
     nbytes = forms.bytes(cls)
     n = forms.copies[cls]
@@ -693,7 +699,8 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
     rows, seen = [], set()
     for cfg in [-1, *range(n_cfg)]:
         for sp in ((0,) if cfg < 0 else splits_list):
-            plan = launch_plan(mats, nnz, m, gate_up=pair, config_id=cfg, splits=sp, carried=carried)
+            plan = launch_plan(mats, nnz, m, gate_up=pair, config_id=cfg, splits=sp, carried=carried,
+                               producer=bool(single))
             key = (plan["config_id"], plan["splits"])
             if cfg >= 0 and key in seen:
                 continue
@@ -708,17 +715,18 @@ def launch_sweep(cls="gate_up_pair_norm", nnz=32, m=64, splits_list=(4, 6, 7, 8,
             def launch(i, cfg=cfg, sp=sp):
                 forms.launch(cls, i, config_id=cfg, splits=sp)
 
-            if carried:
+            if carried or single:
                 try:
                     launch(0)
                 except _lib.NmSparseLibraryError:
-                    log(f"{cls} {name} s={plan['splits']}: this plan cannot take a carried input, skipped")
+                    log(f"{cls} {name} s={plan['splits']}: the library rejects this plan for the launch, skipped")
                     continue
             us = graph_us_per_launch([lambda i=i: launch(i) for i in range(n)], reps, warmup)
-            rows.append({"config": name, "config_id": plan["config_id"], "n_out": sum(hs), "n_in": forms.dim,
+            rows.append({"config": name, "config_id": plan["config_id"], "n_out": sum(hs),
+                         "n_in": forms.inter if single == "down" else forms.dim,
                          "ratio": f"{nnz}:{m}", "splits": plan["splits"], "blocks": plan["blocks"],
                          "us": round(us, 3), "GBps": round(nbytes / us / 1e3, 1), "nmat": 2 if pair else 1,
-                         "norm": 1})
+                         "norm": 0 if single else 1})
             log(f"{cls} {name} s={plan['splits']} blocks {plan['blocks']}: {us:.2f} us {nbytes / us / 1e3:.0f} GB/s")
     del forms
     torch.cuda.empty_cache()
@@ -827,6 +835,9 @@ def main(argv=None):
     p.add_argument("--qkv-sweep", action="store_true",
                    help="the same for the decoder's q/k/v launch (norm, RoPE, cache write) and the plain "
                         "configurations")
+    p.add_argument("--launch-sweep", default=None, metavar="CLASS",
+                   help="the same for one accumulated-carry launch class: gate_up_pair_acc, qkv_decode_acc, o_acc "
+                        "or down_silu_acc")
     p.add_argument("--decode-classes", default=None, metavar="MODEL",
                    help="time the fused decoder layer's four launches at MODEL's shapes (llama-3.1-8b, qwen3-14b, "
                         "qwen3-32b) for each --ratios entry")
@@ -838,9 +849,10 @@ def main(argv=None):
                         "(o and down leave their partials, gate/up and q/k/v finish them); with --pair-sweep / "
                         "--qkv-sweep: sweep the launch with a carried input")
     a = p.parse_args(argv)
-    if a.pair_sweep or a.qkv_sweep:
+    if a.pair_sweep or a.qkv_sweep or a.launch_sweep:
         nnz, m = _parse_pairs(a.ratios, ":")[0]
-        cls = ("gate_up_pair_norm" if a.pair_sweep else "qkv_decode") + ("_carried" if a.carried else "")
+        cls = a.launch_sweep or (("gate_up_pair_norm" if a.pair_sweep else "qkv_decode")
+                                 + ("_carried" if a.carried else ""))
         rows = launch_sweep(cls, nnz, m, reps=a.reps, warmup=a.warmup, log=lambda s: print(s, flush=True),
                             model=a.model)
         if a.csv:
