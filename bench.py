@@ -479,15 +479,21 @@ def main():
         b1 = per_shape[cls]["us_per_launch"]
         rows = {}
         for batch in (2, 4, 8, 16, 32, 64):
-            us = MB.time_spmm(h, K, nnz, m, batch, reps=reps)
-            rows[str(batch)] = {"kernel": "small-batch" if batch <= 8 else "matrix-core",
+            routed = batch > 8 and hip_spmv.library_route(batch, K, h)
+            us = MB.time_spmm(h, K, nnz, m, batch, reps=reps)  # the library's automatic choice
+            rows[str(batch)] = {"kernel": ("small-batch" if batch <= 8 else
+                                           "gather + hipBLASLt" if routed else "matrix-core"),
                                 "us_per_launch": round(us, 3), "us_per_row": round(us / batch, 3),
                                 "speedup_per_row_vs_batch1": round(b1 * batch / us, 3),
                                 "weight_GBps": round(sparse_bytes(K, h, nnz, m) / (us * 1e-6) / 1e9, 1)}
-            if batch > 8:  # the library route beside it: gather + one hipBLASLt GEMM of [batch, w] x [w, h]
+            if batch > 8:  # the matrix-core kernel and the library route (gather + one hipBLASLt GEMM) side by side
+                mc_us = MB.time_spmm(h, K, nnz, m, batch, reps=reps, matrix_cores=True) if routed else us
                 lib_us = MB.time_gather_gemm(h, K, nnz, m, batch, reps=reps)
+                rows[str(batch)]["matrix_core_us"] = round(mc_us, 3)
+                rows[str(batch)]["matrix_core_weight_GBps"] = round(sparse_bytes(K, h, nnz, m) / (mc_us * 1e-6) / 1e9,
+                                                                    1)
                 rows[str(batch)]["gather_plus_hipblaslt_us"] = round(lib_us, 3)
-                rows[str(batch)]["speedup_vs_gather_plus_hipblaslt"] = round(lib_us / us, 3)
+                rows[str(batch)]["speedup_matrix_core_vs_gather_plus_hipblaslt"] = round(lib_us / mc_us, 3)
             log(f"spmm {cls:8s} batch {batch}: {us:7.2f} us/launch, {us / batch:6.2f} us/row "
                 f"({rows[str(batch)]['speedup_per_row_vs_batch1']}x per row vs batch 1)")
         spmm[cls] = rows

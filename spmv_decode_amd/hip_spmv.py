@@ -224,6 +224,18 @@ def _aligned(md):
     return md if md.data_ptr() % 16 == 0 else md.clone()
 
 
+def library_route(rows: int, K: int, h: int) -> bool:
+    """Whether nmsparse_spmm_forward_hip's automatic choice, for a 16-bit
+    product of `rows` (> NM_MAX_BATCH) rows, is the gathered activations times
+    mat_data on hipBLASLt rather than the matrix-core SpMM: past
+    NM_MC_MAX_BATCH rows (one GEMM instead of several launches), and from 32
+    rows for the wide shapes (h >= 3 K: the gate/up projections), where the
+    library's GEMM measured 1-8% faster on MI355X (Llama-3.1-8B 4096 -> 14336
+    at 64 rows 22.0 against 23.7 us, Qwen3-14B / Qwen3-32B gate/up alike);
+    the matrix-core kernel is faster at every other shape, by up to 2.2x."""
+    return rows > _lib.NM_MC_MAX_BATCH or (rows >= 32 and h >= 3 * K)
+
+
 def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1,
                               splits=0, matrix_cores=None):
     """out[..., r, :] = W_sparse @ x[..., r, :] for every row of x ([..., rows, K]),
@@ -240,13 +252,13 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     (NM_MC_MAX_BATCH rows per launch; fp32 accumulation in the matrix cores'
     own order, see _lib.spmm_mc_plan). matrix_cores=None takes the matrix
     cores for NM_MAX_BATCH < rows <= NM_MC_MAX_BATCH of a 16-bit type when
-    config_id and splits are left to the library, and beyond that the
-    gathered activations (nm_gather_columns, [rows, w]) times mat_data as one
-    hipBLASLt GEMM (torch.matmul: a plain GEMM over half the input width,
-    faster than launches of 64 rows on the matrix-core kernel); else the
-    small-batch kernel. True / False forces one of the two HIP kernels (True
-    needs fp16 or bf16). config_id and splits are those of the kernel that
-    runs.
+    config_id and splits are left to the library, and the library route
+    instead (library_route) past NM_MC_MAX_BATCH rows and where it measured
+    faster: the gathered activations (nm_gather_columns, [rows, w]) times
+    mat_data as one hipBLASLt GEMM (torch.matmul: a plain GEMM over half the
+    input width); else the small-batch kernel. True / False forces one of the
+    two HIP kernels (True needs fp16 or bf16). config_id and splits are those
+    of the kernel that runs.
     """
     if not (x.is_cuda and mat_data.is_cuda and mat_index.is_cuda):
         raise ValueError("x, mat_data, and mat_index must be GPU (HIP) tensors")
@@ -283,7 +295,7 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     library_gemm = False
     if matrix_cores is None:
         matrix_cores = sixteen and rows > _lib.NM_MAX_BATCH and config_id < 0 and splits <= 0
-        library_gemm = matrix_cores and rows > _lib.NM_MC_MAX_BATCH
+        library_gemm = matrix_cores and library_route(rows, K, h)
     elif matrix_cores and not sixteen:
         raise TypeError("the matrix-core SpMM takes fp16 or bf16")
     md = _aligned(mat_data)
@@ -714,4 +726,5 @@ def nmsparse_qkv_decode(vec, q, k, v, BLOCK_WIDTH, VEC_WIDTH, *, q_out, k_cache_
 __all__ = ["nmsparse_spmv_forward_hip", "nmsparse_spmv_forward_triton_ptx", "nmsparse_gemv_grouped",
            "nmsparse_gate_up_silu", "nmsparse_gemv_launch", "nmsparse_qkv_decode", "nmsparse_spmm_forward_hip",
            "nmsparse_gemv_partials", "carry_splits", "GemvProblem", "launch_plan", "validate_args", "workspace_for",
-           "nmsparse_gemv_accumulate", "nmsparse_gate_up_accumulate", "nmsparse_gemv_silu", "gate_up_ssq_slots"]
+           "nmsparse_gemv_accumulate", "nmsparse_gate_up_accumulate", "nmsparse_gemv_silu", "gate_up_ssq_slots",
+           "library_route"]

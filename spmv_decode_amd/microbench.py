@@ -352,9 +352,11 @@ CARRIED_CLASSES = ("qkv_decode_carried", "o_partials", "gate_up_pair_norm_carrie
 ACCUMULATED_CLASSES = ("qkv_decode_acc", "o_acc", "gate_up_pair_acc", "down_silu_acc")
 
 
-def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60) -> float:
-    """us per SpMM call of `batch` rows (the library's kernel choice: the
-    small-batch SpMM up to 8 rows, the matrix-core SpMM above), weights rotated."""
+def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60, matrix_cores=None) -> float:
+    """us per SpMM call of `batch` rows (matrix_cores=None: the library's
+    choice, the small-batch SpMM up to 8 rows, then the matrix-core SpMM or the
+    gather + hipBLASLt route, hip_spmv.library_route; True: the matrix-core
+    kernel), weights rotated."""
     from .hip_spmv import nmsparse_spmm_forward_hip
 
     case = RotatingCase(n_out, n_in, nnz, m, rotate_bytes=rotate_bytes, seed=seed)
@@ -363,7 +365,7 @@ def time_spmm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=60
 
     def launch(i):
         md, mi = case.mats[i]
-        nmsparse_spmm_forward_hip(X, md, mi, case.w, n_out, nnz, m, out=out)
+        nmsparse_spmm_forward_hip(X, md, mi, case.w, n_out, nnz, m, out=out, matrix_cores=matrix_cores)
 
     us = graph_us_per_launch([lambda i=i: launch(i) for i in range(case.copies)], reps)
     del case

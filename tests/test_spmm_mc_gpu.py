@@ -95,6 +95,31 @@ def test_more_than_64_rows_gather_and_library_gemm(gpu, dtype):
         assert bool((xg[:, w:] == 0).all())
 
 
+def test_wide_shapes_from_32_rows_take_the_library_route(gpu):
+    """hip_spmv.library_route: from 32 rows a wide product (h >= 3 K, the
+    gate/up shapes) gathers and multiplies on hipBLASLt, the same bits as the
+    explicit gather + GEMM; 31 rows, and narrower shapes at 32, keep the
+    matrix-core kernel (the same bits as forcing it). Both within the oracle
+    bar."""
+    for K, h, rows, routed in ((4096, 14336, 32, True), (4096, 14336, 31, False), (4096, 14336, 64, True),
+                               (5120, 17408, 40, True), (4096, 4096, 32, False), (14336, 4096, 64, False)):
+        assert hip_spmv.library_route(rows, K, h) == routed, (K, h, rows)
+        _, md, mi = make_case(K, h, 32, 64, seed=K + h + rows)
+        w = md.shape[0]
+        X = torch.randn(rows, K, generator=torch.Generator(device="cuda").manual_seed(rows), device="cuda").half()
+        say(f"spmm auto route K{K} h{h} rows {rows} library {routed}")
+        auto = hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, h, 32, 64)
+        if routed:
+            wp = (w + 7) // 8 * 8
+            xg = torch.empty(rows, wp, dtype=X.dtype, device="cuda")
+            _lib.check(_lib.load().nm_gather_columns(0, X.data_ptr(), K, rows, mi.data_ptr(), w, 32, 64, xg.data_ptr(),
+                                                     wp, torch.cuda.current_stream().cuda_stream), "nm_gather_columns")
+            assert torch.equal(auto, torch.matmul(xg[:, :w], md))
+        else:
+            assert torch.equal(auto, mc(X, md, mi, 32, 64))
+        check_rows(auto, X, md, mi, 32, 64, f"auto K{K} h{h} rows {rows}")
+
+
 def test_c_abi_row_strides(gpu):
     """x and out with padded rows through the C ABI directly."""
     K, h, nnz, m, B = 4096, 4096, 32, 64, 20
