@@ -789,7 +789,9 @@ def decode_ms_per_token(m, log):
                "protocol": "the fixed-context protocol above, torch.compile (inductor, fullgraph) of the step of the "
                            "model as written for dense Linears, swapped by swap_to_nmsparse: every projection a module "
                            "call; the compile pass (spmv_decode_amd/compile_pass.py) turns each layer's sibling gemv "
-                           "calls into one grouped q/k/v launch (HF names) and one gate/up pair launch with SiLU*mul",
+                           "calls into one grouped q/k/v launch (HF names) and one gate/up pair launch with SiLU*mul, "
+                           "folds the RMSNorm in front of q/k/v and gate/up into those launches and the residual "
+                           "adds after o and down into theirs",
                "hf_names": {"sparse_ms_per_token": _finite(fixed_mod_c["median"]),
                             "eager_sparse_ms_per_token": round(fixed_mod["median"], 4),
                             "speedup_vs_fastest_compiled_dense": ratio(fastest_fcc, fixed_mod_c["median"]),

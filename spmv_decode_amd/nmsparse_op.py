@@ -29,11 +29,14 @@ run to run) adds `nmsparse::gemv_accumulate_`, `nmsparse::gate_up_accumulate_`
 gathers its input), and the `zero` argument of the q/k/v ops (an accumulator
 cleared by the launch).
 
-`nmsparse::gemv_grouped` (one launch for 2-4 gemv calls on the same input)
-and `nmsparse::gemv_silu_mul` (silu(gemv gate) * gemv up in one launch) are
-what the torch.compile pass of compile_pass.py rewrites sibling `gemv` calls
-into, so that unmodified model code compiled with torch.compile gets one
-q/k/v and one gate/up launch per layer (no reference counterpart).
+`nmsparse::gemv_grouped` (one launch for 1-4 gemv calls on the same input),
+`nmsparse::gemv_silu_mul` (silu(gemv gate) * gemv up in one launch), both
+with an optional input RMSNorm folded in, and `nmsparse::gemv_residual`
+(residual + gemv in one launch) are what the torch.compile pass of
+compile_pass.py rewrites `gemv` calls into, so that unmodified model code
+compiled with torch.compile gets one q/k/v and one gate/up launch per layer,
+with the RMSNorm in front of them and the residual adds after o and down
+inside the launches (no reference counterpart).
 
 Backend selection keeps the reference's `NM_KERNEL` contract of refusing
 unknown values (src/spmv/nmsparse_op.py:20-22). Unset, "hip" and
@@ -118,40 +121,79 @@ def _fp16(t: torch.Tensor) -> torch.Tensor:
     return t if t.dtype == torch.float16 else t.to(torch.float16)
 
 
+def _norm(x16: torch.Tensor, weight: Optional[torch.Tensor], eps: float):
+    """The launch's input RMSNorm argument: (weight as x16's dtype, eps), or None."""
+    return None if weight is None else (weight.to(x16.dtype).contiguous(), float(eps))
+
+
+def _normed_input(x: torch.Tensor, weight: Optional[torch.Tensor], name: str) -> torch.Tensor:
+    """_decode_rows(x), copied to fresh memory when a folded RMSNorm needs a
+    16-byte aligned input and x is a view that starts elsewhere."""
+    xh = _decode_rows(x, name)
+    return xh.clone() if weight is not None and xh.data_ptr() % 16 else xh
+
+
 @torch.library.custom_op("nmsparse::gemv_grouped", mutates_args=())
 def gemv_grouped(x: torch.Tensor, mat_data: list[torch.Tensor], mat_index: list[torch.Tensor], w: int,
-                 h: list[int], block_width: int, vec_width: int) -> list[torch.Tensor]:
-    """[gemv(x, mat_data[i], mat_index[i], w, h[i], ...) for i] as one launch
-    (2-4 problems sharing x, w and N:M; hip_spmv.nmsparse_gemv_grouped), with
-    gemv's rows check, casts and output shapes. What the compile pass
-    (compile_pass.group_sibling_gemvs) puts in place of sibling gemv calls."""
-    xh = _decode_rows(x, "gemv_grouped")
+                 h: list[int], block_width: int, vec_width: int, norm_weight: Optional[torch.Tensor],
+                 norm_eps: float) -> list[torch.Tensor]:
+    """[gemv(x', mat_data[i], mat_index[i], w, h[i], ...) for i] as one launch
+    (1-4 problems sharing x, w and N:M; hip_spmv.nmsparse_gemv_grouped), with
+    gemv's rows check, casts and output shapes; x' = RMSNorm(x) * norm_weight
+    folded into the launch when norm_weight is given, else x. What the
+    compile pass (compile_pass.py) puts in place of sibling gemv calls, and of
+    gemv calls on an RMSNorm's output."""
+    xh = _normed_input(x, norm_weight, "gemv_grouped")
     outs = nmsparse_gemv_grouped(xh, [(_fp16(md), mi) for md, mi in zip(mat_data, mat_index)], int(block_width),
-                                 int(vec_width))
+                                 int(vec_width), norm=_norm(xh, norm_weight, norm_eps))
     return [o.to(dtype=x.dtype).reshape(*x.shape[:-1], int(hi)) for o, hi in zip(outs, h)]
 
 
 @gemv_grouped.register_fake
-def _(x, mat_data, mat_index, w, h, block_width, vec_width):
+def _(x, mat_data, mat_index, w, h, block_width, vec_width, norm_weight, norm_eps):
     return [x.new_empty((*x.shape[:-1], int(hi))) for hi in h]
 
 
 @torch.library.custom_op("nmsparse::gemv_silu_mul", mutates_args=())
 def gemv_silu_mul(x: torch.Tensor, gate_data: torch.Tensor, gate_index: torch.Tensor, up_data: torch.Tensor,
-                  up_index: torch.Tensor, w: int, h: int, block_width: int, vec_width: int) -> torch.Tensor:
-    """silu(gemv(x, gate)) * gemv(x, up) as one launch of the gate/up pair
+                  up_index: torch.Tensor, w: int, h: int, block_width: int, vec_width: int,
+                  norm_weight: Optional[torch.Tensor], norm_eps: float) -> torch.Tensor:
+    """silu(gemv(x', gate)) * gemv(x', up) as one launch of the gate/up pair
     kernel (fp32 sums, SiLU and product, one rounding to fp16), with gemv's
-    rows check, casts and output shape. What the compile pass puts in place of
-    a SiLU-gated pair of sibling gemv calls."""
-    xh = _decode_rows(x, "gemv_silu_mul")
+    rows check, casts and output shape; x' = RMSNorm(x) * norm_weight folded
+    into the launch when norm_weight is given. What the compile pass puts in
+    place of a SiLU-gated pair of sibling gemv calls."""
+    xh = _normed_input(x, norm_weight, "gemv_silu_mul")
     y = nmsparse_gate_up_silu(xh, (_fp16(gate_data), gate_index), (_fp16(up_data), up_index), int(block_width),
-                              int(vec_width))
+                              int(vec_width), norm=_norm(xh, norm_weight, norm_eps))
     return y.to(dtype=x.dtype).reshape(*x.shape[:-1], int(h))
 
 
 @gemv_silu_mul.register_fake
-def _(x, gate_data, gate_index, up_data, up_index, w, h, block_width, vec_width):
+def _(x, gate_data, gate_index, up_data, up_index, w, h, block_width, vec_width, norm_weight, norm_eps):
     return x.new_empty((*x.shape[:-1], int(h)))
+
+
+@torch.library.custom_op("nmsparse::gemv_residual", mutates_args=())
+def gemv_residual(x: torch.Tensor, mat_data: torch.Tensor, mat_index: torch.Tensor, w: int, h: int,
+                  block_width: int, vec_width: int, residual: torch.Tensor) -> torch.Tensor:
+    """residual + gemv(x, ...) with the add inside the launch (fp32, one
+    rounding to fp16), shaped like residual ([..., h], fp16). What the compile
+    pass puts in place of a gemv call whose only use is a residual add."""
+    xh = _decode_rows(x, "gemv_residual")
+    res = residual.reshape(-1).contiguous()
+    if res.numel() != int(h) or res.dtype != torch.float16:
+        raise RuntimeError(f"gemv_residual: residual must hold {int(h)} fp16 values, got {tuple(residual.shape)} "
+                           f"{residual.dtype}")
+    out = torch.empty(1, int(h), dtype=torch.float16, device=xh.device)
+    nmsparse_gemv_launch(xh, [GemvProblem(_fp16(mat_data), mat_index, out, residual=res)], int(block_width),
+                         int(vec_width))
+    return out.reshape(residual.shape)
+
+
+@gemv_residual.register_fake
+def _(x, mat_data, mat_index, w, h, block_width, vec_width, residual):
+    return residual.new_empty(residual.shape)
 
 
 @torch.library.custom_op("nmsparse::qkv_decode", mutates_args=("q_out", "k_cache_t", "v_cache_t", "zero"))
@@ -321,6 +363,6 @@ def _(silu_in, mat_data, mat_index, block_width, vec_width, ssq_n, silu_k, silu_
     return None
 
 
-__all__ = ["gemv", "spmm", "gemv_grouped", "gemv_silu_mul", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_",
+__all__ = ["gemv", "spmm", "gemv_grouped", "gemv_silu_mul", "gemv_residual", "qkv_decode", "gemv_add_", "gate_up_silu", "gemv_partials_",
            "qkv_decode_carried", "gate_up_silu_carried", "gemv_accumulate_", "gate_up_accumulate_",
            "gemv_silu_accumulate_", "gemv_silu_add_"]

@@ -76,6 +76,76 @@ def test_pass_rewrites_the_decoder_step(layout, qk_norm):
                 assert all(u.target is operator.getitem for u in n.users)
 
 
+@pytest.mark.parametrize("layout,qk_norm", [("hf", False), ("hf", True), ("gpt-fast", False)])
+def test_pass_folds_input_norms_and_residual_adds(layout, qk_norm):
+    """After the grouping, the RMSNorm in front of q/k/v and of the gate/up pair
+    folds into those launches (they read the residual stream with the norm's
+    weight and eps; the norm's own nodes are gone), and each residual add
+    after o and down folds into that gemv (gemv_residual). Left: the final
+    norm before the dense lm_head and Qwen3's q/k norms."""
+    model = _sparse_tiny(layout, qk_norm)
+    gm = _trace_step(model)
+    L = model.cfg.n_layers
+    compile_pass.group_sibling_gemvs(gm.graph)
+    assert compile_pass.fold_input_norms(gm.graph) == 2 * L
+    assert compile_pass.fold_residuals(gm.graph) == 2 * L
+    gm.recompile()
+    assert _counts(gm.graph) == {"gemv_grouped": L, "gemv_silu_mul": L}
+    res = [n for n in gm.graph.nodes if n.op == "call_function" and n.target is OPS.gemv_residual.default]
+    assert len(res) == 2 * L and all("val" in n.meta for n in res)
+    for n in gm.graph.nodes:
+        if n.op == "call_function" and n.target in (OPS.gemv_grouped.default, OPS.gemv_silu_mul.default):
+            assert n.args[-2] is not None and abs(n.args[-1] - model.cfg.norm_eps) < 1e-9
+            assert n.args[0].meta["val"].dtype == torch.float16
+    rsqrt = sum(1 for n in gm.graph.nodes if n.op == "call_function" and n.target is torch.ops.aten.rsqrt.default)
+    assert rsqrt == 1 + (2 * L if qk_norm else 0)
+
+
+def test_norm_and_residual_folds_need_their_exact_forms():
+    """Norm forms as Hugging Face and gpt-fast write them fold too (weight after
+    the rounding, x*x for the square); a norm whose weight is fp32, an add
+    that broadcasts and a gemv with a second use stay as they are."""
+    lin = NmSparseLinear(128, 64, 8, 1, "cpu")
+    w16 = torch.rand(64).half()
+    w32 = torch.rand(64)
+    from torch._inductor.decomposition import select_decomp_table
+
+    def hf_norm(x, w):
+        h = x.to(torch.float32)
+        h = h * torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + 1e-6)
+        return w * h.to(x.dtype)
+
+    def gpt_fast_norm(x, w):
+        h = x.float()
+        h = h * torch.rsqrt(torch.mean(h * h, dim=-1, keepdim=True) + 1e-5)
+        return h.type_as(x) * w
+
+    def trace(f, x):
+        return make_fx(f, tracing_mode="fake", decomposition_table=select_decomp_table(),
+                       _allow_non_fake_inputs=True)(x)
+
+    x = torch.randn(1, 1, 64).half()
+    for norm, w, folds in ((hf_norm, w16, 1), (gpt_fast_norm, w16, 1), (hf_norm, w32, 0)):
+        gm = trace(lambda t: lin(norm(t, w)), x)
+        assert compile_pass.fold_input_norms(gm.graph) == folds, (norm.__name__, w.dtype)
+    r = torch.randn(1, 1, 128).half()
+    gm = trace(lambda t: lin(t) + r, x)
+    assert compile_pass.fold_residuals(gm.graph) == 1
+    gm = trace(lambda t: lin(t) + r[..., :1], x)  # broadcasts
+    assert compile_pass.fold_residuals(gm.graph) == 0
+    gm = trace(lambda t: (lin(t) + r) * lin(t).sum(), x)
+    before = sum(1 for n in gm.graph.nodes if n.op == "call_function")
+    compile_pass.fold_residuals(gm.graph)  # two separate gemv calls: each used once, so the add folds
+    assert sum(1 for n in gm.graph.nodes if n.op == "call_function") == before - 1
+
+    def used_twice(t):
+        y = lin(t)
+        return (y + r) * y.sum()
+
+    gm = trace(used_twice, x)
+    assert compile_pass.fold_residuals(gm.graph) == 0
+
+
 def test_pass_leaves_other_graphs_alone():
     """No gemv nodes, a single gemv, or siblings of different N:M or input:
     nothing to group."""
@@ -150,7 +220,7 @@ def test_installed_pass_runs_inside_inductor(monkeypatch):
             torch.compile(block, fullgraph=True)(torch.randn(1, 1, 128).half())
     finally:
         torch._dynamo.reset()
-    assert seen == [{"gemv_grouped": 1, "gemv_silu_mul": 1, "gemv": 1}]
+    assert seen == [{"gemv_grouped": 1, "gemv_silu_mul": 1, "gemv": 1}]  # after the grouping, before the folds
 
 
 def test_install_keeps_an_existing_pass_and_uninstall_restores_it(monkeypatch):

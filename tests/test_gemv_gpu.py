@@ -781,9 +781,11 @@ def test_compiled_unmodified_model_groups_siblings(gpu, layout, monkeypatch):
     compiled with inductor (fullgraph, as the reference benchmark compiles its
     step: benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:155): the compile pass
     gives each layer 4 launches (HF names: q/k/v grouped, o, the gate/up pair
-    with SiLU*mul, down; gpt-fast names: wqkv, wo, the w1/w3 pair, w2), counted
-    at the library calls of one compiled step, and its logits agree with the
-    eager steps' (which launch through the sibling ties) within fp16 rounding."""
+    with SiLU*mul, down; gpt-fast names: wqkv, wo, the w1/w3 pair, w2), the
+    RMSNorms in front of q/k/v and gate/up folded into those launches and the
+    residual adds after o and down into theirs, counted at the library calls
+    of one compiled step, and its logits agree with the eager steps' (which
+    launch through the sibling ties) within fp16 rounding."""
     from spmv_decode_amd import nmsparse_op
     from spmv_decode_amd.decode.model import Decoder, init_weights_, tiny_config
     from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
@@ -807,7 +809,8 @@ def test_compiled_unmodified_model_groups_siblings(gpu, layout, monkeypatch):
             say(f"compiling the {layout} step")
             run(compiled)  # compile once
             counts = {}
-            for name in ("nmsparse_spmv_forward_hip", "nmsparse_gemv_grouped", "nmsparse_gate_up_silu"):
+            for name in ("nmsparse_spmv_forward_hip", "nmsparse_gemv_grouped", "nmsparse_gate_up_silu",
+                         "nmsparse_gemv_launch"):
                 real = getattr(nmsparse_op, name)
 
                 def counted(*a, _real=real, _name=name, **k):
@@ -820,8 +823,9 @@ def test_compiled_unmodified_model_groups_siblings(gpu, layout, monkeypatch):
             torch._dynamo.reset()
     torch.cuda.synchronize()
     L, T = cfg.n_layers, tokens.numel()
-    want = ({"nmsparse_gemv_grouped": L * T, "nmsparse_gate_up_silu": L * T, "nmsparse_spmv_forward_hip": 2 * L * T}
-            if layout == "hf" else {"nmsparse_gate_up_silu": L * T, "nmsparse_spmv_forward_hip": 3 * L * T})
+    # q/k/v (HF: three siblings grouped; gpt-fast: wqkv) with the input RMSNorm folded in, the gate/up pair with
+    # the post-attention RMSNorm, o and down with their residual adds (gemv_residual: one launch each)
+    want = {"nmsparse_gemv_grouped": L * T, "nmsparse_gate_up_silu": L * T, "nmsparse_gemv_launch": 2 * L * T}
     assert counts == want, counts
     assert torch.isfinite(got).all()
     rel = float((got.float() - eager.float()).norm() / eager.float().norm())
