@@ -269,10 +269,10 @@ def decode_stats(stats_csv, decode_json, md_path, cmd):
         g = gemv_args(n)
         if g is not None:
             if g["nmat"] == 2:
-                return "sparse GEMV: gate/up pair + RMSNorm + SiLU*mul"
+                return "sparse GEMV: gate/up pair + RMSNorm (+ SiLU*mul, or its sums accumulated)"
             # the input norm marks the q/k/v launch
             return ("sparse GEMV: q/k/v + RMSNorm + RoPE + cache write" if g["norm"]
-                    else "sparse GEMV: o or down (+ residual, or partials left)")
+                    else "sparse GEMV: o or down (+ residual, or partials left / accumulated)")
         if n.startswith("Cijk_"):
             return "attention product (hipBLASLt)" if per_step > 1.5 else "lm_head (hipBLASLt, dense)"
         if "softmax" in n:
