@@ -160,8 +160,8 @@ def test_decode_stats_roles_per_step(tmp_path, setup_calls):
         line = next(ln for ln in text.splitlines() if ln.startswith(f"| {name} |"))
         return float(line.split(" | ")[1])
 
-    assert role("sparse GEMV: gate/up pair + RMSNorm + SiLU*mul") == pytest.approx(32 * 23.0)
-    assert role("sparse GEMV: o or down (+ residual, or partials left)") == pytest.approx(64 * 10.0)
+    assert role("sparse GEMV: gate/up pair + RMSNorm (+ SiLU*mul, or its sums accumulated)") == pytest.approx(32 * 23.0)
+    assert role("sparse GEMV: o or down (+ residual, or partials left / accumulated)") == pytest.approx(64 * 10.0)
     assert role("sparse GEMV: q/k/v + RMSNorm + RoPE + cache write") == pytest.approx(32 * 9.5)
     assert role("attention product (hipBLASLt)") == pytest.approx(32 * 14.0)
     assert role("lm_head (hipBLASLt, dense)") == pytest.approx(180.0)
