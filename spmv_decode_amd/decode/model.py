@@ -399,14 +399,21 @@ class GptFastBlock(nn.Module):
         return h + self.feed_forward(self.ffn_norm(h))
 
 
-def fusable(block: Block) -> bool:
+def fusable(block: Block, dtype=None) -> bool:
     """True when the block's projections can run as the fused sparse layer:
-    q/k/v and gate/up each share one launch, o and down are sparse too."""
+    q/k/v and gate/up each share one launch, o and down are sparse too, and
+    (with `dtype`, the activations' type) every packed weight has that type:
+    the fused launches take their inputs as they are, where a lone
+    `nmsparse::gemv` casts them to the packed weights' fp16 (a bf16 model whose
+    packed weights are fp16 runs its projections one op at a time)."""
     from ..nmsparse_linear import NmSparseLinear
 
     if not isinstance(block, Block):
         return False
     at, mlp = block.self_attn, block.mlp
+    mods = (at.q_proj, at.k_proj, at.v_proj, at.o_proj, mlp.gate_proj, mlp.up_proj, mlp.down_proj)
+    if dtype is not None and not all(getattr(getattr(m, "mat_data", None), "dtype", None) == dtype for m in mods):
+        return False
     return (grouped_sparse((at.q_proj, at.k_proj, at.v_proj)) and grouped_sparse((mlp.gate_proj, mlp.up_proj))
             and isinstance(at.o_proj, NmSparseLinear) and isinstance(mlp.down_proj, NmSparseLinear))
 
@@ -853,7 +860,7 @@ class Decoder(nn.Module):
             self.k_mask.copy_(torch.where(keep, self.zero, self.neg_inf))
         else:
             torch.where(keep, self.zero, self.neg_inf, out=self.k_mask)
-        if self.fuse_epilogues and all(fusable(b) and b.self_attn.group_launches for b in self.layers):
+        if self.fuse_epilogues and all(fusable(b, x.dtype) and b.self_attn.group_launches for b in self.layers):
             x2d = x.view(1, -1)
             if not torch.compiler.is_compiling():
                 self.prepare_decode()

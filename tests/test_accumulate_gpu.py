@@ -295,43 +295,55 @@ def test_accumulate_argument_errors(gpu):
         nmsparse_gemv_launch(x, [GemvProblem(md, mi)], 2, 4, zero=torch.zeros(6, device="cuda"))
 
 
-@pytest.mark.parametrize("qk_norm", [False, True])
-def test_decoder_accumulated_carry_matches_split_carry(gpu, qk_norm):
-    """The tiny decoder with carry_mode "accumulate" (fused_layers_accumulated)
-    against the default split carry over several eager steps, then its graph
-    replays against its eager steps (within fp16 tolerance: the atomic adds'
-    order varies)."""
+@pytest.mark.parametrize("qk_norm,dtype", [(False, torch.float16), (True, torch.float16), (True, torch.bfloat16)],
+                         ids=str)
+def test_decoder_accumulated_carry_matches_split_carry(gpu, qk_norm, dtype):
+    """The tiny decoder with carry_mode "accumulate" (fused_layers_accumulated,
+    the default) against the split carry over several eager steps, then its
+    graph replays against its eager steps (within 16-bit tolerance: the atomic
+    adds' order varies)."""
     from spmv_decode_amd import swap_to_nmsparse
     from spmv_decode_amd.decode import model as dm
     from spmv_decode_amd.decode.runner import GraphDecoder
 
     cfg = dm.tiny_config(qk_norm=qk_norm)
     torch.manual_seed(0)
-    mdl = dm.Decoder(cfg).to("cuda", torch.float16)
+    mdl = dm.Decoder(cfg).to("cuda", dtype)
+    tol = 5e-3 if dtype == torch.float16 else 4e-2
     dm.init_weights_(mdl, seed=0, std=0.05)
     with torch.no_grad():
         for name, prm in mdl.named_parameters():
             if name.endswith("norm.weight"):
                 prm.uniform_(0.5, 1.5)
     swap_to_nmsparse(mdl, 8, "cuda", seed=1, init="device", keep_dense=False)
-    assert dm.accumulate_supported(mdl.layers)
+    if dtype != torch.float16:  # the swap packs fp16 (the reference's layout); the fused launches take bf16 weights
+        assert not dm.fusable(mdl.layers[0], dtype)
+        mdl.setup_cache(16, "cuda", dtype=dtype)
+        # fp16 packed weights under bf16 activations: the op's own dtype check
+        # refuses them, as the reference wrapper does (triton_spmv.py:245-283).
+        with torch.no_grad(), pytest.raises(TypeError, match="same dtype"):
+            mdl.forward_step(torch.tensor([[3]], device="cuda"), torch.tensor([0], device="cuda"))
+        for mod in mdl.modules():
+            if hasattr(mod, "mat_data"):
+                mod.mat_data = mod.mat_data.to(dtype)
+    assert dm.accumulate_supported(mdl.layers) and all(dm.fusable(b, dtype) for b in mdl.layers)
     toks = [3, 5, 7, 9, 11, 13]
 
     def run(mode):
         mdl.carry_mode = mode
-        mdl.setup_cache(16, "cuda", dtype=torch.float16)
+        mdl.setup_cache(16, "cuda", dtype=dtype)
         with torch.no_grad():
             return [mdl.forward_step(torch.tensor([[t]], device="cuda"), torch.tensor([i], device="cuda")).float()
                     for i, t in enumerate(toks)]
 
-    say(f"decoder accumulated carry qk_norm {qk_norm}: eager")
+    say(f"decoder accumulated carry qk_norm {qk_norm} {dtype}: eager")
     split = run("split")
     assert len(mdl._carry[1]) == 3
     acc = run("accumulate")
     assert len(mdl._carry[1]) == 4
     for a, b in zip(acc, split):
-        torch.testing.assert_close(a, b, rtol=5e-3, atol=5e-3)
-    say(f"decoder accumulated carry qk_norm {qk_norm}: graph replays")
+        torch.testing.assert_close(a, b, rtol=tol, atol=tol)
+    say(f"decoder accumulated carry qk_norm {qk_norm} {dtype}: graph replays")
     gd = GraphDecoder(mdl, 12)
     prompt = torch.tensor([3, 5, 7])
     gd.run_prompt(prompt)
@@ -345,5 +357,5 @@ def test_decoder_accumulated_carry_matches_split_carry(gpu, qk_norm):
                 break  # a near-tie of a greedy choice went the other way: this step would see another token
             gd.replay()
             torch.cuda.synchronize()
-            torch.testing.assert_close(gd.logits.float(), eager[i].float(), rtol=5e-3, atol=5e-3)
+            torch.testing.assert_close(gd.logits.float(), eager[i].float(), rtol=tol, atol=tol)
     mdl.carry_mode = "split"

@@ -223,7 +223,14 @@ def test_capture_without_warmup_owns_its_workspace(gpu):
     eager = [run(x, md, mi, 32, 64).clone() for x, md, mi in cases]
     torch.cuda.synchronize()
     default_ws = hip_spmv._workspaces[(gpu.index or 0, torch.cuda.current_stream().cuda_stream)]
-    s = torch.cuda.Stream()
+    # torch hands out streams from a small per-device pool, so an earlier test
+    # may already have run GEMVs on the next one: take one that never has.
+    for _ in range(64):
+        s = torch.cuda.Stream()
+        if (gpu.index or 0, s.cuda_stream) not in hip_spmv._workspaces:
+            break
+    else:
+        pytest.skip("every pooled stream has already run a GEMV in this process")
     s.wait_stream(torch.cuda.current_stream())
     graphs, outs = [], []
     for half in (cases[:2], cases[2:]):
