@@ -18,14 +18,16 @@
 //    rounded up to whole 64-column chunks, zero past w).
 //  * The main kernel: a workgroup (256 lanes = 4 wave64) owns an output tile
 //    of HT columns r and all BT >= batch rows (16, 32 or 64), over one split
-//    of the compressed columns c. The 4 waves split the tile into BT/16 row
-//    blocks x 64/BT column ranges (each activation row block is loaded by
-//    as few waves as possible); a wave keeps its 16 rows x HT*BT/64 columns
-//    as 16 x 16 fp32 accumulator blocks in registers. Chunks of 64 compressed columns (two
-//    MFMA K steps): the weight rows [64 x HT] are loaded 16 B per lane
-//    (non-temporal) and staged through LDS, two buffers; the activation
-//    operands come straight from Xg, 16 B per lane and row block. Two chunks
-//    are in flight in registers while one is multiplied.
+//    of the compressed columns c. The 4 waves split the tile into row
+//    ranges (one 16-row block each up to 32 rows, two blocks each at 64) x
+//    column ranges; a wave keeps its rows x columns as 16 x 16 fp32
+//    accumulator blocks in registers. Chunks of 64 compressed columns (two
+//    MFMA K steps): the weight rows [64 x HT] are staged through LDS. Up to
+//    1024 outputs (register-staged): loaded 16 B per lane (non-temporal),
+//    two LDS buffers, the activation operands straight from Xg, two chunks
+//    in flight in registers while one is multiplied. Past that (DMA): the
+//    weight rows and the chunk's activation fragments go from memory into a
+//    ring of LDS stages (global_load_lds_dwordx4), see the kernel.
 //  * MFMA operands: the activation block is K-contiguous in Xg; the weight
 //    block, stored with the outputs contiguous, is read transposed with
 //    ds_read_b64_tr_b16 (lane l of a 16-lane group receives element l of
@@ -66,12 +68,13 @@ __device__ inline f4 mfma16x16x32<NM_DTYPE_BF16>(s8 a, s8 b, f4 c) {
 // lane l holds row l % 16, K elements 8*(l/16) .. +7; B[32 x 16]: column
 // l % 16, K elements 8*(l/16) .. +7; D[16 x 16]: column l % 16, rows
 // 4*(l/16) .. +3.
-// LDS stages of the DMA variant per tile width: about 64 KB of weight chunks
-// in flight per workgroup (S - 1 chunks of 64 x HT 16-bit weights), at most
-// 80 KB of LDS, so that two workgroups fit in a CU. (Rings of about 128 KB,
-// one workgroup per CU, measured no faster: the per-CU request pipeline, not
-// the bytes in flight, bounds the stream.)
-constexpr int mc_stages(int ht) { return ht == 64 ? 8 : (ht == 128 ? 5 : 3); }
+// LDS stages of the DMA variant per tile width (S - 1 chunks of 64 x HT
+// weights and their activation fragments in flight): 4 / 3 / 3 for 64- /
+// 128- / 256-column tiles, fitted to graph-replay sweeps of 2-8 stages at
+// 16-64 rows over the Llama-3.1-8B and Qwen3 shapes (deeper rings measured
+// up to 8% slower, two stages up to 30%). At most 65 KB of LDS per
+// workgroup.
+constexpr int mc_stages(int ht) { return ht == 64 ? 4 : 3; }
 constexpr int kMcNtAux = 2;  // cache policy of the weight DMA: non-temporal
 
 // Inline asm with register constraints exists only in the device pass (the
@@ -94,6 +97,13 @@ __device__ inline void mc_read_tr_pair(s4& lo, s4& hi, uint32_t addr) {
 #endif
 }
 
+// One 16-B LDS read without a wait: see mc_lds_wait.
+__device__ inline void mc_read_b128(s8& v, uint32_t addr) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+#endif
+}
+
 __device__ inline void mc_lds_wait() {
 #if defined(__HIP_DEVICE_COMPILE__)
   asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
@@ -106,6 +116,11 @@ __device__ inline void mc_after_wait(s4& v) {
   asm volatile("" : "+v"(v));
 #endif
 }
+__device__ inline void mc_after_wait8(s8& v) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  asm volatile("" : "+v"(v));
+#endif
+}
 
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) char lds_char;
@@ -114,9 +129,13 @@ template <int DT, int BT, int HT, bool DMA>
 __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   using E = Elem<DT>;
   typedef typename E::scalar T;  // 16-bit storage
-  constexpr int WM = BT / 16;               // waves along the rows (one 16-row block each)
+  constexpr int RBT = BT / 16;              // 16-row blocks per tile
+  // Waves along the rows: one per 16-row block up to 32 rows, two of two
+  // blocks each at 64 rows (four waves of one block each read the whole
+  // weight tile from LDS four times over, and measured 2-9% slower).
+  constexpr int WM = BT == 64 ? 2 : RBT;
   constexpr int WN = 4 / WM;                // waves along the output columns
-  constexpr int MB = 1;                     // 16-row blocks per wave
+  constexpr int MB = RBT / WM;              // 16-row blocks per wave
   constexpr int NW = HT / WN;               // output columns per wave
   constexpr int NBK = NW / 16;              // 16-column blocks per wave
   constexpr int LPR = HT / 8;               // lanes per weight row (16 B each)
@@ -128,12 +147,14 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
 
   constexpr int S = mc_stages(HT);           // DMA variant: LDS stages
   constexpr int RB = HT * 2;                 // DMA variant: bytes per LDS weight row (no padding)
-  constexpr int SB = kMcCK * RB;             // DMA variant: bytes per stage
-  constexpr int kLdsBytes = DMA ? S * SB : 2 * kMcCK * WSTR * (int)sizeof(T);
-  // The whole static LDS is the weight staging (the split-K tail reuses its
-  // first word once every wave is past the main loop): at 80 KB per
-  // workgroup two of them fit in a CU's 160 KB, which one more word would
-  // prevent.
+  constexpr int SB = kMcCK * RB;             // DMA variant: weight bytes per stage
+  constexpr int NFA = RBT * KS;              // DMA variant: activation fragments (1 KB) per chunk
+  constexpr int NA = (NFA + 3) / 4;          // DMA variant: activation fragments each wave loads per chunk
+  constexpr int SA = NFA * 1024;             // DMA variant: activation bytes per stage
+  // (waves without a fragment of their own load one into a spare 1 KB that is never read)
+  constexpr int kLdsBytes = DMA ? S * (SB + SA) + (4 * NA > NFA ? 1024 : 0) : 2 * kMcCK * WSTR * (int)sizeof(T);
+  // The whole static LDS is the staging (the split-K tail reuses its first
+  // word once every wave is past the main loop).
   __shared__ __attribute__((aligned(16))) char lds[kLdsBytes];
   T(*ws)[kMcCK * WSTR] = reinterpret_cast<T(*)[kMcCK * WSTR]>(lds);
   int& is_last = *reinterpret_cast<int*>(lds);
@@ -141,7 +162,7 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   const int h = a.h;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
-  const int rb = 16 * (wave % WM);  // the wave's first batch row
+  const int rb = 16 * MB * (wave % WM);  // the wave's first batch row
   const int cb = NW * (wave / WM);  // the wave's first column within the tile
   const int lg = (tid & 63) >> 4;
   const int li = tid & 15;
@@ -196,19 +217,24 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
 #if defined(__HIP_DEVICE_COMPILE__)  // device code only: the host pass needs just the kernel's stub
     // Weight chunks go from HBM straight into a ring of S LDS stages
     // (global_load_lds_dwordx4: no registers held while in flight), S - 1
-    // chunks ahead of the one multiplied; the activation operands of the same
-    // chunks are loaded into a register ring in the same order, so that one
-    // in-order vmcnt wait covers both. Lane tid fills 16 B at byte
-    // i * kBlock * 16 + tid * 16 of a stage: row wrow + i * RPI, physical slot
-    // tid % LPR, which holds logical 16-B column slot (tid % LPR) ^ sw(row),
-    // sw(row) = 2 * (row & 3); the four rows one 16-lane transposed read
-    // addresses then fall in four distinct 32-B bank groups without padding.
-    constexpr int OPS = NI + MB * KS;  // vector memory instructions per lane per chunk
+    // chunks ahead of the one multiplied, and so do the activation fragments
+    // of the same chunks (once per workgroup, shared by its waves), so that
+    // one in-order vmcnt wait covers both and no load into registers is in
+    // flight across the ring: the compiler's own wait for such a load, at
+    // the ring's loop header, emptied the ring once every S chunks. Lane tid
+    // fills 16 B at byte i * kBlock * 16 + tid * 16 of a stage: row
+    // wrow + i * RPI, physical slot tid % LPR, which holds logical 16-B
+    // column slot (tid % LPR) ^ sw(row), sw(row) = 2 * (row & 3); the four
+    // rows one 16-lane transposed read addresses then fall in four distinct
+    // 32-B bank groups without padding. The activation fragment f = ks * RBT + j
+    // (K step ks, row block j) of a stage sits at S * SB + stage * SA + f * 1024,
+    // in the gather's operand order (lane l's 16 B at l * 16).
+    constexpr int OPS = NI + NA;  // vector memory instructions per lane per chunk
     static_assert((S - 1) * OPS < 64, "vmcnt is a 6-bit counter");
     static_assert(RPI % 4 == 0, "the rows a lane fills share their swizzle");
-    static_assert(S * SB <= 160 * 1024, "LDS");
+    static_assert(kLdsBytes <= 160 * 1024, "LDS");
     const int gcol_d = min(tile * HT + 8 * ((tid % LPR) ^ (2 * (wrow & 3))), h - 8);
-    u32x4 aR[S][MB][KS];
+    const int wv = __builtin_amdgcn_readfirstlane(wave);
     // Every step issues the same instructions (a static vmcnt count, and no
     // branch for the compiler's own waits to merge): rows past the split
     // re-read its last row (zeroed in LDS once landed, below), chunks past its
@@ -221,7 +247,16 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
         __builtin_amdgcn_global_load_lds(md + (size_t)(c0 + r) * (size_t)h + gcol_d,
                                          (lds_void*)(lds + s * SB + i * kBlock * 16 + wave * 1024), 16, 0, kMcNtAux);
       }
-      load_a(aR[s], min(k, nch - 1));
+      const int q = c0 / kMcCK + min(k, nch - 1);
+#pragma unroll
+      for (int i = 0; i < NA; ++i) {
+        const int f = wv + 4 * i;
+        const bool own = f < NFA;
+        const int ks = own ? f / RBT : 0, j = own ? f % RBT : 0;
+        const size_t frag = ((size_t)q * KS + ks) * (size_t)rbk_n + (size_t)min(j, rbk_n - 1);
+        char* dst = own ? lds + S * SB + s * SA + f * 1024 : lds + S * (SB + SA);
+        __builtin_amdgcn_global_load_lds(xg + frag * 512 + (size_t)lane * 8, (lds_void*)dst, 16, 0, 0);
+      }
     };
     // The lane's transposed-read address (LDS bytes) of 16-column block nb,
     // stage 0, K step 0: row rr = 8 * lg + li / 4 (and rr + 4), logical
@@ -238,10 +273,15 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
     // apart and would wait for every DMA in flight before each LDS read.
     // Their results are used only after the lgkmcnt wait (the empty asm
     // statements order each result after it).
-    auto compute_d = [&](const u32x4 (&af)[MB][KS], int s) {
+    // The lane's activation-operand address (LDS bytes) of its row block, stage 0, K step 0.
+    const uint32_t ra = lds0 + (uint32_t)(S * SB + (rb >> 4) * 1024 + lane * 16);
+    auto compute_d = [&](int s) {
 #pragma unroll
       for (int ks = 0; ks < KS; ++ks) {
         s4 lo[NBK], hi[NBK];
+        s8 af[MB];
+#pragma unroll
+        for (int mb = 0; mb < MB; ++mb) mc_read_b128(af[mb], ra + (uint32_t)(s * SA + (ks * RBT + mb) * 1024));
 #pragma unroll
         for (int nb = 0; nb < NBK; ++nb) {
           const uint32_t ad = rd[nb] + (uint32_t)(s * SB + ks * 32 * RB);
@@ -249,13 +289,14 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
         }
         mc_lds_wait();
 #pragma unroll
+        for (int mb = 0; mb < MB; ++mb) mc_after_wait8(af[mb]);
+#pragma unroll
         for (int nb = 0; nb < NBK; ++nb) {
           mc_after_wait(lo[nb]);
           mc_after_wait(hi[nb]);
           const s8 bf = {lo[nb][0], lo[nb][1], lo[nb][2], lo[nb][3], hi[nb][0], hi[nb][1], hi[nb][2], hi[nb][3]};
 #pragma unroll
-          for (int mb = 0; mb < MB; ++mb)
-            acc[mb][nb] = mfma16x16x32<DT>(__builtin_bit_cast(s8, af[mb][ks]), bf, acc[mb][nb]);
+          for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16x16x32<DT>(af[mb], bf, acc[mb][nb]);
         }
       }
     };
@@ -281,7 +322,7 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
           __builtin_amdgcn_s_barrier();
         }
         issue(k0 + s + S - 1, (s + S - 1) % S);
-        compute_d(aR[s], s);
+        compute_d(s);
       }
     }
   mc_dma_done:
@@ -530,8 +571,7 @@ struct McPlan {
 // still runs in one round (at most one per CU; a second round of a few
 // workgroups costs more than it brings), ties broken by
 //  * splits of at most 2560 compressed rows (deep K runs slower per split);
-//  * up to 16 rows: 128-column tiles, then 256, then 64 (the 64 x 64 tile
-//    reads as many activation bytes per chunk as weight bytes);
+//  * up to 16 rows: 64-column tiles, then 128, then 256;
 //  * past 16 rows: fewer splits (their partials, [splits, batch, h] fp32,
 //    grow with the rows), then 128-, 64-, 256-column tiles;
 // and past 32 rows a plan whose partials would reach a quarter of the weight
@@ -567,7 +607,7 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
     // search the DMA configurations (or the given one) x split counts (or the given one)
     const int c_lo = cfg < 0 ? 3 : cfg, c_hi = cfg < 0 ? 5 : cfg;
     const int s_lo = splits > 0 ? splits : 1, s_hi = splits > 0 ? splits : 8;
-    const int pref_small[3] = {2, 0, 1};  // ranks of HT = 64, 128, 256 up to 16 rows (lower is better)
+    const int pref_small[3] = {0, 1, 2};  // ranks of HT = 64, 128, 256 up to 16 rows (lower is better)
     const int pref_large[3] = {1, 0, 2};  // past 16 rows
     int best_c = -1, best_s = 0, best_b = 0, best_r = 0, free_c = -1, free_b = 0;
     auto better = [&](int c, int sp, int b, int r) {

@@ -228,12 +228,13 @@ def library_route(rows: int, K: int, h: int) -> bool:
     """Whether nmsparse_spmm_forward_hip's automatic choice, for a 16-bit
     product of `rows` (> NM_MAX_BATCH) rows, is the gathered activations times
     mat_data on hipBLASLt rather than the matrix-core SpMM: past
-    NM_MC_MAX_BATCH rows (one GEMM instead of several launches), and from 32
-    rows for the wide shapes (h >= 3 K: the gate/up projections), where the
-    library's GEMM measured 1-8% faster on MI355X (Llama-3.1-8B 4096 -> 14336
-    at 64 rows 22.0 against 23.7 us, Qwen3-14B / Qwen3-32B gate/up alike);
-    the matrix-core kernel is faster at every other shape, by up to 2.2x."""
-    return rows > _lib.NM_MC_MAX_BATCH or (rows >= 32 and h >= 3 * K)
+    NM_MC_MAX_BATCH rows, where one GEMM replaces several launches of the
+    kernel. From 9 to 64 rows the matrix-core kernel measured faster at every
+    Llama-3.1-8B and Qwen3 shape on MI355X (by 1.1-2.4x; 8-10% at the
+    gate/up projections, the closest). K and h are kept for callers that
+    route by shape."""
+    del K, h
+    return rows > _lib.NM_MC_MAX_BATCH
 
 
 def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1,
@@ -253,8 +254,7 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     own order, see _lib.spmm_mc_plan). matrix_cores=None takes the matrix
     cores for NM_MAX_BATCH < rows <= NM_MC_MAX_BATCH of a 16-bit type when
     config_id and splits are left to the library, and the library route
-    instead (library_route) past NM_MC_MAX_BATCH rows and where it measured
-    faster: the gathered activations (nm_gather_columns, [rows, w]) times
+    instead (library_route) past NM_MC_MAX_BATCH rows: the gathered activations (nm_gather_columns, [rows, w]) times
     mat_data as one hipBLASLt GEMM (torch.matmul: a plain GEMM over half the
     input width); else the small-batch kernel. True / False forces one of the
     two HIP kernels (True needs fp16 or bf16). config_id and splits are those

@@ -95,14 +95,14 @@ def test_more_than_64_rows_gather_and_library_gemm(gpu, dtype):
         assert bool((xg[:, w:] == 0).all())
 
 
-def test_wide_shapes_from_32_rows_take_the_library_route(gpu):
-    """hip_spmv.library_route: from 32 rows a wide product (h >= 3 K, the
-    gate/up shapes) gathers and multiplies on hipBLASLt, the same bits as the
-    explicit gather + GEMM; 31 rows, and narrower shapes at 32, keep the
-    matrix-core kernel (the same bits as forcing it). Both within the oracle
-    bar."""
-    for K, h, rows, routed in ((4096, 14336, 32, True), (4096, 14336, 31, False), (4096, 14336, 64, True),
-                               (5120, 17408, 40, True), (4096, 4096, 32, False), (14336, 4096, 64, False)):
+def test_automatic_route_keeps_the_matrix_cores_up_to_64_rows(gpu):
+    """hip_spmv.library_route: up to 64 rows every shape, the wide gate/up
+    products included, runs on the matrix-core kernel (the same bits as
+    forcing it); past 64 rows the activations are gathered and multiplied on
+    hipBLASLt (the same bits as the explicit gather + GEMM). Both within the
+    oracle bar."""
+    for K, h, rows, routed in ((4096, 14336, 32, False), (4096, 14336, 64, False), (5120, 17408, 40, False),
+                               (4096, 4096, 32, False), (14336, 4096, 64, False), (4096, 14336, 65, True)):
         assert hip_spmv.library_route(rows, K, h) == routed, (K, h, rows)
         _, md, mi = make_case(K, h, 32, 64, seed=K + h + rows)
         w = md.shape[0]
