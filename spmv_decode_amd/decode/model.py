@@ -287,6 +287,21 @@ class Attention(nn.Module):
         return project(self.o_proj, y.view(1, 1, qd))
 
 
+@torch.library.custom_op("nmsparse_decode::cache_write", mutates_args=("cache",))
+def cache_write(cache: torch.Tensor, pos: torch.Tensor, values: torch.Tensor) -> None:
+    """cache[:, :rows, pos] = values ([heads, rows]) in place. An op of its
+    own so that torch.compile writes the cache in place: traced as indexing
+    into a view of a tensor that other graph inputs alias (the key caches
+    are views of one tensor), the compiler copied the view out and back
+    around the write, every layer, every step."""
+    cache[:, :values.shape[1]].index_copy_(2, pos, values.unsqueeze(-1))
+
+
+@cache_write.register_fake
+def _(cache, pos, values):
+    return None
+
+
 def attention_core(at, qkv, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
     """The attention of one decode token from its projections qkv [1, q + k + v]
     (at: the attention module, for its config and Qwen3's q/k norms): head
@@ -301,7 +316,10 @@ def attention_core(at, qkv, freqs, k_cache_t, v_cache_t, pos, q_pad, zero):
     q, k = qk[:c.n_heads], qk[c.n_heads:]
     v = qkv[0, qd + kvd:].view(c.n_kv_heads, c.head_dim, 1)
     q_pad[:, :c.head_dim].copy_(q)
-    k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
+    if torch.compiler.is_compiling():
+        cache_write(k_cache_t, pos, k)
+    else:
+        k_cache_t[:, :c.head_dim].index_copy_(2, pos, k.unsqueeze(-1))
     v_cache_t.index_copy_(2, pos, v)
     return attend(q_pad, k_cache_t, v_cache_t, c, zero)
 

@@ -447,6 +447,45 @@ def test_compiled_step_is_one_graph_and_matches_eager(gpu):
             assert got["token"] == ref["token"], sparse
 
 
+def test_compiled_module_step_writes_the_caches_like_eager():
+    """torch.compile of the module-by-module step (fp32 on the CPU): the key
+    goes into the cache through the mutating op nmsparse_decode::cache_write,
+    which the compiler runs in place (indexing into a view of the one
+    key-cache tensor made it copy the view out and back around the write).
+    Four steps compiled give the eager steps' logits, and the key caches
+    (mask rows included) and value caches end up the same."""
+    cfg = tiny_config(n_layers=2)
+    model = Decoder(cfg).float()
+    init_weights_(model, seed=0)
+    tokens = [3, 7, 11, 5]
+
+    def run(step):
+        model.setup_cache(64, "cpu", dtype=torch.float32)
+        with torch.no_grad():
+            logits = [step(torch.tensor([[t]]), torch.tensor([i])) for i, t in enumerate(tokens)]
+        return logits, model.k_store.clone(), [v.clone() for v in model.v_cache_t]
+
+    eager, k_eager, v_eager = run(model.forward_step)
+    torch._dynamo.reset()
+    try:
+        from torch._inductor.utils import run_and_get_code
+
+        step = torch.compile(model.forward_step, dynamic=False, fullgraph=True)
+        model.setup_cache(64, "cpu", dtype=torch.float32)
+        with torch.no_grad():
+            _, code = run_and_get_code(step, torch.tensor([[1]]), torch.tensor([0]))
+        assert sum(c.count("nmsparse_decode.cache_write") for c in code) >= cfg.n_layers
+        compiled, k_comp, v_comp = run(step)
+    finally:
+        torch._dynamo.reset()
+    for a, b in zip(eager, compiled):
+        torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-5)
+    assert torch.equal(torch.isinf(k_comp), torch.isinf(k_eager))
+    torch.testing.assert_close(k_comp.nan_to_num(0.0, 0.0, 0.0), k_eager.nan_to_num(0.0, 0.0, 0.0), rtol=1e-5, atol=1e-5)
+    for a, b in zip(v_eager, v_comp):
+        torch.testing.assert_close(b, a, rtol=1e-5, atol=1e-5)
+
+
 @pytest.mark.gpu
 def test_restored_compressed_checkpoint_decodes_identically(gpu):
     """A swapped model saved with torch.save and restored into a fresh
