@@ -119,9 +119,15 @@ class RMSNorm(nn.Module):
 
 def rotate(x: torch.Tensor, freqs: torch.Tensor) -> torch.Tensor:
     """Rotary embedding on interleaved (even, odd) pairs, in fp32.
-    x: [..., head_dim]; freqs: complex64 [head_dim/2] (cos + i sin)."""
-    xc = torch.view_as_complex(x.float().reshape(*x.shape[:-1], -1, 2))
-    return torch.view_as_real(xc * freqs).flatten(-2).to(x.dtype)
+    x: [..., head_dim]; freqs: complex64 [head_dim/2] (cos + i sin), or the
+    same as fp32 (cos, sin) pairs [head_dim/2, 2], which torch.compile fuses
+    with its neighbours (it runs complex products as library kernels of their
+    own)."""
+    xp = x.float().reshape(*x.shape[:-1], -1, 2)
+    if freqs.is_complex():
+        return torch.view_as_real(torch.view_as_complex(xp) * freqs).flatten(-2).to(x.dtype)
+    x0, x1, c, s = xp[..., 0], xp[..., 1], freqs[..., 0], freqs[..., 1]
+    return torch.stack((x0 * c - x1 * s, x0 * s + x1 * c), dim=-1).flatten(-2).to(x.dtype)
 
 
 # Rows per head after head_dim in the key cache (and columns in the query
@@ -892,7 +898,7 @@ class Decoder(nn.Module):
                 fused_block_step(blk, x2d, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero,
                                  self.rope_real)
             return project(self.lm_head, self.norm(x)).view(1, -1)
-        freqs = self.rope.index_select(0, pos)
+        freqs = (self.rope_real if torch.compiler.is_compiling() else self.rope).index_select(0, pos)
         for i, layer in enumerate(self.layers):
             x = layer(x, freqs, self.k_cache_t[i], self.v_cache_t[i], pos, self.q_pad, self.zero)
         return project(self.lm_head, self.norm(x)).view(1, -1)
