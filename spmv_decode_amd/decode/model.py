@@ -146,8 +146,13 @@ def attend(q_pad: torch.Tensor, k_cache_t: torch.Tensor, v_cache_t: torch.Tensor
     a 0-dim tensor (the product's ignored addend). Returns [kv_heads, g,
     head_dim] with g = n_heads / kv_heads, contiguous."""
     kvh = cfg.n_kv_heads
-    scores = torch.baddbmm(zero, q_pad.view(kvh, cfg.n_heads // kvh, q_pad.shape[1]), k_cache_t, beta=0.0,
-                           alpha=1.0 / math.sqrt(cfg.head_dim))
+    q3 = q_pad.view(kvh, cfg.n_heads // kvh, q_pad.shape[1])
+    if torch.compiler.is_compiling():
+        # Traced, baddbmm's addend is written out by a kernel of its own
+        # before the product; the scale instead joins the softmax kernel.
+        scores = torch.bmm(q3, k_cache_t) * (1.0 / math.sqrt(cfg.head_dim))
+    else:
+        scores = torch.baddbmm(zero, q3, k_cache_t, beta=0.0, alpha=1.0 / math.sqrt(cfg.head_dim))
     probs = torch.softmax(scores, dim=-1)  # fp16 in/out, fp32 inside
     return torch.bmm(probs, v_cache_t.transpose(1, 2))
 
