@@ -148,11 +148,16 @@ def attend(q_pad: torch.Tensor, k_cache_t: torch.Tensor, v_cache_t: torch.Tensor
     kvh = cfg.n_kv_heads
     q3 = q_pad.view(kvh, cfg.n_heads // kvh, q_pad.shape[1])
     if torch.compiler.is_compiling():
-        # Traced, baddbmm's addend is written out by a kernel of its own
-        # before the product; the scale instead joins the softmax kernel.
+        # Traced: baddbmm's addend would be written out by a kernel of its own
+        # before the product, so the scale joins the softmax kernel instead;
+        # and probabilities x values as a reduction over the positions (fp32),
+        # which the compiler generates in place of the library's batched
+        # product of 4-row matrices (Llama-3.1-8B, 512 positions: 0.26 ms per
+        # token less).
         scores = torch.bmm(q3, k_cache_t) * (1.0 / math.sqrt(cfg.head_dim))
-    else:
-        scores = torch.baddbmm(zero, q3, k_cache_t, beta=0.0, alpha=1.0 / math.sqrt(cfg.head_dim))
+        probs = torch.softmax(scores, dim=-1)
+        return (probs.float().unsqueeze(2) * v_cache_t.float().unsqueeze(1)).sum(-1).to(q_pad.dtype)
+    scores = torch.baddbmm(zero, q3, k_cache_t, beta=0.0, alpha=1.0 / math.sqrt(cfg.head_dim))
     probs = torch.softmax(scores, dim=-1)  # fp16 in/out, fp32 inside
     return torch.bmm(probs, v_cache_t.transpose(1, 2))
 
