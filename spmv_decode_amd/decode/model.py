@@ -436,10 +436,10 @@ class GptFastBlock(nn.Module):
 def fusable(block: Block, dtype=None) -> bool:
     """True when the block's projections can run as the fused sparse layer:
     q/k/v and gate/up each share one launch, o and down are sparse too, and
-    (with `dtype`, the activations' type) every packed weight has that type:
-    the fused launches take their inputs as they are, where a lone
-    `nmsparse::gemv` casts them to the packed weights' fp16 (a bf16 model whose
-    packed weights are fp16 runs its projections one op at a time)."""
+    (with `dtype`, the activations' type) every packed weight has that type.
+    Activations of another type than the packed weights are not fused: the
+    projections then run one op at a time, whose own dtype check refuses them
+    as the reference wrapper does (triton_spmv.py:245-283)."""
     from ..nmsparse_linear import NmSparseLinear
 
     if not isinstance(block, Block):
