@@ -62,19 +62,20 @@ __global__ __launch_bounds__(256) void stripe_read_kernel(const u32x4* __restric
 }  // namespace
 
 // Reads a row-major [R, C16] matrix of 16-byte words in column stripes of
-// `sw` words (16, 32, 64 or 128: 256 B to 2 KB per row, as the GEMV's 128- to
-// 1024-row tiles read fp16 weights) with (C16 / sw) * splits workgroups, 8
-// rows per lane in flight. R must be a multiple of splits; `sink` must hold
+// `sw` words (8, 16, 32, 64 or 128: 128 B to 2 KB per row; the GEMV's 128- to
+// 1024-row tiles read 256 B to 2 KB of fp16 weights) with (C16 / sw) * splits
+// workgroups, 8 rows per lane in flight. R must be a multiple of splits; `sink` must hold
 // one uint32 per workgroup. Returns a hipError_t (0 on success), or -1.
 extern "C" int nm_probe_stripe_read(const void* data, int R, int C16, int sw, int splits, void* sink, void* stream) {
   if (!data || !sink || R <= 0 || C16 <= 0 || splits <= 0 || R % splits || ((uintptr_t)data & 15)) return -1;
-  if ((sw != 16 && sw != 32 && sw != 64 && sw != 128) || C16 % sw) return -1;
+  if ((sw != 8 && sw != 16 && sw != 32 && sw != 64 && sw != 128) || C16 % sw) return -1;
   const int tiles = C16 / sw;
   const dim3 grid((unsigned)(tiles * splits));
   hipStream_t s = static_cast<hipStream_t>(stream);
   const u32x4* p = static_cast<const u32x4*>(data);
   unsigned* k = static_cast<unsigned*>(sink);
   switch (sw) {
+    case 8: hipLaunchKernelGGL((stripe_read_kernel<8, 8>), grid, dim3(256), 0, s, p, R, C16, tiles, splits, k); break;
     case 16: hipLaunchKernelGGL((stripe_read_kernel<16, 8>), grid, dim3(256), 0, s, p, R, C16, tiles, splits, k); break;
     case 32: hipLaunchKernelGGL((stripe_read_kernel<32, 8>), grid, dim3(256), 0, s, p, R, C16, tiles, splits, k); break;
     case 64: hipLaunchKernelGGL((stripe_read_kernel<64, 8>), grid, dim3(256), 0, s, p, R, C16, tiles, splits, k); break;

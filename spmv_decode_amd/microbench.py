@@ -527,10 +527,11 @@ STRIPE_SHAPES = {  # name: (rows R = w, outputs h) of the fp16 weights one launc
 
 def stripe_ceiling(shapes=STRIPE_SHAPES, pool_bytes=2 << 30, reps=10, log=print):
     """Best time of one launch that only reads the weights of a GEMV launch
-    in the GEMV's pattern (column stripes of 256 B - 2 KB per row, split over
+    in the GEMV's pattern (column stripes of 128 B - 2 KB per row, split over
     rows; roofline_probe.hip: nm_probe_stripe_read), over stripe widths and
     split counts: the ceiling for this access pattern, graph replay, weights
-    rotated through `pool_bytes`."""
+    rotated through `pool_bytes`; also the best with a single split (no
+    split-K reduction would be needed)."""
     import ctypes
 
     from .build import PROBE_LIB_PATH
@@ -546,9 +547,9 @@ def stripe_ceiling(shapes=STRIPE_SHAPES, pool_bytes=2 << 30, reps=10, log=print)
         nb = R * h * 2
         C16 = h // 8
         copies = min(256, max(1, pool_bytes // nb))
-        best = None
-        for sw in (16, 32, 64, 128):
-            for splits in (2, 4, 8, 16, 32):
+        best = best1 = None
+        for sw in (8, 16, 32, 64, 128):
+            for splits in (1, 2, 4, 8, 16, 32):
                 if C16 % sw or R % splits or (C16 // sw) * splits > sink.numel():
                     continue
 
@@ -560,8 +561,11 @@ def stripe_ceiling(shapes=STRIPE_SHAPES, pool_bytes=2 << 30, reps=10, log=print)
                 us = graph_us_per_launch([lambda i=i: launch(i) for i in range(copies)], reps)
                 if best is None or us < best[0]:
                     best = (us, sw * 16, splits, (C16 // sw) * splits)
+                if splits == 1 and (best1 is None or us < best1[0]):
+                    best1 = (us, sw * 16)
         out[name] = {"bytes": nb, "us": round(best[0], 3), "GBps": round(nb / best[0] / 1e3, 1),
-                     "stripe_bytes": best[1], "splits": best[2], "workgroups": best[3]}
+                     "stripe_bytes": best[1], "splits": best[2], "workgroups": best[3],
+                     "one_split_us": round(best1[0], 3), "one_split_stripe_bytes": best1[1]}
         log(f"stripe ceiling {name:13s} {nb / 1e6:7.1f} MB: {best[0]:7.2f} us {nb / best[0] / 1e3:6.0f} GB/s "
             f"(stripe {best[1]} B, {best[2]} splits, {best[3]} workgroups)")
     return out
@@ -570,16 +574,19 @@ def stripe_ceiling(shapes=STRIPE_SHAPES, pool_bytes=2 << 30, reps=10, log=print)
 def write_stripe_md(res, path, cmd):
     lines = ["# Read ceiling in the GEMV's access pattern (MI355X, fp16 weights of the Llama-3.1-8B shapes, 32:64)", "",
              "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
-             "Each row: the fastest launch, over stripe widths (256 B - 2 KB of a row per workgroup, i.e. 128- to",
-             "1024-row output tiles) and split counts (2-32), of a kernel that only reads the launch's weights in",
-             "column stripes as the GEMV does (`roofline_probe.hip: nm_probe_stripe_read`, 8 rows per lane in",
-             "flight). Graph replay over >= 1 GiB of rotated copies, inter-kernel gap included, as for the GEMV",
-             "classes in bench.py. `gate_up_pair` reads gate and up side by side (the pair launch's weight bytes).", "",
-             "| Launch | Weight bytes | us | GB/s | % of 8 TB/s | stripe | splits | workgroups |",
-             "|---|---|---|---|---|---|---|---|"]
+             "Each row: the fastest launch, over stripe widths (128 B - 2 KB of a row per workgroup; the GEMV's",
+             "128- to 1024-row output tiles read 256 B - 2 KB) and split counts (1-32), of a kernel that only reads",
+             "the launch's weights in column stripes as the GEMV does (`roofline_probe.hip: nm_probe_stripe_read`,",
+             "8 rows per lane in flight), and the fastest with a single split (a GEMV launch of that shape would",
+             "need no split-K reduction). Graph replay over >= 1 GiB of rotated copies, inter-kernel gap included,",
+             "as for the GEMV classes in bench.py. `gate_up_pair` reads gate and up side by side (the pair",
+             "launch's weight bytes).", "",
+             "| Launch | Weight bytes | us | GB/s | % of 8 TB/s | stripe | splits | workgroups | one split: us | stripe |",
+             "|---|---|---|---|---|---|---|---|---|---|"]
     for name, r in res.items():
         lines.append(f"| {name} | {r['bytes']:,} | {r['us']:.2f} | {r['GBps']:.0f} | {r['GBps'] / 80:.1f}% | "
-                     f"{r['stripe_bytes']} B | {r['splits']} | {r['workgroups']} |")
+                     f"{r['stripe_bytes']} B | {r['splits']} | {r['workgroups']} | {r['one_split_us']:.2f} | "
+                     f"{r['one_split_stripe_bytes']} B |")
     Path(path).write_text("\n".join(lines) + "\n")
 
 
