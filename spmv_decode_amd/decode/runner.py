@@ -53,6 +53,22 @@ def cache_length(max_seq: int) -> int:
     return -(-max_seq // CACHE_ALIGN) * CACHE_ALIGN
 
 
+def softmax_row(logits: torch.Tensor) -> torch.Tensor:
+    """torch.softmax(logits.float(), dim=-1) of [1, V] logits in two parallel
+    stages over the C-wide chunks greedy_token uses (the maximum and the sum
+    of exponentials per chunk, then over the chunks): a single-row softmax over
+    a 128K vocabulary is one workgroup's pass (~40 us on MI355X). Exact up to
+    the order of the fp32 sum."""
+    x = logits.float()
+    V = x.shape[-1]
+    C = _chunk_width(V)
+    if C == 0 or V // C < 2:
+        return torch.softmax(x, dim=-1)
+    xv = x.reshape(V // C, C)
+    e = torch.exp(xv - xv.amax(dim=1).amax())
+    return (e / e.sum(dim=1).sum()).reshape(x.shape)
+
+
 def sample_token(logits: torch.Tensor, out: torch.Tensor, generator: torch.Generator | None = None) -> torch.Tensor:
     """The reference's sampling step (generate.py:46-63;
     benchmarks/bench_qwen_31_14b_fp16_fixed_ptx.py:356-357): the softmax of the
@@ -68,7 +84,7 @@ def sample_token(logits: torch.Tensor, out: torch.Tensor, generator: torch.Gener
     reductions whose multi-block form clears its semaphores with memset nodes
     when captured; replayed, those gave wrong results on MI355X and the check's
     device-side assert then aborted the run."""
-    probs = torch.softmax(logits.float(), dim=-1).to(logits.dtype)
+    probs = softmax_row(logits).to(logits.dtype)
     race = torch.empty(probs.shape, dtype=torch.float32, device=probs.device).exponential_(generator=generator)
     return greedy_token(probs.float() / race, out=out)
 

@@ -726,6 +726,22 @@ def test_sample_token_draws_from_the_softmax_distribution():
     assert ((freq - p).abs() <= 5 * se).all(), (freq, p)
 
 
+@pytest.mark.parametrize("V", [151936, 128256, 1009])
+def test_softmax_row_matches_torch_softmax(V):
+    """The sampling step's two-stage softmax equals torch.softmax in fp32 up to
+    the order of its sums (a prime vocabulary takes torch.softmax itself), and
+    sums to one; an omitted max shift or a sum over one chunk only would not."""
+    from spmv_decode_amd.decode.runner import softmax_row
+
+    logits = (torch.randn(1, V, generator=torch.Generator().manual_seed(V)) * 4).half()
+    logits[0, V // 3] = 30.0
+    got = softmax_row(logits)
+    want = torch.softmax(logits.float(), dim=-1)
+    assert got.dtype == torch.float32 and got.shape == (1, V)
+    torch.testing.assert_close(got, want, rtol=1e-5, atol=1e-9)
+    assert abs(float(got.sum()) - 1.0) < 1e-5
+
+
 @pytest.mark.gpu
 def test_sample_token_in_a_captured_graph_over_many_replays(gpu):
     """sample_token captured in a hipGraph at Qwen3's vocabulary (151936) and replayed
