@@ -397,6 +397,53 @@ def time_gather_gemm(n_out, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, 
     return us
 
 
+# name: (outputs, inputs, N, M) of the products a batched decode or a prompt runs through the SpMM
+SPMM_COMPARE_SHAPES = {
+    "Llama-3.1-8B q/o": (4096, 4096, 32, 64), "Llama-3.1-8B k/v": (1024, 4096, 32, 64),
+    "Llama-3.1-8B gate/up": (14336, 4096, 32, 64), "Llama-3.1-8B down": (4096, 14336, 32, 64),
+    "Qwen3-14B q/o": (5120, 5120, 32, 64), "Qwen3-14B k/v": (1024, 5120, 32, 64),
+    "Qwen3-14B gate/up": (17408, 5120, 32, 64), "Qwen3-14B down": (5120, 17408, 32, 64),
+    "Qwen3-32B q": (8192, 5120, 16, 32), "Qwen3-32B o": (5120, 8192, 16, 32), "Qwen3-32B k/v": (1024, 5120, 16, 32),
+    "Qwen3-32B gate/up": (25600, 5120, 16, 32), "Qwen3-32B down": (5120, 25600, 16, 32),
+}
+
+
+def spmm_compare(shapes=SPMM_COMPARE_SHAPES, rows=(9, 16, 32, 64), reps=20, log=print):
+    """The matrix-core SpMM (its default plan, the activation gather included)
+    beside the library route (the same gather, then one hipBLASLt GEMM) per
+    shape and row count: us per call, weight bytes per second, graph replay
+    over >= 1 GiB of rotated weights."""
+    out = {}
+    for name, (h, K, nnz, m) in shapes.items():
+        wbytes = (K // m * nnz) * h * 2
+        for b in rows:
+            mc = time_spmm(h, K, nnz, m, b, reps=reps, matrix_cores=True)
+            lib = time_gather_gemm(h, K, nnz, m, b, reps=reps)
+            out[f"{name}|{b}"] = {"shape": name, "rows": b, "weight_bytes": wbytes, "matrix_core_us": round(mc, 3),
+                                  "library_us": round(lib, 3), "matrix_core_weight_GBps": round(wbytes / mc / 1e3, 1),
+                                  "speedup": round(lib / mc, 3)}
+            log(f"spmm {name:22s} {b:3d} rows: matrix-core {mc:7.2f} us ({wbytes / mc / 1e3:6.0f} GB/s), "
+                f"gather + hipBLASLt {lib:7.2f} us ({lib / mc:.2f}x)")
+        torch.cuda.empty_cache()
+    return out
+
+
+def write_spmm_compare_md(res, path, cmd):
+    lines = ["# Matrix-core SpMM against gather + hipBLASLt (MI355X, fp16)", "",
+             "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
+             "Per shape and activation-row count: `nm_spmm_mc` with its default plan (`nmsparse_spmm_forward_hip(...,",
+             "matrix_cores=True)`: the activation gather into operand order, then the matrix-core kernel) and the",
+             "library route for the same product (`nm_gather_columns`, then one `torch.matmul` of the gathered",
+             "activations and `mat_data`, hipBLASLt). us per call, median of graph replays over >= 1 GiB of rotated",
+             "weights (`microbench.time_spmm`, `time_gather_gemm`); GB/s counts the packed weight bytes.", "",
+             "| Shape | Rows | Weight bytes | matrix-core us | GB/s | gather + hipBLASLt us | speedup |",
+             "|---|---|---|---|---|---|---|"]
+    for r in res.values():
+        lines.append(f"| {r['shape']} | {r['rows']} | {r['weight_bytes']:,} | {r['matrix_core_us']:.2f} | "
+                     f"{r['matrix_core_weight_GBps']:.0f} | {r['library_us']:.2f} | {r['speedup']:.2f}x |")
+    Path(path).write_text("\n".join(lines) + "\n")
+
+
 def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda", warmup=3,
                stats=False, form="best", return_form=False):
     """Dense GEMV y = x * W^T through the BLAS library, weights rotated over
@@ -838,6 +885,8 @@ def main(argv=None):
     p.add_argument("--stripe-ceiling", action="store_true",
                    help="measure launches that only read each Llama shape's weights in the GEMV's pattern")
     p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
+    p.add_argument("--spmm-compare", action="store_true",
+                   help="the matrix-core SpMM beside gather + hipBLASLt at the Llama / Qwen3 shapes, 9-64 rows")
     p.add_argument("--pair-sweep", action="store_true",
                    help="time the decoder's gate/up pair launch under every pair configuration x split count "
                         "(Llama-3.1-8B shapes, the first --ratios entry); --csv for profiling sweep-stats")
@@ -895,6 +944,13 @@ def main(argv=None):
         return 0
     if a.traffic_probe:
         traffic_probe(_parse_pairs(a.dims, "x"), log=lambda s: print(s, flush=True))
+        return 0
+    if a.spmm_compare:
+        res = spmm_compare(reps=a.reps, log=lambda s: print(s, flush=True))
+        if a.json:
+            Path(a.json).write_text(json.dumps(res, indent=1))
+        if a.md:
+            write_spmm_compare_md(res, a.md, "python -u -m spmv_decode_amd.microbench --spmm-compare --json <json> --md <md>")
         return 0
     rows = run(_parse_pairs(a.dims, "x"), _parse_pairs(a.ratios, ":"), a.dtype, a.sweep, a.rotate_mib, a.reps,
                a.csv, not a.no_dense, log=lambda s: print(s, flush=True), warmup=a.warmup)
