@@ -230,9 +230,9 @@ def library_route(rows: int, K: int, h: int) -> bool:
     mat_data on hipBLASLt rather than the matrix-core SpMM: past
     NM_MC_MAX_BATCH rows, where one GEMM replaces several launches of the
     kernel. From 9 to 64 rows the matrix-core kernel measured faster at every
-    Llama-3.1-8B and Qwen3 shape on MI355X (by 1.1-2.4x; 8-10% at the
-    gate/up projections, the closest). K and h are kept for callers that
-    route by shape."""
+    Llama-3.1-8B and Qwen3 shape on MI355X (by 1.05-2.5x; 5-14% at the
+    gate/up projections from 32 rows, the closest). K and h are kept for
+    callers that route by shape."""
     del K, h
     return rows > _lib.NM_MC_MAX_BATCH
 
