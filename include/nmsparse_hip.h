@@ -343,8 +343,9 @@ int nm_spmm_plan(int batch, int h, int w, int nnz, int m, int config_id, int spl
  * out_row_stride >= h apart; mat_data and out 16-byte aligned, workspace
  * 256-byte aligned with zeroed arrival counters (as nm_gemv_ex).
  * config_id: 0..2 (output tiles of 64, 128, 256 columns, weights staged
- * through registers), 3..5 (the same tiles, weights loaded straight into a
- * ring of LDS stages), or < 0 for the library's choice; splits <= 0 likewise. No reference counterpart (the
+ * through registers), 3..5 (the same tiles, weights and gathered
+ * activations loaded straight into a ring of LDS stages), or < 0 for the
+ * library's choice; splits <= 0 likewise. No reference counterpart (the
  * reference op rejects rows != 1, src/spmv/nmsparse_op.py:83-86, and its
  * module runs them through a dense F.linear, src/spmv/nmsparse_linear.py:62-68).
  */
