@@ -414,14 +414,17 @@ def test_fixed_context_protocol_dense_and_sparse(gpu):
 
 
 @pytest.mark.gpu
-def test_compiled_step_is_one_graph_and_matches_eager(gpu):
+@pytest.mark.parametrize("ctx", [20, 300])
+def test_compiled_step_is_one_graph_and_matches_eager(gpu, ctx):
     """The reference benchmark compiles the decode step before capturing it
     (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:152-155). The fused sparse
     step, whose launches are torch.ops.nmsparse ops, compiles with
     fullgraph=True (no graph break), and so does the dense step; under the
     fixed-context protocol (with the reference's sampling) the compiled step's
     logits match the eager step's within fp16 tolerance and pick the same
-    greedy token wherever the top two logits are apart by more than that."""
+    greedy token wherever the top two logits are apart by more than that; at
+    20 and at 300 positions (a cache of 384: the compiled attention's
+    reduction over the positions)."""
     from spmv_decode_amd.decode.runner import fixed_context_ms
 
     cfg = tiny_config(qk_norm=True)
@@ -432,11 +435,11 @@ def test_compiled_step_is_one_graph_and_matches_eager(gpu):
     for sparse in (False, True):
         if sparse:
             swap_to_nmsparse(model, 16, "cuda", seed=3, init="device", keep_dense=False)
-        ref = fixed_context_ms(model, 20, warmup=2, repeat=2, inner=2)
+        ref = fixed_context_ms(model, ctx, warmup=2, repeat=2, inner=2)
         torch._dynamo.reset()
         model.forward_step = torch.compile(eager_step, dynamic=False, fullgraph=True)
         try:
-            got = fixed_context_ms(model, 20, warmup=2, repeat=2, inner=2)
+            got = fixed_context_ms(model, ctx, warmup=2, repeat=2, inner=2)
         finally:
             model.forward_step = eager_step
             torch._dynamo.reset()
