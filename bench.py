@@ -499,6 +499,20 @@ def main():
         spmm[cls] = rows
         torch.cuda.empty_cache()
     result["spmm_batch"] = spmm
+    # sibling products of one input in one grouped launch (q/k/v, gate/up) against one call per product
+    group = {}
+    for name, (hs, K) in {"q_k_v": ((4096, 1024, 1024), 4096), "gate_up": ((14336, 14336), 4096)}.items():
+        wbytes = sum(((K // m) * nnz) * h * 2 for h in hs)
+        group[name] = {}
+        for batch in (16, 32, 64):
+            g_us, sep_us = MB.time_spmm_group(hs, K, nnz, m, batch, reps=reps)
+            group[name][str(batch)] = {"grouped_us": round(g_us, 3), "separate_us": round(sep_us, 3),
+                                       "grouped_weight_GBps": round(wbytes / (g_us * 1e-6) / 1e9, 1),
+                                       "speedup_grouped_vs_separate": round(sep_us / g_us, 3)}
+            log(f"spmm group {name:6s} batch {batch}: grouped {g_us:7.2f} us ({wbytes / g_us / 1e3:6.0f} GB/s), "
+                f"separate {sep_us:7.2f} us")
+        torch.cuda.empty_cache()
+    result["spmm_group"] = group
 
     # ---- dense fp16 baseline on the same shapes ------------------------------
     if not args.no_dense:

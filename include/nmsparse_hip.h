@@ -358,6 +358,27 @@ int nm_spmm_mc_plan(int batch, int h, int w, int nnz, int m, int config_id, int 
                     int* out_splits, int* out_blocks, int* out_rows_per_block);
 
 /*
+ * Several matrix-core SpMMs of the same activations in one grid: product i
+ * (0 <= i < n <= NM_MC_MAX_GROUP) is out[i] = mat_data[i] / mat_index[i]
+ * applied to every row of x, h[i] outputs, out rows out_row_stride[i] apart;
+ * all products share x, batch, w, nnz and m (sibling Linears: q/k/v, gate/up)
+ * and one tile width and split count. Each product's rows are those
+ * nm_spmm_mc gives with the same config_id and splits. One gather launch for
+ * every product's activations, one product launch. No reference counterpart
+ * (the reference has no multi-row path; its benchmark runs each Linear on its
+ * own, src/spmv/nmsparse_linear.py:62-68).
+ */
+#define NM_MC_MAX_GROUP 4
+size_t nm_spmm_mc_group_workspace_bytes(int batch, int n, const int* h, int w, int nnz, int m, int config_id,
+                                        int splits);
+int nm_spmm_mc_group(int dtype, const void* x, long long x_row_stride, int batch, int n,
+                     const void* const* mat_data, const uint8_t* const* mat_index, void* const* out,
+                     const long long* out_row_stride, const int* h, void* workspace, size_t workspace_bytes,
+                     int w, int nnz, int m, int config_id, int splits, void* stream);
+int nm_spmm_mc_group_plan(int batch, int n, const int* h, int w, int nnz, int m, int config_id, int splits,
+                          int* out_config_id, int* out_splits, int* out_blocks, int* out_rows_per_block);
+
+/*
  * The gathered activations alone: out[r, c] = x[r, (c/nnz)*m + mat_index[c]]
  * for c < w, zero for out_row_stride > c >= w (fp16 / bf16; out 16-byte
  * aligned, out_row_stride a multiple of 8 and >= w rounded up to 8). With

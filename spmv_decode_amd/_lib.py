@@ -29,6 +29,7 @@ NM_ERR = {
 NM_KIND_GROUPED, NM_KIND_GATE_UP = 0, 1
 NM_MAX_BATCH = 8
 NM_MC_MAX_BATCH = 64
+NM_MC_MAX_GROUP = 4
 NM_STATIC_SCRATCH_BYTES = NM_TICKET_BYTES + (16 << 20)
 
 _vp = ctypes.c_void_p
@@ -85,6 +86,10 @@ ABI = {
     "nm_spmm_mc_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "nm_spmm_mc": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_spmm_mc_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
+    "nm_spmm_mc_group_workspace_bytes": (_sz, [_i, _i, _ip, _i, _i, _i, _i, _i]),
+    "nm_spmm_mc_group": (_i, [_i, _vp, _ll, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
+                              ctypes.POINTER(_ll), _ip, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
+    "nm_spmm_mc_group_plan": (_i, [_i, _i, _ip, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
     "nm_gather_columns": (_i, [_i, _vp, _ll, _i, _vp, _i, _i, _i, _vp, _ll, _vp]),
     "nm_config_describe": (_i, [_i, ctypes.c_char_p, _i]),
     "nm_gemv_plan": (_i, [_i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
@@ -92,7 +97,7 @@ ABI = {
     "nm_abi_version": (_i, []),
     "nm_stream_capture_id": (_i, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _lib = None
 _lock = threading.Lock()
@@ -169,6 +174,19 @@ def spmm_mc_plan(batch: int, h: int, w: int, nnz: int, m: int, config_id: int = 
     rc = load().nm_spmm_mc_plan(batch, h, w, nnz, m, config_id, splits, ctypes.byref(cfg), ctypes.byref(sp),
                                 ctypes.byref(blocks), ctypes.byref(rows))
     check(rc, "nm_spmm_mc_plan")
+    return {"config_id": cfg.value, "splits": sp.value, "blocks": blocks.value, "rows_per_split": rows.value,
+            "config": MC_CONFIGS[cfg.value]}
+
+
+def spmm_mc_group_plan(batch: int, hs, w: int, nnz: int, m: int, config_id: int = -1, splits: int = 0) -> dict:
+    """Configuration, split count, grid size and rows per split of a grouped
+    matrix-core SpMM launch (products of output widths hs)."""
+    n = len(hs)
+    harr = (ctypes.c_int * max(n, 1))(*hs)
+    cfg, sp, blocks, rows = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    rc = load().nm_spmm_mc_group_plan(batch, n, harr, w, nnz, m, config_id, splits, ctypes.byref(cfg),
+                                      ctypes.byref(sp), ctypes.byref(blocks), ctypes.byref(rows))
+    check(rc, "nm_spmm_mc_group_plan")
     return {"config_id": cfg.value, "splits": sp.value, "blocks": blocks.value, "rows_per_split": rows.value,
             "config": MC_CONFIGS[cfg.value]}
 

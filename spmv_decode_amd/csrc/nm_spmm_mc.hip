@@ -125,8 +125,11 @@ __device__ inline void mc_after_wait8(s8& v) {
 typedef __attribute__((address_space(3))) void lds_void;
 typedef __attribute__((address_space(3))) char lds_char;
 
+// Workgroup `block` of one product (the tile and split it owns follow from
+// it); the kernels below are this for one product, or for several products
+// of the same activations in one grid.
 template <int DT, int BT, int HT, bool DMA>
-__global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
+__device__ __forceinline__ void mc_tile(const SpmmArgs& a, const int block) {
   using E = Elem<DT>;
   typedef typename E::scalar T;  // 16-bit storage
   constexpr int RBT = BT / 16;              // 16-row blocks per tile
@@ -166,8 +169,8 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   const int cb = NW * (wave / WM);  // the wave's first column within the tile
   const int lg = (tid & 63) >> 4;
   const int li = tid & 15;
-  const int tile = (int)blockIdx.x % a.tiles;
-  const int split = (int)blockIdx.x / a.tiles;
+  const int tile = block % a.tiles;
+  const int split = block / a.tiles;
   const int c0 = split * a.rows_per_split;
   const int cw = min(a.rows_per_split, a.w - c0);
   const int nch = (cw + kMcCK - 1) / kMcCK;  // c0 + nch * kMcCK <= wp (rows_per_split: whole chunks)
@@ -496,6 +499,31 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
   }
 }
 
+template <int DT, int BT, int HT, bool DMA>
+__global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
+  mc_tile<DT, BT, HT, DMA>(a, (int)blockIdx.x);
+}
+
+// Several products of the same activations in one grid (sibling Linears:
+// q/k/v, gate/up): product i owns workgroups first[i] .. first[i + 1] - 1,
+// with its own weights, gathered activations, outputs, partials and
+// arrival counters, the same tile width, batch and split count.
+constexpr int kMcMaxGroup = NM_MC_MAX_GROUP;
+struct McGroupArgs {
+  SpmmArgs p[kMcMaxGroup];
+  int first[kMcMaxGroup];
+  int n;
+};
+
+template <int DT, int BT, int HT, bool DMA>
+__global__ __launch_bounds__(kBlock) void nm_spmm_mc_group_kernel(McGroupArgs g) {
+  const int b = (int)blockIdx.x;
+  int i = 0;
+#pragma unroll
+  for (int j = 1; j < kMcMaxGroup; ++j) i += (j < g.n && b >= g.first[j]) ? 1 : 0;
+  mc_tile<DT, BT, HT, DMA>(g.p[i], b - g.first[i]);
+}
+
 // The gathered activations xg[b, c] = x[b, (c/nnz)*m + mat_index[c]] for
 // c < w, zero for positions outside x, for w <= c < wp and for rows past the
 // batch. Lane i writes 8 consecutive columns of one row as one 16-B store:
@@ -504,10 +532,9 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_kernel(SpmmArgs a) {
 // 16-B slot i of the fragments described at nm_spmm_mc_kernel's load_a; wp
 // a multiple of 64; rbk row blocks of 16 rows).
 template <bool FRAG>
-__global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __restrict__ x, long long x_row_stride,
-                                                            int batch, const uint8_t* __restrict__ mat_index, int w,
-                                                            int wp, int nnz, int m, int K, int rbk,
-                                                            uint16_t* __restrict__ xg) {
+__device__ __forceinline__ void gather_slot(const uint16_t* __restrict__ x, long long x_row_stride, int batch,
+                                            const uint8_t* __restrict__ mat_index, int w, int wp, int nnz, int m,
+                                            int K, int rbk, uint16_t* __restrict__ xg) {
   const int per_row = wp / 8;  // rows * per_row < 2^31 (host)
   const int i = (int)blockIdx.x * kBlock + (int)threadIdx.x;
   if (i >= (FRAG ? 16 * rbk : batch) * per_row) return;
@@ -540,7 +567,29 @@ __global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __
   *reinterpret_cast<u32x4*>(xg + (FRAG ? (long long)i * 8 : (long long)b * wp + c0)) = word;
 }
 
+template <bool FRAG>
+__global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __restrict__ x, long long x_row_stride,
+                                                            int batch, const uint8_t* __restrict__ mat_index, int w,
+                                                            int wp, int nnz, int m, int K, int rbk,
+                                                            uint16_t* __restrict__ xg) {
+  gather_slot<FRAG>(x, x_row_stride, batch, mat_index, w, wp, nnz, m, K, rbk, xg);
+}
+
+// The operand-order gathers of a group's products, product blockIdx.y each.
+struct McGatherGroup {
+  const uint8_t* mat_index[kMcMaxGroup];
+  uint16_t* xg[kMcMaxGroup];
+};
+
+__global__ __launch_bounds__(kBlock) void nm_gather_mc_group_kernel(const uint16_t* __restrict__ x,
+                                                                  long long x_row_stride, int batch, int w, int wp,
+                                                                  int nnz, int m, int K, int rbk, McGatherGroup gg) {
+  const int i = (int)blockIdx.y;
+  gather_slot<true>(x, x_row_stride, batch, gg.mat_index[i], w, wp, nnz, m, K, rbk, gg.xg[i]);
+}
+
 typedef void (*McFn)(SpmmArgs);
+typedef void (*McGroupFn)(McGroupArgs);
 
 // fn[config: HT = 64, 128, 256][batch tile: 16, 32, 64 rows]
 #define NM_MC_ROW(DT, HT, DMA) \
@@ -550,6 +599,12 @@ typedef void (*McFn)(SpmmArgs);
    NM_MC_ROW(DT, 128, true), NM_MC_ROW(DT, 256, true)}
 const McFn kMcKernelsF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_F16);
 const McFn kMcKernelsBF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_BF16);
+#undef NM_MC_ROW
+#define NM_MC_ROW(DT, HT, DMA)                                                                     \
+  {&nm_spmm_mc_group_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_group_kernel<DT, 32, HT, DMA>,          \
+   &nm_spmm_mc_group_kernel<DT, 64, HT, DMA>}
+const McGroupFn kMcGroupKernelsF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_F16);
+const McGroupFn kMcGroupKernelsBF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_BF16);
 #undef NM_MC_TABLE
 #undef NM_MC_ROW
 
@@ -560,7 +615,7 @@ inline int ceil_div_mc(int a, int b) { return (a + b - 1) / b; }
 
 struct McPlan {
   int cfg, splits, rows, tiles, blocks, wp;
-  size_t xg_off, workspace;
+  size_t xg_off, xg_bytes, workspace;
 };
 
 // Plan, fitted to graph-replay sweeps of the DMA configurations x 1-8 splits
@@ -580,27 +635,43 @@ struct McPlan {
 // arrival counters, the partials [splits, batch, h] fp32 when splits > 1,
 // then the gathered activations in operand order (ceil(batch / 16) blocks of
 // 16 rows x wp columns, wp = w rounded up to whole chunks).
-int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, McPlan* p) {
-  if (batch < 1 || batch > NM_MC_MAX_BATCH) return NM_ERR_BAD_SHAPE;
-  if (h <= 0 || w <= 0 || nnz <= 0 || m <= 0 || m > 256 || nnz > m) return NM_ERR_BAD_SHAPE;
-  if (h % 128 != 0) return NM_ERR_H_NOT_MULTIPLE_128;
+// A group (n products of the same activations, output widths hs[0 .. n-1])
+// is planned as one product whose tiles are all the products' tiles: one
+// tile width and split count; partials and gathered activations per product,
+// one after another.
+int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg, int splits, McPlan* p) {
+  if (batch < 1 || batch > NM_MC_MAX_BATCH || n < 1 || n > kMcMaxGroup || !hs) return NM_ERR_BAD_SHAPE;
+  if (w <= 0 || nnz <= 0 || m <= 0 || m > 256 || nnz > m) return NM_ERR_BAD_SHAPE;
+  long long hsum = 0;
+  int hmax = 0;
+  for (int i = 0; i < n; ++i) {
+    if (hs[i] <= 0) return NM_ERR_BAD_SHAPE;
+    if (hs[i] % 128 != 0) return NM_ERR_H_NOT_MULTIPLE_128;
+    hsum += hs[i];
+    hmax = hs[i] > hmax ? hs[i] : hmax;
+  }
   if (w % nnz != 0) return NM_ERR_W_NOT_MULTIPLE_NNZ;
   if ((long long)(w / nnz) * (long long)m > 0x7fffffffLL || w > 0x7fffffff - kMcCK) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
-  if ((long long)batch * (long long)h > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;  // the reduction's 32-bit offsets
+  if ((long long)batch * (long long)hmax > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;  // the reduction's 32-bit offsets
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
   const int wp = ceil_div_mc(w, kMcCK) * kMcCK;
+  auto tiles_of = [&](int c) {
+    int t = 0;
+    for (int i = 0; i < n; ++i) t += ceil_div_mc(hs[i], kMcTileCols[c]);
+    return t;
+  };
   // (tiles, splits, rows per split) of a configuration and a requested split count
   auto shape_of = [&](int c, int sp, int* tiles_out, int* rows_out) {
     if (sp > wp / kMcCK) sp = wp / kMcCK;
     const int r = ceil_div_mc(ceil_div_mc(w, sp), kMcCK) * kMcCK;
-    *tiles_out = ceil_div_mc(h, kMcTileCols[c]);
+    *tiles_out = tiles_of(c);
     *rows_out = r;
     return ceil_div_mc(w, r);
   };
-  if (cfg < 0 && h <= 1024) cfg = 0;
+  if (cfg < 0 && hmax <= 1024) cfg = 0;
   if (cfg >= 0 && cfg < 3 && splits <= 0) {  // register-staged: about one workgroup per CU
-    const int t = ceil_div_mc(h, kMcTileCols[cfg]);
+    const int t = tiles_of(cfg);
     splits = (kMcCUs + t / 2) / t;
     splits = splits < 1 ? 1 : (splits > 8 ? 8 : splits);
   } else if (cfg < 0 || splits <= 0) {
@@ -652,10 +723,15 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   p->tiles = tiles;
   p->blocks = tiles * splits;
   p->wp = wp;
-  const size_t part = splits > 1 ? (size_t)splits * (size_t)batch * (size_t)h * sizeof(float) : (size_t)0;
+  const size_t part = splits > 1 ? (size_t)splits * (size_t)batch * (size_t)hsum * sizeof(float) : (size_t)0;
   p->xg_off = ((size_t)NM_TICKET_BYTES + part + 255) / 256 * 256;
-  p->workspace = p->xg_off + (size_t)ceil_div_mc(batch, 16) * 16 * (size_t)wp * 2;
+  p->xg_bytes = (size_t)ceil_div_mc(batch, 16) * 16 * (size_t)wp * 2;  // per product, a multiple of 2 KB
+  p->workspace = p->xg_off + (size_t)n * p->xg_bytes;
   return NM_OK;
+}
+
+int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, McPlan* p) {
+  return make_mc_plan(batch, 1, &h, w, nnz, m, cfg, splits, p);
 }
 
 }  // namespace
@@ -746,6 +822,93 @@ int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, cons
   const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : 2);
   const McFn fn = (dtype == NM_DTYPE_F16 ? kMcKernelsF16 : kMcKernelsBF16)[p.cfg][bt];
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, a);
+  e = hipGetLastError();
+  return e == hipSuccess ? NM_OK : (int)e;
+}
+
+size_t nm_spmm_mc_group_workspace_bytes(int batch, int n, const int* h, int w, int nnz, int m, int config_id,
+                                        int splits) {
+  McPlan p;
+  return make_mc_plan(batch, n, h, w, nnz, m, config_id, splits, &p) == NM_OK ? p.workspace : 0;
+}
+
+int nm_spmm_mc_group_plan(int batch, int n, const int* h, int w, int nnz, int m, int config_id, int splits,
+                          int* out_config_id, int* out_splits, int* out_blocks, int* out_rows_per_block) {
+  McPlan p;
+  const int rc = make_mc_plan(batch, n, h, w, nnz, m, config_id, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (out_config_id) *out_config_id = p.cfg;
+  if (out_splits) *out_splits = p.splits;
+  if (out_blocks) *out_blocks = p.blocks;
+  if (out_rows_per_block) *out_rows_per_block = p.rows;
+  return NM_OK;
+}
+
+int nm_spmm_mc_group(int dtype, const void* x, long long x_row_stride, int batch, int n, const void* const* mat_data,
+                     const uint8_t* const* mat_index, void* const* out, const long long* out_row_stride,
+                     const int* h, void* workspace, size_t workspace_bytes, int w, int nnz, int m, int config_id,
+                     int splits, void* stream) {
+  if (dtype != NM_DTYPE_F16 && dtype != NM_DTYPE_BF16) return NM_ERR_BAD_CONFIG;
+  if (!mat_data || !mat_index || !out || !out_row_stride || !h) return NM_ERR_NULL_POINTER;
+  McPlan p;
+  const int rc = make_mc_plan(batch, n, h, w, nnz, m, config_id, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (!x || !workspace) return NM_ERR_NULL_POINTER;
+  const long long K = (long long)(w / nnz) * (long long)m;
+  if (x_row_stride < K) return NM_ERR_BAD_SHAPE;
+  for (int i = 0; i < n; ++i) {
+    if (!mat_data[i] || !mat_index[i] || !out[i]) return NM_ERR_NULL_POINTER;
+    if (out_row_stride[i] < h[i]) return NM_ERR_BAD_SHAPE;
+    if (((uintptr_t)mat_data[i] & 15u) != 0) return NM_ERR_MISALIGNED;
+  }
+  if (((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
+  if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int rbk = ceil_div_mc(batch, 16);
+  McGatherGroup gg;
+  memset(&gg, 0, sizeof(gg));
+  McGroupArgs g;
+  memset(&g, 0, sizeof(g));
+  g.n = n;
+  size_t part_off = 0;
+  int tile_off = 0, block_off = 0;
+  for (int i = 0; i < n; ++i) {
+    uint16_t* xg = reinterpret_cast<uint16_t*>(static_cast<char*>(workspace) + p.xg_off + (size_t)i * p.xg_bytes);
+    gg.mat_index[i] = mat_index[i];
+    gg.xg[i] = xg;
+    SpmmArgs& a = g.p[i];
+    const int tiles = ceil_div_mc(h[i], kMcTileCols[p.cfg]);
+    a.x = xg;
+    a.x_row_stride = rbk;  // operand-order activations: the row blocks stored
+    a.mat_data = mat_data[i];
+    a.mat_index = mat_index[i];
+    a.out = out[i];
+    a.out_row_stride = out_row_stride[i];
+    a.tickets = static_cast<uint32_t*>(workspace) + tile_off;
+    a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + NM_TICKET_BYTES) + part_off;
+    a.batch = batch;
+    a.h = h[i];
+    a.tiles = tiles;
+    a.w = w;
+    a.nnz = nnz;
+    a.m = m;
+    a.K = (int)K;
+    a.splits = p.splits;
+    a.rows_per_split = p.rows;
+    g.first[i] = block_off;
+    tile_off += tiles;
+    block_off += tiles * p.splits;
+    part_off += p.splits > 1 ? (size_t)p.splits * (size_t)batch * (size_t)h[i] : (size_t)0;
+  }
+  const long long gathered = (long long)16 * rbk * (long long)(p.wp / 8);
+  const unsigned gblocks = (unsigned)((gathered + kBlock - 1) / kBlock);
+  hipLaunchKernelGGL(nm_gather_mc_group_kernel, dim3(gblocks, (unsigned)n), dim3(kBlock), 0, st,
+                     static_cast<const uint16_t*>(x), x_row_stride, batch, w, p.wp, nnz, m, (int)K, rbk, gg);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : 2);
+  const McGroupFn fn = (dtype == NM_DTYPE_F16 ? kMcGroupKernelsF16 : kMcGroupKernelsBF16)[p.cfg][bt];
+  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, g);
   e = hipGetLastError();
   return e == hipSuccess ? NM_OK : (int)e;
 }

@@ -229,6 +229,26 @@ def project_rows(lin: nn.Module, x2d: torch.Tensor) -> torch.Tensor:
     return lin(x2d)
 
 
+def project_rows_group(lins, x2d: torch.Tensor) -> list:
+    """[project_rows(lin, x2d) for lin in lins] for sibling Linears of one
+    input (q/k/v, gate/up): NmSparseLinears of one packed width and N:M run as
+    one grouped SpMM (hip_spmv.nmsparse_spmm_group_hip: one gather and one
+    matrix-core launch for all of them from 9 to 64 rows), anything else one
+    at a time."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    lins = list(lins)
+    if len(lins) > 1 and all(isinstance(l, NmSparseLinear) for l in lins):
+        l0 = lins[0]
+        if all(l.w == l0.w and l.block_width == l0.block_width and l.vec_width == l0.vec_width
+               and l.mat_data.dtype == x2d.dtype for l in lins):
+            from ..hip_spmv import nmsparse_spmm_group_hip
+
+            return nmsparse_spmm_group_hip(x2d, [(l.mat_data, l.mat_index) for l in lins], l0.block_width,
+                                           l0.vec_width)
+    return [project_rows(l, x2d) for l in lins]
+
+
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n_kv_heads: int) -> torch.Tensor:
     """softmax(q kᵀ / sqrt(d) + causal mask) v over P positions, grouped query
     heads: q [P, n_heads, d], k and v [P, kv_heads, d] -> [P, n_heads * d].
@@ -845,7 +865,8 @@ class Decoder(nn.Module):
     def prefill(self, tokens: torch.Tensor) -> torch.Tensor:
         """The prompt in one pass: tokens [P] int64 at positions 0 .. P-1 on
         the device. Every Linear sees all P rows (sparse ones through the SpMM:
-        project_rows), causal attention over the prompt in PyTorch
+        project_rows; q/k/v and gate/up as one grouped SpMM each,
+        project_rows_group), causal attention over the prompt in PyTorch
         (causal_attention), keys and values written to the static caches at
         positions 0 .. P-1 as the decode steps write them. Returns the logits
         of position P-1 [1, vocab]; decoding continues at position P (each
@@ -865,7 +886,7 @@ class Decoder(nn.Module):
                 ln1, ln2, o_proj = blk.input_layernorm, blk.post_attention_layernorm, at.o_proj
                 gate, up, down = mlp.gate_proj, mlp.up_proj, mlp.down_proj
                 h = ln1(x)
-                q, k, v = (project_rows(p, h) for p in (at.q_proj, at.k_proj, at.v_proj))
+                q, k, v = project_rows_group((at.q_proj, at.k_proj, at.v_proj), h)
             else:  # gpt-fast names
                 at, ff = blk.attention, blk.feed_forward
                 ln1, ln2, o_proj = blk.attention_norm, blk.ffn_norm, at.wo
@@ -880,7 +901,8 @@ class Decoder(nn.Module):
             self.v_cache_t[i][:, :, :P].copy_(v.permute(1, 2, 0))
             x = x + project_rows(o_proj, causal_attention(q, k, v, c.n_kv_heads))
             h = ln2(x)
-            act = F.silu(project_rows(gate, h)) * project_rows(up, h)
+            g_out, u_out = project_rows_group((gate, up), h)
+            act = F.silu(g_out) * u_out
             x = x + project_rows(down, act)
         return project(self.lm_head, self.norm(x[-1:].view(1, 1, -1))).view(1, -1)
 

@@ -332,6 +332,85 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     return out
 
 
+def nmsparse_spmm_group_hip(x, mats, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, config_id=-1, splits=0):
+    """[W_i x[..., r, :] for every row r] for the products mats = [(mat_data,
+    mat_index), ...] of one input (sibling Linears: q/k/v, gate/up), each as
+    nmsparse_spmm_forward_hip would compute it; returns the list of outputs
+    [..., rows, h_i] in x.dtype (or writes `outs`).
+
+    fp16 / bf16 with NM_MAX_BATCH < rows <= NM_MC_MAX_BATCH per launch and up to
+    NM_MC_MAX_GROUP products of the same w: one gather launch for every
+    product's activations and one matrix-core launch over all their tiles
+    (nm_spmm_mc_group; each product's rows equal nm_spmm_mc's with the same
+    config_id and splits). Otherwise (fewer or more rows, fp32, more products)
+    each product runs through nmsparse_spmm_forward_hip on its own.
+    """
+    mats = list(mats)
+    if not mats:
+        return []
+    K = x.shape[-1]
+    lead = x.shape[:-1]
+    rows = x.reshape(-1, K).shape[0]
+    w = mats[0][0].shape[0]
+    hs = [int(md.shape[1]) for md, _ in mats]
+    if outs is None:
+        outs = [None] * len(mats)
+    grouped = (x.dtype in (torch.float16, torch.bfloat16) and _lib.NM_MAX_BATCH < rows
+               and not library_route(rows, K, max(hs)) and 1 < len(mats) <= _lib.NM_MC_MAX_GROUP
+               and all(md.shape[0] == w for md, _ in mats))
+    if not grouped:
+        return [nmsparse_spmm_forward_hip(x, md, mi, w, h, BLOCK_WIDTH, VEC_WIDTH, out=o, config_id=config_id,
+                                          splits=splits)
+                for (md, mi), h, o in zip(mats, hs, outs)]
+    if not x.is_cuda or any(not (md.is_cuda and mi.is_cuda) for md, mi in mats):
+        raise ValueError("x, mat_data, and mat_index must be GPU (HIP) tensors")
+    if w % BLOCK_WIDTH != 0 or K != (w // BLOCK_WIDTH) * VEC_WIDTH:
+        raise ValueError(f"x has {K} columns; w={w}, N={BLOCK_WIDTH}, M={VEC_WIDTH} need {w // BLOCK_WIDTH * VEC_WIDTH}")
+    for (md, mi), h in zip(mats, hs):
+        if md.dtype != x.dtype:
+            raise TypeError("x and mat_data must have same dtype")
+        if mi.dtype != torch.uint8:
+            raise TypeError("mat_index must be uint8")
+        if md.device != x.device or mi.device != x.device:
+            raise ValueError("x, mat_data and mat_index must be on one device")
+        if not md.is_contiguous() or tuple(mi.shape) != (w // BLOCK_WIDTH, BLOCK_WIDTH) or not mi.is_contiguous():
+            raise ValueError(f"mat_data must be a contiguous [{w}, h] tensor, mat_index a contiguous "
+                             f"{(w // BLOCK_WIDTH, BLOCK_WIDTH)} tensor")
+    x2d = x.reshape(-1, K).contiguous()
+    res = []
+    for o, h in zip(outs, hs):
+        if o is None:
+            o = torch.empty(*lead, h, dtype=x.dtype, device=x.device)
+        elif (o.dtype != x.dtype or tuple(o.shape) != (*lead, h) or not o.is_contiguous() or o.device != x.device
+              or o.data_ptr() % 16):
+            raise ValueError(f"out must be a contiguous, 16-byte aligned {(*lead, h)} tensor of x.dtype")
+        res.append(o)
+    mds = [_aligned(md) for md, _ in mats]
+    n = len(mats)
+    per = _lib.NM_MC_MAX_BATCH
+    lib = _lib.load()
+    harr = (ctypes.c_int * n)(*hs)
+    need = lib.nm_spmm_mc_group_workspace_bytes(min(rows, per), n, harr, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id),
+                                                int(splits))
+    if need == 0:
+        raise ValueError("spmm group shape outside what libnmsparse_hip supports")
+    esize = x.element_size()
+    mds_arr = (ctypes.c_void_p * n)(*[md.data_ptr() for md in mds])
+    mis_arr = (ctypes.c_void_p * n)(*[mi.data_ptr() for _, mi in mats])
+    ostr = (ctypes.c_longlong * n)(*hs)
+    with torch.cuda.device(x.device):
+        stream = torch.cuda.current_stream(x.device).cuda_stream
+        ws = workspace_for(x.device, need, stream)
+        for r0 in range(0, rows, per):
+            b = min(per, rows - r0)
+            outs_arr = (ctypes.c_void_p * n)(*[o.data_ptr() + r0 * h * esize for o, h in zip(res, hs)])
+            rc = lib.nm_spmm_mc_group(_DTYPE_CODE[x.dtype], x2d.data_ptr() + r0 * K * esize, K, b, n, mds_arr,
+                                      mis_arr, outs_arr, ostr, harr, ws.data_ptr(), ws.numel(), w, BLOCK_WIDTH,
+                                      VEC_WIDTH, int(config_id), int(splits), stream)
+            _lib.check(rc, "nm_spmm_mc_group")
+    return res
+
+
 def _check_vector(t, n, like, what):
     """t must be a contiguous [n] or [1, n] tensor of like.dtype on like.device."""
     if t.device != like.device or t.dtype != like.dtype or t.numel() != n or not t.is_contiguous():

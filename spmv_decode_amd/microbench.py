@@ -444,6 +444,68 @@ def write_spmm_compare_md(res, path, cmd):
     Path(path).write_text("\n".join(lines) + "\n")
 
 
+def time_spmm_group(hs, n_in, nnz, m, batch, rotate_bytes=1 << 30, reps=20, seed=80) -> tuple:
+    """us per call of sibling products of one input (output widths hs):
+    (grouped, separate) = nmsparse_spmm_group_hip (one gather and one
+    matrix-core launch for all of them) and one nmsparse_spmm_forward_hip per
+    product, weights rotated over >= rotate_bytes as in time_spmm."""
+    from .hip_spmv import nmsparse_spmm_forward_hip, nmsparse_spmm_group_hip
+
+    group_bytes = sum(sparse_bytes(n_in, h, nnz, m, 2) for h in hs)
+    copies = max(1, math.ceil(rotate_bytes / group_bytes))
+    cases = [RotatingCase(h, n_in, nnz, m, rotate_bytes=0, min_copies=copies, seed=seed + i) for i, h in enumerate(hs)]
+    X = torch.randn(batch, n_in, device="cuda").to(cases[0].dtype)
+    sets = [[c.mats[i] for c in cases] for i in range(copies)]
+    grouped = graph_us_per_launch([lambda st=st: nmsparse_spmm_group_hip(X, st, nnz, m) for st in sets], reps)
+    separate = graph_us_per_launch(
+        [lambda st=st: [nmsparse_spmm_forward_hip(X, md, mi, md.shape[0], md.shape[1], nnz, m) for md, mi in st]
+         for st in sets], reps)
+    del cases, sets
+    return grouped, separate
+
+
+# name: (output widths, inputs, N, M) of sibling products of one input
+SPMM_GROUP_SHAPES = {
+    "Llama-3.1-8B q/k/v": ((4096, 1024, 1024), 4096, 32, 64), "Llama-3.1-8B gate/up": ((14336, 14336), 4096, 32, 64),
+    "Qwen3-14B q/k/v": ((5120, 1024, 1024), 5120, 32, 64), "Qwen3-14B gate/up": ((17408, 17408), 5120, 32, 64),
+    "Qwen3-32B q/k/v": ((8192, 1024, 1024), 5120, 16, 32), "Qwen3-32B gate/up": ((25600, 25600), 5120, 16, 32),
+}
+
+
+def spmm_group(shapes=SPMM_GROUP_SHAPES, rows=(9, 16, 32, 64), reps=20, log=print):
+    """Grouped against separate matrix-core SpMMs of sibling products per
+    shape and row count: us per call and the group's weight bytes per second."""
+    out = {}
+    for name, (hs, K, nnz, m) in shapes.items():
+        wbytes = sum((K // m * nnz) * h * 2 for h in hs)
+        for b in rows:
+            g, sep = time_spmm_group(hs, K, nnz, m, b, reps=reps)
+            out[f"{name}|{b}"] = {"shape": name, "rows": b, "weight_bytes": wbytes, "grouped_us": round(g, 3),
+                                  "separate_us": round(sep, 3), "grouped_weight_GBps": round(wbytes / g / 1e3, 1),
+                                  "speedup": round(sep / g, 3)}
+            log(f"spmm group {name:22s} {b:3d} rows: grouped {g:7.2f} us ({wbytes / g / 1e3:6.0f} GB/s), "
+                f"separate {sep:7.2f} us ({sep / g:.2f}x)")
+        torch.cuda.empty_cache()
+    return out
+
+
+def write_spmm_group_md(res, path, cmd):
+    lines = ["# Grouped matrix-core SpMM of sibling products (MI355X, fp16)", "",
+             "Command (repository root, one MI355X):", "", "```", cmd, "```", "",
+             "Per group of sibling products of one input and activation-row count: `nm_spmm_mc_group` through",
+             "`nmsparse_spmm_group_hip` (one gather launch for every product's activations, one matrix-core launch",
+             "over all their tiles; the default plan) against one `nmsparse_spmm_forward_hip` call per product (a",
+             "gather and a matrix-core launch each). us per call of the whole group, median of graph replays over",
+             ">= 1 GiB of rotated weights (`microbench.time_spmm_group`); GB/s counts the group's packed weight",
+             "bytes.", "",
+             "| Group | Rows | Weight bytes | grouped us | GB/s | separate us | speedup |",
+             "|---|---|---|---|---|---|---|"]
+    for r in res.values():
+        lines.append(f"| {r['shape']} | {r['rows']} | {r['weight_bytes']:,} | {r['grouped_us']:.2f} | "
+                     f"{r['grouped_weight_GBps']:.0f} | {r['separate_us']:.2f} | {r['speedup']:.2f}x |")
+    Path(path).write_text("\n".join(lines) + "\n")
+
+
 def time_dense(n_out, n_in, dtype=torch.float16, rotate_bytes=1 << 30, reps=20, seed=1, device="cuda", warmup=3,
                stats=False, form="best", return_form=False):
     """Dense GEMV y = x * W^T through the BLAS library, weights rotated over
@@ -887,6 +949,8 @@ def main(argv=None):
     p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
     p.add_argument("--spmm-compare", action="store_true",
                    help="the matrix-core SpMM beside gather + hipBLASLt at the Llama / Qwen3 shapes, 9-64 rows")
+    p.add_argument("--spmm-group", action="store_true",
+                   help="grouped against separate matrix-core SpMMs of q/k/v and gate/up, Llama / Qwen3, 9-64 rows")
     p.add_argument("--pair-sweep", action="store_true",
                    help="time the decoder's gate/up pair launch under every pair configuration x split count "
                         "(Llama-3.1-8B shapes, the first --ratios entry); --csv for profiling sweep-stats")
@@ -951,6 +1015,13 @@ def main(argv=None):
             Path(a.json).write_text(json.dumps(res, indent=1))
         if a.md:
             write_spmm_compare_md(res, a.md, "python -u -m spmv_decode_amd.microbench --spmm-compare --json <json> --md <md>")
+        return 0
+    if a.spmm_group:
+        res = spmm_group(reps=a.reps, log=lambda s: print(s, flush=True))
+        if a.json:
+            Path(a.json).write_text(json.dumps(res, indent=1))
+        if a.md:
+            write_spmm_group_md(res, a.md, "python -u -m spmv_decode_amd.microbench --spmm-group --json <json> --md <md>")
         return 0
     rows = run(_parse_pairs(a.dims, "x"), _parse_pairs(a.ratios, ":"), a.dtype, a.sweep, a.rotate_mib, a.reps,
                a.csv, not a.no_dense, log=lambda s: print(s, flush=True), warmup=a.warmup)

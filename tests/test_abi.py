@@ -269,6 +269,53 @@ def test_spmm_rejections_and_plans():
         assert (g["rows_per_split"], g["splits"]) == (s["rows_per_split"], s["splits"])
 
 
+def test_spmm_mc_group_rejections_and_plans():
+    """The grouped matrix-core SpMM: rejections before any launch, and its plan
+    and workspace against the single-product ones."""
+    lib = _lib.load()
+    n_max = _lib.NM_MC_MAX_GROUP
+
+    def arr(t, vals):
+        return (t * max(len(vals), 1))(*vals)
+
+    def call(n=3, hs=(4096, 1024, 1024), x=FAKE, xs=4096, batch=20, md=FAKE, mi=FAKE, out=FAKE, ostr=None,
+             ws=FAKE, wsb=1 << 30, w=2048, nnz=32, m=64, cfg=-1, splits=0, dtype=0):
+        k = len(hs)
+        ostr = hs if ostr is None else ostr
+        return lib.nm_spmm_mc_group(dtype, x, xs, batch, n, arr(ctypes.c_void_p, [md] * k),
+                                    arr(ctypes.c_void_p, [mi] * k), arr(ctypes.c_void_p, [out] * k),
+                                    arr(ctypes.c_longlong, list(ostr)), arr(ctypes.c_int, list(hs)), ws, wsb, w, nnz,
+                                    m, cfg, splits, None)
+
+    assert call(n=0, hs=()) == -2 and call(n=n_max + 1, hs=(128,) * (n_max + 1)) == -2
+    assert call(batch=0) == -2 and call(batch=_lib.NM_MC_MAX_BATCH + 1) == -2
+    assert call(dtype=2) == -7 and call(cfg=6) == -7
+    assert call(x=None) == -1 and call(md=None) == -1 and call(out=None) == -1 and call(ws=None) == -1
+    assert call(hs=(4096, 1000, 1024)) == -3 and call(w=2047) == -4
+    assert call(xs=4095) == -2 and call(ostr=(4096, 1000, 1024)) == -2
+    assert call(md=FAKE + 2) == -5 and call(ws=FAKE + 16) == -5 and call(wsb=1024) == -6
+    for batch in (9, 16, 33, 64):
+        for hs, w in (((4096, 1024, 1024), 2048), ((14336, 14336), 2048), ((384, 128, 256, 640), 500)):
+            for cfg, splits in ((-1, 0), (0, 2), (3, 0), (5, 3)):
+                nnz, m = (32, 64) if w == 2048 else (4, 8)
+                g = _lib.spmm_mc_group_plan(batch, list(hs), w, nnz, m, cfg, splits)
+                tiles = sum(-(-h // (64, 128, 256)[g["config_id"] % 3]) for h in hs)
+                assert g["blocks"] == tiles * g["splits"]
+                wp = -(-w // 64) * 64
+                part = g["splits"] * batch * sum(hs) * 4 if g["splits"] > 1 else 0
+                xg_off = -(-(_lib.NM_TICKET_BYTES + part) // 256) * 256
+                need = lib.nm_spmm_mc_group_workspace_bytes(batch, len(hs), arr(ctypes.c_int, list(hs)), w, nnz, m,
+                                                            cfg, splits)
+                assert need == xg_off + len(hs) * (-(-batch // 16) * 16 * wp * 2)
+                # a group of one is the single-product plan
+                for h in hs:
+                    one = _lib.spmm_mc_group_plan(batch, [h], w, nnz, m, cfg, splits)
+                    assert one == _lib.spmm_mc_plan(batch, h, w, nnz, m, cfg, splits)
+                    assert (lib.nm_spmm_mc_group_workspace_bytes(batch, 1, arr(ctypes.c_int, [h]), w, nnz, m, cfg,
+                                                                 splits)
+                            == lib.nm_spmm_mc_workspace_bytes(batch, h, w, nnz, m, cfg, splits))
+
+
 def test_launch_plan_query():
     """Host-only plan query of a fused launch (shapes only: no kernel runs)."""
     import torch

@@ -1,8 +1,9 @@
 """GPU parity of the matrix-core SpMM (nm_spmm_mc: 9-64 rows per launch,
 fp16 / bf16) against the oracle, at the Llama-3.1-8B and Qwen3 shapes, on
 ragged shapes (a last chunk shorter than 32 columns, a last tile past h,
-positions outside x), every configuration and split count, strided rows
-through the C ABI, graph replay and the automatic routing."""
+positions outside x), every configuration and split count, groups of sibling
+products in one launch, strided rows through the C ABI, graph replay and the
+automatic routing."""
 import numpy as np
 import pytest
 import torch
@@ -57,6 +58,68 @@ def test_ragged_shapes_configs_and_splits(gpu, dtype):
                 say(f"spmm_mc {dtype} K{K} h{h} {nnz}:{m} batch {batch} cfg {cfg} splits {splits} -> {p}")
                 check_rows(mc(X, md, mi, nnz, m, config_id=cfg, splits=splits), X, md, mi, nnz, m,
                            f"{dtype} {K}x{h} {nnz}:{m} b{batch} cfg{cfg} s{splits}")
+
+
+# (K, [h...], nnz, m): sibling products of one input (q/k/v, gate/up; ragged widths and groups of 4)
+MC_GROUPS = [(4096, [4096, 1024, 1024], 32, 64), (4096, [14336, 14336], 32, 64), (5120, [5120, 1024, 1024], 16, 32),
+             (1000, [384, 128, 256, 640], 4, 8), (2048, [1280, 128], 3, 4)]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+def test_grouped_products_match_single_launches(gpu, dtype):
+    """nm_spmm_mc_group: each product of a group is bit for bit the
+    single-product launch with the group's configuration and split count, and
+    within the oracle bar, for the default plan and forced ones."""
+    for K, hs, nnz, m in MC_GROUPS:
+        cases = [make_case(K, h, nnz, m, seed=K + 7 * h + i, dtype=dtype) for i, h in enumerate(hs)]
+        w = cases[0][1].shape[0]
+        mats = [(md, mi) for _, md, mi in cases]
+        for batch in (9, 16, 33, 64):
+            X = torch.randn(batch, K, generator=torch.Generator(device="cuda").manual_seed(batch), device="cuda")
+            X = X.to(dtype)
+            for cfg, splits in ((-1, 0), (0, 2), (4, 0), (5, 3), (3, 1)):
+                p = _lib.spmm_mc_group_plan(batch, hs, w, nnz, m, cfg, splits)
+                say(f"spmm_mc group {dtype} K{K} h{hs} {nnz}:{m} batch {batch} cfg {cfg} splits {splits} -> {p}")
+                outs = hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, config_id=cfg, splits=splits)
+                for (md, mi), o in zip(mats, outs):
+                    check_rows(o, X, md, mi, nnz, m, f"group {dtype} {K}x{md.shape[1]} b{batch} cfg{cfg}")
+                    assert torch.equal(o, mc(X, md, mi, nnz, m, config_id=p["config_id"], splits=p["splits"]))
+
+
+def test_grouped_products_replay_and_route(gpu):
+    """A captured group (split-K arrival counters of every product in one
+    workspace) replayed with eager launches between, each replay equal to
+    eager; outside 9-64 rows the group helper runs each product through the
+    single-product route (the same bits)."""
+    K, hs, nnz, m = 4096, [4096, 1024, 1024], 32, 64
+    cases = [make_case(K, h, nnz, m, seed=300 + i) for i, h in enumerate(hs)]
+    mats = [(md, mi) for _, md, mi in cases]
+    X = torch.randn(40, K, device="cuda").half()
+    eager = [o.clone() for o in hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, config_id=4, splits=2)]
+    outs = [torch.empty_like(o) for o in eager]
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.stream(s):
+        hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, outs=outs, config_id=4, splits=2)
+        torch.cuda.synchronize()
+        with torch.cuda.graph(g, stream=s):
+            hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, outs=outs, config_id=4, splits=2)
+    torch.cuda.current_stream().wait_stream(s)
+    say("spmm_mc group graph replays")
+    for rep in range(6):
+        for o in outs:
+            o.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        for o, e in zip(outs, eager):
+            assert torch.equal(o, e), rep
+        hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, config_id=4, splits=2)  # eager work between replays
+    for rows in (3, 8, 65, 100):
+        Xr = torch.randn(rows, K, device="cuda").half()
+        say(f"spmm group route {rows} rows")
+        for (md, mi), o in zip(mats, hip_spmv.nmsparse_spmm_group_hip(Xr, mats, nnz, m)):
+            assert torch.equal(o, hip_spmv.nmsparse_spmm_forward_hip(Xr, md, mi, md.shape[0], md.shape[1], nnz, m))
 
 
 def test_more_than_64_rows_and_determinism(gpu):
