@@ -230,6 +230,11 @@ class NmSparseLinear(nn.Module):
         args = (self.mat_data, self.mat_index, self.w, self.h, self.block_width, self.vec_width)
         if SPARSE_BATCH != "0" and rows > 1:
             if not self._has_dense() or (SPARSE_BATCH == "1" and rows <= SPARSE_BATCH_MAX_ROWS):
+                group = self.__dict__.get("_siblings")
+                if group is not None and not torch.compiler.is_compiling():
+                    y = group.output(self, x)
+                    if y is not None:
+                        return y
                 return torch.ops.nmsparse.spmm(x, *args)
         if x.shape[-2] == 1:
             group = self.__dict__.get("_siblings")
@@ -250,13 +255,15 @@ class SiblingLaunch:
     one launch each, without any change to the model code that calls them.
 
     The first member called with a one-row input launches the grouped GEMV for
-    every member and keeps the other members' outputs; a member then called
-    with the very same input tensor (same object, unchanged version counter)
-    takes its output, once. Any other call (another input, a repeated member,
-    more than one row, a dtype or device the grouped launch does not take, or
-    torch.compile tracing) goes through the member's own op as before, so the
-    results never depend on the call order, only the last bit of a sum may
-    (the grouped plan splits the columns like a launch of the summed width).
+    every member (with 9-64 rows of fp16 / bf16 on the sparse path: the
+    grouped matrix-core SpMM, hip_spmv.nmsparse_spmm_group_hip) and keeps the
+    other members' outputs; a member then called with the very same input
+    tensor (same object, unchanged version counter) takes its output, once.
+    Any other call (another input, a repeated member, other row counts, a
+    dtype or device the grouped launch does not take, or torch.compile
+    tracing) goes through the member's own op as before, so the results never
+    depend on the call order, only the last bit of a sum may (the grouped plan
+    splits the columns like a launch of the summed width).
     The bookkeeping is on the host, so under hipGraph capture the graph holds
     the one grouped launch and the siblings read its outputs. The group holds
     the input tensor it launched for until the next launch, so that tensor's
@@ -294,8 +301,10 @@ class SiblingLaunch:
 
     def _usable(self, x) -> bool:
         md = self.members[0].mat_data
-        return (x.is_cuda and x.dtype == md.dtype and x.device == md.device and x.is_contiguous()
-                and x.numel() == x.shape[-1] and all(m.mat_data.device == md.device for m in self.members))
+        rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
+        grouped_rows = rows == 1 or (x.dtype in (torch.float16, torch.bfloat16) and 8 < rows <= 64)
+        return (x.is_cuda and x.dtype == md.dtype and x.device == md.device and x.is_contiguous() and grouped_rows
+                and all(m.mat_data.device == md.device for m in self.members))
 
     def output(self, member, x):
         """member(x) from the group's launch, or None when the group does not
@@ -314,12 +323,15 @@ class SiblingLaunch:
                 "had not taken their outputs of its previous launch (siblings called with different inputs?); "
                 "those weights were streamed for nothing. Results are unaffected; untie_siblings(model) makes "
                 "every Linear launch on its own.", RuntimeWarning, stacklevel=3)
-        from .hip_spmv import nmsparse_gemv_grouped
+        from .hip_spmv import nmsparse_gemv_grouped, nmsparse_spmm_group_hip
 
         m0 = self.members[0]
         outs = [torch.empty(*x.shape[:-1], m.h, dtype=x.dtype, device=x.device) for m in self.members]
-        nmsparse_gemv_grouped(x.view(1, -1), [(m.mat_data, m.mat_index) for m in self.members], m0.block_width,
-                              m0.vec_width, outs=[o.view(1, -1) for o in outs])
+        mats = [(m.mat_data, m.mat_index) for m in self.members]
+        if x.numel() == x.shape[-1]:
+            nmsparse_gemv_grouped(x.view(1, -1), mats, m0.block_width, m0.vec_width, outs=[o.view(1, -1) for o in outs])
+        else:
+            nmsparse_spmm_group_hip(x, mats, m0.block_width, m0.vec_width, outs=outs)
         self._x, self._version = x, version
         self._pending = {j: o for j, o in enumerate(outs) if j != i}
         return outs[i]

@@ -746,6 +746,38 @@ def test_tied_siblings_against_the_oracle(gpu, monkeypatch):
         torch.cuda.synchronize()
 
 
+def test_tied_siblings_group_multi_row_inputs(gpu, monkeypatch):
+    """Tied siblings called with 9-64 rows of fp16 (a batch of short prompts)
+    run as ONE grouped matrix-core SpMM: each member's output equal to the
+    grouped launch's and within the oracle bar; 2-8 rows and more than 64 rows
+    go through each member's own op."""
+    from spmv_decode_amd.nmsparse_linear import NmSparseLinear, tie_siblings
+    from test_spmm_gpu import check_rows
+
+    K, M = 4096, 64
+    mods = [NmSparseLinear(h, K, M, 50 + i, "cuda", init="device") for i, h in enumerate((4096, 1024, 1024))]
+    tie_siblings(*mods)
+    launches = []
+    real = hip_spmv.nmsparse_spmm_group_hip
+    monkeypatch.setattr(hip_spmv, "nmsparse_spmm_group_hip", lambda *a, **k: launches.append(1) or real(*a, **k))
+    g = torch.Generator(device="cuda").manual_seed(5)
+    x = torch.randn(2, 12, K, generator=g, device="cuda").half()
+    say("tied siblings 24 rows")
+    outs = [mods[i](x) for i in (2, 0, 1)]
+    outs = [outs[1], outs[2], outs[0]]
+    assert len(launches) == 1
+    ref = real(x, [(m.mat_data, m.mat_index) for m in mods], 32, 64)
+    for mod, o, r in zip(mods, outs, ref):
+        assert o.shape == (2, 12, mod.h) and torch.equal(o, r)
+        check_rows(o.view(24, -1), x.view(24, -1), mod.mat_data, mod.mat_index, 32, 64, f"tied rows h{mod.h}")
+    for rows in (4, 70):
+        xr = torch.randn(rows, K, generator=g, device="cuda").half()
+        say(f"tied siblings {rows} rows")
+        for mod in mods:
+            assert torch.equal(mod(xr), torch.ops.nmsparse.spmm(xr, mod.mat_data, mod.mat_index, mod.w, mod.h, 32, 64))
+    assert len(launches) == 1
+
+
 def test_swapped_model_decodes_under_inference_mode(gpu):
     """The reference's benchmarks swap the model and run it under
     torch.inference_mode() (benchmarks/bench_llama_3_8b_fp16_fixed_ptx.py:87,
