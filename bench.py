@@ -471,14 +471,14 @@ def main():
     result["per_shape_sparse"] = per_shape
 
     # ---- batch > 1: the small-batch SpMM (up to 8 rows) and the matrix-core
-    #      SpMM (16-64 rows, one launch plus its activation gather), per row vs
+    #      SpMM (16-128 rows, one launch plus its activation gather), per row vs
     #      the batch-1 GEMV ------------------------------------------------------
     spmm = {}
     for cls in ("q_o", "gate_up", "down"):
         K, h = SHAPES[classes[cls][0]]
         b1 = per_shape[cls]["us_per_launch"]
         rows = {}
-        for batch in (2, 4, 8, 16, 32, 64):
+        for batch in (2, 4, 8, 16, 32, 64, 128):
             routed = batch > 8 and hip_spmv.library_route(batch, K, h)
             us = MB.time_spmm(h, K, nnz, m, batch, reps=reps)  # the library's automatic choice
             rows[str(batch)] = {"kernel": ("small-batch" if batch <= 8 else
@@ -504,7 +504,7 @@ def main():
     for name, (hs, K) in {"q_k_v": ((4096, 1024, 1024), 4096), "gate_up": ((14336, 14336), 4096)}.items():
         wbytes = sum(((K // m) * nnz) * h * 2 for h in hs)
         group[name] = {}
-        for batch in (16, 32, 64):
+        for batch in (16, 32, 64, 128):
             g_us, sep_us = MB.time_spmm_group(hs, K, nnz, m, batch, reps=reps)
             group[name][str(batch)] = {"grouped_us": round(g_us, 3), "separate_us": round(sep_us, 3),
                                        "grouped_weight_GBps": round(wbytes / (g_us * 1e-6) / 1e9, 1),
@@ -623,9 +623,8 @@ def decode_ms_per_token(m, log):
 
     def prefill_ms(model, reps=10):
         """The prompt's GPU time in one Decoder.prefill pass (every Linear over its 128 rows: hipBLASLt on the
-        dense weights for the dense model; for the sparse one the gathered activations [128, w] times the
-        packed weights as one hipBLASLt GEMM), captured as a hipGraph after an eager warm-up; median of reps
-        replays."""
+        dense weights for the dense model; for the sparse one the matrix-core SpMM, q/k/v and gate/up grouped),
+        captured as a hipGraph after an eager warm-up; median of reps replays."""
         from spmv_decode_amd.decode.runner import cache_length
 
         model.setup_cache(cache_length(prompt.numel() + 1), torch.device("cuda"), dtype=torch.float16)
@@ -728,9 +727,9 @@ def decode_ms_per_token(m, log):
            "prefill_one_pass": {"dense_ms": prefill_dense, "sparse_ms": prefill_sparse,
                                 "speedup_sparse_vs_dense": ratio(prefill_dense, prefill_sparse),
                                 "what": "the 128-token prompt through Decoder.prefill as one hipGraph: every "
-                                        "Linear over 128 rows (dense: hipBLASLt on the dense weights; sparse: "
-                                        "nm_gather_columns + one hipBLASLt GEMM over the packed weights, half the "
-                                        "input width), causal attention in PyTorch"},
+                                        "Linear over 128 rows (dense: hipBLASLt on the dense weights; sparse: the "
+                                        "matrix-core SpMM's 128-row tiles, q/k/v and gate/up grouped), causal "
+                                        "attention through PyTorch's scaled_dot_product_attention"},
            "dense_ms_per_token": dense["ms_per_token"], "sparse_ms_per_token": sparse["ms_per_token"],
            "dense_launches": "q/k/v fused into one GEMM (the reference's dense model), gate/up/o/down one each; "
                              "each shape in the faster of hipBLASLt's x*W^T and W*x forms",

@@ -349,7 +349,7 @@ int nm_spmm_plan(int batch, int h, int w, int nnz, int m, int config_id, int spl
  * reference op rejects rows != 1, src/spmv/nmsparse_op.py:83-86, and its
  * module runs them through a dense F.linear, src/spmv/nmsparse_linear.py:62-68).
  */
-#define NM_MC_MAX_BATCH 64
+#define NM_MC_MAX_BATCH 128
 size_t nm_spmm_mc_workspace_bytes(int batch, int h, int w, int nnz, int m, int config_id, int splits);
 int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
                const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace,

@@ -28,7 +28,7 @@ NM_ERR = {
 }
 NM_KIND_GROUPED, NM_KIND_GATE_UP = 0, 1
 NM_MAX_BATCH = 8
-NM_MC_MAX_BATCH = 64
+NM_MC_MAX_BATCH = 128
 NM_MC_MAX_GROUP = 4
 NM_STATIC_SCRATCH_BYTES = NM_TICKET_BYTES + (16 << 20)
 
@@ -97,7 +97,7 @@ ABI = {
     "nm_abi_version": (_i, []),
     "nm_stream_capture_id": (_i, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _lib = None
 _lock = threading.Lock()

@@ -17,10 +17,10 @@
 //    x[b, (c/nnz)*m + mat_index[c]], into the workspace ([batch, wp], wp = w
 //    rounded up to whole 64-column chunks, zero past w).
 //  * The main kernel: a workgroup (256 lanes = 4 wave64) owns an output tile
-//    of HT columns r and all BT >= batch rows (16, 32 or 64), over one split
-//    of the compressed columns c. The 4 waves split the tile into row
-//    ranges (one 16-row block each up to 32 rows, two blocks each at 64) x
-//    column ranges; a wave keeps its rows x columns as 16 x 16 fp32
+//    of HT columns r and all BT >= batch rows (16, 32, 64 or 128), over one
+//    split of the compressed columns c. The 4 waves split the tile into row
+//    ranges (one 16-row block each up to 32 rows, two / four blocks each at
+//    64 / 128) x column ranges; a wave keeps its rows x columns as 16 x 16 fp32
 //    accumulator blocks in registers. Chunks of 64 compressed columns (two
 //    MFMA K steps): the weight rows [64 x HT] are staged through LDS. Up to
 //    1024 outputs (register-staged): loaded 16 B per lane (non-temporal),
@@ -44,7 +44,7 @@ namespace {
 
 constexpr int kMcCK = 64;         // compressed columns per chunk: two MFMA K steps of 32
 constexpr int kMcNumConfigs = 6;  // output tile HT = 64, 128, 256; register-staged (0-2) or DMA (3-5) weights
-static_assert(NM_MC_MAX_BATCH == 64, "batch tiles of 16, 32 and 64 rows");
+static_assert(NM_MC_MAX_BATCH == 128, "batch tiles of 16, 32, 64 and 128 rows");
 
 typedef short s4 __attribute__((ext_vector_type(4)));
 typedef short s8 __attribute__((ext_vector_type(8)));
@@ -134,9 +134,10 @@ __device__ __forceinline__ void mc_tile(const SpmmArgs& a, const int block) {
   typedef typename E::scalar T;  // 16-bit storage
   constexpr int RBT = BT / 16;              // 16-row blocks per tile
   // Waves along the rows: one per 16-row block up to 32 rows, two of two
-  // blocks each at 64 rows (four waves of one block each read the whole
-  // weight tile from LDS four times over, and measured 2-9% slower).
-  constexpr int WM = BT == 64 ? 2 : RBT;
+  // (four) blocks each at 64 (128) rows (four waves of one block each read
+  // the whole weight tile from LDS four times over, and measured 2-9% slower
+  // at 64 rows).
+  constexpr int WM = RBT < 2 ? RBT : 2;
   constexpr int WN = 4 / WM;                // waves along the output columns
   constexpr int MB = RBT / WM;              // 16-row blocks per wave
   constexpr int NW = HT / WN;               // output columns per wave
@@ -591,22 +592,33 @@ __global__ __launch_bounds__(kBlock) void nm_gather_mc_group_kernel(const uint16
 typedef void (*McFn)(SpmmArgs);
 typedef void (*McGroupFn)(McGroupArgs);
 
-// fn[config: HT = 64, 128, 256][batch tile: 16, 32, 64 rows]
-#define NM_MC_ROW(DT, HT, DMA) \
-  {&nm_spmm_mc_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_kernel<DT, 32, HT, DMA>, &nm_spmm_mc_kernel<DT, 64, HT, DMA>}
-#define NM_MC_TABLE(DT)                                                                                    \
-  {NM_MC_ROW(DT, 64, false), NM_MC_ROW(DT, 128, false), NM_MC_ROW(DT, 256, false), NM_MC_ROW(DT, 64, true), \
-   NM_MC_ROW(DT, 128, true), NM_MC_ROW(DT, 256, true)}
-const McFn kMcKernelsF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_F16);
-const McFn kMcKernelsBF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_BF16);
+// fn[config: HT = 64, 128, 256][batch tile: 16, 32, 64, 128 rows]
+// (no 128-row tile of 256 columns: its accumulators and operands exceed the
+// register file; the plan does not take HT = 256 past 64 rows)
+#define NM_MC_ROW(DT, HT, DMA)                                                                               \
+  {&nm_spmm_mc_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_kernel<DT, 32, HT, DMA>, &nm_spmm_mc_kernel<DT, 64, HT, DMA>, \
+   &nm_spmm_mc_kernel<DT, 128, HT, DMA>}
+#define NM_MC_ROW3(DT, HT, DMA)                                                                              \
+  {&nm_spmm_mc_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_kernel<DT, 32, HT, DMA>, &nm_spmm_mc_kernel<DT, 64, HT, DMA>, \
+   nullptr}
+#define NM_MC_TABLE(DT)                                                                                     \
+  {NM_MC_ROW(DT, 64, false), NM_MC_ROW(DT, 128, false), NM_MC_ROW3(DT, 256, false), NM_MC_ROW(DT, 64, true), \
+   NM_MC_ROW(DT, 128, true), NM_MC_ROW3(DT, 256, true)}
+const McFn kMcKernelsF16[kMcNumConfigs][4] = NM_MC_TABLE(NM_DTYPE_F16);
+const McFn kMcKernelsBF16[kMcNumConfigs][4] = NM_MC_TABLE(NM_DTYPE_BF16);
 #undef NM_MC_ROW
+#undef NM_MC_ROW3
 #define NM_MC_ROW(DT, HT, DMA)                                                                     \
   {&nm_spmm_mc_group_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_group_kernel<DT, 32, HT, DMA>,          \
-   &nm_spmm_mc_group_kernel<DT, 64, HT, DMA>}
-const McGroupFn kMcGroupKernelsF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_F16);
-const McGroupFn kMcGroupKernelsBF16[kMcNumConfigs][3] = NM_MC_TABLE(NM_DTYPE_BF16);
+   &nm_spmm_mc_group_kernel<DT, 64, HT, DMA>, &nm_spmm_mc_group_kernel<DT, 128, HT, DMA>}
+#define NM_MC_ROW3(DT, HT, DMA)                                                                    \
+  {&nm_spmm_mc_group_kernel<DT, 16, HT, DMA>, &nm_spmm_mc_group_kernel<DT, 32, HT, DMA>,          \
+   &nm_spmm_mc_group_kernel<DT, 64, HT, DMA>, nullptr}
+const McGroupFn kMcGroupKernelsF16[kMcNumConfigs][4] = NM_MC_TABLE(NM_DTYPE_F16);
+const McGroupFn kMcGroupKernelsBF16[kMcNumConfigs][4] = NM_MC_TABLE(NM_DTYPE_BF16);
 #undef NM_MC_TABLE
 #undef NM_MC_ROW
+#undef NM_MC_ROW3
 
 constexpr int kMcTileCols[kMcNumConfigs] = {64, 128, 256, 64, 128, 256};
 constexpr int kMcCUs = 256;  // MI355X compute units; split counts aim at about this many workgroups
@@ -655,6 +667,7 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
   if ((long long)batch * (long long)(w / 8 + kMcCK) > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;
   if ((long long)batch * (long long)hmax > 0x7fffffffLL) return NM_ERR_BAD_SHAPE;  // the reduction's 32-bit offsets
   if (cfg >= kMcNumConfigs) return NM_ERR_BAD_CONFIG;
+  if (batch > 64 && kMcTileCols[cfg < 0 ? 0 : cfg] == 256) return NM_ERR_BAD_CONFIG;  // no 128 x 256 tile
   const int wp = ceil_div_mc(w, kMcCK) * kMcCK;
   auto tiles_of = [&](int c) {
     int t = 0;
@@ -695,6 +708,7 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
     };
     for (int c = c_lo; c <= c_hi; ++c)
       for (int sp = s_lo; sp <= s_hi; ++sp) {
+        if (batch > 64 && kMcTileCols[c] == 256) continue;
         int t, r;
         const int se = shape_of(c, sp, &t, &r);
         if (se != sp && splits <= 0) continue;  // the same grid as a smaller request
@@ -819,7 +833,7 @@ int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, cons
   a.K = (int)K;
   a.splits = p.splits;
   a.rows_per_split = p.rows;
-  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : 2);
+  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : (batch <= 64 ? 2 : 3));
   const McFn fn = (dtype == NM_DTYPE_F16 ? kMcKernelsF16 : kMcKernelsBF16)[p.cfg][bt];
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, a);
   e = hipGetLastError();
@@ -906,7 +920,7 @@ int nm_spmm_mc_group(int dtype, const void* x, long long x_row_stride, int batch
                      static_cast<const uint16_t*>(x), x_row_stride, batch, w, p.wp, nnz, m, (int)K, rbk, gg);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return (int)e;
-  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : 2);
+  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : (batch <= 64 ? 2 : 3));
   const McGroupFn fn = (dtype == NM_DTYPE_F16 ? kMcGroupKernelsF16 : kMcGroupKernelsBF16)[p.cfg][bt];
   hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, g);
   e = hipGetLastError();

@@ -229,12 +229,15 @@ def library_route(rows: int, K: int, h: int) -> bool:
     product of `rows` (> NM_MAX_BATCH) rows, is the gathered activations times
     mat_data on hipBLASLt rather than the matrix-core SpMM: past
     NM_MC_MAX_BATCH rows, where one GEMM replaces several launches of the
-    kernel. From 9 to 64 rows the matrix-core kernel measured faster at every
-    Llama-3.1-8B and Qwen3 shape on MI355X (by 1.05-2.5x; 5-14% at the
-    gate/up projections from 32 rows, the closest). K and h are kept for
-    callers that route by shape."""
-    del K, h
-    return rows > _lib.NM_MC_MAX_BATCH
+    kernel, and past 64 rows for products of at most 1024 outputs. Measured on
+    MI355X at every Llama-3.1-8B and Qwen3 shape: from 9 to 64 rows the
+    matrix-core kernel is faster everywhere (1.05-2.5x); from 65 to 128 rows
+    (its 128-row tiles) it is 1.3-2.15x faster at the down and o projections,
+    level at gate/up (0.89-1.20x), and 8-23% slower at the 1024-output k/v
+    products, which stay on the library. K is kept for callers that route by
+    shape."""
+    del K
+    return rows > _lib.NM_MC_MAX_BATCH or (rows > 64 and h <= 1024)
 
 
 def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, *, out=None, config_id=-1,
@@ -338,12 +341,14 @@ def nmsparse_spmm_group_hip(x, mats, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, confi
     nmsparse_spmm_forward_hip would compute it; returns the list of outputs
     [..., rows, h_i] in x.dtype (or writes `outs`).
 
-    fp16 / bf16 with NM_MAX_BATCH < rows <= NM_MC_MAX_BATCH per launch and up to
+    fp16 / bf16 with NM_MAX_BATCH < rows <= NM_MC_MAX_BATCH and up to
     NM_MC_MAX_GROUP products of the same w: one gather launch for every
     product's activations and one matrix-core launch over all their tiles
     (nm_spmm_mc_group; each product's rows equal nm_spmm_mc's with the same
-    config_id and splits). Otherwise (fewer or more rows, fp32, more products)
-    each product runs through nmsparse_spmm_forward_hip on its own.
+    config_id and splits). Otherwise (fewer or more rows, fp32, more
+    products, or with the plan left to the library past 64 rows of products
+    of at most 1024 outputs: library_route) each product runs through
+    nmsparse_spmm_forward_hip on its own.
     """
     mats = list(mats)
     if not mats:
@@ -355,8 +360,9 @@ def nmsparse_spmm_group_hip(x, mats, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, confi
     hs = [int(md.shape[1]) for md, _ in mats]
     if outs is None:
         outs = [None] * len(mats)
-    grouped = (x.dtype in (torch.float16, torch.bfloat16) and _lib.NM_MAX_BATCH < rows
-               and not library_route(rows, K, max(hs)) and 1 < len(mats) <= _lib.NM_MC_MAX_GROUP
+    explicit = config_id >= 0 or splits > 0  # a matrix-core plan named by the caller
+    grouped = (x.dtype in (torch.float16, torch.bfloat16) and _lib.NM_MAX_BATCH < rows <= _lib.NM_MC_MAX_BATCH
+               and (explicit or not library_route(rows, K, max(hs))) and 1 < len(mats) <= _lib.NM_MC_MAX_GROUP
                and all(md.shape[0] == w for md, _ in mats))
     if not grouped:
         return [nmsparse_spmm_forward_hip(x, md, mi, w, h, BLOCK_WIDTH, VEC_WIDTH, out=o, config_id=config_id,

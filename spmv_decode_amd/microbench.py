@@ -408,7 +408,7 @@ SPMM_COMPARE_SHAPES = {
 }
 
 
-def spmm_compare(shapes=SPMM_COMPARE_SHAPES, rows=(9, 16, 32, 64), reps=20, log=print):
+def spmm_compare(shapes=SPMM_COMPARE_SHAPES, rows=(9, 16, 32, 64, 96, 128), reps=20, log=print):
     """The matrix-core SpMM (its default plan, the activation gather included)
     beside the library route (the same gather, then one hipBLASLt GEMM) per
     shape and row count: us per call, weight bytes per second, graph replay
@@ -472,7 +472,7 @@ SPMM_GROUP_SHAPES = {
 }
 
 
-def spmm_group(shapes=SPMM_GROUP_SHAPES, rows=(9, 16, 32, 64), reps=20, log=print):
+def spmm_group(shapes=SPMM_GROUP_SHAPES, rows=(9, 16, 32, 64, 96, 128), reps=20, log=print):
     """Grouped against separate matrix-core SpMMs of sibling products per
     shape and row count: us per call and the group's weight bytes per second."""
     out = {}
@@ -948,9 +948,9 @@ def main(argv=None):
                    help="measure launches that only read each Llama shape's weights in the GEMV's pattern")
     p.add_argument("--traffic-probe", action="store_true", help="run the rocprof --pmc calibration workload only")
     p.add_argument("--spmm-compare", action="store_true",
-                   help="the matrix-core SpMM beside gather + hipBLASLt at the Llama / Qwen3 shapes, 9-64 rows")
+                   help="the matrix-core SpMM beside gather + hipBLASLt at the Llama / Qwen3 shapes, 9-128 rows")
     p.add_argument("--spmm-group", action="store_true",
-                   help="grouped against separate matrix-core SpMMs of q/k/v and gate/up, Llama / Qwen3, 9-64 rows")
+                   help="grouped against separate matrix-core SpMMs of q/k/v and gate/up, Llama / Qwen3, 9-128 rows")
     p.add_argument("--pair-sweep", action="store_true",
                    help="time the decoder's gate/up pair launch under every pair configuration x split count "
                         "(Llama-3.1-8B shapes, the first --ratios entry); --csv for profiling sweep-stats")

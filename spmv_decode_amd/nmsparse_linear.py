@@ -255,7 +255,7 @@ class SiblingLaunch:
     one launch each, without any change to the model code that calls them.
 
     The first member called with a one-row input launches the grouped GEMV for
-    every member (with 9-64 rows of fp16 / bf16 on the sparse path: the
+    every member (with 9-128 rows of fp16 / bf16 on the sparse path: the
     grouped matrix-core SpMM, hip_spmv.nmsparse_spmm_group_hip) and keeps the
     other members' outputs; a member then called with the very same input
     tensor (same object, unchanged version counter) takes its output, once.
@@ -302,7 +302,7 @@ class SiblingLaunch:
     def _usable(self, x) -> bool:
         md = self.members[0].mat_data
         rows = x.numel() // x.shape[-1] if x.shape[-1] else 0
-        grouped_rows = rows == 1 or (x.dtype in (torch.float16, torch.bfloat16) and 8 < rows <= 64)
+        grouped_rows = rows == 1 or (x.dtype in (torch.float16, torch.bfloat16) and 8 < rows <= 128)
         return (x.is_cuda and x.dtype == md.dtype and x.device == md.device and x.is_contiguous() and grouped_rows
                 and all(m.mat_data.device == md.device for m in self.members))
 

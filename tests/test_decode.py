@@ -316,7 +316,8 @@ def test_graph_replay_matches_eager_and_masked_dense(gpu):
 @pytest.mark.parametrize("prompt_len", [5, 24, 70])
 def test_sparse_prefill_matches_per_token_prompt(gpu, prompt_len):
     """The sparse model's one-pass prompt (every projection through the SpMM:
-    5 rows on the small-batch kernel, 24 and 70 on the matrix cores) against
+    5 rows on the small-batch kernel, 24 on the matrix cores, 70 on gather +
+    hipBLASLt: products of at most 1024 outputs past 64 rows) against
     feeding the prompt one step at a time: last-position logits and the KV
     caches within fp16 tolerance, and the masked dense twin's prefill within
     the same tolerance; decoding after either continues with the same logits

@@ -747,10 +747,10 @@ def test_tied_siblings_against_the_oracle(gpu, monkeypatch):
 
 
 def test_tied_siblings_group_multi_row_inputs(gpu, monkeypatch):
-    """Tied siblings called with 9-64 rows of fp16 (a batch of short prompts)
+    """Tied siblings called with 9-128 rows of fp16 (a batch of short prompts)
     run as ONE grouped matrix-core SpMM: each member's output equal to the
-    grouped launch's and within the oracle bar; 2-8 rows and more than 64 rows
-    go through each member's own op."""
+    grouped launch's and within the oracle bar; 2-8 rows and more than 128
+    rows go through each member's own op."""
     from spmv_decode_amd.nmsparse_linear import NmSparseLinear, tie_siblings
     from test_spmm_gpu import check_rows
 
@@ -770,7 +770,7 @@ def test_tied_siblings_group_multi_row_inputs(gpu, monkeypatch):
     for mod, o, r in zip(mods, outs, ref):
         assert o.shape == (2, 12, mod.h) and torch.equal(o, r)
         check_rows(o.view(24, -1), x.view(24, -1), mod.mat_data, mod.mat_index, 32, 64, f"tied rows h{mod.h}")
-    for rows in (4, 70):
+    for rows in (4, 130):
         xr = torch.randn(rows, K, generator=g, device="cuda").half()
         say(f"tied siblings {rows} rows")
         for mod in mods:

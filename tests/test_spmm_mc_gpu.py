@@ -1,4 +1,4 @@
-"""GPU parity of the matrix-core SpMM (nm_spmm_mc: 9-64 rows per launch,
+"""GPU parity of the matrix-core SpMM (nm_spmm_mc: 9-128 rows per launch,
 fp16 / bf16) against the oracle, at the Llama-3.1-8B and Qwen3 shapes, on
 ragged shapes (a last chunk shorter than 32 columns, a last tile past h,
 positions outside x), every configuration and split count, groups of sibling
@@ -21,7 +21,7 @@ def mc(X, md, mi, nnz, m, **kw):
     return hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, h, nnz, m, matrix_cores=True, **kw)
 
 
-@pytest.mark.parametrize("batch", [9, 16, 24, 33, 64])
+@pytest.mark.parametrize("batch", [9, 16, 24, 33, 64, 96, 128])
 @pytest.mark.parametrize("shape", [(4096, 14336), (14336, 4096), (4096, 4096), (4096, 1024)], ids=str)
 def test_llama_shapes_default_plan(gpu, shape, batch):
     K, h = shape
@@ -50,10 +50,12 @@ def test_ragged_shapes_configs_and_splits(gpu, dtype):
     for K, h, nnz, m in RAGGED:
         _, md, mi = make_case(K, h, nnz, m, seed=K + 5 * h, dtype=dtype)
         w = md.shape[0]
-        for batch in (3, 9, 17, 40, 64):
+        for batch in (3, 9, 17, 40, 64, 100):
             X = torch.randn(batch, K, device="cuda").to(dtype)
             for cfg, splits in ((-1, 0), (0, 1), (1, 3), (2, 2), (2, 0), (0, 64), (3, 0), (3, 1), (4, 3), (4, 64),
                                 (5, 2), (5, 0)):
+                if batch > 64 and cfg in (2, 5):  # no 128-row tile of 256 columns
+                    continue
                 p = _lib.spmm_mc_plan(batch, h, w, nnz, m, cfg, splits)
                 say(f"spmm_mc {dtype} K{K} h{h} {nnz}:{m} batch {batch} cfg {cfg} splits {splits} -> {p}")
                 check_rows(mc(X, md, mi, nnz, m, config_id=cfg, splits=splits), X, md, mi, nnz, m,
@@ -74,22 +76,27 @@ def test_grouped_products_match_single_launches(gpu, dtype):
         cases = [make_case(K, h, nnz, m, seed=K + 7 * h + i, dtype=dtype) for i, h in enumerate(hs)]
         w = cases[0][1].shape[0]
         mats = [(md, mi) for _, md, mi in cases]
-        for batch in (9, 16, 33, 64):
+        for batch in (9, 16, 33, 64, 100):
             X = torch.randn(batch, K, generator=torch.Generator(device="cuda").manual_seed(batch), device="cuda")
             X = X.to(dtype)
             for cfg, splits in ((-1, 0), (0, 2), (4, 0), (5, 3), (3, 1)):
+                if batch > 64 and cfg == 5:  # no 128-row tile of 256 columns
+                    continue
                 p = _lib.spmm_mc_group_plan(batch, hs, w, nnz, m, cfg, splits)
                 say(f"spmm_mc group {dtype} K{K} h{hs} {nnz}:{m} batch {batch} cfg {cfg} splits {splits} -> {p}")
                 outs = hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, config_id=cfg, splits=splits)
+                alone = cfg < 0 and hip_spmv.library_route(batch, K, max(hs))  # each product on the library
                 for (md, mi), o in zip(mats, outs):
                     check_rows(o, X, md, mi, nnz, m, f"group {dtype} {K}x{md.shape[1]} b{batch} cfg{cfg}")
-                    assert torch.equal(o, mc(X, md, mi, nnz, m, config_id=p["config_id"], splits=p["splits"]))
+                    ref = (hip_spmv.nmsparse_spmm_forward_hip(X, md, mi, w, md.shape[1], nnz, m) if alone
+                           else mc(X, md, mi, nnz, m, config_id=p["config_id"], splits=p["splits"]))
+                    assert torch.equal(o, ref)
 
 
 def test_grouped_products_replay_and_route(gpu):
     """A captured group (split-K arrival counters of every product in one
     workspace) replayed with eager launches between, each replay equal to
-    eager; outside 9-64 rows the group helper runs each product through the
+    eager; outside 9-128 rows the group helper runs each product through the
     single-product route (the same bits)."""
     K, hs, nnz, m = 4096, [4096, 1024, 1024], 32, 64
     cases = [make_case(K, h, nnz, m, seed=300 + i) for i, h in enumerate(hs)]
@@ -115,14 +122,14 @@ def test_grouped_products_replay_and_route(gpu):
         for o, e in zip(outs, eager):
             assert torch.equal(o, e), rep
         hip_spmv.nmsparse_spmm_group_hip(X, mats, nnz, m, config_id=4, splits=2)  # eager work between replays
-    for rows in (3, 8, 65, 100):
+    for rows in (3, 8, 129, 150):
         Xr = torch.randn(rows, K, device="cuda").half()
         say(f"spmm group route {rows} rows")
         for (md, mi), o in zip(mats, hip_spmv.nmsparse_spmm_group_hip(Xr, mats, nnz, m)):
             assert torch.equal(o, hip_spmv.nmsparse_spmm_forward_hip(Xr, md, mi, md.shape[0], md.shape[1], nnz, m))
 
 
-def test_more_than_64_rows_and_determinism(gpu):
+def test_more_than_128_rows_and_determinism(gpu):
     K, h = 4096, 4096
     _, md, mi = make_case(K, h, 32, 64, seed=77)
     X = torch.randn(150, K, device="cuda").half()
@@ -131,17 +138,19 @@ def test_more_than_64_rows_and_determinism(gpu):
     check_rows(y, X, md, mi, 32, 64, "150 rows")
     for _ in range(3):
         assert torch.equal(mc(X, md, mi, 32, 64), y)
-    # the first 64 rows are one launch of their own: the same bits alone
-    assert torch.equal(mc(X[:64].contiguous(), md, mi, 32, 64), y[:64])
+    # the first 128 rows are one launch of their own: the same bits alone
+    assert torch.equal(mc(X[:128].contiguous(), md, mi, 32, 64), y[:128])
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
-def test_more_than_64_rows_gather_and_library_gemm(gpu, dtype):
-    """Past NM_MC_MAX_BATCH rows the automatic route gathers the activations
-    (nm_gather_columns) and multiplies them with mat_data in one hipBLASLt
-    GEMM: the oracle bar at Llama-3.1-8B shapes and a ragged one, and the
-    gather alone bit-exact against a PyTorch index_select."""
-    for K, h, nnz, m, rows in ((4096, 14336, 32, 64, 128), (14336, 4096, 32, 64, 96), (1000, 384, 4, 8, 200)):
+def test_past_the_matrix_core_rows_gather_and_library_gemm(gpu, dtype):
+    """Past NM_MC_MAX_BATCH rows (past 64 for products of at most 1024
+    outputs) the automatic route gathers the activations (nm_gather_columns)
+    and multiplies them with mat_data in one hipBLASLt GEMM: the oracle bar at
+    Llama-3.1-8B shapes and a ragged one, and the gather alone bit-exact
+    against a PyTorch index_select."""
+    for K, h, nnz, m, rows in ((4096, 14336, 32, 64, 160), (14336, 4096, 32, 64, 200), (4096, 1024, 32, 64, 96),
+                               (1000, 384, 4, 8, 200)):
         _, md, mi = make_case(K, h, nnz, m, seed=K + rows, dtype=dtype)
         w = md.shape[0]
         X = torch.randn(rows, K, device="cuda").to(dtype)
@@ -158,14 +167,16 @@ def test_more_than_64_rows_gather_and_library_gemm(gpu, dtype):
         assert bool((xg[:, w:] == 0).all())
 
 
-def test_automatic_route_keeps_the_matrix_cores_up_to_64_rows(gpu):
-    """hip_spmv.library_route: up to 64 rows every shape, the wide gate/up
-    products included, runs on the matrix-core kernel (the same bits as
-    forcing it); past 64 rows the activations are gathered and multiplied on
-    hipBLASLt (the same bits as the explicit gather + GEMM). Both within the
-    oracle bar."""
+def test_automatic_route_keeps_the_matrix_cores_up_to_128_rows(gpu):
+    """hip_spmv.library_route: up to 64 rows every shape, and up to 128 rows
+    every shape of more than 1024 outputs, runs on the matrix-core kernel (the
+    same bits as forcing it); past that the activations are gathered and
+    multiplied on hipBLASLt (the same bits as the explicit gather + GEMM).
+    Both within the oracle bar."""
     for K, h, rows, routed in ((4096, 14336, 32, False), (4096, 14336, 64, False), (5120, 17408, 40, False),
-                               (4096, 4096, 32, False), (14336, 4096, 64, False), (4096, 14336, 65, True)):
+                               (4096, 4096, 32, False), (14336, 4096, 64, False), (4096, 14336, 65, False),
+                               (14336, 4096, 128, False), (4096, 1024, 64, False), (4096, 1024, 65, True),
+                               (4096, 14336, 129, True)):
         assert hip_spmv.library_route(rows, K, h) == routed, (K, h, rows)
         _, md, mi = make_case(K, h, 32, 64, seed=K + h + rows)
         w = md.shape[0]
