@@ -20,11 +20,13 @@ dense F.linear as in the reference; without one the reference raises
 "prefill requires dense weight", and so does a [B, 1, K] input (the op
 rejects rows != 1), where this build computes them with the small-batch SpMM
 (`torch.ops.nmsparse.spmm`). NM_SPARSE_BATCH=0 restores the reference's
-errors; NM_SPARSE_BATCH=1 also sends inputs of up to 64 rows to the SpMM when
-a dense weight is present. NM_SYNTH_INIT=device (this build only) draws the
-synthetic weights with a seeded on-device generator instead of the CPU
-stream — same distribution and shapes, much faster for 8B+ models, NOT
-bit-exact with the reference; the default is the bit-exact CPU stream.
+errors; NM_SPARSE_BATCH=1 also sends inputs of up to 128 rows to the SpMM when
+a dense weight is present (the matrix-core SpMM's row limit; at the
+Llama-3.1-8B shapes it is faster there than hipBLASLt on the dense weight).
+NM_SYNTH_INIT=device (this build only) draws the synthetic weights with a
+seeded on-device generator instead of the CPU stream — same distribution and
+shapes, much faster for 8B+ models, NOT bit-exact with the reference; the
+default is the bit-exact CPU stream.
 
 Beyond the reference: `NmSparseLinear.from_dense` / `pack_dense` build the
 packed buffers from a real dense weight and a shared N:M mask (a pure gather);
@@ -52,7 +54,7 @@ WEIGHT_CPU = os.environ.get("NM_WEIGHT_CPU", "0") == "1" or DECODE_ONLY
 SPARSE_BATCH = os.environ.get("NM_SPARSE_BATCH", "auto")
 if SPARSE_BATCH not in ("auto", "0", "1"):
     raise ValueError(f"Unknown NM_SPARSE_BATCH={SPARSE_BATCH!r}; use auto, 0 or 1")
-SPARSE_BATCH_MAX_ROWS = 64
+SPARSE_BATCH_MAX_ROWS = 128
 SYNTH_INIT = os.environ.get("NM_SYNTH_INIT", "reference")
 if SYNTH_INIT not in ("reference", "device"):
     raise ValueError(f"Unknown NM_SYNTH_INIT={SYNTH_INIT!r}; use 'reference' or 'device'")
