@@ -360,6 +360,8 @@ def nmsparse_spmm_group_hip(x, mats, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, confi
     hs = [int(md.shape[1]) for md, _ in mats]
     if outs is None:
         outs = [None] * len(mats)
+    elif len(outs) != len(mats):
+        raise ValueError(f"{len(outs)} outputs for {len(mats)} products")
     explicit = config_id >= 0 or splits > 0  # a matrix-core plan named by the caller
     grouped = (x.dtype in (torch.float16, torch.bfloat16) and _lib.NM_MAX_BATCH < rows <= _lib.NM_MC_MAX_BATCH
                and (explicit or not library_route(rows, K, max(hs))) and 1 < len(mats) <= _lib.NM_MC_MAX_GROUP
