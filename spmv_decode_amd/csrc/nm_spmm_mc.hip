@@ -631,7 +631,8 @@ struct McPlan {
 };
 
 // Plan, fitted to graph-replay sweeps of the DMA configurations x 1-8 splits
-// at the Llama-3.1-8B, Qwen3-14B and Qwen3-32B shapes, 16 / 32 / 64 rows.
+// at the Llama-3.1-8B, Qwen3-14B and Qwen3-32B shapes, 16 / 32 / 64 rows (and the
+// Llama-3.1-8B shapes at 96 / 128 rows).
 // Up to 1024 outputs: register-staged 64-column tiles, about one workgroup
 // per CU (256 / tiles splits, at most 8). Otherwise the DMA-staged tile width
 // and split count are chosen together: the grid of the most workgroups that
@@ -640,7 +641,8 @@ struct McPlan {
 //  * splits of at most 2560 compressed rows (deep K runs slower per split);
 //  * up to 16 rows: 64-column tiles, then 128, then 256;
 //  * past 16 rows: fewer splits (their partials, [splits, batch, h] fp32,
-//    grow with the rows), then 128-, 64-, 256-column tiles;
+//    grow with the rows), then 128-, 64-, 256-column tiles (past 64 rows:
+//    64-column tiles first, 1-4% faster at 96-128 rows; no 256-column tile);
 // and past 32 rows a plan whose partials would reach a quarter of the weight
 // bytes gives way to the widest grid without splits, when that has at least
 // half its workgroups. Each split is whole chunks of 64 columns. Workspace:
@@ -691,8 +693,8 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
     // search the DMA configurations (or the given one) x split counts (or the given one)
     const int c_lo = cfg < 0 ? 3 : cfg, c_hi = cfg < 0 ? 5 : cfg;
     const int s_lo = splits > 0 ? splits : 1, s_hi = splits > 0 ? splits : 8;
-    const int pref_small[3] = {0, 1, 2};  // ranks of HT = 64, 128, 256 up to 16 rows (lower is better)
-    const int pref_large[3] = {1, 0, 2};  // past 16 rows
+    const int pref_small[3] = {0, 1, 2};  // ranks of HT = 64, 128, 256 up to 16 rows and past 64 (lower is better)
+    const int pref_large[3] = {1, 0, 2};  // 17-64 rows
     int best_c = -1, best_s = 0, best_b = 0, best_r = 0, free_c = -1, free_b = 0;
     auto better = [&](int c, int sp, int b, int r) {
       if (best_c < 0) return true;
@@ -703,7 +705,7 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
       const bool deep = r > 2560, best_deep = best_r > 2560;
       if (deep != best_deep) return !deep;
       if (batch > 16 && sp != best_s) return sp < best_s;
-      const int* pref = batch > 16 ? pref_large : pref_small;
+      const int* pref = batch > 16 && batch <= 64 ? pref_large : pref_small;
       return pref[c - 3] < pref[best_c - 3];
     };
     for (int c = c_lo; c <= c_hi; ++c)
