@@ -261,21 +261,29 @@ def test_split_k_handoff_soak_500_replays(gpu):
     """The matrix-core SpMM's split-K handoff (agent-scope atomic-store
     publish, ticket, ordered partial reads) under repetition: gate/up, down
     and q/o at the Llama-3.1-8B shapes with 48 rows (2-4 splits, 224-256
-    workgroups) in one hipGraph, replayed 500 times, every replay bitwise
-    equal to the first, stopping at the first mismatch."""
+    workgroups), a grouped q/k/v launch (3 products' counters in one
+    workspace, 2 splits) and down at 128 rows (4 splits) in one hipGraph,
+    replayed 500 times, every replay bitwise equal to the first, stopping at
+    the first mismatch."""
     cases = []
-    # (K, h, config, splits): gate/up on the 128-column DMA tiles with 2 splits (its default plan at 48 rows
-    # has none), down and q/o on their default plans (4 splits each)
-    for i, (K, h, cfg, splits) in enumerate(((4096, 14336, 4, 2), (14336, 4096, -1, 0), (4096, 4096, -1, 0))):
+    # (K, h, config, splits, rows): gate/up on the 128-column DMA tiles with 2 splits (its default plan at 48
+    # rows has none), down and q/o on their default plans (4 splits each)
+    for i, (K, h, cfg, splits, rows) in enumerate(((4096, 14336, 4, 2, 48), (14336, 4096, -1, 0, 48),
+                                                   (4096, 4096, -1, 0, 48), (14336, 4096, -1, 0, 128))):
         _, md, mi = make_case(K, h, 32, 64, seed=90 + i)
-        X = torch.randn(48, K, device="cuda").half()
-        p = _lib.spmm_mc_plan(48, h, md.shape[0], 32, 64, cfg, splits)
+        X = torch.randn(rows, K, device="cuda").half()
+        p = _lib.spmm_mc_plan(rows, h, md.shape[0], 32, 64, cfg, splits)
         assert p["splits"] > 1, p
-        cases.append((X, md, mi, torch.empty(48, h, dtype=torch.float16, device="cuda"), cfg, splits))
+        cases.append((X, md, mi, torch.empty(rows, h, dtype=torch.float16, device="cuda"), cfg, splits))
+    qkv = [make_case(4096, h, 32, 64, seed=95 + i)[1:] for i, h in enumerate((4096, 1024, 1024))]
+    Xq = torch.randn(48, 4096, device="cuda").half()
+    assert _lib.spmm_mc_group_plan(48, [4096, 1024, 1024], 2048, 32, 64, 3, 2)["splits"] == 2
+    qkv_outs = [torch.empty(48, md.shape[1], dtype=torch.float16, device="cuda") for md, _ in qkv]
 
     def launches():
         for X, md, mi, out, cfg, splits in cases:
             mc(X, md, mi, 32, 64, out=out, config_id=cfg, splits=splits)
+        hip_spmv.nmsparse_spmm_group_hip(Xq, qkv, 32, 64, outs=qkv_outs, config_id=3, splits=2)
 
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
@@ -289,10 +297,17 @@ def test_split_k_handoff_soak_500_replays(gpu):
     g.replay()
     torch.cuda.synchronize()
     first = [c[3].clone() for c in cases]
+    first_qkv = [o.clone() for o in qkv_outs]
     check_rows(first[0], cases[0][0], cases[0][1], cases[0][2], 32, 64, "soak gate/up")
+    check_rows(first[3], cases[3][0], cases[3][1], cases[3][2], 32, 64, "soak down 128 rows")
+    for (md, mi), o in zip(qkv, first_qkv):
+        check_rows(o, Xq, md, mi, 32, 64, "soak grouped q/k/v")
     for rep in range(1, 500):
         g.replay()
         torch.cuda.synchronize()
         for k, c in enumerate(cases):
             if not torch.equal(c[3], first[k]):
                 pytest.fail(f"replay {rep}: case {k} differs from the first replay")
+        for k, o in enumerate(qkv_outs):
+            if not torch.equal(o, first_qkv[k]):
+                pytest.fail(f"replay {rep}: grouped product {k} differs from the first replay")
