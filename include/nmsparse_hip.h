@@ -358,6 +358,20 @@ int nm_spmm_mc_plan(int batch, int h, int w, int nnz, int m, int config_id, int 
                     int* out_splits, int* out_blocks, int* out_rows_per_block);
 
 /*
+ * The matrix-core SpMM of round(silu(gate) * up): nm_spmm_mc whose
+ * activations are formed from the gate and up projections' outputs (rows
+ * x_row_stride apart in both) at the gathered positions, in fp32 with one
+ * rounding to the element type, as the GEMV gate/up pair's epilogue. The
+ * workspace is nm_spmm_mc_workspace_bytes'. No reference counterpart (the
+ * reference forms F.silu(w1(x)) * w3(x) in PyTorch before w2, model.py:255-256,
+ * for one row at a time).
+ */
+int nm_spmm_mc_silu_mul(int dtype, const void* gate, const void* up, long long x_row_stride, int batch,
+                        const void* mat_data, const uint8_t* mat_index, void* out, long long out_row_stride,
+                        void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m, int config_id,
+                        int splits, void* stream);
+
+/*
  * Several matrix-core SpMMs of the same activations in one grid: product i
  * (0 <= i < n <= NM_MC_MAX_GROUP) is out[i] = mat_data[i] / mat_index[i]
  * applied to every row of x, h[i] outputs, out rows out_row_stride[i] apart;

@@ -86,6 +86,7 @@ ABI = {
     "nm_spmm_mc_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i]),
     "nm_spmm_mc": (_i, [_i, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_spmm_mc_plan": (_i, [_i, _i, _i, _i, _i, _i, _i, _ip, _ip, _ip, _ip]),
+    "nm_spmm_mc_silu_mul": (_i, [_i, _vp, _vp, _ll, _i, _vp, _vp, _vp, _ll, _vp, _sz, _i, _i, _i, _i, _i, _i, _vp]),
     "nm_spmm_mc_group_workspace_bytes": (_sz, [_i, _i, _ip, _i, _i, _i, _i, _i]),
     "nm_spmm_mc_group": (_i, [_i, _vp, _ll, _i, _i, ctypes.POINTER(_vp), ctypes.POINTER(_vp), ctypes.POINTER(_vp),
                               ctypes.POINTER(_ll), _ip, _vp, _sz, _i, _i, _i, _i, _i, _vp]),
@@ -97,7 +98,7 @@ ABI = {
     "nm_abi_version": (_i, []),
     "nm_stream_capture_id": (_i, [_vp, ctypes.POINTER(ctypes.c_ulonglong)]),
 }
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _lib = None
 _lock = threading.Lock()

@@ -44,7 +44,7 @@ constexpr int kBlock = 256;        // lanes per workgroup
 constexpr int kVec = 8;            // output rows per lane
 constexpr int kMaxRows = 2048;     // compressed columns per split (LDS gather bound)
 constexpr int kMaxTickets = NM_TICKET_BYTES / 4;
-constexpr int kAbiVersion = 11;
+constexpr int kAbiVersion = 12;
 
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));

@@ -532,10 +532,14 @@ __global__ __launch_bounds__(kBlock) void nm_spmm_mc_group_kernel(McGroupArgs g)
 // or in the matrix-core kernel's operand order (FRAG = true: lane i fills
 // 16-B slot i of the fragments described at nm_spmm_mc_kernel's load_a; wp
 // a multiple of 64; rbk row blocks of 16 rows).
-template <bool FRAG>
+// SDT >= 0 (an element type): the activations are round_SDT(silu(x) * x2)
+// of two inputs with the same row stride, computed in fp32 as the gate/up
+// pair's epilogue does, only at the gathered positions.
+template <bool FRAG, int SDT = -1>
 __device__ __forceinline__ void gather_slot(const uint16_t* __restrict__ x, long long x_row_stride, int batch,
                                             const uint8_t* __restrict__ mat_index, int w, int wp, int nnz, int m,
-                                            int K, int rbk, uint16_t* __restrict__ xg) {
+                                            int K, int rbk, uint16_t* __restrict__ xg,
+                                            const uint16_t* __restrict__ x2 = nullptr) {
   const int per_row = wp / 8;  // rows * per_row < 2^31 (host)
   const int i = (int)blockIdx.x * kBlock + (int)threadIdx.x;
   if (i >= (FRAG ? 16 * rbk : batch) * per_row) return;
@@ -557,7 +561,12 @@ __device__ __forceinline__ void gather_slot(const uint16_t* __restrict__ x, long
     const int c = c0 + e;
     const int cc = c < w ? c : w - 1;  // clamped: the load stays in range
     const int p = (cc / nnz) * m + (int)mat_index[cc];
-    const uint16_t t = xr[p < K ? p : 0];
+    uint16_t t = xr[p < K ? p : 0];
+    if constexpr (SDT >= 0) {
+      using E = Elem<SDT>;
+      const uint16_t u = x2[(long long)(row_ok ? b : 0) * x_row_stride + (p < K ? p : 0)];
+      t = E::from_f32(silu(E::to_f32(t)) * E::to_f32(u));
+    }
     v[e] = (row_ok && c < w && p < K) ? t : (uint16_t)0;
   }
   u32x4 word;
@@ -574,6 +583,17 @@ __global__ __launch_bounds__(kBlock) void nm_gather_mc_kernel(const uint16_t* __
                                                             int wp, int nnz, int m, int K, int rbk,
                                                             uint16_t* __restrict__ xg) {
   gather_slot<FRAG>(x, x_row_stride, batch, mat_index, w, wp, nnz, m, K, rbk, xg);
+}
+
+// The operand-order gather of round_SDT(silu(gate) * up).
+template <int SDT>
+__global__ __launch_bounds__(kBlock) void nm_gather_mc_silu_kernel(const uint16_t* __restrict__ gate,
+                                                                 const uint16_t* __restrict__ up,
+                                                                 long long x_row_stride, int batch,
+                                                                 const uint8_t* __restrict__ mat_index, int w,
+                                                                 int wp, int nnz, int m, int K, int rbk,
+                                                                 uint16_t* __restrict__ xg) {
+  gather_slot<true, SDT>(gate, x_row_stride, batch, mat_index, w, wp, nnz, m, K, rbk, xg, up);
 }
 
 // The operand-order gathers of a group's products, product blockIdx.y each.
@@ -750,6 +770,64 @@ int make_mc_plan(int batch, int h, int w, int nnz, int m, int cfg, int splits, M
   return make_mc_plan(batch, 1, &h, w, nnz, m, cfg, splits, p);
 }
 
+// nm_spmm_mc, and with x2 (the up projection's output, rows x_row_stride
+// apart like x) nm_spmm_mc_silu_mul: the gather then forms round_T(silu(x)
+// * x2) at the gathered positions.
+int spmm_mc_run(int dtype, const void* x, const void* x2, long long x_row_stride, int batch, const void* mat_data,
+                const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace,
+                size_t workspace_bytes, int h, int w, int nnz, int m, int config_id, int splits, void* stream) {
+  if (dtype != NM_DTYPE_F16 && dtype != NM_DTYPE_BF16) return NM_ERR_BAD_CONFIG;
+  McPlan p;
+  const int rc = make_mc_plan(batch, h, w, nnz, m, config_id, splits, &p);
+  if (rc != NM_OK) return rc;
+  if (!x || !mat_data || !mat_index || !out || !workspace) return NM_ERR_NULL_POINTER;
+  const long long K = (long long)(w / nnz) * (long long)m;
+  if (x_row_stride < K || out_row_stride < h) return NM_ERR_BAD_SHAPE;
+  if (((uintptr_t)mat_data & 15u) != 0 || ((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
+  if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  void* xg = static_cast<char*>(workspace) + p.xg_off;
+  const int rbk = ceil_div_mc(batch, 16);  // row blocks of 16 stored (operand order, zero rows past the batch)
+  const long long gathered = (long long)16 * rbk * (long long)(p.wp / 8);
+  const unsigned gblocks = (unsigned)((gathered + kBlock - 1) / kBlock);
+  if (!x2)
+    hipLaunchKernelGGL(nm_gather_mc_kernel<true>, dim3(gblocks), dim3(kBlock), 0, st,
+                       static_cast<const uint16_t*>(x), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K,
+                       rbk, static_cast<uint16_t*>(xg));  // fp16 and bf16 alike: a copy of 16-bit words
+  else
+    hipLaunchKernelGGL(dtype == NM_DTYPE_F16 ? nm_gather_mc_silu_kernel<NM_DTYPE_F16>
+                                             : nm_gather_mc_silu_kernel<NM_DTYPE_BF16>,
+                       dim3(gblocks), dim3(kBlock), 0, st, static_cast<const uint16_t*>(x),
+                       static_cast<const uint16_t*>(x2), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K,
+                       rbk, static_cast<uint16_t*>(xg));
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return (int)e;
+  SpmmArgs a;
+  memset(&a, 0, sizeof(a));
+  a.x = xg;
+  a.x_row_stride = rbk;  // operand-order activations: the row blocks stored
+  a.mat_data = mat_data;
+  a.mat_index = mat_index;
+  a.out = out;
+  a.out_row_stride = out_row_stride;
+  a.tickets = static_cast<uint32_t*>(workspace);
+  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + NM_TICKET_BYTES);
+  a.batch = batch;
+  a.h = h;
+  a.tiles = p.tiles;
+  a.w = w;
+  a.nnz = nnz;
+  a.m = m;
+  a.K = (int)K;
+  a.splits = p.splits;
+  a.rows_per_split = p.rows;
+  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : (batch <= 64 ? 2 : 3));
+  const McFn fn = (dtype == NM_DTYPE_F16 ? kMcKernelsF16 : kMcKernelsBF16)[p.cfg][bt];
+  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, a);
+  e = hipGetLastError();
+  return e == hipSuccess ? NM_OK : (int)e;
+}
+
 }  // namespace
 }  // namespace nm_hip
 
@@ -797,49 +875,17 @@ int nm_gather_columns(int dtype, const void* x, long long x_row_stride, int rows
 int nm_spmm_mc(int dtype, const void* x, long long x_row_stride, int batch, const void* mat_data,
                const uint8_t* mat_index, void* out, long long out_row_stride, void* workspace, size_t workspace_bytes,
                int h, int w, int nnz, int m, int config_id, int splits, void* stream) {
-  if (dtype != NM_DTYPE_F16 && dtype != NM_DTYPE_BF16) return NM_ERR_BAD_CONFIG;
-  McPlan p;
-  const int rc = make_mc_plan(batch, h, w, nnz, m, config_id, splits, &p);
-  if (rc != NM_OK) return rc;
-  if (!x || !mat_data || !mat_index || !out || !workspace) return NM_ERR_NULL_POINTER;
-  const long long K = (long long)(w / nnz) * (long long)m;
-  if (x_row_stride < K || out_row_stride < h) return NM_ERR_BAD_SHAPE;
-  if (((uintptr_t)mat_data & 15u) != 0 || ((uintptr_t)workspace & 255u) != 0) return NM_ERR_MISALIGNED;
-  if (workspace_bytes < p.workspace) return NM_ERR_WORKSPACE;
-  hipStream_t st = static_cast<hipStream_t>(stream);
-  void* xg = static_cast<char*>(workspace) + p.xg_off;
-  const int rbk = ceil_div_mc(batch, 16);  // row blocks of 16 stored (operand order, zero rows past the batch)
-  const long long gathered = (long long)16 * rbk * (long long)(p.wp / 8);
-  const unsigned gblocks = (unsigned)((gathered + kBlock - 1) / kBlock);
-  hipLaunchKernelGGL(nm_gather_mc_kernel<true>, dim3(gblocks), dim3(kBlock), 0, st,
-                     static_cast<const uint16_t*>(x), x_row_stride, batch, mat_index, w, p.wp, nnz, m, (int)K, rbk,
-                     static_cast<uint16_t*>(xg));  // fp16 and bf16 alike: a copy of 16-bit words
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return (int)e;
-  SpmmArgs a;
-  memset(&a, 0, sizeof(a));
-  a.x = xg;
-  a.x_row_stride = rbk;  // operand-order activations: the row blocks stored
-  a.mat_data = mat_data;
-  a.mat_index = mat_index;
-  a.out = out;
-  a.out_row_stride = out_row_stride;
-  a.tickets = static_cast<uint32_t*>(workspace);
-  a.partial = reinterpret_cast<float*>(static_cast<char*>(workspace) + NM_TICKET_BYTES);
-  a.batch = batch;
-  a.h = h;
-  a.tiles = p.tiles;
-  a.w = w;
-  a.nnz = nnz;
-  a.m = m;
-  a.K = (int)K;
-  a.splits = p.splits;
-  a.rows_per_split = p.rows;
-  const int bt = batch <= 16 ? 0 : (batch <= 32 ? 1 : (batch <= 64 ? 2 : 3));
-  const McFn fn = (dtype == NM_DTYPE_F16 ? kMcKernelsF16 : kMcKernelsBF16)[p.cfg][bt];
-  hipLaunchKernelGGL(fn, dim3(p.blocks), dim3(kBlock), 0, st, a);
-  e = hipGetLastError();
-  return e == hipSuccess ? NM_OK : (int)e;
+  return spmm_mc_run(dtype, x, nullptr, x_row_stride, batch, mat_data, mat_index, out, out_row_stride, workspace,
+                     workspace_bytes, h, w, nnz, m, config_id, splits, stream);
+}
+
+int nm_spmm_mc_silu_mul(int dtype, const void* gate, const void* up, long long x_row_stride, int batch,
+                        const void* mat_data, const uint8_t* mat_index, void* out, long long out_row_stride,
+                        void* workspace, size_t workspace_bytes, int h, int w, int nnz, int m, int config_id,
+                        int splits, void* stream) {
+  if (!up) return NM_ERR_NULL_POINTER;
+  return spmm_mc_run(dtype, gate, up, x_row_stride, batch, mat_data, mat_index, out, out_row_stride, workspace,
+                     workspace_bytes, h, w, nnz, m, config_id, splits, stream);
 }
 
 size_t nm_spmm_mc_group_workspace_bytes(int batch, int n, const int* h, int w, int nnz, int m, int config_id,

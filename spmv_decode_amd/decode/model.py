@@ -249,6 +249,21 @@ def project_rows_group(lins, x2d: torch.Tensor) -> list:
     return [project_rows(l, x2d) for l in lins]
 
 
+def project_rows_silu_mul(lin: nn.Module, gate: torch.Tensor, up: torch.Tensor) -> torch.Tensor:
+    """project_rows(lin, silu(gate) * up): an NmSparseLinear forms the SiLU
+    product inside its SpMM's activation gather (hip_spmv.
+    nmsparse_spmm_silu_mul_hip: in fp32 with one rounding, as the decode
+    steps' gate/up pair does), any other module gets F.silu(gate) * up."""
+    from ..nmsparse_linear import NmSparseLinear
+
+    if isinstance(lin, NmSparseLinear) and lin.mat_data.dtype == gate.dtype:
+        from ..hip_spmv import nmsparse_spmm_silu_mul_hip
+
+        return nmsparse_spmm_silu_mul_hip(gate, up, lin.mat_data, lin.mat_index, lin.w, lin.h, lin.block_width,
+                                          lin.vec_width)
+    return project_rows(lin, F.silu(gate) * up)
+
+
 def causal_attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, n_kv_heads: int) -> torch.Tensor:
     """softmax(q kᵀ / sqrt(d) + causal mask) v over P positions, grouped query
     heads: q [P, n_heads, d], k and v [P, kv_heads, d] -> [P, n_heads * d].
@@ -901,8 +916,7 @@ class Decoder(nn.Module):
             x = x + project_rows(o_proj, causal_attention(q, k, v, c.n_kv_heads))
             h = ln2(x)
             g_out, u_out = project_rows_group((gate, up), h)
-            act = F.silu(g_out) * u_out
-            x = x + project_rows(down, act)
+            x = x + project_rows_silu_mul(down, g_out, u_out)
         return project(self.lm_head, self.norm(x[-1:].view(1, 1, -1))).view(1, -1)
 
     def forward_step(self, token: torch.Tensor, pos: torch.Tensor) -> torch.Tensor:

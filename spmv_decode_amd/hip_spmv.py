@@ -335,6 +335,60 @@ def nmsparse_spmm_forward_hip(x, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WID
     return out
 
 
+def nmsparse_spmm_silu_mul_hip(gate, up, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, *, out=None,
+                               config_id=-1, splits=0):
+    """W applied to every row of round(silu(gate) * up) (the down projection
+    of a SwiGLU MLP; gate and up [..., rows, K] of one 16-bit dtype): from 9 to
+    NM_MC_MAX_BATCH rows on the matrix cores with the SiLU product formed at
+    the gathered positions inside the activation gather (nm_spmm_mc_silu_mul:
+    no separate SiLU and multiply launches, one rounding, like the GEMV
+    gate/up pair's epilogue), otherwise the product formed in fp32 with one
+    rounding and then nmsparse_spmm_forward_hip. Returns [..., rows, h]."""
+    if gate.shape != up.shape or gate.dtype != up.dtype or gate.device != up.device:
+        raise ValueError("gate and up must have one shape, dtype and device")
+    K = gate.shape[-1]
+    rows = gate.numel() // K if K else 0
+    explicit = config_id >= 0 or splits > 0
+    fused = (gate.dtype in (torch.float16, torch.bfloat16) and gate.is_cuda and _lib.NM_MAX_BATCH < rows
+             <= _lib.NM_MC_MAX_BATCH and (explicit or not library_route(rows, K, h)))
+    if not fused:
+        act = (torch.nn.functional.silu(gate.float()) * up.float()).to(gate.dtype)
+        return nmsparse_spmm_forward_hip(act, mat_data, mat_index, w, h, BLOCK_WIDTH, VEC_WIDTH, out=out,
+                                         config_id=config_id, splits=splits)
+    if not (mat_data.is_cuda and mat_index.is_cuda) or mat_data.device != gate.device:
+        raise ValueError("gate, up, mat_data, and mat_index must be GPU (HIP) tensors on one device")
+    if mat_data.dtype != gate.dtype:
+        raise TypeError("x and mat_data must have same dtype")
+    if mat_index.dtype != torch.uint8:
+        raise TypeError("mat_index must be uint8")
+    if w % BLOCK_WIDTH != 0 or K != (w // BLOCK_WIDTH) * VEC_WIDTH:
+        raise ValueError(f"x has {K} columns; w={w}, N={BLOCK_WIDTH}, M={VEC_WIDTH} need {w // BLOCK_WIDTH * VEC_WIDTH}")
+    if tuple(mat_data.shape) != (w, h) or not mat_data.is_contiguous():
+        raise ValueError(f"mat_data must be a contiguous {(w, h)} tensor, got {tuple(mat_data.shape)}")
+    if tuple(mat_index.shape) != (w // BLOCK_WIDTH, BLOCK_WIDTH) or not mat_index.is_contiguous():
+        raise ValueError(f"mat_index must be a contiguous {(w // BLOCK_WIDTH, BLOCK_WIDTH)} tensor")
+    lead = gate.shape[:-1]
+    g2d, u2d = gate.reshape(-1, K).contiguous(), up.reshape(-1, K).contiguous()
+    if out is None:
+        out = torch.empty(*lead, h, dtype=gate.dtype, device=gate.device)
+    elif (out.dtype != gate.dtype or tuple(out.shape) != (*lead, h) or not out.is_contiguous()
+          or out.device != gate.device or out.data_ptr() % 16):
+        raise ValueError(f"out must be a contiguous, 16-byte aligned {(*lead, h)} tensor of x.dtype")
+    md = _aligned(mat_data)
+    lib = _lib.load()
+    need = lib.nm_spmm_mc_workspace_bytes(rows, h, w, BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits))
+    if need == 0:
+        raise ValueError("spmm shape outside what libnmsparse_hip supports")
+    with torch.cuda.device(gate.device):
+        stream = torch.cuda.current_stream(gate.device).cuda_stream
+        ws = workspace_for(gate.device, need, stream)
+        rc = lib.nm_spmm_mc_silu_mul(_DTYPE_CODE[gate.dtype], g2d.data_ptr(), u2d.data_ptr(), K, rows, md.data_ptr(),
+                                     mat_index.data_ptr(), out.data_ptr(), h, ws.data_ptr(), ws.numel(), h, w,
+                                     BLOCK_WIDTH, VEC_WIDTH, int(config_id), int(splits), stream)
+        _lib.check(rc, "nm_spmm_mc_silu_mul")
+    return out
+
+
 def nmsparse_spmm_group_hip(x, mats, BLOCK_WIDTH, VEC_WIDTH, *, outs=None, config_id=-1, splits=0):
     """[W_i x[..., r, :] for every row r] for the products mats = [(mat_data,
     mat_index), ...] of one input (sibling Linears: q/k/v, gate/up), each as

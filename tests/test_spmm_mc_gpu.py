@@ -129,6 +129,42 @@ def test_grouped_products_replay_and_route(gpu):
             assert torch.equal(o, hip_spmv.nmsparse_spmm_forward_hip(Xr, md, mi, md.shape[0], md.shape[1], nnz, m))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=str)
+def test_silu_product_formed_in_the_gather(gpu, dtype):
+    """nm_spmm_mc_silu_mul (the down projection of round(silu(gate) * up),
+    the product formed at the gathered positions in fp32): within the oracle
+    bar of the product formed in float64 and rounded to the element type (the
+    kernel's SiLU, on the hardware's exp2 and reciprocal, is within about an
+    ulp of fp32 before that rounding), at the Llama-3.1-8B down shape and a
+    ragged one, 9-128 rows, default and forced plans; outside its rows (and
+    where the automatic route takes the library) the helper forms the product
+    in fp32 with one rounding and takes the single-product route (the same
+    bits)."""
+    for K, h, nnz, m in ((14336, 4096, 32, 64), (1000, 384, 4, 8)):
+        _, md, mi = make_case(K, h, nnz, m, seed=K + 11 * h, dtype=dtype)
+        w = md.shape[0]
+        for rows in (9, 40, 100, 128):
+            g = torch.Generator(device="cuda").manual_seed(rows)
+            gate = torch.randn(rows, K, generator=g, device="cuda").to(dtype)
+            up = torch.randn(rows, K, generator=g, device="cuda").to(dtype)
+            act = (torch.nn.functional.silu(gate.double()) * up.double()).to(dtype)
+            act32 = (torch.nn.functional.silu(gate.float()) * up.float()).to(dtype)
+            for cfg, splits in ((-1, 0), (3, 2), (0, 1)):
+                say(f"spmm silu product {dtype} K{K} h{h} {nnz}:{m} rows {rows} cfg {cfg} splits {splits}")
+                out = hip_spmv.nmsparse_spmm_silu_mul_hip(gate, up, md, mi, w, h, nnz, m, config_id=cfg,
+                                                          splits=splits)
+                if cfg < 0 and hip_spmv.library_route(rows, K, h):  # the product in fp32, then the library
+                    assert torch.equal(out, hip_spmv.nmsparse_spmm_forward_hip(act32, md, mi, w, h, nnz, m))
+                    continue
+                check_rows(out, act, md, mi, nnz, m, f"silu product {dtype} {K}x{h} rows {rows} cfg {cfg}")
+        for rows in (4, 200):
+            gate = torch.randn(rows, K, device="cuda").to(dtype)
+            up = torch.randn(rows, K, device="cuda").to(dtype)
+            act = (torch.nn.functional.silu(gate.float()) * up.float()).to(dtype)
+            assert torch.equal(hip_spmv.nmsparse_spmm_silu_mul_hip(gate, up, md, mi, w, h, nnz, m),
+                               hip_spmv.nmsparse_spmm_forward_hip(act, md, mi, w, h, nnz, m))
+
+
 def test_more_than_128_rows_and_determinism(gpu):
     K, h = 4096, 4096
     _, md, mi = make_case(K, h, 32, 64, seed=77)
