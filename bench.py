@@ -578,7 +578,7 @@ def decode_ms_per_token(m, log):
     eager and compiled."""
     import torch
 
-    from spmv_decode_amd.decode.bench_decode import linear_bytes, run_variant
+    from spmv_decode_amd.decode.bench_decode import linear_bytes, prefill_ms, run_variant
     from spmv_decode_amd.decode.model import LLAMA31_8B, Decoder, init_weights_
     from spmv_decode_amd.decode.runner import fixed_context_logits_fp32, fixed_context_ms, logits_envelope
     from spmv_decode_amd.nmsparse_linear import swap_to_nmsparse
@@ -621,34 +621,6 @@ def decode_ms_per_token(m, log):
             model.forward_step = eager
             torch._dynamo.reset()
 
-    def prefill_ms(model, reps=10):
-        """The prompt's GPU time in one Decoder.prefill pass (every Linear over its 128 rows: hipBLASLt on the
-        dense weights for the dense model; for the sparse one the matrix-core SpMM, q/k/v and gate/up grouped),
-        captured as a hipGraph after an eager warm-up; median of reps replays."""
-        from spmv_decode_amd.decode.runner import cache_length
-
-        model.setup_cache(cache_length(prompt.numel() + 1), torch.device("cuda"), dtype=torch.float16)
-        ids = prompt.cuda()
-        st = torch.cuda.Stream()
-        st.wait_stream(torch.cuda.current_stream())
-        with torch.cuda.stream(st):
-            model.prefill(ids)
-        torch.cuda.current_stream().wait_stream(st)
-        torch.cuda.synchronize()
-        g = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(g, stream=st):
-            model.prefill(ids)
-        times = []
-        for _ in range(reps):
-            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-            a.record()
-            g.replay()
-            b.record()
-            b.synchronize()
-            times.append(a.elapsed_time(b))
-        del g
-        return round(sorted(times)[len(times) // 2], 4)
-
     dense_by_fusion, forms, fixed_dense, fixed_dense_c = {}, {}, {}, {}
     ref32_dense = fixed_context_logits_fp32(model, 512)  # the dense step in fp32: the envelope's reference
     for mode in ("qkv", "none", "qkv_gate_up"):  # "qkv": the reference's dense model (model.py:198 wqkv)
@@ -659,10 +631,10 @@ def decode_ms_per_token(m, log):
         fixed_dense_c[mode] = compiled_fixed(model, fixed_dense[mode], ref32_dense, f"dense ({mode} fused)")
     model.set_dense_fusion("none")
     dense = dense_by_fusion["qkv"]
-    prefill_dense = prefill_ms(model)
+    prefill_dense = prefill_ms(model, prompt)
     swap_to_nmsparse(model, m, "cuda", seed=0, init="device", keep_dense=False)
     torch.cuda.empty_cache()
-    prefill_sparse = prefill_ms(model)
+    prefill_sparse = prefill_ms(model, prompt)
     log(f"prefill of the {prompt.numel()}-token prompt in one pass: dense {prefill_dense} ms, "
         f"sparse {prefill_sparse} ms ({prefill_dense / prefill_sparse:.3f}x)")
     sparse = run_variant(model, LLAMA31_8B, prompt, 256, "sparse", log)

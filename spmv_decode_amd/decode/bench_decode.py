@@ -58,6 +58,37 @@ def linear_bytes(cfg, m: int) -> int:
     return total * cfg.n_layers
 
 
+def prefill_ms(model, prompt, reps=10):
+    """The prompt's GPU time in one Decoder.prefill pass (every Linear over all
+    its rows: hipBLASLt on the dense weights for the dense model; for the
+    sparse one the matrix-core SpMM, q/k/v and gate/up grouped, down_proj's
+    SiLU product formed in its gather), captured as a hipGraph after an eager
+    warm-up; median of reps replays, in ms."""
+    from .runner import cache_length
+
+    model.setup_cache(cache_length(prompt.numel() + 1), torch.device("cuda"), dtype=torch.float16)
+    ids = prompt.cuda()
+    st = torch.cuda.Stream()
+    st.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(st):
+        model.prefill(ids)
+    torch.cuda.current_stream().wait_stream(st)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        model.prefill(ids)
+    times = []
+    for _ in range(reps):
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        g.replay()
+        b.record()
+        b.synchronize()
+        times.append(a.elapsed_time(b))
+    del g
+    return round(sorted(times)[len(times) // 2], 4)
+
+
 def run_variant(model, cfg, prompt, gen, label, log, batched_prompt=False):
     """Capture the decode step, feed the prompt (untimed; one graph replay per
     token, or with batched_prompt one Decoder.prefill pass), then time `gen`
@@ -109,6 +140,9 @@ def main(argv=None):
     p.add_argument("--fc-warmup", type=int, default=30)
     p.add_argument("--fc-repeat", type=int, default=30)
     p.add_argument("--fc-inner", type=int, default=10)
+    p.add_argument("--prefill-only", action="store_true",
+                   help="time only the --prompt tokens through Decoder.prefill in one pass (one hipGraph), dense "
+                        "and sparse, instead of decoding")
     p.add_argument("--json", default=None)
     a = p.parse_args(argv)
 
@@ -141,6 +175,28 @@ def main(argv=None):
         res.update(protocol="fixed_context", ctx=a.fixed_ctx, warmup=a.fc_warmup, repeat=a.fc_repeat,
                    inner=a.fc_inner)
         del res["prompt"], res["gen"]
+
+    if a.prefill_only:
+        res.update(protocol="prefill_one_pass")
+        del res["gen"]
+        if not a.no_dense:
+            res["dense_prefill_ms"] = prefill_ms(model, prompt)
+            print(f"RESULT model={cfg.name} dense_float16 prompt={a.prompt} prefill_ms={res['dense_prefill_ms']}",
+                  flush=True)
+        if a.m:
+            swap_to_nmsparse(model, a.m, "cuda", seed=a.seed, init="device", keep_dense=False)
+            gc.collect()
+            torch.cuda.empty_cache()
+            res["sparse_prefill_ms"] = prefill_ms(model, prompt)
+            res["ratio"] = f"{a.m // 2}:{a.m}"
+            print(f"RESULT model={cfg.name} M={a.m}({a.m // 2}:{a.m}) prompt={a.prompt} "
+                  f"prefill_ms={res['sparse_prefill_ms']}", flush=True)
+        if "dense_prefill_ms" in res and "sparse_prefill_ms" in res:
+            res["speedup_sparse_vs_dense"] = round(res["dense_prefill_ms"] / res["sparse_prefill_ms"], 4)
+        if a.json:
+            with open(a.json, "w") as f:
+                json.dump(res, f, indent=1)
+        return 0
 
     eager_step = model.forward_step
     if a.compile:
