@@ -807,7 +807,7 @@ def decode_ms_per_token(m, log):
     return out
 
 
-QWEN3_DECODE = (  # BASELINE configs 4 and 5: (model, M, prompt tokens, generated tokens)
+QWEN3_DECODE = (  # the Qwen3 decode workloads: (model, M, prompt tokens, generated tokens)
     ("qwen3-14b", 64, 128, 256),
     ("qwen3-32b", 32, 512, 512),
 )

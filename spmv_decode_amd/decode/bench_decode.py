@@ -3,7 +3,7 @@
     python -m spmv_decode_amd.decode.bench_decode --model llama-3.1-8b --m 64 \\
         [--prompt 128] [--gen 256] [--no-dense] [--json out.json]
 
-Protocol: random-init weights of the named architecture
+Protocol (the Llama-3.1-8B / Qwen3 decode workloads): random-init weights of the named architecture
 in fp16 on one GPU; the prompt (seeded random token ids) is fed one token per
 graph replay (untimed), then `--gen` greedy decode steps are replayed from one
 captured hipGraph and timed with HIP events. Dense first (nn.Linear ->

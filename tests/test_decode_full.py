@@ -1,4 +1,4 @@
-"""Decode parity at the benchmark configurations themselves:
+"""Decode parity at the benchmark configurations themselves (the decode workloads):
 Llama-3.1-8B at 32:64 (32 layers), Qwen3-14B at 32:64 (40 layers) and at 8:16 /
 128:256 (4 layers), Qwen3-32B at 16:32 (64 layers), random-init, fp16, batch 1.
 
@@ -197,7 +197,7 @@ def test_full_depth_decode_parity(gpu, name, M, layers):
     _free()
 
 
-LONG_CASES = [  # (model, M, prompt tokens, positions): BASELINE configs 3 and 5
+LONG_CASES = [  # (model, M, prompt tokens, positions): the Llama-3.1-8B and Qwen3-32B workloads
     ("llama-3.1-8b", 64, 128, 128 + 256),
     ("qwen3-32b", 32, 512, 512 + 512),
 ]

@@ -1,7 +1,7 @@
 """GPU parity of the HIP N:M GEMV against the CPU oracle.
 
 Bar (north star): fp16 outputs within max-abs 1e-2 and rel-L2 1e-3 of the
-fp32-accumulated reference value on the BASELINE distributions (weights
+fp32-accumulated reference value on the benchmark distributions (weights
 N(0, 0.02), activations N(0, 1)); additionally every output must be within
 one unit in the last place of its dtype from the float64 value (the kernel
 rounds an fp32 sum once), fp32 outputs within 1e-5 relative of the row scale.
@@ -69,7 +69,7 @@ def check_parity(out, x, md, mi, nnz, m, tag=""):
 
 
 def test_config1_qwen06b_up_proj(gpu):
-    """dense W [3072, 1024] ~ N(0, 0.02), 2:4 pattern from the
+    """The Qwen3-0.6B up-projection case: dense W [3072, 1024] ~ N(0, 0.02), 2:4 pattern from the
     reference's index sequence, packed; x ~ N(0, 1); checked against the fp32
     dense matvec on the masked weight (the reference's own oracle)."""
     say("config1 3072<-1024 2:4")
