@@ -661,11 +661,14 @@ struct McPlan {
 //  * splits of at most 2560 compressed rows (deep K runs slower per split);
 //  * up to 16 rows: 64-column tiles, then 128, then 256;
 //  * past 16 rows: fewer splits (their partials, [splits, batch, h] fp32,
-//    grow with the rows), then 128-, 64-, 256-column tiles (past 64 rows:
-//    64-column tiles first, 1-4% faster at 96-128 rows; no 256-column tile);
-// and past 32 rows a plan whose partials would reach a quarter of the weight
-// bytes gives way to the widest grid without splits, when that has at least
-// half its workgroups. Each split is whole chunks of 64 columns. Workspace:
+//    grow with the rows), then 128-, 64-, 256-column tiles;
+//  * past 64 rows: 64-column tiles whenever their grid fits one round (at
+//    96-128 rows the 128-column tiles measured 5-25% slower at every
+//    Llama-3.1-8B product and the grouped q/k/v; no 256-column tile), then
+//    the most workgroups;
+// and from 33 to 64 rows a plan whose partials would reach a quarter of the
+// weight bytes gives way to the widest grid without splits, when that has at
+// least half its workgroups. Each split is whole chunks of 64 columns. Workspace:
 // arrival counters, the partials [splits, batch, h] fp32 when splits > 1,
 // then the gathered activations in operand order (ceil(batch / 16) blocks of
 // 16 rows x wp columns, wp = w rounded up to whole chunks).
@@ -713,7 +716,7 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
     // search the DMA configurations (or the given one) x split counts (or the given one)
     const int c_lo = cfg < 0 ? 3 : cfg, c_hi = cfg < 0 ? 5 : cfg;
     const int s_lo = splits > 0 ? splits : 1, s_hi = splits > 0 ? splits : 8;
-    const int pref_small[3] = {0, 1, 2};  // ranks of HT = 64, 128, 256 up to 16 rows and past 64 (lower is better)
+    const int pref_small[3] = {0, 1, 2};  // ranks of HT = 64, 128, 256 up to 16 rows (lower is better)
     const int pref_large[3] = {1, 0, 2};  // 17-64 rows
     int best_c = -1, best_s = 0, best_b = 0, best_r = 0, free_c = -1, free_b = 0;
     auto better = [&](int c, int sp, int b, int r) {
@@ -721,11 +724,12 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
       const bool fits = b <= kMcCUs, best_fits = best_b <= kMcCUs;
       if (fits != best_fits) return fits;
       if (!fits) return b < best_b;  // nothing fits one round: the smallest grid
+      if (batch > 64 && (kMcTileCols[c] == 64) != (kMcTileCols[best_c] == 64)) return kMcTileCols[c] == 64;
       if (b != best_b) return b > best_b;
       const bool deep = r > 2560, best_deep = best_r > 2560;
       if (deep != best_deep) return !deep;
       if (batch > 16 && sp != best_s) return sp < best_s;
-      const int* pref = batch > 16 && batch <= 64 ? pref_large : pref_small;
+      const int* pref = batch > 16 ? pref_large : pref_small;
       return pref[c - 3] < pref[best_c - 3];
     };
     for (int c = c_lo; c <= c_hi; ++c)
@@ -743,7 +747,8 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
       }
     if (best_c < 0) return NM_ERR_BAD_SHAPE;
     const long long part4 = 4LL * best_s * batch;  // partials written and read, relative to 2 * w weight bytes
-    if (batch > 32 && splits <= 0 && best_s > 1 && part4 * 4 >= (long long)w && free_c >= 0 && 2 * free_b >= best_b) {
+    if (batch > 32 && batch <= 64 && splits <= 0 && best_s > 1 && part4 * 4 >= (long long)w && free_c >= 0 &&
+        2 * free_b >= best_b) {
       best_c = free_c;
       best_s = 1;
     }
