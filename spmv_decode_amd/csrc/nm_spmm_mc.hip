@@ -662,10 +662,13 @@ struct McPlan {
 //  * up to 16 rows: 64-column tiles, then 128, then 256;
 //  * past 16 rows: fewer splits (their partials, [splits, batch, h] fp32,
 //    grow with the rows), then 128-, 64-, 256-column tiles;
-//  * past 64 rows: 64-column tiles whenever their grid fits one round (at
-//    96-128 rows the 128-column tiles measured 5-25% slower at every
-//    Llama-3.1-8B product and the grouped q/k/v; no 256-column tile), then
-//    the most workgroups;
+//  * past 32 rows, among grids that fit one round: splits of at most 2560
+//    compressed rows, then 64-column tiles, then the most workgroups (the
+//    grouped Llama-3.1-8B q/k/v on 64-column tiles and 192 workgroups ran 17-19%
+//    faster than on 128-column tiles and 240 at 40-64 rows, and the 64-column
+//    tiles were faster at every Llama-3.1-8B product at 96-128 rows; Qwen3
+//    down's deeper 64-column splits were 3-8% slower); no 256-column tile past
+//    64 rows;
 // and from 33 to 64 rows a plan whose partials would reach a quarter of the
 // weight bytes gives way to the widest grid without splits, when that has at
 // least half its workgroups. Each split is whole chunks of 64 columns. Workspace:
@@ -724,9 +727,12 @@ int make_mc_plan(int batch, int n, const int* hs, int w, int nnz, int m, int cfg
       const bool fits = b <= kMcCUs, best_fits = best_b <= kMcCUs;
       if (fits != best_fits) return fits;
       if (!fits) return b < best_b;  // nothing fits one round: the smallest grid
-      if (batch > 64 && (kMcTileCols[c] == 64) != (kMcTileCols[best_c] == 64)) return kMcTileCols[c] == 64;
-      if (b != best_b) return b > best_b;
       const bool deep = r > 2560, best_deep = best_r > 2560;
+      if (batch > 32) {  // past 32 rows: shallow splits, then 64-column tiles, then the most workgroups
+        if (deep != best_deep) return !deep;
+        if ((kMcTileCols[c] == 64) != (kMcTileCols[best_c] == 64)) return kMcTileCols[c] == 64;
+      }
+      if (b != best_b) return b > best_b;
       if (deep != best_deep) return !deep;
       if (batch > 16 && sp != best_s) return sp < best_s;
       const int* pref = batch > 16 ? pref_large : pref_small;
